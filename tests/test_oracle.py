@@ -1,0 +1,553 @@
+"""Pins the C oracle (`oracle/`) before anything is compared against it.
+
+Each check is chosen so that a plausible slip in the restatement (a dropped
+term, a wrong sign, a transposed operand, a wrong index) fails it:
+
+* the reference's own CPU-vs-CPU gates (FA vs 3-pass attention, CCE vs the
+  materialised softmax-CE, LoRA vs the materialised W_eff) on the same shape
+  cases and tolerances the reference's tests use;
+* closed forms computed independently in numpy float64;
+* finite differences of the loss;
+* known-answer tests (duplicate-token embedding scatter, Adam on hand values).
+
+Inputs come from the oracle's own SplitMix64 generator with the reference's
+distributions (`(rng.float() - 0.5) * s` = uniform(-s/2, s/2)); the Zig
+generator's exact draws cannot be reproduced without running Zig.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+
+def grel(ref, got):
+    """Global relative error max|a-b| / max|a| (reference: cce.zig:358-368)."""
+    ref = np.asarray(ref, np.float64).ravel()
+    got = np.asarray(got, np.float64).ravel()
+    m = np.abs(ref).max()
+    d = np.abs(ref - got).max()
+    return d / m if m > 1e-30 else d
+
+
+def rel_l2(ref, got):
+    ref = np.asarray(ref, np.float64).ravel()
+    got = np.asarray(got, np.float64).ravel()
+    n = np.linalg.norm(ref)
+    return np.linalg.norm(ref - got) / (n if n > 0 else 1.0)
+
+
+# ── FlashAttention vs 3-pass attention: smoke/cpu.zig:746-767, :909-935 ──
+
+FWD_CASES = [
+    # n_q, n_kv, H, Hkv, hd, causal, Br, Bc
+    (1, 8, 4, 2, 16, False, 1, 4),
+    (1, 128, 4, 2, 32, False, 1, 32),
+    (4, 4, 4, 2, 16, True, 2, 2),
+    (16, 16, 16, 8, 128, True, 4, 4),
+    (1, 128, 8, 2, 256, False, 1, 8),
+    (8, 8, 8, 2, 256, True, 4, 4),
+    (10, 12, 4, 2, 16, True, 4, 5),
+    (4, 4, 2, 1, 8, True, 2, 2),  # the "lse-output" case
+]
+
+
+@pytest.mark.parametrize("case", FWD_CASES)
+def test_flash_forward_matches_three_pass(case):
+    n_q, n_kv, H, Hkv, hd, causal, Br, Bc = case
+    Q = O.uniform(n_q * H * hd, 11, -0.5, 0.5)
+    K = O.uniform(n_kv * Hkv * hd, 12, -0.5, 0.5)
+    V = O.uniform(n_kv * Hkv * hd, 13, -0.5, 0.5)
+    out_ref, attn = O.attention_forward(Q, K, V, n_q, n_kv, H, Hkv, hd, causal)
+    out_fa, lse = O.flash_forward(Q, K, V, n_q, n_kv, H, Hkv, hd, causal, Br, Bc)
+    assert grel(out_ref, out_fa) < 1e-4
+    # LSE = log sum_k exp(S) from an independent float64 evaluation of the scores
+    q = Q.reshape(n_q, H, hd).astype(np.float64)
+    k = K.reshape(n_kv, Hkv, hd).astype(np.float64)
+    hpk = H // Hkv
+    for qi in range(n_q):
+        lim = qi + (n_kv - n_q) if causal else n_kv - 1
+        for h in range(H):
+            s = k[: lim + 1, h // hpk] @ q[qi, h] / math.sqrt(hd)
+            ref = s.max() + math.log(np.exp(s - s.max()).sum())
+            assert abs(ref - lse[qi * H + h]) < 1e-4 * max(1.0, abs(ref))
+
+
+BWD_CASES = [
+    (4, 4, 4, 2, 16, True),
+    (16, 16, 16, 8, 128, True),
+    (8, 8, 8, 2, 256, True),
+    (10, 12, 4, 2, 16, True),
+    (8, 8, 4, 1, 16, True),
+    (4, 8, 4, 2, 16, False),
+]
+
+
+@pytest.mark.parametrize("case", BWD_CASES)
+def test_flash_backward_matches_three_pass(case):
+    n_q, n_kv, H, Hkv, hd, causal = case
+    Q = O.uniform(n_q * H * hd, 21, -0.5, 0.5)
+    K = O.uniform(n_kv * Hkv * hd, 22, -0.5, 0.5)
+    V = O.uniform(n_kv * Hkv * hd, 23, -0.5, 0.5)
+    dO = O.uniform(n_q * H * hd, 24, -0.5, 0.5)
+    out_ref, attn = O.attention_forward(Q, K, V, n_q, n_kv, H, Hkv, hd, causal)
+    out_fa, lse = O.flash_forward(Q, K, V, n_q, n_kv, H, Hkv, hd, causal, min(n_q, 4), 4)
+    dq_r, dk_r, dv_r = O.attention_backward(dO, Q, K, V, attn, n_q, n_kv, H, Hkv, hd)
+    dq, dk, dv = O.flash_backward(Q, K, V, out_fa, dO, lse, n_q, n_kv, H, Hkv, hd, causal)
+    assert grel(dq_r, dq) < 1e-4
+    assert grel(dk_r, dk) < 1e-4
+    assert grel(dv_r, dv) < 1e-4
+
+
+def test_attention_backward_finite_difference():
+    """Independent of both attention oracles: d/dQ of sum(out * dO)."""
+    n, H, Hkv, hd = 5, 2, 1, 8
+    Q = O.uniform(n * H * hd, 31, -1, 1)
+    K = O.uniform(n * Hkv * hd, 32, -1, 1)
+    V = O.uniform(n * Hkv * hd, 33, -1, 1)
+    dO = O.uniform(n * H * hd, 34, -1, 1)
+    out, lse = O.flash_forward(Q, K, V, n, n, H, Hkv, hd, True, 2, 2)
+    dq, dk, dv = O.flash_backward(Q, K, V, out, dO, lse, n, n, H, Hkv, hd, True)
+
+    def loss(q, k, v):
+        o, _ = O.flash_forward(q, k, v, n, n, H, Hkv, hd, True, 2, 2)
+        return float(np.dot(o.astype(np.float64), dO))
+
+    h = 1e-2
+    for arr, grad in ((Q, dq), (K, dk), (V, dv)):
+        for idx in np.argsort(-np.abs(grad))[:6]:
+            p, m = arr.copy(), arr.copy()
+            p[idx] += h
+            m[idx] -= h
+            args_p = [p if a is arr else a for a in (Q, K, V)]
+            args_m = [m if a is arr else a for a in (Q, K, V)]
+            fd = (loss(*args_p) - loss(*args_m)) / (2 * h)
+            assert abs(fd - grad[idx]) < 1e-2 * max(1e-3, abs(grad[idx])) + 1e-4
+
+
+def test_flash_backward_masked_row_contributes_nothing():
+    """fa_bw_dq.comp:100-107: a row with LSE = -inf yields dQ = 0 and no dK/dV."""
+    n, H, hd = 4, 1, 8
+    Q = O.uniform(n * H * hd, 41, -1, 1)
+    K = O.uniform(n * hd, 42, -1, 1)
+    V = O.uniform(n * hd, 43, -1, 1)
+    dO = O.uniform(n * H * hd, 44, -1, 1)
+    out, lse = O.flash_forward(Q, K, V, n, n, H, 1, hd, True, 2, 2)
+    lse2 = lse.copy()
+    lse2[2] = -np.inf
+    dq, dk, dv = O.flash_backward(Q, K, V, out, dO, lse2, n, n, H, 1, hd, True)
+    assert np.all(dq.reshape(n, hd)[2] == 0)
+    # row 2 removed: dV equals the backward with dO[2] = 0 and lse[2] = -inf
+    dO3 = dO.copy()
+    dO3.reshape(n, hd)[2] = 0
+    _, _, dv3 = O.flash_backward(Q, K, V, out, dO3, lse2, n, n, H, 1, hd, True)
+    assert np.array_equal(dv, dv3)
+
+
+def test_fa_bw_d_closed_form():
+    n, H, hd = 7, 3, 16
+    Ov = O.normal(n * H * hd, 51)
+    dO = O.normal(n * H * hd, 52)
+    D = O.fa_bw_d(Ov, dO, n, H, hd)
+    ref = (Ov.astype(np.float64).reshape(n, H, hd) * dO.reshape(n, H, hd)).sum(-1).ravel()
+    assert np.allclose(D, ref, rtol=1e-6, atol=1e-6)
+
+
+# ── CCE: cce.zig:370-753 ─────────────────────────────────────────────────
+
+def _cce_inputs(n, dim, vocab, seed, scale):
+    h = O.uniform(n * dim, seed, -scale / 2, scale / 2)
+    w = O.uniform(vocab * dim, seed + 1, -scale / 2, scale / 2)
+    t = O.ids(n, seed + 2, vocab)
+    return h, w, t
+
+
+@pytest.mark.parametrize("chunk", [64, 128, 256, 333, 1024])
+def test_cce_forward_matches_materialized(chunk):
+    n, dim, vocab = 4, 32, 1024
+    h, w, t = _cce_inputs(n, dim, vocab, 0xC0FFEE, 0.1)
+    logits = O.matmul_nt(h, w, n, vocab, dim)
+    ref = O.softmax_ce_loss(logits, t, n, vocab)
+    loss, lse, loss_row = O.cce_forward(h, w, t, n, vocab, dim, chunk)
+    assert abs(loss - ref) / abs(ref) < 1e-5
+    assert abs(loss_row.astype(np.float64).mean() - loss) < 1e-5
+
+
+def test_cce_backward_matches_materialized():
+    n, dim, vocab = 4, 32, 1024
+    h, w, t = _cce_inputs(n, dim, vocab, 0xBADF00D, 0.1)
+    logits = O.matmul_nt(h, w, n, vocab, dim)
+    dlog = O.softmax_ce_loss_grad(logits, t, n, vocab)
+    dh_ref, dW_ref = O.linear_backward(dlog, h, w, n, vocab, dim)
+    _, lse, _ = O.cce_forward(h, w, t, n, vocab, dim, 256)
+    dh, dW = O.cce_backward(h, w, t, lse, n, vocab, dim, 256)
+    assert grel(dh_ref, dh) < 1e-5
+    assert grel(dW_ref, dW) < 1e-5
+
+
+def test_cce_chunk_irrelevance():
+    n, dim, vocab = 3, 16, 512
+    h, w, t = _cce_inputs(n, dim, vocab, 0xCA11AB1E, 0.3)
+    lf, lse_f, _ = O.cce_forward(h, w, t, n, vocab, dim, vocab)
+    dh_f, dW_f = O.cce_backward(h, w, t, lse_f, n, vocab, dim, vocab)
+    for c in (32, 64, 128, 250, 333):
+        lc, lse_c, _ = O.cce_forward(h, w, t, n, vocab, dim, c)
+        dh_c, dW_c = O.cce_backward(h, w, t, lse_c, n, vocab, dim, c)
+        assert abs(lc - lf) / abs(lf) < 1e-5
+        assert grel(lse_f, lse_c) < 1e-5
+        assert grel(dh_f, dh_c) < 1e-5
+        assert grel(dW_f, dW_c) < 1e-5
+
+
+def test_cce_backward_accumulates_dw():
+    n, dim, vocab = 2, 8, 64
+    h, w, t = _cce_inputs(n, dim, vocab, 0xACCD, 1.0)
+    _, lse, _ = O.cce_forward(h, w, t, n, vocab, dim, 32)
+    _, dWa = O.cce_backward(h, w, t, lse, n, vocab, dim, 32)
+    # second call onto a pre-filled dW must add, not overwrite
+    dWb = dWa.copy()
+    O.lib().orc_cce_backward(h, w, t, lse, n, vocab, dim, 32, 0.0, 0.0,
+                             np.empty(n * dim, np.float32), dWb.ctypes.data)
+    nz = np.abs(dWa) > 0
+    assert np.all(np.abs(dWb[nz] - 2 * dWa[nz]) / np.abs(2 * dWa[nz]) < 1e-5)
+
+
+@pytest.mark.parametrize("zl,ls", [(1e-4, 0.0), (1e-4, 0.1)])
+def test_cce_zloss_label_smoothing_closed_form(zl, ls):
+    n, dim, vocab = 4, 32, 1024
+    h, w, t = _cce_inputs(n, dim, vocab, 0xC105550, 0.1)
+    loss, lse, _ = O.cce_forward(h, w, t, n, vocab, dim, 256, zl, ls)
+    dh, dW = O.cce_backward(h, w, t, lse, n, vocab, dim, 256, zl, ls)
+    z = h.astype(np.float64).reshape(n, dim) @ w.astype(np.float64).reshape(vocab, dim).T
+    lse_r = np.log(np.exp(z - z.max(1, keepdims=True)).sum(1)) + z.max(1)
+    ce = lse_r - (1 - ls) * z[np.arange(n), t] - ls * z.mean(1) + zl * lse_r ** 2
+    assert abs(ce.mean() - loss) / abs(ce.mean()) < 1e-5
+    p = np.exp(z - lse_r[:, None])
+    oh = np.zeros_like(z)
+    oh[np.arange(n), t] = 1
+    dz = ((1 + 2 * zl * lse_r)[:, None] * p - (1 - ls) * oh - ls / vocab) / n
+    assert grel(dz @ w.reshape(vocab, dim), dh) < 1e-5
+    assert grel(dz.T @ h.reshape(n, dim), dW) < 1e-5
+
+
+# ── linear layers (train_decoder.zig:45-58, :294-332) ───────────────────
+
+def test_linear_closed_form_and_transpose_identity():
+    M, N, K = 7, 5, 9
+    x = O.normal(M * K, 61)
+    W = O.normal(N * K, 62)
+    dy = O.normal(M * N, 63)
+    y = O.matmul_nt(x, W, M, N, K)
+    x64, W64, dy64 = (a.astype(np.float64) for a in (x, W, dy))
+    assert np.allclose(y, (x64.reshape(M, K) @ W64.reshape(N, K).T).ravel(), rtol=1e-5, atol=1e-5)
+    dx, dW = O.linear_backward(dy, x, W, M, N, K)
+    assert grel((dy64.reshape(M, N) @ W64.reshape(N, K)).ravel(), dx) < 1e-7
+    assert grel((dy64.reshape(M, N).T @ x64.reshape(M, K)).ravel(), dW) < 1e-7
+    # transpose identity: dW of (x, dy) equals dx of the transposed problem
+    dx_t, _ = O.linear_backward(np.ascontiguousarray(dy.reshape(M, N).T), np.zeros(N * K, np.float32),
+                                np.ascontiguousarray(x.reshape(M, K)), N, M, K, True, False)
+    assert grel(dW, dx_t) < 1e-7
+
+
+# ── LoRA (lora.zig:281-570) ──────────────────────────────────────────────
+
+def _lora_inputs(M, N, K, r, seed, zero_b=False, scales=(0.5, 0.3, 0.2, 0.2, 0.4)):
+    x = O.uniform(M * K, seed, -scales[0] / 2, scales[0] / 2)
+    w = O.uniform(N * K, seed + 1, -scales[1] / 2, scales[1] / 2)
+    a = O.uniform(r * K, seed + 2, -scales[2] / 2, scales[2] / 2)
+    b = np.zeros(N * r, np.float32) if zero_b else O.uniform(N * r, seed + 3, -scales[3] / 2, scales[3] / 2)
+    dy = O.uniform(M * N, seed + 4, -scales[4] / 2, scales[4] / 2)
+    return x, w, a, b, dy
+
+
+def _w_eff(w, a, b, N, K, r, aor):
+    return (w.astype(np.float64).reshape(N, K) + aor * b.astype(np.float64).reshape(N, r) @ a.astype(np.float64).reshape(r, K)).astype(np.float32)
+
+
+def test_lora_b_zero_forward_equals_plain():
+    M, N, K, r = 4, 8, 16, 4
+    x, w, a, b, _ = _lora_inputs(M, N, K, r, 0x10AA1, zero_b=True)
+    y, _ = O.lora_forward(x, w, a, b, M, N, K, r, 2.0)
+    assert grel(O.matmul_nt(x, w, M, N, K), y) < 1e-5
+
+
+def test_lora_forward_equals_materialized():
+    M, N, K, r = 4, 12, 32, 4
+    x, w, a, b, _ = _lora_inputs(M, N, K, r, 0x10AA2)
+    y, _ = O.lora_forward(x, w, a, b, M, N, K, r, 2.0)
+    assert grel(O.matmul_nt(x, _w_eff(w, a, b, N, K, r, 2.0), M, N, K), y) < 1e-5
+
+
+def test_lora_backward_chain_rule_decomposition():
+    M, N, K, r, aor = 6, 16, 24, 8, 2.0
+    x, w, a, b, dy = _lora_inputs(M, N, K, r, 0x10AA3)
+    _, inter = O.lora_forward(x, w, a, b, M, N, K, r, aor)
+    dx, dA, dB = O.lora_backward(dy, x, w, a, b, inter, M, N, K, r, aor)
+    weff = _w_eff(w, a, b, N, K, r, aor)
+    dx_r, dWe = O.linear_backward(dy, x, weff, M, N, K)
+    dWe = dWe.astype(np.float64).reshape(N, K)
+    dA_r = aor * (b.astype(np.float64).reshape(N, r).T @ dWe)
+    dB_r = aor * (dWe @ a.astype(np.float64).reshape(r, K).T)
+    assert grel(dx_r, dx) < 1e-5
+    assert grel(dA_r.ravel(), dA) < 1e-5
+    assert grel(dB_r.ravel(), dB) < 1e-5
+
+
+def test_lora_b_zero_gives_exact_zero_dA():
+    M, N, K, r = 4, 8, 16, 4
+    x, w, a, b, dy = _lora_inputs(M, N, K, r, 0x10AA4, zero_b=True)
+    _, inter = O.lora_forward(x, w, a, b, M, N, K, r, 2.0)
+    _, dA, dB = O.lora_backward(dy, x, w, a, b, inter, M, N, K, r, 2.0)
+    assert np.all(dA == 0)
+    assert np.any(dB != 0)
+
+
+def test_lora_backward_accumulates():
+    M, N, K, r, aor = 3, 6, 8, 2, 1.5
+    x, w, a, b, dy = _lora_inputs(M, N, K, r, 0x10AA5, scales=(1, 1, 1, 1, 1))
+    _, inter = O.lora_forward(x, w, a, b, M, N, K, r, aor)
+    _, dA1, dB1 = O.lora_backward(dy, x, w, a, b, inter, M, N, K, r, aor)
+    _, dA2, dB2 = O.lora_backward(dy, x, w, a, b, inter, M, N, K, r, aor, dA=dA1, dB=dB1)
+    assert np.allclose(dA2, 2 * dA1, rtol=1e-5)
+    assert np.allclose(dB2, 2 * dB1, rtol=1e-5)
+
+
+# ── RMSNorm backward (train_transformer.zig:68-111) ─────────────────────
+
+def test_rmsnorm_backward_finite_difference_and_identity():
+    rows, D, eps = 3, 24, 1e-6
+    x = O.normal(rows * D, 71)
+    w = O.uniform(D, 72, 0.5, 1.5)
+    dy = O.normal(rows * D, 73)
+    dx, dw = O.rmsnorm_backward(dy, x, w, eps)
+
+    def loss(xx, ww):
+        return float(np.dot(O.rmsnorm_forward(xx, ww, eps).astype(np.float64), dy))
+
+    h = 1e-2
+    for arr, g in ((x, dx), (w, dw)):
+        for i in np.argsort(-np.abs(g))[:8]:
+            p, m = arr.copy(), arr.copy()
+            p[i] += h
+            m[i] -= h
+            a_p = (p, w) if arr is x else (x, p)
+            a_m = (m, w) if arr is x else (x, m)
+            fd = (loss(*a_p) - loss(*a_m)) / (2 * h)
+            assert abs(fd - g[i]) < 1e-2 * abs(g[i]) + 1e-3
+    # closed-form row identity: sum_i dx_i x_i = ri A (1 - ri^2 mean(x^2))
+    X, DY, DX = (a.reshape(rows, D).astype(np.float64) for a in (x, dy, dx))
+    ms = (X * X).mean(1)
+    ri = 1 / np.sqrt(ms + eps)
+    A = (DY * w * X).sum(1)
+    assert np.allclose((DX * X).sum(1), ri * A * (1 - ri * ri * ms), rtol=1e-4, atol=1e-5)
+
+
+def test_rmsnorm_gemma_quirk_gradient_unchanged_form():
+    """(w+1) and w have the same derivative: dw is identical, dx uses gain=w+1."""
+    rows, D = 2, 16
+    x = O.normal(rows * D, 81)
+    w = O.normal(D, 82)
+    dy = O.normal(rows * D, 83)
+    dx_q, dw_q = O.rmsnorm_backward(dy, x, w, 1e-6, True)
+    dx_p, dw_p = O.rmsnorm_backward(dy, x, w + 1, 1e-6, False)
+    assert np.array_equal(dw_q, dw_p)
+    assert np.allclose(dx_q, dx_p, rtol=1e-6, atol=1e-7)
+
+
+# ── RoPE (train_transformer.zig:420-563) ─────────────────────────────────
+
+@pytest.mark.parametrize("rotary_dim", [16, 8])
+def test_rope_roundtrip_pos0_and_closed_form(rotary_dim):
+    n, H, hd, theta = 6, 3, 16, 1e6
+    x = O.normal(n * H * hd, 91)
+    y = O.rope_forward(x, n, H, hd, rotary_dim, theta)
+    xb = O.rope_backward(y, n, H, hd, rotary_dim, theta)
+    assert np.allclose(xb, x, rtol=1e-5, atol=1e-6)  # orthogonal rotation
+    assert np.array_equal(y.reshape(n, H, hd)[0], x.reshape(n, H, hd)[0])  # pos 0
+    half = rotary_dim // 2
+    X = x.reshape(n, H, hd).astype(np.float64)
+    j = np.arange(half)
+    ang = np.arange(n)[:, None] * theta ** (-2.0 * j / rotary_dim)[None, :]
+    a, b = X[:, :, :half], X[:, :, half:rotary_dim]
+    c, s = np.cos(ang)[:, None, :], np.sin(ang)[:, None, :]
+    ref = X.copy()
+    ref[:, :, :half] = a * c - b * s
+    ref[:, :, half:rotary_dim] = a * s + b * c
+    assert np.allclose(y.reshape(n, H, hd), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_rope_batch_positions_restart():
+    S, B, H, hd = 5, 3, 2, 8
+    x = O.normal(S * B * H * hd, 92)
+    y = O.rope_forward(x, S * B, H, hd, hd, 1e4, S)
+    for b in range(B):
+        blk = slice(b * S * H * hd, (b + 1) * S * H * hd)
+        assert np.array_equal(y[blk], O.rope_forward(x[blk], S, H, hd, hd, 1e4))
+
+
+# ── SwiGLU (train_transformer.zig:832-875) ──────────────────────────────
+
+def test_swiglu_closed_form():
+    n = 257
+    z = O.normal(n, 101, 2.0)
+    u = O.normal(n, 102)
+    dg = O.normal(n, 103)
+    g = O.swiglu_forward(z, u)
+    dz, du = O.swiglu_backward(dg, z, u)
+    Z, U, DG = (a.astype(np.float64) for a in (z, u, dg))
+    sig = 1 / (1 + np.exp(-Z))
+    assert np.allclose(g, Z * sig * U, rtol=1e-5, atol=1e-6)
+    assert np.allclose(du, DG * Z * sig, rtol=1e-5, atol=1e-6)
+    assert np.allclose(dz, DG * U * sig * (1 + Z * (1 - sig)), rtol=1e-5, atol=1e-6)
+
+
+# ── embedding scatter KAT (gpu_train.zig:4855-4884 duplicate-id case) ────
+
+def test_embedding_backward_duplicate_ids_bit_exact():
+    ids = np.array([3, 7, 3, 11, 7, 3], np.uint32)
+    vocab, dim = 16, 5
+    dy = O.normal(ids.size * dim, 111)
+    dE = O.embedding_backward(dy, ids, vocab, dim).reshape(vocab, dim)
+    manual = np.zeros((vocab, dim), np.float32)
+    for p, t in enumerate(ids):  # position order, fp32 adds
+        manual[t] = manual[t] + dy.reshape(-1, dim)[p]
+    assert np.array_equal(dE, manual)
+    untouched = [v for v in range(vocab) if v not in (3, 7, 11)]
+    assert np.all(dE[untouched] == 0)
+
+
+# ── Adam (adam_step.comp:41-62; train_decoder.zig:938-962) ──────────────
+
+def test_adam_hand_values():
+    p = np.array([1.0, -2.0, 0.5], np.float32)
+    g = np.array([0.1, -0.2, 0.0], np.float32)
+    m = np.zeros(3, np.float32)
+    v = np.zeros(3, np.float32)
+    O.adam_step(p, g, m, v, 0.01, 0.9, 0.999, 1e-8, 1)
+    # t=1: m_hat = g, v_hat = g^2  =>  p -= lr * g / (|g| + eps)
+    assert np.allclose(m, 0.1 * np.array([0.1, -0.2, 0.0]), rtol=1e-6)
+    assert np.allclose(v, 0.001 * np.array([0.01, 0.04, 0.0]), rtol=1e-5)
+    assert np.allclose(p, [1.0 - 0.01, -2.0 + 0.01, 0.5], rtol=1e-6)
+
+
+def test_adam_shader_and_folded_forms_agree_closely():
+    n = 1000
+    # |g| bounded away from 0: for tiny g the two forms legitimately differ,
+    # because the folded form adds eps to sqrt(v) rather than sqrt(v_hat)
+    g = O.uniform(n, 121, 5e-3, 1.5e-2) * np.where(O.uniform(n, 123) > 0, 1, -1).astype(np.float32)
+    p0 = O.normal(n, 122, 1e-3)
+    p1, p2 = p0.copy(), p0.copy()
+    m1, v1, m2, v2 = (np.zeros(n, np.float32) for _ in range(4))
+    for t in range(1, 6):
+        O.adam_step(p1, g, m1, v1, 1e-3, 0.9, 0.999, 1e-8, t)
+        O.adam_step_folded(p2, g, m2, v2, 1e-3, 0.9, 0.999, 1e-8, t)
+    # the two forms differ only in where eps enters (and fp32 rounding)
+    u1 = p1.astype(np.float64) - p0
+    u2 = p2.astype(np.float64) - p0
+    assert rel_l2(u1, u2) < 1e-4
+
+
+# ── whole model ──────────────────────────────────────────────────────────
+
+TINY = dict(dim=16, n_heads=4, n_kv_heads=2, head_dim=8, ff_dim=24, seq_len=6, n_seqs=2,
+            n_layers=2, vocab_size=11, rms_eps=1e-6, causal=1, rotary_dim=8, rope_theta=1e4,
+            qk_norm=1, lr=1e-3, beta1=0.9, beta2=0.999, eps_adam=1e-8, lora_targets=0,
+            lora_rank=0, lora_alpha=0.0, lora_lr_b_scale=1.0, tied_embeddings=0, bf16_operands=0)
+
+
+def _tiny_model(**over):
+    cfg = dict(TINY)
+    cfg.update(over)
+    m = O.Model(**cfg)
+    m.init_random(1234, std=0.3, lora_std=0.3)
+    T = cfg["seq_len"] * cfg["n_seqs"]
+    tok = O.ids(T, 5, cfg["vocab_size"])
+    tgt = O.ids(T, 6, cfg["vocab_size"])
+    return m, tok, tgt
+
+
+TENSORS = [(-1, 0), (-1, 1), (-1, 2)] + [(l, w) for l in (0, 1) for w in range(11)]
+
+
+@pytest.mark.parametrize("over", [{}, {"tied_embeddings": 1}, {"qk_norm": 0, "rotary_dim": 4}])
+def test_model_gradients_finite_difference(over):
+    m, tok, tgt = _tiny_model(**over)
+    m.forward_backward(tok, tgt)
+    grads = {}
+    for (l, w) in TENSORS:
+        g = m.tensor(O.Model.GRAD, l, w)
+        if g is not None:
+            grads[(l, w)] = g.copy()
+    h = 2e-3
+    for key, g in grads.items():
+        p = m.tensor(O.Model.PARAM, *key)
+        for i in np.argsort(-np.abs(g))[:2]:
+            old = p[i]
+            p[i] = old + h
+            lp = m.forward_backward(tok, tgt)
+            p[i] = old - h
+            lm = m.forward_backward(tok, tgt)
+            p[i] = old
+            fd = (lp - lm) / (2 * h)
+            assert abs(fd - g[i]) < 3e-2 * abs(g[i]) + 2e-4, (key, i, fd, g[i])
+
+
+def test_model_lora_finite_difference_and_b_zero():
+    m, tok, tgt = _tiny_model(lora_targets=0b1111, lora_rank=2, lora_alpha=4.0)
+    # B = 0 at init => loss equals the frozen-base loss (lora.zig:1-21)
+    base, _, _ = _tiny_model()
+    assert abs(m.forward_backward(tok, tgt) - base.forward_backward(tok, tgt)) < 1e-6
+    for l in (0, 1):
+        assert np.all(m.tensor(O.Model.GRAD, l, 16) == 0)  # dA_q == 0 exactly
+    # move B off zero, then check dA/dB by finite differences
+    for l in (0, 1):
+        for p in range(4):
+            b = m.tensor(O.Model.PARAM, l, 17 + 2 * p)
+            b[:] = O.normal(b.size, 700 + 10 * l + p, 0.3)
+    m.forward_backward(tok, tgt)
+    h = 2e-3
+    for l in (0, 1):
+        for which in (16, 17, 20, 23):
+            g = m.tensor(O.Model.GRAD, l, which).copy()
+            pp = m.tensor(O.Model.PARAM, l, which)
+            i = int(np.argmax(np.abs(g)))
+            old = pp[i]
+            pp[i] = old + h
+            lp = m.forward_backward(tok, tgt)
+            pp[i] = old - h
+            lm = m.forward_backward(tok, tgt)
+            pp[i] = old
+            fd = (lp - lm) / (2 * h)
+            assert abs(fd - g[i]) < 3e-2 * abs(g[i]) + 2e-4
+
+
+def test_model_single_sequence_is_independent_of_batchmates():
+    """Block-diagonal attention: sequence 0's logits do not see sequence 1."""
+    m, tok, tgt = _tiny_model()
+    S, V = TINY["seq_len"], TINY["vocab_size"]
+    la = m.forward_logits(tok).reshape(-1, V)
+    tok2 = tok.copy()
+    tok2[S:] = (tok2[S:] + 1) % V
+    lb = m.forward_logits(tok2).reshape(-1, V)
+    assert np.array_equal(la[:S], lb[:S])
+    assert not np.array_equal(la[S:], lb[S:])
+
+
+def test_model_loss_decreases_and_step_t():
+    m, tok, tgt = _tiny_model(lr=1e-2)
+    assert m.step_t == 1
+    losses = [m.step(tok, tgt) for _ in range(30)]
+    assert m.step_t == 31
+    assert losses[-1] < 0.5 * losses[0]
+    assert all(np.isfinite(losses))
+
+
+def test_model_lora_freezes_base():
+    m, tok, tgt = _tiny_model(lora_targets=0b1111, lora_rank=2, lora_alpha=4.0)
+    before = {k: m.tensor(O.Model.PARAM, *k).copy() for k in TENSORS if m.tensor(O.Model.PARAM, *k) is not None}
+    for _ in range(3):
+        m.step(tok, tgt)
+    for k, v in before.items():
+        assert np.array_equal(v, m.tensor(O.Model.PARAM, *k)), k
+    assert np.any(m.tensor(O.Model.PARAM, 0, 17) != 0)  # B moved
