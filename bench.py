@@ -1,0 +1,255 @@
+"""Benchmark: BASELINE.json metric on one MI355X.
+
+  train tokens/s of a Qwen3-0.6B-shaped fwd + bwd + Adam step (config 3:
+  28 layers, dim 1024, 16/8 heads, head_dim 128, QK-norm, SwiGLU 3072,
+  vocab 151936 tied, batch 4 x seq 512, bf16 operands with fp32 master
+  weights / accumulation / Adam), synthetic random-init weights and
+  uniform token ids.
+
+One JSON line on stdout.  `roofline` is the FA-2 backward (fa_bw_d + dK/dV +
+dQ kernels) at config 2 (B=4, S=2048, 16/8 heads, hd 128, causal, bf16
+operands), timed with HIP events on the stream it runs on; its algorithmic
+work is 10 * B * Hq * hd * S(S+1)/2 = 171.88 GFLOP per call.
+`cpu_baseline` is the C oracle (a scalar restatement of valkyr's CPU
+reference path) timed on this host on a bounded sample and scaled to
+tokens/s of the same step (see `sample`).
+
+usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
+                       [--no-cpu-baseline] [--fa-reps R]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+FP32_PEAK_TFLOPS = 157.3
+
+# BASELINE.json configs[2]
+QWEN3_06B = dict(dim=1024, n_heads=16, n_kv_heads=8, head_dim=128, ff_dim=3072, n_pos=512,
+                 n_layers=28, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=128,
+                 rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
+                 n_seqs=4, tied_embeddings=1)
+
+
+def step_flops(c) -> float:
+    """Algorithmic FLOP of one step (6 * tokens * matmul params + CCE + attention)."""
+    T = c["n_pos"] * c["n_seqs"]
+    D, F, V, L = c["dim"], c["ff_dim"], c["vocab_size"], c["n_layers"]
+    qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
+    p_mat = L * (D * (qd + 2 * kvd) + qd * D + 3 * D * F)
+    gemm = 6.0 * T * p_mat
+    cce = 6.0 * T * V * D
+    S, H, hd = c["n_pos"], c["n_heads"], c["head_dim"]
+    causal_pairs = c["n_seqs"] * S * (S + 1) / 2
+    attn = L * H * hd * causal_pairs * (4 + 10)  # fwd 2 GEMMs (4), bwd 5 GEMMs (10)
+    return gemm + cce + attn
+
+
+def bench_step(args, dev_info):
+    import valkyr_amd as v
+    from valkyr_amd.device import Event
+
+    c = dict(QWEN3_06B)
+    prec = 1 if args.precision == "bf16" else 0
+    cfg = v.make_config(**c, precision=prec)
+    r = v.Runner(cfg)
+    r.init_random(seed=20261201, std=0.02)
+    T = c["n_pos"] * c["n_seqs"]
+    rng = np.random.default_rng(1)
+    tok = rng.integers(0, c["vocab_size"], T, dtype=np.uint32)
+    tgt = rng.integers(0, c["vocab_size"], T, dtype=np.uint32)
+    print(f"[bench] runner ready: {r.param_count():,} params, "
+          f"{r.device_bytes() / 2**30:.1f} GiB device memory", file=sys.stderr, flush=True)
+    for _ in range(args.warmup):
+        r.step_async(tok, tgt)
+    r.synchronize()
+    loss0 = r.last_loss()
+    e0, e1 = Event(), Event()
+    r.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        r.step_async(tok, tgt)
+    r.synchronize()
+    e1.record()
+    e1.synchronize()
+    t1 = time.perf_counter()
+    wall = t1 - t0
+    loss1 = r.last_loss()
+    ms = 1000.0 * wall / args.steps
+    tokens_s = T * args.steps / wall
+    flops = step_flops(c)
+    print(f"[bench] step {ms:.2f} ms, {tokens_s:,.0f} tok/s, loss {loss0:.4f} -> {loss1:.4f}",
+          file=sys.stderr, flush=True)
+    r.close()
+    return dict(ms=ms, tokens_s=tokens_s, T=T, flops=flops, loss_first=loss0, loss_last=loss1,
+                params=None)
+
+
+def bench_fa_bwd(args):
+    """FA-2 backward at config 2, events on the launch stream."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import DeviceBuffer, Event, Stream, f32_to_bf16_bits
+
+    B, S, H, Hkv, hd = 4, 2048, 16, 8, 128
+    rng = np.random.default_rng(2)
+    nq, nk = B * S * H * hd, B * S * Hkv * hd
+    q = DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(nq, np.float32)))
+    k = DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(nk, np.float32)))
+    vv = DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(nk, np.float32)))
+    dout = DeviceBuffer.from_numpy((0.1 * rng.standard_normal(nq)).astype(np.float32))
+    o = DeviceBuffer(nq * 4)
+    lse = DeviceBuffer(B * S * H * 4)
+    d = DeviceBuffer(B * S * H * 4)
+    dout16 = DeviceBuffer(nq * 2)
+    dq, dk, dv = DeviceBuffer(nq * 4), DeviceBuffer(nk * 4), DeviceBuffer(nk * 4)
+    p = K.attn_params(S, S, H, Hkv, hd, True, B, K.BF16)
+    s = Stream()
+    K.fa_forward(p, q, k, vv, o, lse, stream=s)  # O and LSE of the same inputs
+
+    def once():
+        K.fa_bw_d(p, o, dout, d, dout16, stream=s)
+        K.fa_bw_dkv(p, q, k, vv, dout16, lse, d, dk, dv, stream=s)
+        K.fa_bw_dq(p, q, k, vv, dout16, lse, d, dq, stream=s)
+
+    for _ in range(3):
+        once()
+    s.synchronize()
+    e0, e1 = Event(), Event()
+    e0.record(s)
+    for _ in range(args.fa_reps):
+        once()
+    e1.record(s)
+    e1.synchronize()
+    ms = e0.elapsed_ms(e1) / args.fa_reps
+    flops = 10.0 * B * H * hd * S * (S + 1) / 2
+    tflops = flops / (ms * 1e-3) / 1e12
+    # HBM traffic floor of one call: bf16 Q,K,V,dO read, fp32 O/dO for D, fp32 dQ/dK/dV written
+    print(f"[bench] fa-bwd {ms:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
+    return dict(ms=ms, flops=flops, tflops=tflops)
+
+
+def cpu_baseline(args):
+    """The C oracle (single thread) on a bounded sample of the step, scaled to tokens/s.
+
+    Sample: the config-3 model shape with 1 and 2 layers at T = 16 tokens
+    (one sequence), full 151936 vocab, tied embeddings; per-layer and
+    per-head costs per token come from the two timings, Adam from the
+    1-layer model's optimizer step scaled by parameter count.  Extrapolated:
+    t(step) = 2048 * (28 * c_layer + c_head) + t_adam(596M params)."""
+    import oracle as O
+
+    c = dict(QWEN3_06B)
+    Ts = 16
+
+    def model(nl):
+        m = O.Model(dim=c["dim"], n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"],
+                    head_dim=c["head_dim"], ff_dim=c["ff_dim"], seq_len=Ts, n_seqs=1,
+                    n_layers=nl, vocab_size=c["vocab_size"], rms_eps=c["rms_eps"], causal=1,
+                    rotary_dim=c["rotary_dim"], rope_theta=c["rope_theta"], qk_norm=1, lr=1e-4,
+                    beta1=0.9, beta2=0.999, eps_adam=1e-8, lora_targets=0, lora_rank=0,
+                    lora_alpha=0.0, lora_lr_b_scale=1.0, tied_embeddings=1, bf16_operands=0)
+        m.init_random(3, std=0.02)
+        return m
+
+    tok = O.ids(Ts, 11, c["vocab_size"])
+    tgt = O.ids(Ts, 12, c["vocab_size"])
+    m1 = model(1)
+    t0 = O.now()
+    m1.forward_backward(tok, tgt)
+    t_fb1 = O.now() - t0
+    t0 = O.now()
+    m1.adam()
+    t_adam1 = O.now() - t0
+    n1 = sum(m1.tensor(0, l, w).size for l, w in [(-1, 0), (-1, 1)] + [(0, i) for i in range(11)])
+    del m1
+    m2 = model(2)
+    t0 = O.now()
+    m2.forward_backward(tok, tgt)
+    t_fb2 = O.now() - t0
+    del m2
+    c_layer = max(t_fb2 - t_fb1, 1e-9) / Ts
+    c_head = max(t_fb1 / Ts - c_layer, 0.0)
+    T = c["n_pos"] * c["n_seqs"]
+    n_full = 596_049_920
+    t_step = T * (c["n_layers"] * c_layer + c_head) + t_adam1 * n_full / n1
+    return dict(value=T / t_step, unit="tokens/s", cores=1, kind="port",
+                sample=(f"C oracle (src/cpu/*.zig restatement, 1 thread, fp64 accumulators) on the "
+                        f"config-3 shape at T={Ts}: 1-layer fwd+bwd {t_fb1:.1f} s, 2-layer "
+                        f"{t_fb2:.1f} s, Adam over {n1:,} params {t_adam1:.2f} s; scaled to 28 "
+                        f"layers x 2048 tokens + Adam over {n_full:,} params "
+                        f"= {t_step:,.0f} s/step (extrapolated)"),
+                seconds_measured=round(t_fb1 + t_fb2 + t_adam1, 1))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
+    ap.add_argument("--fa-reps", type=int, default=20)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: this build has no multi-GPU path "
+              "(see DESIGN.md for how the step would shard); run with --gpus 1",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import valkyr_amd as v
+
+    if v.device_count() < 1:
+        print("bench.py: no GPU visible", file=sys.stderr)
+        sys.exit(1)
+    st = bench_step(args, None)
+    fa = bench_fa_bwd(args)
+    cpu = None if args.no_cpu_baseline else cpu_baseline(args)
+    peak = BF16_PEAK_TFLOPS if args.precision == "bf16" else FP32_PEAK_TFLOPS
+    mfu = st["flops"] / (st["ms"] * 1e-3) / 1e12 / peak
+    out = {
+        "metric": "train tokens/s, Qwen3-0.6B fwd+bwd+Adam",
+        "value": round(st["tokens_s"], 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(st["ms"], 3),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16" if args.precision == "bf16" else "fp32",
+        "data": "synthetic (random-init weights ~N(0,0.02), uniform token ids)",
+        "config": {"workload": "qwen3-0.6b full fine-tune step (BASELINE config 3)",
+                   "global_batch": st["T"], "seq_len": QWEN3_06B["n_pos"], "batch": 4,
+                   "layers": 28, "vocab": 151936, "tied_embeddings": True,
+                   "master_weights": "fp32", "optimizer": "adam",
+                   "parallelism": "single GPU"},
+        "step_tflops": round(st["flops"] / (st["ms"] * 1e-3) / 1e12, 1),
+        "step_mfu": round(mfu, 4),
+        "loss": [round(st["loss_first"], 4), round(st["loss_last"], 4)],
+        "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (BASELINE config 2)",
+                   "ms": round(fa["ms"], 4), "tflops": round(fa["tflops"], 1),
+                   "frac_bf16_peak": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4)},
+        "roofline": {"kernel": "fa_bw_d + fa_bwd_dkv + fa_bwd_dq (config 2)", "bound": "mfma",
+                     "achieved": round(fa["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

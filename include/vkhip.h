@@ -1,0 +1,381 @@
+/*
+ * vkhip — MI355X (gfx950) training backward path of valkyr, C ABI.
+ *
+ * Drop-in boundary for valkyr's transformer training step
+ * (src/train/transformer.zig `Runner`) and the kernels it records.  All entry
+ * points are `extern "C"`, take plain pointers and sizes, and return a
+ * `vkh_status`; no C++ or framework types cross the boundary.  A Zig host
+ * binds this header with `@cImport` / `extern fn`.
+ *
+ * Conventions
+ *   - Errors: `vkh_status`, mirroring the Zig error names of the reference;
+ *     `vkh_last_error()` returns a thread-local message for the last failure.
+ *   - Ownership: input pointers are borrowed; the runner owns its device memory.
+ *   - Threading: one runner per thread; a runner is never called concurrently.
+ *   - Streams: `vkh_stream` is a `hipStream_t` (NULL = the runner's own
+ *     stream for runner calls, the null stream for kernel calls).  Kernel
+ *     entry points only enqueue; runner `step`/`forward_logits`/checkpoint
+ *     calls are blocking like the reference's.
+ *   - Layout: weights are [N, K] row-major with y = x W^T; activations are
+ *     [T, dim] with T = n_seqs * n_pos rows; Q, O, dO are [T, n_heads, head_dim]
+ *     and K, V are [T, n_kv_heads, head_dim]; LSE and D are [T, n_heads].
+ */
+#ifndef VKHIP_H
+#define VKHIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t *vkh_stream;
+typedef struct ihipEvent_t *vkh_event;
+
+typedef enum vkh_status {
+    VKH_OK = 0,
+    VKH_ERR_INVALID_ARGUMENT = 1,
+    VKH_ERR_HIP = 2,               /* a HIP runtime call or kernel launch failed */
+    VKH_ERR_OUT_OF_MEMORY = 3,
+    VKH_ERR_UNSUPPORTED = 4,       /* shape outside what the kernels implement */
+    VKH_ERR_NO_DEVICE = 5,
+    /* Runner.step / forwardLogits: transformer.zig:1259-1260, :1326-1327 */
+    VKH_ERR_TOKEN_IDS_LEN = 10,
+    VKH_ERR_TARGET_LEN = 11,
+    VKH_ERR_OUT_LOGITS_LEN = 12,
+    VKH_ERR_TOKEN_OUT_OF_RANGE = 13,
+    /* Runner.init shape validation: transformer.zig:497-515 */
+    VKH_ERR_EMBED_SHAPE = 20,
+    VKH_ERR_FINAL_NORM_SHAPE = 21,
+    VKH_ERR_LM_HEAD_SHAPE = 22,
+    VKH_ERR_LAYER_COUNT = 23,
+    VKH_ERR_LAYER_N1_SHAPE = 24,
+    VKH_ERR_LAYER_Q_SHAPE = 25,
+    VKH_ERR_LAYER_K_SHAPE = 26,
+    VKH_ERR_LAYER_V_SHAPE = 27,
+    VKH_ERR_LAYER_O_SHAPE = 28,
+    VKH_ERR_LAYER_N2_SHAPE = 29,
+    VKH_ERR_LAYER_GATE_SHAPE = 30,
+    VKH_ERR_LAYER_UP_SHAPE = 31,
+    VKH_ERR_LAYER_DOWN_SHAPE = 32,
+    VKH_ERR_LAYER_Q_NORM_SHAPE = 33,
+    VKH_ERR_LAYER_K_NORM_SHAPE = 34,
+    VKH_ERR_LORA_RANK_ZERO = 35,
+    VKH_ERR_LORA_INIT_LEN = 36,
+    /* checkpoints: transformer.zig:1434-1440, :1480, :1527-1533 */
+    VKH_ERR_INVALID_CHECKPOINT_MAGIC = 40,
+    VKH_ERR_UNSUPPORTED_CHECKPOINT_VERSION = 41,
+    VKH_ERR_CHECKPOINT_CONFIG_SIZE_MISMATCH = 42,
+    VKH_ERR_CHECKPOINT_CONFIG_MISMATCH = 43,
+    VKH_ERR_END_OF_STREAM = 44,    /* truncated file (readNoEof) */
+    VKH_ERR_INVALID_LORA_CHECKPOINT_MAGIC = 45,
+    VKH_ERR_UNSUPPORTED_LORA_CHECKPOINT_VERSION = 46,
+    VKH_ERR_LORA_CHECKPOINT_CONFIG_SIZE_MISMATCH = 47,
+    VKH_ERR_LORA_CHECKPOINT_CONFIG_MISMATCH = 48,
+    VKH_ERR_LORA_CHECKPOINT_EMPTY = 49,
+    VKH_ERR_IO = 50
+} vkh_status;
+
+typedef enum vkh_precision {
+    VKH_PRECISION_FP32 = 0, /* fp32 operands on v_mfma_f32_16x16x4_f32 (reference numerics) */
+    VKH_PRECISION_BF16 = 1  /* bf16 operands, fp32 accumulate, fp32 master weights/optimizer */
+} vkh_precision;
+
+typedef enum vkh_dtype { VKH_F32 = 0, VKH_BF16 = 1 } vkh_dtype;
+
+/* LoRA target bits: transformer.zig:82-98 (LoraTarget). */
+enum {
+    VKH_LORA_Q = 1u << 0, VKH_LORA_K = 1u << 1, VKH_LORA_V = 1u << 2, VKH_LORA_O = 1u << 3,
+    VKH_LORA_GATE = 1u << 4, VKH_LORA_UP = 1u << 5, VKH_LORA_DOWN = 1u << 6,
+    VKH_LORA_ALL_ATTN = 0xFu, VKH_LORA_ALL_FFN = 0x70u, VKH_LORA_ALL = 0x7Fu
+};
+
+/* transformer.zig:31-77 (Config) plus three extensions at the end. */
+typedef struct vkh_config {
+    uint32_t dim, n_heads, n_kv_heads, head_dim, ff_dim;
+    uint32_t n_pos;            /* positions per sequence */
+    uint32_t n_layers, vocab_size;
+    float rms_eps;
+    uint32_t causal;
+    uint32_t rotary_dim;
+    float rope_theta;
+    uint32_t qk_norm;
+    float lr, beta1, beta2, eps_adam;
+    uint32_t lora_targets, lora_rank;
+    float lora_alpha, lora_lr_b_scale;
+    /* extensions */
+    uint32_t n_seqs;           /* sequences per step (0 means 1); T = n_seqs * n_pos */
+    uint32_t tied_embeddings;  /* lm_head aliases embed; grad = dE + dW_lm */
+    uint32_t precision;        /* vkh_precision */
+    uint32_t reserved;
+} vkh_config;
+
+/* A borrowed host fp32 tensor (a Zig slice: pointer + element count). */
+typedef struct vkh_tensor {
+    const float *data;
+    size_t len;
+} vkh_tensor;
+
+/* transformer.zig:113-127 (LayerWeights). */
+typedef struct vkh_layer_weights {
+    vkh_tensor w_n1, w_q, w_k, w_v, w_o, w_n2, w_gate, w_up, w_down, w_q_norm, w_k_norm;
+} vkh_layer_weights;
+
+/* transformer.zig:152-155 (LoraInitWeights). */
+typedef struct vkh_lora_init {
+    vkh_tensor a; /* [r, K_proj] */
+    vkh_tensor b; /* [N_proj, r] */
+} vkh_lora_init;
+
+/* transformer.zig:129-150 (InitWeights).  `lora[p]` is NULL (default init:
+ * A ~ N(0, 1/sqrt(r)) from a fixed seed, B = 0) or an array of n_layers. */
+typedef struct vkh_init_weights {
+    vkh_tensor embed, final_norm, lm_head;
+    const vkh_layer_weights *layers;
+    size_t n_layers;
+    const vkh_lora_init *lora[7];
+    size_t lora_len[7];
+} vkh_init_weights;
+
+typedef struct vkh_runner vkh_runner;
+
+/* Tensor addressing for get/set: stack-level tensors use layer = -1 and
+ * which = 0 embed, 1 final_norm, 2 lm_head; per-layer which = 0 n1, 1 q, 2 k,
+ * 3 v, 4 o, 5 n2, 6 gate, 7 up, 8 down, 9 q_norm, 10 k_norm; LoRA adapters
+ * which = 16 + 2 * proj (A) and 17 + 2 * proj (B), proj = 0..6 (q..down). */
+typedef enum vkh_kind { VKH_PARAM = 0, VKH_GRAD = 1, VKH_ADAM_M = 2, VKH_ADAM_V = 3 } vkh_kind;
+
+/* ── runner (transformer.zig Runner) ─────────────────────────────────── */
+
+/* Runner.init (transformer.zig:482).  `weights` may be NULL: matrices start
+ * at zero and norm gains at one, to be filled with vkh_runner_set_tensor or
+ * vkh_runner_init_random. */
+vkh_status vkh_runner_create(const vkh_config *cfg, const vkh_init_weights *weights,
+                             vkh_runner **out);
+/* Runner.deinit (transformer.zig:1125) */
+void vkh_runner_destroy(vkh_runner *r);
+/* Device-side deterministic random init of the synthetic configs: matrices
+ * ~N(0, std), norm gains 1, LoRA A ~N(0, lora_std), B = 0. */
+vkh_status vkh_runner_init_random(vkh_runner *r, uint64_t seed, float std, float lora_std);
+
+/* Runner.step (transformer.zig:1257): one Adam step on n_seqs * n_pos
+ * tokens; blocking; step_t += 1 afterwards. */
+vkh_status vkh_runner_step(vkh_runner *r, const uint32_t *token_ids, size_t n_tokens,
+                           const uint32_t *target_ids, size_t n_targets);
+/* The same step enqueued on `stream` without waiting (NULL = runner stream). */
+vkh_status vkh_runner_step_async(vkh_runner *r, const uint32_t *token_ids, size_t n_tokens,
+                                 const uint32_t *target_ids, size_t n_targets,
+                                 vkh_stream stream);
+/* Mean CE loss of the last completed step (waits for it). */
+vkh_status vkh_runner_last_loss(vkh_runner *r, float *loss);
+/* Runner.forwardLogits (transformer.zig:1324): logits [T, vocab] fp32. */
+vkh_status vkh_runner_forward_logits(vkh_runner *r, const uint32_t *token_ids, size_t n_tokens,
+                                     float *out_logits, size_t out_len);
+/* Forward + loss + backward only (grads written, Adam not applied). */
+vkh_status vkh_runner_forward_backward(vkh_runner *r, const uint32_t *token_ids,
+                                       size_t n_tokens, const uint32_t *target_ids,
+                                       size_t n_targets);
+vkh_status vkh_runner_synchronize(vkh_runner *r);
+
+uint32_t vkh_runner_step_t(const vkh_runner *r);
+vkh_status vkh_runner_set_step_t(vkh_runner *r, uint32_t step_t);
+float vkh_runner_get_lr(const vkh_runner *r);
+vkh_status vkh_runner_set_lr(vkh_runner *r, float lr); /* cfg.lr is mutable between steps */
+vkh_status vkh_runner_get_config(const vkh_runner *r, vkh_config *out);
+size_t vkh_runner_param_count(const vkh_runner *r);          /* trainable params */
+size_t vkh_runner_device_bytes(const vkh_runner *r);
+
+/* Tensor access (host <-> device copies, blocking). */
+vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int which,
+                                   size_t *numel);
+vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, float *host,
+                                 size_t numel);
+vkh_status vkh_runner_set_tensor(vkh_runner *r, int kind, int layer, int which,
+                                 const float *host, size_t numel);
+/* Device pointer of a tensor (valid until vkh_runner_destroy). */
+vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int which,
+                                        float **dptr, size_t *numel);
+
+/* Checkpoints, byte layout of transformer.zig:157-205, :1390-1655:
+ * 16-byte header {magic, version 1, step_t, cfg_size} + config bytes +
+ * positional fp32 blobs (.vkpt: (param, m, v) per tensor in collectBlobs
+ * order; .lvkpt: (A, mA, vA, B, mB, vB) per enabled projection and layer). */
+vkh_status vkh_runner_save_checkpoint(vkh_runner *r, const char *path);
+vkh_status vkh_runner_load_checkpoint(vkh_runner *r, const char *path);
+vkh_status vkh_runner_save_lora_checkpoint(vkh_runner *r, const char *path);
+vkh_status vkh_runner_load_lora_checkpoint(vkh_runner *r, const char *path);
+
+/* ── cooperative per-frame API (shape of runner.zig:129-176, :904-986) ── */
+typedef enum vkh_budget_mode {
+    VKH_BUDGET_STEPS = 0,
+    VKH_BUDGET_MICROSECONDS = 1,
+    VKH_BUDGET_EITHER = 2
+} vkh_budget_mode;
+
+typedef struct vkh_train_budget {
+    uint32_t mode;         /* vkh_budget_mode */
+    uint32_t steps;        /* max steps this tick */
+    uint64_t microseconds; /* max host enqueue time this tick */
+} vkh_train_budget;
+
+typedef struct vkh_tick_result {
+    uint32_t steps_completed; /* steps enqueued this tick */
+    uint32_t has_loss;        /* last_loss valid (one-tick latency) */
+    float last_loss;
+    uint32_t idle;            /* loss target reached: nothing enqueued */
+    uint64_t elapsed_us;
+} vkh_tick_result;
+
+/* runner.zig:797 uploadTrainBatch: the batch the following ticks train on. */
+vkh_status vkh_runner_upload_train_batch(vkh_runner *r, const uint32_t *token_ids,
+                                         size_t n_tokens, const uint32_t *target_ids,
+                                         size_t n_targets);
+/* runner.zig:61-68 LossDecay target: ticks go idle once last_loss <= target
+ * (target <= 0 disables). */
+vkh_status vkh_runner_set_loss_target(vkh_runner *r, float target);
+/* runner.zig:904 tickFrameTrain: enqueue up to the budget of steps on the
+ * caller's stream and return without waiting; the loss of the previous tick
+ * is reported once its copy has landed. */
+vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
+                                       vkh_train_budget budget, vkh_tick_result *out);
+
+/* ── kernels (device pointers; enqueue on `stream`) ─────────────────── */
+
+/* Attention shape shared by the FA entry points: FaForwardPush,
+ * FaBwDPush, FaBwDqPush, FaBwDkvPush (runtime.zig:377-416) plus n_batch
+ * (sequences stacked along rows, block-diagonal attention). */
+typedef struct vkh_attn_params {
+    uint32_t n_batch, n_q, n_kv, n_heads, n_kv_heads, head_dim;
+    uint32_t causal;
+    float inv_sqrt_dim;
+    uint32_t dtype; /* vkh_dtype of q, k, v, dO; bf16 requires head_dim 64 or 128 */
+} vkh_attn_params;
+
+/* shaders/fa_forward.comp (write_lse = 1 when lse != NULL): O fp32. */
+vkh_status vkh_fa_forward(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                          float *o, float *lse, vkh_stream stream);
+/* shaders/fa_bw_d.comp: D[t, h] = sum_d O * dO.  With p->dtype == bf16, dO is
+ * fp32 and `dout_bf16` (if non-NULL) receives its bf16 copy, D pairing with it. */
+vkh_status vkh_fa_bw_d(const vkh_attn_params *p, const float *o, const float *dout, float *d,
+                       void *dout_bf16, vkh_stream stream);
+/* shaders/fa_bw_dq.comp: dQ fp32 (overwrite). */
+vkh_status vkh_fa_bw_dq(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                        const void *dout, const float *lse, const float *d, float *dq,
+                        vkh_stream stream);
+/* shaders/fa_bw_dkv.comp: dK, dV fp32 (overwrite), GQA fold inside. */
+vkh_status vkh_fa_bw_dkv(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                         const void *dout, const float *lse, const float *d, float *dk,
+                         float *dv, vkh_stream stream);
+
+/* shaders/matmul_nt_v2.comp (MatmulPush {m, n, k}): y[M,N] = x[M,K] w[N,K]^T. */
+vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,
+                         uint32_t K, uint32_t precision, vkh_stream stream);
+/* shaders/linear_backward_dx_batched.comp (LinearBatchedPush {M, N, K}):
+ * dx[M,K] = dy[M,N] w[N,K]  (overwrite). */
+vkh_status vkh_linear_backward_dx(const float *dy, const float *w, float *dx, uint32_t M,
+                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream);
+/* shaders/linear_backward_dw_batched.comp: dw[N,K] = dy[M,N]^T x[M,K]  (overwrite). */
+vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, uint32_t M,
+                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream);
+
+/* train/lora.zig:99-129: y = x w^T + (alpha/r) (x a^T) b^T; inter = x a^T. */
+vkh_status vkh_lora_forward(const float *x, const float *w, const float *a, const float *b,
+                            float *y, float *inter, uint32_t M, uint32_t N, uint32_t K,
+                            uint32_t r, float alpha_over_r, uint32_t precision,
+                            vkh_stream stream);
+/* train/lora.zig:137-251: dx = dy w + (alpha/r) (dy b) a (overwrite, if dx);
+ * dA = (alpha/r) (dy b)^T x;  dB = (alpha/r) dy^T inter  (overwrite). */
+vkh_status vkh_lora_backward(const float *dy, const float *x, const float *w, const float *a,
+                             const float *b, const float *inter, float *dx, float *dA,
+                             float *dB, uint32_t M, uint32_t N, uint32_t K, uint32_t r,
+                             float alpha_over_r, uint32_t precision, vkh_stream stream);
+
+/* CceForwardPush / CceBackwardPush {N, V, D, z_loss, label_smoothing}
+ * (runtime.zig:484-496). */
+typedef struct vkh_cce_params {
+    uint32_t n, vocab, dim;
+    float z_loss_scale, label_smoothing;
+    uint32_t precision;
+} vkh_cce_params;
+/* shaders/cce_forward.comp: lse[n], loss_row[n] (and the mean if non-NULL). */
+vkh_status vkh_cce_forward(const vkh_cce_params *p, const float *h, const float *w,
+                           const uint32_t *targets, float *lse, float *loss_row,
+                           float *loss_mean, vkh_stream stream);
+/* shaders/cce_backward_dh.comp + cce_backward_dw.comp in one pass:
+ * dh overwritten (if non-NULL); dw += (accumulate_dw) or = dz^T h (if non-NULL). */
+vkh_status vkh_cce_backward(const vkh_cce_params *p, const float *h, const float *w,
+                            const uint32_t *targets, const float *lse, float *dh, float *dw,
+                            uint32_t accumulate_dw, vkh_stream stream);
+
+/* shaders/rmsnorm.comp (RmsnormPush {dim, eps, gemma_quirk}) */
+vkh_status vkh_rmsnorm_forward(const float *x, const float *w, float *y, uint32_t n_rows,
+                               uint32_t dim, float eps, uint32_t gemma_quirk, vkh_stream stream);
+/* shaders/rmsnorm_backward.comp with the gain gradient reduced on the GPU:
+ * dx [n_rows, dim] (+ residual if non-NULL), dw [dim] (overwrite, if non-NULL). */
+vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
+                                const float *residual, float *dw, uint32_t n_rows, uint32_t dim,
+                                float eps, uint32_t gemma_quirk, vkh_stream stream);
+/* shaders/swiglu_forward.comp / swiglu_backward.comp (SwigluPush {n}) */
+vkh_status vkh_swiglu_forward(const float *pre_gate, const float *up, float *gated, size_t n,
+                              vkh_stream stream);
+vkh_status vkh_swiglu_backward(const float *d_gated, const float *pre_gate, const float *up,
+                               float *d_pre_gate, float *d_up, size_t n, vkh_stream stream);
+/* shaders/qk_rope_partial_batched.comp / qk_rope_backward_batched.comp
+ * (QkRopeBatchedPush, runtime.zig:221-228) + seq_len: position = row % seq_len. */
+typedef struct vkh_rope_params {
+    uint32_t n_pos, n_q_heads, n_kv_heads, head_dim, rotary_dim;
+    float theta_base;
+    uint32_t seq_len; /* 0 means n_pos */
+} vkh_rope_params;
+vkh_status vkh_qk_rope_forward(const vkh_rope_params *p, const float *q_in, float *q_out,
+                               const float *k_in, float *k_out, vkh_stream stream);
+vkh_status vkh_qk_rope_backward(const vkh_rope_params *p, const float *dq_out, float *dq_in,
+                                const float *dk_out, float *dk_in, vkh_stream stream);
+/* shaders/embed_lookup_batched.comp (EmbedLookupBatchedPush {dim, n_pos, scale}) */
+vkh_status vkh_embed_lookup(const float *embed, const uint32_t *ids, float *out, uint32_t n_pos,
+                            uint32_t dim, float scale, vkh_stream stream);
+/* shaders/embedding_backward.comp (EmbeddingBackwardPush {dim, n_pos, vocab}):
+ * dE[tok] += sum of dy rows holding tok (position order); other rows untouched.
+ * n_pos <= 16384. */
+vkh_status vkh_embedding_backward(const float *dy, const uint32_t *ids, float *dE,
+                                  uint32_t n_pos, uint32_t dim, uint32_t vocab,
+                                  vkh_stream stream);
+/* shaders/adam_step.comp (AdamStepPush {n, lr, beta1, beta2, eps, t, wd}) */
+vkh_status vkh_adam_step(float *param, const float *grad, float *m, float *v, size_t n, float lr,
+                         float beta1, float beta2, float eps, uint32_t t, float weight_decay,
+                         vkh_stream stream);
+/* shaders/add_in_place.comp, vec_add.comp, scale.comp */
+vkh_status vkh_add_in_place(float *dst, const float *src, size_t n, vkh_stream stream);
+vkh_status vkh_vec_add(const float *a, const float *b, float *c, size_t n, vkh_stream stream);
+vkh_status vkh_scale(const float *in, float *out, size_t n, float scale, vkh_stream stream);
+vkh_status vkh_cast_f32_to_bf16(const float *in, void *out, size_t n, vkh_stream stream);
+
+/* ── device memory, streams, events (HIP plumbing for hosts without HIP) ── */
+vkh_status vkh_device_count(int *count);
+vkh_status vkh_set_device(int device);
+vkh_status vkh_malloc(void **ptr, size_t bytes);
+vkh_status vkh_free(void *ptr);
+vkh_status vkh_memcpy_h2d(void *dst, const void *src, size_t bytes);
+vkh_status vkh_memcpy_d2h(void *dst, const void *src, size_t bytes);
+vkh_status vkh_memset(void *ptr, int value, size_t bytes);
+vkh_status vkh_device_synchronize(void);
+vkh_status vkh_stream_create(vkh_stream *out);
+vkh_status vkh_stream_destroy(vkh_stream s);
+vkh_status vkh_stream_synchronize(vkh_stream s);
+vkh_status vkh_event_create(vkh_event *out);
+vkh_status vkh_event_destroy(vkh_event e);
+vkh_status vkh_event_record(vkh_event e, vkh_stream s);
+vkh_status vkh_event_synchronize(vkh_event e);
+vkh_status vkh_event_elapsed_ms(vkh_event start, vkh_event stop, float *ms);
+
+const char *vkh_last_error(void);
+const char *vkh_status_name(vkh_status s);
+/* "gfx950" build info; 0 on success. */
+const char *vkh_build_info(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* VKHIP_H */

@@ -1,0 +1,101 @@
+"""CPU-side checks of the C ABI: the library loads, exports every symbol
+include/vkhip.h declares, the Python binding covers them all, and host-side
+argument validation works without a GPU."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "vkhip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vkh_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_compiles_as_c_and_cpp(tmp_path):
+    src = tmp_path / "t.c"
+    src.write_text('#include "vkhip.h"\nint main(void){ vkh_config c = {0}; (void)c; return 0; }\n')
+    for cc, flag in (("gcc", "-std=c99"), ("g++", "-std=c++17")):
+        out = tmp_path / f"t_{cc}"
+        r = subprocess.run([cc, flag, "-Wall", "-Werror", "-I", os.path.dirname(HEADER),
+                            "-x", "c" if cc == "gcc" else "c++", str(src), "-o", str(out)],
+                           capture_output=True, text=True)
+        assert r.returncode == 0, r.stderr
+
+
+def test_library_exports_every_declared_symbol():
+    from valkyr_amd._lib import LIB_PATH, lib
+
+    lib()  # loads
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB_PATH], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (vkh_[a-z0-9_]+)", out))
+    missing = [f for f in declared_functions() if f not in exported]
+    assert not missing, missing
+
+
+def test_binding_covers_every_declared_symbol():
+    from valkyr_amd._lib import SIGNATURES
+
+    bound = {name for name, _, _ in SIGNATURES}
+    assert set(declared_functions()) == bound
+
+
+def test_config_struct_layout_matches_header(tmp_path):
+    """sizeof/offsets of the ABI structs agree between C and ctypes."""
+    from valkyr_amd import _lib as L
+
+    structs = {"vkh_config": L.Config, "vkh_attn_params": L.AttnParams,
+               "vkh_cce_params": L.CceParams, "vkh_rope_params": L.RopeParams,
+               "vkh_train_budget": L.TrainBudget, "vkh_tick_result": L.TickResult,
+               "vkh_init_weights": L.InitWeights, "vkh_layer_weights": L.LayerWeights}
+    body = "\n".join(f'printf("%s %zu\\n", "{n}", sizeof({n}));' for n in structs)
+    src = tmp_path / "s.c"
+    src.write_text(f'#include <stdio.h>\n#include "vkhip.h"\nint main(void){{ {body} return 0; }}\n')
+    exe = tmp_path / "s"
+    subprocess.run(["gcc", "-I", os.path.dirname(HEADER), str(src), "-o", str(exe)], check=True)
+    sizes = dict(line.split() for line in subprocess.run([str(exe)], capture_output=True,
+                                                          text=True, check=True).stdout.split("\n") if line)
+    for n, cls in structs.items():
+        assert int(sizes[n]) == C.sizeof(cls), n
+
+
+def test_status_names_match():
+    from valkyr_amd._lib import STATUS, lib
+
+    for code, name in STATUS.items():
+        assert lib().vkh_status_name(code).decode() == name
+
+
+def test_invalid_arguments_rejected_on_host():
+    """Argument validation happens before any device work."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd._lib import VkhError
+
+    with pytest.raises(VkhError) as e:
+        K.fa_forward(K.attn_params(4, 4, 3, 2, 16), None, None, None, None)  # 3 % 2 != 0
+    assert e.value.name == "InvalidArgument"
+    with pytest.raises(VkhError) as e:
+        K.fa_forward(K.attn_params(8, 4, 4, 2, 16, causal=True), 1, 1, 1, 1)  # n_q > n_kv
+    assert e.value.name == "InvalidArgument"
+    with pytest.raises(VkhError) as e:
+        K.fa_forward(K.attn_params(8, 8, 4, 2, 96, dtype=K.BF16), 1, 1, 1, 1)
+    assert e.value.name == "Unsupported"
+
+
+def test_runner_without_device_reports_no_device():
+    import valkyr_amd as v
+
+    if v.device_count() > 0:
+        pytest.skip("a GPU is present")
+    cfg = v.make_config(dim=16, n_heads=2, n_kv_heads=1, head_dim=8, ff_dim=32, n_pos=4,
+                        n_layers=1, vocab_size=8)
+    with pytest.raises(v.VkhError) as e:
+        v.Runner(cfg)
+    assert e.value.name == "NoDevice"

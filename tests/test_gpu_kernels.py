@@ -1,0 +1,402 @@
+"""Per-kernel parity of the HIP kernels (through the C ABI) against the C
+oracle on identical seeded inputs.
+
+Bars: bit-exact for integer / index work (embedding
+scatter targets, token gather), rel-L2 <= 1e-3 for fp32, rel-L2 <= 1e-2 for
+bf16-operand contractions (compared with the oracle run on the same
+bf16-rounded inputs).  Elementwise kernels that restate the reference formula
+with identical fp32 rounding are held to much tighter bounds where that holds.
+"""
+import math
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import bf16_dev, dev, grel, host, note, rel_l2, zeros
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-3
+BF16_TOL = 1e-2
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _gpu():
+    import valkyr_amd as v
+
+    assert v.device_count() > 0, "no GPU visible"
+    note(f"[gpu] {v.lib().vkh_build_info().decode()}")
+
+
+# ── bandwidth kernels ────────────────────────────────────────────────────
+
+def test_rmsnorm_forward_backward_fused_dw():
+    from valkyr_amd import kernels as K
+
+    for rows, dim in ((128, 256), (2048, 1024), (300, 128), (7, 96)):
+        note(f"rmsnorm rows={rows} dim={dim}")
+        x = O.normal(rows * dim, 1)
+        w = O.uniform(dim, 2, 0.5, 1.5)
+        dy = O.normal(rows * dim, 3)
+        res = O.normal(rows * dim, 4)
+        y_ref = O.rmsnorm_forward(x, w, 1e-6)
+        dx_ref, dw_ref = O.rmsnorm_backward(dy, x, w, 1e-6)
+        bx, bw, bdy, bres = dev(x), dev(w), dev(dy), dev(res)
+        by, bdx, bdw = zeros(rows * dim), zeros(rows * dim), zeros(dim)
+        K.rmsnorm_forward(bx, bw, by, rows, dim, 1e-6)
+        K.rmsnorm_backward(bdy, bx, bw, bdx, bdw, rows, dim, 1e-6, residual=bres)
+        y, dx, dw = host(by), host(bdx), host(bdw)
+        assert grel(y_ref, y) < 1e-6
+        assert grel(dx_ref + res, dx) < 1e-5
+        assert rel_l2(dw_ref, dw) < 1e-5
+
+
+def test_swiglu_forward_backward():
+    from valkyr_amd import kernels as K
+
+    for n in (2048 * 3072, 1001):
+        z, u, dg = O.normal(n, 11, 2.0), O.normal(n, 12), O.normal(n, 13)
+        g_ref = O.swiglu_forward(z, u)
+        dz_ref, du_ref = O.swiglu_backward(dg, z, u)
+        bz, bu, bdg = dev(z), dev(u), dev(dg)
+        bg, bdz, bdu = zeros(n), zeros(n), zeros(n)
+        K.swiglu_forward(bz, bu, bg, n)
+        K.swiglu_backward(bdg, bz, bu, bdz, bdu, n)
+        assert grel(g_ref, host(bg)) < 1e-6
+        assert grel(dz_ref, host(bdz)) < 1e-6
+        assert grel(du_ref, host(bdu)) < 1e-6
+
+
+@pytest.mark.parametrize("rot", [128, 64])
+def test_qk_rope_forward_backward(rot):
+    from valkyr_amd import kernels as K
+
+    S, B, Hq, Hkv, hd, theta = 512, 2, 4, 2, 128, 1e6
+    n = S * B
+    q, k = O.normal(n * Hq * hd, 21), O.normal(n * Hkv * hd, 22)
+    q_ref = O.rope_forward(q, n, Hq, hd, rot, theta, S)
+    k_ref = O.rope_forward(k, n, Hkv, hd, rot, theta, S)
+    dq_ref = O.rope_backward(q, n, Hq, hd, rot, theta, S)
+    dk_ref = O.rope_backward(k, n, Hkv, hd, rot, theta, S)
+    p = K.rope_params(n, Hq, Hkv, hd, rot, theta, S)
+    bq, bk = dev(q), dev(k)
+    oq, ok = zeros(q.size), zeros(k.size)
+    K.qk_rope_forward(p, bq, oq, bk, ok)
+    assert grel(q_ref, host(oq)) < 1e-6 and grel(k_ref, host(ok)) < 1e-6
+    K.qk_rope_backward(p, bq, oq, bk, ok)
+    assert grel(dq_ref, host(oq)) < 1e-6 and grel(dk_ref, host(ok)) < 1e-6
+
+
+def test_embed_lookup_is_exact_gather():
+    from valkyr_amd import kernels as K
+
+    V, D, n = 4096, 256, 300
+    E = O.normal(V * D, 31)
+    ids = O.ids(n, 32, V)
+    out = zeros(n * D)
+    K.embed_lookup(dev(E), dev(ids), out, n, D)
+    assert np.array_equal(host(out), O.embedding_forward(E, ids, D))
+
+
+@pytest.mark.parametrize("n,V,D", [(6, 16, 5), (2048, 151936, 1024), (8192, 4096, 64)])
+def test_embedding_backward_bit_exact(n, V, D):
+    """gpu_train.zig:4845-4930: exact scatter targets and position-order sums."""
+    from valkyr_amd import kernels as K
+
+    ids = np.array([3, 7, 3, 11, 7, 3], np.uint32) if n == 6 else O.ids(n, 41, V)
+    if n == 8192:
+        ids = (ids % 97).astype(np.uint32)  # heavy duplication
+    dy = O.normal(n * D, 42)
+    base = O.normal(V * D, 43) if n == 6 else np.zeros(V * D, np.float32)
+    # embedding_backward.comp:41-46 sums a token's rows in position order and then
+    # adds the sum once (dE += acc); the CPU oracle scatter-adds into a zeroed dE,
+    # which is the same value when dE starts at zero (as in Runner.step)
+    sums = O.embedding_backward(dy, ids, V, D)
+    touched = np.zeros(V, bool)
+    touched[ids] = True
+    ref = base.copy().reshape(V, D)
+    ref[touched] = ref[touched] + sums.reshape(V, D)[touched]
+    ref = ref.ravel()
+    bE = dev(base)
+    K.embedding_backward(dev(dy), dev(ids), bE, n, D, V)
+    got = host(bE)
+    assert np.array_equal(got, ref), "embedding backward is not bit-exact"
+
+
+def test_adam_matches_shader_formula():
+    from valkyr_amd import kernels as K
+
+    n = 1_000_003
+    p, g = O.normal(n, 51), O.normal(n, 52, 1e-2)
+    m, v = O.normal(n, 53, 1e-3), np.abs(O.normal(n, 54, 1e-5))
+    bp, bg, bm, bv = dev(p), dev(g), dev(m), dev(v)
+    for t in (1, 2, 7):
+        O.adam_step(p, g, m, v, 1e-3, 0.9, 0.999, 1e-8, t)
+        K.adam_step(bp, bg, bm, bv, n, 1e-3, 0.9, 0.999, 1e-8, t)
+    assert grel(m, host(bm)) < 1e-6
+    assert grel(v, host(bv)) < 1e-6
+    assert rel_l2(p, host(bp)) < 1e-6
+
+
+# ── GEMMs ────────────────────────────────────────────────────────────────
+
+GEMM_SHAPES = [(128, 256, 256), (2048, 1024, 1024), (257, 130, 72), (64, 16, 96)]
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("shape", GEMM_SHAPES)
+def test_linear_gemms(prec, shape):
+    from valkyr_amd import kernels as K
+
+    M, N, Kd = shape
+    note(f"gemm prec={prec} M={M} N={N} K={Kd}")
+    x, W, dy = O.normal(M * Kd, 61), O.normal(N * Kd, 62, 0.05), O.normal(M * N, 63)
+    if prec == 1:
+        x, W, dy = O.round_bf16(x), O.round_bf16(W), O.round_bf16(dy)
+    y_ref = (x.astype(np.float64).reshape(M, Kd) @ W.astype(np.float64).reshape(N, Kd).T).ravel()
+    dx_ref, dW_ref = O.linear_backward(dy, x, W, M, N, Kd)
+    bx, bW, bdy = dev(x), dev(W), dev(dy)
+    by, bdx, bdW = zeros(M * N), zeros(M * Kd), zeros(N * Kd)
+    K.matmul_nt(bx, bW, by, M, N, Kd, prec)
+    K.linear_backward_dx(bdy, bW, bdx, M, N, Kd, prec)
+    K.linear_backward_dw(bdy, bx, bdW, M, N, Kd, prec)
+    tol = 1e-5  # operands already bf16-exact, accumulation fp32 in both precisions
+    assert rel_l2(y_ref, host(by)) < tol
+    assert rel_l2(dx_ref, host(bdx)) < tol
+    assert rel_l2(dW_ref, host(bdW)) < tol
+
+
+def test_gemm_bf16_rounding_within_north_star_tolerance():
+    """bf16-operand GEMM on fp32 inputs vs the fp32 oracle: rel-L2 <= 1e-2."""
+    from valkyr_amd import kernels as K
+
+    M, N, Kd = 512, 768, 1024
+    x, W = O.normal(M * Kd, 64), O.normal(N * Kd, 65, 0.02)
+    y_ref = O.matmul_nt(x, W, M, N, Kd)
+    by = zeros(M * N)
+    K.matmul_nt(dev(x), dev(W), by, M, N, Kd, 1)
+    e = rel_l2(y_ref, host(by))
+    note(f"bf16 gemm rel-L2 vs fp32 oracle: {e:.2e}")
+    assert e < BF16_TOL
+
+
+@pytest.mark.parametrize("prec", [0, 1])
+def test_lora_forward_backward(prec):
+    from valkyr_amd import kernels as K
+
+    M, N, Kd, r, aor = 256, 384, 256, 16, 2.0
+    x, w = O.normal(M * Kd, 71), O.normal(N * Kd, 72, 0.05)
+    a, b = O.normal(r * Kd, 73, 0.05), O.normal(N * r, 74, 0.05)
+    dy = O.normal(M * N, 75)
+    if prec == 1:
+        x, w, a, b, dy = (O.round_bf16(t) for t in (x, w, a, b, dy))
+    y_ref, inter_ref = O.lora_forward(x, w, a, b, M, N, Kd, r, aor)
+    dx_ref, dA_ref, dB_ref = O.lora_backward(dy, x, w, a, b, inter_ref, M, N, Kd, r, aor)
+    bx, bw, ba, bb, bdy = dev(x), dev(w), dev(a), dev(b), dev(dy)
+    by, binter = zeros(M * N), zeros(M * r)
+    K.lora_forward(bx, bw, ba, bb, by, binter, M, N, Kd, r, aor, prec)
+    bdx, bdA, bdB = zeros(M * Kd), zeros(r * Kd), zeros(N * r)
+    K.lora_backward(bdy, bx, bw, ba, bb, binter, bdx, bdA, bdB, M, N, Kd, r, aor, prec)
+    tol = FP32_TOL if prec == 0 else BF16_TOL
+    assert rel_l2(y_ref, host(by)) < tol
+    assert rel_l2(inter_ref, host(binter)) < tol
+    assert rel_l2(dx_ref, host(bdx)) < tol
+    assert rel_l2(dA_ref, host(bdA)) < tol
+    assert rel_l2(dB_ref, host(bdB)) < tol
+
+
+def test_lora_b_zero_gives_zero_dA_on_gpu():
+    from valkyr_amd import kernels as K
+
+    M, N, Kd, r = 64, 128, 64, 16
+    x, w, a = O.normal(M * Kd, 76), O.normal(N * Kd, 77), O.normal(r * Kd, 78)
+    b = np.zeros(N * r, np.float32)
+    dy = O.normal(M * N, 79)
+    bx, bw, ba, bb = dev(x), dev(w), dev(a), dev(b)
+    by, bi = zeros(M * N), zeros(M * r)
+    K.lora_forward(bx, bw, ba, bb, by, bi, M, N, Kd, r, 2.0)
+    bdA, bdB = zeros(r * Kd), zeros(N * r)
+    K.lora_backward(dev(dy), bx, bw, ba, bb, bi, None, bdA, bdB, M, N, Kd, r, 2.0)
+    assert np.all(host(bdA) == 0)
+    assert np.any(host(bdB) != 0)
+
+
+# ── CCE ──────────────────────────────────────────────────────────────────
+
+@pytest.mark.parametrize("prec", [0, 1])
+@pytest.mark.parametrize("n,V,D,zl,ls", [(128, 4096, 256, 0.0, 0.0), (64, 5000, 128, 1e-4, 0.1),
+                                         (33, 1000, 64, 0.0, 0.0)])
+def test_cce_forward_backward(prec, n, V, D, zl, ls):
+    from valkyr_amd import kernels as K
+
+    note(f"cce prec={prec} n={n} V={V} D={D}")
+    h, w = O.normal(n * D, 81), O.normal(V * D, 82, 0.05)
+    if prec == 1:
+        h, w = O.round_bf16(h), O.round_bf16(w)
+    t = O.ids(n, 83, V)
+    loss_ref, lse_ref, row_ref = O.cce_forward(h, w, t, n, V, D, 1024, zl, ls)
+    dh_ref, dW_ref = O.cce_backward(h, w, t, lse_ref, n, V, D, 1024, zl, ls)
+    p = K.cce_params(n, V, D, zl, ls, prec)
+    bh, bw, bt = dev(h), dev(w), dev(t)
+    blse, brow, bmean = zeros(n), zeros(n), zeros(1)
+    K.cce_forward(p, bh, bw, bt, blse, brow, bmean)
+    assert grel(lse_ref, host(blse)) < 1e-5
+    assert grel(row_ref, host(brow)) < 1e-4
+    assert abs(host(bmean)[0] - loss_ref) < 1e-4 * abs(loss_ref)
+    bdh, bdW = zeros(n * D), zeros(V * D)
+    K.cce_backward(p, bh, bw, bt, blse, bdh, bdW)
+    tol = FP32_TOL if prec == 0 else BF16_TOL
+    assert rel_l2(dh_ref, host(bdh)) < tol
+    assert rel_l2(dW_ref, host(bdW)) < tol
+
+
+# ── FlashAttention ───────────────────────────────────────────────────────
+
+FA_F32_CASES = [  # smoke/cpu.zig:909-916 shapes (n_q, n_kv, H, Hkv, hd, causal) + batch
+    (4, 4, 4, 2, 16, True, 1), (16, 16, 16, 8, 128, True, 1), (8, 8, 8, 2, 256, True, 1),
+    (10, 12, 4, 2, 16, True, 1), (8, 8, 4, 1, 16, True, 1), (4, 8, 4, 2, 16, False, 1),
+    (128, 128, 4, 2, 64, True, 3),
+]
+
+
+def _fa_oracle(Q, K_, V_, dO, B, n_q, n_kv, H, Hkv, hd, causal):
+    outs, lses, dqs, dks, dvs = [], [], [], [], []
+    for b in range(B):
+        q = Q[b * n_q * H * hd:(b + 1) * n_q * H * hd]
+        k = K_[b * n_kv * Hkv * hd:(b + 1) * n_kv * Hkv * hd]
+        v = V_[b * n_kv * Hkv * hd:(b + 1) * n_kv * Hkv * hd]
+        do = dO[b * n_q * H * hd:(b + 1) * n_q * H * hd]
+        o, lse = O.flash_forward(q, k, v, n_q, n_kv, H, Hkv, hd, causal)
+        dq, dk, dv = O.flash_backward(q, k, v, o, do, lse, n_q, n_kv, H, Hkv, hd, causal)
+        outs.append(o); lses.append(lse); dqs.append(dq); dks.append(dk); dvs.append(dv)
+    c = np.concatenate
+    return c(outs), c(lses), c(dqs), c(dks), c(dvs)
+
+
+def _run_fa_gpu(p, qb, kb, vb, O_, dO_b, dO_f32, lse, B, n_q, n_kv, H, Hkv, hd, bf16_do=None):
+    from valkyr_amd import kernels as K
+
+    nq, nk = B * n_q * H * hd, B * n_kv * Hkv * hd
+    bo, blse = zeros(nq), zeros(B * n_q * H)
+    K.fa_forward(p, qb, kb, vb, bo, blse)
+    bd = zeros(B * n_q * H)
+    K.fa_bw_d(p, dev(O_), dO_f32, bd, bf16_do)
+    bdq, bdk, bdv = zeros(nq), zeros(nk), zeros(nk)
+    lse_b = dev(lse)
+    K.fa_bw_dkv(p, qb, kb, vb, dO_b, lse_b, bd, bdk, bdv)
+    K.fa_bw_dq(p, qb, kb, vb, dO_b, lse_b, bd, bdq)
+    return host(bo), host(blse), host(bd), host(bdq), host(bdk), host(bdv)
+
+
+@pytest.mark.parametrize("case", FA_F32_CASES)
+def test_flash_attention_fp32(case):
+    from valkyr_amd import kernels as K
+
+    n_q, n_kv, H, Hkv, hd, causal, B = case
+    note(f"fa fp32 {case}")
+    Q = O.uniform(B * n_q * H * hd, 91, -0.5, 0.5)
+    Kk = O.uniform(B * n_kv * Hkv * hd, 92, -0.5, 0.5)
+    Vv = O.uniform(B * n_kv * Hkv * hd, 93, -0.5, 0.5)
+    dO = O.uniform(B * n_q * H * hd, 94, -0.5, 0.5)
+    o_r, lse_r, dq_r, dk_r, dv_r = _fa_oracle(Q, Kk, Vv, dO, B, n_q, n_kv, H, Hkv, hd, causal)
+    p = K.attn_params(n_q, n_kv, H, Hkv, hd, causal, B, K.F32)
+    bdo = dev(dO)
+    o, lse, d, dq, dk, dv = _run_fa_gpu(p, dev(Q), dev(Kk), dev(Vv), o_r, bdo, bdo, lse_r, B, n_q,
+                                        n_kv, H, Hkv, hd)
+    assert grel(o_r, o) < 1e-4 and grel(lse_r, lse) < 1e-5
+    assert rel_l2(O.fa_bw_d(o_r, dO, B * n_q, H, hd), d) < 1e-6
+    assert grel(dq_r, dq) < 1e-4, grel(dq_r, dq)
+    assert grel(dk_r, dk) < 1e-4, grel(dk_r, dk)
+    assert grel(dv_r, dv) < 1e-4, grel(dv_r, dv)
+
+
+FA_BF16_CASES = [  # (n, H, Hkv, hd, causal, B)
+    (128, 4, 2, 64, True, 1), (256, 16, 8, 128, True, 2), (200, 4, 1, 128, True, 1),
+    (192, 8, 2, 64, False, 2), (512, 4, 2, 128, True, 1),
+]
+
+
+@pytest.mark.parametrize("case", FA_BF16_CASES)
+def test_flash_attention_bf16_mfma(case):
+    """MFMA kernels vs the oracle on the same bf16-rounded Q/K/V/dO."""
+    from valkyr_amd import kernels as K
+
+    n, H, Hkv, hd, causal, B = case
+    note(f"fa bf16 {case}")
+    Q = O.normal(B * n * H * hd, 101)
+    Kk = O.normal(B * n * Hkv * hd, 102)
+    Vv = O.normal(B * n * Hkv * hd, 103)
+    dO = O.normal(B * n * H * hd, 104, 0.1)
+    qb, Qr = bf16_dev(Q)
+    kb, Kr = bf16_dev(Kk)
+    vb, Vr = bf16_dev(Vv)
+    dob, dOr = bf16_dev(dO)
+    o_r, lse_r, dq_r, dk_r, dv_r = _fa_oracle(Qr, Kr, Vr, dOr, B, n, n, H, Hkv, hd, causal)
+    p = K.attn_params(n, n, H, Hkv, hd, causal, B, K.BF16)
+    dob16 = zeros(dO.size // 2 + 8)
+    o, lse, d, dq, dk, dv = _run_fa_gpu(p, qb, kb, vb, o_r, dob, dev(dO), lse_r, B, n, n, H, Hkv,
+                                        hd, dob16)
+    # fa_bw_d with a bf16 copy: D pairs with the rounded dO, and the copy is exact RNE
+    assert rel_l2(O.fa_bw_d(o_r, dOr, B * n, H, hd), d) < 1e-5
+    assert np.array_equal(host(dob16, dO.size, np.uint16), O.to_bf16_bits(dO))
+    e = [rel_l2(o_r, o), rel_l2(dq_r, dq), rel_l2(dk_r, dk), rel_l2(dv_r, dv)]
+    note(f"  rel-L2 O={e[0]:.2e} dQ={e[1]:.2e} dK={e[2]:.2e} dV={e[3]:.2e}")
+    assert max(abs(lse_r - lse)) < 2e-2
+    assert all(x < BF16_TOL for x in e), e
+
+
+def test_flash_attention_bf16_full_size_invariants():
+    """Config-2 shape (B=4, S=2048, 16/8 heads, hd 128): size-independent checks.
+
+    sum_k dV[k] = sum_{q, h in group} dO[q]   (rows of P sum to 1)
+    sum_k dK[k] = 0                           (rows of dS sum to 0)
+    plus closed-form dQ / dK / dV rows in float64 at sampled positions.
+    """
+    from valkyr_amd import kernels as K
+
+    B, S, H, Hkv, hd = 4, 2048, 16, 8, 128
+    note("fa bf16 config-2 invariants")
+    Q = O.normal(B * S * H * hd, 111)
+    Kk = O.normal(B * S * Hkv * hd, 112)
+    Vv = O.normal(B * S * Hkv * hd, 113)
+    dO = O.normal(B * S * H * hd, 114, 0.1)
+    qb, Qr = bf16_dev(Q)
+    kb, Kr = bf16_dev(Kk)
+    vb, Vr = bf16_dev(Vv)
+    dob, dOr = bf16_dev(dO)
+    p = K.attn_params(S, S, H, Hkv, hd, True, B, K.BF16)
+    bo, blse, bd = zeros(Q.size), zeros(B * S * H), zeros(B * S * H)
+    K.fa_forward(p, qb, kb, vb, bo, blse)
+    dob16 = zeros(dO.size // 2 + 8)
+    K.fa_bw_d(p, bo, dev(dO), bd, dob16)
+    bdq, bdk, bdv = zeros(Q.size), zeros(Kk.size), zeros(Kk.size)
+    K.fa_bw_dkv(p, qb, kb, vb, dob16, blse, bd, bdk, bdv)
+    K.fa_bw_dq(p, qb, kb, vb, dob16, blse, bd, bdq)
+    o, lse, dq, dk, dv = host(bo), host(blse), host(bdq), host(bdk), host(bdv)
+    hpk = H // Hkv
+    dv4 = dv.reshape(B, S, Hkv, hd).astype(np.float64)
+    dO4 = dOr.reshape(B, S, Hkv, hpk, hd).astype(np.float64)
+    lhs, rhs = dv4.sum(1), dO4.sum(axis=(1, 3))
+    assert rel_l2(rhs, lhs) < 5e-3
+    dk4 = dk.reshape(B, S, Hkv, hd).astype(np.float64)
+    # the sum over keys cancels: far below the sum of magnitudes
+    assert np.all(np.abs(dk4.sum(1)) <= 2e-2 * np.abs(dk4).sum(1) + 1e-6)
+    # closed-form rows (float64 from the bf16-exact operands)
+    q5 = Qr.reshape(B, S, H, hd).astype(np.float64)
+    k5 = Kr.reshape(B, S, Hkv, hd).astype(np.float64)
+    v5 = Vr.reshape(B, S, Hkv, hd).astype(np.float64)
+    do5 = dOr.reshape(B, S, H, hd).astype(np.float64)
+    sc = 1.0 / math.sqrt(hd)
+    rng = np.random.default_rng(5)
+    for _ in range(6):
+        b, h, qi = rng.integers(B), rng.integers(H), rng.integers(S)
+        kv = h // hpk
+        s = k5[b, :qi + 1, kv] @ q5[b, qi, h] * sc
+        pr = np.exp(s - s.max()); pr /= pr.sum()
+        o_ref = pr @ v5[b, :qi + 1, kv]
+        assert rel_l2(o_ref, o.reshape(B, S, H, hd)[b, qi, h]) < 1e-2
+        dp = v5[b, :qi + 1, kv] @ do5[b, qi, h]
+        dd = (pr * dp).sum()
+        dq_ref = sc * ((pr * (dp - dd)) @ k5[b, :qi + 1, kv])
+        assert rel_l2(dq_ref, dq.reshape(B, S, H, hd)[b, qi, h]) < 1e-2

@@ -1,0 +1,306 @@
+"""Whole-step parity: the HIP Runner vs the C oracle's GPU-Runner semantics on
+identical seeded weights and tokens (BASELINE config 1 and variants), plus
+the Runner API behaviour (checkpoints, tick API, error paths).
+
+Per-tensor bars: fp32 precision rel-L2 <= 1e-3 for every gradient and Adam
+moment; bf16-operand precision rel-L2 <= 1e-2 against the oracle run with
+bf16-rounded contraction operands.
+"""
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+from helpers import note, rel_l2
+
+pytestmark = pytest.mark.gpu
+
+CONFIG1 = dict(dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ff_dim=768, seq_len=128, n_seqs=1,
+               n_layers=2, vocab_size=4096, rms_eps=1e-6, causal=1, rotary_dim=64,
+               rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
+               lora_targets=0, lora_rank=0, lora_alpha=0.0, lora_lr_b_scale=1.0,
+               tied_embeddings=0, bf16_operands=0)
+
+LAYER_KEYS = ["w_n1", "w_q", "w_k", "w_v", "w_o", "w_n2", "w_gate", "w_up", "w_down", "w_q_norm",
+              "w_k_norm"]
+
+
+def build_pair(precision=0, seed=1234, lora_std=0.02, **over):
+    import valkyr_amd as v
+
+    cfg = dict(CONFIG1)
+    cfg.update(over)
+    if precision == 1:
+        cfg["bf16_operands"] = 1
+    m = O.Model(**cfg)
+    m.init_random(seed, std=0.02, lora_std=lora_std)
+    L = cfg["n_layers"]
+    weights = {
+        "embed": m.tensor(0, -1, 0).copy(),
+        "final_norm": m.tensor(0, -1, 1).copy(),
+        "lm_head": None if cfg["tied_embeddings"] else m.tensor(0, -1, 2).copy(),
+        "layers": [{LAYER_KEYS[w]: (m.tensor(0, l, w).copy() if m.tensor(0, l, w) is not None else None)
+                    for w in range(11)} for l in range(L)],
+    }
+    if cfg["lora_targets"]:
+        weights["lora"] = {p: [{"a": m.tensor(0, l, 16 + 2 * p).copy(),
+                                "b": m.tensor(0, l, 17 + 2 * p).copy()} for l in range(L)]
+                           for p in range(7) if cfg["lora_targets"] & (1 << p)}
+    rc = v.make_config(dim=cfg["dim"], n_heads=cfg["n_heads"], n_kv_heads=cfg["n_kv_heads"],
+                       head_dim=cfg["head_dim"], ff_dim=cfg["ff_dim"], n_pos=cfg["seq_len"],
+                       n_layers=L, vocab_size=cfg["vocab_size"], rms_eps=cfg["rms_eps"],
+                       causal=cfg["causal"], rotary_dim=cfg["rotary_dim"],
+                       rope_theta=cfg["rope_theta"], qk_norm=cfg["qk_norm"], lr=cfg["lr"],
+                       beta1=cfg["beta1"], beta2=cfg["beta2"], eps_adam=cfg["eps_adam"],
+                       lora_targets=cfg["lora_targets"], lora_rank=cfg["lora_rank"],
+                       lora_alpha=cfg["lora_alpha"], lora_lr_b_scale=cfg["lora_lr_b_scale"],
+                       n_seqs=cfg["n_seqs"], tied_embeddings=cfg["tied_embeddings"],
+                       precision=precision)
+    r = v.Runner(rc, weights)
+    T = cfg["seq_len"] * cfg["n_seqs"]
+    tok = O.ids(T, seed + 1, cfg["vocab_size"])
+    tgt = O.ids(T, seed + 2, cfg["vocab_size"])
+    return m, r, tok, tgt, cfg
+
+
+def tensor_keys(cfg):
+    keys = [(-1, 0), (-1, 1)] + ([] if cfg["tied_embeddings"] else [(-1, 2)])
+    for l in range(cfg["n_layers"]):
+        keys += [(l, w) for w in range(9)]
+        if cfg["qk_norm"]:
+            keys += [(l, 9), (l, 10)]
+    return keys
+
+
+def lora_keys(cfg):
+    return [(l, 16 + 2 * p + ab) for l in range(cfg["n_layers"]) for p in range(7)
+            if cfg["lora_targets"] & (1 << p) for ab in (0, 1)]
+
+
+def compare(m, r, keys, kind, tol, what):
+    worst = (0.0, None)
+    for (l, w) in keys:
+        ref = m.tensor(kind, l, w)
+        got = r.get(kind, l, w)
+        e = rel_l2(ref, got)
+        if e > worst[0]:
+            worst = (e, (l, w))
+        assert e < tol, f"{what} {(l, w)} rel-L2 {e:.3e} >= {tol}"
+    note(f"  {what}: worst rel-L2 {worst[0]:.2e} at {worst[1]}")
+    return worst[0]
+
+
+@pytest.mark.parametrize("variant", [{}, {"tied_embeddings": 1}, {"n_seqs": 2, "seq_len": 64},
+                                     {"qk_norm": 0, "rotary_dim": 32}])
+def test_step_parity_fp32(variant):
+    note(f"step fp32 {variant}")
+    m, r, tok, tgt, cfg = build_pair(0, **variant)
+    keys = tensor_keys(cfg)
+    p0 = {k: m.tensor(0, *k).copy() for k in keys}
+    loss_ref = m.forward_backward(tok, tgt)
+    loss = r.forward_backward(tok, tgt)
+    note(f"  loss oracle {loss_ref:.6f} gpu {loss:.6f}")
+    assert abs(loss - loss_ref) < 1e-5 * abs(loss_ref)
+    compare(m, r, keys, 1, 1e-3, "grad")
+    m.adam()
+    r.step(tok, tgt)  # same grads again (weights unchanged), then Adam
+    assert r.step_t == m.step_t == 2
+    compare(m, r, keys, 2, 1e-3, "adam m")
+    compare(m, r, keys, 3, 1e-3, "adam v")
+    for k in keys:
+        # updated weights ...
+        assert rel_l2(m.tensor(0, *k), r.get(0, *k)) < 1e-3
+        # ... and the update itself: at t = 1 Adam moves every weight by about
+        # lr * sign(g), so entries with |g| near eps are sign-sensitive; 1e-2
+        du_ref = m.tensor(0, *k) - p0[k]
+        du = r.get(0, *k) - p0[k]
+        assert rel_l2(du_ref, du) < 1e-2, (k, rel_l2(du_ref, du))
+
+
+def test_step_parity_bf16():
+    """bf16-operand step vs the oracle with the same operand rounding.
+
+    The 1e-2 bar of the north star is per bf16-operand GEMM (held by the
+    kernel tests).  A 2-layer step chains about a dozen such GEMMs plus the
+    bf16 attention / dz operands, and an element that lands near a bf16
+    rounding boundary can round differently on each side, so whole-step
+    gradients are held to 2e-2 here; for scale, merely rounding the oracle's
+    own operands moves its gradients by up to 1.4e-2 from the fp32 oracle.
+    """
+    note("step bf16")
+    m, r, tok, tgt, cfg = build_pair(1)
+    keys = tensor_keys(cfg)
+    loss_ref = m.forward_backward(tok, tgt)
+    loss = r.forward_backward(tok, tgt)
+    note(f"  loss oracle(bf16 operands) {loss_ref:.6f} gpu {loss:.6f}")
+    assert abs(loss - loss_ref) < 1e-3 * abs(loss_ref)
+    compare(m, r, keys, 1, 2e-2, "grad")
+    m.adam()
+    r.step(tok, tgt)
+    compare(m, r, keys, 2, 2e-2, "adam m")
+    for k in keys:  # updated weights
+        assert rel_l2(m.tensor(0, *k), r.get(0, *k)) < 1e-2
+
+
+def test_step_bf16_vs_pure_fp32_oracle():
+    """bf16-operand GPU path against the unrounded fp32 oracle (reported; 5e-2 bar)."""
+    m, r, tok, tgt, cfg = build_pair(0)
+    import valkyr_amd as v
+    rb = v.Runner(v.make_config(**{f: getattr(r.cfg, f) for f, _ in r.cfg._fields_ if f != "precision"},
+                                precision=1),
+                  {"embed": m.tensor(0, -1, 0), "final_norm": m.tensor(0, -1, 1),
+                   "lm_head": m.tensor(0, -1, 2),
+                   "layers": [{LAYER_KEYS[w]: m.tensor(0, l, w) for w in range(11)} for l in range(2)]})
+    m.forward_backward(tok, tgt)
+    rb.forward_backward(tok, tgt)
+    compare(m, rb, tensor_keys(cfg), 1, 5e-2, "grad bf16-vs-fp32")
+
+
+def test_lora_step_parity():
+    """Config-4 shape class: LoRA r=16 on q/k/v/o, B=0 init, frozen base."""
+    note("lora step")
+    over = dict(lora_targets=0xF, lora_rank=16, lora_alpha=32.0, lora_lr_b_scale=1.0)
+    m, r, tok, tgt, cfg = build_pair(0, **over)
+    lk = lora_keys(cfg)
+    loss_ref = m.forward_backward(tok, tgt)
+    loss = r.forward_backward(tok, tgt)
+    assert abs(loss - loss_ref) < 1e-5 * abs(loss_ref)
+    for (l, w) in lk:
+        if w % 2 == 0:  # dA == 0 exactly at B = 0 (lora.zig:449-505)
+            assert np.all(r.get(1, l, w) == 0)
+    compare(m, r, [k for k in lk if k[1] % 2 == 1], 1, 1e-3, "dB")
+    base_before = r.get(0, 0, 1).copy()
+    m.adam()
+    r.step(tok, tgt)
+    # second step: B != 0, dA flows; frozen base unchanged bit-for-bit
+    loss_ref = m.forward_backward(tok, tgt)
+    loss = r.forward_backward(tok, tgt)
+    assert abs(loss - loss_ref) < 1e-5 * abs(loss_ref)
+    compare(m, r, lk, 1, 1e-3, "lora grad step 2")
+    assert np.array_equal(base_before, r.get(0, 0, 1))
+
+
+def test_forward_logits_matches_oracle():
+    m, r, tok, tgt, cfg = build_pair(0)
+    ref = m.forward_logits(tok)
+    got = r.forward_logits(tok)
+    assert rel_l2(ref, got) < 1e-4
+
+
+def test_loss_decreases_over_steps():
+    m, r, tok, tgt, cfg = build_pair(0, lr=1e-3)
+    losses = []
+    for _ in range(8):
+        r.step(tok, tgt)
+        losses.append(r.last_loss())
+    note(f"  losses {losses[0]:.4f} -> {losses[-1]:.4f}")
+    assert losses[-1] < losses[0]
+    assert all(np.isfinite(losses))
+
+
+def test_checkpoint_roundtrip_and_errors(tmp_path):
+    import valkyr_amd as v
+
+    m, r, tok, tgt, cfg = build_pair(0, lr=1e-3)
+    for _ in range(2):
+        r.step(tok, tgt)
+    path = str(tmp_path / "a.vkpt")
+    r.save_checkpoint(path)
+    with open(path, "rb") as f:
+        head = f.read(16)
+    assert head[:4] == b"VKPT"
+    assert int.from_bytes(head[4:8], "little") == 1
+    assert int.from_bytes(head[8:12], "little") == 3  # step_t after two steps
+    r.step(tok, tgt)
+    after_a = r.get(0, 0, 1)
+    # a fresh runner resumes from the checkpoint and reproduces the next step bit-for-bit
+    m2, r2, _, _, _ = build_pair(0, seed=99, lr=5e-2)
+    r2.load_checkpoint(path)
+    assert r2.step_t == 3 and abs(r2.lr - 1e-3) < 1e-9
+    r2.step(tok, tgt)
+    assert np.array_equal(after_a, r2.get(0, 0, 1))
+    # corrupted magic, truncated file, config mismatch
+    bad = tmp_path / "bad.vkpt"
+    data = open(path, "rb").read()
+    bad.write_bytes(b"XXXX" + data[4:])
+    with pytest.raises(v.VkhError) as e:
+        r2.load_checkpoint(str(bad))
+    assert e.value.name == "InvalidCheckpointMagic"
+    bad.write_bytes(data[: len(data) // 2])
+    with pytest.raises(v.VkhError) as e:
+        r2.load_checkpoint(str(bad))
+    assert e.value.name == "EndOfStream"
+    _, r3, _, _, _ = build_pair(0, n_layers=1)
+    with pytest.raises(v.VkhError) as e:
+        r3.load_checkpoint(path)
+    assert e.value.name == "CheckpointConfigMismatch"
+
+
+def test_lora_checkpoint_roundtrip(tmp_path):
+    import valkyr_amd as v
+
+    over = dict(lora_targets=0xF, lora_rank=16, lora_alpha=32.0, lora_lr_b_scale=4.0, lr=1e-3)
+    m, r, tok, tgt, cfg = build_pair(0, **over)
+    for _ in range(2):
+        r.step(tok, tgt)
+    path = str(tmp_path / "a.lvkpt")
+    r.save_lora_checkpoint(path)
+    assert open(path, "rb").read(4) == b"VLKP"
+    _, r2, _, _, _ = build_pair(0, seed=7, **over)
+    r2.load_lora_checkpoint(path)
+    for k in lora_keys(cfg):
+        assert np.array_equal(r.get(0, *k), r2.get(0, *k))
+    _, rf, _, _, _ = build_pair(0)
+    with pytest.raises(v.VkhError) as e:
+        rf.save_lora_checkpoint(path)
+    assert e.value.name == "LoraCheckpointEmpty"
+
+
+def test_tick_frame_train_budget_and_loss_latency():
+    from valkyr_amd.device import Stream
+
+    m, r, tok, tgt, cfg = build_pair(0, lr=1e-3)
+    r.upload_train_batch(tok, tgt)
+    s = Stream()
+    res = r.tick_frame_train(steps=3, stream=s)
+    assert res.steps_completed == 3 and not res.has_loss
+    s.synchronize()
+    res2 = r.tick_frame_train(steps=1, stream=s)
+    assert res2.has_loss and np.isfinite(res2.last_loss)
+    s.synchronize()
+    assert r.step_t == 5
+    r.set_loss_target(1e9)  # any loss is below: the next tick goes idle
+    res3 = r.tick_frame_train(steps=2, stream=s)
+    assert res3.idle and res3.steps_completed == 0
+
+
+def test_runner_error_paths():
+    import valkyr_amd as v
+
+    m, r, tok, tgt, cfg = build_pair(0)
+    with pytest.raises(v.VkhError) as e:
+        r.step(tok[:-1], tgt)
+    assert e.value.name == "TokenIdsLen"
+    with pytest.raises(v.VkhError) as e:
+        r.step(tok, tgt[:-1])
+    assert e.value.name == "TargetLen"
+    bad = tok.copy()
+    bad[3] = cfg["vocab_size"]
+    with pytest.raises(v.VkhError) as e:
+        r.step(bad, tgt)
+    assert e.value.name == "TokenOutOfRange"
+    w = {"embed": np.zeros(10, np.float32), "final_norm": np.ones(256, np.float32),
+         "lm_head": None, "layers": []}
+    with pytest.raises(v.VkhError) as e:
+        v.Runner(r.cfg, w)
+    assert e.value.name == "EmbedShape"
+
+
+def test_nonfinite_weights_give_nonfinite_loss():
+    m, r, tok, tgt, cfg = build_pair(0)
+    w = r.get(0, 0, 1)
+    w[5] = np.nan
+    r.set(0, 0, 1, w)
+    loss = r.forward_backward(tok, tgt)
+    assert not np.isfinite(loss)

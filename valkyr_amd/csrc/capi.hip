@@ -1,0 +1,463 @@
+// C ABI for the individual kernels plus the HIP plumbing (memory, streams,
+// events) a host without its own HIP bindings needs.  Every function checks
+// its arguments, enqueues, and reports launch errors as VKH_ERR_HIP.
+#include <math.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <tuple>
+#include <vector>
+
+#include "internal.hpp"
+
+namespace vkh {
+
+static thread_local char g_err[512] = "";
+
+vkh_status fail(vkh_status st, const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof(g_err), fmt, ap);
+    va_end(ap);
+    return st;
+}
+
+vkh_status hip_fail(hipError_t e, const char *what) {
+    if (e == hipErrorOutOfMemory || e == hipErrorMemoryAllocation)
+        return fail(VKH_ERR_OUT_OF_MEMORY, "%s: %s", what, hipGetErrorString(e));
+    return fail(VKH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+// RoPE tables for the standalone kernel entry points, cached per
+// (device, seq_len, rotary_dim, theta) for the life of the process.
+static vkh_status rope_table_cached(int seq_len, int rot, float theta, const float2 **out) {
+    static std::mutex mu;
+    static std::map<std::tuple<int, int, int, uint32_t>, float2 *> cache;
+    int dev = 0;
+    VKH_HIP(hipGetDevice(&dev));
+    uint32_t tb;
+    memcpy(&tb, &theta, 4);
+    std::lock_guard<std::mutex> lk(mu);
+    auto key = std::make_tuple(dev, seq_len, rot, tb);
+    auto it = cache.find(key);
+    if (it != cache.end()) { *out = it->second; return VKH_OK; }
+    const int half = rot / 2;
+    std::vector<float2> tab((size_t)seq_len * (half ? half : 1));
+    if (half) rope_table_host(tab.data(), seq_len, rot, theta);
+    float2 *d = nullptr;
+    VKH_HIP(hipMalloc(&d, tab.size() * sizeof(float2)));
+    VKH_HIP(hipMemcpy(d, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
+    cache[key] = d;
+    *out = d;
+    return VKH_OK;
+}
+
+}  // namespace vkh
+
+using namespace vkh;
+
+#define CHECK_ARG(cond, msg)                                              \
+    do {                                                                  \
+        if (!(cond)) return fail(VKH_ERR_INVALID_ARGUMENT, "%s", msg);    \
+    } while (0)
+
+static inline hipStream_t S(vkh_stream s) { return (hipStream_t)s; }
+static inline Precision PR(uint32_t p) { return p == VKH_PRECISION_BF16 ? Precision::BF16 : Precision::FP32; }
+
+static AttnShape attn_shape(const vkh_attn_params *p) {
+    AttnShape s;
+    s.n_batch = p->n_batch ? (int)p->n_batch : 1;
+    s.n_q = p->n_q; s.n_kv = p->n_kv; s.n_heads = p->n_heads; s.n_kv_heads = p->n_kv_heads;
+    s.head_dim = p->head_dim; s.causal = p->causal ? 1 : 0; s.inv_sqrt_dim = p->inv_sqrt_dim;
+    return s;
+}
+
+static vkh_status check_attn(const vkh_attn_params *p) {
+    CHECK_ARG(p, "null params");
+    CHECK_ARG(p->n_heads && p->n_kv_heads && p->head_dim && p->n_q && p->n_kv, "zero attention dimension");
+    CHECK_ARG(p->n_heads % p->n_kv_heads == 0, "n_heads % n_kv_heads != 0");
+    CHECK_ARG(!p->causal || p->n_q <= p->n_kv, "causal attention needs n_q <= n_kv");
+    CHECK_ARG(p->dtype <= VKH_BF16, "dtype");
+    if (p->dtype == VKH_BF16 && p->head_dim != 64 && p->head_dim != 128)
+        return fail(VKH_ERR_UNSUPPORTED, "bf16 attention supports head_dim 64 and 128");
+    if (p->head_dim > 256) return fail(VKH_ERR_UNSUPPORTED, "head_dim > 256");
+    return VKH_OK;
+}
+
+extern "C" {
+
+const char *vkh_last_error(void) { return g_err; }
+
+const char *vkh_build_info(void) { return "vkhip for gfx950 (MI355X), built with hipcc " __VERSION__; }
+
+const char *vkh_status_name(vkh_status s) {
+    switch (s) {
+    case VKH_OK: return "Ok";
+    case VKH_ERR_INVALID_ARGUMENT: return "InvalidArgument";
+    case VKH_ERR_HIP: return "HipError";
+    case VKH_ERR_OUT_OF_MEMORY: return "OutOfMemory";
+    case VKH_ERR_UNSUPPORTED: return "Unsupported";
+    case VKH_ERR_NO_DEVICE: return "NoDevice";
+    case VKH_ERR_TOKEN_IDS_LEN: return "TokenIdsLen";
+    case VKH_ERR_TARGET_LEN: return "TargetLen";
+    case VKH_ERR_OUT_LOGITS_LEN: return "OutLogitsLen";
+    case VKH_ERR_TOKEN_OUT_OF_RANGE: return "TokenOutOfRange";
+    case VKH_ERR_EMBED_SHAPE: return "EmbedShape";
+    case VKH_ERR_FINAL_NORM_SHAPE: return "FinalNormShape";
+    case VKH_ERR_LM_HEAD_SHAPE: return "LmHeadShape";
+    case VKH_ERR_LAYER_COUNT: return "LayerCount";
+    case VKH_ERR_LAYER_N1_SHAPE: return "LayerN1Shape";
+    case VKH_ERR_LAYER_Q_SHAPE: return "LayerQShape";
+    case VKH_ERR_LAYER_K_SHAPE: return "LayerKShape";
+    case VKH_ERR_LAYER_V_SHAPE: return "LayerVShape";
+    case VKH_ERR_LAYER_O_SHAPE: return "LayerOShape";
+    case VKH_ERR_LAYER_N2_SHAPE: return "LayerN2Shape";
+    case VKH_ERR_LAYER_GATE_SHAPE: return "LayerGateShape";
+    case VKH_ERR_LAYER_UP_SHAPE: return "LayerUpShape";
+    case VKH_ERR_LAYER_DOWN_SHAPE: return "LayerDownShape";
+    case VKH_ERR_LAYER_Q_NORM_SHAPE: return "LayerQNormShape";
+    case VKH_ERR_LAYER_K_NORM_SHAPE: return "LayerKNormShape";
+    case VKH_ERR_LORA_RANK_ZERO: return "LoraRankZero";
+    case VKH_ERR_LORA_INIT_LEN: return "LoraInitLen";
+    case VKH_ERR_INVALID_CHECKPOINT_MAGIC: return "InvalidCheckpointMagic";
+    case VKH_ERR_UNSUPPORTED_CHECKPOINT_VERSION: return "UnsupportedCheckpointVersion";
+    case VKH_ERR_CHECKPOINT_CONFIG_SIZE_MISMATCH: return "CheckpointConfigSizeMismatch";
+    case VKH_ERR_CHECKPOINT_CONFIG_MISMATCH: return "CheckpointConfigMismatch";
+    case VKH_ERR_END_OF_STREAM: return "EndOfStream";
+    case VKH_ERR_INVALID_LORA_CHECKPOINT_MAGIC: return "InvalidLoraCheckpointMagic";
+    case VKH_ERR_UNSUPPORTED_LORA_CHECKPOINT_VERSION: return "UnsupportedLoraCheckpointVersion";
+    case VKH_ERR_LORA_CHECKPOINT_CONFIG_SIZE_MISMATCH: return "LoraCheckpointConfigSizeMismatch";
+    case VKH_ERR_LORA_CHECKPOINT_CONFIG_MISMATCH: return "LoraCheckpointConfigMismatch";
+    case VKH_ERR_LORA_CHECKPOINT_EMPTY: return "LoraCheckpointEmpty";
+    case VKH_ERR_IO: return "IoError";
+    }
+    return "Unknown";
+}
+
+// ── attention ──────────────────────────────────────────────────────────
+
+vkh_status vkh_fa_forward(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                          float *o, float *lse, vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(q && k && v && o, "null pointer");
+    const AttnShape s = attn_shape(p);
+    const long ldq = (long)p->n_heads * p->head_dim, ldk = (long)p->n_kv_heads * p->head_dim;
+    VKH_HIP(fa_forward(s, q, ldq, k, ldk, v, ldk, o, ldq, lse,
+                       p->dtype == VKH_BF16 ? DType::BF16 : DType::F32, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_fa_bw_d(const vkh_attn_params *p, const float *o, const float *dout, float *d,
+                       void *dout_bf16, vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(o && dout && d, "null pointer");
+    const AttnShape s = attn_shape(p);
+    const long ld = (long)p->n_heads * p->head_dim;
+    VKH_HIP(fa_bw_d(s, o, ld, dout, ld, d, p->dtype == VKH_BF16 ? (bf16 *)dout_bf16 : nullptr, ld,
+                    S(stream)));
+    return VKH_OK;
+}
+
+static AttnPtrs attn_ptrs(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                          const void *dout, const float *lse, const float *d) {
+    AttnPtrs a{};
+    const long ldq = (long)p->n_heads * p->head_dim, ldk = (long)p->n_kv_heads * p->head_dim;
+    a.q = q; a.ldq = ldq; a.k = k; a.ldk = ldk; a.v = v; a.ldv = ldk;
+    a.dout = dout; a.lddo = ldq; a.lse = lse; a.d = (float *)d;
+    a.lddq = ldq; a.lddk = ldk; a.lddv = ldk;
+    a.dt = p->dtype == VKH_BF16 ? DType::BF16 : DType::F32;
+    return a;
+}
+
+vkh_status vkh_fa_bw_dq(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                        const void *dout, const float *lse, const float *d, float *dq,
+                        vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(q && k && v && dout && lse && d && dq, "null pointer");
+    AttnPtrs a = attn_ptrs(p, q, k, v, dout, lse, d);
+    a.dq = dq;
+    VKH_HIP(fa_bw_dq(attn_shape(p), a, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_fa_bw_dkv(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                         const void *dout, const float *lse, const float *d, float *dk,
+                         float *dv, vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(q && k && v && dout && lse && d && dk && dv, "null pointer");
+    AttnPtrs a = attn_ptrs(p, q, k, v, dout, lse, d);
+    a.dk = dk;
+    a.dv = dv;
+    VKH_HIP(fa_bw_dkv(attn_shape(p), a, S(stream)));
+    return VKH_OK;
+}
+
+// ── GEMMs ──────────────────────────────────────────────────────────────
+
+vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,
+                         uint32_t K, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(x && w && y, "null pointer");
+    VKH_HIP(gemm_nt(PR(precision), matf(x, K), matf(w, K), y, N, M, N, K, nullptr, 0, 1.f, 0.f, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_linear_backward_dx(const float *dy, const float *w, float *dx, uint32_t M,
+                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(dy && w && dx, "null pointer");
+    VKH_HIP(gemm_nn(PR(precision), matf(dy, N), matf(w, K), dx, K, M, N, K, 1.f, 0.f, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, uint32_t M,
+                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(dy && x && dw, "null pointer");
+    VKH_HIP(gemm_tn(PR(precision), matf(dy, N), matf(x, K), dw, K, M, N, K, 1.f, 0.f, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_lora_forward(const float *x, const float *w, const float *a, const float *b,
+                            float *y, float *inter, uint32_t M, uint32_t N, uint32_t K,
+                            uint32_t r, float aor, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(x && w && a && b && y && inter, "null pointer");
+    CHECK_ARG(r > 0, "rank 0");
+    const Precision pr = PR(precision);
+    hipStream_t st = S(stream);
+    VKH_HIP(gemm_nt(pr, matf(x, K), matf(w, K), y, N, M, N, K, nullptr, 0, 1.f, 0.f, st));
+    VKH_HIP(gemm_nt(pr, matf(x, K), matf(a, K), inter, r, M, r, K, nullptr, 0, 1.f, 0.f, st));
+    VKH_HIP(gemm_nt(pr, matf(inter, r), matf(b, r), y, N, M, N, r, nullptr, 0, aor, 1.f, st));
+    return VKH_OK;
+}
+
+vkh_status vkh_lora_backward(const float *dy, const float *x, const float *w, const float *a,
+                             const float *b, const float *inter, float *dx, float *dA,
+                             float *dB, uint32_t M, uint32_t N, uint32_t K, uint32_t r,
+                             float aor, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(dy && x && w && a && b && inter && dA && dB, "null pointer");
+    CHECK_ARG(r > 0, "rank 0");
+    const Precision pr = PR(precision);
+    hipStream_t st = S(stream);
+    float *dyB = nullptr;
+    VKH_HIP(hipMallocAsync((void **)&dyB, (size_t)M * r * 4, st));
+    hipError_t e = gemm_nn(pr, matf(dy, N), matf(b, r), dyB, r, M, N, r, 1.f, 0.f, st);
+    if (e == hipSuccess && dx) e = gemm_nn(pr, matf(dy, N), matf(w, K), dx, K, M, N, K, 1.f, 0.f, st);
+    if (e == hipSuccess && dx) e = gemm_nn(pr, matf(dyB, r), matf(a, K), dx, K, M, r, K, aor, 1.f, st);
+    if (e == hipSuccess) e = gemm_tn(pr, matf(dyB, r), matf(x, K), dA, K, M, r, K, aor, 0.f, st);
+    if (e == hipSuccess) e = gemm_tn(pr, matf(dy, N), matf(inter, r), dB, r, M, N, r, aor, 0.f, st);
+    (void)hipFreeAsync(dyB, st);
+    if (e != hipSuccess) return hip_fail(e, "lora_backward");
+    return VKH_OK;
+}
+
+// ── CCE ────────────────────────────────────────────────────────────────
+
+vkh_status vkh_cce_forward(const vkh_cce_params *p, const float *h, const float *w,
+                           const uint32_t *targets, float *lse, float *loss_row,
+                           float *loss_mean, vkh_stream stream) {
+    CHECK_ARG(p && h && w && targets && lse, "null pointer");
+    CHECK_ARG(p->n && p->vocab && p->dim, "zero dimension");
+    const CceShape s{(int)p->n, (int)p->vocab, (int)p->dim, p->z_loss_scale, p->label_smoothing};
+    hipStream_t st = S(stream);
+    float *work = nullptr;
+    VKH_HIP(hipMallocAsync((void **)&work, cce_work_floats(s) * 4, st));
+    hipError_t e = cce_forward(PR(p->precision), s, h, w, targets, lse, loss_row, loss_mean, work, st);
+    (void)hipFreeAsync(work, st);
+    if (e != hipSuccess) return hip_fail(e, "cce_forward");
+    return VKH_OK;
+}
+
+vkh_status vkh_cce_backward(const vkh_cce_params *p, const float *h, const float *w,
+                            const uint32_t *targets, const float *lse, float *dh, float *dw,
+                            uint32_t accumulate_dw, vkh_stream stream) {
+    CHECK_ARG(p && h && w && targets && lse, "null pointer");
+    CHECK_ARG(p->n && p->vocab && p->dim, "zero dimension");
+    const CceShape s{(int)p->n, (int)p->vocab, (int)p->dim, p->z_loss_scale, p->label_smoothing};
+    hipStream_t st = S(stream);
+    void *dz = nullptr;
+    const size_t zb = (size_t)p->n * p->vocab * (p->precision == VKH_PRECISION_BF16 ? 2 : 4);
+    VKH_HIP(hipMallocAsync(&dz, zb, st));
+    hipError_t e = cce_backward(PR(p->precision), s, h, w, targets, lse, dz, dh, dw,
+                                accumulate_dw ? 1.f : 0.f, st);
+    (void)hipFreeAsync(dz, st);
+    if (e != hipSuccess) return hip_fail(e, "cce_backward");
+    return VKH_OK;
+}
+
+// ── norms, rope, elementwise ───────────────────────────────────────────
+
+vkh_status vkh_rmsnorm_forward(const float *x, const float *w, float *y, uint32_t n_rows,
+                               uint32_t dim, float eps, uint32_t gq, vkh_stream stream) {
+    CHECK_ARG(x && w && y, "null pointer");
+    VKH_HIP(rmsnorm_forward(x, w, y, n_rows, dim, eps, gq ? 1 : 0, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
+                                const float *residual, float *dw, uint32_t n_rows, uint32_t dim,
+                                float eps, uint32_t gq, vkh_stream stream) {
+    CHECK_ARG(dy && x && w && dx, "null pointer");
+    if (dim > 4096) return fail(VKH_ERR_UNSUPPORTED, "rmsnorm_backward dim > 4096");
+    hipStream_t st = S(stream);
+    float *partial = nullptr;
+    VKH_HIP(hipMallocAsync((void **)&partial, rmsnorm_partial_floats(n_rows, dim) * 4 + 16, st));
+    hipError_t e = rmsnorm_backward(dy, x, w, dx, residual, dw, partial, n_rows, dim, eps, gq ? 1 : 0, st);
+    (void)hipFreeAsync(partial, st);
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm_backward");
+    return VKH_OK;
+}
+
+vkh_status vkh_swiglu_forward(const float *pg, const float *up, float *g, size_t n,
+                              vkh_stream stream) {
+    CHECK_ARG(pg && up && g, "null pointer");
+    CHECK_ARG(n < (1ull << 31), "n too large");
+    VKH_HIP(swiglu_forward(pg, (long)n, up, (long)n, g, (long)n, 1, (int)n, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_swiglu_backward(const float *dg, const float *pg, const float *up, float *dpg,
+                               float *dup, size_t n, vkh_stream stream) {
+    CHECK_ARG(dg && pg && up && dpg && dup, "null pointer");
+    CHECK_ARG(n < (1ull << 31), "n too large");
+    VKH_HIP(swiglu_backward(dg, (long)n, pg, (long)n, up, (long)n, dpg, (long)n, dup, (long)n, 1,
+                            (int)n, S(stream)));
+    return VKH_OK;
+}
+
+static vkh_status rope_common(const vkh_rope_params *p, const float *qi, float *qo,
+                              const float *ki, float *ko, bool bw, vkh_stream stream) {
+    CHECK_ARG(p && qi && qo && ki && ko, "null pointer");
+    CHECK_ARG(p->rotary_dim <= p->head_dim && (p->rotary_dim % 2) == 0, "rotary_dim");
+    const int seq = p->seq_len ? (int)p->seq_len : (int)p->n_pos;
+    const float2 *tab = nullptr;
+    VKH_TRY(rope_table_cached(seq, p->rotary_dim, p->theta_base, &tab));
+    const long ldq = (long)p->n_q_heads * p->head_dim, ldk = (long)p->n_kv_heads * p->head_dim;
+    VKH_HIP(qk_rope(qi, ldq, qo, ldq, ki, ldk, ko, ldk, p->n_pos, p->n_q_heads, p->n_kv_heads,
+                    p->head_dim, p->rotary_dim, seq, tab, bw, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_qk_rope_forward(const vkh_rope_params *p, const float *q_in, float *q_out,
+                               const float *k_in, float *k_out, vkh_stream stream) {
+    return rope_common(p, q_in, q_out, k_in, k_out, false, stream);
+}
+
+vkh_status vkh_qk_rope_backward(const vkh_rope_params *p, const float *dq_out, float *dq_in,
+                                const float *dk_out, float *dk_in, vkh_stream stream) {
+    return rope_common(p, dq_out, dq_in, dk_out, dk_in, true, stream);
+}
+
+vkh_status vkh_embed_lookup(const float *embed, const uint32_t *ids, float *out, uint32_t n_pos,
+                            uint32_t dim, float scale, vkh_stream stream) {
+    CHECK_ARG(embed && ids && out, "null pointer");
+    VKH_HIP(embed_lookup(embed, ids, out, n_pos, dim, scale, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_embedding_backward(const float *dy, const uint32_t *ids, float *dE,
+                                  uint32_t n_pos, uint32_t dim, uint32_t vocab,
+                                  vkh_stream stream) {
+    CHECK_ARG(dy && ids && dE, "null pointer");
+    if (n_pos > (uint32_t)kEmbedBwMaxPos) return fail(VKH_ERR_UNSUPPORTED, "n_pos > %d", kEmbedBwMaxPos);
+    hipStream_t st = S(stream);
+    void *work = nullptr;
+    VKH_HIP(hipMallocAsync(&work, embed_bw_work_bytes(n_pos), st));
+    hipError_t e = embedding_backward(dy, ids, dE, n_pos, dim, vocab, true, work, st);
+    (void)hipFreeAsync(work, st);
+    if (e != hipSuccess) return hip_fail(e, "embedding_backward");
+    return VKH_OK;
+}
+
+vkh_status vkh_adam_step(float *param, const float *grad, float *m, float *v, size_t n, float lr,
+                         float beta1, float beta2, float eps, uint32_t t, float wd,
+                         vkh_stream stream) {
+    CHECK_ARG(param && grad && m && v, "null pointer");
+    CHECK_ARG(t >= 1, "t must be >= 1");
+    const float tf = (float)t;
+    VKH_HIP(adam_step(param, grad, m, v, n, lr, beta1, beta2, eps, 1.0f - powf(beta1, tf),
+                      1.0f - powf(beta2, tf), wd, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_add_in_place(float *dst, const float *src, size_t n, vkh_stream stream) {
+    CHECK_ARG(dst && src, "null pointer");
+    VKH_HIP(add_in_place(dst, src, n, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_vec_add(const float *a, const float *b, float *c, size_t n, vkh_stream stream) {
+    CHECK_ARG(a && b && c, "null pointer");
+    VKH_HIP(vec_add(a, b, c, n, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_scale(const float *in, float *out, size_t n, float s, vkh_stream stream) {
+    CHECK_ARG(in && out, "null pointer");
+    VKH_HIP(scale(in, out, n, s, S(stream)));
+    return VKH_OK;
+}
+
+vkh_status vkh_cast_f32_to_bf16(const float *in, void *out, size_t n, vkh_stream stream) {
+    CHECK_ARG(in && out, "null pointer");
+    VKH_HIP(cast_f32_to_bf16(in, (bf16 *)out, n, S(stream)));
+    return VKH_OK;
+}
+
+// ── plumbing ───────────────────────────────────────────────────────────
+
+vkh_status vkh_device_count(int *count) {
+    CHECK_ARG(count, "null pointer");
+    *count = 0;
+    hipError_t e = hipGetDeviceCount(count);
+    if (e != hipSuccess) { *count = 0; return fail(VKH_ERR_NO_DEVICE, "%s", hipGetErrorString(e)); }
+    return VKH_OK;
+}
+vkh_status vkh_set_device(int device) { VKH_HIP(hipSetDevice(device)); return VKH_OK; }
+vkh_status vkh_malloc(void **ptr, size_t bytes) {
+    CHECK_ARG(ptr, "null pointer");
+    VKH_HIP(hipMalloc(ptr, bytes ? bytes : 1));
+    return VKH_OK;
+}
+vkh_status vkh_free(void *ptr) { VKH_HIP(hipFree(ptr)); return VKH_OK; }
+vkh_status vkh_memcpy_h2d(void *dst, const void *src, size_t bytes) {
+    VKH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyHostToDevice));
+    return VKH_OK;
+}
+vkh_status vkh_memcpy_d2h(void *dst, const void *src, size_t bytes) {
+    VKH_HIP(hipMemcpy(dst, src, bytes, hipMemcpyDeviceToHost));
+    return VKH_OK;
+}
+vkh_status vkh_memset(void *ptr, int value, size_t bytes) {
+    VKH_HIP(hipMemset(ptr, value, bytes));
+    return VKH_OK;
+}
+vkh_status vkh_device_synchronize(void) { VKH_HIP(hipDeviceSynchronize()); return VKH_OK; }
+vkh_status vkh_stream_create(vkh_stream *out) {
+    CHECK_ARG(out, "null pointer");
+    hipStream_t s;
+    VKH_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *out = (vkh_stream)s;
+    return VKH_OK;
+}
+vkh_status vkh_stream_destroy(vkh_stream s) { VKH_HIP(hipStreamDestroy(S(s))); return VKH_OK; }
+vkh_status vkh_stream_synchronize(vkh_stream s) { VKH_HIP(hipStreamSynchronize(S(s))); return VKH_OK; }
+vkh_status vkh_event_create(vkh_event *out) {
+    CHECK_ARG(out, "null pointer");
+    hipEvent_t e;
+    VKH_HIP(hipEventCreate(&e));
+    *out = (vkh_event)e;
+    return VKH_OK;
+}
+vkh_status vkh_event_destroy(vkh_event e) { VKH_HIP(hipEventDestroy((hipEvent_t)e)); return VKH_OK; }
+vkh_status vkh_event_record(vkh_event e, vkh_stream s) {
+    VKH_HIP(hipEventRecord((hipEvent_t)e, S(s)));
+    return VKH_OK;
+}
+vkh_status vkh_event_synchronize(vkh_event e) { VKH_HIP(hipEventSynchronize((hipEvent_t)e)); return VKH_OK; }
+vkh_status vkh_event_elapsed_ms(vkh_event a, vkh_event b, float *ms) {
+    CHECK_ARG(ms, "null pointer");
+    VKH_HIP(hipEventElapsedTime(ms, (hipEvent_t)a, (hipEvent_t)b));
+    return VKH_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,76 @@
+// Shared definitions for the gfx950 (CDNA4) kernels of libvkhip.
+//
+// Everything here is written for one target: wave64, MFMA matrix cores,
+// 160 KB LDS per CU.  No portability layers.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stddef.h>
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+#define VKH_DEV __device__ __forceinline__
+
+namespace vkh {
+
+constexpr int kWave = 64;
+
+// fp32 -> bf16, round-to-nearest-even (v_cvt_pk_bf16_f32 on gfx950).
+VKH_DEV bf16 to_bf16(float x) { return (bf16)x; }
+VKH_DEV float to_f32(bf16 x) { return (float)x; }
+VKH_DEV float to_f32(float x) { return x; }
+
+VKH_DEV bf16x8 cvt8(float a0, float a1, float a2, float a3, float a4, float a5, float a6,
+                    float a7) {
+    bf16x8 r;
+    r[0] = (bf16)a0; r[1] = (bf16)a1; r[2] = (bf16)a2; r[3] = (bf16)a3;
+    r[4] = (bf16)a4; r[5] = (bf16)a5; r[6] = (bf16)a6; r[7] = (bf16)a7;
+    return r;
+}
+
+VKH_DEV f32x4 mfma16x16x32(const bf16x8 &a, const bf16x8 &b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+VKH_DEV f32x4 mfma16x16x4(float a, float b, const f32x4 &c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Wave-wide reductions (64 lanes) via DPP-friendly shuffles.
+VKH_DEV float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+VKH_DEV double wave_sum(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+VKH_DEV float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Block-wide sum for blockDim.x == NT (multiple of 64). `sh` needs NT/64 floats.
+template <int NT>
+VKH_DEV float block_sum(float v, float *sh) {
+    v = wave_sum(v);
+    const int w = threadIdx.x / kWave, l = threadIdx.x % kWave;
+    __syncthreads();
+    if (l == 0) sh[w] = v;
+    __syncthreads();
+    float t = 0.f;
+#pragma unroll
+    for (int i = 0; i < NT / kWave; ++i) t += sh[i];
+    return t;
+}
+
+inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
+
+}  // namespace vkh

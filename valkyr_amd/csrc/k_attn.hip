@@ -1,0 +1,690 @@
+// FlashAttention forward (with LSE) and the FA-2 backward for gfx950.
+//
+// Reference kernels: shaders/fa_forward.comp, fa_bw_d.comp, fa_bw_dq.comp,
+// fa_bw_dkv.comp; CPU oracle src/cpu/flash_attn.zig:91-376.  Same math
+// (online softmax; backward recomputes P = exp(S - LSE), D = rowsum(O * dO),
+// dS = P (dP - D)); causal limit k <= q + (n_kv - n_q); GQA head h reads
+// kv head h / (n_heads / n_kv_heads).  Batch extension: rows are
+// [n_batch * n], attention is block-diagonal per sequence.
+//
+// bf16 path (the hot path): v_mfma_f32_16x16x32_bf16 with fp32 accumulate.
+// Scores are formed transposed where that lets P / dS be used straight from
+// the accumulator registers as the B operand of the next MFMA:
+//
+//   forward:  S^T = K Q^T  ->  O^T += V^T P^T      (per-lane q column)
+//   dK/dV:    S   = Q K^T  ->  dV^T += dO^T P,  dK^T += Q^T dS   (K, V in regs)
+//   dQ:       S^T = K Q^T  ->  dQ^T += K^T dS^T                  (Q, dO in regs)
+//
+// An MFMA accumulator holds rows 4*(lane/16)+r and column lane%16; used as a
+// B operand its rows become the contraction index, so the A operand that
+// pairs with it reads its k values in the matching order {4g..4g+3,
+// 16+4g..16+4g+3} from a transposed ([d][row]) LDS copy.  The transposed
+// copies are produced in registers (4x8 bf16 block transpose) while the tile
+// is staged, so every LDS access is an 8- or 16-byte vector op.
+//
+// Causal tiles that are entirely masked are skipped (the reference dQ kernel
+// visits every key tile, fa_bw_dq.comp:114).  dQ is produced by its own
+// kernel, so no atomics and the result is deterministic.
+//
+// fp32 path (precision = fp32, parity mode): one wave per query (or key) row,
+// scalar FMAs with wave reductions, structured like the reference shaders.
+#include "ops.hpp"
+
+namespace vkh {
+
+namespace {
+
+constexpr float LOG2E = 1.4426950408889634f;
+constexpr float LN2 = 0.6931471805599453f;
+constexpr int NT = 256;
+
+// ── bf16 tile staging ────────────────────────────────────────────────
+
+// Stage a ROWS x HD bf16 tile (global rows [row0, row0 + ROWS), zero past
+// rmax) into LDS: `direct` [ROWS][HD + 8] and/or `trans` [HD][ROWS + 8].
+template <int ROWS, int HD>
+VKH_DEV void stage_tile(const bf16 *g, long ld, int row0, int rmax, bf16 (*direct)[HD + 8],
+                        bf16 (*trans)[ROWS + 8], int tid) {
+    constexpr int DC = HD / 8, UNITS = (ROWS / 4) * DC;
+    for (int u = tid; u < UNITS; u += NT) {
+        const int rg = u / DC, dc = u % DC;
+        uint4 w[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int r = row0 + rg * 4 + j;
+            w[j] = r < rmax ? *reinterpret_cast<const uint4 *>(g + (long)r * ld + dc * 8)
+                            : make_uint4(0, 0, 0, 0);
+        }
+        if (direct) {
+#pragma unroll
+            for (int j = 0; j < 4; ++j) *reinterpret_cast<uint4 *>(&direct[rg * 4 + j][dc * 8]) = w[j];
+        }
+        if (trans) {
+            const uint32_t *w0 = &w[0].x, *w1 = &w[1].x, *w2 = &w[2].x, *w3 = &w[3].x;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                uint2 lo, hi;
+                lo.x = (w0[c] & 0xffffu) | (w1[c] << 16);
+                lo.y = (w2[c] & 0xffffu) | (w3[c] << 16);
+                hi.x = (w0[c] >> 16) | (w1[c] & 0xffff0000u);
+                hi.y = (w2[c] >> 16) | (w3[c] & 0xffff0000u);
+                *reinterpret_cast<uint2 *>(&trans[dc * 8 + 2 * c][rg * 4]) = lo;
+                *reinterpret_cast<uint2 *>(&trans[dc * 8 + 2 * c + 1][rg * 4]) = hi;
+            }
+        }
+    }
+}
+
+// A-operand fragment from a transposed LDS copy: row `d`, contraction
+// block starting at `k0` (32 wide), lane group g -> k {4g..4g+3, 16+4g..}.
+template <int W>
+VKH_DEV bf16x8 frag_trans(const bf16 (*t)[W], int d, int k0, int g) {
+    const bf16x4 lo = *reinterpret_cast<const bf16x4 *>(&t[d][k0 + 4 * g]);
+    const bf16x4 hi = *reinterpret_cast<const bf16x4 *>(&t[d][k0 + 16 + 4 * g]);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// B-operand fragment from two accumulator tiles (contraction rows 0-15 of
+// tile a, 16-31 of tile b).
+VKH_DEV bf16x8 frag_acc(const f32x4 &a, const f32x4 &b) {
+    return cvt8(a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]);
+}
+
+VKH_DEV bf16x8 ld_frag(const bf16 *p) { return *reinterpret_cast<const bf16x8 *>(p); }
+
+// ── forward ──────────────────────────────────────────────────────────
+// Block: one (q-tile of 128 rows, head, sequence); 4 waves x 32 queries.
+template <int HD>
+__global__ __launch_bounds__(NT, 2) void fa_fwd_bf16_k(AttnShape s, const bf16 *q, long ldq,
+                                                        const bf16 *k, long ldk, const bf16 *v,
+                                                        long ldv, float *o, long ldo,
+                                                        float *lse) {
+    constexpr int BM = 128, BN = 64, DS = HD / 32, DSUB = HD / 16;
+    __shared__ __attribute__((aligned(16))) bf16 Ks[BN][HD + 8];
+    __shared__ __attribute__((aligned(16))) bf16 Vt[HD][BN + 8];
+
+    const int nqt = (s.n_q + BM - 1) / BM;
+    const int qt = s.causal ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (s.n_heads / s.n_kv_heads);
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
+    const int q0 = qt * BM, qw0 = q0 + wave * 32;
+    const int off = s.n_kv - s.n_q;
+    const bf16 *qb = q + (long)b * s.n_q * ldq + h * HD;
+    const bf16 *kb = k + (long)b * s.n_kv * ldk + kvh * HD;
+    const bf16 *vb = v + (long)b * s.n_kv * ldv + kvh * HD;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+
+    bf16x8 qf[2][DS];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int qr = qw0 + 16 * qs + c16;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+            qf[qs][ds] = qr < s.n_q ? ld_frag(qb + (long)qr * ldq + 32 * ds + 8 * g) : bf16x8{};
+    }
+    f32x4 oacc[DSUB][2];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i) oacc[i][0] = oacc[i][1] = f32x4{0, 0, 0, 0};
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+
+    int kend = s.n_kv;
+    if (s.causal) kend = min(s.n_kv, q0 + BM + off);
+    const int nkt = (kend + BN - 1) / BN;
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * BN;
+        __syncthreads();
+        stage_tile<BN, HD>(kb, ldk, k0, s.n_kv, Ks, nullptr, tid);
+        stage_tile<BN, HD>(vb, ldv, k0, s.n_kv, nullptr, Vt, tid);
+        __syncthreads();
+        // keys beyond this wave's last visible key are masked; skip if all are
+        const int wave_last_q = min(qw0 + 31, s.n_q - 1);
+        if (s.causal && k0 > wave_last_q + off) continue;
+
+        f32x4 st[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) st[ks][0] = st[ks][1] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 kf = ld_frag(&Ks[16 * ks + c16][32 * ds + 8 * g]);
+                st[ks][0] = mfma16x16x32(kf, qf[0][ds], st[ks][0]);
+                st[ks][1] = mfma16x16x32(kf, qf[1][ds], st[ks][1]);
+            }
+        bf16x8 pf[2][2];
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+            const int qa = qw0 + 16 * qs + c16;
+            float mt = -INFINITY;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ka = k0 + 16 * ks + 4 * g + r;
+                    float x = st[ks][qs][r] * c2;
+                    if (ka >= s.n_kv || (s.causal && ka > qa + off)) x = -INFINITY;
+                    st[ks][qs][r] = x;
+                    mt = fmaxf(mt, x);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float mn = fmaxf(m[qs], mt);
+            const float so = (m[qs] == -INFINITY) ? 0.f : exp2f(m[qs] - mn);
+            float lt = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = st[ks][qs][r];
+                    const float p = (x == -INFINITY) ? 0.f : exp2f(x - mn);
+                    st[ks][qs][r] = p;
+                    lt += p;
+                }
+            lt += __shfl_xor(lt, 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            l[qs] = l[qs] * so + lt;
+            m[qs] = mn;
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) oacc[i][qs] *= so;
+            pf[qs][0] = frag_acc(st[0][qs], st[1][qs]);
+            pf[qs][1] = frag_acc(st[2][qs], st[3][qs]);
+        }
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst)
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) {
+                const bf16x8 vf = frag_trans<BN + 8>(Vt, 16 * i + c16, 32 * kst, g);
+                oacc[i][0] = mfma16x16x32(vf, pf[0][kst], oacc[i][0]);
+                oacc[i][1] = mfma16x16x32(vf, pf[1][kst], oacc[i][1]);
+            }
+    }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int qa = qw0 + 16 * qs + c16;
+        if (qa >= s.n_q) continue;
+        const float inv = l[qs] > 0.f ? 1.0f / l[qs] : 0.f;
+        float *orow = o + ((long)b * s.n_q + qa) * ldo + h * HD;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = oacc[i][qs];
+            *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) =
+                make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+        }
+        if (lse && g == 0)
+            lse[((long)b * s.n_q + qa) * s.n_heads + h] =
+                l[qs] > 0.f ? (m[qs] + log2f(l[qs])) * LN2 : -INFINITY;
+    }
+}
+
+// ── backward: D = rowsum(O * dO) (fa_bw_d.comp), optional bf16 dO ─────
+__global__ void fa_bw_d_k(AttnShape s, const float *o, long ldo, const float *dout, long lddo,
+                          float *d, bf16 *dout16, long lddo16) {
+    const int lane = threadIdx.x % 64;
+    const long rows = (long)s.n_batch * s.n_q * s.n_heads;
+    const long row = (long)blockIdx.x * (NT / 64) + threadIdx.x / 64;
+    if (row >= rows) return;
+    const long t = row / s.n_heads;
+    const int h = (int)(row % s.n_heads);
+    const float *orow = o + t * ldo + h * s.head_dim;
+    const float *drow = dout + t * lddo + h * s.head_dim;
+    double acc = 0;
+    for (int e = lane; e < s.head_dim; e += 64) {
+        float dv = drow[e];
+        if (dout16) {
+            const bf16 r = (bf16)dv;
+            dout16[t * lddo16 + h * s.head_dim + e] = r;
+            dv = (float)r;  // D must pair with the dO the MFMA kernels see
+        }
+        acc += (double)orow[e] * (double)dv;
+    }
+    acc = wave_sum(acc);
+    if (lane == 0) d[t * s.n_heads + h] = (float)acc;
+}
+
+// ── backward: dK, dV (fa_bw_dkv.comp) ────────────────────────────────
+// Block: 128 keys of one kv head and sequence; 4 waves x 32 keys, K and V
+// fragments resident in registers; loops over the heads of the GQA group
+// and the q tiles (64 rows) that can see these keys.
+template <int HD>
+__global__ __launch_bounds__(NT, 1) void fa_bwd_dkv_bf16_k(AttnShape s, AttnPtrs p) {
+    constexpr int BN = 128, BM = 64, DS = HD / 32, DSUB = HD / 16;
+    __shared__ __attribute__((aligned(16))) bf16 Qs[BM][HD + 8];
+    __shared__ __attribute__((aligned(16))) bf16 dOs[BM][HD + 8];
+    __shared__ __attribute__((aligned(16))) bf16 Qt[HD][BM + 8];
+    __shared__ __attribute__((aligned(16))) bf16 dOt[HD][BM + 8];
+    __shared__ float lse_s[BM], d_s[BM];
+
+    const int nkt = (s.n_kv + BN - 1) / BN;
+    const int kt = s.causal ? nkt - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int hpk = s.n_heads / s.n_kv_heads;
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
+    const int k0 = kt * BN, kw0 = k0 + wave * 32;
+    const int off = s.n_kv - s.n_q;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+    const bf16 *kb = (const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD;
+    const bf16 *vb = (const bf16 *)p.v + (long)b * s.n_kv * p.ldv + kvh * HD;
+
+    bf16x8 kf[2][DS], vf[2][DS];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int kr = kw0 + 16 * ks + c16;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            kf[ks][ds] = kr < s.n_kv ? ld_frag(kb + (long)kr * p.ldk + 32 * ds + 8 * g) : bf16x8{};
+            vf[ks][ds] = kr < s.n_kv ? ld_frag(vb + (long)kr * p.ldv + 32 * ds + 8 * g) : bf16x8{};
+        }
+    }
+    f32x4 dvt[DSUB][2], dkt[DSUB][2];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i) dvt[i][0] = dvt[i][1] = dkt[i][0] = dkt[i][1] = f32x4{0, 0, 0, 0};
+
+    int qstart = 0;
+    if (s.causal) qstart = max(0, k0 - off) / BM * BM;
+    const int wave_first_k = kw0;
+    for (int hh = 0; hh < hpk; ++hh) {
+        const int h = kvh * hpk + hh;
+        const bf16 *qb = (const bf16 *)p.q + (long)b * s.n_q * p.ldq + h * HD;
+        const bf16 *ob = (const bf16 *)p.dout + (long)b * s.n_q * p.lddo + h * HD;
+        for (int q0 = qstart; q0 < s.n_q; q0 += BM) {
+            __syncthreads();
+            stage_tile<BM, HD>(qb, p.ldq, q0, s.n_q, Qs, Qt, tid);
+            stage_tile<BM, HD>(ob, p.lddo, q0, s.n_q, dOs, dOt, tid);
+            if (tid < BM) {
+                const int qa = q0 + tid;
+                const long t = (long)b * s.n_q + qa;
+                lse_s[tid] = qa < s.n_q ? p.lse[t * s.n_heads + h] * LOG2E : INFINITY;
+                d_s[tid] = qa < s.n_q ? p.d[t * s.n_heads + h] : 0.f;
+            }
+            __syncthreads();
+            // this wave's keys are all masked for every query of the tile?
+            if (s.causal && wave_first_k > q0 + BM - 1 + off) continue;
+
+            f32x4 sc[4][2], dp[4][2];
+#pragma unroll
+            for (int qs = 0; qs < 4; ++qs) sc[qs][0] = sc[qs][1] = dp[qs][0] = dp[qs][1] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+                for (int qs = 0; qs < 4; ++qs) {
+                    const bf16x8 qa = ld_frag(&Qs[16 * qs + c16][32 * ds + 8 * g]);
+                    const bf16x8 oa = ld_frag(&dOs[16 * qs + c16][32 * ds + 8 * g]);
+                    sc[qs][0] = mfma16x16x32(qa, kf[0][ds], sc[qs][0]);
+                    sc[qs][1] = mfma16x16x32(qa, kf[1][ds], sc[qs][1]);
+                    dp[qs][0] = mfma16x16x32(oa, vf[0][ds], dp[qs][0]);
+                    dp[qs][1] = mfma16x16x32(oa, vf[1][ds], dp[qs][1]);
+                }
+#pragma unroll
+            for (int qs = 0; qs < 4; ++qs)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ql = 16 * qs + 4 * g + r;
+                    const int qa = q0 + ql;
+                    const float lq = lse_s[ql], dq = d_s[ql];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const int ka = kw0 + 16 * ks + c16;
+                        float pv = (lq == -INFINITY) ? 0.f : exp2f(sc[qs][ks][r] * c2 - lq);
+                        if (qa >= s.n_q || ka >= s.n_kv || (s.causal && ka > qa + off)) pv = 0.f;
+                        sc[qs][ks][r] = pv;
+                        dp[qs][ks][r] = pv * (dp[qs][ks][r] - dq);
+                    }
+                }
+#pragma unroll
+            for (int qst = 0; qst < 2; ++qst) {
+                const bf16x8 pb0 = frag_acc(sc[2 * qst][0], sc[2 * qst + 1][0]);
+                const bf16x8 pb1 = frag_acc(sc[2 * qst][1], sc[2 * qst + 1][1]);
+                const bf16x8 sb0 = frag_acc(dp[2 * qst][0], dp[2 * qst + 1][0]);
+                const bf16x8 sb1 = frag_acc(dp[2 * qst][1], dp[2 * qst + 1][1]);
+#pragma unroll
+                for (int i = 0; i < DSUB; ++i) {
+                    const bf16x8 oa = frag_trans<BM + 8>(dOt, 16 * i + c16, 32 * qst, g);
+                    const bf16x8 qa = frag_trans<BM + 8>(Qt, 16 * i + c16, 32 * qst, g);
+                    dvt[i][0] = mfma16x16x32(oa, pb0, dvt[i][0]);
+                    dvt[i][1] = mfma16x16x32(oa, pb1, dvt[i][1]);
+                    dkt[i][0] = mfma16x16x32(qa, sb0, dkt[i][0]);
+                    dkt[i][1] = mfma16x16x32(qa, sb1, dkt[i][1]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int ka = kw0 + 16 * ks + c16;
+        if (ka >= s.n_kv) continue;
+        const long t = (long)b * s.n_kv + ka;
+        float *dkr = p.dk + t * p.lddk + kvh * HD;
+        float *dvr = p.dv + t * p.lddv + kvh * HD;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = dkt[i][ks], c = dvt[i][ks];
+            const float sc_ = s.inv_sqrt_dim;
+            *reinterpret_cast<float4 *>(dkr + 16 * i + 4 * g) = make_float4(a[0] * sc_, a[1] * sc_, a[2] * sc_, a[3] * sc_);
+            *reinterpret_cast<float4 *>(dvr + 16 * i + 4 * g) = make_float4(c[0], c[1], c[2], c[3]);
+        }
+    }
+}
+
+// ── backward: dQ (fa_bw_dq.comp) ─────────────────────────────────────
+// Block: 128 queries of one head and sequence; 4 waves x 32 queries with
+// Q and dO fragments in registers; loops over the key tiles (64) visible
+// under the causal mask.
+template <int HD>
+__global__ __launch_bounds__(NT, 1) void fa_bwd_dq_bf16_k(AttnShape s, AttnPtrs p) {
+    constexpr int BM = 128, BN = 64, DS = HD / 32, DSUB = HD / 16;
+    __shared__ __attribute__((aligned(16))) bf16 Ks[BN][HD + 8];
+    __shared__ __attribute__((aligned(16))) bf16 Vs[BN][HD + 8];
+    __shared__ __attribute__((aligned(16))) bf16 Kt[HD][BN + 8];
+
+    const int nqt = (s.n_q + BM - 1) / BM;
+    const int qt = s.causal ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (s.n_heads / s.n_kv_heads);
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
+    const int q0 = qt * BM, qw0 = q0 + wave * 32;
+    const int off = s.n_kv - s.n_q;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+    const bf16 *qb = (const bf16 *)p.q + (long)b * s.n_q * p.ldq + h * HD;
+    const bf16 *ob = (const bf16 *)p.dout + (long)b * s.n_q * p.lddo + h * HD;
+    const bf16 *kb = (const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD;
+    const bf16 *vb = (const bf16 *)p.v + (long)b * s.n_kv * p.ldv + kvh * HD;
+
+    bf16x8 qf[2][DS], of[2][DS];
+    float lq[2], dq[2];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int qa = qw0 + 16 * qs + c16;
+        const bool ok = qa < s.n_q;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            qf[qs][ds] = ok ? ld_frag(qb + (long)qa * p.ldq + 32 * ds + 8 * g) : bf16x8{};
+            of[qs][ds] = ok ? ld_frag(ob + (long)qa * p.lddo + 32 * ds + 8 * g) : bf16x8{};
+        }
+        const long t = (long)b * s.n_q + qa;
+        lq[qs] = ok ? p.lse[t * s.n_heads + h] * LOG2E : INFINITY;
+        dq[qs] = ok ? p.d[t * s.n_heads + h] : 0.f;
+    }
+    f32x4 acc[DSUB][2];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i) acc[i][0] = acc[i][1] = f32x4{0, 0, 0, 0};
+
+    int kend = s.n_kv;
+    if (s.causal) kend = min(s.n_kv, q0 + BM + off);
+    const int nkt = (kend + BN - 1) / BN;
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * BN;
+        __syncthreads();
+        stage_tile<BN, HD>(kb, p.ldk, k0, s.n_kv, Ks, Kt, tid);
+        stage_tile<BN, HD>(vb, p.ldv, k0, s.n_kv, Vs, nullptr, tid);
+        __syncthreads();
+        const int wave_last_q = min(qw0 + 31, s.n_q - 1);
+        if (s.causal && k0 > wave_last_q + off) continue;
+
+        f32x4 st[4][2], dpt[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) st[ks][0] = st[ks][1] = dpt[ks][0] = dpt[ks][1] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 ka = ld_frag(&Ks[16 * ks + c16][32 * ds + 8 * g]);
+                const bf16x8 va = ld_frag(&Vs[16 * ks + c16][32 * ds + 8 * g]);
+                st[ks][0] = mfma16x16x32(ka, qf[0][ds], st[ks][0]);
+                st[ks][1] = mfma16x16x32(ka, qf[1][ds], st[ks][1]);
+                dpt[ks][0] = mfma16x16x32(va, of[0][ds], dpt[ks][0]);
+                dpt[ks][1] = mfma16x16x32(va, of[1][ds], dpt[ks][1]);
+            }
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+            const int qa = qw0 + 16 * qs + c16;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ka = k0 + 16 * ks + 4 * g + r;
+                    float pv = (lq[qs] == -INFINITY) ? 0.f : exp2f(st[ks][qs][r] * c2 - lq[qs]);
+                    if (qa >= s.n_q || ka >= s.n_kv || (s.causal && ka > qa + off)) pv = 0.f;
+                    dpt[ks][qs][r] = pv * (dpt[ks][qs][r] - dq[qs]);
+                }
+        }
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst) {
+            const bf16x8 s0 = frag_acc(dpt[2 * kst][0], dpt[2 * kst + 1][0]);
+            const bf16x8 s1 = frag_acc(dpt[2 * kst][1], dpt[2 * kst + 1][1]);
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) {
+                const bf16x8 ka = frag_trans<BN + 8>(Kt, 16 * i + c16, 32 * kst, g);
+                acc[i][0] = mfma16x16x32(ka, s0, acc[i][0]);
+                acc[i][1] = mfma16x16x32(ka, s1, acc[i][1]);
+            }
+        }
+    }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int qa = qw0 + 16 * qs + c16;
+        if (qa >= s.n_q) continue;
+        float *dqr = p.dq + ((long)b * s.n_q + qa) * p.lddq + h * HD;
+        const float sc_ = s.inv_sqrt_dim;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = acc[i][qs];
+            *reinterpret_cast<float4 *>(dqr + 16 * i + 4 * g) = make_float4(a[0] * sc_, a[1] * sc_, a[2] * sc_, a[3] * sc_);
+        }
+    }
+}
+
+// ── fp32 path: one wave per row ──────────────────────────────────────
+
+constexpr int MAXE = 4;  // head_dim <= 256
+
+VKH_DEV float dot_wave(const float (&a)[MAXE], const float (&b)[MAXE]) {
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXE; ++i) acc += a[i] * b[i];
+    return wave_sum(acc);
+}
+
+VKH_DEV void load_row(float (&x)[MAXE], const float *p, int hd, int lane) {
+#pragma unroll
+    for (int i = 0; i < MAXE; ++i) {
+        const int e = lane + 64 * i;
+        x[i] = e < hd ? p[e] : 0.f;
+    }
+}
+
+// fa_forward.comp: wave per (query, head)
+__global__ void fa_fwd_f32_k(AttnShape s, const float *q, long ldq, const float *k, long ldk,
+                             const float *v, long ldv, float *o, long ldo, float *lse) {
+    const int lane = threadIdx.x % 64;
+    const long row = (long)blockIdx.x * (NT / 64) + threadIdx.x / 64;
+    const long rows = (long)s.n_batch * s.n_q * s.n_heads;
+    if (row >= rows) return;
+    const int h = (int)(row % s.n_heads);
+    const long t = row / s.n_heads;
+    const int b = (int)(t / s.n_q), qi = (int)(t % s.n_q);
+    const int kvh = h / (s.n_heads / s.n_kv_heads), hd = s.head_dim;
+    float qr[MAXE], orow[MAXE] = {0, 0, 0, 0};
+    load_row(qr, q + t * ldq + h * hd, hd, lane);
+    const int klim = s.causal ? min(s.n_kv - 1, qi + s.n_kv - s.n_q) : s.n_kv - 1;
+    float m = -INFINITY, l = 0.f;
+    for (int kk = 0; kk <= klim; ++kk) {
+        const long kt = (long)b * s.n_kv + kk;
+        float kr[MAXE], vr[MAXE];
+        load_row(kr, k + kt * ldk + kvh * hd, hd, lane);
+        const float sc = dot_wave(qr, kr) * s.inv_sqrt_dim;
+        const float mn = fmaxf(m, sc);
+        const float so = m == -INFINITY ? 0.f : expf(m - mn);
+        const float pv = expf(sc - mn);
+        load_row(vr, v + kt * ldv + kvh * hd, hd, lane);
+#pragma unroll
+        for (int i = 0; i < MAXE; ++i) orow[i] = orow[i] * so + pv * vr[i];
+        l = l * so + pv;
+        m = mn;
+    }
+    const float inv = l > 0.f ? 1.0f / l : 0.f;
+#pragma unroll
+    for (int i = 0; i < MAXE; ++i) {
+        const int e = lane + 64 * i;
+        if (e < hd) o[t * ldo + h * hd + e] = orow[i] * inv;
+    }
+    if (lse && lane == 0) lse[t * s.n_heads + h] = l > 0.f ? m + logf(l) : -INFINITY;
+}
+
+// fa_bw_dq.comp: wave per (query, head)
+__global__ void fa_bwd_dq_f32_k(AttnShape s, AttnPtrs p) {
+    const int lane = threadIdx.x % 64;
+    const long row = (long)blockIdx.x * (NT / 64) + threadIdx.x / 64;
+    const long rows = (long)s.n_batch * s.n_q * s.n_heads;
+    if (row >= rows) return;
+    const int h = (int)(row % s.n_heads);
+    const long t = row / s.n_heads;
+    const int b = (int)(t / s.n_q), qi = (int)(t % s.n_q);
+    const int kvh = h / (s.n_heads / s.n_kv_heads), hd = s.head_dim;
+    const float *Q = (const float *)p.q, *K = (const float *)p.k, *V = (const float *)p.v,
+                *dO = (const float *)p.dout;
+    float qr[MAXE], dor[MAXE], acc[MAXE] = {0, 0, 0, 0};
+    const float lq = p.lse[t * s.n_heads + h], dd = p.d[t * s.n_heads + h];
+    if (lq != -INFINITY) {
+        load_row(qr, Q + t * p.ldq + h * hd, hd, lane);
+        load_row(dor, dO + t * p.lddo + h * hd, hd, lane);
+        const int klim = s.causal ? min(s.n_kv - 1, qi + s.n_kv - s.n_q) : s.n_kv - 1;
+        for (int kk = 0; kk <= klim; ++kk) {
+            const long kt = (long)b * s.n_kv + kk;
+            float kr[MAXE], vr[MAXE];
+            load_row(kr, K + kt * p.ldk + kvh * hd, hd, lane);
+            load_row(vr, V + kt * p.ldv + kvh * hd, hd, lane);
+            const float pv = expf(dot_wave(qr, kr) * s.inv_sqrt_dim - lq);
+            const float ds = pv * (dot_wave(dor, vr) - dd) * s.inv_sqrt_dim;
+#pragma unroll
+            for (int i = 0; i < MAXE; ++i) acc[i] += ds * kr[i];
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXE; ++i) {
+        const int e = lane + 64 * i;
+        if (e < hd) p.dq[t * p.lddq + h * hd + e] = acc[i];
+    }
+}
+
+// fa_bw_dkv.comp: wave per (key, kv head), GQA fold inside
+__global__ void fa_bwd_dkv_f32_k(AttnShape s, AttnPtrs p) {
+    const int lane = threadIdx.x % 64;
+    const long row = (long)blockIdx.x * (NT / 64) + threadIdx.x / 64;
+    const long rows = (long)s.n_batch * s.n_kv * s.n_kv_heads;
+    if (row >= rows) return;
+    const int kvh = (int)(row % s.n_kv_heads);
+    const long t = row / s.n_kv_heads;
+    const int b = (int)(t / s.n_kv), ki = (int)(t % s.n_kv);
+    const int hpk = s.n_heads / s.n_kv_heads, hd = s.head_dim;
+    const float *Q = (const float *)p.q, *K = (const float *)p.k, *V = (const float *)p.v,
+                *dO = (const float *)p.dout;
+    float kr[MAXE], vr[MAXE], dk[MAXE] = {0, 0, 0, 0}, dv[MAXE] = {0, 0, 0, 0};
+    load_row(kr, K + t * p.ldk + kvh * hd, hd, lane);
+    load_row(vr, V + t * p.ldv + kvh * hd, hd, lane);
+    const int off = s.n_kv - s.n_q;
+    const int qmin = s.causal ? max(0, ki - off) : 0;
+    for (int hh = 0; hh < hpk; ++hh) {
+        const int h = kvh * hpk + hh;
+        for (int qi = qmin; qi < s.n_q; ++qi) {
+            const long qt = (long)b * s.n_q + qi;
+            const float lq = p.lse[qt * s.n_heads + h];
+            if (lq == -INFINITY) continue;
+            float qr[MAXE], dor[MAXE];
+            load_row(qr, Q + qt * p.ldq + h * hd, hd, lane);
+            load_row(dor, dO + qt * p.lddo + h * hd, hd, lane);
+            const float pv = expf(dot_wave(qr, kr) * s.inv_sqrt_dim - lq);
+            const float ds = pv * (dot_wave(dor, vr) - p.d[qt * s.n_heads + h]) * s.inv_sqrt_dim;
+#pragma unroll
+            for (int i = 0; i < MAXE; ++i) {
+                dv[i] += pv * dor[i];
+                dk[i] += ds * qr[i];
+            }
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < MAXE; ++i) {
+        const int e = lane + 64 * i;
+        if (e < hd) {
+            p.dk[t * p.lddk + kvh * hd + e] = dk[i];
+            p.dv[t * p.lddv + kvh * hd + e] = dv[i];
+        }
+    }
+}
+
+bool bf16_ok(const AttnShape &s) { return s.head_dim == 64 || s.head_dim == 128; }
+
+inline unsigned rows_grid(long rows) { return (unsigned)((rows + (NT / 64) - 1) / (NT / 64)); }
+
+}  // namespace
+
+hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
+                      const void *v, long ldv, float *o, long ldo, float *lse, DType dt,
+                      hipStream_t st) {
+    if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
+    if (s.n_kv_heads <= 0 || s.n_heads % s.n_kv_heads) return hipErrorInvalidValue;
+    if (dt == DType::BF16) {
+        if (!bf16_ok(s)) return hipErrorInvalidValue;
+        dim3 grid((s.n_q + 127) / 128, s.n_heads, s.n_batch);
+        if (s.head_dim == 128)
+            hipLaunchKernelGGL(fa_fwd_bf16_k<128>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
+                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse);
+        else
+            hipLaunchKernelGGL(fa_fwd_bf16_k<64>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
+                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse);
+    } else {
+        if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(fa_fwd_f32_k, dim3(rows_grid((long)s.n_batch * s.n_q * s.n_heads)),
+                           dim3(NT), 0, st, s, (const float *)q, ldq, (const float *)k, ldk,
+                           (const float *)v, ldv, o, ldo, lse);
+    }
+    return hipGetLastError();
+}
+
+hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *dout, long lddo,
+                   float *d, bf16 *dout_bf16, long lddo16, hipStream_t st) {
+    const long rows = (long)s.n_batch * s.n_q * s.n_heads;
+    if (rows <= 0) return hipSuccess;
+    hipLaunchKernelGGL(fa_bw_d_k, dim3(rows_grid(rows)), dim3(NT), 0, st, s, o, ldo, dout, lddo, d,
+                       dout_bf16, lddo16);
+    return hipGetLastError();
+}
+
+hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
+    if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
+    if (s.n_kv_heads <= 0 || s.n_heads % s.n_kv_heads) return hipErrorInvalidValue;
+    if (p.dt == DType::BF16) {
+        if (!bf16_ok(s)) return hipErrorInvalidValue;
+        dim3 grid((s.n_q + 127) / 128, s.n_heads, s.n_batch);
+        if (s.head_dim == 128)
+            hipLaunchKernelGGL(fa_bwd_dq_bf16_k<128>, grid, dim3(NT), 0, st, s, p);
+        else
+            hipLaunchKernelGGL(fa_bwd_dq_bf16_k<64>, grid, dim3(NT), 0, st, s, p);
+    } else {
+        if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(fa_bwd_dq_f32_k, dim3(rows_grid((long)s.n_batch * s.n_q * s.n_heads)),
+                           dim3(NT), 0, st, s, p);
+    }
+    return hipGetLastError();
+}
+
+hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
+    if (s.n_batch <= 0 || s.n_kv <= 0) return hipSuccess;
+    if (s.n_kv_heads <= 0 || s.n_heads % s.n_kv_heads) return hipErrorInvalidValue;
+    if (p.dt == DType::BF16) {
+        if (!bf16_ok(s)) return hipErrorInvalidValue;
+        dim3 grid((s.n_kv + 127) / 128, s.n_kv_heads, s.n_batch);
+        if (s.head_dim == 128)
+            hipLaunchKernelGGL(fa_bwd_dkv_bf16_k<128>, grid, dim3(NT), 0, st, s, p);
+        else
+            hipLaunchKernelGGL(fa_bwd_dkv_bf16_k<64>, grid, dim3(NT), 0, st, s, p);
+    } else {
+        if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
+        hipLaunchKernelGGL(fa_bwd_dkv_f32_k,
+                           dim3(rows_grid((long)s.n_batch * s.n_kv * s.n_kv_heads)), dim3(NT), 0,
+                           st, s, p);
+    }
+    return hipGetLastError();
+}
+
+}  // namespace vkh

@@ -1,0 +1,223 @@
+// Cut cross-entropy over the vocabulary (reference: shaders/cce_forward.comp,
+// cce_backward_dh.comp, cce_backward_dw.comp; oracle src/cpu/cce.zig:89-268).
+//
+// Forward: the logits z = h W^T are produced tile by tile by the MFMA GEMM
+// and never stored; its epilogue reduces each wave's 64-column slice of a row
+// to (max, sum exp(z - max), sum z) and captures the target logit.  A second
+// kernel merges the slices per row (fp64) into lse and the per-row loss
+// lse - (1 - eps) z_t - eps mean(z) + lambda_z lse^2, and a third averages.
+//
+// Backward: the logits are recomputed once by the GEMM whose epilogue writes
+//   dz = ((1 + 2 lambda_z lse) exp(z - lse) - (1 - eps)[v == t] - eps / V) / N
+// (bf16 in the bf16 precision, fp32 otherwise) to HBM, then two MFMA GEMMs
+// form dh = dz W and dW = dz^T h.  The reference recomputes the logits twice
+// with scalar dot products (per row for dh, per vocab row for dW,
+// cce_backward_dh.comp:109-123, cce_backward_dw.comp:73-103); on a 288 GB
+// part the [N, V] dz buffer (0.6 GB at N = 2048) is cheap and turns the
+// backward into three dense GEMMs.
+#include "gemm.hpp"
+#include "ops.hpp"
+
+namespace vkh {
+
+namespace {
+
+constexpr int WN = 64;  // columns per wave slice with the 128x128 tile
+constexpr float LOG2E = 1.4426950408889634f;
+
+struct CceWork {
+    float *pm, *ps, *pz;  // [N][nparts]
+    float *zt;            // [N]
+    int nparts;
+};
+
+inline CceWork carve(float *work, const CceShape &s) {
+    const int np = (s.V + WN - 1) / WN;
+    const size_t part = (size_t)s.N * np;
+    return CceWork{work, work + part, work + 2 * part, work + 3 * part, np};
+}
+
+struct EpiCceStats {
+    CceWork w;
+    const uint32_t *tgt;
+    int V;
+
+    template <int TM, int TN>
+    VKH_DEV void apply(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s) const {
+        static_assert(TN * 16 == WN, "wave slice width");
+        const int c16 = fp.lane % 16, g = fp.lane / 16;
+        const int part = fp.col0 / WN;
+        // the last tile's second slice can lie wholly past V: it owns no partial
+        if (part >= w.nparts) return;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = fp.row0 + 16 * i + 4 * g + r;
+                const bool rok = row < s.M;
+                const uint32_t t = rok ? tgt[row] : 0xffffffffu;
+                float mx = -INFINITY, zs = 0.f;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = fp.col0 + 16 * j + c16;
+                    if (col < V) {
+                        const float z = acc[i][j][r];
+                        mx = fmaxf(mx, z);
+                        zs += z;
+                        if ((uint32_t)col == t) w.zt[row] = z;
+                    }
+                }
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                float se = 0.f;
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = fp.col0 + 16 * j + c16;
+                    if (col < V) se += exp2f((acc[i][j][r] - mx) * LOG2E);
+                }
+#pragma unroll
+                for (int o = 1; o < 16; o <<= 1) {
+                    se += __shfl_xor(se, o, 64);
+                    zs += __shfl_xor(zs, o, 64);
+                }
+                if (rok && c16 == 0) {
+                    const size_t idx = (size_t)row * w.nparts + part;
+                    w.pm[idx] = mx;
+                    w.ps[idx] = se;
+                    w.pz[idx] = zs;
+                }
+            }
+    }
+};
+
+template <typename TZ>
+struct EpiCceDz {
+    TZ *dz;
+    const uint32_t *tgt;
+    const float *lse;
+    int V;
+    float inv_n, t_scale, eps_over_v, zl2;
+
+    template <int TM, int TN>
+    VKH_DEV void apply(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s) const {
+        const int c16 = fp.lane % 16, g = fp.lane / 16;
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = fp.row0 + 16 * i + 4 * g + r;
+                if (row >= s.M) continue;
+                const float l = lse[row];
+                const float sf = 1.0f + zl2 * l;
+                const uint32_t t = tgt[row];
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const int col = fp.col0 + 16 * j + c16;
+                    if (col >= V) continue;
+                    const float p = expf(acc[i][j][r] - l);
+                    const float ti = ((uint32_t)col == t) ? t_scale : 0.0f;
+                    const float d = (sf * p - ti - eps_over_v) * inv_n;
+                    dz[(size_t)row * V + col] = (TZ)d;
+                }
+            }
+    }
+};
+
+__global__ void cce_merge_k(CceShape s, CceWork w, float *lse, float *loss_row) {
+    const int lane = threadIdx.x % 64;
+    const int row = blockIdx.x * (blockDim.x / 64) + threadIdx.x / 64;
+    if (row >= s.N) return;
+    const float *pm = w.pm + (size_t)row * w.nparts;
+    const float *ps = w.ps + (size_t)row * w.nparts;
+    const float *pz = w.pz + (size_t)row * w.nparts;
+    float M = -INFINITY;
+    for (int i = lane; i < w.nparts; i += 64) M = fmaxf(M, pm[i]);
+    M = wave_max(M);
+    double S = 0, Z = 0;
+    for (int i = lane; i < w.nparts; i += 64) {
+        S += (double)ps[i] * exp((double)pm[i] - (double)M);
+        Z += (double)pz[i];
+    }
+    S = wave_sum(S);
+    Z = wave_sum(Z);
+    if (lane == 0) {
+        const float l = (float)(log(S) + (double)M);
+        lse[row] = l;
+        const double eps = s.label_smoothing;
+        const double ce = (double)l - (double)(1.0f - s.label_smoothing) * (double)w.zt[row] -
+                          eps * (Z / (double)s.V);
+        const double zp = (double)s.z_loss_scale * (double)l * (double)l;
+        if (loss_row) loss_row[row] = (float)(ce + zp);
+        w.pm[(size_t)row * w.nparts] = (float)(ce + zp);  // reuse slot 0 for the mean
+    }
+}
+
+__global__ void cce_mean_k(CceShape s, CceWork w, float *loss_mean) {
+    __shared__ double sh[4];
+    double acc = 0;
+    for (int r = threadIdx.x; r < s.N; r += blockDim.x) acc += (double)w.pm[(size_t)r * w.nparts];
+    acc = wave_sum(acc);
+    if (threadIdx.x % 64 == 0) sh[threadIdx.x / 64] = acc;
+    __syncthreads();
+    if (threadIdx.x == 0) loss_mean[0] = (float)((sh[0] + sh[1] + sh[2] + sh[3]) / (double)s.N);
+}
+
+template <class Epi>
+hipError_t logits_gemm(Precision pr, const CceShape &s, const float *h, const float *w,
+                       const Epi &epi, hipStream_t st) {
+    GemmOperand a{h, s.D, vec_ok(h, s.D, 4, Lay::K)};
+    GemmOperand b{w, s.D, vec_ok(w, s.D, 4, Lay::K)};
+    GemmShape sh{s.N, s.V, s.D};
+    if (pr == Precision::BF16)
+        return launch_gemm<TileCfg<128, 128, 64>, true, float, Lay::K, float, Lay::K>(a, b, sh, epi, st);
+    return launch_gemm<TileCfg<128, 128, 32>, false, float, Lay::K, float, Lay::K>(a, b, sh, epi, st);
+}
+
+}  // namespace
+
+size_t cce_work_floats(const CceShape &s) {
+    const size_t np = (s.V + WN - 1) / WN;
+    return 3 * (size_t)s.N * np + s.N;
+}
+
+hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const float *w,
+                       const uint32_t *tgt, float *lse, float *loss_row, float *loss_mean,
+                       float *work, hipStream_t st) {
+    if (s.N <= 0) return hipSuccess;
+    CceWork cw = carve(work, s);
+    EpiCceStats e{cw, tgt, s.V};
+    hipError_t err = logits_gemm(pr, s, h, w, e, st);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(cce_merge_k, dim3(ceil_div(s.N, 4)), dim3(256), 0, st, s, cw, lse, loss_row);
+    if (loss_mean) hipLaunchKernelGGL(cce_mean_k, dim3(1), dim3(256), 0, st, s, cw, loss_mean);
+    return hipGetLastError();
+}
+
+hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const float *w,
+                        const uint32_t *tgt, const float *lse, void *dz, float *dh, float *dw,
+                        float dw_beta, hipStream_t st) {
+    if (s.N <= 0) return hipSuccess;
+    const float inv_n = 1.0f / (float)s.N;
+    const float t_scale = 1.0f - s.label_smoothing;
+    const float eps_over_v = s.label_smoothing / (float)s.V;
+    const float zl2 = 2.0f * s.z_loss_scale;
+    hipError_t err;
+    const DType zdt = pr == Precision::BF16 ? DType::BF16 : DType::F32;
+    if (zdt == DType::BF16) {
+        EpiCceDz<bf16> e{(bf16 *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2};
+        err = logits_gemm(pr, s, h, w, e, st);
+    } else {
+        EpiCceDz<float> e{(float *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2};
+        err = logits_gemm(pr, s, h, w, e, st);
+    }
+    if (err != hipSuccess) return err;
+    const Mat mz{dz, s.V, zdt};
+    if (dw) {
+        err = gemm_tn(pr, mz, matf(h, s.D), dw, s.D, s.N, s.V, s.D, 1.f, dw_beta, st);
+        if (err != hipSuccess) return err;
+    }
+    if (dh) err = gemm_nn(pr, mz, matf(w, s.D), dh, s.D, s.N, s.V, s.D, 1.f, 0.f, st);
+    return err;
+}
+
+}  // namespace vkh

@@ -1,0 +1,285 @@
+// Bandwidth-bound elementwise kernels: fill, add, scale, cast, SwiGLU fwd/bwd,
+// embedding lookup and Adam.  All are float4-vectorised grid-stride loops
+// sized to fill the 256 CUs; fp contraction is disabled so each kernel
+// rounds exactly like the scalar reference formula it restates.
+#include "ops.hpp"
+
+#pragma clang fp contract(off)
+
+namespace vkh {
+
+namespace {
+
+constexpr int NT = 256;
+
+inline unsigned grid_for(size_t n_vec) {
+    size_t g = (n_vec + NT - 1) / NT;
+    const size_t cap = 256 * 16;  // 16 blocks per CU is plenty for a streaming kernel
+    if (g > cap) g = cap;
+    return (unsigned)(g ? g : 1);
+}
+
+__global__ void fill_k(float *p, size_t n, float v, bool vec) {
+    const size_t n4 = vec ? n / 4 : 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    float4 f = make_float4(v, v, v, v);
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride)
+        reinterpret_cast<float4 *>(p)[i] = f;
+    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) p[i] = v;
+}
+
+__global__ void add_k(float *dst, const float *a, const float *b, size_t n, bool vec) {
+    // dst = a + b  (dst may alias a)
+    const size_t n4 = vec ? n / 4 : 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 x = reinterpret_cast<const float4 *>(a)[i];
+        float4 y = reinterpret_cast<const float4 *>(b)[i];
+        reinterpret_cast<float4 *>(dst)[i] = make_float4(x.x + y.x, x.y + y.y, x.z + y.z, x.w + y.w);
+    }
+    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride)
+        dst[i] = a[i] + b[i];
+}
+
+__global__ void scale_k(const float *in, float *out, size_t n, float s, bool vec) {
+    const size_t n4 = vec ? n / 4 : 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 x = reinterpret_cast<const float4 *>(in)[i];
+        reinterpret_cast<float4 *>(out)[i] = make_float4(x.x * s, x.y * s, x.z * s, x.w * s);
+    }
+    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = in[i] * s;
+}
+
+__global__ void cast_bf16_k(const float *in, bf16 *out, size_t n, bool vec) {
+    const size_t n4 = vec ? n / 4 : 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 x = reinterpret_cast<const float4 *>(in)[i];
+        bf16x4 y;
+        y[0] = (bf16)x.x; y[1] = (bf16)x.y; y[2] = (bf16)x.z; y[3] = (bf16)x.w;
+        reinterpret_cast<bf16x4 *>(out)[i] = y;
+    }
+    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride)
+        out[i] = (bf16)in[i];
+}
+
+// sigmoid(z) = 1 / (1 + exp(-z))  (train_transformer.zig:832-834)
+__device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
+
+// swiglu_forward.comp / train_transformer.zig:839-851
+__global__ void swiglu_fwd_k(const float *pg, long ldpg, const float *up, long ldup, float *g,
+                             long ldg, int rows, int cols4) {
+    const size_t n = (size_t)rows * cols4;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int r = (int)(i / cols4), c = (int)(i % cols4) * 4;
+        float4 z = *reinterpret_cast<const float4 *>(pg + r * ldpg + c);
+        float4 u = *reinterpret_cast<const float4 *>(up + r * ldup + c);
+        float4 o;
+        o.x = z.x * sigmoidf_(z.x) * u.x;
+        o.y = z.y * sigmoidf_(z.y) * u.y;
+        o.z = z.z * sigmoidf_(z.z) * u.z;
+        o.w = z.w * sigmoidf_(z.w) * u.w;
+        *reinterpret_cast<float4 *>(g + r * ldg + c) = o;
+    }
+}
+
+__device__ __forceinline__ void swiglu_bw1(float dg, float z, float u, float &dz, float &du) {
+    const float sig = sigmoidf_(z);
+    const float silu_z = z * sig;
+    const float silu_grad = sig + silu_z * (1.0f - sig);
+    du = dg * silu_z;
+    dz = dg * u * silu_grad;
+}
+
+// swiglu_backward.comp / train_transformer.zig:857-875
+__global__ void swiglu_bwd_k(const float *dg, long lddg, const float *pg, long ldpg,
+                             const float *up, long ldup, float *dpg, long lddpg, float *dup,
+                             long lddup, int rows, int cols4) {
+    const size_t n = (size_t)rows * cols4;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int r = (int)(i / cols4), c = (int)(i % cols4) * 4;
+        float4 d = *reinterpret_cast<const float4 *>(dg + r * lddg + c);
+        float4 z = *reinterpret_cast<const float4 *>(pg + r * ldpg + c);
+        float4 u = *reinterpret_cast<const float4 *>(up + r * ldup + c);
+        float4 oz, ou;
+        swiglu_bw1(d.x, z.x, u.x, oz.x, ou.x);
+        swiglu_bw1(d.y, z.y, u.y, oz.y, ou.y);
+        swiglu_bw1(d.z, z.z, u.z, oz.z, ou.z);
+        swiglu_bw1(d.w, z.w, u.w, oz.w, ou.w);
+        *reinterpret_cast<float4 *>(dpg + r * lddpg + c) = oz;
+        *reinterpret_cast<float4 *>(dup + r * lddup + c) = ou;
+    }
+}
+
+// scalar fallbacks for shapes whose columns are not a multiple of 4
+__global__ void swiglu_fwd_s(const float *pg, long ldpg, const float *up, long ldup, float *g,
+                             long ldg, int rows, int cols) {
+    const size_t n = (size_t)rows * cols;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int r = (int)(i / cols), c = (int)(i % cols);
+        const float z = pg[r * ldpg + c];
+        g[r * ldg + c] = z * sigmoidf_(z) * up[r * ldup + c];
+    }
+}
+
+__global__ void swiglu_bwd_s(const float *dg, long lddg, const float *pg, long ldpg,
+                             const float *up, long ldup, float *dpg, long lddpg, float *dup,
+                             long lddup, int rows, int cols) {
+    const size_t n = (size_t)rows * cols;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+        const int r = (int)(i / cols), c = (int)(i % cols);
+        float dz, du;
+        swiglu_bw1(dg[r * lddg + c], pg[r * ldpg + c], up[r * ldup + c], dz, du);
+        dpg[r * lddpg + c] = dz;
+        dup[r * lddup + c] = du;
+    }
+}
+
+// embed_lookup_batched.comp
+__global__ void embed_lookup_k(const float *embed, const uint32_t *ids, float *out, int n_pos,
+                               int dim, float scale, bool vec) {
+    const size_t n = (size_t)n_pos * dim;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    if (vec) {
+        const int d4 = dim / 4;
+        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n / 4; i += stride) {
+            const int p = (int)(i / d4), c = (int)(i % d4);
+            float4 e = reinterpret_cast<const float4 *>(embed + (size_t)ids[p] * dim)[c];
+            reinterpret_cast<float4 *>(out)[i] = make_float4(e.x * scale, e.y * scale, e.z * scale, e.w * scale);
+        }
+    } else {
+        for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
+            const int p = (int)(i / dim), c = (int)(i % dim);
+            out[i] = embed[(size_t)ids[p] * dim + c] * scale;
+        }
+    }
+}
+
+// adam_step.comp:41-62
+__device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, float lr, float b1,
+                                      float b2, float eps, float bc1, float bc2, float wd) {
+    const float nm = b1 * m + (1.0f - b1) * g;
+    const float nv = b2 * v + (1.0f - b2) * g * g;
+    m = nm;
+    v = nv;
+    const float m_hat = nm / bc1;
+    const float v_hat = nv / bc2;
+    float q = p;
+    if (wd > 0.0f) q = q * (1.0f - lr * wd);
+    p = q - lr * m_hat / (sqrtf(v_hat) + eps);
+}
+
+__global__ void adam_k(float *p, const float *g, float *m, float *v, size_t n, float lr, float b1,
+                       float b2, float eps, float bc1, float bc2, float wd, bool vec) {
+    const size_t n4 = vec ? n / 4 : 0;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+        float4 pp = reinterpret_cast<float4 *>(p)[i];
+        float4 gg = reinterpret_cast<const float4 *>(g)[i];
+        float4 mm = reinterpret_cast<float4 *>(m)[i];
+        float4 vv = reinterpret_cast<float4 *>(v)[i];
+        adam1(pp.x, gg.x, mm.x, vv.x, lr, b1, b2, eps, bc1, bc2, wd);
+        adam1(pp.y, gg.y, mm.y, vv.y, lr, b1, b2, eps, bc1, bc2, wd);
+        adam1(pp.z, gg.z, mm.z, vv.z, lr, b1, b2, eps, bc1, bc2, wd);
+        adam1(pp.w, gg.w, mm.w, vv.w, lr, b1, b2, eps, bc1, bc2, wd);
+        reinterpret_cast<float4 *>(p)[i] = pp;
+        reinterpret_cast<float4 *>(m)[i] = mm;
+        reinterpret_cast<float4 *>(v)[i] = vv;
+    }
+    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride)
+        adam1(p[i], g[i], m[i], v[i], lr, b1, b2, eps, bc1, bc2, wd);
+}
+
+inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+}  // namespace
+
+hipError_t fill_f32(float *p, size_t n, float v, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(fill_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, p, n, v, al16(p));
+    return hipGetLastError();
+}
+
+hipError_t add_in_place(float *dst, const float *src, size_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(add_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, dst, (const float *)dst,
+                       src, n, al16(dst) && al16(src));
+    return hipGetLastError();
+}
+
+hipError_t vec_add(const float *a, const float *b, float *c, size_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(add_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, c, a, b, n,
+                       al16(a) && al16(b) && al16(c));
+    return hipGetLastError();
+}
+
+hipError_t scale(const float *in, float *out, size_t n, float s, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(scale_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, in, out, n, s,
+                       al16(in) && al16(out));
+    return hipGetLastError();
+}
+
+hipError_t cast_f32_to_bf16(const float *in, bf16 *out, size_t n, hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(cast_bf16_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, in, out, n,
+                       al16(in) && ((uintptr_t)out & 7u) == 0);
+    return hipGetLastError();
+}
+
+hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup, float *g,
+                          long ldg, int rows, int cols, hipStream_t st) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const bool v4 = (cols % 4 == 0) && (ldpg % 4 == 0) && (ldup % 4 == 0) && (ldg % 4 == 0) &&
+                    al16(pg) && al16(up) && al16(g);
+    if (v4)
+        hipLaunchKernelGGL(swiglu_fwd_k, dim3(grid_for((size_t)rows * cols / 4)), dim3(NT), 0, st,
+                           pg, ldpg, up, ldup, g, ldg, rows, cols / 4);
+    else
+        hipLaunchKernelGGL(swiglu_fwd_s, dim3(grid_for((size_t)rows * cols)), dim3(NT), 0, st, pg,
+                           ldpg, up, ldup, g, ldg, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t swiglu_backward(const float *dg, long lddg, const float *pg, long ldpg,
+                           const float *up, long ldup, float *dpg, long lddpg, float *dup,
+                           long lddup, int rows, int cols, hipStream_t st) {
+    if (rows <= 0 || cols <= 0) return hipSuccess;
+    const bool v4 = (cols % 4 == 0) && (lddg % 4 == 0) && (ldpg % 4 == 0) && (ldup % 4 == 0) &&
+                    (lddpg % 4 == 0) && (lddup % 4 == 0) && al16(dg) && al16(pg) && al16(up) &&
+                    al16(dpg) && al16(dup);
+    if (v4)
+        hipLaunchKernelGGL(swiglu_bwd_k, dim3(grid_for((size_t)rows * cols / 4)), dim3(NT), 0, st,
+                           dg, lddg, pg, ldpg, up, ldup, dpg, lddpg, dup, lddup, rows, cols / 4);
+    else
+        hipLaunchKernelGGL(swiglu_bwd_s, dim3(grid_for((size_t)rows * cols)), dim3(NT), 0, st, dg,
+                           lddg, pg, ldpg, up, ldup, dpg, lddpg, dup, lddup, rows, cols);
+    return hipGetLastError();
+}
+
+hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int n_pos, int dim,
+                        float scale_, hipStream_t st) {
+    if (n_pos <= 0 || dim <= 0) return hipSuccess;
+    const bool v4 = (dim % 4 == 0) && al16(embed) && al16(out);
+    hipLaunchKernelGGL(embed_lookup_k, dim3(grid_for((size_t)n_pos * dim / (v4 ? 4 : 1))), dim3(NT),
+                       0, st, embed, ids, out, n_pos, dim, scale_, v4);
+    return hipGetLastError();
+}
+
+hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,
+                     float beta1, float beta2, float eps, float bc1, float bc2, float wd,
+                     hipStream_t st) {
+    if (!n) return hipSuccess;
+    hipLaunchKernelGGL(adam_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, p, g, m, v, n, lr,
+                       beta1, beta2, eps, bc1, bc2, wd, al16(p) && al16(g) && al16(m) && al16(v));
+    return hipGetLastError();
+}
+
+}  // namespace vkh

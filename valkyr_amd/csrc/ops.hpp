@@ -1,0 +1,143 @@
+// Host-side entry points of the HIP kernels (internal to libvkhip; the C ABI
+// in include/vkhip.h wraps them).  All pointers are device pointers; every
+// function only enqueues on `st` and returns the launch status.
+#pragma once
+
+#include "common.hpp"
+
+namespace vkh {
+
+enum class DType : int { F32 = 0, BF16 = 1 };
+enum class Precision : int { FP32 = 0, BF16 = 1 };
+
+struct Mat {
+    const void *p;
+    long ld;
+    DType dt;
+};
+
+inline Mat matf(const float *p, long ld) { return Mat{p, ld, DType::F32}; }
+
+// ── GEMMs (k_gemm.hip) ────────────────────────────────────────────────
+// y[M,N] = alpha * x[M,K] W[N,K]^T  (+ R[M,N] residual, optional; + beta*y_old)
+hipError_t gemm_nt(Precision pr, Mat x, Mat w, float *y, long ldy, int M, int N, int K,
+                   const float *R, long ldr, float alpha, float beta, hipStream_t st);
+// dx[M,K] = dy[M,N] W[N,K]  (+ beta*dx_old)
+hipError_t gemm_nn(Precision pr, Mat dy, Mat w, float *dx, long lddx, int M, int N, int K,
+                   float alpha, float beta, hipStream_t st);
+// dW[N,K] = dy[M,N]^T x[M,K]  (+ beta*dW_old)
+hipError_t gemm_tn(Precision pr, Mat dy, Mat x, float *dw, long lddw, int M, int N, int K,
+                   float alpha, float beta, hipStream_t st);
+// bf16-output forward GEMM (used for LoRA intermediates and bf16 copies)
+hipError_t gemm_nt_bf16out(Mat x, Mat w, bf16 *y, long ldy, int M, int N, int K, float alpha,
+                           hipStream_t st);
+
+// ── elementwise / normalisation (k_elementwise.hip, k_norm.hip) ───────
+hipError_t fill_f32(float *p, size_t n, float v, hipStream_t st);
+hipError_t add_in_place(float *dst, const float *src, size_t n, hipStream_t st);
+hipError_t vec_add(const float *a, const float *b, float *c, size_t n, hipStream_t st);
+hipError_t scale(const float *in, float *out, size_t n, float s, hipStream_t st);
+hipError_t cast_f32_to_bf16(const float *in, bf16 *out, size_t n, hipStream_t st);
+hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup, float *g,
+                          long ldg, int rows, int cols, hipStream_t st);
+hipError_t swiglu_backward(const float *dg, long lddg, const float *pg, long ldpg,
+                           const float *up, long ldup, float *dpg, long lddpg, float *dup,
+                           long lddup, int rows, int cols, hipStream_t st);
+hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int n_pos, int dim,
+                        float scale, hipStream_t st);
+// Adam (adam_step.comp): bc1 = 1 - beta1^t, bc2 = 1 - beta2^t computed by the caller.
+hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,
+                     float beta1, float beta2, float eps, float bc1, float bc2, float wd,
+                     hipStream_t st);
+
+hipError_t rmsnorm_forward(const float *x, const float *w, float *y, int rows, int dim,
+                           float eps, int gemma_quirk, hipStream_t st);
+// dx = rmsnorm_bw(dy) (+ residual add), dw (reduced over rows, overwrite);
+// `partial` must hold rmsnorm_partial_floats(rows, dim) floats.
+hipError_t rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
+                            const float *residual, float *dw, float *partial, int rows,
+                            int dim, float eps, int gemma_quirk, hipStream_t st);
+size_t rmsnorm_partial_floats(int rows, int dim);
+
+// RoPE cos/sin table [seq_len][rotary_dim/2] as float2, built on the host
+// with the fp32 formula of qk_rope_partial_batched.comp:76-81.
+void rope_table_host(float2 *tab, int seq_len, int rotary_dim, float theta);
+// qk_rope_partial_batched.comp / qk_rope_backward_batched.comp (position of
+// row r = r % seq_len).
+hipError_t qk_rope(const float *q_in, long ldq_in, float *q_out, long ldq_out, const float *k_in,
+                   long ldk_in, float *k_out, long ldk_out, int n_rows, int n_q_heads,
+                   int n_kv_heads, int head_dim, int rotary_dim, int seq_len, const float2 *tab,
+                   bool backward, hipStream_t st);
+
+// Fused per-head Q/K RMSNorm + RoPE forward, emitting the attention
+// operands (fp32 or bf16) for q, k and (copy/cast of) v.
+struct QkvLayout {
+    int n_rows, n_q_heads, n_kv_heads, head_dim;
+    int seq_len, rotary_dim;
+    float theta, eps;
+    int qk_norm;
+};
+hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv,
+                               const float *wq, const float *wk, void *out, long ld_out,
+                               DType out_dt, const float2 *rope_tab, hipStream_t st);
+// Backward of the above on the fused d_qkv buffer, in place for the q/k
+// columns: d(post-rope) -> d(pre-norm); dwq/dwk reduced gains (overwrite).
+hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const float *qkv,
+                                long ld_qkv, const float *wq, const float *wk, float *dwq,
+                                float *dwk, float *partial, const float2 *rope_tab,
+                                hipStream_t st);
+size_t qkv_partial_floats(const QkvLayout &L);
+
+// ── embedding backward (k_embed.hip) ─────────────────────────────────
+// out[tok] = (accumulate ? out[tok] : 0) + sum over positions p with
+// ids[p] == tok of dy[p] (position order).  Rows of untouched tokens are not
+// written.  `work` must hold embed_bw_work_bytes(n_pos) bytes.
+hipError_t embedding_backward(const float *dy, const uint32_t *ids, float *out, int n_pos,
+                              int dim, int vocab, bool accumulate, void *work, hipStream_t st);
+size_t embed_bw_work_bytes(int n_pos);
+constexpr int kEmbedBwMaxPos = 16384;
+
+// ── attention (k_attn.hip) ───────────────────────────────────────────
+struct AttnShape {
+    int n_batch, n_q, n_kv, n_heads, n_kv_heads, head_dim;
+    int causal;
+    float inv_sqrt_dim;
+};
+struct AttnPtrs {
+    const void *q; long ldq;   // [T, n_heads*hd] rows, elements of dtype dt
+    const void *k; long ldk;
+    const void *v; long ldv;
+    const float *o; long ldo;  // fp32 forward output (for D)
+    const void *dout; long lddo; // upstream gradient (dtype dt)
+    const float *lse;          // [T, n_heads]
+    float *d;                  // [T, n_heads]
+    float *dq; long lddq;
+    float *dk; long lddk;
+    float *dv; long lddv;
+    DType dt;
+};
+hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
+                      const void *v, long ldv, float *o, long ldo, float *lse, DType dt,
+                      hipStream_t st);
+// D = rowsum(O * dO); optionally also writes dO as bf16 (dout_bf16, ld lddo16)
+hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *dout, long lddo,
+                   float *d, bf16 *dout_bf16, long lddo16, hipStream_t st);
+hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
+hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
+
+// ── cut cross-entropy (k_cce.hip) ────────────────────────────────────
+struct CceShape {
+    int N, V, D;
+    float z_loss_scale, label_smoothing;
+};
+size_t cce_work_floats(const CceShape &s);
+hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const float *w,
+                       const uint32_t *tgt, float *lse, float *loss_row, float *loss_mean,
+                       float *work, hipStream_t st);
+// dz (bf16 for Precision::BF16 else fp32) [N, V] is materialised in `dz`;
+// dh overwritten (if non-null); dW = beta*dW + dz^T h (if non-null).
+hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const float *w,
+                        const uint32_t *tgt, const float *lse, void *dz, float *dh, float *dw,
+                        float dw_beta, hipStream_t st);
+
+}  // namespace vkh

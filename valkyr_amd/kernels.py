@@ -1,0 +1,157 @@
+"""Python mirror of the reference's per-kernel dispatches.
+
+Each function takes `DeviceBuffer`s (or raw device addresses) and the fields
+of the reference push-constant struct it replaces (runtime.zig push ABI),
+and enqueues the gfx950 kernel through the C ABI.  Nothing here computes on
+the host.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import math
+
+from ._lib import AttnParams, CceParams, RopeParams, check, lib
+
+F32, BF16 = 0, 1
+PRECISION_FP32, PRECISION_BF16 = 0, 1
+
+
+def _p(x):
+    if x is None:
+        return None
+    if isinstance(x, C.c_void_p):
+        return x
+    if isinstance(x, int):
+        return C.c_void_p(x)
+    return x.ptr
+
+
+def _s(stream):
+    return stream.handle if stream is not None else None
+
+
+def attn_params(n_q, n_kv, n_heads, n_kv_heads, head_dim, causal=True, n_batch=1, dtype=F32,
+                inv_sqrt_dim=None):
+    """FaForwardPush / FaBwDqPush / FaBwDkvPush (runtime.zig:377-416) + n_batch."""
+    return AttnParams(n_batch, n_q, n_kv, n_heads, n_kv_heads, head_dim, 1 if causal else 0,
+                      inv_sqrt_dim if inv_sqrt_dim is not None else 1.0 / math.sqrt(head_dim), dtype)
+
+
+def fa_forward(p, q, k, v, o, lse=None, stream=None):
+    check(lib().vkh_fa_forward(C.byref(p), _p(q), _p(k), _p(v), _p(o), _p(lse), _s(stream)))
+
+
+def fa_bw_d(p, o, dout, d, dout_bf16=None, stream=None):
+    check(lib().vkh_fa_bw_d(C.byref(p), _p(o), _p(dout), _p(d), _p(dout_bf16), _s(stream)))
+
+
+def fa_bw_dq(p, q, k, v, dout, lse, d, dq, stream=None):
+    check(lib().vkh_fa_bw_dq(C.byref(p), _p(q), _p(k), _p(v), _p(dout), _p(lse), _p(d), _p(dq),
+                             _s(stream)))
+
+
+def fa_bw_dkv(p, q, k, v, dout, lse, d, dk, dv, stream=None):
+    check(lib().vkh_fa_bw_dkv(C.byref(p), _p(q), _p(k), _p(v), _p(dout), _p(lse), _p(d), _p(dk),
+                              _p(dv), _s(stream)))
+
+
+def matmul_nt(x, w, y, M, N, K, precision=PRECISION_FP32, stream=None):
+    """matmul_nt_v2.comp: y[M,N] = x[M,K] w[N,K]^T."""
+    check(lib().vkh_matmul_nt(_p(x), _p(w), _p(y), M, N, K, precision, _s(stream)))
+
+
+def linear_backward_dx(dy, w, dx, M, N, K, precision=PRECISION_FP32, stream=None):
+    check(lib().vkh_linear_backward_dx(_p(dy), _p(w), _p(dx), M, N, K, precision, _s(stream)))
+
+
+def linear_backward_dw(dy, x, dw, M, N, K, precision=PRECISION_FP32, stream=None):
+    check(lib().vkh_linear_backward_dw(_p(dy), _p(x), _p(dw), M, N, K, precision, _s(stream)))
+
+
+def lora_forward(x, w, a, b, y, inter, M, N, K, r, alpha_over_r, precision=PRECISION_FP32,
+                 stream=None):
+    check(lib().vkh_lora_forward(_p(x), _p(w), _p(a), _p(b), _p(y), _p(inter), M, N, K, r,
+                                 alpha_over_r, precision, _s(stream)))
+
+
+def lora_backward(dy, x, w, a, b, inter, dx, dA, dB, M, N, K, r, alpha_over_r,
+                  precision=PRECISION_FP32, stream=None):
+    check(lib().vkh_lora_backward(_p(dy), _p(x), _p(w), _p(a), _p(b), _p(inter), _p(dx), _p(dA),
+                                  _p(dB), M, N, K, r, alpha_over_r, precision, _s(stream)))
+
+
+def cce_params(n, vocab, dim, z_loss_scale=0.0, label_smoothing=0.0, precision=PRECISION_FP32):
+    return CceParams(n, vocab, dim, z_loss_scale, label_smoothing, precision)
+
+
+def cce_forward(p, h, w, targets, lse, loss_row=None, loss_mean=None, stream=None):
+    check(lib().vkh_cce_forward(C.byref(p), _p(h), _p(w), _p(targets), _p(lse), _p(loss_row),
+                                _p(loss_mean), _s(stream)))
+
+
+def cce_backward(p, h, w, targets, lse, dh=None, dw=None, accumulate_dw=False, stream=None):
+    check(lib().vkh_cce_backward(C.byref(p), _p(h), _p(w), _p(targets), _p(lse), _p(dh), _p(dw),
+                                 1 if accumulate_dw else 0, _s(stream)))
+
+
+def rmsnorm_forward(x, w, y, n_rows, dim, eps, gemma_quirk=False, stream=None):
+    check(lib().vkh_rmsnorm_forward(_p(x), _p(w), _p(y), n_rows, dim, eps, int(gemma_quirk),
+                                    _s(stream)))
+
+
+def rmsnorm_backward(dy, x, w, dx, dw=None, n_rows=0, dim=0, eps=1e-6, gemma_quirk=False,
+                     residual=None, stream=None):
+    check(lib().vkh_rmsnorm_backward(_p(dy), _p(x), _p(w), _p(dx), _p(residual), _p(dw), n_rows,
+                                     dim, eps, int(gemma_quirk), _s(stream)))
+
+
+def swiglu_forward(pre_gate, up, gated, n, stream=None):
+    check(lib().vkh_swiglu_forward(_p(pre_gate), _p(up), _p(gated), n, _s(stream)))
+
+
+def swiglu_backward(d_gated, pre_gate, up, d_pre_gate, d_up, n, stream=None):
+    check(lib().vkh_swiglu_backward(_p(d_gated), _p(pre_gate), _p(up), _p(d_pre_gate), _p(d_up), n,
+                                    _s(stream)))
+
+
+def rope_params(n_pos, n_q_heads, n_kv_heads, head_dim, rotary_dim, theta_base, seq_len=0):
+    """QkRopeBatchedPush (runtime.zig:221-228) + seq_len."""
+    return RopeParams(n_pos, n_q_heads, n_kv_heads, head_dim, rotary_dim, theta_base, seq_len)
+
+
+def qk_rope_forward(p, q_in, q_out, k_in, k_out, stream=None):
+    check(lib().vkh_qk_rope_forward(C.byref(p), _p(q_in), _p(q_out), _p(k_in), _p(k_out), _s(stream)))
+
+
+def qk_rope_backward(p, dq_out, dq_in, dk_out, dk_in, stream=None):
+    check(lib().vkh_qk_rope_backward(C.byref(p), _p(dq_out), _p(dq_in), _p(dk_out), _p(dk_in),
+                                     _s(stream)))
+
+
+def embed_lookup(embed, ids, out, n_pos, dim, scale=1.0, stream=None):
+    check(lib().vkh_embed_lookup(_p(embed), _p(ids), _p(out), n_pos, dim, scale, _s(stream)))
+
+
+def embedding_backward(dy, ids, dE, n_pos, dim, vocab, stream=None):
+    check(lib().vkh_embedding_backward(_p(dy), _p(ids), _p(dE), n_pos, dim, vocab, _s(stream)))
+
+
+def adam_step(param, grad, m, v, n, lr, beta1, beta2, eps, t, weight_decay=0.0, stream=None):
+    check(lib().vkh_adam_step(_p(param), _p(grad), _p(m), _p(v), n, lr, beta1, beta2, eps, t,
+                              weight_decay, _s(stream)))
+
+
+def add_in_place(dst, src, n, stream=None):
+    check(lib().vkh_add_in_place(_p(dst), _p(src), n, _s(stream)))
+
+
+def vec_add(a, b, c, n, stream=None):
+    check(lib().vkh_vec_add(_p(a), _p(b), _p(c), n, _s(stream)))
+
+
+def scale(x, out, n, s, stream=None):
+    check(lib().vkh_scale(_p(x), _p(out), n, s, _s(stream)))
+
+
+def cast_f32_to_bf16(x, out, n, stream=None):
+    check(lib().vkh_cast_f32_to_bf16(_p(x), _p(out), n, _s(stream)))
