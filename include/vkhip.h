@@ -279,6 +279,18 @@ vkh_status vkh_linear_backward_dx(const float *dy, const float *w, float *dx, ui
 vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, uint32_t M,
                                   uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream);
 
+/* bf16-operand forms of the three GEMMs above: every operand is bf16 (RNE
+ * bits, as uint16), accumulation and output fp32.  These are the contractions
+ * the bf16 training step runs (VKH_PRECISION_BF16 keeps all GEMM operands
+ * resident as bf16); the reference's shaders take fp32 buffers only, so they
+ * have no direct counterpart there beyond the three entry points above. */
+vkh_status vkh_matmul_nt_bf16(const void *x, const void *w, float *y, uint32_t M, uint32_t N,
+                              uint32_t K, vkh_stream stream);
+vkh_status vkh_linear_backward_dx_bf16(const void *dy, const void *w, float *dx, uint32_t M,
+                                       uint32_t N, uint32_t K, vkh_stream stream);
+vkh_status vkh_linear_backward_dw_bf16(const void *dy, const void *x, float *dw, uint32_t M,
+                                       uint32_t N, uint32_t K, vkh_stream stream);
+
 /* train/lora.zig:99-129: y = x w^T + (alpha/r) (x a^T) b^T; inter = x a^T. */
 vkh_status vkh_lora_forward(const float *x, const float *w, const float *a, const float *b,
                             float *y, float *inter, uint32_t M, uint32_t N, uint32_t K,

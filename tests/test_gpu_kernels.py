@@ -181,6 +181,39 @@ def test_gemm_bf16_rounding_within_north_star_tolerance():
     assert e < BF16_TOL
 
 
+# (M, N, K) chosen to reach every plan of the bf16-operand GEMM: 256x256 tiles
+# (>= 512 of them), 128x128, 128x128 split-K (long K, few tiles), 128x64,
+# ragged edges, and the generic fallback (K not a multiple of 8).
+GEMM16_SHAPES = [(2048, 16384, 256), (2048, 3072, 512), (1024, 1024, 8192), (2048, 1024, 1024),
+                 (1000, 520, 1000), (72, 40, 24), (130, 66, 1001)]
+
+
+@pytest.mark.parametrize("shape", GEMM16_SHAPES)
+def test_linear_gemms_bf16_operands(shape):
+    """All three contractions on bf16 operands vs the oracle on the same
+    bf16 values (products exact in fp32): layout, tiling and split-K errors
+    show up far above the 1e-5 accumulation-order noise."""
+    from valkyr_amd import kernels as K
+
+    M, N, Kd = shape
+    note(f"gemm16 M={M} N={N} K={Kd}")
+    bx, x = bf16_dev(O.normal(M * Kd, 71))
+    bW, W = bf16_dev(O.normal(N * Kd, 72, 0.05))
+    bdy, dy = bf16_dev(O.normal(M * N, 73))
+    x64, W64, dy64 = (a.astype(np.float64) for a in (x, W, dy))
+    y_ref = (x64.reshape(M, Kd) @ W64.reshape(N, Kd).T).ravel()
+    dx_ref = (dy64.reshape(M, N) @ W64.reshape(N, Kd)).ravel()
+    dW_ref = (dy64.reshape(M, N).T @ x64.reshape(M, Kd)).ravel()
+    by, bdx, bdW = zeros(M * N), zeros(M * Kd), zeros(N * Kd)
+    K.matmul_nt_bf16(bx, bW, by, M, N, Kd)
+    K.linear_backward_dx_bf16(bdy, bW, bdx, M, N, Kd)
+    K.linear_backward_dw_bf16(bdy, bx, bdW, M, N, Kd)
+    for name, ref, got in (("y", y_ref, by), ("dx", dx_ref, bdx), ("dW", dW_ref, bdW)):
+        e = rel_l2(ref, host(got))
+        note(f"  {name} rel-L2 {e:.2e}")
+        assert e < 1e-5, name
+
+
 @pytest.mark.parametrize("prec", [0, 1])
 def test_lora_forward_backward(prec):
     from valkyr_amd import kernels as K

@@ -145,6 +145,9 @@ SIGNATURES = [
     ("vkh_matmul_nt", ST, [P, P, P, U32, U32, U32, U32, P]),
     ("vkh_linear_backward_dx", ST, [P, P, P, U32, U32, U32, U32, P]),
     ("vkh_linear_backward_dw", ST, [P, P, P, U32, U32, U32, U32, P]),
+    ("vkh_matmul_nt_bf16", ST, [P, P, P, U32, U32, U32, P]),
+    ("vkh_linear_backward_dx_bf16", ST, [P, P, P, U32, U32, U32, P]),
+    ("vkh_linear_backward_dw_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_lora_forward", ST, [P, P, P, P, P, P, U32, U32, U32, U32, F, U32, P]),
     ("vkh_lora_backward", ST, [P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, F, U32, P]),
     ("vkh_cce_forward", ST, [C.POINTER(CceParams), P, P, P, P, P, P, P]),

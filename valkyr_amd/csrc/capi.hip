@@ -145,7 +145,7 @@ vkh_status vkh_fa_forward(const vkh_attn_params *p, const void *q, const void *k
     const AttnShape s = attn_shape(p);
     const long ldq = (long)p->n_heads * p->head_dim, ldk = (long)p->n_kv_heads * p->head_dim;
     VKH_HIP(fa_forward(s, q, ldq, k, ldk, v, ldk, o, ldq, lse,
-                       p->dtype == VKH_BF16 ? DType::BF16 : DType::F32, S(stream)));
+                       p->dtype == VKH_BF16 ? DType::BF16 : DType::F32, nullptr, 0, S(stream)));
     return VKH_OK;
 }
 
@@ -215,6 +215,47 @@ vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, ui
     CHECK_ARG(dy && x && dw, "null pointer");
     VKH_HIP(gemm_tn(PR(precision), matf(dy, N), matf(x, K), dw, K, M, N, K, 1.f, 0.f, S(stream)));
     return VKH_OK;
+}
+
+// Split-K workspace for one call (stream-ordered allocation), if the plan wants one.
+extern "C++" {
+template <class F>
+static vkh_status with_g16_ws(int M, int N, int K, hipStream_t st, const char *what, F &&f) {
+    GemmWs ws{nullptr, g16_ws_bytes_for(M, N, K)};
+    if (ws.bytes) VKH_HIP(hipMallocAsync(&ws.p, ws.bytes, st));
+    const hipError_t e = f(ws);
+    if (ws.p) (void)hipFreeAsync(ws.p, st);
+    if (e != hipSuccess) return hip_fail(e, what);
+    return VKH_OK;
+}
+}
+
+vkh_status vkh_matmul_nt_bf16(const void *x, const void *w, float *y, uint32_t M, uint32_t N,
+                              uint32_t K, vkh_stream stream) {
+    CHECK_ARG(x && w && y, "null pointer");
+    hipStream_t st = S(stream);
+    return with_g16_ws(M, N, K, st, "matmul_nt_bf16", [&](const GemmWs &ws) {
+        return g16_nt((const bf16 *)x, K, (const bf16 *)w, K, y, N, M, N, K, nullptr, 0, 1.f, 0.f,
+                      ws, st);
+    });
+}
+
+vkh_status vkh_linear_backward_dx_bf16(const void *dy, const void *w, float *dx, uint32_t M,
+                                       uint32_t N, uint32_t K, vkh_stream stream) {
+    CHECK_ARG(dy && w && dx, "null pointer");
+    hipStream_t st = S(stream);
+    return with_g16_ws(M, K, N, st, "linear_backward_dx_bf16", [&](const GemmWs &ws) {
+        return g16_nn((const bf16 *)dy, N, (const bf16 *)w, K, dx, K, M, N, K, 1.f, 0.f, ws, st);
+    });
+}
+
+vkh_status vkh_linear_backward_dw_bf16(const void *dy, const void *x, float *dw, uint32_t M,
+                                       uint32_t N, uint32_t K, vkh_stream stream) {
+    CHECK_ARG(dy && x && dw, "null pointer");
+    hipStream_t st = S(stream);
+    return with_g16_ws(N, K, M, st, "linear_backward_dw_bf16", [&](const GemmWs &ws) {
+        return g16_tn((const bf16 *)dy, N, (const bf16 *)x, K, dw, K, M, N, K, 1.f, 0.f, ws, st);
+    });
 }
 
 vkh_status vkh_lora_forward(const float *x, const float *w, const float *a, const float *b,
@@ -289,7 +330,7 @@ vkh_status vkh_cce_backward(const vkh_cce_params *p, const float *h, const float
 vkh_status vkh_rmsnorm_forward(const float *x, const float *w, float *y, uint32_t n_rows,
                                uint32_t dim, float eps, uint32_t gq, vkh_stream stream) {
     CHECK_ARG(x && w && y, "null pointer");
-    VKH_HIP(rmsnorm_forward(x, w, y, n_rows, dim, eps, gq ? 1 : 0, S(stream)));
+    VKH_HIP(rmsnorm_forward(x, w, y, DType::F32, n_rows, dim, eps, gq ? 1 : 0, S(stream)));
     return VKH_OK;
 }
 
@@ -301,7 +342,8 @@ vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w,
     hipStream_t st = S(stream);
     float *partial = nullptr;
     VKH_HIP(hipMallocAsync((void **)&partial, rmsnorm_partial_floats(n_rows, dim) * 4 + 16, st));
-    hipError_t e = rmsnorm_backward(dy, x, w, dx, residual, dw, partial, n_rows, dim, eps, gq ? 1 : 0, st);
+    hipError_t e = rmsnorm_backward(dy, x, w, dx, nullptr, residual, dw, partial, n_rows, dim, eps,
+                                    gq ? 1 : 0, st);
     (void)hipFreeAsync(partial, st);
     if (e != hipSuccess) return hip_fail(e, "rmsnorm_backward");
     return VKH_OK;
@@ -311,7 +353,7 @@ vkh_status vkh_swiglu_forward(const float *pg, const float *up, float *g, size_t
                               vkh_stream stream) {
     CHECK_ARG(pg && up && g, "null pointer");
     CHECK_ARG(n < (1ull << 31), "n too large");
-    VKH_HIP(swiglu_forward(pg, (long)n, up, (long)n, g, (long)n, 1, (int)n, S(stream)));
+    VKH_HIP(swiglu_forward(pg, (long)n, up, (long)n, g, (long)n, DType::F32, 1, (int)n, S(stream)));
     return VKH_OK;
 }
 
@@ -319,8 +361,8 @@ vkh_status vkh_swiglu_backward(const float *dg, const float *pg, const float *up
                                float *dup, size_t n, vkh_stream stream) {
     CHECK_ARG(dg && pg && up && dpg && dup, "null pointer");
     CHECK_ARG(n < (1ull << 31), "n too large");
-    VKH_HIP(swiglu_backward(dg, (long)n, pg, (long)n, up, (long)n, dpg, (long)n, dup, (long)n, 1,
-                            (int)n, S(stream)));
+    VKH_HIP(swiglu_backward(dg, (long)n, pg, (long)n, up, (long)n, dpg, (long)n, dup, (long)n,
+                            DType::F32, 1, (int)n, S(stream)));
     return VKH_OK;
 }
 
@@ -375,7 +417,7 @@ vkh_status vkh_adam_step(float *param, const float *grad, float *m, float *v, si
     CHECK_ARG(t >= 1, "t must be >= 1");
     const float tf = (float)t;
     VKH_HIP(adam_step(param, grad, m, v, n, lr, beta1, beta2, eps, 1.0f - powf(beta1, tf),
-                      1.0f - powf(beta2, tf), wd, S(stream)));
+                      1.0f - powf(beta2, tf), wd, nullptr, S(stream)));
     return VKH_OK;
 }
 

@@ -98,7 +98,7 @@ template <int HD>
 __global__ __launch_bounds__(NT, 2) void fa_fwd_bf16_k(AttnShape s, const bf16 *q, long ldq,
                                                         const bf16 *k, long ldk, const bf16 *v,
                                                         long ldv, float *o, long ldo,
-                                                        float *lse) {
+                                                        float *lse, bf16 *ob, long ldob) {
     constexpr int BM = 128, BN = 64, DS = HD / 32, DSUB = HD / 16;
     __shared__ __attribute__((aligned(16))) bf16 Ks[BN][HD + 8];
     __shared__ __attribute__((aligned(16))) bf16 Vt[HD][BN + 8];
@@ -208,8 +208,13 @@ __global__ __launch_bounds__(NT, 2) void fa_fwd_bf16_k(AttnShape s, const bf16 *
 #pragma unroll
         for (int i = 0; i < DSUB; ++i) {
             const f32x4 a = oacc[i][qs];
-            *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) =
-                make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+            const float4 ov = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+            *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) = ov;
+            if (ob) {
+                bf16x4 bv;
+                bv[0] = (bf16)ov.x; bv[1] = (bf16)ov.y; bv[2] = (bf16)ov.z; bv[3] = (bf16)ov.w;
+                *reinterpret_cast<bf16x4 *>(ob + ((long)b * s.n_q + qa) * ldob + h * HD + 16 * i + 4 * g) = bv;
+            }
         }
         if (lse && g == 0)
             lse[((long)b * s.n_q + qa) * s.n_heads + h] =
@@ -620,20 +625,21 @@ inline unsigned rows_grid(long rows) { return (unsigned)((rows + (NT / 64) - 1) 
 
 hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
                       const void *v, long ldv, float *o, long ldo, float *lse, DType dt,
-                      hipStream_t st) {
+                      bf16 *ob, long ldob, hipStream_t st) {
     if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
     if (s.n_kv_heads <= 0 || s.n_heads % s.n_kv_heads) return hipErrorInvalidValue;
     if (dt == DType::BF16) {
         if (!bf16_ok(s)) return hipErrorInvalidValue;
+        if (ob && (ldob % 4 || ((uintptr_t)ob & 7u))) return hipErrorInvalidValue;
         dim3 grid((s.n_q + 127) / 128, s.n_heads, s.n_batch);
         if (s.head_dim == 128)
             hipLaunchKernelGGL(fa_fwd_bf16_k<128>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
-                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse);
+                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
         else
             hipLaunchKernelGGL(fa_fwd_bf16_k<64>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
-                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse);
+                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
     } else {
-        if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
+        if (s.head_dim > 64 * MAXE || ob) return hipErrorInvalidValue;
         hipLaunchKernelGGL(fa_fwd_f32_k, dim3(rows_grid((long)s.n_batch * s.n_q * s.n_heads)),
                            dim3(NT), 0, st, s, (const float *)q, ldq, (const float *)k, ldk,
                            (const float *)v, ldv, o, ldo, lse);

@@ -15,7 +15,7 @@
 // cce_backward_dh.comp:109-123, cce_backward_dw.comp:73-103); on a 288 GB
 // part the [N, V] dz buffer (0.6 GB at N = 2048) is cheap and turns the
 // backward into three dense GEMMs.
-#include "gemm.hpp"
+#include "gemm16.hpp"
 #include "ops.hpp"
 
 namespace vkh {
@@ -173,6 +173,27 @@ hipError_t logits_gemm(Precision pr, const CceShape &s, const float *h, const fl
     return launch_gemm<TileCfg<128, 128, 32>, false, float, Lay::K, float, Lay::K>(a, b, sh, epi, st);
 }
 
+// bf16 operands: the gemm16 kernel with 64-column wave slices (8 waves in a
+// 2 x 4 grid), falling back to the generic MFMA GEMM for unaligned shapes.
+template <class Epi>
+hipError_t logits16(const CceShape &s, const bf16 *h, const bf16 *w, const Epi &epi,
+                    hipStream_t st) {
+    GemmShape sh{s.N, s.V, s.D};
+    const size_t hb = ((size_t)(s.N - 1) * s.D + s.D) * 2, wb = ((size_t)(s.V - 1) * s.D + s.D) * 2;
+    const bool ok = s.D % 8 == 0 && ((uintptr_t)h & 15u) == 0 && ((uintptr_t)w & 15u) == 0 &&
+                    hb < (1ull << 31) && wb < (1ull << 31);
+    if (!ok) {
+        GemmOperand a{h, s.D, vec_ok(h, s.D, 2, Lay::K)};
+        GemmOperand b{w, s.D, vec_ok(w, s.D, 2, Lay::K)};
+        return launch_gemm<TileCfg<128, 128, 64>, true, bf16, Lay::K, bf16, Lay::K>(a, b, sh, epi, st);
+    }
+    const Op16 a{h, s.D, (unsigned)hb}, b{w, s.D, (unsigned)wb};
+    const SplitK one{1, nullptr};
+    if ((long)ceil_div(s.N, 256) * ceil_div(s.V, 256) >= 256)
+        return launch_gemm16<Tile16<256, 256, 2, 4>, Lay::K, Lay::K>(a, b, sh, epi, one, st);
+    return launch_gemm16<Tile16<128, 256, 2, 4>, Lay::K, Lay::K>(a, b, sh, epi, one, st);
+}
+
 }  // namespace
 
 size_t cce_work_floats(const CceShape &s) {
@@ -217,6 +238,40 @@ hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const f
         if (err != hipSuccess) return err;
     }
     if (dh) err = gemm_nn(pr, mz, matf(w, s.D), dh, s.D, s.N, s.V, s.D, 1.f, 0.f, st);
+    return err;
+}
+
+}  // namespace vkh
+
+namespace vkh {
+
+hipError_t cce_forward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
+                         float *lse, float *loss_row, float *loss_mean, float *work,
+                         hipStream_t st) {
+    if (s.N <= 0) return hipSuccess;
+    CceWork cw = carve(work, s);
+    EpiCceStats e{cw, tgt, s.V};
+    hipError_t err = logits16(s, h, w, e, st);
+    if (err != hipSuccess) return err;
+    hipLaunchKernelGGL(cce_merge_k, dim3(ceil_div(s.N, 4)), dim3(256), 0, st, s, cw, lse, loss_row);
+    if (loss_mean) hipLaunchKernelGGL(cce_mean_k, dim3(1), dim3(256), 0, st, s, cw, loss_mean);
+    return hipGetLastError();
+}
+
+hipError_t cce_backward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
+                          const float *lse, bf16 *dz, float *dh, float *dw, float dw_beta,
+                          const GemmWs &ws, hipStream_t st) {
+    if (s.N <= 0) return hipSuccess;
+    EpiCceDz<bf16> e{dz, tgt, lse, s.V, 1.0f / (float)s.N, 1.0f - s.label_smoothing,
+                     s.label_smoothing / (float)s.V, 2.0f * s.z_loss_scale};
+    hipError_t err = logits16(s, h, w, e, st);
+    if (err != hipSuccess) return err;
+    // dW[V, D] = dz^T h ;  dh[N, D] = dz W
+    if (dw) {
+        err = g16_tn(dz, s.V, h, s.D, dw, s.D, s.N, s.V, s.D, 1.f, dw_beta, ws, st);
+        if (err != hipSuccess) return err;
+    }
+    if (dh) err = g16_nn(dz, s.V, w, s.D, dh, s.D, s.N, s.V, s.D, 1.f, 0.f, ws, st);
     return err;
 }
 

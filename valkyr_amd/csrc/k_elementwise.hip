@@ -12,6 +12,15 @@ namespace {
 
 constexpr int NT = 256;
 
+VKH_DEV void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+VKH_DEV void st4(bf16 *p, float4 v) {
+    bf16x4 b;
+    b[0] = (bf16)v.x; b[1] = (bf16)v.y; b[2] = (bf16)v.z; b[3] = (bf16)v.w;
+    *reinterpret_cast<bf16x4 *>(p) = b;
+}
+VKH_DEV void st1(float *p, float v) { *p = v; }
+VKH_DEV void st1(bf16 *p, float v) { *p = (bf16)v; }
+
 inline unsigned grid_for(size_t n_vec) {
     size_t g = (n_vec + NT - 1) / NT;
     const size_t cap = 256 * 16;  // 16 blocks per CU is plenty for a streaming kernel
@@ -69,12 +78,14 @@ __global__ void cast_bf16_k(const float *in, bf16 *out, size_t n, bool vec) {
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
 
 // swiglu_forward.comp / train_transformer.zig:839-851
-__global__ void swiglu_fwd_k(const float *pg, long ldpg, const float *up, long ldup, float *g,
+template <typename TO>
+__global__ void swiglu_fwd_k(const float *pg, long ldpg, const float *up, long ldup, TO *g,
                              long ldg, int rows, int cols4) {
     const size_t n = (size_t)rows * cols4;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int r = (int)(i / cols4), c = (int)(i % cols4) * 4;
+        const long r = (long)(i / cols4);
+        const int c = (int)(i % cols4) * 4;
         float4 z = *reinterpret_cast<const float4 *>(pg + r * ldpg + c);
         float4 u = *reinterpret_cast<const float4 *>(up + r * ldup + c);
         float4 o;
@@ -82,7 +93,7 @@ __global__ void swiglu_fwd_k(const float *pg, long ldpg, const float *up, long l
         o.y = z.y * sigmoidf_(z.y) * u.y;
         o.z = z.z * sigmoidf_(z.z) * u.z;
         o.w = z.w * sigmoidf_(z.w) * u.w;
-        *reinterpret_cast<float4 *>(g + r * ldg + c) = o;
+        st4(g + r * ldg + c, o);
     }
 }
 
@@ -95,13 +106,15 @@ __device__ __forceinline__ void swiglu_bw1(float dg, float z, float u, float &dz
 }
 
 // swiglu_backward.comp / train_transformer.zig:857-875
+template <typename TO>
 __global__ void swiglu_bwd_k(const float *dg, long lddg, const float *pg, long ldpg,
-                             const float *up, long ldup, float *dpg, long lddpg, float *dup,
+                             const float *up, long ldup, TO *dpg, long lddpg, TO *dup,
                              long lddup, int rows, int cols4) {
     const size_t n = (size_t)rows * cols4;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int r = (int)(i / cols4), c = (int)(i % cols4) * 4;
+        const long r = (long)(i / cols4);
+        const int c = (int)(i % cols4) * 4;
         float4 d = *reinterpret_cast<const float4 *>(dg + r * lddg + c);
         float4 z = *reinterpret_cast<const float4 *>(pg + r * ldpg + c);
         float4 u = *reinterpret_cast<const float4 *>(up + r * ldup + c);
@@ -110,34 +123,38 @@ __global__ void swiglu_bwd_k(const float *dg, long lddg, const float *pg, long l
         swiglu_bw1(d.y, z.y, u.y, oz.y, ou.y);
         swiglu_bw1(d.z, z.z, u.z, oz.z, ou.z);
         swiglu_bw1(d.w, z.w, u.w, oz.w, ou.w);
-        *reinterpret_cast<float4 *>(dpg + r * lddpg + c) = oz;
-        *reinterpret_cast<float4 *>(dup + r * lddup + c) = ou;
+        st4(dpg + r * lddpg + c, oz);
+        st4(dup + r * lddup + c, ou);
     }
 }
 
 // scalar fallbacks for shapes whose columns are not a multiple of 4
-__global__ void swiglu_fwd_s(const float *pg, long ldpg, const float *up, long ldup, float *g,
+template <typename TO>
+__global__ void swiglu_fwd_s(const float *pg, long ldpg, const float *up, long ldup, TO *g,
                              long ldg, int rows, int cols) {
     const size_t n = (size_t)rows * cols;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int r = (int)(i / cols), c = (int)(i % cols);
+        const long r = (long)(i / cols);
+        const int c = (int)(i % cols);
         const float z = pg[r * ldpg + c];
-        g[r * ldg + c] = z * sigmoidf_(z) * up[r * ldup + c];
+        st1(g + r * ldg + c, z * sigmoidf_(z) * up[r * ldup + c]);
     }
 }
 
+template <typename TO>
 __global__ void swiglu_bwd_s(const float *dg, long lddg, const float *pg, long ldpg,
-                             const float *up, long ldup, float *dpg, long lddpg, float *dup,
+                             const float *up, long ldup, TO *dpg, long lddpg, TO *dup,
                              long lddup, int rows, int cols) {
     const size_t n = (size_t)rows * cols;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        const int r = (int)(i / cols), c = (int)(i % cols);
+        const long r = (long)(i / cols);
+        const int c = (int)(i % cols);
         float dz, du;
         swiglu_bw1(dg[r * lddg + c], pg[r * ldpg + c], up[r * ldup + c], dz, du);
-        dpg[r * lddpg + c] = dz;
-        dup[r * lddup + c] = du;
+        st1(dpg + r * lddpg + c, dz);
+        st1(dup + r * lddup + c, du);
     }
 }
 
@@ -175,8 +192,9 @@ __device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, flo
     p = q - lr * m_hat / (sqrtf(v_hat) + eps);
 }
 
-__global__ void adam_k(float *p, const float *g, float *m, float *v, size_t n, float lr, float b1,
-                       float b2, float eps, float bc1, float bc2, float wd, bool vec) {
+// pb (optional): bf16 copy of the updated parameters (the GEMM operand shadow)
+__global__ void adam_k(float *p, const float *g, float *m, float *v, bf16 *pb, size_t n, float lr,
+                       float b1, float b2, float eps, float bc1, float bc2, float wd, bool vec) {
     const size_t n4 = vec ? n / 4 : 0;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
@@ -191,9 +209,12 @@ __global__ void adam_k(float *p, const float *g, float *m, float *v, size_t n, f
         reinterpret_cast<float4 *>(p)[i] = pp;
         reinterpret_cast<float4 *>(m)[i] = mm;
         reinterpret_cast<float4 *>(v)[i] = vv;
+        if (pb) st4(pb + 4 * i, pp);
     }
-    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride)
+    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
         adam1(p[i], g[i], m[i], v[i], lr, b1, b2, eps, bc1, bc2, wd);
+        if (pb) pb[i] = (bf16)p[i];
+    }
 }
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
@@ -234,33 +255,54 @@ hipError_t cast_f32_to_bf16(const float *in, bf16 *out, size_t n, hipStream_t st
     return hipGetLastError();
 }
 
-hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup, float *g,
-                          long ldg, int rows, int cols, hipStream_t st) {
+hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup, void *g,
+                          long ldg, DType gdt, int rows, int cols, hipStream_t st) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
     const bool v4 = (cols % 4 == 0) && (ldpg % 4 == 0) && (ldup % 4 == 0) && (ldg % 4 == 0) &&
-                    al16(pg) && al16(up) && al16(g);
-    if (v4)
-        hipLaunchKernelGGL(swiglu_fwd_k, dim3(grid_for((size_t)rows * cols / 4)), dim3(NT), 0, st,
-                           pg, ldpg, up, ldup, g, ldg, rows, cols / 4);
-    else
-        hipLaunchKernelGGL(swiglu_fwd_s, dim3(grid_for((size_t)rows * cols)), dim3(NT), 0, st, pg,
-                           ldpg, up, ldup, g, ldg, rows, cols);
+                    al16(pg) && al16(up) && ((uintptr_t)g & (gdt == DType::F32 ? 15u : 7u)) == 0;
+    const unsigned gv = grid_for((size_t)rows * cols / 4), gs = grid_for((size_t)rows * cols);
+    if (gdt == DType::F32) {
+        if (v4)
+            hipLaunchKernelGGL(swiglu_fwd_k<float>, dim3(gv), dim3(NT), 0, st, pg, ldpg, up, ldup,
+                               (float *)g, ldg, rows, cols / 4);
+        else
+            hipLaunchKernelGGL(swiglu_fwd_s<float>, dim3(gs), dim3(NT), 0, st, pg, ldpg, up, ldup,
+                               (float *)g, ldg, rows, cols);
+    } else {
+        if (v4)
+            hipLaunchKernelGGL(swiglu_fwd_k<bf16>, dim3(gv), dim3(NT), 0, st, pg, ldpg, up, ldup,
+                               (bf16 *)g, ldg, rows, cols / 4);
+        else
+            hipLaunchKernelGGL(swiglu_fwd_s<bf16>, dim3(gs), dim3(NT), 0, st, pg, ldpg, up, ldup,
+                               (bf16 *)g, ldg, rows, cols);
+    }
     return hipGetLastError();
 }
 
 hipError_t swiglu_backward(const float *dg, long lddg, const float *pg, long ldpg,
-                           const float *up, long ldup, float *dpg, long lddpg, float *dup,
-                           long lddup, int rows, int cols, hipStream_t st) {
+                           const float *up, long ldup, void *dpg, long lddpg, void *dup,
+                           long lddup, DType odt, int rows, int cols, hipStream_t st) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
+    const uintptr_t om = odt == DType::F32 ? 15u : 7u;
     const bool v4 = (cols % 4 == 0) && (lddg % 4 == 0) && (ldpg % 4 == 0) && (ldup % 4 == 0) &&
                     (lddpg % 4 == 0) && (lddup % 4 == 0) && al16(dg) && al16(pg) && al16(up) &&
-                    al16(dpg) && al16(dup);
-    if (v4)
-        hipLaunchKernelGGL(swiglu_bwd_k, dim3(grid_for((size_t)rows * cols / 4)), dim3(NT), 0, st,
-                           dg, lddg, pg, ldpg, up, ldup, dpg, lddpg, dup, lddup, rows, cols / 4);
-    else
-        hipLaunchKernelGGL(swiglu_bwd_s, dim3(grid_for((size_t)rows * cols)), dim3(NT), 0, st, dg,
-                           lddg, pg, ldpg, up, ldup, dpg, lddpg, dup, lddup, rows, cols);
+                    ((uintptr_t)dpg & om) == 0 && ((uintptr_t)dup & om) == 0;
+    const unsigned gv = grid_for((size_t)rows * cols / 4), gs = grid_for((size_t)rows * cols);
+    if (odt == DType::F32) {
+        if (v4)
+            hipLaunchKernelGGL(swiglu_bwd_k<float>, dim3(gv), dim3(NT), 0, st, dg, lddg, pg, ldpg,
+                               up, ldup, (float *)dpg, lddpg, (float *)dup, lddup, rows, cols / 4);
+        else
+            hipLaunchKernelGGL(swiglu_bwd_s<float>, dim3(gs), dim3(NT), 0, st, dg, lddg, pg, ldpg,
+                               up, ldup, (float *)dpg, lddpg, (float *)dup, lddup, rows, cols);
+    } else {
+        if (v4)
+            hipLaunchKernelGGL(swiglu_bwd_k<bf16>, dim3(gv), dim3(NT), 0, st, dg, lddg, pg, ldpg,
+                               up, ldup, (bf16 *)dpg, lddpg, (bf16 *)dup, lddup, rows, cols / 4);
+        else
+            hipLaunchKernelGGL(swiglu_bwd_s<bf16>, dim3(gs), dim3(NT), 0, st, dg, lddg, pg, ldpg,
+                               up, ldup, (bf16 *)dpg, lddpg, (bf16 *)dup, lddup, rows, cols);
+    }
     return hipGetLastError();
 }
 
@@ -275,10 +317,11 @@ hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int
 
 hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,
                      float beta1, float beta2, float eps, float bc1, float bc2, float wd,
-                     hipStream_t st) {
+                     bf16 *pb, hipStream_t st) {
     if (!n) return hipSuccess;
-    hipLaunchKernelGGL(adam_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, p, g, m, v, n, lr,
-                       beta1, beta2, eps, bc1, bc2, wd, al16(p) && al16(g) && al16(m) && al16(v));
+    const bool vec = al16(p) && al16(g) && al16(m) && al16(v) && ((uintptr_t)pb & 7u) == 0;
+    hipLaunchKernelGGL(adam_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, p, g, m, v, pb, n, lr,
+                       beta1, beta2, eps, bc1, bc2, wd, vec);
     return hipGetLastError();
 }
 

@@ -1,0 +1,110 @@
+// Linear-layer GEMMs on bf16 operands (the bf16 precision of the training
+// step): forward y = x W^T (matmul_nt_v2.comp), dx = dy W
+// (linear_backward_dx_batched.comp) and dW = dy^T x
+// (linear_backward_dw_batched.comp), on the gemm16 kernel.
+//
+// Tile plan (measured on MI355X for the T = 2048-token step shapes):
+//   * >= 512 tiles of 256 x 256       -> 256 x 256, 8 waves (vocab-sized GEMMs)
+//   * >= 384 tiles of 128 x 128       -> 128 x 128, 4 waves
+//   * long K (>= 4096), < 256 tiles   -> 128 x 128 split-K (up to 4 ways)
+//   * otherwise                       -> 128 x 64 (twice the tiles of 128 x 128)
+// Operands that break the kernel's layout rules (16-byte alignment, ld and
+// the contiguous extent multiples of 8, < 2 GiB) take the generic MFMA GEMM.
+#include <algorithm>
+
+#include "gemm16.hpp"
+#include "ops.hpp"
+
+namespace vkh {
+
+namespace {
+
+using TBig = Tile16<256, 256, 2, 4>;
+using T128 = Tile16<128, 128, 2, 2>;
+using T128x64 = Tile16<128, 64, 2, 2>;
+
+enum class Pick { Big, T128, T128x64 };
+struct Plan {
+    Pick tile;
+    int splits;
+};
+
+Plan plan(const GemmShape &s, size_t ws_bytes) {
+    auto tiles = [&](int bm, int bn) { return (long)ceil_div(s.M, bm) * (long)ceil_div(s.N, bn); };
+    if (tiles(256, 256) >= 512) return {Pick::Big, 1};
+    const long t128 = tiles(128, 128);
+    if (t128 >= 384) return {Pick::T128, 1};
+    const int nk = (s.K + 63) / 64;
+    if (s.K >= 4096 && t128 < 256) {
+        int sp = (int)std::min<long>(4, std::max<long>(1, 512 / t128));
+        while (sp > 1 && (nk / sp < 8 || gemm16_ws_bytes<T128>(s, sp) > ws_bytes)) --sp;
+        if (sp > 1) return {Pick::T128, sp};
+    }
+    return {Pick::T128x64, 1};
+}
+
+template <Lay LA, Lay LB, class Epi>
+hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e, const GemmWs &ws,
+                 hipStream_t st) {
+    const Plan p = plan(s, ws.p ? ws.bytes : 0);
+    const SplitK sk{p.splits, (f32x4 *)ws.p};
+    switch (p.tile) {
+    case Pick::Big: return launch_gemm16<TBig, LA, LB>(a, b, s, e, sk, st);
+    case Pick::T128: return launch_gemm16<T128, LA, LB>(a, b, s, e, sk, st);
+    default: return launch_gemm16<T128x64, LA, LB>(a, b, s, e, sk, st);
+    }
+}
+
+// Operand of `rows` storage rows whose contiguous run is `run` elements.
+bool make_op(const bf16 *p, long ld, long rows, long run, Op16 &o) {
+    if (((uintptr_t)p & 15u) || ld % 8 || run % 8 || rows <= 0) return false;
+    const size_t bytes = ((size_t)(rows - 1) * ld + run) * 2;
+    if (bytes >= (1ull << 31)) return false;
+    o = Op16{p, ld, (unsigned)bytes};
+    return true;
+}
+
+Mat matb(const bf16 *p, long ld) { return Mat{p, ld, DType::BF16}; }
+
+}  // namespace
+
+hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
+                  int N, int K, const float *R, long ldr, float alpha, float beta,
+                  const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op(x, ldx, M, K, a) || !make_op(w, ldw, N, K, b))
+        return gemm_nt(Precision::BF16, matb(x, ldx), matb(w, ldw), y, ldy, M, N, K, R, ldr, alpha,
+                       beta, st);
+    EpiStore e{y, ldy, R, ldr, alpha, beta};
+    return run16<Lay::K, Lay::K>(a, b, GemmShape{M, N, K}, e, ws, st);
+}
+
+hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
+    // C[m, k'] = sum_n dy[m, n] W[n, k']: A = dy (K-major over n), B(k', n) = W[n][k'] (MN)
+    Op16 a, b;
+    if (!make_op(dy, lddy, M, N, a) || !make_op(w, ldw, N, K, b))
+        return gemm_nn(Precision::BF16, matb(dy, lddy), matb(w, ldw), dx, lddx, M, N, K, alpha,
+                       beta, st);
+    EpiStore e{dx, lddx, nullptr, 0, alpha, beta};
+    return run16<Lay::K, Lay::MN>(a, b, GemmShape{M, K, N}, e, ws, st);
+}
+
+hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw, long lddw, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
+    // C[n, k'] = sum_m dy[m, n] x[m, k']: both operands MN-major over m
+    Op16 a, b;
+    if (!make_op(dy, lddy, M, N, a) || !make_op(x, ldx, M, K, b))
+        return gemm_tn(Precision::BF16, matb(dy, lddy), matb(x, ldx), dw, lddw, M, N, K, alpha,
+                       beta, st);
+    EpiStore e{dw, lddw, nullptr, 0, alpha, beta};
+    return run16<Lay::MN, Lay::MN>(a, b, GemmShape{N, K, M}, e, ws, st);
+}
+
+size_t g16_ws_bytes_for(int M, int N, int K) {
+    const GemmShape s{M, N, K};
+    const Plan p = plan(s, ~size_t(0));
+    return p.splits > 1 ? gemm16_ws_bytes<T128>(s, p.splits) : 0;
+}
+
+}  // namespace vkh

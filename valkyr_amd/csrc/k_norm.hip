@@ -32,12 +32,13 @@ VKH_DEV double block_sum_d(double v, double *sh) {
     return t;
 }
 
-__global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float *w, float *y,
+template <typename TO>
+__global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float *w, TO *y,
                                                      int dim, float eps, int gq) {
     __shared__ double sh[NT / 64];
     const long row = blockIdx.x;
     const float *xr = x + row * dim;
-    float *yr = y + row * dim;
+    TO *yr = y + row * dim;
     double ss = 0;
     for (int c = threadIdx.x; c < dim; c += NT) ss += (double)xr[c] * (double)xr[c];
     ss = block_sum_d(ss, sh);
@@ -45,13 +46,14 @@ __global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float 
     const float ri = 1.0f / sqrtf((float)m + eps);
     for (int c = threadIdx.x; c < dim; c += NT) {
         const float gain = gq ? w[c] + 1.0f : w[c];
-        yr[c] = gain * ri * xr[c];
+        yr[c] = (TO)(gain * ri * xr[c]);
     }
 }
 
 // Rows [blockIdx.x * rpb, ...) of one norm; per-thread gain-gradient partials.
+// dxb (optional): bf16 copy of dx, the operand of the next GEMMs.
 __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float *x,
-                                                     const float *w, float *dx,
+                                                     const float *w, float *dx, bf16 *dxb,
                                                      const float *res, float *partial,
                                                      int rows, int dim, float eps, int gq,
                                                      int rpb) {
@@ -91,6 +93,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
                 float o = ri * gain * dv - ri3_over_D * xv * A_f;
                 if (res) o = o + res[(long)row * dim + c];
                 dx[(long)row * dim + c] = o;
+                if (dxb) dxb[(long)row * dim + c] = (bf16)o;
                 dwacc[k] += dv * ri * xv;
             }
         }
@@ -102,13 +105,35 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
     }
 }
 
-// out[c] = sum_b partial[b * stride + c], b ascending.
-__global__ void colsum_k(const float *partial, int nparts, long stride, int dim, float *out) {
-    const int c = blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= dim) return;
-    float s = 0.f;
-    for (int b = 0; b < nparts; ++b) s += partial[(long)b * stride + c];
-    out[c] = s;
+// out[c] = sum_b partial[b * stride + c].  A block owns 16 columns; its 16
+// row groups each sum a strided subset of the partial rows with four
+// independent accumulators, then the groups are combined in LDS in a fixed
+// order, so the result does not depend on scheduling.
+constexpr int CS_COLS = 16, CS_GROUPS = 16;
+__global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *partial, int nparts,
+                                                              long stride, int dim, float *out) {
+    __shared__ float sh[CS_GROUPS][CS_COLS + 1];
+    const int cl = threadIdx.x % CS_COLS, g = threadIdx.x / CS_COLS;
+    const int c = blockIdx.x * CS_COLS + cl;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (c < dim) {
+        int b = g;
+        for (; b + 3 * CS_GROUPS < nparts; b += 4 * CS_GROUPS) {
+            a0 += partial[(long)b * stride + c];
+            a1 += partial[(long)(b + CS_GROUPS) * stride + c];
+            a2 += partial[(long)(b + 2 * CS_GROUPS) * stride + c];
+            a3 += partial[(long)(b + 3 * CS_GROUPS) * stride + c];
+        }
+        for (; b < nparts; b += CS_GROUPS) a0 += partial[(long)b * stride + c];
+    }
+    sh[g][cl] = (a0 + a1) + (a2 + a3);
+    __syncthreads();
+    if (g == 0 && c < dim) {
+        float s = 0.f;
+#pragma unroll
+        for (int i = 0; i < CS_GROUPS; ++i) s += sh[i][cl];
+        out[c] = s;
+    }
 }
 
 inline int rms_blocks(int rows) { return rows < 512 ? rows : 512; }
@@ -230,10 +255,13 @@ __global__ __launch_bounds__(NT) void qkv_fwd_k(QkvLayout L, const float *qkv, l
 
 // Backward on the fused d_qkv buffer (q/k columns in place):
 //   dn = rope^T(g);  d_pre = rmsnorm_bw(dn; x = pre-norm q/k);  dw += dn*ri*x
+// outb (optional): the results go to this bf16 copy of the whole row (q, k
+// and the untouched v columns) instead of back into dqkv.
 __global__ __launch_bounds__(NT) void qkv_bwd_k(QkvLayout L, float *dqkv, long ld,
                                                  const float *qkv, long ld_qkv, const float *wq,
                                                  const float *wk, float *partial,
-                                                 const float2 *tab, int rpb) {
+                                                 const float2 *tab, int rpb, bf16 *outb,
+                                                 long ldb) {
     __shared__ float stage[NT / 64][256];
     __shared__ float red[NT / 64][2][256];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
@@ -297,17 +325,25 @@ __global__ __launch_bounds__(NT) void qkv_bwd_k(QkvLayout L, float *dqkv, long l
                         const float o = ri * g[e] * dn[k] - ri3_over_D * xv[k] * A_f;
                         const float dwv = dn[k] * ri * xv[k];
                         if (is_q) dwq[k] += dwv; else dwk[k] += dwv;
-                        drow[h * hd + e] = o;
+                        if (outb) outb[(long)t * ldb + h * hd + e] = (bf16)o;
+                        else drow[h * hd + e] = o;
                     }
                 } else {
 #pragma unroll
                     for (int k = 0; k < MAX_EPL; ++k) {
                         const int e = lane + 64 * k;
-                        if (e < hd) drow[h * hd + e] = dn[k];
+                        if (e >= hd) continue;
+                        if (outb) outb[(long)t * ldb + h * hd + e] = (bf16)dn[k];
+                        else drow[h * hd + e] = dn[k];
                     }
                 }
             }
             __syncthreads();
+        }
+        if (outb) {
+            const int vcol0 = H * hd, vn = L.n_kv_heads * hd;
+            for (int c = threadIdx.x; c < vn; c += NT)
+                outb[(long)t * ldb + vcol0 + c] = (bf16)drow[vcol0 + c];
         }
     }
     // combine the 4 waves' gain partials, fixed order
@@ -335,25 +371,30 @@ inline int qkv_blocks(int rows) { return rows < 512 ? rows : 512; }
 
 size_t rmsnorm_partial_floats(int rows, int dim) { return (size_t)rms_blocks(rows) * dim; }
 
-hipError_t rmsnorm_forward(const float *x, const float *w, float *y, int rows, int dim,
+hipError_t rmsnorm_forward(const float *x, const float *w, void *y, DType ydt, int rows, int dim,
                            float eps, int gemma_quirk, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
-    hipLaunchKernelGGL(rmsnorm_fwd_k, dim3(rows), dim3(NT), 0, st, x, w, y, dim, eps, gemma_quirk);
+    if (ydt == DType::BF16)
+        hipLaunchKernelGGL(rmsnorm_fwd_k<bf16>, dim3(rows), dim3(NT), 0, st, x, w, (bf16 *)y, dim,
+                           eps, gemma_quirk);
+    else
+        hipLaunchKernelGGL(rmsnorm_fwd_k<float>, dim3(rows), dim3(NT), 0, st, x, w, (float *)y, dim,
+                           eps, gemma_quirk);
     return hipGetLastError();
 }
 
 hipError_t rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
-                            const float *residual, float *dw, float *partial, int rows,
+                            bf16 *dxb, const float *residual, float *dw, float *partial, int rows,
                             int dim, float eps, int gemma_quirk, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
     if (dim > NT * MAX_CPT) return hipErrorInvalidValue;
     const int nb = rms_blocks(rows);
     const int rpb = (rows + nb - 1) / nb;
     const int nblocks = (rows + rpb - 1) / rpb;
-    hipLaunchKernelGGL(rmsnorm_bwd_k, dim3(nblocks), dim3(NT), 0, st, dy, x, w, dx, residual,
+    hipLaunchKernelGGL(rmsnorm_bwd_k, dim3(nblocks), dim3(NT), 0, st, dy, x, w, dx, dxb, residual,
                        partial, rows, dim, eps, gemma_quirk, rpb);
     if (dw)
-        hipLaunchKernelGGL(colsum_k, dim3(ceil_div(dim, 256)), dim3(256), 0, st,
+        hipLaunchKernelGGL(colsum_k, dim3(ceil_div(dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
                            (const float *)partial, nblocks, (long)dim, dim, dw);
     return hipGetLastError();
 }
@@ -393,7 +434,7 @@ hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv
 hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const float *qkv,
                                 long ld_qkv, const float *wq, const float *wk, float *dwq,
                                 float *dwk, float *partial, const float2 *rope_tab,
-                                hipStream_t st) {
+                                bf16 *outb, long ldb, hipStream_t st) {
     if (L.n_rows <= 0) return hipSuccess;
     if (L.head_dim > 64 * MAX_EPL || L.rotary_dim > L.head_dim || (L.rotary_dim & 1))
         return hipErrorInvalidValue;
@@ -401,11 +442,11 @@ hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const 
     const int rpb = (L.n_rows + nb - 1) / nb;
     const int nblocks = (L.n_rows + rpb - 1) / rpb;
     hipLaunchKernelGGL(qkv_bwd_k, dim3(nblocks), dim3(NT), 0, st, L, dqkv, ld, qkv, ld_qkv, wq, wk,
-                       partial, rope_tab, rpb);
+                       partial, rope_tab, rpb, outb, ldb);
     if (L.qk_norm && dwq && dwk) {
-        hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, 256)), dim3(256), 0, st,
+        hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
                            (const float *)partial, nblocks, (long)2 * L.head_dim, L.head_dim, dwq);
-        hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, 256)), dim3(256), 0, st,
+        hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
                            (const float *)partial + L.head_dim, nblocks, (long)2 * L.head_dim,
                            L.head_dim, dwk);
     }

@@ -28,6 +28,24 @@ hipError_t gemm_nn(Precision pr, Mat dy, Mat w, float *dx, long lddx, int M, int
 // dW[N,K] = dy[M,N]^T x[M,K]  (+ beta*dW_old)
 hipError_t gemm_tn(Precision pr, Mat dy, Mat x, float *dw, long lddw, int M, int N, int K,
                    float alpha, float beta, hipStream_t st);
+// ── bf16-operand GEMMs (k_gemm16.hip) ─────────────────────────────────
+// Same contractions as gemm_nt / gemm_nn / gemm_tn with every operand bf16
+// (fp32 accumulate and output).  `ws` is the split-K workspace (may be
+// empty: no split); g16_ws_bytes_for(M, N, K) of the C = [M, N] x K product
+// is the size the planner would like for that shape.
+struct GemmWs {
+    void *p;
+    size_t bytes;
+};
+hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
+                  int N, int K, const float *R, long ldr, float alpha, float beta,
+                  const GemmWs &ws, hipStream_t st);
+hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
+hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw, long lddw, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
+size_t g16_ws_bytes_for(int M, int N, int K);
+
 // bf16-output forward GEMM (used for LoRA intermediates and bf16 copies)
 hipError_t gemm_nt_bf16out(Mat x, Mat w, bf16 *y, long ldy, int M, int N, int K, float alpha,
                            hipStream_t st);
@@ -38,24 +56,27 @@ hipError_t add_in_place(float *dst, const float *src, size_t n, hipStream_t st);
 hipError_t vec_add(const float *a, const float *b, float *c, size_t n, hipStream_t st);
 hipError_t scale(const float *in, float *out, size_t n, float s, hipStream_t st);
 hipError_t cast_f32_to_bf16(const float *in, bf16 *out, size_t n, hipStream_t st);
-hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup, float *g,
-                          long ldg, int rows, int cols, hipStream_t st);
+// SwiGLU outputs are fp32 or bf16 (the GEMM-operand copy) per `gdt` / `odt`.
+hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup, void *g,
+                          long ldg, DType gdt, int rows, int cols, hipStream_t st);
 hipError_t swiglu_backward(const float *dg, long lddg, const float *pg, long ldpg,
-                           const float *up, long ldup, float *dpg, long lddpg, float *dup,
-                           long lddup, int rows, int cols, hipStream_t st);
+                           const float *up, long ldup, void *dpg, long lddpg, void *dup,
+                           long lddup, DType odt, int rows, int cols, hipStream_t st);
 hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int n_pos, int dim,
                         float scale, hipStream_t st);
 // Adam (adam_step.comp): bc1 = 1 - beta1^t, bc2 = 1 - beta2^t computed by the caller.
+// pb (optional) receives bf16(p) after the update.
 hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,
                      float beta1, float beta2, float eps, float bc1, float bc2, float wd,
-                     hipStream_t st);
+                     bf16 *pb, hipStream_t st);
 
-hipError_t rmsnorm_forward(const float *x, const float *w, float *y, int rows, int dim,
+// y (fp32 or bf16 per ydt) = rmsnorm(x) * w
+hipError_t rmsnorm_forward(const float *x, const float *w, void *y, DType ydt, int rows, int dim,
                            float eps, int gemma_quirk, hipStream_t st);
-// dx = rmsnorm_bw(dy) (+ residual add), dw (reduced over rows, overwrite);
-// `partial` must hold rmsnorm_partial_floats(rows, dim) floats.
+// dx = rmsnorm_bw(dy) (+ residual add), dxb (optional) = bf16(dx), dw (reduced
+// over rows, overwrite); `partial` must hold rmsnorm_partial_floats(rows, dim) floats.
 hipError_t rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
-                            const float *residual, float *dw, float *partial, int rows,
+                            bf16 *dxb, const float *residual, float *dw, float *partial, int rows,
                             int dim, float eps, int gemma_quirk, hipStream_t st);
 size_t rmsnorm_partial_floats(int rows, int dim);
 
@@ -80,12 +101,13 @@ struct QkvLayout {
 hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv,
                                const float *wq, const float *wk, void *out, long ld_out,
                                DType out_dt, const float2 *rope_tab, hipStream_t st);
-// Backward of the above on the fused d_qkv buffer, in place for the q/k
-// columns: d(post-rope) -> d(pre-norm); dwq/dwk reduced gains (overwrite).
+// Backward of the above on the fused d_qkv buffer: d(post-rope) ->
+// d(pre-norm) for the q/k columns, in place, or (outb non-null) written with
+// the v columns to the bf16 copy outb; dwq/dwk reduced gains (overwrite).
 hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const float *qkv,
                                 long ld_qkv, const float *wq, const float *wk, float *dwq,
                                 float *dwk, float *partial, const float2 *rope_tab,
-                                hipStream_t st);
+                                bf16 *outb, long ldb, hipStream_t st);
 size_t qkv_partial_floats(const QkvLayout &L);
 
 // ── embedding backward (k_embed.hip) ─────────────────────────────────
@@ -116,9 +138,10 @@ struct AttnPtrs {
     float *dv; long lddv;
     DType dt;
 };
+// ob (optional, bf16 operands only): bf16 copy of O for the output projection.
 hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
                       const void *v, long ldv, float *o, long ldo, float *lse, DType dt,
-                      hipStream_t st);
+                      bf16 *ob, long ldob, hipStream_t st);
 // D = rowsum(O * dO); optionally also writes dO as bf16 (dout_bf16, ld lddo16)
 hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *dout, long lddo,
                    float *d, bf16 *dout_bf16, long lddo16, hipStream_t st);
@@ -134,6 +157,13 @@ size_t cce_work_floats(const CceShape &s);
 hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const float *w,
                        const uint32_t *tgt, float *lse, float *loss_row, float *loss_mean,
                        float *work, hipStream_t st);
+// bf16-operand forms (h, W bf16; dz bf16), on the gemm16 kernel.
+hipError_t cce_forward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
+                         float *lse, float *loss_row, float *loss_mean, float *work,
+                         hipStream_t st);
+hipError_t cce_backward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
+                          const float *lse, bf16 *dz, float *dh, float *dw, float dw_beta,
+                          const GemmWs &ws, hipStream_t st);
 // dz (bf16 for Precision::BF16 else fp32) [N, V] is materialised in `dz`;
 // dh overwritten (if non-null); dW = beta*dW + dz^T h (if non-null).
 hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const float *w,

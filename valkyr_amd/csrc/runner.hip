@@ -18,6 +18,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <chrono>
 #include <vector>
 
@@ -40,6 +41,8 @@ struct Acts {
     float *n1, *qkv, *attn_out, *lse, *mid, *n2, *gu, *gated, *y;
     void *qkv_attn;
     float *inter[7];
+    // bf16 precision: GEMM operand copies (n1, attention output, n2, gated)
+    bf16 *n1b, *attn_b, *n2b, *gatedb;
 };
 
 __global__ void init_normal_k(float *p, size_t n, uint64_t seed, float stddev) {
@@ -80,6 +83,13 @@ struct vkh_runner {
     size_t total = 0, tb = 0, te = 0, lora_a_begin = 0, lora_b_begin = 0;
 
     float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
+    // bf16 precision: bf16 shadow of P (the GEMM weight operands), refreshed
+    // by Adam and re-cast whenever parameters change from the host side
+    bf16 *Pb = nullptr;
+    bool shadow_dirty = true;
+    bf16 *fn_outb = nullptr, *d_gub = nullptr, *d_midb = nullptr, *d_qkvb = nullptr,
+         *dxb[2] = {nullptr, nullptr};
+    GemmWs gws{nullptr, 0};
     std::vector<Acts> acts;
     float *x_emb = nullptr, *fn_out = nullptr, *ce_lse = nullptr, *loss_row = nullptr,
           *loss_mean = nullptr;
@@ -209,6 +219,8 @@ struct vkh_runner {
         return base + (s.off - tb);
     }
     float *W(const Span &s) const { return P + s.off; }
+    const bf16 *Wb(const Span &s) const { return Pb + s.off; }
+    bool b16() const { return pr == Precision::BF16; }
     float *Gd(const Span &s) const { return lora ? nullptr : G + (s.off - tb); }
 
     // ── init ────────────────────────────────────────────────────────
@@ -249,6 +261,7 @@ struct vkh_runner {
 
         VKH_TRY(alloc(P, total));
         VKH_HIP(hipMemsetAsync(P, 0, total * 4, own));
+        if (b16()) VKH_TRY(alloc(Pb, total));
         const size_t nt = te - tb;
         VKH_TRY(alloc(G, nt));
         VKH_TRY(alloc(M, nt));
@@ -271,7 +284,16 @@ struct vkh_runner {
         acts.assign(L, Acts{});
         for (int l = 0; l < L; ++l) {
             Acts &a = acts[l];
-            VKH_TRY(alloc(a.n1, (size_t)T * D));
+            if (b16()) {
+                VKH_TRY(alloc(a.n1b, (size_t)T * D));
+                VKH_TRY(alloc(a.attn_b, (size_t)T * qd));
+                VKH_TRY(alloc(a.n2b, (size_t)T * D));
+                VKH_TRY(alloc(a.gatedb, (size_t)T * F));
+            } else {
+                VKH_TRY(alloc(a.n1, (size_t)T * D));
+                VKH_TRY(alloc(a.n2, (size_t)T * D));
+                VKH_TRY(alloc(a.gated, (size_t)T * F));
+            }
             VKH_TRY(alloc(a.qkv, (size_t)T * qkvd));
             char *qa = nullptr;
             VKH_TRY(alloc(qa, (size_t)T * qkvd * asz));
@@ -279,9 +301,7 @@ struct vkh_runner {
             VKH_TRY(alloc(a.attn_out, (size_t)T * qd));
             VKH_TRY(alloc(a.lse, (size_t)T * H));
             VKH_TRY(alloc(a.mid, (size_t)T * D));
-            VKH_TRY(alloc(a.n2, (size_t)T * D));
             VKH_TRY(alloc(a.gu, (size_t)T * 2 * F));
-            VKH_TRY(alloc(a.gated, (size_t)T * F));
             VKH_TRY(alloc(a.y, (size_t)T * D));
             for (int p = 0; p < 7; ++p) {
                 a.inter[p] = nullptr;
@@ -289,12 +309,33 @@ struct vkh_runner {
             }
         }
         VKH_TRY(alloc(x_emb, (size_t)T * D));
-        VKH_TRY(alloc(fn_out, (size_t)T * D));
+        if (b16()) {
+            VKH_TRY(alloc(fn_outb, (size_t)T * D));
+            VKH_TRY(alloc(d_gub, (size_t)T * 2 * F));
+            VKH_TRY(alloc(d_midb, (size_t)T * D));
+            VKH_TRY(alloc(d_qkvb, (size_t)T * qkvd));
+            VKH_TRY(alloc(dxb[0], (size_t)T * D));
+            VKH_TRY(alloc(dxb[1], (size_t)T * D));
+            // split-K workspace: the largest the planner asks for over the step's GEMMs
+            size_t wsb = 0;
+            auto need = [&](int m, int n, int k) { wsb = std::max(wsb, g16_ws_bytes_for(m, n, k)); };
+            need(T, qkvd, D); need(T, D, qd); need(T, 2 * F, D); need(T, D, F);
+            need(T, F, D); need(T, D, 2 * F); need(T, qd, D); need(T, D, qkvd);
+            need(D, F, T); need(2 * F, D, T); need(D, qd, T); need(qkvd, D, T);
+            need(T, D, V); need(V, D, T);
+            if (wsb) {
+                char *w = nullptr;
+                VKH_TRY(alloc(w, wsb));
+                gws = GemmWs{w, wsb};
+            }
+        } else {
+            VKH_TRY(alloc(fn_out, (size_t)T * D));
+        }
         VKH_TRY(alloc(ce_lse, T));
         VKH_TRY(alloc(loss_row, T));
         VKH_TRY(alloc(loss_mean, 4));
         VKH_TRY(alloc(d_gated, (size_t)T * F));
-        VKH_TRY(alloc(d_gu, (size_t)T * 2 * F));
+        if (!b16()) VKH_TRY(alloc(d_gu, (size_t)T * 2 * F));
         VKH_TRY(alloc(d_n, (size_t)T * D));
         VKH_TRY(alloc(d_mid, (size_t)T * D));
         VKH_TRY(alloc(d_attn_out, (size_t)T * qd));
@@ -311,7 +352,7 @@ struct vkh_runner {
         CceShape cs{T, V, D, 0.f, 0.f};
         VKH_TRY(alloc(cce_work, cce_work_floats(cs)));
         char *z = nullptr;
-        VKH_TRY(alloc(z, (size_t)T * V * (pr == Precision::BF16 ? 2 : 4)));
+        VKH_TRY(alloc(z, (size_t)T * V * (b16() ? 2 : 4)));
         dz = z;
         char *ew = nullptr;
         VKH_TRY(alloc(ew, embed_bw_work_bytes(T)));
@@ -415,6 +456,7 @@ struct vkh_runner {
     }
 
     vkh_status init_random(uint64_t seed, float std_, float lora_std) {
+        shadow_dirty = true;
         auto normal = [&](const Span &s, uint64_t tag, float sd) -> vkh_status {
             if (!s.numel) return VKH_OK;
             const unsigned g = (unsigned)std::min<size_t>(4096, (s.numel + 255) / 256);
@@ -448,13 +490,62 @@ struct vkh_runner {
 
     // y = x W^T for one projection p, plus the LoRA term when p is a target
     // (train/lora.zig:99-129; oracle lora.zig:75-121).
-    vkh_status lora_fwd(int l, int p, const float *x, long ldx, float *y, long ldy) {
+    vkh_status lora_fwd(int l, int p, Mat x, float *y, long ldy) {
         int N, K;
         proj_shape(p, N, K);
         float *A = W(ls[l].la[p]), *Bm = W(ls[l].lb[p]);
         float *inter = acts[l].inter[p];
-        VKH_HIP(gemm_nt(pr, matf(x, ldx), matf(A, K), inter, R, T, R, K, nullptr, 0, 1.f, 0.f, cur));
+        VKH_HIP(gemm_nt(pr, x, matf(A, K), inter, R, T, R, K, nullptr, 0, 1.f, 0.f, cur));
         VKH_HIP(gemm_nt(pr, matf(inter, R), matf(Bm, R), y, ldy, T, N, R, nullptr, 0, aor, 1.f, cur));
+        return VKH_OK;
+    }
+
+    static Mat matb(const bf16 *p, long ld) { return Mat{p, ld, DType::BF16}; }
+
+    // y[T, N] = x[T, K] W[N, K]^T (+ R residual): bf16 shadow operands in the
+    // bf16 precision, fp32 operands otherwise.
+    vkh_status linear_fwd(Mat x, const Span &w, float *y, long ldy, int N, int K, const float *R,
+                          long ldr) {
+        if (b16())
+            VKH_HIP(g16_nt((const bf16 *)x.p, x.ld, Wb(w), K, y, ldy, T, N, K, R, ldr, 1.f, 0.f, gws, cur));
+        else
+            VKH_HIP(gemm_nt(pr, x, matf(W(w), K), y, ldy, T, N, K, R, ldr, 1.f, 0.f, cur));
+        return VKH_OK;
+    }
+    // dx[T, K] = dy[T, N] W[N, K]
+    vkh_status linear_dx(Mat dy, const Span &w, float *dx, long lddx, int N, int K) {
+        if (b16())
+            VKH_HIP(g16_nn((const bf16 *)dy.p, dy.ld, Wb(w), K, dx, lddx, T, N, K, 1.f, 0.f, gws, cur));
+        else
+            VKH_HIP(gemm_nn(pr, dy, matf(W(w), K), dx, lddx, T, N, K, 1.f, 0.f, cur));
+        return VKH_OK;
+    }
+    // dW[N, K] = dy[T, N]^T x[T, K] (overwrite)
+    vkh_status linear_dw(Mat dy, Mat x, const Span &w, int N, int K) {
+        if (lora) return VKH_OK;  // base weights frozen
+        if (b16())
+            VKH_HIP(g16_tn((const bf16 *)dy.p, dy.ld, (const bf16 *)x.p, x.ld, Gd(w), K, T, N, K, 1.f,
+                           0.f, gws, cur));
+        else
+            VKH_HIP(gemm_tn(pr, dy, x, Gd(w), K, T, N, K, 1.f, 0.f, cur));
+        return VKH_OK;
+    }
+
+    // operand views of the per-layer activations in the current precision
+    Mat m_n1(const Acts &a) const { return b16() ? matb(a.n1b, D) : matf(a.n1, D); }
+    Mat m_n2(const Acts &a) const { return b16() ? matb(a.n2b, D) : matf(a.n2, D); }
+    Mat m_attn(const Acts &a) const { return b16() ? matb(a.attn_b, qd) : matf(a.attn_out, qd); }
+    Mat m_gated(const Acts &a) const { return b16() ? matb(a.gatedb, F) : matf(a.gated, F); }
+    static Mat shift(Mat m, long cols) {
+        m.p = (const char *)m.p + cols * (m.dt == DType::BF16 ? 2 : 4);
+        return m;
+    }
+
+    vkh_status sync_shadow() {
+        if (b16() && shadow_dirty) {
+            VKH_HIP(cast_f32_to_bf16(P, Pb, total, cur));
+            shadow_dirty = false;
+        }
         return VKH_OK;
     }
 
@@ -462,12 +553,15 @@ struct vkh_runner {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const float *x_in = l == 0 ? x_emb : acts[l - 1].y;
+        const DType odt = b16() ? DType::BF16 : DType::F32;
         // transformer.zig:1794-1885
-        VKH_HIP(rmsnorm_forward(x_in, W(s.t[0]), a.n1, T, D, cfg.rms_eps, 0, cur));
-        VKH_HIP(gemm_nt(pr, matf(a.n1, D), matf(W(s.t[1]), D), a.qkv, qkvd, T, qkvd, D, nullptr, 0, 1.f, 0.f, cur));
-        if (proj_lora(0)) VKH_TRY(lora_fwd(l, 0, a.n1, D, a.qkv, qkvd));
-        if (proj_lora(1)) VKH_TRY(lora_fwd(l, 1, a.n1, D, a.qkv + qd, qkvd));
-        if (proj_lora(2)) VKH_TRY(lora_fwd(l, 2, a.n1, D, a.qkv + qd + kvd, qkvd));
+        VKH_HIP(rmsnorm_forward(x_in, W(s.t[0]), b16() ? (void *)a.n1b : (void *)a.n1, odt, T, D,
+                                cfg.rms_eps, 0, cur));
+        const Mat n1 = m_n1(a);
+        VKH_TRY(linear_fwd(n1, s.t[1], a.qkv, qkvd, qkvd, D, nullptr, 0));
+        if (proj_lora(0)) VKH_TRY(lora_fwd(l, 0, n1, a.qkv, qkvd));
+        if (proj_lora(1)) VKH_TRY(lora_fwd(l, 1, n1, a.qkv + qd, qkvd));
+        if (proj_lora(2)) VKH_TRY(lora_fwd(l, 2, n1, a.qkv + qd + kvd, qkvd));
         const QkvLayout ql = qkv_layout();
         VKH_HIP(qkv_prepare_forward(ql, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                     cfg.qk_norm ? W(s.t[10]) : nullptr, a.qkv_attn, qkvd, adt,
@@ -475,26 +569,35 @@ struct vkh_runner {
         const AttnShape as = attn_shape();
         const size_t es = adt == DType::BF16 ? 2 : 4;
         const char *qa = (const char *)a.qkv_attn;
+        const bool ob = b16() && adt == DType::BF16;
         VKH_HIP(fa_forward(as, qa, qkvd, qa + qd * es, qkvd, qa + (qd + kvd) * es, qkvd, a.attn_out,
-                           qd, a.lse, adt, cur));
+                           qd, a.lse, adt, ob ? a.attn_b : nullptr, qd, cur));
+        if (b16() && !ob) VKH_HIP(cast_f32_to_bf16(a.attn_out, a.attn_b, (size_t)T * qd, cur));
         // mid = x_in + attn_out W_o^T (+ LoRA)
-        VKH_HIP(gemm_nt(pr, matf(a.attn_out, qd), matf(W(s.t[4]), qd), a.mid, D, T, D, qd, x_in, D, 1.f, 0.f, cur));
-        if (proj_lora(3)) VKH_TRY(lora_fwd(l, 3, a.attn_out, qd, a.mid, D));
-        VKH_HIP(rmsnorm_forward(a.mid, W(s.t[5]), a.n2, T, D, cfg.rms_eps, 0, cur));
-        VKH_HIP(gemm_nt(pr, matf(a.n2, D), matf(W(s.t[6]), D), a.gu, 2 * F, T, 2 * F, D, nullptr, 0, 1.f, 0.f, cur));
-        if (proj_lora(4)) VKH_TRY(lora_fwd(l, 4, a.n2, D, a.gu, 2 * F));
-        if (proj_lora(5)) VKH_TRY(lora_fwd(l, 5, a.n2, D, a.gu + F, 2 * F));
-        VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F, a.gated, F, T, F, cur));
+        const Mat att = m_attn(a);
+        VKH_TRY(linear_fwd(att, s.t[4], a.mid, D, D, qd, x_in, D));
+        if (proj_lora(3)) VKH_TRY(lora_fwd(l, 3, att, a.mid, D));
+        VKH_HIP(rmsnorm_forward(a.mid, W(s.t[5]), b16() ? (void *)a.n2b : (void *)a.n2, odt, T, D,
+                                cfg.rms_eps, 0, cur));
+        const Mat n2 = m_n2(a);
+        VKH_TRY(linear_fwd(n2, s.t[6], a.gu, 2 * F, 2 * F, D, nullptr, 0));
+        if (proj_lora(4)) VKH_TRY(lora_fwd(l, 4, n2, a.gu, 2 * F));
+        if (proj_lora(5)) VKH_TRY(lora_fwd(l, 5, n2, a.gu + F, 2 * F));
+        VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F, b16() ? (void *)a.gatedb : (void *)a.gated,
+                               F, odt, T, F, cur));
         // y = mid + gated W_down^T (+ LoRA)
-        VKH_HIP(gemm_nt(pr, matf(a.gated, F), matf(W(s.t[8]), F), a.y, D, T, D, F, a.mid, D, 1.f, 0.f, cur));
-        if (proj_lora(6)) VKH_TRY(lora_fwd(l, 6, a.gated, F, a.y, D));
+        const Mat gt = m_gated(a);
+        VKH_TRY(linear_fwd(gt, s.t[8], a.y, D, D, F, a.mid, D));
+        if (proj_lora(6)) VKH_TRY(lora_fwd(l, 6, gt, a.y, D));
         return VKH_OK;
     }
 
     vkh_status forward_all() {
+        VKH_TRY(sync_shadow());
         VKH_HIP(embed_lookup(W(embed), tok_d, x_emb, T, D, 1.0f, cur));
         for (int l = 0; l < L; ++l) VKH_TRY(layer_forward(l));
-        VKH_HIP(rmsnorm_forward(acts[L - 1].y, W(final_norm), fn_out, T, D, cfg.rms_eps, 0, cur));
+        VKH_HIP(rmsnorm_forward(acts[L - 1].y, W(final_norm), b16() ? (void *)fn_outb : (void *)fn_out,
+                                b16() ? DType::BF16 : DType::F32, T, D, cfg.rms_eps, 0, cur));
         return VKH_OK;
     }
 
@@ -502,40 +605,51 @@ struct vkh_runner {
 
     // LoRA backward of projection p after the base dx GEMM (train/lora.zig:137-251):
     // dx += aor (dy B) A;  dA = aor (dy B)^T x;  dB = aor dy^T inter.
-    vkh_status lora_bwd(int l, int p, const float *dy, long lddy, const float *x, long ldx,
-                        float *dxo, long lddx) {
+    vkh_status lora_bwd(int l, int p, Mat dy, Mat x, float *dxo, long lddx) {
         int N, K;
         proj_shape(p, N, K);
         float *A = W(ls[l].la[p]), *Bm = W(ls[l].lb[p]);
         float *dA = G + (ls[l].la[p].off - tb), *dB = G + (ls[l].lb[p].off - tb);
-        VKH_HIP(gemm_nn(pr, matf(dy, lddy), matf(Bm, R), dyB, R, T, N, R, 1.f, 0.f, cur));
+        VKH_HIP(gemm_nn(pr, dy, matf(Bm, R), dyB, R, T, N, R, 1.f, 0.f, cur));
         if (dxo) VKH_HIP(gemm_nn(pr, matf(dyB, R), matf(A, K), dxo, lddx, T, R, K, aor, 1.f, cur));
-        VKH_HIP(gemm_tn(pr, matf(dyB, R), matf(x, ldx), dA, K, T, R, K, aor, 0.f, cur));
-        VKH_HIP(gemm_tn(pr, matf(dy, lddy), matf(acts[l].inter[p], R), dB, R, T, N, R, aor, 0.f, cur));
+        VKH_HIP(gemm_tn(pr, matf(dyB, R), x, dA, K, T, R, K, aor, 0.f, cur));
+        VKH_HIP(gemm_tn(pr, dy, matf(acts[l].inter[p], R), dB, R, T, N, R, aor, 0.f, cur));
         return VKH_OK;
     }
 
-    vkh_status layer_backward(int l, const float *dy, float *dxo) {
+    // dy / dyb: the residual-stream gradient (fp32) and its bf16 copy; the
+    // layer input gradient goes to dxo / dxob.
+    vkh_status layer_backward(int l, const float *dy, const bf16 *dyb, float *dxo, bf16 *dxob) {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const float *x_in = l == 0 ? x_emb : acts[l - 1].y;
+        const Mat mdy = b16() ? matb(dyb, D) : matf(dy, D);
         // transformer.zig:1967-2070 (order), train_decoder.zig:340-498 (math)
         // down: d_gated = dy W_down;  dW_down = dy^T gated
-        VKH_HIP(gemm_nn(pr, matf(dy, D), matf(W(s.t[8]), F), d_gated, F, T, D, F, 1.f, 0.f, cur));
-        if (!lora) VKH_HIP(gemm_tn(pr, matf(dy, D), matf(a.gated, F), Gd(s.t[8]), F, T, D, F, 1.f, 0.f, cur));
-        if (proj_lora(6)) VKH_TRY(lora_bwd(l, 6, dy, D, a.gated, F, d_gated, F));
-        VKH_HIP(swiglu_backward(d_gated, F, a.gu, 2 * F, a.gu + F, 2 * F, d_gu, 2 * F, d_gu + F, 2 * F, T, F, cur));
+        VKH_TRY(linear_dx(mdy, s.t[8], d_gated, F, D, F));
+        VKH_TRY(linear_dw(mdy, m_gated(a), s.t[8], D, F));
+        if (proj_lora(6)) VKH_TRY(lora_bwd(l, 6, mdy, m_gated(a), d_gated, F));
+        // swiglu: d_gu = [d_gate | d_up] (bf16 copy only in the bf16 precision)
+        if (b16())
+            VKH_HIP(swiglu_backward(d_gated, F, a.gu, 2 * F, a.gu + F, 2 * F, d_gub, 2 * F, d_gub + F,
+                                    2 * F, DType::BF16, T, F, cur));
+        else
+            VKH_HIP(swiglu_backward(d_gated, F, a.gu, 2 * F, a.gu + F, 2 * F, d_gu, 2 * F, d_gu + F,
+                                    2 * F, DType::F32, T, F, cur));
+        const Mat mdgu = b16() ? matb(d_gub, 2 * F) : matf(d_gu, 2 * F);
         // gate/up (one [2F, D] matrix): d_n2 = d_gu W_gu; dW_gu = d_gu^T n2
-        VKH_HIP(gemm_nn(pr, matf(d_gu, 2 * F), matf(W(s.t[6]), D), d_n, D, T, 2 * F, D, 1.f, 0.f, cur));
-        if (!lora) VKH_HIP(gemm_tn(pr, matf(d_gu, 2 * F), matf(a.n2, D), Gd(s.t[6]), D, T, 2 * F, D, 1.f, 0.f, cur));
-        if (proj_lora(4)) VKH_TRY(lora_bwd(l, 4, d_gu, 2 * F, a.n2, D, d_n, D));
-        if (proj_lora(5)) VKH_TRY(lora_bwd(l, 5, d_gu + F, 2 * F, a.n2, D, d_n, D));
+        VKH_TRY(linear_dx(mdgu, s.t[6], d_n, D, 2 * F, D));
+        VKH_TRY(linear_dw(mdgu, m_n2(a), s.t[6], 2 * F, D));
+        if (proj_lora(4)) VKH_TRY(lora_bwd(l, 4, mdgu, m_n2(a), d_n, D));
+        if (proj_lora(5)) VKH_TRY(lora_bwd(l, 5, shift(mdgu, F), m_n2(a), d_n, D));
         // n2: d_mid = rmsnorm_bw(d_n2) + dy
-        VKH_HIP(rmsnorm_backward(d_n, a.mid, W(s.t[5]), d_mid, dy, Gd(s.t[5]), partial, T, D, cfg.rms_eps, 0, cur));
+        VKH_HIP(rmsnorm_backward(d_n, a.mid, W(s.t[5]), d_mid, d_midb, dy, Gd(s.t[5]), partial, T, D,
+                                 cfg.rms_eps, 0, cur));
+        const Mat mdmid = b16() ? matb(d_midb, D) : matf(d_mid, D);
         // o: d_attn_out = d_mid W_o; dW_o = d_mid^T attn_out
-        VKH_HIP(gemm_nn(pr, matf(d_mid, D), matf(W(s.t[4]), qd), d_attn_out, qd, T, D, qd, 1.f, 0.f, cur));
-        if (!lora) VKH_HIP(gemm_tn(pr, matf(d_mid, D), matf(a.attn_out, qd), Gd(s.t[4]), qd, T, D, qd, 1.f, 0.f, cur));
-        if (proj_lora(3)) VKH_TRY(lora_bwd(l, 3, d_mid, D, a.attn_out, qd, d_attn_out, qd));
+        VKH_TRY(linear_dx(mdmid, s.t[4], d_attn_out, qd, D, qd));
+        VKH_TRY(linear_dw(mdmid, m_attn(a), s.t[4], D, qd));
+        if (proj_lora(3)) VKH_TRY(lora_bwd(l, 3, mdmid, m_attn(a), d_attn_out, qd));
         // attention: D, dK/dV, dQ into the fused d_qkv buffer
         const AttnShape as = attn_shape();
         VKH_HIP(fa_bw_d(as, a.attn_out, qd, d_attn_out, qd, fa_d, dout16, qd, cur));
@@ -554,35 +668,46 @@ struct vkh_runner {
         ap.dt = adt;
         VKH_HIP(fa_bw_dkv(as, ap, cur));
         VKH_HIP(fa_bw_dq(as, ap, cur));
-        // RoPE^T and Q/K-norm backward in place on the q/k columns
+        // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
         const QkvLayout ql = qkv_layout();
         VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                      cfg.qk_norm ? W(s.t[10]) : nullptr,
                                      cfg.qk_norm ? Gd(s.t[9]) : nullptr,
-                                     cfg.qk_norm ? Gd(s.t[10]) : nullptr, partial, rope_tab, cur));
+                                     cfg.qk_norm ? Gd(s.t[10]) : nullptr, partial, rope_tab,
+                                     b16() ? d_qkvb : nullptr, qkvd, cur));
+        const Mat mdqkv = b16() ? matb(d_qkvb, qkvd) : matf(d_qkv, qkvd);
         // q/k/v (one [qkvd, D] matrix): d_n1 = d_qkv W_qkv; dW_qkv = d_qkv^T n1
-        VKH_HIP(gemm_nn(pr, matf(d_qkv, qkvd), matf(W(s.t[1]), D), d_n, D, T, qkvd, D, 1.f, 0.f, cur));
-        if (!lora) VKH_HIP(gemm_tn(pr, matf(d_qkv, qkvd), matf(a.n1, D), Gd(s.t[1]), D, T, qkvd, D, 1.f, 0.f, cur));
-        if (proj_lora(0)) VKH_TRY(lora_bwd(l, 0, d_qkv, qkvd, a.n1, D, d_n, D));
-        if (proj_lora(1)) VKH_TRY(lora_bwd(l, 1, d_qkv + qd, qkvd, a.n1, D, d_n, D));
-        if (proj_lora(2)) VKH_TRY(lora_bwd(l, 2, d_qkv + qd + kvd, qkvd, a.n1, D, d_n, D));
+        VKH_TRY(linear_dx(mdqkv, s.t[1], d_n, D, qkvd, D));
+        VKH_TRY(linear_dw(mdqkv, m_n1(a), s.t[1], qkvd, D));
+        if (proj_lora(0)) VKH_TRY(lora_bwd(l, 0, mdqkv, m_n1(a), d_n, D));
+        if (proj_lora(1)) VKH_TRY(lora_bwd(l, 1, shift(mdqkv, qd), m_n1(a), d_n, D));
+        if (proj_lora(2)) VKH_TRY(lora_bwd(l, 2, shift(mdqkv, qd + kvd), m_n1(a), d_n, D));
         // n1: d_x_in = rmsnorm_bw(d_n1) + d_mid
-        VKH_HIP(rmsnorm_backward(d_n, x_in, W(s.t[0]), dxo, d_mid, Gd(s.t[0]), partial, T, D, cfg.rms_eps, 0, cur));
+        VKH_HIP(rmsnorm_backward(d_n, x_in, W(s.t[0]), dxo, dxob, d_mid, Gd(s.t[0]), partial, T, D,
+                                 cfg.rms_eps, 0, cur));
         return VKH_OK;
     }
 
     vkh_status forward_backward_enqueue() {
         VKH_TRY(forward_all());
         const CceShape cs{T, V, D, 0.f, 0.f};
-        VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean, cce_work, cur));
         // head backward: dh and dW_lm (tied: the embed grad slot)
         float *dw_lm = lora ? nullptr : Gd(lm_head);
-        VKH_HIP(cce_backward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, dz, d_fn, dw_lm, 0.f, cur));
-        VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), dx[0], nullptr, Gd(final_norm),
-                                 partial, T, D, cfg.rms_eps, 0, cur));
+        if (b16()) {
+            VKH_HIP(cce_forward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
+                                  cce_work, cur));
+            VKH_HIP(cce_backward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, (bf16 *)dz, d_fn, dw_lm,
+                                   0.f, gws, cur));
+        } else {
+            VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
+                                cce_work, cur));
+            VKH_HIP(cce_backward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, dz, d_fn, dw_lm, 0.f, cur));
+        }
+        VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), dx[0], dxb[0], nullptr,
+                                 Gd(final_norm), partial, T, D, cfg.rms_eps, 0, cur));
         int c = 0;
         for (int l = L - 1; l >= 0; --l) {
-            VKH_TRY(layer_backward(l, dx[c], dx[c ^ 1]));
+            VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
             c ^= 1;
         }
         if (!lora) {
@@ -597,13 +722,17 @@ struct vkh_runner {
         const float t = (float)step_t;
         const float bc1 = 1.0f - powf(cfg.beta1, t);
         const float bc2 = 1.0f - powf(cfg.beta2, t);
+        bf16 *pb = b16() ? Pb : nullptr;
         if (!lora) {
-            VKH_HIP(adam_step(P, G, M, Vm, total, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2, 0.f, cur));
+            VKH_HIP(adam_step(P, G, M, Vm, total, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2,
+                              0.f, pb, cur));
         } else {
             const size_t na = lora_b_begin - lora_a_begin, nb = total - lora_b_begin;
-            VKH_HIP(adam_step(P + lora_a_begin, G, M, Vm, na, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2, 0.f, cur));
+            VKH_HIP(adam_step(P + lora_a_begin, G, M, Vm, na, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam,
+                              bc1, bc2, 0.f, pb ? pb + lora_a_begin : nullptr, cur));
             VKH_HIP(adam_step(P + lora_b_begin, G + na, M + na, Vm + na, nb, cfg.lr * cfg.lora_lr_b_scale,
-                              cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2, 0.f, cur));
+                              cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2, 0.f,
+                              pb ? pb + lora_b_begin : nullptr, cur));
         }
         return VKH_OK;
     }
@@ -878,7 +1007,10 @@ vkh_status vkh_runner_forward_logits(vkh_runner *r, const uint32_t *token_ids, s
     VKH_TRY(r->forward_all());
     float *logits = nullptr;
     VKH_HIP(hipMallocAsync((void **)&logits, (size_t)r->T * r->V * 4, r->own));
-    hipError_t e = gemm_nt(r->pr, matf(r->fn_out, r->D), matf(r->W(r->lm_head), r->D), logits, r->V,
+    hipError_t e =
+        r->b16() ? g16_nt(r->fn_outb, r->D, r->Wb(r->lm_head), r->D, logits, r->V, r->T, r->V, r->D,
+                          nullptr, 0, 1.f, 0.f, r->gws, r->own)
+                 : gemm_nt(r->pr, matf(r->fn_out, r->D), matf(r->W(r->lm_head), r->D), logits, r->V,
                            r->T, r->V, r->D, nullptr, 0, 1.f, 0.f, r->own);
     if (e == hipSuccess)
         e = hipMemcpyAsync(out_logits, logits, (size_t)r->T * r->V * 4, hipMemcpyDeviceToHost, r->own);
@@ -936,8 +1068,8 @@ vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int
     return VKH_OK;
 }
 
-vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int which,
-                                        float **dptr, size_t *numel) {
+static vkh_status tensor_ptr(vkh_runner *r, int kind, int layer, int which, float **dptr,
+                             size_t *numel) {
     if (!r || !dptr) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
     size_t n = 0;
     VKH_TRY(vkh_runner_tensor_numel(r, kind, layer, which, &n));
@@ -946,11 +1078,20 @@ vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int 
     return VKH_OK;
 }
 
+// The caller may write parameters through the returned pointer, so the bf16
+// weight shadow is re-cast before the next forward pass.
+vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int which,
+                                        float **dptr, size_t *numel) {
+    VKH_TRY(tensor_ptr(r, kind, layer, which, dptr, numel));
+    if (kind == VKH_PARAM) r->shadow_dirty = true;
+    return VKH_OK;
+}
+
 vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, float *host,
                                  size_t numel) {
     float *d = nullptr;
     size_t n = 0;
-    VKH_TRY(vkh_runner_tensor_device_ptr(r, kind, layer, which, &d, &n));
+    VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n));
     if (numel != n || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
     VKH_HIP(hipStreamSynchronize(r->own));
     VKH_HIP(hipMemcpy(host, d, n * 4, hipMemcpyDeviceToHost));
@@ -961,10 +1102,11 @@ vkh_status vkh_runner_set_tensor(vkh_runner *r, int kind, int layer, int which,
                                  const float *host, size_t numel) {
     float *d = nullptr;
     size_t n = 0;
-    VKH_TRY(vkh_runner_tensor_device_ptr(r, kind, layer, which, &d, &n));
+    VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n));
     if (numel != n || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
     VKH_HIP(hipStreamSynchronize(r->own));
     VKH_HIP(hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice));
+    if (kind == VKH_PARAM) r->shadow_dirty = true;
     return VKH_OK;
 }
 
@@ -979,6 +1121,7 @@ vkh_status vkh_runner_load_checkpoint(vkh_runner *r, const char *path) {
     if (!r || !path) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
     std::vector<Blob> b;
     collect_blobs(r, b);
+    r->shadow_dirty = true;
     return load_blobs(r, path, "VKPT", false, b);
 }
 
@@ -995,6 +1138,7 @@ vkh_status vkh_runner_load_lora_checkpoint(vkh_runner *r, const char *path) {
     if (!r->lora) return fail(VKH_ERR_LORA_CHECKPOINT_EMPTY, "runner has no LoRA state");
     std::vector<Blob> b;
     collect_lora_blobs(r, b);
+    r->shadow_dirty = true;
     return load_blobs(r, path, "VLKP", true, b);
 }
 

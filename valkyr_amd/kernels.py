@@ -68,6 +68,21 @@ def linear_backward_dw(dy, x, dw, M, N, K, precision=PRECISION_FP32, stream=None
     check(lib().vkh_linear_backward_dw(_p(dy), _p(x), _p(dw), M, N, K, precision, _s(stream)))
 
 
+def matmul_nt_bf16(x, w, y, M, N, K, stream=None):
+    """y[M,N] = x[M,K] w[N,K]^T on bf16 operands (the bf16 training step's GEMM)."""
+    check(lib().vkh_matmul_nt_bf16(_p(x), _p(w), _p(y), M, N, K, _s(stream)))
+
+
+def linear_backward_dx_bf16(dy, w, dx, M, N, K, stream=None):
+    """dx[M,K] = dy[M,N] w[N,K] on bf16 operands."""
+    check(lib().vkh_linear_backward_dx_bf16(_p(dy), _p(w), _p(dx), M, N, K, _s(stream)))
+
+
+def linear_backward_dw_bf16(dy, x, dw, M, N, K, stream=None):
+    """dw[N,K] = dy[M,N]^T x[M,K] on bf16 operands."""
+    check(lib().vkh_linear_backward_dw_bf16(_p(dy), _p(x), _p(dw), M, N, K, _s(stream)))
+
+
 def lora_forward(x, w, a, b, y, inter, M, N, K, r, alpha_over_r, precision=PRECISION_FP32,
                  stream=None):
     check(lib().vkh_lora_forward(_p(x), _p(w), _p(a), _p(b), _p(y), _p(inter), M, N, K, r,
