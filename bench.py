@@ -115,13 +115,13 @@ def bench_fa_bwd(args):
     dout16 = DeviceBuffer(nq * 2)
     dq, dk, dv = DeviceBuffer(nq * 4), DeviceBuffer(nk * 4), DeviceBuffer(nk * 4)
     p = K.attn_params(S, S, H, Hkv, hd, True, B, K.BF16)
+    ws = DeviceBuffer(max(K.fa_backward_workspace_bytes(p), 4))  # bf16 dS
     s = Stream()
     K.fa_forward(p, q, k, vv, o, lse, stream=s)  # O and LSE of the same inputs
 
     def once():
         K.fa_bw_d(p, o, dout, d, dout16, stream=s)
-        K.fa_bw_dkv(p, q, k, vv, dout16, lse, d, dk, dv, stream=s)
-        K.fa_bw_dq(p, q, k, vv, dout16, lse, d, dq, stream=s)
+        K.fa_backward(p, q, k, vv, dout16, lse, d, dq, dk, dv, ws, stream=s)
 
     for _ in range(3):
         once()

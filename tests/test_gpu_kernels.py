@@ -377,6 +377,19 @@ def test_flash_attention_bf16_mfma(case):
     note(f"  rel-L2 O={e[0]:.2e} dQ={e[1]:.2e} dK={e[2]:.2e} dV={e[3]:.2e}")
     assert max(abs(lse_r - lse)) < 2e-2
     assert all(x < BF16_TOL for x in e), e
+    # the fused backward (bf16 dS workspace + dQ GEMM where the shape allows)
+    ws_bytes = K.fa_backward_workspace_bytes(p)
+    note(f"  fused path: workspace {ws_bytes} bytes")
+    bdq, bdk, bdv = zeros(dq.size), zeros(dk.size), zeros(dv.size)
+    ws = zeros(ws_bytes // 4 + 1) if ws_bytes else None
+    K.fa_backward(p, qb, kb, vb, dob16, dev(lse_r), dev(d), bdq, bdk, bdv, ws)
+    f = [rel_l2(dq_r, host(bdq)), rel_l2(dk_r, host(bdk)), rel_l2(dv_r, host(bdv))]
+    g = [rel_l2(dq, host(bdq)), rel_l2(dk, host(bdk)), rel_l2(dv, host(bdv))]
+    note(f"  fused vs oracle dQ={f[0]:.2e} dK={f[1]:.2e} dV={f[2]:.2e}; "
+         f"vs two-kernel dQ={g[0]:.2e} dK={g[1]:.2e} dV={g[2]:.2e}")
+    assert all(x < BF16_TOL for x in f), f
+    # same dS values and products, only the dQ summation order differs
+    assert all(x < 1e-5 for x in g), g
 
 
 def test_flash_attention_bf16_full_size_invariants():
@@ -404,8 +417,7 @@ def test_flash_attention_bf16_full_size_invariants():
     dob16 = zeros(dO.size // 2 + 8)
     K.fa_bw_d(p, bo, dev(dO), bd, dob16)
     bdq, bdk, bdv = zeros(Q.size), zeros(Kk.size), zeros(Kk.size)
-    K.fa_bw_dkv(p, qb, kb, vb, dob16, blse, bd, bdk, bdv)
-    K.fa_bw_dq(p, qb, kb, vb, dob16, blse, bd, bdq)
+    K.fa_backward(p, qb, kb, vb, dob16, blse, bd, bdq, bdk, bdv)
     o, lse, dq, dk, dv = host(bo), host(blse), host(bdq), host(bdk), host(bdv)
     hpk = H // Hkv
     dv4 = dv.reshape(B, S, Hkv, hd).astype(np.float64)

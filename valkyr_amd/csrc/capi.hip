@@ -194,6 +194,36 @@ vkh_status vkh_fa_bw_dkv(const vkh_attn_params *p, const void *q, const void *k,
     return VKH_OK;
 }
 
+size_t vkh_fa_backward_workspace_bytes(const vkh_attn_params *p) {
+    if (!p || check_attn(p) != VKH_OK) return 0;
+    const AttnShape s = attn_shape(p);
+    return p->dtype == VKH_BF16 && fa_bw_fused_ok(s) ? fa_bw_ws_bytes(s) : 0;
+}
+
+vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *k, const void *v,
+                           const void *dout, const float *lse, const float *d, float *dq,
+                           float *dk, float *dv, void *workspace, vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(q && k && v && dout && lse && d && dq && dk && dv, "null pointer");
+    AttnPtrs a = attn_ptrs(p, q, k, v, dout, lse, d);
+    a.dq = dq;
+    a.dk = dk;
+    a.dv = dv;
+    const AttnShape s = attn_shape(p);
+    hipStream_t st = S(stream);
+    if (p->dtype != VKH_BF16 || !fa_bw_fused_ok(s)) {
+        VKH_HIP(fa_bw_dkv(s, a, st));
+        VKH_HIP(fa_bw_dq(s, a, st));
+        return VKH_OK;
+    }
+    void *ws = workspace;
+    if (!ws) VKH_HIP(hipMallocAsync(&ws, fa_bw_ws_bytes(s), st));
+    const hipError_t e = fa_bw_fused(s, a, (bf16 *)ws, st);
+    if (!workspace) (void)hipFreeAsync(ws, st);
+    if (e != hipSuccess) return hip_fail(e, "fa_backward");
+    return VKH_OK;
+}
+
 // ── GEMMs ──────────────────────────────────────────────────────────────
 
 vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,

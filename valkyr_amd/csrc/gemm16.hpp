@@ -191,49 +191,30 @@ struct SplitK {
     f32x4 *ws;  // [tiles][splits][BM * BN / 4]
 };
 
-template <class Cfg, Lay LA, Lay LB, class Epi>
-__global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, GemmShape s, Epi epi,
-                                                            SplitK sk) {
+// One block's BM x BN output tile over the K slabs [kbase, kbase + 64 nk):
+// acc (per wave, accumulator layout) += A(m0.., k) B(n0.., k).  `smem` must
+// hold 2 (BM + BN) 128 bytes.  Shared by the GEMM kernels and the attention
+// dQ kernel.
+template <class Cfg, Lay LA, Lay LB, int TM, int TN>
+VKH_DEV void gemm16_tile(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
+                         int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
-    constexpr int TM = WM / 16, TN = WN / 16;
+    static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
     constexpr int ABYTES = BM * 128, BBYTES = BN * 128, STAGE = ABYTES + BBYTES;
-    __shared__ __attribute__((aligned(16))) char smem[2 * STAGE];
-
     const int tid = threadIdx.x;
     const int lane = tid % 64, wave = tid / 64;
     const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
-
-    const int nbm = (s.M + BM - 1) / BM, nbn = (s.N + BN - 1) / BN;
-    const int nb = nbm * nbn * sk.splits;
-    int bid = blockIdx.x;
-    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
-    const int split = bid % sk.splits, tile = bid / sk.splits;
-    const int bm = tile % nbm, bn = tile / nbm;
-    const int m0 = bm * BM, n0 = bn * BN;
-
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a), rb = make_rsrc(b);
     // register staging sets (the second is used only with PF == 2)
     typename Ld16Sel<LA, BM, NT>::T la0, la1;
     typename Ld16Sel<LB, BN, NT>::T lb0, lb1;
-    la0.setup(a, m0, s.M, tid);
-    lb0.setup(b, n0, s.N, tid);
+    la0.setup(a, m0, M, tid);
+    lb0.setup(b, n0, N, tid);
     if constexpr (Cfg::PF == 2) {
-        la1.setup(a, m0, s.M, tid);
-        lb1.setup(b, n0, s.N, tid);
+        la1.setup(a, m0, M, tid);
+        lb1.setup(b, n0, N, tid);
     }
-
-    f32x4 acc[TM][TN];
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    const int nk_all = (s.K + 63) / 64;
-    const int kt0 = (int)((long)nk_all * split / sk.splits);
-    const int nk = (int)((long)nk_all * (split + 1) / sk.splits) - kt0;
-    const int kbase = kt0 * 64;
-
     // per-lane fragment offsets: row fr of each 16-row group, chunk (4 ks + fg)
     const int fr = lane % 16, fg = lane / 16;
     const int sw = fg ^ (fr & 7);
@@ -260,15 +241,15 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
     char *const lds0 = smem, *const lds1 = smem + STAGE;
 
     if constexpr (Cfg::PF == 1) {
-        la0.load(ra, a.ld, kbase, s.K, tid);
-        lb0.load(rb, b.ld, kbase, s.K, tid);
+        la0.load(ra, a.ld, kbase, Kmax, tid);
+        lb0.load(rb, b.ld, kbase, Kmax, tid);
         la0.store(lds0, tid);
         lb0.store(lds0 + ABYTES, tid);
         __syncthreads();
         for (int kt = 0; kt < nk; ++kt) {
             if (kt + 1 < nk) {
-                la0.load(ra, a.ld, kbase + (kt + 1) * 64, s.K, tid);
-                lb0.load(rb, b.ld, kbase + (kt + 1) * 64, s.K, tid);
+                la0.load(ra, a.ld, kbase + (kt + 1) * 64, Kmax, tid);
+                lb0.load(rb, b.ld, kbase + (kt + 1) * 64, Kmax, tid);
             }
             compute(kt & 1 ? lds1 : lds0);
             if (kt + 1 < nk) {
@@ -281,17 +262,17 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
     } else {
         // Invariant at an even step kt: lds0 holds slab kt, set 1 holds slab
         // kt+1 and set 0 slab kt+2 (both in flight); odd steps swap roles.
-        la0.load(ra, a.ld, kbase, s.K, tid);
-        lb0.load(rb, b.ld, kbase, s.K, tid);
+        la0.load(ra, a.ld, kbase, Kmax, tid);
+        lb0.load(rb, b.ld, kbase, Kmax, tid);
         if (nk > 1) {
-            la1.load(ra, a.ld, kbase + 64, s.K, tid);
-            lb1.load(rb, b.ld, kbase + 64, s.K, tid);
+            la1.load(ra, a.ld, kbase + 64, Kmax, tid);
+            lb1.load(rb, b.ld, kbase + 64, Kmax, tid);
         }
         la0.store(lds0, tid);
         lb0.store(lds0 + ABYTES, tid);
         if (nk > 2) {
-            la0.load(ra, a.ld, kbase + 128, s.K, tid);
-            lb0.load(rb, b.ld, kbase + 128, s.K, tid);
+            la0.load(ra, a.ld, kbase + 128, Kmax, tid);
+            lb0.load(rb, b.ld, kbase + 128, Kmax, tid);
         }
         __syncthreads();
         for (int kt = 0; kt < nk; kt += 2) {
@@ -301,8 +282,8 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
                 lb1.store(lds1 + ABYTES, tid);
             }
             if (kt + 3 < nk) {
-                la1.load(ra, a.ld, kbase + (kt + 3) * 64, s.K, tid);
-                lb1.load(rb, b.ld, kbase + (kt + 3) * 64, s.K, tid);
+                la1.load(ra, a.ld, kbase + (kt + 3) * 64, Kmax, tid);
+                lb1.load(rb, b.ld, kbase + (kt + 3) * 64, Kmax, tid);
             }
             __syncthreads();
             if (kt + 1 >= nk) break;
@@ -312,12 +293,45 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
                 lb0.store(lds0 + ABYTES, tid);
             }
             if (kt + 4 < nk) {
-                la0.load(ra, a.ld, kbase + (kt + 4) * 64, s.K, tid);
-                lb0.load(rb, b.ld, kbase + (kt + 4) * 64, s.K, tid);
+                la0.load(ra, a.ld, kbase + (kt + 4) * 64, Kmax, tid);
+                lb0.load(rb, b.ld, kbase + (kt + 4) * 64, Kmax, tid);
             }
             __syncthreads();
         }
     }
+
+}
+
+template <class Cfg, Lay LA, Lay LB, class Epi>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, GemmShape s, Epi epi,
+                                                            SplitK sk) {
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
+    constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    __shared__ __attribute__((aligned(16))) char smem[2 * (BM + BN) * 128];
+
+    const int tid = threadIdx.x;
+    const int lane = tid % 64, wave = tid / 64;
+    const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+
+    const int nbm = (s.M + BM - 1) / BM, nbn = (s.N + BN - 1) / BN;
+    const int nb = nbm * nbn * sk.splits;
+    int bid = blockIdx.x;
+    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+    const int split = bid % sk.splits, tile = bid / sk.splits;
+    const int bm = tile % nbm, bn = tile / nbm;
+    const int m0 = bm * BM, n0 = bn * BN;
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nk_all = (s.K + 63) / 64;
+    const int kt0 = (int)((long)nk_all * split / sk.splits);
+    const int nk = (int)((long)nk_all * (split + 1) / sk.splits) - kt0;
+    gemm16_tile<Cfg, LA, LB, TM, TN>(a, b, m0, n0, s.M, s.N, kt0 * 64, nk, s.K, acc, smem);
 
     if (sk.splits > 1) {
         f32x4 *own = sk.ws + ((size_t)tile * sk.splits + split) * (BM * BN / 4);

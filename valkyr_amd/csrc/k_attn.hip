@@ -28,6 +28,7 @@
 //
 // fp32 path (precision = fp32, parity mode): one wave per query (or key) row,
 // scalar FMAs with wave reductions, structured like the reference shaders.
+#include "gemm16.hpp"
 #include "ops.hpp"
 
 namespace vkh {
@@ -479,6 +480,252 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dq_bf16_k(AttnShape s, AttnPtrs 
     }
 }
 
+// ── backward v2: dK/dV + dS (bf16) then dQ = dS K as a GEMM ───────────
+//
+// The dK/dV kernel keeps K and V of its 32 keys per wave in registers and
+// streams the 64-row Q / dO tiles of every query head of the GQA group
+// through double-buffered LDS, the next tile's global loads in flight while
+// the current one computes (one barrier per tile).  The transposed operands
+// (dO^T for dV, Q^T for dK) are read from the same row-major tiles with the
+// gfx950 transposing LDS load (ds_read_b64_tr_b16), so no transposed copies
+// are staged.  dS = P (dP - D) is written once as bf16 (exactly the values
+// the dK MFMAs consume) to a [batch, head, n_q, n_kv] workspace, and dQ is
+// then the plain product dS K, computed by the shared GEMM tile routine with
+// the causal K limit; S and dP are not recomputed for dQ.
+//
+// ds_read_b64_tr_b16 (measured on MI355X): within each 16-lane group, lane i
+// receives element (i % 4) of the 8-byte chunks addressed by lanes
+// 4 j + i / 4, j = 0..3.  So if lane l of the group addresses row r0 + l / 4,
+// column c0 + 4 (l % 4) of a row-major tile X, lane i gets X[r0 + j][c0 + i].
+
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4;
+
+// X[r0 + j][c0 + (lane % 16)], j = 0..3, from a row-major LDS tile of pitch P
+template <int P>
+VKH_DEV bf16x4 ld_tr4(const bf16 *tile, int r0, int c0, int l16) {
+    const bf16 *src = tile + (r0 + l16 / 4) * P + c0 + 4 * (l16 % 4);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)src);
+}
+
+// A operand (rows = tile columns c0 + lane%16, contraction = tile rows
+// k0 + {4g..4g+3, 16+4g..16+4g+3}) read transposed from a row-major tile:
+// the k order matches an accumulator used as the B operand (frag_acc).
+template <int P>
+VKH_DEV bf16x8 frag_tr(const bf16 *tile, int c0, int k0, int g, int l16) {
+    const bf16x4 lo = ld_tr4<P>(tile, k0 + 4 * g, c0, l16);
+    const bf16x4 hi = ld_tr4<P>(tile, k0 + 16 + 4 * g, c0, l16);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+template <int HD>
+__global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, bf16 *dsw) {
+    constexpr int BN = 128, BM = 64, DS = HD / 32, DSUB = HD / 16;
+    constexpr int P = HD + 16;      // LDS pitch (elements): conflict-free b128 and tr reads
+    constexpr int CH = HD / 8;      // 16-byte chunks per row
+    constexpr int PER = BM * CH / NT;
+    static_assert(PER * NT == BM * CH, "tile / thread mismatch");
+    __shared__ __attribute__((aligned(16))) bf16 Qs[2][BM][P];
+    __shared__ __attribute__((aligned(16))) bf16 Os[2][BM][P];
+    __shared__ float lse_s[2][BM], d_s[2][BM];
+
+    const int nkt = (s.n_kv + BN - 1) / BN;
+    const int kt = s.causal ? nkt - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
+    const int kvh = blockIdx.y, b = blockIdx.z;
+    const int hpk = s.n_heads / s.n_kv_heads;
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
+    const int k0 = kt * BN, kw0 = k0 + wave * 32;
+    const int off = s.n_kv - s.n_q;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+    const bf16 *kb = (const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD;
+    const bf16 *vb = (const bf16 *)p.v + (long)b * s.n_kv * p.ldv + kvh * HD;
+
+    bf16x8 kf[2][DS], vf[2][DS];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int kr = kw0 + 16 * ks + c16;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            kf[ks][ds] = kr < s.n_kv ? ld_frag(kb + (long)kr * p.ldk + 32 * ds + 8 * g) : bf16x8{};
+            vf[ks][ds] = kr < s.n_kv ? ld_frag(vb + (long)kr * p.ldv + 32 * ds + 8 * g) : bf16x8{};
+        }
+    }
+    f32x4 dvt[DSUB][2], dkt[DSUB][2];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i) dvt[i][0] = dvt[i][1] = dkt[i][0] = dkt[i][1] = f32x4{0, 0, 0, 0};
+
+    // (query head, q tile) iterations, flattened so prefetch crosses heads
+    const int qstart = s.causal ? max(0, k0 - off) / BM * BM : 0;
+    const int nqt = s.n_q > qstart ? (s.n_q - qstart + BM - 1) / BM : 0;
+    const int niter = hpk * nqt;
+
+    uint4 rq[PER], ro[PER];
+    float rl = 0.f, rd = 0.f;
+    auto gload = [&](int it) {
+        const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+        const bf16 *qb = (const bf16 *)p.q + (long)b * s.n_q * p.ldq + h * HD;
+        const bf16 *ob = (const bf16 *)p.dout + (long)b * s.n_q * p.lddo + h * HD;
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT, r = u / CH, c = u % CH, qa = q0 + r;
+            rq[i] = qa < s.n_q ? *reinterpret_cast<const uint4 *>(qb + (long)qa * p.ldq + c * 8) : make_uint4(0, 0, 0, 0);
+            ro[i] = qa < s.n_q ? *reinterpret_cast<const uint4 *>(ob + (long)qa * p.lddo + c * 8) : make_uint4(0, 0, 0, 0);
+        }
+        if (tid < BM) {
+            const int qa = q0 + tid;
+            const long t = (long)b * s.n_q + qa;
+            rl = qa < s.n_q ? p.lse[t * s.n_heads + h] * LOG2E : INFINITY;
+            rd = qa < s.n_q ? p.d[t * s.n_heads + h] : 0.f;
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+            const int u = tid + i * NT, r = u / CH, c = u % CH;
+            *reinterpret_cast<uint4 *>(&Qs[buf][r][c * 8]) = rq[i];
+            *reinterpret_cast<uint4 *>(&Os[buf][r][c * 8]) = ro[i];
+        }
+        if (tid < BM) {
+            lse_s[buf][tid] = rl;
+            d_s[buf][tid] = rd;
+        }
+    };
+
+    if (niter > 0) {
+        gload(0);
+        lstore(0);
+    }
+    __syncthreads();
+    for (int it = 0; it < niter; ++it) {
+        const int buf = it & 1;
+        if (it + 1 < niter) gload(it + 1);
+        const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+        bf16 *dsr = dsw ? dsw + (((long)b * s.n_heads + h) * s.n_q + q0) * s.n_kv : nullptr;
+        if (s.causal && kw0 > q0 + BM - 1 + off) {
+            // every key of this wave is masked for the tile: dS is zero
+            if (dsr) {
+#pragma unroll
+                for (int qs = 0; qs < 4; ++qs)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int ql = 16 * qs + 4 * g + r;
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            const int ka = kw0 + 16 * ks + c16;
+                            if (q0 + ql < s.n_q && ka < s.n_kv) dsr[(long)ql * s.n_kv + ka] = (bf16)0.f;
+                        }
+                    }
+            }
+        } else {
+            const bf16 *Qb = &Qs[buf][0][0], *Ob = &Os[buf][0][0];
+            f32x4 sc[4][2], dp[4][2];
+#pragma unroll
+            for (int qs = 0; qs < 4; ++qs) sc[qs][0] = sc[qs][1] = dp[qs][0] = dp[qs][1] = f32x4{0, 0, 0, 0};
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+                for (int qs = 0; qs < 4; ++qs) {
+                    const bf16x8 qa = ld_frag(Qb + (16 * qs + c16) * P + 32 * ds + 8 * g);
+                    const bf16x8 oa = ld_frag(Ob + (16 * qs + c16) * P + 32 * ds + 8 * g);
+                    sc[qs][0] = mfma16x16x32(qa, kf[0][ds], sc[qs][0]);
+                    sc[qs][1] = mfma16x16x32(qa, kf[1][ds], sc[qs][1]);
+                    dp[qs][0] = mfma16x16x32(oa, vf[0][ds], dp[qs][0]);
+                    dp[qs][1] = mfma16x16x32(oa, vf[1][ds], dp[qs][1]);
+                }
+#pragma unroll
+            for (int qs = 0; qs < 4; ++qs)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int ql = 16 * qs + 4 * g + r;
+                    const int qa = q0 + ql;
+                    const float lq = lse_s[buf][ql], dq = d_s[buf][ql];
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks) {
+                        const int ka = kw0 + 16 * ks + c16;
+                        float pv = (lq == -INFINITY) ? 0.f : exp2f(sc[qs][ks][r] * c2 - lq);
+                        if (qa >= s.n_q || ka >= s.n_kv || (s.causal && ka > qa + off)) pv = 0.f;
+                        sc[qs][ks][r] = pv;
+                        const float dsv = pv * (dp[qs][ks][r] - dq);
+                        dp[qs][ks][r] = dsv;
+                        if (dsr && qa < s.n_q && ka < s.n_kv) dsr[(long)ql * s.n_kv + ka] = (bf16)dsv;
+                    }
+                }
+#pragma unroll
+            for (int qst = 0; qst < 2; ++qst) {
+                const bf16x8 pb0 = frag_acc(sc[2 * qst][0], sc[2 * qst + 1][0]);
+                const bf16x8 pb1 = frag_acc(sc[2 * qst][1], sc[2 * qst + 1][1]);
+                const bf16x8 sb0 = frag_acc(dp[2 * qst][0], dp[2 * qst + 1][0]);
+                const bf16x8 sb1 = frag_acc(dp[2 * qst][1], dp[2 * qst + 1][1]);
+#pragma unroll
+                for (int i = 0; i < DSUB; ++i) {
+                    const bf16x8 oa = frag_tr<P>(Ob, 16 * i, 32 * qst, g, c16);
+                    const bf16x8 qa = frag_tr<P>(Qb, 16 * i, 32 * qst, g, c16);
+                    dvt[i][0] = mfma16x16x32(oa, pb0, dvt[i][0]);
+                    dvt[i][1] = mfma16x16x32(oa, pb1, dvt[i][1]);
+                    dkt[i][0] = mfma16x16x32(qa, sb0, dkt[i][0]);
+                    dkt[i][1] = mfma16x16x32(qa, sb1, dkt[i][1]);
+                }
+            }
+        }
+        if (it + 1 < niter) lstore(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int ka = kw0 + 16 * ks + c16;
+        if (ka >= s.n_kv) continue;
+        const long t = (long)b * s.n_kv + ka;
+        float *dkr = p.dk + t * p.lddk + kvh * HD;
+        float *dvr = p.dv + t * p.lddv + kvh * HD;
+        const float sc_ = s.inv_sqrt_dim;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = dkt[i][ks], c = dvt[i][ks];
+            *reinterpret_cast<float4 *>(dkr + 16 * i + 4 * g) = make_float4(a[0] * sc_, a[1] * sc_, a[2] * sc_, a[3] * sc_);
+            *reinterpret_cast<float4 *>(dvr + 16 * i + 4 * g) = make_float4(c[0], c[1], c[2], c[3]);
+        }
+    }
+}
+
+// dQ[q, :] = inv_sqrt_dim * sum_{k visible} dS[q, k] K[k, :]: one 128 x HD
+// output tile per (q tile, head, sequence) on the GEMM tile routine (A = dS
+// rows, K-major; B = K rows, MN-major).
+template <int HD>
+__global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, const bf16 *dsw) {
+    using Cfg = Tile16<128, HD, 2, 2>;
+    constexpr int TM = 128 / 2 / 16, TN = HD / 2 / 16;
+    __shared__ __attribute__((aligned(16))) char smem[2 * (128 + HD) * 128];
+    const int qt = s.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
+    const int h = blockIdx.y, b = blockIdx.z;
+    const int kvh = h / (s.n_heads / s.n_kv_heads);
+    const int q0 = qt * 128;
+    const int off = s.n_kv - s.n_q;
+    const int kend = s.causal ? min(s.n_kv, q0 + 128 + off) : s.n_kv;
+    const Op16 a{dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv, s.n_kv,
+                 (unsigned)((size_t)s.n_q * s.n_kv * 2)};
+    const Op16 bk{(const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD, p.ldk,
+                  (unsigned)(((size_t)(s.n_kv - 1) * p.ldk + HD) * 2)};
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gemm16_tile<Cfg, Lay::K, Lay::MN, TM, TN>(a, bk, q0, 0, s.n_q, HD, 0, (kend + 63) / 64, kend,
+                                              acc, smem);
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int row0 = q0 + (wave / 2) * 64, col0 = (wave % 2) * (HD / 2);
+    const float sc_ = s.inv_sqrt_dim;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int q = row0 + 16 * i + 4 * (lane / 16) + r;
+            if (q >= s.n_q) continue;
+            float *dqr = p.dq + ((long)b * s.n_q + q) * p.lddq + h * HD;
+#pragma unroll
+            for (int j = 0; j < TN; ++j) dqr[col0 + 16 * j + lane % 16] = acc[i][j][r] * sc_;
+        }
+}
+
 // ── fp32 path: one wave per row ──────────────────────────────────────
 
 constexpr int MAXE = 4;  // head_dim <= 256
@@ -670,6 +917,31 @@ hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
         if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
         hipLaunchKernelGGL(fa_bwd_dq_f32_k, dim3(rows_grid((long)s.n_batch * s.n_q * s.n_heads)),
                            dim3(NT), 0, st, s, p);
+    }
+    return hipGetLastError();
+}
+
+bool fa_bw_fused_ok(const AttnShape &s) {
+    return bf16_ok(s) && s.n_q % 64 == 0 && s.n_kv % 64 == 0 && (!s.causal || s.n_q == s.n_kv) &&
+           (size_t)s.n_q * s.n_kv * 2 < (1ull << 31) && s.n_kv_heads > 0 &&
+           s.n_heads % s.n_kv_heads == 0;
+}
+
+size_t fa_bw_ws_bytes(const AttnShape &s) {
+    return (size_t)s.n_batch * s.n_heads * s.n_q * s.n_kv * sizeof(bf16);
+}
+
+hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipStream_t st) {
+    if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
+    if (p.dt != DType::BF16 || !fa_bw_fused_ok(s) || !ds_ws) return hipErrorInvalidValue;
+    dim3 gkv((s.n_kv + 127) / 128, s.n_kv_heads, s.n_batch);
+    dim3 gq((s.n_q + 127) / 128, s.n_heads, s.n_batch);
+    if (s.head_dim == 128) {
+        hipLaunchKernelGGL(fa_bwd_dkv2_k<128>, gkv, dim3(NT), 0, st, s, p, ds_ws);
+        hipLaunchKernelGGL(fa_dq_gemm_k<128>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);
+    } else {
+        hipLaunchKernelGGL(fa_bwd_dkv2_k<64>, gkv, dim3(NT), 0, st, s, p, ds_ws);
+        hipLaunchKernelGGL(fa_dq_gemm_k<64>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);
     }
     return hipGetLastError();
 }

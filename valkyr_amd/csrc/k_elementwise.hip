@@ -192,28 +192,66 @@ __device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, flo
     p = q - lr * m_hat / (sqrtf(v_hat) + eps);
 }
 
-// pb (optional): bf16 copy of the updated parameters (the GEMM operand shadow)
-__global__ void adam_k(float *p, const float *g, float *m, float *v, bf16 *pb, size_t n, float lr,
-                       float b1, float b2, float eps, float bc1, float bc2, float wd, bool vec) {
+VKH_DEV void adam4(f32x4 &p, const f32x4 &g, f32x4 &m, f32x4 &v, float lr, float b1, float b2,
+                   float eps, float bc1, float bc2, float wd) {
+    float pp[4] = {p.x, p.y, p.z, p.w}, mm[4] = {m.x, m.y, m.z, m.w}, vv[4] = {v.x, v.y, v.z, v.w};
+    const float gg[4] = {g.x, g.y, g.z, g.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) adam1(pp[i], gg[i], mm[i], vv[i], lr, b1, b2, eps, bc1, bc2, wd);
+    p = f32x4{pp[0], pp[1], pp[2], pp[3]};
+    m = f32x4{mm[0], mm[1], mm[2], mm[3]};
+    v = f32x4{vv[0], vv[1], vv[2], vv[3]};
+}
+
+// Streaming update: every byte is touched once, so loads and stores are
+// non-temporal, and two grid-stride iterations are in flight per thread.
+// pb (optional): bf16 copy of the updated parameters (the GEMM operand shadow).
+constexpr int ADAM_GRID = 256 * 32;
+
+__global__ __launch_bounds__(NT) void adam_k(float *p_, const float *g_, float *m_, float *v_,
+                                              bf16 *pb, size_t n, float lr, float b1, float b2,
+                                              float eps, float bc1, float bc2, float wd, bool vec) {
     const size_t n4 = vec ? n / 4 : 0;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
-        float4 pp = reinterpret_cast<float4 *>(p)[i];
-        float4 gg = reinterpret_cast<const float4 *>(g)[i];
-        float4 mm = reinterpret_cast<float4 *>(m)[i];
-        float4 vv = reinterpret_cast<float4 *>(v)[i];
-        adam1(pp.x, gg.x, mm.x, vv.x, lr, b1, b2, eps, bc1, bc2, wd);
-        adam1(pp.y, gg.y, mm.y, vv.y, lr, b1, b2, eps, bc1, bc2, wd);
-        adam1(pp.z, gg.z, mm.z, vv.z, lr, b1, b2, eps, bc1, bc2, wd);
-        adam1(pp.w, gg.w, mm.w, vv.w, lr, b1, b2, eps, bc1, bc2, wd);
-        reinterpret_cast<float4 *>(p)[i] = pp;
-        reinterpret_cast<float4 *>(m)[i] = mm;
-        reinterpret_cast<float4 *>(v)[i] = vv;
-        if (pb) st4(pb + 4 * i, pp);
+    f32x4 *p = reinterpret_cast<f32x4 *>(p_), *m = reinterpret_cast<f32x4 *>(m_),
+          *v = reinterpret_cast<f32x4 *>(v_);
+    const f32x4 *g = reinterpret_cast<const f32x4 *>(g_);
+    size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
+    for (; i + stride < n4; i += 2 * stride) {
+        f32x4 pp[2], gg[2], mm[2], vv[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const size_t j = i + u * stride;
+            pp[u] = __builtin_nontemporal_load(&p[j]);
+            gg[u] = __builtin_nontemporal_load(&g[j]);
+            mm[u] = __builtin_nontemporal_load(&m[j]);
+            vv[u] = __builtin_nontemporal_load(&v[j]);
+        }
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+            const size_t j = i + u * stride;
+            adam4(pp[u], gg[u], mm[u], vv[u], lr, b1, b2, eps, bc1, bc2, wd);
+            __builtin_nontemporal_store(pp[u], &p[j]);
+            __builtin_nontemporal_store(mm[u], &m[j]);
+            __builtin_nontemporal_store(vv[u], &v[j]);
+            if (pb) {
+                bf16x4 b;
+                b[0] = (bf16)pp[u].x; b[1] = (bf16)pp[u].y; b[2] = (bf16)pp[u].z; b[3] = (bf16)pp[u].w;
+                __builtin_nontemporal_store(b, reinterpret_cast<bf16x4 *>(pb) + j);
+            }
+        }
     }
-    for (size_t i = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        adam1(p[i], g[i], m[i], v[i], lr, b1, b2, eps, bc1, bc2, wd);
-        if (pb) pb[i] = (bf16)p[i];
+    for (; i < n4; i += stride) {
+        f32x4 pp = p[i], mm = m[i], vv = v[i];
+        adam4(pp, g[i], mm, vv, lr, b1, b2, eps, bc1, bc2, wd);
+        p[i] = pp;
+        m[i] = mm;
+        v[i] = vv;
+        if (pb) st4(pb + 4 * i, make_float4(pp.x, pp.y, pp.z, pp.w));
+    }
+    for (size_t k = n4 * 4 + blockIdx.x * (size_t)blockDim.x + threadIdx.x; k < n; k += stride) {
+        adam1(p_[k], g_[k], m_[k], v_[k], lr, b1, b2, eps, bc1, bc2, wd);
+        if (pb) pb[k] = (bf16)p_[k];
     }
 }
 
@@ -320,7 +358,9 @@ hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, flo
                      bf16 *pb, hipStream_t st) {
     if (!n) return hipSuccess;
     const bool vec = al16(p) && al16(g) && al16(m) && al16(v) && ((uintptr_t)pb & 7u) == 0;
-    hipLaunchKernelGGL(adam_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, p, g, m, v, pb, n, lr,
+    size_t grid = (n / 4 + NT - 1) / NT;
+    grid = grid < 1 ? 1 : (grid > ADAM_GRID ? ADAM_GRID : grid);
+    hipLaunchKernelGGL(adam_k, dim3((unsigned)grid), dim3(NT), 0, st, p, g, m, v, pb, n, lr,
                        beta1, beta2, eps, bc1, bc2, wd, vec);
     return hipGetLastError();
 }

@@ -9,6 +9,16 @@
 // Row reductions accumulate in fp64 like the CPU oracle
 // (train_transformer.zig:88-99), and fp contraction is off so the per-element
 // fp32 formulas round exactly as written.
+//
+// Layout on the GPU: one wave owns one row (RMSNorm) or one (row, head)
+// (Q/K norm + RoPE).  Each lane holds contiguous vector chunks of the row, the
+// row reductions are wave shuffles (no block barriers in the row loop), and
+// the RoPE partner element (i <-> i +- rotary_dim/2) comes from a lane
+// shuffle.  Gain gradients stay in registers across a wave's rows and are
+// combined per block in a fixed order.
+#include <algorithm>
+#include <type_traits>
+
 #include "ops.hpp"
 
 #pragma clang fp contract(off)
@@ -18,91 +28,143 @@ namespace vkh {
 namespace {
 
 constexpr int NT = 256;
-constexpr int MAX_CPT = 16;  // columns per thread => dim <= 4096
-
-VKH_DEV double block_sum_d(double v, double *sh) {
-    v = wave_sum(v);
-    const int w = threadIdx.x / 64, l = threadIdx.x % 64;
-    __syncthreads();
-    if (l == 0) sh[w] = v;
-    __syncthreads();
-    double t = 0;
-#pragma unroll
-    for (int i = 0; i < NT / 64; ++i) t += sh[i];
-    return t;
-}
+constexpr int NW = NT / 64;
 
 template <typename TO>
-__global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float *w, TO *y,
+VKH_DEV void store4(TO *p, float a, float b, float c, float d);
+template <>
+VKH_DEV void store4<float>(float *p, float a, float b, float c, float d) {
+    *reinterpret_cast<float4 *>(p) = make_float4(a, b, c, d);
+}
+template <>
+VKH_DEV void store4<bf16>(bf16 *p, float a, float b, float c, float d) {
+    bf16x4 v;
+    v[0] = (bf16)a; v[1] = (bf16)b; v[2] = (bf16)c; v[3] = (bf16)d;
+    *reinterpret_cast<bf16x4 *>(p) = v;
+}
+
+// ── RMSNorm: one wave per row, lane l holds columns 4 l + 256 j ─────────
+
+// C4 = float4 chunks per lane (dim <= 256 * C4)
+template <typename TO, int C4>
+__global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float *w, TO *y, int rows,
                                                      int dim, float eps, int gq) {
-    __shared__ double sh[NT / 64];
-    const long row = blockIdx.x;
-    const float *xr = x + row * dim;
-    TO *yr = y + row * dim;
-    double ss = 0;
-    for (int c = threadIdx.x; c < dim; c += NT) ss += (double)xr[c] * (double)xr[c];
-    ss = block_sum_d(ss, sh);
-    const double m = ss / (double)dim;
-    const float ri = 1.0f / sqrtf((float)m + eps);
-    for (int c = threadIdx.x; c < dim; c += NT) {
-        const float gain = gq ? w[c] + 1.0f : w[c];
-        yr[c] = (TO)(gain * ri * xr[c]);
+    const int lane = threadIdx.x % 64;
+    const int nw = gridDim.x * NW;
+    for (int row = blockIdx.x * NW + threadIdx.x / 64; row < rows; row += nw) {
+        const float *xr = x + (long)row * dim;
+        float4 xv[C4];
+        double ss = 0;
+#pragma unroll
+        for (int j = 0; j < C4; ++j) {
+            const int c = 4 * lane + 256 * j;
+            xv[j] = c < dim ? *reinterpret_cast<const float4 *>(xr + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            ss += (double)xv[j].x * (double)xv[j].x;
+            ss += (double)xv[j].y * (double)xv[j].y;
+            ss += (double)xv[j].z * (double)xv[j].z;
+            ss += (double)xv[j].w * (double)xv[j].w;
+        }
+        ss = wave_sum(ss);
+        const double m = ss / (double)dim;
+        const float ri = 1.0f / sqrtf((float)m + eps);
+#pragma unroll
+        for (int j = 0; j < C4; ++j) {
+            const int c = 4 * lane + 256 * j;
+            if (c >= dim) continue;
+            float4 g = *reinterpret_cast<const float4 *>(w + c);
+            if (gq) g = make_float4(g.x + 1.0f, g.y + 1.0f, g.z + 1.0f, g.w + 1.0f);
+            store4<TO>(y + (long)row * dim + c, g.x * ri * xv[j].x, g.y * ri * xv[j].y,
+                       g.z * ri * xv[j].z, g.w * ri * xv[j].w);
+        }
     }
 }
 
-// Rows [blockIdx.x * rpb, ...) of one norm; per-thread gain-gradient partials.
 // dxb (optional): bf16 copy of dx, the operand of the next GEMMs.
+// partial[blockIdx.x][dim]: this block's gain-gradient sum over its rows.
+template <int C4>
 __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float *x,
                                                      const float *w, float *dx, bf16 *dxb,
-                                                     const float *res, float *partial,
-                                                     int rows, int dim, float eps, int gq,
-                                                     int rpb) {
-    __shared__ double sh[NT / 64];
-    float dwacc[MAX_CPT];
+                                                     const float *res, float *partial, int rows,
+                                                     int dim, float eps, int gq) {
+    __shared__ float red[256 * C4];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    const int nw = gridDim.x * NW;
+    float4 gain[C4], dwa[C4];
 #pragma unroll
-    for (int k = 0; k < MAX_CPT; ++k) dwacc[k] = 0.f;
-    const int r0 = blockIdx.x * rpb;
-    const int r1 = min(rows, r0 + rpb);
+    for (int j = 0; j < C4; ++j) {
+        const int c = 4 * lane + 256 * j;
+        gain[j] = c < dim ? *reinterpret_cast<const float4 *>(w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (gq) gain[j] = make_float4(gain[j].x + 1.0f, gain[j].y + 1.0f, gain[j].z + 1.0f, gain[j].w + 1.0f);
+        dwa[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
     const float ri3_div = (float)dim;
-    for (int row = r0; row < r1; ++row) {
-        const float *xr = x + (long)row * dim;
-        const float *dyr = dy + (long)row * dim;
+    for (int row = blockIdx.x * NW + wave; row < rows; row += nw) {
+        const long ro = (long)row * dim;
+        float4 xv[C4], dv[C4], rv[C4];
         double ss = 0, A = 0;
 #pragma unroll
-        for (int k = 0; k < MAX_CPT; ++k) {
-            const int c = threadIdx.x + k * NT;
-            if (c < dim) {
-                const double xv = xr[c];
-                const float gain = gq ? w[c] + 1.0f : w[c];
-                ss += xv * xv;
-                A += (double)dyr[c] * (double)gain * xv;
+        for (int j = 0; j < C4; ++j) {
+            const int c = 4 * lane + 256 * j;
+            const bool ok = c < dim;
+            xv[j] = ok ? *reinterpret_cast<const float4 *>(x + ro + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            dv[j] = ok ? *reinterpret_cast<const float4 *>(dy + ro + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            rv[j] = (ok && res) ? *reinterpret_cast<const float4 *>(res + ro + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < C4; ++j) {
+            const float xs[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            const float ds[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+            const float gs[4] = {gain[j].x, gain[j].y, gain[j].z, gain[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const double xd = xs[q];
+                ss += xd * xd;
+                A += (double)ds[q] * (double)gs[q] * xd;
             }
         }
-        ss = block_sum_d(ss, sh);
-        A = block_sum_d(A, sh);
+        ss = wave_sum(ss);
+        A = wave_sum(A);
         const double m = ss / (double)dim;
         const float ri = 1.0f / sqrtf((float)m + eps);
         const float ri3_over_D = ri * ri * ri / ri3_div;
         const float A_f = (float)A;
 #pragma unroll
-        for (int k = 0; k < MAX_CPT; ++k) {
-            const int c = threadIdx.x + k * NT;
-            if (c < dim) {
-                const float gain = gq ? w[c] + 1.0f : w[c];
-                const float xv = xr[c], dv = dyr[c];
-                float o = ri * gain * dv - ri3_over_D * xv * A_f;
-                if (res) o = o + res[(long)row * dim + c];
-                dx[(long)row * dim + c] = o;
-                if (dxb) dxb[(long)row * dim + c] = (bf16)o;
-                dwacc[k] += dv * ri * xv;
+        for (int j = 0; j < C4; ++j) {
+            const int c = 4 * lane + 256 * j;
+            if (c >= dim) continue;
+            const float xs[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            const float ds[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+            const float gs[4] = {gain[j].x, gain[j].y, gain[j].z, gain[j].w};
+            float o[4], dw[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                o[q] = ri * gs[q] * ds[q] - ri3_over_D * xs[q] * A_f;
+                dw[q] = ds[q] * ri * xs[q];
             }
+            if (res) {
+                const float4 r = rv[j];
+                o[0] = o[0] + r.x; o[1] = o[1] + r.y; o[2] = o[2] + r.z; o[3] = o[3] + r.w;
+            }
+            store4<float>(dx + ro + c, o[0], o[1], o[2], o[3]);
+            if (dxb) store4<bf16>(dxb + ro + c, o[0], o[1], o[2], o[3]);
+            dwa[j].x += dw[0]; dwa[j].y += dw[1]; dwa[j].z += dw[2]; dwa[j].w += dw[3];
         }
     }
+    // combine the waves' gain partials in a fixed order: ((w0 + w1) + w2) + w3
+    for (int wv = 0; wv < NW; ++wv) {
+        if (wave == wv) {
 #pragma unroll
-    for (int k = 0; k < MAX_CPT; ++k) {
-        const int c = threadIdx.x + k * NT;
-        if (c < dim) partial[(long)blockIdx.x * dim + c] = dwacc[k];
+            for (int j = 0; j < C4; ++j) {
+                const int c = 4 * lane + 256 * j;
+                if (c >= dim) continue;
+                float4 a = dwa[j];
+                if (wv > 0) a = make_float4(red[c] + a.x, red[c + 1] + a.y, red[c + 2] + a.z, red[c + 3] + a.w);
+                red[c] = a.x; red[c + 1] = a.y; red[c + 2] = a.z; red[c + 3] = a.w;
+            }
+        }
+        __syncthreads();
     }
+    for (int c = threadIdx.x; c < dim; c += NT) partial[(long)blockIdx.x * dim + c] = red[c];
 }
 
 // out[c] = sum_b partial[b * stride + c].  A block owns 16 columns; its 16
@@ -135,8 +197,6 @@ __global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *part
         out[c] = s;
     }
 }
-
-inline int rms_blocks(int rows) { return rows < 512 ? rows : 512; }
 
 // ── RoPE ─────────────────────────────────────────────────────────────
 
@@ -176,226 +236,310 @@ __global__ void qk_rope_k(const float *q_in, long ldq_in, float *q_out, long ldq
 
 // ── fused per-head Q/K RMSNorm + RoPE (+ operand cast) ───────────────
 
-template <typename TO>
-VKH_DEV void store_out(TO *p, float v);
-template <>
-VKH_DEV void store_out<float>(float *p, float v) { *p = v; }
-template <>
-VKH_DEV void store_out<bf16>(bf16 *p, float v) { *p = (bf16)v; }
+// One wave per (row, head); lane l holds elements EPL l .. EPL l + EPL - 1
+// of the head (EPL = 1, 2, 4 for head_dim <= 64, 128, 256).
+template <int EPL>
+VKH_DEV void ld_epl(const float *p, float (&v)[EPL], bool ok) {
+    if (!ok) {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) v[i] = 0.f;
+        return;
+    }
+    if constexpr (EPL == 4) {
+        const float4 t = *reinterpret_cast<const float4 *>(p);
+        v[0] = t.x; v[1] = t.y; v[2] = t.z; v[3] = t.w;
+    } else if constexpr (EPL == 2) {
+        const float2 t = *reinterpret_cast<const float2 *>(p);
+        v[0] = t.x; v[1] = t.y;
+    } else {
+        v[0] = *p;
+    }
+}
 
-constexpr int MAX_EPL = 4;  // elements per lane => head_dim <= 256
+template <typename TO, int EPL>
+VKH_DEV void st_epl(TO *p, const float (&v)[EPL]) {
+    if constexpr (EPL == 4) {
+        store4<TO>(p, v[0], v[1], v[2], v[3]);
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) p[i] = (TO)v[i];
+    }
+}
 
-// One block per row; waves take heads round-robin.  Forward: normalised and
-// rotated q, k plus v, written as attention operands of type TO.
-template <typename TO>
+// pv[i] = the head's element j(e) = e < half ? e + half : e - half, e = EPL lane + i
+template <int EPL>
+VKH_DEV void rope_partner(const float (&v)[EPL], float (&pv)[EPL], int lane, int half) {
+    if (half % EPL == 0) {
+        const int e0 = EPL * lane;
+        int src = (e0 < half ? e0 + half : e0 - half) / EPL;
+        src = src < 0 ? 0 : (src > 63 ? 63 : src);
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) pv[i] = __shfl(v[i], src, 64);
+    } else {
+#pragma unroll
+        for (int i = 0; i < EPL; ++i) {
+            const int e = EPL * lane + i;
+            const int j = e < half ? e + half : e - half;
+            int src = j / EPL;
+            src = src < 0 ? 0 : (src > 63 ? 63 : src);
+            const int si = j - src * EPL;
+            float r = 0.f;
+#pragma unroll
+            for (int i2 = 0; i2 < EPL; ++i2) {
+                const float t = __shfl(v[i2], src, 64);
+                if (si == i2) r = t;
+            }
+            pv[i] = r;
+        }
+    }
+}
+
+// The per-item inputs of a wave: the head's values, the pre-norm q/k (for
+// the backward's norm) and the RoPE (cos, sin) of each lane's elements.
+template <int EPL>
+struct HeadItem {
+    float v[EPL], x[EPL];
+    float2 cs[EPL];
+};
+
+template <int EPL>
+VKH_DEV void load_item(HeadItem<EPL> &it, const float *vp, const float *xp, const float2 *tr,
+                       int e0, int rot, int half, bool on, bool qk) {
+    ld_epl<EPL>(vp, it.v, on);
+    ld_epl<EPL>(xp, it.x, on && xp != nullptr);
+#pragma unroll
+    for (int i = 0; i < EPL; ++i) {
+        const int e = e0 + i;
+        it.cs[i] = (qk && e < rot) ? tr[e < half ? e : e - half] : make_float2(1.f, 0.f);
+    }
+}
+
+// Forward: normalised and rotated q, k plus v, written as attention operands
+// of type TO.  Items are (row, head) over the q, k and v heads; each wave
+// prefetches its next item while it finishes the current one.
+template <typename TO, int EPL>
 __global__ __launch_bounds__(NT) void qkv_fwd_k(QkvLayout L, const float *qkv, long ld_qkv,
                                                  const float *wq, const float *wk, TO *out,
                                                  long ld_out, const float2 *tab) {
-    __shared__ float stage[NT / 64][256];
-    const int t = blockIdx.x;
-    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const int hd = L.head_dim, H = L.n_q_heads + L.n_kv_heads;
-    const int half = L.rotary_dim / 2;
-    const int p = t % L.seq_len;
-    const float *row = qkv + (long)t * ld_qkv;
-    TO *orow = out + (long)t * ld_out;
-    const int iters = (H + 3) / 4;
-    for (int it = 0; it < iters; ++it) {
-        const int h = it * 4 + wave;
-        const bool active = h < H;
-        float y[MAX_EPL];
-        if (active) {
-            const bool is_q = h < L.n_q_heads;
-            const int col0 = h * hd;  // q heads then k heads are contiguous
-            const float *g = is_q ? wq : wk;
-            double ss = 0;
+    const int lane = threadIdx.x % 64;
+    const int hd = L.head_dim, Hqk = L.n_q_heads + L.n_kv_heads, Htot = Hqk + L.n_kv_heads;
+    const int half = L.rotary_dim / 2, rot = L.rotary_dim;
+    const long items = (long)L.n_rows * Htot;
+    const long nw = (long)gridDim.x * NW;
+    const int e0 = EPL * lane;
+    const bool on = e0 < hd;
+    float gq[EPL], gk[EPL];
+    ld_epl<EPL>(wq + e0, gq, on && L.qk_norm);
+    ld_epl<EPL>(wk + e0, gk, on && L.qk_norm);
+    auto fetch = [&](long it, HeadItem<EPL> &d) {
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        load_item<EPL>(d, qkv + (long)t * ld_qkv + h * hd + e0, nullptr,
+                       tab + (long)(t % L.seq_len) * half, e0, rot, half, on, h < Hqk);
+    };
+    long it = (long)blockIdx.x * NW + threadIdx.x / 64;
+    HeadItem<EPL> cur;
+    if (it < items) fetch(it, cur);
+    for (; it < items; it += nw) {
+        HeadItem<EPL> nxt;
+        if (it + nw < items) fetch(it + nw, nxt);
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        float y[EPL];
 #pragma unroll
-            for (int k = 0; k < MAX_EPL; ++k) {
-                const int e = lane + 64 * k;
-                y[k] = e < hd ? row[col0 + e] : 0.f;
-                ss += (double)y[k] * (double)y[k];
-            }
+        for (int i = 0; i < EPL; ++i) y[i] = cur.v[i];
+        if (h < Hqk) {
             if (L.qk_norm) {
+                const bool is_q = h < L.n_q_heads;
+                double ss = 0;
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) ss += (double)y[i] * (double)y[i];
                 ss = wave_sum(ss);
                 const float ri = 1.0f / sqrtf((float)(ss / (double)hd) + L.eps);
 #pragma unroll
-                for (int k = 0; k < MAX_EPL; ++k) {
-                    const int e = lane + 64 * k;
-                    if (e < hd) y[k] = g[e] * ri * y[k];
+                for (int i = 0; i < EPL; ++i) y[i] = (is_q ? gq[i] : gk[i]) * ri * y[i];
+            }
+            if (rot > 0) {
+                float pv[EPL];
+                rope_partner<EPL>(y, pv, lane, half);
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) {
+                    const int e = e0 + i;
+                    if (e >= rot) continue;
+                    const float2 cs = cur.cs[i];
+                    y[i] = e < half ? y[i] * cs.x - pv[i] * cs.y : pv[i] * cs.y + y[i] * cs.x;
                 }
             }
-#pragma unroll
-            for (int k = 0; k < MAX_EPL; ++k) {
-                const int e = lane + 64 * k;
-                if (e < hd) stage[wave][e] = y[k];
-            }
         }
-        __syncthreads();
-        if (active) {
-#pragma unroll
-            for (int k = 0; k < MAX_EPL; ++k) {
-                const int e = lane + 64 * k;
-                if (e >= hd) continue;
-                float o = y[k];
-                if (e < L.rotary_dim) {
-                    const int j = e < half ? e : e - half;
-                    const float2 cs = tab[(long)p * half + j];
-                    const float a = stage[wave][j], b = stage[wave][j + half];
-                    o = (e < half) ? a * cs.x - b * cs.y : a * cs.y + b * cs.x;
-                }
-                store_out<TO>(orow + h * hd + e, o);
-            }
-        }
-        __syncthreads();
+        if (on) st_epl<TO, EPL>(out + (long)t * ld_out + h * hd + e0, y);
+        cur = nxt;
     }
-    // v: copy / cast
-    const int vcol0 = H * hd, vn = L.n_kv_heads * hd;
-    for (int c = threadIdx.x; c < vn; c += NT) store_out<TO>(orow + vcol0 + c, row[vcol0 + c]);
 }
 
-// Backward on the fused d_qkv buffer (q/k columns in place):
+// Backward on the fused d_qkv buffer:
 //   dn = rope^T(g);  d_pre = rmsnorm_bw(dn; x = pre-norm q/k);  dw += dn*ri*x
 // outb (optional): the results go to this bf16 copy of the whole row (q, k
 // and the untouched v columns) instead of back into dqkv.
+template <int EPL>
 __global__ __launch_bounds__(NT) void qkv_bwd_k(QkvLayout L, float *dqkv, long ld,
                                                  const float *qkv, long ld_qkv, const float *wq,
                                                  const float *wk, float *partial,
-                                                 const float2 *tab, int rpb, bf16 *outb,
-                                                 long ldb) {
-    __shared__ float stage[NT / 64][256];
-    __shared__ float red[NT / 64][2][256];
+                                                 const float2 *tab, bf16 *outb, long ldb) {
+    __shared__ float red[2][256];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const int hd = L.head_dim, H = L.n_q_heads + L.n_kv_heads;
-    const int half = L.rotary_dim / 2;
-    float dwq[MAX_EPL], dwk[MAX_EPL];
+    const int hd = L.head_dim, Hqk = L.n_q_heads + L.n_kv_heads;
+    const int Htot = outb ? Hqk + L.n_kv_heads : Hqk;
+    const int half = L.rotary_dim / 2, rot = L.rotary_dim;
+    const long items = (long)L.n_rows * Htot;
+    const long nw = (long)gridDim.x * NW;
+    const int e0 = EPL * lane;
+    const bool on = e0 < hd;
+    float gq[EPL], gk[EPL], dwq[EPL], dwk[EPL];
+    ld_epl<EPL>(wq + e0, gq, on && L.qk_norm);
+    ld_epl<EPL>(wk + e0, gk, on && L.qk_norm);
 #pragma unroll
-    for (int k = 0; k < MAX_EPL; ++k) dwq[k] = dwk[k] = 0.f;
-    const int r0 = blockIdx.x * rpb, r1 = min(L.n_rows, r0 + rpb);
-    const int iters = (H + 3) / 4;
-    for (int t = r0; t < r1; ++t) {
-        const int p = t % L.seq_len;
-        float *drow = dqkv + (long)t * ld;
-        const float *xrow = qkv + (long)t * ld_qkv;
-        for (int it = 0; it < iters; ++it) {
-            const int h = it * 4 + wave;
-            const bool active = h < H;
-            float gv[MAX_EPL];
-            if (active) {
+    for (int i = 0; i < EPL; ++i) dwq[i] = dwk[i] = 0.f;
+    auto fetch = [&](long it, HeadItem<EPL> &d) {
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        const bool qk = h < Hqk;
+        load_item<EPL>(d, dqkv + (long)t * ld + h * hd + e0,
+                       (qk && L.qk_norm) ? qkv + (long)t * ld_qkv + h * hd + e0 : nullptr,
+                       tab + (long)(t % L.seq_len) * half, e0, rot, half, on, qk);
+    };
+    long it = (long)blockIdx.x * NW + wave;
+    HeadItem<EPL> cur;
+    if (it < items) fetch(it, cur);
+    for (; it < items; it += nw) {
+        HeadItem<EPL> nxt;
+        if (it + nw < items) fetch(it + nw, nxt);
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        float gv[EPL];
 #pragma unroll
-                for (int k = 0; k < MAX_EPL; ++k) {
-                    const int e = lane + 64 * k;
-                    gv[k] = e < hd ? drow[h * hd + e] : 0.f;
-                    if (e < hd) stage[wave][e] = gv[k];
+        for (int i = 0; i < EPL; ++i) gv[i] = cur.v[i];
+        if (h < Hqk) {
+            const bool is_q = h < L.n_q_heads;
+            if (rot > 0) {
+                float pv[EPL];
+                rope_partner<EPL>(gv, pv, lane, half);
+#pragma unroll
+                for (int i = 0; i < EPL; ++i) {
+                    const int e = e0 + i;
+                    if (e >= rot) continue;
+                    const float2 cs = cur.cs[i];
+                    gv[i] = e < half ? cs.x * gv[i] + cs.y * pv[i] : -cs.y * pv[i] + cs.x * gv[i];
                 }
             }
-            __syncthreads();
-            if (active) {
-                const bool is_q = h < L.n_q_heads;
-                const float *g = is_q ? wq : wk;
-                float dn[MAX_EPL], xv[MAX_EPL];
+            if (L.qk_norm) {
                 double ss = 0, A = 0;
 #pragma unroll
-                for (int k = 0; k < MAX_EPL; ++k) {
-                    const int e = lane + 64 * k;
-                    dn[k] = gv[k];
-                    xv[k] = 0.f;
-                    if (e >= hd) continue;
-                    if (e < L.rotary_dim) {
-                        const int j = e < half ? e : e - half;
-                        const float2 cs = tab[(long)p * half + j];
-                        const float a = stage[wave][j], b = stage[wave][j + half];
-                        dn[k] = (e < half) ? cs.x * a + cs.y * b : -cs.y * a + cs.x * b;
-                    }
-                    if (L.qk_norm) {
-                        xv[k] = xrow[h * hd + e];
-                        ss += (double)xv[k] * (double)xv[k];
-                        A += (double)dn[k] * (double)g[e] * (double)xv[k];
-                    }
+                for (int i = 0; i < EPL; ++i) {
+                    const float gw = is_q ? gq[i] : gk[i];
+                    ss += (double)cur.x[i] * (double)cur.x[i];
+                    A += (double)gv[i] * (double)gw * (double)cur.x[i];
                 }
-                if (L.qk_norm) {
-                    ss = wave_sum(ss);
-                    A = wave_sum(A);
-                    const float ri = 1.0f / sqrtf((float)(ss / (double)hd) + L.eps);
-                    const float ri3_over_D = ri * ri * ri / (float)hd;
-                    const float A_f = (float)A;
+                ss = wave_sum(ss);
+                A = wave_sum(A);
+                const float ri = 1.0f / sqrtf((float)(ss / (double)hd) + L.eps);
+                const float ri3_over_D = ri * ri * ri / (float)hd;
+                const float A_f = (float)A;
 #pragma unroll
-                    for (int k = 0; k < MAX_EPL; ++k) {
-                        const int e = lane + 64 * k;
-                        if (e >= hd) continue;
-                        const float o = ri * g[e] * dn[k] - ri3_over_D * xv[k] * A_f;
-                        const float dwv = dn[k] * ri * xv[k];
-                        if (is_q) dwq[k] += dwv; else dwk[k] += dwv;
-                        if (outb) outb[(long)t * ldb + h * hd + e] = (bf16)o;
-                        else drow[h * hd + e] = o;
-                    }
-                } else {
-#pragma unroll
-                    for (int k = 0; k < MAX_EPL; ++k) {
-                        const int e = lane + 64 * k;
-                        if (e >= hd) continue;
-                        if (outb) outb[(long)t * ldb + h * hd + e] = (bf16)dn[k];
-                        else drow[h * hd + e] = dn[k];
-                    }
+                for (int i = 0; i < EPL; ++i) {
+                    const float gw = is_q ? gq[i] : gk[i];
+                    const float o = ri * gw * gv[i] - ri3_over_D * cur.x[i] * A_f;
+                    const float dwv = gv[i] * ri * cur.x[i];
+                    if (is_q) dwq[i] += dwv; else dwk[i] += dwv;
+                    gv[i] = o;
                 }
             }
-            __syncthreads();
         }
-        if (outb) {
-            const int vcol0 = H * hd, vn = L.n_kv_heads * hd;
-            for (int c = threadIdx.x; c < vn; c += NT)
-                outb[(long)t * ldb + vcol0 + c] = (bf16)drow[vcol0 + c];
+        if (on) {
+            if (outb) st_epl<bf16, EPL>(outb + (long)t * ldb + h * hd + e0, gv);
+            else if (h < Hqk) st_epl<float, EPL>(dqkv + (long)t * ld + h * hd + e0, gv);
         }
+        cur = nxt;
     }
-    // combine the 4 waves' gain partials, fixed order
+    // combine the waves' gain partials in a fixed order
+    for (int wv = 0; wv < NW; ++wv) {
+        if (wave == wv && on) {
 #pragma unroll
-    for (int k = 0; k < MAX_EPL; ++k) {
-        const int e = lane + 64 * k;
-        if (e < hd) {
-            red[wave][0][e] = dwq[k];
-            red[wave][1][e] = dwk[k];
+            for (int i = 0; i < EPL; ++i) {
+                red[0][e0 + i] = wv ? red[0][e0 + i] + dwq[i] : dwq[i];
+                red[1][e0 + i] = wv ? red[1][e0 + i] + dwk[i] : dwk[i];
+            }
         }
+        __syncthreads();
     }
-    __syncthreads();
-    for (int c = threadIdx.x; c < 2 * hd; c += NT) {
-        const int which = c / hd, e = c % hd;
-        float s = 0.f;
-#pragma unroll
-        for (int wv = 0; wv < NT / 64; ++wv) s += red[wv][which][e];
-        partial[(long)blockIdx.x * 2 * hd + c] = s;
-    }
+    for (int c = threadIdx.x; c < 2 * hd; c += NT)
+        partial[(long)blockIdx.x * 2 * hd + c] = red[c / hd][c % hd];
 }
 
-inline int qkv_blocks(int rows) { return rows < 512 ? rows : 512; }
+constexpr int kRmsMaxBlocks = 512, kQkvMaxBlocks = 512;
+
+inline int rms_grid(int rows) { return std::max(1, std::min(kRmsMaxBlocks, (rows + NW - 1) / NW)); }
+
+inline long qkv_items(const QkvLayout &L, bool with_v) {
+    return (long)L.n_rows * (L.n_q_heads + L.n_kv_heads + (with_v ? L.n_kv_heads : 0));
+}
+inline int qkv_grid(long items, int cap) {
+    return (int)std::max<long>(1, std::min<long>(cap, (items + 4 * NW - 1) / (4 * NW)));
+}
+
+template <class F>
+hipError_t by_c4(int dim, F &&f) {
+    if (dim <= 256) return f(std::integral_constant<int, 1>{});
+    if (dim <= 512) return f(std::integral_constant<int, 2>{});
+    if (dim <= 1024) return f(std::integral_constant<int, 4>{});
+    if (dim <= 2048) return f(std::integral_constant<int, 8>{});
+    return f(std::integral_constant<int, 16>{});
+}
+
+template <class F>
+hipError_t by_epl(int hd, F &&f) {
+    if (hd <= 64) return f(std::integral_constant<int, 1>{});
+    if (hd <= 128) return f(std::integral_constant<int, 2>{});
+    return f(std::integral_constant<int, 4>{});
+}
+
+inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
 
-size_t rmsnorm_partial_floats(int rows, int dim) { return (size_t)rms_blocks(rows) * dim; }
+size_t rmsnorm_partial_floats(int rows, int dim) { return (size_t)rms_grid(rows) * dim; }
 
 hipError_t rmsnorm_forward(const float *x, const float *w, void *y, DType ydt, int rows, int dim,
                            float eps, int gemma_quirk, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
-    if (ydt == DType::BF16)
-        hipLaunchKernelGGL(rmsnorm_fwd_k<bf16>, dim3(rows), dim3(NT), 0, st, x, w, (bf16 *)y, dim,
-                           eps, gemma_quirk);
-    else
-        hipLaunchKernelGGL(rmsnorm_fwd_k<float>, dim3(rows), dim3(NT), 0, st, x, w, (float *)y, dim,
-                           eps, gemma_quirk);
-    return hipGetLastError();
+    if (dim <= 0 || dim > 4096 || dim % 4 || !al16(x) || !al16(w) || ((uintptr_t)y & 7u))
+        return hipErrorInvalidValue;
+    const int grid = std::max(1, std::min(4096, (rows + NW - 1) / NW));
+    return by_c4(dim, [&](auto c4) {
+        constexpr int C4 = decltype(c4)::value;
+        if (ydt == DType::BF16)
+            hipLaunchKernelGGL((rmsnorm_fwd_k<bf16, C4>), dim3(grid), dim3(NT), 0, st, x, w,
+                               (bf16 *)y, rows, dim, eps, gemma_quirk);
+        else
+            hipLaunchKernelGGL((rmsnorm_fwd_k<float, C4>), dim3(grid), dim3(NT), 0, st, x, w,
+                               (float *)y, rows, dim, eps, gemma_quirk);
+        return hipGetLastError();
+    });
 }
 
 hipError_t rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
                             bf16 *dxb, const float *residual, float *dw, float *partial, int rows,
                             int dim, float eps, int gemma_quirk, hipStream_t st) {
     if (rows <= 0) return hipSuccess;
-    if (dim > NT * MAX_CPT) return hipErrorInvalidValue;
-    const int nb = rms_blocks(rows);
-    const int rpb = (rows + nb - 1) / nb;
-    const int nblocks = (rows + rpb - 1) / rpb;
-    hipLaunchKernelGGL(rmsnorm_bwd_k, dim3(nblocks), dim3(NT), 0, st, dy, x, w, dx, dxb, residual,
-                       partial, rows, dim, eps, gemma_quirk, rpb);
+    if (dim <= 0 || dim > 4096 || dim % 4 || !al16(dy) || !al16(x) || !al16(w) || !al16(dx) ||
+        ((uintptr_t)dxb & 7u) || !al16(residual))
+        return hipErrorInvalidValue;
+    const int grid = rms_grid(rows);
+    hipError_t e = by_c4(dim, [&](auto c4) {
+        constexpr int C4 = decltype(c4)::value;
+        hipLaunchKernelGGL((rmsnorm_bwd_k<C4>), dim3(grid), dim3(NT), 0, st, dy, x, w, dx, dxb,
+                           residual, partial, rows, dim, eps, gemma_quirk);
+        return hipGetLastError();
+    });
+    if (e != hipSuccess) return e;
     if (dw)
         hipLaunchKernelGGL(colsum_k, dim3(ceil_div(dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
-                           (const float *)partial, nblocks, (long)dim, dim, dw);
+                           (const float *)partial, grid, (long)dim, dim, dw);
     return hipGetLastError();
 }
 
@@ -414,21 +558,31 @@ hipError_t qk_rope(const float *q_in, long ldq_in, float *q_out, long ldq_out, c
     return hipGetLastError();
 }
 
-size_t qkv_partial_floats(const QkvLayout &L) { return (size_t)qkv_blocks(L.n_rows) * 2 * L.head_dim; }
+size_t qkv_partial_floats(const QkvLayout &L) { return (size_t)kQkvMaxBlocks * 2 * L.head_dim; }
+
+static bool qkv_shape_ok(const QkvLayout &L, long ld_in, long ld_out) {
+    return L.head_dim > 0 && L.head_dim <= 256 && L.head_dim % 4 == 0 && L.rotary_dim <= L.head_dim &&
+           (L.rotary_dim & 1) == 0 && L.seq_len > 0 && ld_in % 4 == 0 && ld_out % 4 == 0;
+}
 
 hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv,
                                const float *wq, const float *wk, void *out, long ld_out,
                                DType out_dt, const float2 *rope_tab, hipStream_t st) {
     if (L.n_rows <= 0) return hipSuccess;
-    if (L.head_dim > 64 * MAX_EPL || L.rotary_dim > L.head_dim || (L.rotary_dim & 1))
+    if (!qkv_shape_ok(L, ld_qkv, ld_out) || !al16(qkv) || ((uintptr_t)out & 7u) ||
+        (L.qk_norm && (!al16(wq) || !al16(wk))))
         return hipErrorInvalidValue;
-    if (out_dt == DType::BF16)
-        hipLaunchKernelGGL(qkv_fwd_k<bf16>, dim3(L.n_rows), dim3(NT), 0, st, L, qkv, ld_qkv, wq, wk,
-                           (bf16 *)out, ld_out, rope_tab);
-    else
-        hipLaunchKernelGGL(qkv_fwd_k<float>, dim3(L.n_rows), dim3(NT), 0, st, L, qkv, ld_qkv, wq,
-                           wk, (float *)out, ld_out, rope_tab);
-    return hipGetLastError();
+    const int grid = qkv_grid(qkv_items(L, true), 2048);
+    return by_epl(L.head_dim, [&](auto epl) {
+        constexpr int EPL = decltype(epl)::value;
+        if (out_dt == DType::BF16)
+            hipLaunchKernelGGL((qkv_fwd_k<bf16, EPL>), dim3(grid), dim3(NT), 0, st, L, qkv, ld_qkv,
+                               wq, wk, (bf16 *)out, ld_out, rope_tab);
+        else
+            hipLaunchKernelGGL((qkv_fwd_k<float, EPL>), dim3(grid), dim3(NT), 0, st, L, qkv, ld_qkv,
+                               wq, wk, (float *)out, ld_out, rope_tab);
+        return hipGetLastError();
+    });
 }
 
 hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const float *qkv,
@@ -436,18 +590,22 @@ hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const 
                                 float *dwk, float *partial, const float2 *rope_tab,
                                 bf16 *outb, long ldb, hipStream_t st) {
     if (L.n_rows <= 0) return hipSuccess;
-    if (L.head_dim > 64 * MAX_EPL || L.rotary_dim > L.head_dim || (L.rotary_dim & 1))
+    if (!qkv_shape_ok(L, ld, ld_qkv) || (outb && ldb % 4) || !al16(dqkv) || !al16(qkv) ||
+        ((uintptr_t)outb & 7u) || (L.qk_norm && (!al16(wq) || !al16(wk))))
         return hipErrorInvalidValue;
-    const int nb = qkv_blocks(L.n_rows);
-    const int rpb = (L.n_rows + nb - 1) / nb;
-    const int nblocks = (L.n_rows + rpb - 1) / rpb;
-    hipLaunchKernelGGL(qkv_bwd_k, dim3(nblocks), dim3(NT), 0, st, L, dqkv, ld, qkv, ld_qkv, wq, wk,
-                       partial, rope_tab, rpb, outb, ldb);
+    const int grid = qkv_grid(qkv_items(L, outb != nullptr), kQkvMaxBlocks);
+    hipError_t e = by_epl(L.head_dim, [&](auto epl) {
+        constexpr int EPL = decltype(epl)::value;
+        hipLaunchKernelGGL((qkv_bwd_k<EPL>), dim3(grid), dim3(NT), 0, st, L, dqkv, ld, qkv, ld_qkv,
+                           wq, wk, partial, rope_tab, outb, ldb);
+        return hipGetLastError();
+    });
+    if (e != hipSuccess) return e;
     if (L.qk_norm && dwq && dwk) {
         hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
-                           (const float *)partial, nblocks, (long)2 * L.head_dim, L.head_dim, dwq);
+                           (const float *)partial, grid, (long)2 * L.head_dim, L.head_dim, dwq);
         hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
-                           (const float *)partial + L.head_dim, nblocks, (long)2 * L.head_dim,
+                           (const float *)partial + L.head_dim, grid, (long)2 * L.head_dim,
                            L.head_dim, dwk);
     }
     return hipGetLastError();

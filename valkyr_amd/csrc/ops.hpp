@@ -147,6 +147,12 @@ hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *do
                    float *d, bf16 *dout_bf16, long lddo16, hipStream_t st);
 hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
+// Fused bf16 backward: dK/dV and bf16 dS into ds_ws (fa_bw_ws_bytes), then
+// dQ = dS K.  Requires fa_bw_fused_ok(s) (bf16 head_dim 64/128, n_q and n_kv
+// multiples of 64, self-attention when causal).
+bool fa_bw_fused_ok(const AttnShape &s);
+size_t fa_bw_ws_bytes(const AttnShape &s);
+hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipStream_t st);
 
 // ── cut cross-entropy (k_cce.hip) ────────────────────────────────────
 struct CceShape {

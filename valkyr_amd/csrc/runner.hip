@@ -89,6 +89,7 @@ struct vkh_runner {
     bool shadow_dirty = true;
     bf16 *fn_outb = nullptr, *d_gub = nullptr, *d_midb = nullptr, *d_qkvb = nullptr,
          *dxb[2] = {nullptr, nullptr};
+    bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward
     GemmWs gws{nullptr, 0};
     std::vector<Acts> acts;
     float *x_emb = nullptr, *fn_out = nullptr, *ce_lse = nullptr, *loss_row = nullptr,
@@ -316,6 +317,8 @@ struct vkh_runner {
             VKH_TRY(alloc(d_qkvb, (size_t)T * qkvd));
             VKH_TRY(alloc(dxb[0], (size_t)T * D));
             VKH_TRY(alloc(dxb[1], (size_t)T * D));
+            if (adt == DType::BF16 && fa_bw_fused_ok(attn_shape()))
+                VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape()) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
             size_t wsb = 0;
             auto need = [&](int m, int n, int k) { wsb = std::max(wsb, g16_ws_bytes_for(m, n, k)); };
@@ -666,8 +669,12 @@ struct vkh_runner {
         ap.dk = d_qkv + qd; ap.lddk = qkvd;
         ap.dv = d_qkv + qd + kvd; ap.lddv = qkvd;
         ap.dt = adt;
-        VKH_HIP(fa_bw_dkv(as, ap, cur));
-        VKH_HIP(fa_bw_dq(as, ap, cur));
+        if (attn_ds) {
+            VKH_HIP(fa_bw_fused(as, ap, attn_ds, cur));
+        } else {
+            VKH_HIP(fa_bw_dkv(as, ap, cur));
+            VKH_HIP(fa_bw_dq(as, ap, cur));
+        }
         // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
         const QkvLayout ql = qkv_layout();
         VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,

@@ -55,6 +55,18 @@ def fa_bw_dkv(p, q, k, v, dout, lse, d, dk, dv, stream=None):
                               _p(dv), _s(stream)))
 
 
+def fa_backward_workspace_bytes(p):
+    return lib().vkh_fa_backward_workspace_bytes(C.byref(p))
+
+
+def fa_backward(p, q, k, v, dout, lse, d, dq, dk, dv, workspace=None, stream=None):
+    """dK, dV and dQ of one attention call (after fa_bw_d); bf16 shapes take
+    the fused dS path (workspace of fa_backward_workspace_bytes(p) bytes, or
+    None to allocate per call)."""
+    check(lib().vkh_fa_backward(C.byref(p), _p(q), _p(k), _p(v), _p(dout), _p(lse), _p(d),
+                                _p(dq), _p(dk), _p(dv), _p(workspace), _s(stream)))
+
+
 def matmul_nt(x, w, y, M, N, K, precision=PRECISION_FP32, stream=None):
     """matmul_nt_v2.comp: y[M,N] = x[M,K] w[N,K]^T."""
     check(lib().vkh_matmul_nt(_p(x), _p(w), _p(y), M, N, K, precision, _s(stream)))
