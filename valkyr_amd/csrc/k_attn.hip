@@ -489,7 +489,8 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dq_bf16_k(AttnShape s, AttnPtrs 
 // (dO^T for dV, Q^T for dK) are read from the same row-major tiles with the
 // gfx950 transposing LDS load (ds_read_b64_tr_b16), so no transposed copies
 // are staged.  dS = P (dP - D) is written once as bf16 (exactly the values
-// the dK MFMAs consume) to a [batch, head, n_q, n_kv] workspace, and dQ is
+// the dK MFMAs consume) to a [batch, head, n_kv, n_q] workspace (dS^T: each
+// lane's 4 consecutive queries of one key are one 8-byte store), and dQ is
 // then the plain product dS K, computed by the shared GEMM tile routine with
 // the causal K limit; S and dP are not recomputed for dQ.
 //
@@ -517,9 +518,10 @@ VKH_DEV bf16x8 frag_tr(const bf16 *tile, int c0, int k0, int g, int l16) {
     return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
 }
 
-template <int HD>
+template <int HD, int BM>
 __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, bf16 *dsw) {
-    constexpr int BN = 128, BM = 64, DS = HD / 32, DSUB = HD / 16;
+    constexpr int BN = 128, DS = HD / 32, DSUB = HD / 16;
+    constexpr int QS = BM / 16, QST = BM / 32;  // 16-row score tiles, 32-row contraction steps
     constexpr int P = HD + 16;      // LDS pitch (elements): conflict-free b128 and tr reads
     constexpr int CH = HD / 8;      // 16-byte chunks per row
     constexpr int PER = BM * CH / NT;
@@ -599,31 +601,31 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
         const int buf = it & 1;
         if (it + 1 < niter) gload(it + 1);
         const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
-        bf16 *dsr = dsw ? dsw + (((long)b * s.n_heads + h) * s.n_q + q0) * s.n_kv : nullptr;
+        // dS^T rows of this lane's two keys: dsr[k * n_q + q]; 4 consecutive q per store
+        bf16 *dsr = dsw ? dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv +
+                              (long)(kw0 + c16) * s.n_q + q0 + 4 * g
+                        : nullptr;
+        const long ds_ks = 16L * s.n_q;
+        const bool keys_ok = kw0 + 32 <= s.n_kv;
         if (s.causal && kw0 > q0 + BM - 1 + off) {
             // every key of this wave is masked for the tile: dS is zero
             if (dsr) {
 #pragma unroll
-                for (int qs = 0; qs < 4; ++qs)
+                for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                    for (int r = 0; r < 4; ++r) {
-                        const int ql = 16 * qs + 4 * g + r;
-#pragma unroll
-                        for (int ks = 0; ks < 2; ++ks) {
-                            const int ka = kw0 + 16 * ks + c16;
-                            if (q0 + ql < s.n_q && ka < s.n_kv) dsr[(long)ql * s.n_kv + ka] = (bf16)0.f;
-                        }
-                    }
+                    for (int qs = 0; qs < QS; ++qs)
+                        if (keys_ok || kw0 + 16 * ks + c16 < s.n_kv)
+                            *reinterpret_cast<bf16x4 *>(dsr + ks * ds_ks + 16 * qs) = bf16x4{};
             }
         } else {
             const bf16 *Qb = &Qs[buf][0][0], *Ob = &Os[buf][0][0];
-            f32x4 sc[4][2], dp[4][2];
+            f32x4 sc[QS][2], dp[QS][2];
 #pragma unroll
-            for (int qs = 0; qs < 4; ++qs) sc[qs][0] = sc[qs][1] = dp[qs][0] = dp[qs][1] = f32x4{0, 0, 0, 0};
+            for (int qs = 0; qs < QS; ++qs) sc[qs][0] = sc[qs][1] = dp[qs][0] = dp[qs][1] = f32x4{0, 0, 0, 0};
 #pragma unroll
             for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
-                for (int qs = 0; qs < 4; ++qs) {
+                for (int qs = 0; qs < QS; ++qs) {
                     const bf16x8 qa = ld_frag(Qb + (16 * qs + c16) * P + 32 * ds + 8 * g);
                     const bf16x8 oa = ld_frag(Ob + (16 * qs + c16) * P + 32 * ds + 8 * g);
                     sc[qs][0] = mfma16x16x32(qa, kf[0][ds], sc[qs][0]);
@@ -631,26 +633,43 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
                     dp[qs][0] = mfma16x16x32(oa, vf[0][ds], dp[qs][0]);
                     dp[qs][1] = mfma16x16x32(oa, vf[1][ds], dp[qs][1]);
                 }
+            // P = exp2(S c2 - lse2); a fully masked row (lse = -inf) gets +inf -> P = 0.
+            // Only tiles that touch the causal diagonal or an edge need per-element masks.
+            const bool edge = (s.causal && kw0 + 31 > q0 + off) || !keys_ok;
 #pragma unroll
-            for (int qs = 0; qs < 4; ++qs)
+            for (int qs = 0; qs < QS; ++qs) {
+                const float4 l4 = *reinterpret_cast<const float4 *>(&lse_s[buf][16 * qs + 4 * g]);
+                const float4 d4 = *reinterpret_cast<const float4 *>(&d_s[buf][16 * qs + 4 * g]);
+                const float lqs[4] = {l4.x, l4.y, l4.z, l4.w}, dqs[4] = {d4.x, d4.y, d4.z, d4.w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const int ql = 16 * qs + 4 * g + r;
-                    const int qa = q0 + ql;
-                    const float lq = lse_s[buf][ql], dq = d_s[buf][ql];
+                    const float lq = lqs[r] == -INFINITY ? INFINITY : lqs[r];
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        const int ka = kw0 + 16 * ks + c16;
-                        float pv = (lq == -INFINITY) ? 0.f : exp2f(sc[qs][ks][r] * c2 - lq);
-                        if (qa >= s.n_q || ka >= s.n_kv || (s.causal && ka > qa + off)) pv = 0.f;
+                        float pv = __builtin_amdgcn_exp2f(sc[qs][ks][r] * c2 - lq);
+                        if (edge) {
+                            const int qa = q0 + 16 * qs + 4 * g + r, ka = kw0 + 16 * ks + c16;
+                            if (ka >= s.n_kv || (s.causal && ka > qa + off)) pv = 0.f;
+                        }
                         sc[qs][ks][r] = pv;
-                        const float dsv = pv * (dp[qs][ks][r] - dq);
-                        dp[qs][ks][r] = dsv;
-                        if (dsr && qa < s.n_q && ka < s.n_kv) dsr[(long)ql * s.n_kv + ka] = (bf16)dsv;
+                        dp[qs][ks][r] = pv * (dp[qs][ks][r] - dqs[r]);
                     }
                 }
+            }
+            if (dsr) {
 #pragma unroll
-            for (int qst = 0; qst < 2; ++qst) {
+                for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                    for (int qs = 0; qs < QS; ++qs) {
+                        bf16x4 v;
+                        v[0] = (bf16)dp[qs][ks][0]; v[1] = (bf16)dp[qs][ks][1];
+                        v[2] = (bf16)dp[qs][ks][2]; v[3] = (bf16)dp[qs][ks][3];
+                        if (keys_ok || kw0 + 16 * ks + c16 < s.n_kv)
+                            *reinterpret_cast<bf16x4 *>(dsr + ks * ds_ks + 16 * qs) = v;
+                    }
+            }
+#pragma unroll
+            for (int qst = 0; qst < QST; ++qst) {
                 const bf16x8 pb0 = frag_acc(sc[2 * qst][0], sc[2 * qst + 1][0]);
                 const bf16x8 pb1 = frag_acc(sc[2 * qst][1], sc[2 * qst + 1][1]);
                 const bf16x8 sb0 = frag_acc(dp[2 * qst][0], dp[2 * qst + 1][0]);
@@ -667,6 +686,12 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
             }
         }
         if (it + 1 < niter) lstore(buf ^ 1);
+        // Pin the loop-carried dK/dV accumulators to AGPRs (the register
+        // file the MFMAs accumulate in); otherwise the compiler carries them
+        // in VGPRs and copies all of them in and out on every tile.
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i)
+            asm volatile("" : "+a"(dvt[i][0]), "+a"(dvt[i][1]), "+a"(dkt[i][0]), "+a"(dkt[i][1]));
         __syncthreads();
     }
 #pragma unroll
@@ -688,7 +713,7 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
 
 // dQ[q, :] = inv_sqrt_dim * sum_{k visible} dS[q, k] K[k, :]: one 128 x HD
 // output tile per (q tile, head, sequence) on the GEMM tile routine (A = dS
-// rows, K-major; B = K rows, MN-major).
+// from its transposed [k][q] store, B = K rows; both MN-major).
 template <int HD>
 __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, const bf16 *dsw) {
     using Cfg = Tile16<128, HD, 2, 2>;
@@ -700,7 +725,8 @@ __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, c
     const int q0 = qt * 128;
     const int off = s.n_kv - s.n_q;
     const int kend = s.causal ? min(s.n_kv, q0 + 128 + off) : s.n_kv;
-    const Op16 a{dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv, s.n_kv,
+    // A(q, k) = dS^T[k][q]: MN-major
+    const Op16 a{dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv, s.n_q,
                  (unsigned)((size_t)s.n_q * s.n_kv * 2)};
     const Op16 bk{(const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD, p.ldk,
                   (unsigned)(((size_t)(s.n_kv - 1) * p.ldk + HD) * 2)};
@@ -709,7 +735,7 @@ __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, c
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    gemm16_tile<Cfg, Lay::K, Lay::MN, TM, TN>(a, bk, q0, 0, s.n_q, HD, 0, (kend + 63) / 64, kend,
+    gemm16_tile<Cfg, Lay::MN, Lay::MN, TM, TN>(a, bk, q0, 0, s.n_q, HD, 0, (kend + 63) / 64, kend,
                                               acc, smem);
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int row0 = q0 + (wave / 2) * 64, col0 = (wave % 2) * (HD / 2);
@@ -921,6 +947,10 @@ hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     return hipGetLastError();
 }
 
+#ifndef FA_BM
+#define FA_BM 64
+#endif
+
 bool fa_bw_fused_ok(const AttnShape &s) {
     return bf16_ok(s) && s.n_q % 64 == 0 && s.n_kv % 64 == 0 && (!s.causal || s.n_q == s.n_kv) &&
            (size_t)s.n_q * s.n_kv * 2 < (1ull << 31) && s.n_kv_heads > 0 &&
@@ -937,10 +967,10 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipSt
     dim3 gkv((s.n_kv + 127) / 128, s.n_kv_heads, s.n_batch);
     dim3 gq((s.n_q + 127) / 128, s.n_heads, s.n_batch);
     if (s.head_dim == 128) {
-        hipLaunchKernelGGL(fa_bwd_dkv2_k<128>, gkv, dim3(NT), 0, st, s, p, ds_ws);
+        hipLaunchKernelGGL((fa_bwd_dkv2_k<128, FA_BM>), gkv, dim3(NT), 0, st, s, p, ds_ws);
         hipLaunchKernelGGL(fa_dq_gemm_k<128>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);
     } else {
-        hipLaunchKernelGGL(fa_bwd_dkv2_k<64>, gkv, dim3(NT), 0, st, s, p, ds_ws);
+        hipLaunchKernelGGL((fa_bwd_dkv2_k<64, FA_BM>), gkv, dim3(NT), 0, st, s, p, ds_ws);
         hipLaunchKernelGGL(fa_dq_gemm_k<64>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);
     }
     return hipGetLastError();
