@@ -57,6 +57,27 @@ VKH_DEV float wave_max(float v) {
     return v;
 }
 
+// Reductions over the 16 lanes of a DPP row (lanes 16 g .. 16 g + 15), the
+// lanes that hold one row of an MFMA 16x16 accumulator: quad swaps, then
+// the half-row and row mirrors.  Every lane ends with the row's result.
+template <int CTRL>
+VKH_DEV float dpp_f(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL,
+                                                                 0xf, 0xf, false));
+}
+VKH_DEV float row16_max(float v) {
+    v = fmaxf(v, dpp_f<0xB1>(v));   // quad_perm [1,0,3,2]
+    v = fmaxf(v, dpp_f<0x4E>(v));   // quad_perm [2,3,0,1]
+    v = fmaxf(v, dpp_f<0x141>(v));  // row_half_mirror
+    return fmaxf(v, dpp_f<0x140>(v));  // row_mirror
+}
+VKH_DEV float row16_sum(float v) {
+    v += dpp_f<0xB1>(v);
+    v += dpp_f<0x4E>(v);
+    v += dpp_f<0x141>(v);
+    return v + dpp_f<0x140>(v);
+}
+
 // Block-wide sum for blockDim.x == NT (multiple of 64). `sh` needs NT/64 floats.
 template <int NT>
 VKH_DEV float block_sum(float v, float *sh) {

@@ -18,12 +18,14 @@
 //     position c ^ (r & 7), so the 16-byte fragment reads of 8 consecutive
 //     lanes (8 consecutive rows, same logical chunk) and the staging writes
 //     (8 chunks of one row) each touch all 32 banks exactly once.
-//   * Global -> register -> LDS staging, two LDS buffers, one barrier per
-//     slab: the global loads of slab k+1 (and k+2 with PF = 2) are in
-//     flight while slab k's MFMAs run.  Loads go through buffer resources: out-of-range rows and k are
-//     returned as zero by the hardware range check, so edges need no branches.
-//   * MN-major operands are transposed in registers (8x8 or 4x8 bf16 blocks)
-//     on their way into LDS.
+//   * Global -> LDS by DMA (buffer_load ... lds, see gemm16_tile_dma), two
+//     LDS buffers, one barrier per slab: slab k+1 streams in while slab k's
+//     MFMAs run.  Loads go through buffer resources: out-of-range rows and k
+//     are returned as zero by the hardware range check, so edges need no
+//     branches.  (gemm16_tile is the earlier register-staged form.)
+//   * MN-major operands stay k-row-major in LDS and their MFMA fragments are
+//     read with the transposing LDS load ds_read_b64_tr_b16 (the register-
+//     staged form transposes 8x8 / 4x8 bf16 blocks in registers instead).
 //   * Block ids are regrouped so each XCD (8 on MI355X, round-robin dispatch)
 //     gets a contiguous band of tiles that share operand panels in its L2.
 #pragma once
@@ -203,7 +205,7 @@ VKH_DEV void gemm16_tile(const Op16 &a, const Op16 &b, int m0, int n0, int M, in
     static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
     constexpr int ABYTES = BM * 128, BBYTES = BN * 128, STAGE = ABYTES + BBYTES;
     const int tid = threadIdx.x;
-    const int lane = tid % 64, wave = tid / 64;
+    const int lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
     const __amdgpu_buffer_rsrc_t ra = make_rsrc(a), rb = make_rsrc(b);
     // register staging sets (the second is used only with PF == 2)
@@ -302,6 +304,124 @@ VKH_DEV void gemm16_tile(const Op16 &a, const Op16 &b, int m0, int n0, int M, in
 
 }
 
+// ── DMA staging: global -> LDS without registers ─────────────────────
+//
+// buffer_load_dwordx4 ... lds writes lane l's 16 bytes to M0 + 16 l (the
+// LDS base is wave-uniform), so one wave instruction fills 1 KB of LDS and
+// the layout is chosen through each lane's global address:
+//   * K-major tile (R rows x 64 k): the swizzled rows above; lane l of an
+//     instruction covering rows rb..rb+7 fetches row rb + l/8, logical chunk
+//     (l % 8) ^ ((l / 8) & 7).
+//   * MN-major tile (64 k x R m): stored as its k rows, R m values each, with
+//     16-byte chunk c of row k at position c ^ mn_swz(k); MFMA fragments are
+//     read with ds_read_b64_tr_b16 (transposing), two reads per fragment.
+// The loads are asynchronous: slab k+1 streams into the other LDS buffer
+// while slab k computes, with no staging registers and no ds_write.
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+typedef __attribute__((address_space(3))) bf16x4 lds_bf16x4_t;
+
+// Chunk permutation of MN tile row k (R m values per row).  It is even, so
+// 32-byte pairs stay together, and the rows one half-wave's transposing read
+// touches ({0-3, 8-11} + 4 j) land on disjoint banks: with rows of >= 256 B
+// (a multiple of the 64 x 4 B bank width) the eight rows get eight values;
+// with 128 B rows, even and odd rows already sit in different bank halves
+// and the four rows of each parity get four values.
+template <int R>
+VKH_DEV int mn_swz(int k) {
+    if constexpr (R >= 128) return 2 * ((k & 3) | (((k >> 3) & 1) << 2));
+    else return 2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1));
+}
+
+VKH_DEV void dma16(__amdgpu_buffer_rsrc_t rs, char *lds_wave_base, unsigned voff) {
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)lds_wave_base, 16, voff, 0, 0, 0);
+}
+
+// Issue this wave's share of one slab of an operand tile (R x 64).
+template <Lay L, int R, int NW>
+VKH_DEV void dma_tile(__amdgpu_buffer_rsrc_t rs, const Op16 &o, char *tile, int r0, int rmax, int k0,
+                      int kmax, int wave, int lane) {
+    constexpr int PW = R / 8 / NW;  // 1 KB instructions per wave
+    static_assert(PW >= 1 && PW * NW * 8 == R, "tile / wave mismatch");
+#pragma unroll
+    for (int j = 0; j < PW; ++j) {
+        const int ins = wave * PW + j;
+        char *dst = tile + ins * 1024;
+        unsigned off;
+        if constexpr (L == Lay::K) {
+            const int r = ins * 8 + lane / 8, c = (lane % 8) ^ ((lane / 8) & 7);
+            const int gr = r0 + r, gk = k0 + 8 * c;
+            off = (gr < rmax && gk < kmax) ? (unsigned)(((long)gr * o.ld + gk) * 2) : kOOB;
+        } else {
+            constexpr int CPR = R / 8;        // 16-byte chunks per k row
+        static_assert(R == 64 || R % 128 == 0, "MN tile width");
+            constexpr int RPI = 64 / CPR;     // k rows per instruction
+            const int k = ins * RPI + lane / CPR, pch = lane % CPR;
+            const int c = pch ^ mn_swz<R>(k);
+            const int gk = k0 + k, gm = r0 + 8 * c;
+            off = (gk < kmax && gm < rmax) ? (unsigned)(((long)gk * o.ld + gm) * 2) : kOOB;
+        }
+        dma16(rs, dst, off);
+    }
+}
+
+// Fragment (16 rows of the operand x 32 k at k-step ks) for this lane.
+template <Lay L, int R>
+VKH_DEV bf16x8 frag16(const char *tile, int row16, int ks, int lane) {
+    const int fr = lane % 16, fg = lane / 16;
+    if constexpr (L == Lay::K) {
+        const int r = row16 + fr;
+        return *reinterpret_cast<const bf16x8 *>(tile + r * 128 + ((((ks << 2) + fg) ^ (r & 7)) << 4));
+    } else {
+        // lane (fg, fr) addresses k row 32 ks + 8 fg + fr / 4 (+4), m = row16 + 4 (fr % 4)
+        const int m = row16 + 4 * (fr % 4);
+        const int k_lo = 32 * ks + 8 * fg + fr / 4, k_hi = k_lo + 4;
+        const char *plo = tile + k_lo * (R * 2) + (((m >> 3) ^ mn_swz<R>(k_lo)) << 4) + (m & 7) * 2;
+        const char *phi = tile + k_hi * (R * 2) + (((m >> 3) ^ mn_swz<R>(k_hi)) << 4) + (m & 7) * 2;
+        const bf16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)plo);
+        const bf16x4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4_t *)phi);
+        return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+    }
+}
+
+VKH_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0), exp/lgkm untouched
+
+template <class Cfg, Lay LA, Lay LB, int TM, int TN>
+VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
+                             int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem) {
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::WGM * Cfg::WGN;
+    constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
+    static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
+    constexpr int ABYTES = BM * 128, BBYTES = BN * 128, STAGE = ABYTES + BBYTES;
+    const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a), rb = make_rsrc(b);
+    auto issue = [&](int kt, char *stage) {
+        dma_tile<LA, BM, NW>(ra, a, stage, m0, M, kbase + kt * 64, Kmax, wave, lane);
+        dma_tile<LB, BN, NW>(rb, b, stage + ABYTES, n0, N, kbase + kt * 64, Kmax, wave, lane);
+    };
+    if (nk > 0) issue(0, smem);
+    for (int kt = 0; kt < nk; ++kt) {
+        char *cur = smem + (kt & 1) * STAGE;
+        wait_vm0();
+        __syncthreads();  // slab kt landed for every wave; slab kt-1's buffer is free
+        if (kt + 1 < nk) issue(kt + 1, smem + ((kt + 1) & 1) * STAGE);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+            bf16x8 af[TM], bfr[TN];
+#pragma unroll
+            for (int i = 0; i < TM; ++i) af[i] = frag16<LA, BM>(cur, wm * WM + 16 * i, ks, lane);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) bfr[j] = frag16<LB, BN>(cur + ABYTES, wn * WN + 16 * j, ks, lane);
+#pragma unroll
+            for (int i = 0; i < TM; ++i)
+#pragma unroll
+                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
+        }
+    }
+    __syncthreads();  // the caller may reuse smem
+}
+
 template <class Cfg, Lay LA, Lay LB, class Epi>
 __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, GemmShape s, Epi epi,
                                                             SplitK sk) {
@@ -331,7 +451,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
     const int nk_all = (s.K + 63) / 64;
     const int kt0 = (int)((long)nk_all * split / sk.splits);
     const int nk = (int)((long)nk_all * (split + 1) / sk.splits) - kt0;
-    gemm16_tile<Cfg, LA, LB, TM, TN>(a, b, m0, n0, s.M, s.N, kt0 * 64, nk, s.K, acc, smem);
+    gemm16_tile_dma<Cfg, LA, LB, TM, TN>(a, b, m0, n0, s.M, s.N, kt0 * 64, nk, s.K, acc, smem);
 
     if (sk.splits > 1) {
         f32x4 *own = sk.ws + ((size_t)tile * sk.splits + split) * (BM * BN / 4);

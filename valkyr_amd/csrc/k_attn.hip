@@ -534,7 +534,8 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
     const int kt = s.causal ? nkt - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
     const int kvh = blockIdx.y, b = blockIdx.z;
     const int hpk = s.n_heads / s.n_kv_heads;
-    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // uniform: scalar branches
     const int k0 = kt * BN, kw0 = k0 + wave * 32;
     const int off = s.n_kv - s.n_q;
     const float c2 = s.inv_sqrt_dim * LOG2E;
@@ -639,22 +640,36 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs) {
                 const float4 l4 = *reinterpret_cast<const float4 *>(&lse_s[buf][16 * qs + 4 * g]);
-                const float4 d4 = *reinterpret_cast<const float4 *>(&d_s[buf][16 * qs + 4 * g]);
-                const float lqs[4] = {l4.x, l4.y, l4.z, l4.w}, dqs[4] = {d4.x, d4.y, d4.z, d4.w};
+                const float lqs[4] = {l4.x, l4.y, l4.z, l4.w};
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const float lq = lqs[r] == -INFINITY ? INFINITY : lqs[r];
 #pragma unroll
                     for (int ks = 0; ks < 2; ++ks) {
-                        float pv = __builtin_amdgcn_exp2f(sc[qs][ks][r] * c2 - lq);
-                        if (edge) {
-                            const int qa = q0 + 16 * qs + 4 * g + r, ka = kw0 + 16 * ks + c16;
-                            if (ka >= s.n_kv || (s.causal && ka > qa + off)) pv = 0.f;
-                        }
-                        sc[qs][ks][r] = pv;
-                        dp[qs][ks][r] = pv * (dp[qs][ks][r] - dqs[r]);
+                        sc[qs][ks][r] = __builtin_amdgcn_exp2f(sc[qs][ks][r] * c2 - lq);
                     }
                 }
+            }
+            if (edge) {
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            const int qa = q0 + 16 * qs + 4 * g + r, ka = kw0 + 16 * ks + c16;
+                            if (ka >= s.n_kv || (s.causal && ka > qa + off)) sc[qs][ks][r] = 0.f;
+                        }
+            }
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+                const float4 d4 = *reinterpret_cast<const float4 *>(&d_s[buf][16 * qs + 4 * g]);
+                const float dqs[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        dp[qs][ks][r] = sc[qs][ks][r] * (dp[qs][ks][r] - dqs[r]);
             }
             if (dsr) {
 #pragma unroll
@@ -735,7 +750,7 @@ __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, c
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    gemm16_tile<Cfg, Lay::MN, Lay::MN, TM, TN>(a, bk, q0, 0, s.n_q, HD, 0, (kend + 63) / 64, kend,
+    gemm16_tile_dma<Cfg, Lay::MN, Lay::MN, TM, TN>(a, bk, q0, 0, s.n_q, HD, 0, (kend + 63) / 64, kend,
                                               acc, smem);
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int row0 = q0 + (wave / 2) * 64, col0 = (wave % 2) * (HD / 2);

@@ -67,19 +67,15 @@ struct EpiCceStats {
                         if ((uint32_t)col == t) w.zt[row] = z;
                     }
                 }
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) mx = fmaxf(mx, __shfl_xor(mx, o, 64));
+                mx = row16_max(mx);
                 float se = 0.f;
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     const int col = fp.col0 + 16 * j + c16;
                     if (col < V) se += exp2f((acc[i][j][r] - mx) * LOG2E);
                 }
-#pragma unroll
-                for (int o = 1; o < 16; o <<= 1) {
-                    se += __shfl_xor(se, o, 64);
-                    zs += __shfl_xor(zs, o, 64);
-                }
+                se = row16_sum(se);
+                zs = row16_sum(zs);
                 if (rok && c16 == 0) {
                     const size_t idx = (size_t)row * w.nparts + part;
                     w.pm[idx] = mx;
