@@ -3,11 +3,12 @@
 // (linear_backward_dx_batched.comp) and dW = dy^T x
 // (linear_backward_dw_batched.comp), on the gemm16 kernel.
 //
-// Tile plan (measured on MI355X for the T = 2048-token step shapes):
+// Tile plan (measured on MI355X with DMA staging, T = 2048-token step shapes):
 //   * >= 512 tiles of 256 x 256       -> 256 x 256, 8 waves (vocab-sized GEMMs)
-//   * >= 384 tiles of 128 x 128       -> 128 x 128, 4 waves
-//   * long K (>= 4096), < 256 tiles   -> 128 x 128 split-K (up to 4 ways)
-//   * otherwise                       -> 128 x 64 (twice the tiles of 128 x 128)
+//   * >= 512 tiles of 128 x 128       -> 128 x 128
+//   * K >= 16384 and < 256 such tiles -> 128 x 128 split-K, up to 4 ways (head dh)
+//   * < 384 tiles of 128 x 64, K >= 2048 -> 128 x 64 split-K 2 ways
+//   * otherwise                       -> 128 x 64
 // Operands that break the kernel's layout rules (16-byte alignment, ld and
 // the contiguous extent multiples of 8, < 2 GiB) take the generic MFMA GEMM.
 #include <algorithm>
@@ -29,18 +30,25 @@ struct Plan {
     int splits;
 };
 
+size_t ws_for(const Plan &p, const GemmShape &s) {
+    if (p.splits <= 1) return 0;
+    return p.tile == Pick::T128 ? gemm16_ws_bytes<T128>(s, p.splits)
+                                : gemm16_ws_bytes<T128x64>(s, p.splits);
+}
+
 Plan plan(const GemmShape &s, size_t ws_bytes) {
     auto tiles = [&](int bm, int bn) { return (long)ceil_div(s.M, bm) * (long)ceil_div(s.N, bn); };
     if (tiles(256, 256) >= 512) return {Pick::Big, 1};
-    const long t128 = tiles(128, 128);
-    if (t128 >= 384) return {Pick::T128, 1};
+    const long t128 = tiles(128, 128), t64 = tiles(128, 64);
+    if (t128 >= 512) return {Pick::T128, 1};
     const int nk = (s.K + 63) / 64;
-    if (s.K >= 4096 && t128 < 256) {
-        int sp = (int)std::min<long>(4, std::max<long>(1, 512 / t128));
-        while (sp > 1 && (nk / sp < 8 || gemm16_ws_bytes<T128>(s, sp) > ws_bytes)) --sp;
-        if (sp > 1) return {Pick::T128, sp};
-    }
-    return {Pick::T128x64, 1};
+    Plan p{Pick::T128x64, 1};
+    if (s.K >= 16384 && t128 < 256)
+        p = Plan{Pick::T128, (int)std::min<long>(4, std::max<long>(1, 512 / t128))};
+    else if (t64 < 384 && s.K >= 2048)
+        p = Plan{Pick::T128x64, 2};
+    while (p.splits > 1 && (nk / p.splits < 8 || ws_for(p, s) > ws_bytes)) --p.splits;
+    return p;
 }
 
 template <Lay LA, Lay LB, class Epi>
@@ -103,8 +111,7 @@ hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw,
 
 size_t g16_ws_bytes_for(int M, int N, int K) {
     const GemmShape s{M, N, K};
-    const Plan p = plan(s, ~size_t(0));
-    return p.splits > 1 ? gemm16_ws_bytes<T128>(s, p.splits) : 0;
+    return ws_for(plan(s, ~size_t(0)), s);
 }
 
 }  // namespace vkh
