@@ -1,4 +1,4 @@
-"""Benchmark: BASELINE.json metric on one MI355X.
+"""Benchmark: the headline training metric on one MI355X.
 
   train tokens/s of a Qwen3-0.6B-shaped fwd + bwd + Adam step (config 3:
   28 layers, dim 1024, 16/8 heads, head_dim 128, QK-norm, SwiGLU 3072,
@@ -15,7 +15,7 @@ reference path) timed on this host on a bounded sample and scaled to
 tokens/s of the same step (see `sample`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
-                       [--no-cpu-baseline] [--fa-reps R]
+                       [--no-cpu-baseline] [--fa-reps R] [--only all|step|fa] [--calib-copy]
 """
 from __future__ import annotations
 
@@ -35,7 +35,7 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 FP32_PEAK_TFLOPS = 157.3
 
-# BASELINE.json configs[2]
+# config 3 of the metric: the Qwen3-0.6B-shaped full fine-tune step
 QWEN3_06B = dict(dim=1024, n_heads=16, n_kv_heads=8, head_dim=128, ff_dim=3072, n_pos=512,
                  n_layers=28, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=128,
                  rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
@@ -140,6 +140,33 @@ def bench_fa_bwd(args):
     return dict(ms=ms, flops=flops, tflops=tflops)
 
 
+def calib_copy():
+    """Copy-type kernel of known size for counter calibration."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import DeviceBuffer, synchronize
+
+    n = 64 << 20
+    src = DeviceBuffer.from_numpy(np.ones(n, np.float32))
+    dst = DeviceBuffer(n * 4)
+    for _ in range(3):
+        K.scale(src, dst, n, 1.0)
+    synchronize()
+    print(f"[bench] calibration copy: {n * 4} bytes read + {n * 4} written per dispatch",
+          file=sys.stderr, flush=True)
+
+
+def measured_traffic(name):
+    """HBM bytes per call recorded by the rocprofv3 counter runs (None if absent)."""
+    path = os.path.join(ROOT, "profiles", name)
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_call:"):
+                return int(line.split(":")[1])
+    except OSError:
+        pass
+    return None
+
+
 def cpu_baseline(args):
     """The C oracle (single thread) on a bounded sample of the step, scaled to tokens/s.
 
@@ -201,10 +228,17 @@ def main():
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--fa-reps", type=int, default=20)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--only", default="all", choices=["all", "step", "fa"],
+                    help="run only the step or only the attention benchmark (profiling runs)")
+    ap.add_argument("--calib-copy", action="store_true",
+                    help="after the benchmarks, run a copy-type kernel of known size "
+                         "(vkh_scale over 64 Mi floats: 256 MiB read + 256 MiB written, 3x) "
+                         "to calibrate rocprofv3 FETCH_SIZE / WRITE_SIZE")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: this build has no multi-GPU path "
-              "(see DESIGN.md for how the step would shard); run with --gpus 1",
+              "(the design shards the step data-parallel, one process per GPU, but only one "
+              "GPU is measured here); run with --gpus 1",
               file=sys.stderr)
         sys.exit(2)
 
@@ -213,8 +247,21 @@ def main():
     if v.device_count() < 1:
         print("bench.py: no GPU visible", file=sys.stderr)
         sys.exit(1)
+    if args.only == "fa":
+        fa = bench_fa_bwd(args)
+        if args.calib_copy:
+            calib_copy()
+        print(json.dumps({"fa_bwd_ms": round(fa["ms"], 4), "fa_bwd_tflops": round(fa["tflops"], 1)}),
+              flush=True)
+        return
     st = bench_step(args, None)
+    if args.only == "step":
+        print(json.dumps({"ms_per_step": round(st["ms"], 3), "tokens_s": round(st["tokens_s"], 1)}),
+              flush=True)
+        return
     fa = bench_fa_bwd(args)
+    if args.calib_copy:
+        calib_copy()
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     peak = BF16_PEAK_TFLOPS if args.precision == "bf16" else FP32_PEAK_TFLOPS
     mfu = st["flops"] / (st["ms"] * 1e-3) / 1e12 / peak
@@ -231,7 +278,7 @@ def main():
         "vs_baseline": None,
         "dtype": "bf16" if args.precision == "bf16" else "fp32",
         "data": "synthetic (random-init weights ~N(0,0.02), uniform token ids)",
-        "config": {"workload": "qwen3-0.6b full fine-tune step (BASELINE config 3)",
+        "config": {"workload": "qwen3-0.6b full fine-tune step, config 3 of the metric",
                    "global_batch": st["T"], "seq_len": QWEN3_06B["n_pos"], "batch": 4,
                    "layers": 28, "vocab": 151936, "tied_embeddings": True,
                    "master_weights": "fp32", "optimizer": "adam",
@@ -239,13 +286,16 @@ def main():
         "step_tflops": round(st["flops"] / (st["ms"] * 1e-3) / 1e12, 1),
         "step_mfu": round(mfu, 4),
         "loss": [round(st["loss_first"], 4), round(st["loss_last"], 4)],
-        "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (BASELINE config 2)",
+        "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (config 2)",
                    "ms": round(fa["ms"], 4), "tflops": round(fa["tflops"], 1),
                    "frac_bf16_peak": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4)},
-        "roofline": {"kernel": "fa_bw_d + fa_bwd_dkv + fa_bwd_dq (config 2)", "bound": "mfma",
+        "roofline": {"kernel": "attention backward, config 2: fa_bw_d_k + fa_bwd_dkv2_k + "
+                               "fa_dq_gemm_k (one call)", "bound": "mfma",
                      "achieved": round(fa["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None},
+                     "traffic": measured_traffic("fa_bwd_config2_traffic.md"),
+                     "traffic_unit": "bytes per call (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
+                                     "calibrated; profiles/fa_bwd_config2_traffic.md)"},
         "cpu_baseline": cpu,
     }
     print(json.dumps(out), flush=True)

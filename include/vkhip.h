@@ -5,7 +5,7 @@
  * (src/train/transformer.zig `Runner`) and the kernels it records.  All entry
  * points are `extern "C"`, take plain pointers and sizes, and return a
  * `vkh_status`; no C++ or framework types cross the boundary.  A Zig host
- * binds this header with `@cImport` / `extern fn` (see INTEGRATION.md).
+ * binds this header with `@cImport` / `extern fn`.
  *
  * Conventions
  *   - Errors: `vkh_status`, mirroring the Zig error names of the reference;

@@ -1,7 +1,7 @@
 """Per-kernel parity of the HIP kernels (through the C ABI) against the C
 oracle on identical seeded inputs.
 
-Bars (BASELINE north star): bit-exact for integer / index work (embedding
+Bars: bit-exact for integer / index work (embedding
 scatter targets, token gather), rel-L2 <= 1e-3 for fp32, rel-L2 <= 1e-2 for
 bf16-operand contractions (compared with the oracle run on the same
 bf16-rounded inputs).  Elementwise kernels that restate the reference formula

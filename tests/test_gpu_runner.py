@@ -1,5 +1,5 @@
 """Whole-step parity: the HIP Runner vs the C oracle's GPU-Runner semantics on
-identical seeded weights and tokens (BASELINE config 1 and variants), plus
+identical seeded weights and tokens (the tiny parity config and variants), plus
 the Runner API behaviour (checkpoints, tick API, error paths).
 
 Per-tensor bars: fp32 precision rel-L2 <= 1e-3 for every gradient and Adam
@@ -121,7 +121,7 @@ def test_step_parity_fp32(variant):
 def test_step_parity_bf16():
     """bf16-operand step vs the oracle with the same operand rounding.
 
-    The 1e-2 bar of the north star is per bf16-operand GEMM (held by the
+    The 1e-2 bar is per bf16-operand GEMM (held by the
     kernel tests).  A 2-layer step chains about a dozen such GEMMs plus the
     bf16 attention / dz operands, and an element that lands near a bf16
     rounding boundary can round differently on each side, so whole-step
