@@ -177,7 +177,7 @@ def test_golden_training_step():
         loss = r.last_loss()
         note(f"  loss golden {float(a['loss']):.6f} gpu {loss:.6f}")
         assert abs(loss - float(a["loss"])) < 1e-5 * abs(float(a["loss"]))
-        assert r.step_t == 1
+        assert r.step_t == 2  # Adam's t starts at 1 and is incremented after the update
         worst = 0.0
         for i, k in enumerate(keys):
             s = slice(offs[i], offs[i + 1])

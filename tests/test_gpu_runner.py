@@ -91,8 +91,12 @@ def compare(m, r, keys, kind, tol, what):
     return worst[0]
 
 
+HD128 = {"head_dim": 128, "n_heads": 2, "n_kv_heads": 1, "rotary_dim": 128}  # Qwen3 head size
+
+
 @pytest.mark.parametrize("variant", [{}, {"tied_embeddings": 1}, {"n_seqs": 2, "seq_len": 64},
-                                     {"qk_norm": 0, "rotary_dim": 32}])
+                                     {"qk_norm": 0, "rotary_dim": 32}, HD128,
+                                     dict(HD128, rotary_dim=64, n_seqs=2, seq_len=64)])
 def test_step_parity_fp32(variant):
     note(f"step fp32 {variant}")
     m, r, tok, tgt, cfg = build_pair(0, **variant)
@@ -118,7 +122,8 @@ def test_step_parity_fp32(variant):
         assert rel_l2(du_ref, du) < 1e-2, (k, rel_l2(du_ref, du))
 
 
-def test_step_parity_bf16():
+@pytest.mark.parametrize("variant", [{}, HD128])
+def test_step_parity_bf16(variant):
     """bf16-operand step vs the oracle with the same operand rounding.
 
     The 1e-2 bar is per bf16-operand GEMM (held by the
@@ -128,8 +133,8 @@ def test_step_parity_bf16():
     gradients are held to 2e-2 here; for scale, merely rounding the oracle's
     own operands moves its gradients by up to 1.4e-2 from the fp32 oracle.
     """
-    note("step bf16")
-    m, r, tok, tgt, cfg = build_pair(1)
+    note(f"step bf16 {variant}")
+    m, r, tok, tgt, cfg = build_pair(1, **variant)
     keys = tensor_keys(cfg)
     loss_ref = m.forward_backward(tok, tgt)
     loss = r.forward_backward(tok, tgt)

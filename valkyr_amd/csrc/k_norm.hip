@@ -471,6 +471,272 @@ __global__ __launch_bounds__(NT) void qkv_bwd_k(QkvLayout L, float *dqkv, long l
         partial[(long)blockIdx.x * 2 * hd + c] = red[c / hd][c % hd];
 }
 
+// ── Q/K norm + RoPE, several heads per wave ─────────────────────────────
+// For head_dim 64 / 128 a head is LPH = 8 / 16 lanes holding 8 consecutive
+// elements each, so one wave works on 64 / LPH (row, head) items at once.
+// The per-head reductions stay inside a DPP row (quad swaps, half-row and row
+// mirrors, fp64 like the wave-per-head kernels above) and, for full-width
+// RoPE at LPH = 16, the partner element i +- 64 sits in lane j ^ 8 of the
+// same row (row rotate by 8).  Requires rotary_dim % 16 == 0 so a lane's 8
+// elements are all on one side of the rotation.
+
+template <int CTRL>
+VKH_DEV double dpp_d(double v) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+template <int LPH>
+VKH_DEV double grp_sum(double v) {
+    v += dpp_d<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_d<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_d<0x141>(v);  // row_half_mirror: the other quad of the 8 lanes
+    if constexpr (LPH == 16) v += dpp_d<0x140>(v);  // row_mirror: the other 8 lanes
+    return v;
+}
+
+VKH_DEV void ld8(const float *p, float (&v)[8]) {
+    const float4 a = reinterpret_cast<const float4 *>(p)[0];
+    const float4 b = reinterpret_cast<const float4 *>(p)[1];
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+VKH_DEV void st8(float *p, const float (&v)[8]) {
+    reinterpret_cast<float4 *>(p)[0] = make_float4(v[0], v[1], v[2], v[3]);
+    reinterpret_cast<float4 *>(p)[1] = make_float4(v[4], v[5], v[6], v[7]);
+}
+VKH_DEV void st8(bf16 *p, const float (&v)[8]) {
+    *reinterpret_cast<bf16x8 *>(p) = cvt8(v[0], v[1], v[2], v[3], v[4], v[5], v[6], v[7]);
+}
+
+struct Item8 {
+    float v[8], x[8];
+    float2 cs[8];
+};
+
+// RoPE geometry of lane slot j (elements 8 j .. 8 j + 7) of a head.
+struct Rope8 {
+    int rot_lane;   // 0: no rotation, else the table column base of the slot
+    int src;        // partner slot within the head
+    bool lower;     // slot below half
+    int col;        // first table column of the slot
+};
+
+VKH_DEV Rope8 rope8(int j, int half) {
+    Rope8 r;
+    const int e0 = 8 * j;
+    r.lower = e0 < half;
+    r.rot_lane = e0 < 2 * half;
+    r.src = r.lower ? j + half / 8 : j - half / 8;
+    r.col = r.lower ? e0 : e0 - half;
+    return r;
+}
+
+template <int LPH>
+VKH_DEV void load8(Item8 &d, const float *vp, const float *xp, const float2 *trow, const Rope8 &rp,
+                   bool valid, bool qk) {
+    if (!valid) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d.v[i] = d.x[i] = 0.f, d.cs[i] = make_float2(1.f, 0.f);
+        return;
+    }
+    ld8(vp, d.v);
+    if (xp) {
+        ld8(xp, d.x);
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d.x[i] = 0.f;
+    }
+    if (qk && rp.rot_lane) {
+        const float4 *tp = reinterpret_cast<const float4 *>(trow + rp.col);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float4 c = tp[i];
+            d.cs[2 * i] = make_float2(c.x, c.y);
+            d.cs[2 * i + 1] = make_float2(c.z, c.w);
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) d.cs[i] = make_float2(1.f, 0.f);
+    }
+}
+
+// Partner values of a head's rotation: full-width rope at 16 lanes per head
+// is a row rotate by 8; other widths shuffle from the partner lane.
+template <int LPH>
+VKH_DEV void partner8(const float (&v)[8], float (&pv)[8], int lane, const Rope8 &rp, int half) {
+    if (LPH == 16 && half == 64) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pv[i] = dpp_f<0x128>(v[i]);  // row_ror:8
+    } else {
+        const int src = (lane & ~(LPH - 1)) + (rp.rot_lane ? rp.src : (lane & (LPH - 1)));
+#pragma unroll
+        for (int i = 0; i < 8; ++i) pv[i] = __shfl(v[i], src, 64);
+    }
+}
+
+template <typename TO, int LPH>
+__global__ __launch_bounds__(NT) void qkv_fwd8_k(QkvLayout L, const float *qkv, long ld_qkv,
+                                                  const float *wq, const float *wk, TO *out,
+                                                  long ld_out, const float2 *tab) {
+    constexpr int G = 64 / LPH;
+    const int lane = threadIdx.x % 64, j = lane % LPH, g = lane / LPH;
+    const int hd = L.head_dim, Hqk = L.n_q_heads + L.n_kv_heads, Htot = Hqk + L.n_kv_heads;
+    const int half = L.rotary_dim / 2;
+    const long items = (long)L.n_rows * Htot;
+    const long stride = (long)gridDim.x * NW * G;
+    const Rope8 rp = rope8(j, half);
+    float gq[8], gk[8];
+    if (L.qk_norm) {
+        ld8(wq + 8 * j, gq);
+        ld8(wk + 8 * j, gk);
+    }
+    auto fetch = [&](long it, Item8 &d) {
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        load8<LPH>(d, qkv + (long)t * ld_qkv + h * hd + 8 * j, nullptr,
+                   tab + (long)(t % L.seq_len) * half, rp, it < items, h < Hqk);
+    };
+    long it = ((long)blockIdx.x * NW + threadIdx.x / 64) * G + g;
+    const long wave_first = it - g;
+    Item8 cur;
+    fetch(it, cur);
+    for (long wb = wave_first; wb < items; wb += stride, it += stride) {
+        Item8 nxt;
+        if (wb + stride < items) fetch(it + stride, nxt);
+        const bool valid = it < items;
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        const bool qk = valid && h < Hqk;
+        float y[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) y[i] = cur.v[i];
+        if (L.qk_norm) {
+            double ss = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) ss += (double)y[i] * (double)y[i];
+            ss = grp_sum<LPH>(ss);
+            if (qk) {
+                const bool is_q = h < L.n_q_heads;
+                const float ri = 1.0f / sqrtf((float)(ss / (double)hd) + L.eps);
+#pragma unroll
+                for (int i = 0; i < 8; ++i) y[i] = (is_q ? gq[i] : gk[i]) * ri * y[i];
+            }
+        }
+        if (half > 0) {
+            float pv[8];
+            partner8<LPH>(y, pv, lane, rp, half);
+            if (qk && rp.rot_lane) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float2 cs = cur.cs[i];
+                    y[i] = rp.lower ? y[i] * cs.x - pv[i] * cs.y : pv[i] * cs.y + y[i] * cs.x;
+                }
+            }
+        }
+        if (valid) st8(out + (long)t * ld_out + h * hd + 8 * j, y);
+        if (wb + stride < items) cur = nxt;
+    }
+}
+
+template <int LPH>
+__global__ __launch_bounds__(NT) void qkv_bwd8_k(QkvLayout L, float *dqkv, long ld,
+                                                  const float *qkv, long ld_qkv, const float *wq,
+                                                  const float *wk, float *partial,
+                                                  const float2 *tab, bf16 *outb, long ldb) {
+    constexpr int G = 64 / LPH;
+    __shared__ float red[2][128];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64, j = lane % LPH, g = lane / LPH;
+    const int hd = L.head_dim, Hqk = L.n_q_heads + L.n_kv_heads;
+    const int Htot = outb ? Hqk + L.n_kv_heads : Hqk;
+    const int half = L.rotary_dim / 2;
+    const long items = (long)L.n_rows * Htot;
+    const long stride = (long)gridDim.x * NW * G;
+    const Rope8 rp = rope8(j, half);
+    float gq[8], gk[8], dwq[8], dwk[8];
+    if (L.qk_norm) {
+        ld8(wq + 8 * j, gq);
+        ld8(wk + 8 * j, gk);
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) dwq[i] = dwk[i] = 0.f;
+    auto fetch = [&](long it, Item8 &d) {
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        const bool qk = h < Hqk;
+        load8<LPH>(d, dqkv + (long)t * ld + h * hd + 8 * j,
+                   (qk && L.qk_norm) ? qkv + (long)t * ld_qkv + h * hd + 8 * j : nullptr,
+                   tab + (long)(t % L.seq_len) * half, rp, it < items, qk);
+    };
+    long it = ((long)blockIdx.x * NW + wave) * G + g;
+    const long wave_first = it - g;
+    Item8 cur;
+    fetch(it, cur);
+    for (long wb = wave_first; wb < items; wb += stride, it += stride) {
+        Item8 nxt;
+        if (wb + stride < items) fetch(it + stride, nxt);
+        const bool valid = it < items;
+        const int t = (int)(it / Htot), h = (int)(it % Htot);
+        const bool qk = valid && h < Hqk;
+        const bool is_q = h < L.n_q_heads;
+        float gv[8];
+#pragma unroll
+        for (int i = 0; i < 8; ++i) gv[i] = cur.v[i];
+        if (half > 0) {
+            float pv[8];
+            partner8<LPH>(gv, pv, lane, rp, half);
+            if (qk && rp.rot_lane) {
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float2 cs = cur.cs[i];
+                    gv[i] = rp.lower ? cs.x * gv[i] + cs.y * pv[i] : -cs.y * pv[i] + cs.x * gv[i];
+                }
+            }
+        }
+        if (L.qk_norm) {
+            double ss = 0, A = 0;
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                const float gw = is_q ? gq[i] : gk[i];
+                ss += (double)cur.x[i] * (double)cur.x[i];
+                A += (double)gv[i] * (double)gw * (double)cur.x[i];
+            }
+            ss = grp_sum<LPH>(ss);
+            A = grp_sum<LPH>(A);
+            if (qk) {
+                const float ri = 1.0f / sqrtf((float)(ss / (double)hd) + L.eps);
+                const float ri3_over_D = ri * ri * ri / (float)hd;
+                const float A_f = (float)A;
+#pragma unroll
+                for (int i = 0; i < 8; ++i) {
+                    const float gw = is_q ? gq[i] : gk[i];
+                    const float o = ri * gw * gv[i] - ri3_over_D * cur.x[i] * A_f;
+                    const float dwv = gv[i] * ri * cur.x[i];
+                    if (is_q) dwq[i] += dwv; else dwk[i] += dwv;
+                    gv[i] = o;
+                }
+            }
+        }
+        if (valid) {
+            if (outb) st8(outb + (long)t * ldb + h * hd + 8 * j, gv);
+            else if (h < Hqk) st8(dqkv + (long)t * ld + h * hd + 8 * j, gv);
+        }
+        if (wb + stride < items) cur = nxt;
+    }
+    // combine the lane groups' gain partials in a fixed (wave, group) order
+    for (int s = 0; s < NW * G; ++s) {
+        if (wave * G + g == s) {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) {
+                red[0][8 * j + i] = s ? red[0][8 * j + i] + dwq[i] : dwq[i];
+                red[1][8 * j + i] = s ? red[1][8 * j + i] + dwk[i] : dwk[i];
+            }
+        }
+        __syncthreads();
+    }
+    for (int c = threadIdx.x; c < 2 * hd; c += NT)
+        partial[(long)blockIdx.x * 2 * hd + c] = red[c / hd][c % hd];
+}
+
 constexpr int kRmsMaxBlocks = 512, kQkvMaxBlocks = 512;
 
 inline int rms_grid(int rows) { return std::max(1, std::min(kRmsMaxBlocks, (rows + NW - 1) / NW)); }
@@ -499,6 +765,24 @@ hipError_t by_epl(int hd, F &&f) {
 }
 
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The several-heads-per-wave kernels: head_dim 64 or 128, rotary width a
+// multiple of 16, 16-byte aligned rows (out_align = elements per 16 bytes).
+inline bool qkv8_ok(const QkvLayout &L, const void *in, long ld_in, const void *out, long ld_out,
+                    int out_align) {
+    return (L.head_dim == 64 || L.head_dim == 128) && L.rotary_dim % 16 == 0 &&
+           L.rotary_dim <= L.head_dim && L.seq_len > 0 && al16(in) && al16(out) &&
+           ld_in % 4 == 0 && ld_out % out_align == 0;
+}
+inline int qkv8_grid(const QkvLayout &L, long items, int cap) {
+    const long per_block = (long)NW * (64 / (L.head_dim / 8));
+    return (int)std::max<long>(1, std::min<long>(cap, (items + 2 * per_block - 1) / (2 * per_block)));
+}
+template <class F>
+hipError_t by_lph(int hd, F &&f) {
+    if (hd == 64) return f(std::integral_constant<int, 8>{});
+    return f(std::integral_constant<int, 16>{});
+}
 
 }  // namespace
 
@@ -572,6 +856,19 @@ hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv
     if (!qkv_shape_ok(L, ld_qkv, ld_out) || !al16(qkv) || ((uintptr_t)out & 7u) ||
         (L.qk_norm && (!al16(wq) || !al16(wk))))
         return hipErrorInvalidValue;
+    if (qkv8_ok(L, qkv, ld_qkv, out, ld_out, out_dt == DType::BF16 ? 8 : 4)) {
+        const int grid = qkv8_grid(L, qkv_items(L, true), 2048);
+        return by_lph(L.head_dim, [&](auto lph) {
+            constexpr int LPH = decltype(lph)::value;
+            if (out_dt == DType::BF16)
+                hipLaunchKernelGGL((qkv_fwd8_k<bf16, LPH>), dim3(grid), dim3(NT), 0, st, L, qkv,
+                                   ld_qkv, wq, wk, (bf16 *)out, ld_out, rope_tab);
+            else
+                hipLaunchKernelGGL((qkv_fwd8_k<float, LPH>), dim3(grid), dim3(NT), 0, st, L, qkv,
+                                   ld_qkv, wq, wk, (float *)out, ld_out, rope_tab);
+            return hipGetLastError();
+        });
+    }
     const int grid = qkv_grid(qkv_items(L, true), 2048);
     return by_epl(L.head_dim, [&](auto epl) {
         constexpr int EPL = decltype(epl)::value;
@@ -593,13 +890,25 @@ hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const 
     if (!qkv_shape_ok(L, ld, ld_qkv) || (outb && ldb % 4) || !al16(dqkv) || !al16(qkv) ||
         ((uintptr_t)outb & 7u) || (L.qk_norm && (!al16(wq) || !al16(wk))))
         return hipErrorInvalidValue;
-    const int grid = qkv_grid(qkv_items(L, outb != nullptr), kQkvMaxBlocks);
-    hipError_t e = by_epl(L.head_dim, [&](auto epl) {
-        constexpr int EPL = decltype(epl)::value;
-        hipLaunchKernelGGL((qkv_bwd_k<EPL>), dim3(grid), dim3(NT), 0, st, L, dqkv, ld, qkv, ld_qkv,
-                           wq, wk, partial, rope_tab, outb, ldb);
-        return hipGetLastError();
-    });
+    const bool fast = qkv8_ok(L, qkv, ld_qkv, dqkv, ld, 4) &&
+                      (!outb || (al16(outb) && ldb % 8 == 0));
+    const int grid = fast ? qkv8_grid(L, qkv_items(L, outb != nullptr), kQkvMaxBlocks)
+                          : qkv_grid(qkv_items(L, outb != nullptr), kQkvMaxBlocks);
+    hipError_t e;
+    if (fast)
+        e = by_lph(L.head_dim, [&](auto lph) {
+            constexpr int LPH = decltype(lph)::value;
+            hipLaunchKernelGGL((qkv_bwd8_k<LPH>), dim3(grid), dim3(NT), 0, st, L, dqkv, ld, qkv,
+                               ld_qkv, wq, wk, partial, rope_tab, outb, ldb);
+            return hipGetLastError();
+        });
+    else
+        e = by_epl(L.head_dim, [&](auto epl) {
+            constexpr int EPL = decltype(epl)::value;
+            hipLaunchKernelGGL((qkv_bwd_k<EPL>), dim3(grid), dim3(NT), 0, st, L, dqkv, ld, qkv,
+                               ld_qkv, wq, wk, partial, rope_tab, outb, ldb);
+            return hipGetLastError();
+        });
     if (e != hipSuccess) return e;
     if (L.qk_norm && dwq && dwk) {
         hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
