@@ -105,8 +105,9 @@ __global__ __launch_bounds__(NT, 2) void fa_fwd_bf16_k(AttnShape s, const bf16 *
     __shared__ __attribute__((aligned(16))) bf16 Vt[HD][BN + 8];
 
     const int nqt = (s.n_q + BM - 1) / BM;
-    const int qt = s.causal ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    // blockIdx.x = (head, sequence), blockIdx.y = q tile, heaviest (last) first
+    const int qt = s.causal ? nqt - 1 - (int)blockIdx.y : (int)blockIdx.y;
+    const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int kvh = h / (s.n_heads / s.n_kv_heads);
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
     const int q0 = qt * BM, qw0 = q0 + wave * 32;
@@ -261,9 +262,10 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv_bf16_k(AttnShape s, AttnPtrs
     __shared__ __attribute__((aligned(16))) bf16 dOt[HD][BM + 8];
     __shared__ float lse_s[BM], d_s[BM];
 
-    const int nkt = (s.n_kv + BN - 1) / BN;
-    const int kt = s.causal ? nkt - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    // blockIdx.x = (kv head, sequence), blockIdx.y = key tile: under a causal
+    // mask the first key tiles see the most queries, so they go first
+    const int kt = (int)blockIdx.y;
+    const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
     const int hpk = s.n_heads / s.n_kv_heads;
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
     const int k0 = kt * BN, kw0 = k0 + wave * 32;
@@ -384,8 +386,9 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dq_bf16_k(AttnShape s, AttnPtrs 
     __shared__ __attribute__((aligned(16))) bf16 Kt[HD][BN + 8];
 
     const int nqt = (s.n_q + BM - 1) / BM;
-    const int qt = s.causal ? nqt - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    // blockIdx.x = (head, sequence), blockIdx.y = q tile, heaviest (last) first
+    const int qt = s.causal ? nqt - 1 - (int)blockIdx.y : (int)blockIdx.y;
+    const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int kvh = h / (s.n_heads / s.n_kv_heads);
     const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64, g = lane / 16, c16 = lane % 16;
     const int q0 = qt * BM, qw0 = q0 + wave * 32;
@@ -528,11 +531,14 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
     static_assert(PER * NT == BM * CH, "tile / thread mismatch");
     __shared__ __attribute__((aligned(16))) bf16 Qs[2][BM][P];
     __shared__ __attribute__((aligned(16))) bf16 Os[2][BM][P];
+    __shared__ __attribute__((aligned(16))) bf16 Ks[BN][P];
+    __shared__ __attribute__((aligned(16))) bf16 Vs[BN][P];
     __shared__ float lse_s[2][BM], d_s[2][BM];
 
-    const int nkt = (s.n_kv + BN - 1) / BN;
-    const int kt = s.causal ? nkt - 1 - (int)blockIdx.x : (int)blockIdx.x;  // heavy tiles first
-    const int kvh = blockIdx.y, b = blockIdx.z;
+    // blockIdx.x = (kv head, sequence), blockIdx.y = key tile: under a causal
+    // mask the first key tiles see the most queries, so they go first
+    const int kt = (int)blockIdx.y;
+    const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
     const int hpk = s.n_heads / s.n_kv_heads;
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);  // uniform: scalar branches
@@ -542,15 +548,15 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
     const bf16 *kb = (const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD;
     const bf16 *vb = (const bf16 *)p.v + (long)b * s.n_kv * p.ldv + kvh * HD;
 
-    bf16x8 kf[2][DS], vf[2][DS];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-        const int kr = kw0 + 16 * ks + c16;
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) {
-            kf[ks][ds] = kr < s.n_kv ? ld_frag(kb + (long)kr * p.ldk + 32 * ds + 8 * g) : bf16x8{};
-            vf[ks][ds] = kr < s.n_kv ? ld_frag(vb + (long)kr * p.ldv + 32 * ds + 8 * g) : bf16x8{};
-        }
+    // K and V of the block's keys stay in LDS (read as B fragments per tile):
+    // holding them in registers would leave too few VGPRs for the tile.
+    for (int u = tid; u < BN * CH; u += NT) {
+        const int r = u / CH, c = u % CH, kr = k0 + r;
+        const uint4 zero = make_uint4(0, 0, 0, 0);
+        *reinterpret_cast<uint4 *>(&Ks[r][c * 8]) =
+            kr < s.n_kv ? *reinterpret_cast<const uint4 *>(kb + (long)kr * p.ldk + c * 8) : zero;
+        *reinterpret_cast<uint4 *>(&Vs[r][c * 8]) =
+            kr < s.n_kv ? *reinterpret_cast<const uint4 *>(vb + (long)kr * p.ldv + c * 8) : zero;
     }
     f32x4 dvt[DSUB][2], dkt[DSUB][2];
 #pragma unroll
@@ -603,37 +609,33 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
         if (it + 1 < niter) gload(it + 1);
         const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
         // dS^T rows of this lane's two keys: dsr[k * n_q + q]; 4 consecutive q per store
-        bf16 *dsr = dsw ? dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv +
-                              (long)(kw0 + c16) * s.n_q + q0 + 4 * g
-                        : nullptr;
+        bf16 *dsr = dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv + (long)(kw0 + c16) * s.n_q +
+                    q0 + 4 * g;
         const long ds_ks = 16L * s.n_q;
         const bool keys_ok = kw0 + 32 <= s.n_kv;
-        if (s.causal && kw0 > q0 + BM - 1 + off) {
-            // every key of this wave is masked for the tile: dS is zero
-            if (dsr) {
-#pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-                    for (int qs = 0; qs < QS; ++qs)
-                        if (keys_ok || kw0 + 16 * ks + c16 < s.n_kv)
-                            *reinterpret_cast<bf16x4 *>(dsr + ks * ds_ks + 16 * qs) = bf16x4{};
-            }
-        } else {
+        // Waves whose keys are all above the diagonal run the same code (their
+        // P and dS come out zero): one path keeps the accumulators in place.
+        {
             const bf16 *Qb = &Qs[buf][0][0], *Ob = &Os[buf][0][0];
             f32x4 sc[QS][2], dp[QS][2];
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs) sc[qs][0] = sc[qs][1] = dp[qs][0] = dp[qs][1] = f32x4{0, 0, 0, 0};
 #pragma unroll
-            for (int ds = 0; ds < DS; ++ds)
+            for (int ds = 0; ds < DS; ++ds) {
+                const bf16x8 k0f = ld_frag(&Ks[wave * 32 + c16][32 * ds + 8 * g]);
+                const bf16x8 k1f = ld_frag(&Ks[wave * 32 + 16 + c16][32 * ds + 8 * g]);
+                const bf16x8 v0f = ld_frag(&Vs[wave * 32 + c16][32 * ds + 8 * g]);
+                const bf16x8 v1f = ld_frag(&Vs[wave * 32 + 16 + c16][32 * ds + 8 * g]);
 #pragma unroll
                 for (int qs = 0; qs < QS; ++qs) {
                     const bf16x8 qa = ld_frag(Qb + (16 * qs + c16) * P + 32 * ds + 8 * g);
                     const bf16x8 oa = ld_frag(Ob + (16 * qs + c16) * P + 32 * ds + 8 * g);
-                    sc[qs][0] = mfma16x16x32(qa, kf[0][ds], sc[qs][0]);
-                    sc[qs][1] = mfma16x16x32(qa, kf[1][ds], sc[qs][1]);
-                    dp[qs][0] = mfma16x16x32(oa, vf[0][ds], dp[qs][0]);
-                    dp[qs][1] = mfma16x16x32(oa, vf[1][ds], dp[qs][1]);
+                    sc[qs][0] = mfma16x16x32(qa, k0f, sc[qs][0]);
+                    sc[qs][1] = mfma16x16x32(qa, k1f, sc[qs][1]);
+                    dp[qs][0] = mfma16x16x32(oa, v0f, dp[qs][0]);
+                    dp[qs][1] = mfma16x16x32(oa, v1f, dp[qs][1]);
                 }
+            }
             // P = exp2(S c2 - lse2); a fully masked row (lse = -inf) gets +inf -> P = 0.
             // Only tiles that touch the causal diagonal or an edge need per-element masks.
             const bool edge = (s.causal && kw0 + 31 > q0 + off) || !keys_ok;
@@ -671,18 +673,16 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
                     for (int ks = 0; ks < 2; ++ks)
                         dp[qs][ks][r] = sc[qs][ks][r] * (dp[qs][ks][r] - dqs[r]);
             }
-            if (dsr) {
 #pragma unroll
-                for (int ks = 0; ks < 2; ++ks)
+            for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-                    for (int qs = 0; qs < QS; ++qs) {
-                        bf16x4 v;
-                        v[0] = (bf16)dp[qs][ks][0]; v[1] = (bf16)dp[qs][ks][1];
-                        v[2] = (bf16)dp[qs][ks][2]; v[3] = (bf16)dp[qs][ks][3];
-                        if (keys_ok || kw0 + 16 * ks + c16 < s.n_kv)
-                            *reinterpret_cast<bf16x4 *>(dsr + ks * ds_ks + 16 * qs) = v;
-                    }
-            }
+                for (int qs = 0; qs < QS; ++qs) {
+                    bf16x4 v;
+                    v[0] = (bf16)dp[qs][ks][0]; v[1] = (bf16)dp[qs][ks][1];
+                    v[2] = (bf16)dp[qs][ks][2]; v[3] = (bf16)dp[qs][ks][3];
+                    if (keys_ok || kw0 + 16 * ks + c16 < s.n_kv)
+                        *reinterpret_cast<bf16x4 *>(dsr + ks * ds_ks + 16 * qs) = v;
+                }
 #pragma unroll
             for (int qst = 0; qst < QST; ++qst) {
                 const bf16x8 pb0 = frag_acc(sc[2 * qst][0], sc[2 * qst + 1][0]);
@@ -726,6 +726,252 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
     }
 }
 
+// ── backward v3 (head_dim 128): dK/dV with the work split over two wave groups
+//
+// 8 waves per block of 128 keys.  Waves 0-3 ("P waves") own 32 keys each and
+// compute S^T = K Q^T, P = exp2(S c - lse) and dV += P^T dO; waves 4-7 ("dS
+// waves") own the same 32-key slices and compute dP^T = V dO^T, dS = P (dP - D)
+// and dK += dS^T Q, taking P from the matching P wave through LDS (fp32, so
+// dS is bit-identical to the one-group kernel).  Each wave then holds one
+// 32 x 128 accumulator (64 registers) and one operand slice (K or V), which
+// keeps it within 256 registers: two waves per SIMD, so one group's softmax /
+// dS arithmetic overlaps the other group's MFMAs.
+//
+// Q / dO tiles (64 x 128 bf16) arrive by DMA (buffer_load ... lds) into
+// unpadded LDS rows with a 16-byte chunk swizzle: chunk c of row r sits at
+// c ^ swz(r), swz(r) = 4 (r & 3) + ((r >> 2) & 3).  swz is a bijection on 16
+// consecutive rows (the 16 rows of a b128 fragment read hit 16 different
+// chunks) and, for the 4 rows x 2 adjacent chunks of a transposing read,
+// swz >> 1 differs between the 4 rows, so both read kinds are conflict-free.
+// The next tile's DMA is in flight during the current tile (double buffer);
+// there are two barriers per tile (P ready, tile done).
+
+namespace dkv3 {
+constexpr int NT3 = 512, BN = 128, BM = 64, HD = 128, DS = HD / 32, DSUB = HD / 16;
+constexpr int QS = BM / 16, QST = BM / 32;
+constexpr int TILE = BM * HD * 2;  // bytes of one Q or dO tile
+
+VKH_DEV int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+
+// byte offset of (row r, element col) in a swizzled tile
+VKH_DEV int toff(int r, int col) { return r * (HD * 2) + (((col >> 3) ^ swz(r)) << 4) + (col & 7) * 2; }
+
+VKH_DEV bf16x8 frag_row(const char *tile, int r, int col) {
+    return *reinterpret_cast<const bf16x8 *>(tile + toff(r, col));
+}
+
+// X[r0 + j][c0 + (lane % 16)], j = 0..3 (see ld_tr4), from a swizzled tile
+VKH_DEV bf16x4 tr4(const char *tile, int r0, int c0, int l16) {
+    const char *src = tile + toff(r0 + l16 / 4, c0 + 4 * (l16 % 4));
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4 *)src);
+}
+
+// A operand of the dV / dK products: rows = tile columns c0 + lane % 16,
+// contraction = tile rows k0 + {4g..4g+3, 16+4g..16+4g+3} (frag_acc order)
+VKH_DEV bf16x8 frag_t(const char *tile, int c0, int k0, int g, int l16) {
+    const bf16x4 lo = tr4(tile, k0 + 4 * g, c0, l16);
+    const bf16x4 hi = tr4(tile, k0 + 16 + 4 * g, c0, l16);
+    return __builtin_shufflevector(lo, hi, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+}  // namespace dkv3
+
+__global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnPtrs p, bf16 *dsw) {
+    using namespace dkv3;
+    __shared__ __attribute__((aligned(16))) char Qs[2][TILE];
+    __shared__ __attribute__((aligned(16))) char Os[2][TILE];
+    __shared__ float Ls[2][BM], Dd[2][BM];
+    __shared__ __attribute__((aligned(16))) f32x4 Pex[4][8][64];  // [pair][word/4][lane]
+
+    // blockIdx.x = (kv head, sequence), blockIdx.y = key tile: under a causal
+    // mask the first key tiles see the most queries, so they go first
+    const int kt = (int)blockIdx.y;
+    const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
+    const int hpk = s.n_heads / s.n_kv_heads;
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const bool pw = wave < 4;              // P wave (else dS wave)
+    const int pair = wave & 3;
+    const int k0 = kt * BN, kw0 = k0 + pair * 32;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+    const bool keys_ok = kw0 + 32 <= s.n_kv;
+
+    // this wave's operand slice: K (P waves) or V (dS waves), 32 keys x HD
+    const bf16 *kvb = pw ? (const bf16 *)p.k + (long)b * s.n_kv * p.ldk + kvh * HD
+                         : (const bf16 *)p.v + (long)b * s.n_kv * p.ldv + kvh * HD;
+    const long kvld = pw ? p.ldk : p.ldv;
+    bf16x8 kv[2][DS];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int kr = kw0 + 16 * ks + c16;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+            kv[ks][ds] = kr < s.n_kv ? ld_frag(kvb + (long)kr * kvld + 32 * ds + 8 * g) : bf16x8{};
+    }
+    f32x4 acc[DSUB][2];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i) acc[i][0] = acc[i][1] = f32x4{0, 0, 0, 0};
+
+    // (query head, q tile) iterations; the fused path has n_q % 64 == 0 and
+    // n_q == n_kv when causal
+    const int qstart = s.causal ? k0 / BM * BM : 0;
+    const int nqt = s.n_q > qstart ? (s.n_q - qstart) / BM : 0;
+    const int niter = hpk * nqt;
+
+    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const bf16 *)p.q + (long)b * s.n_q * p.ldq), (short)0,
+        (int)((long)s.n_q * p.ldq * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)((const bf16 *)p.dout + (long)b * s.n_q * p.lddo), (short)0,
+        (int)((long)s.n_q * p.lddo * 2), 0x00020000);
+    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.lse + (long)b * s.n_q * s.n_heads), (short)0, (int)((long)s.n_q * s.n_heads * 4),
+        0x00020000);
+    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)(p.d + (long)b * s.n_q * s.n_heads), (short)0, (int)((long)s.n_q * s.n_heads * 4),
+        0x00020000);
+    // DMA of tile `it` into buffer `buf`: wave w moves rows 8 w .. 8 w + 7 of Q
+    // and dO (two 4-row instructions each); waves 0 / 1 also move lse / D.
+    auto dma = [&](int it, int buf) {
+        const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = 8 * wave + 4 * i + lane / 16;
+            const int c = (lane % 16) ^ swz(r);
+            const unsigned oq = (unsigned)(((long)(q0 + r) * p.ldq + h * HD + 8 * c) * 2);
+            const unsigned oo = (unsigned)(((long)(q0 + r) * p.lddo + h * HD + 8 * c) * 2);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void_t *)(Qs[buf] + (8 * wave + 4 * i) * HD * 2), 16, oq, 0, 0, 0);
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(ro, (lds_void_t *)(Os[buf] + (8 * wave + 4 * i) * HD * 2), 16, oo, 0, 0, 0);
+        }
+        if (wave == 0)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void_t *)Ls[buf], 4,
+                                                     (unsigned)(((q0 + lane) * s.n_heads + h) * 4), 0, 0, 0);
+        if (wave == 1)
+            __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void_t *)Dd[buf], 4,
+                                                     (unsigned)(((q0 + lane) * s.n_heads + h) * 4), 0, 0, 0);
+    };
+
+    if (niter > 0) dma(0, 0);
+    for (int it = 0; it < niter; ++it) {
+        const int buf = it & 1;
+        wait_vm0();
+        __syncthreads();  // tile `it` landed; everyone is done with buffer buf ^ 1
+        if (it + 1 < niter) dma(it + 1, buf ^ 1);
+        const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+        const char *Qb = Qs[buf], *Ob = Os[buf];
+        const bool edge = (s.causal && kw0 + 31 > q0) || !keys_ok;
+        f32x4 sc[QS][2];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) sc[qs][0] = sc[qs][1] = f32x4{0, 0, 0, 0};
+        // phase 1: S^T (P waves) or dP^T (dS waves)
+        const char *A1 = pw ? Qb : Ob;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+                const bf16x8 a = frag_row(A1, 16 * qs + c16, 32 * ds + 8 * g);
+                sc[qs][0] = mfma16x16x32(a, kv[0][ds], sc[qs][0]);
+                sc[qs][1] = mfma16x16x32(a, kv[1][ds], sc[qs][1]);
+            }
+        if (pw) {
+            // P = exp2(S c2 - lse2); a fully masked row (lse = -inf) gets P = 0
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+                const float4 l4 = *reinterpret_cast<const float4 *>(&Ls[buf][16 * qs + 4 * g]);
+                const float lqs[4] = {l4.x, l4.y, l4.z, l4.w};
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float lq = lqs[r] == -INFINITY ? INFINITY : lqs[r] * LOG2E;
+#pragma unroll
+                    for (int ks = 0; ks < 2; ++ks)
+                        sc[qs][ks][r] = __builtin_amdgcn_exp2f(sc[qs][ks][r] * c2 - lq);
+                }
+            }
+            if (edge) {
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int ks = 0; ks < 2; ++ks) {
+                            const int qa = q0 + 16 * qs + 4 * g + r, ka = kw0 + 16 * ks + c16;
+                            if (ka >= s.n_kv || (s.causal && ka > qa)) sc[qs][ks][r] = 0.f;
+                        }
+            }
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) Pex[pair][2 * qs + ks][lane] = sc[qs][ks];
+        }
+        __syncthreads();  // P ready
+        if (pw) {
+            // dV^T += dO^T P
+#pragma unroll
+            for (int qst = 0; qst < QST; ++qst) {
+                const bf16x8 pb0 = frag_acc(sc[2 * qst][0], sc[2 * qst + 1][0]);
+                const bf16x8 pb1 = frag_acc(sc[2 * qst][1], sc[2 * qst + 1][1]);
+#pragma unroll
+                for (int i = 0; i < DSUB; ++i) {
+                    const bf16x8 oa = frag_t(Ob, 16 * i, 32 * qst, g, c16);
+                    acc[i][0] = mfma16x16x32(oa, pb0, acc[i][0]);
+                    acc[i][1] = mfma16x16x32(oa, pb1, acc[i][1]);
+                }
+            }
+        } else {
+            // dS = P (dP - D), stored as bf16 dS^T; dK^T += Q^T dS
+            bf16 *dsr = dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv +
+                        (long)(kw0 + c16) * s.n_q + q0 + 4 * g;
+            const long ds_ks = 16L * s.n_q;
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) {
+                const float4 d4 = *reinterpret_cast<const float4 *>(&Dd[buf][16 * qs + 4 * g]);
+                const float dqs[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+                for (int ks = 0; ks < 2; ++ks) {
+                    const f32x4 pv = Pex[pair][2 * qs + ks][lane];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) sc[qs][ks][r] = pv[r] * (sc[qs][ks][r] - dqs[r]);
+                }
+            }
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs) {
+                    bf16x4 v;
+                    v[0] = (bf16)sc[qs][ks][0]; v[1] = (bf16)sc[qs][ks][1];
+                    v[2] = (bf16)sc[qs][ks][2]; v[3] = (bf16)sc[qs][ks][3];
+                    if (keys_ok || kw0 + 16 * ks + c16 < s.n_kv)
+                        *reinterpret_cast<bf16x4 *>(dsr + ks * ds_ks + 16 * qs) = v;
+                }
+#pragma unroll
+            for (int qst = 0; qst < QST; ++qst) {
+                const bf16x8 sb0 = frag_acc(sc[2 * qst][0], sc[2 * qst + 1][0]);
+                const bf16x8 sb1 = frag_acc(sc[2 * qst][1], sc[2 * qst + 1][1]);
+#pragma unroll
+                for (int i = 0; i < DSUB; ++i) {
+                    const bf16x8 qa = frag_t(Qb, 16 * i, 32 * qst, g, c16);
+                    acc[i][0] = mfma16x16x32(qa, sb0, acc[i][0]);
+                    acc[i][1] = mfma16x16x32(qa, sb1, acc[i][1]);
+                }
+            }
+        }
+    }
+    // dK (scaled) from the dS waves, dV from the P waves
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+        const int ka = kw0 + 16 * ks + c16;
+        if (ka >= s.n_kv) continue;
+        const long t = (long)b * s.n_kv + ka;
+        float *out = pw ? p.dv + t * p.lddv + kvh * HD : p.dk + t * p.lddk + kvh * HD;
+        const float sc_ = pw ? 1.0f : s.inv_sqrt_dim;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = acc[i][ks];
+            *reinterpret_cast<float4 *>(out + 16 * i + 4 * g) =
+                make_float4(a[0] * sc_, a[1] * sc_, a[2] * sc_, a[3] * sc_);
+        }
+    }
+}
+
 // dQ[q, :] = inv_sqrt_dim * sum_{k visible} dS[q, k] K[k, :]: one 128 x HD
 // output tile per (q tile, head, sequence) on the GEMM tile routine (A = dS
 // from its transposed [k][q] store, B = K rows; both MN-major).
@@ -734,8 +980,8 @@ __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, c
     using Cfg = Tile16<128, HD, 2, 2>;
     constexpr int TM = 128 / 2 / 16, TN = HD / 2 / 16;
     __shared__ __attribute__((aligned(16))) char smem[2 * (128 + HD) * 128];
-    const int qt = s.causal ? (int)gridDim.x - 1 - (int)blockIdx.x : (int)blockIdx.x;
-    const int h = blockIdx.y, b = blockIdx.z;
+    const int qt = s.causal ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;
+    const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int kvh = h / (s.n_heads / s.n_kv_heads);
     const int q0 = qt * 128;
     const int off = s.n_kv - s.n_q;
@@ -919,7 +1165,7 @@ hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k
     if (dt == DType::BF16) {
         if (!bf16_ok(s)) return hipErrorInvalidValue;
         if (ob && (ldob % 4 || ((uintptr_t)ob & 7u))) return hipErrorInvalidValue;
-        dim3 grid((s.n_q + 127) / 128, s.n_heads, s.n_batch);
+        dim3 grid(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
         if (s.head_dim == 128)
             hipLaunchKernelGGL(fa_fwd_bf16_k<128>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
                                (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
@@ -949,7 +1195,7 @@ hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     if (s.n_kv_heads <= 0 || s.n_heads % s.n_kv_heads) return hipErrorInvalidValue;
     if (p.dt == DType::BF16) {
         if (!bf16_ok(s)) return hipErrorInvalidValue;
-        dim3 grid((s.n_q + 127) / 128, s.n_heads, s.n_batch);
+        dim3 grid(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
         if (s.head_dim == 128)
             hipLaunchKernelGGL(fa_bwd_dq_bf16_k<128>, grid, dim3(NT), 0, st, s, p);
         else
@@ -979,10 +1225,10 @@ size_t fa_bw_ws_bytes(const AttnShape &s) {
 hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipStream_t st) {
     if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
     if (p.dt != DType::BF16 || !fa_bw_fused_ok(s) || !ds_ws) return hipErrorInvalidValue;
-    dim3 gkv((s.n_kv + 127) / 128, s.n_kv_heads, s.n_batch);
-    dim3 gq((s.n_q + 127) / 128, s.n_heads, s.n_batch);
+    dim3 gkv(s.n_kv_heads * s.n_batch, (s.n_kv + 127) / 128);
+    dim3 gq(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
     if (s.head_dim == 128) {
-        hipLaunchKernelGGL((fa_bwd_dkv2_k<128, FA_BM>), gkv, dim3(NT), 0, st, s, p, ds_ws);
+        hipLaunchKernelGGL(fa_bwd_dkv3_k, gkv, dim3(dkv3::NT3), 0, st, s, p, ds_ws);
         hipLaunchKernelGGL(fa_dq_gemm_k<128>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);
     } else {
         hipLaunchKernelGGL((fa_bwd_dkv2_k<64, FA_BM>), gkv, dim3(NT), 0, st, s, p, ds_ws);
@@ -996,7 +1242,7 @@ hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     if (s.n_kv_heads <= 0 || s.n_heads % s.n_kv_heads) return hipErrorInvalidValue;
     if (p.dt == DType::BF16) {
         if (!bf16_ok(s)) return hipErrorInvalidValue;
-        dim3 grid((s.n_kv + 127) / 128, s.n_kv_heads, s.n_batch);
+        dim3 grid(s.n_kv_heads * s.n_batch, (s.n_kv + 127) / 128);
         if (s.head_dim == 128)
             hipLaunchKernelGGL(fa_bwd_dkv_bf16_k<128>, grid, dim3(NT), 0, st, s, p);
         else
