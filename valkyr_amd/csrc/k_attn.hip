@@ -753,6 +753,46 @@ constexpr int TILE = BM * HD * 2;  // bytes of one Q or dO tile
 
 VKH_DEV int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
 
+// Block barrier for LDS hand-offs only: this wave's LDS operations complete,
+// then s_barrier.  (__syncthreads would also wait for the in-flight tile DMA
+// and the dS stores, which the next tile's barrier covers.)  The memory
+// clobber keeps the compiler from moving memory accesses across it.
+VKH_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Buffer resource as four SGPR words (base, base_hi, num_records, flags).
+typedef int sgpr4 __attribute__((ext_vector_type(4)));
+VKH_DEV sgpr4 rsrc4(const void *base, unsigned bytes) {
+    const unsigned long a = (unsigned long)base;
+    sgpr4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32) & 0xffff);
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
+}
+
+// 16-byte global -> LDS DMA of one wave (lane l lands at lds + 16 l).  Issued
+// as inline assembly so the compiler's wait-count tracking does not treat
+// every later LDS read as a possible alias of the in-flight tile (it would
+// wait for the DMA before the current tile's reads); the tile loop waits for
+// the DMA explicitly (vmcnt(0) before the barrier that publishes the tile).
+VKH_DEV void dma16_async(const sgpr4 &rs, const void *lds, unsigned voff) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (int)(unsigned)(unsigned long)(const __attribute__((address_space(3))) char *)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs)
+                 : "memory");
+}
+VKH_DEV void dma4_async(const sgpr4 &rs, const void *lds, unsigned voff) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (int)(unsigned)(unsigned long)(const __attribute__((address_space(3))) char *)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs)
+                 : "memory");
+}
+
 // byte offset of (row r, element col) in a swizzled tile
 VKH_DEV int toff(int r, int col) { return r * (HD * 2) + (((col >> 3) ^ swz(r)) << 4) + (col & 7) * 2; }
 
@@ -807,6 +847,7 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
         for (int ds = 0; ds < DS; ++ds)
             kv[ks][ds] = kr < s.n_kv ? ld_frag(kvb + (long)kr * kvld + 32 * ds + 8 * g) : bf16x8{};
     }
+    wait_vm0();  // the K / V slice is in registers before any DMA is queued
     f32x4 acc[DSUB][2];
 #pragma unroll
     for (int i = 0; i < DSUB; ++i) acc[i][0] = acc[i][1] = f32x4{0, 0, 0, 0};
@@ -817,45 +858,40 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
     const int nqt = s.n_q > qstart ? (s.n_q - qstart) / BM : 0;
     const int niter = hpk * nqt;
 
-    const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const bf16 *)p.q + (long)b * s.n_q * p.ldq), (short)0,
-        (int)((long)s.n_q * p.ldq * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)((const bf16 *)p.dout + (long)b * s.n_q * p.lddo), (short)0,
-        (int)((long)s.n_q * p.lddo * 2), 0x00020000);
-    const __amdgpu_buffer_rsrc_t rl = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.lse + (long)b * s.n_q * s.n_heads), (short)0, (int)((long)s.n_q * s.n_heads * 4),
-        0x00020000);
-    const __amdgpu_buffer_rsrc_t rd = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)(p.d + (long)b * s.n_q * s.n_heads), (short)0, (int)((long)s.n_q * s.n_heads * 4),
-        0x00020000);
-    // DMA of tile `it` into buffer `buf`: wave w moves rows 8 w .. 8 w + 7 of Q
-    // and dO (two 4-row instructions each); waves 0 / 1 also move lse / D.
+    const sgpr4 rq = rsrc4((const bf16 *)p.q + (long)b * s.n_q * p.ldq,
+                           (unsigned)((long)s.n_q * p.ldq * 2));
+    const sgpr4 ro = rsrc4((const bf16 *)p.dout + (long)b * s.n_q * p.lddo,
+                           (unsigned)((long)s.n_q * p.lddo * 2));
+    const sgpr4 rl = rsrc4(p.lse + (long)b * s.n_q * s.n_heads, (unsigned)((long)s.n_q * s.n_heads * 4));
+    const sgpr4 rd = rsrc4(p.d + (long)b * s.n_q * s.n_heads, (unsigned)((long)s.n_q * s.n_heads * 4));
+    // DMA of tile `it` into buffer `buf`, issued by the P waves only (the dS
+    // waves' global stores then never sit in front of a wait for the tile):
+    // P wave w moves rows 16 w .. 16 w + 15 of Q and dO (four 4-row
+    // instructions each); waves 0 / 1 also move lse / D.
+    // Row r = 16 w + 4 i + g of instruction i has swz(r) = 4 g + i, so lane
+    // (g, c16) fetches chunk (c16 ^ 4 g) ^ i.
+    const int cb = c16 ^ (g << 2);
     auto dma = [&](int it, int buf) {
         const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+        const int r = q0 + 16 * wave + g;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = 8 * wave + 4 * i + lane / 16;
-            const int c = (lane % 16) ^ swz(r);
-            const unsigned oq = (unsigned)(((long)(q0 + r) * p.ldq + h * HD + 8 * c) * 2);
-            const unsigned oo = (unsigned)(((long)(q0 + r) * p.lddo + h * HD + 8 * c) * 2);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void_t *)(Qs[buf] + (8 * wave + 4 * i) * HD * 2), 16, oq, 0, 0, 0);
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(ro, (lds_void_t *)(Os[buf] + (8 * wave + 4 * i) * HD * 2), 16, oo, 0, 0, 0);
+        for (int i = 0; i < 4; ++i) {
+            const int col = h * HD + 8 * (cb ^ i);
+            const unsigned oq = (unsigned)(((r + 4 * i) * (int)p.ldq + col) * 2);
+            const unsigned oo = (unsigned)(((r + 4 * i) * (int)p.lddo + col) * 2);
+            dma16_async(rq, Qs[buf] + (16 * wave + 4 * i) * HD * 2, oq);
+            dma16_async(ro, Os[buf] + (16 * wave + 4 * i) * HD * 2, oo);
         }
-        if (wave == 0)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void_t *)Ls[buf], 4,
-                                                     (unsigned)(((q0 + lane) * s.n_heads + h) * 4), 0, 0, 0);
-        if (wave == 1)
-            __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void_t *)Dd[buf], 4,
-                                                     (unsigned)(((q0 + lane) * s.n_heads + h) * 4), 0, 0, 0);
+        if (wave == 0) dma4_async(rl, Ls[buf], (unsigned)(((q0 + lane) * s.n_heads + h) * 4));
+        if (wave == 1) dma4_async(rd, Dd[buf], (unsigned)(((q0 + lane) * s.n_heads + h) * 4));
     };
 
-    if (niter > 0) dma(0, 0);
+    if (niter > 0 && pw) dma(0, 0);
     for (int it = 0; it < niter; ++it) {
         const int buf = it & 1;
-        wait_vm0();
-        __syncthreads();  // tile `it` landed; everyone is done with buffer buf ^ 1
-        if (it + 1 < niter) dma(it + 1, buf ^ 1);
+        if (pw) wait_vm0();
+        lds_barrier();  // tile `it` landed; everyone is done with buffer buf ^ 1 and Pex
+        if (it + 1 < niter && pw) dma(it + 1, buf ^ 1);
         const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
         const char *Qb = Qs[buf], *Ob = Os[buf];
         const bool edge = (s.causal && kw0 + 31 > q0) || !keys_ok;
@@ -902,7 +938,7 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
 #pragma unroll
                 for (int ks = 0; ks < 2; ++ks) Pex[pair][2 * qs + ks][lane] = sc[qs][ks];
         }
-        __syncthreads();  // P ready
+        lds_barrier();  // P ready
         if (pw) {
             // dV^T += dO^T P
 #pragma unroll
