@@ -123,7 +123,7 @@ def bench_fa_bwd(args):
         K.fa_bw_d(p, o, dout, d, dout16, stream=s)
         K.fa_backward(p, q, k, vv, dout16, lse, d, dq, dk, dv, ws, stream=s)
 
-    for _ in range(3):
+    for _ in range(10):  # clocks settle over the first calls
         once()
     s.synchronize()
     e0, e1 = Event(), Event()
@@ -135,7 +135,6 @@ def bench_fa_bwd(args):
     ms = e0.elapsed_ms(e1) / args.fa_reps
     flops = 10.0 * B * H * hd * S * (S + 1) / 2
     tflops = flops / (ms * 1e-3) / 1e12
-    # HBM traffic floor of one call: bf16 Q,K,V,dO read, fp32 O/dO for D, fp32 dQ/dK/dV written
     print(f"[bench] fa-bwd {ms:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
     return dict(ms=ms, flops=flops, tflops=tflops)
 
@@ -226,7 +225,7 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
-    ap.add_argument("--fa-reps", type=int, default=20)
+    ap.add_argument("--fa-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="all", choices=["all", "step", "fa"],
                     help="run only the step or only the attention benchmark (profiling runs)")

@@ -739,10 +739,10 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
 //
 // Q / dO tiles (64 x 128 bf16) arrive by DMA (buffer_load ... lds) into
 // unpadded LDS rows with a 16-byte chunk swizzle: chunk c of row r sits at
-// c ^ swz(r), swz(r) = 4 (r & 3) + ((r >> 2) & 3).  swz is a bijection on 16
-// consecutive rows (the 16 rows of a b128 fragment read hit 16 different
-// chunks) and, for the 4 rows x 2 adjacent chunks of a transposing read,
-// swz >> 1 differs between the 4 rows, so both read kinds are conflict-free.
+// c ^ (r & 15).  Measured on MI355X with the two fragment read patterns of
+// this kernel (b128 rows, transposing b64): both run at the speed of a
+// padded-pitch layout (no bank conflicts), where an unswizzled 256-byte pitch
+// is 4x (b128) and 2.3x (transposing) slower.
 // The next tile's DMA is in flight during the current tile (double buffer);
 // there are two barriers per tile (P ready, tile done).
 
@@ -751,7 +751,7 @@ constexpr int NT3 = 512, BN = 128, BM = 64, HD = 128, DS = HD / 32, DSUB = HD / 
 constexpr int QS = BM / 16, QST = BM / 32;
 constexpr int TILE = BM * HD * 2;  // bytes of one Q or dO tile
 
-VKH_DEV int swz(int r) { return ((r & 3) << 2) | ((r >> 2) & 3); }
+VKH_DEV int swz(int r) { return r & 15; }
 
 // Block barrier for LDS hand-offs only: this wave's LDS operations complete,
 // then s_barrier.  (__syncthreads would also wait for the in-flight tile DMA
@@ -868,15 +868,14 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
     // waves' global stores then never sit in front of a wait for the tile):
     // P wave w moves rows 16 w .. 16 w + 15 of Q and dO (four 4-row
     // instructions each); waves 0 / 1 also move lse / D.
-    // Row r = 16 w + 4 i + g of instruction i has swz(r) = 4 g + i, so lane
-    // (g, c16) fetches chunk (c16 ^ 4 g) ^ i.
-    const int cb = c16 ^ (g << 2);
+    // Instruction i of P wave w fills tile rows 16 w + 4 i + g; lane (g, c16)
+    // fetches the logical chunk stored at physical chunk c16 of its row.
     auto dma = [&](int it, int buf) {
         const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
         const int r = q0 + 16 * wave + g;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const int col = h * HD + 8 * (cb ^ i);
+            const int col = h * HD + 8 * (c16 ^ swz(16 * wave + 4 * i + g));
             const unsigned oq = (unsigned)(((r + 4 * i) * (int)p.ldq + col) * 2);
             const unsigned oo = (unsigned)(((r + 4 * i) * (int)p.lddo + col) * 2);
             dma16_async(rq, Qs[buf] + (16 * wave + 4 * i) * HD * 2, oq);

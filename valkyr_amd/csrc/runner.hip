@@ -91,6 +91,18 @@ struct vkh_runner {
          *dxb[2] = {nullptr, nullptr};
     bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward
     GemmWs gws{nullptr, 0};
+    // Concurrent weight gradients (bf16 full fine-tune): each layer's dW GEMMs
+    // and its Adam update run on a second stream one layer behind the main
+    // stream's backward, reading per-layer copies of the bf16 gradients.
+    struct LayerGrads {
+        bf16 *dyb = nullptr, *gub = nullptr, *midb = nullptr, *qkvb = nullptr;
+    };
+    bool concurrent = false;
+    hipStream_t side = nullptr;
+    std::vector<hipEvent_t> ev_layer;
+    hipEvent_t ev_side = nullptr;
+    std::vector<LayerGrads> lg;
+    GemmWs gws2{nullptr, 0};
     std::vector<Acts> acts;
     float *x_emb = nullptr, *fn_out = nullptr, *ce_lse = nullptr, *loss_row = nullptr,
           *loss_mean = nullptr;
@@ -113,6 +125,10 @@ struct vkh_runner {
 
     ~vkh_runner() {
         if (own) (void)hipStreamSynchronize(own);
+        if (side) (void)hipStreamSynchronize(side);
+        for (hipEvent_t e : ev_layer) (void)hipEventDestroy(e);
+        if (ev_side) (void)hipEventDestroy(ev_side);
+        if (side) (void)hipStreamDestroy(side);
         for (void *p : allocs) (void)hipFree(p);
         if (tok_h) (void)hipHostFree(tok_h);
         if (tgt_h) (void)hipHostFree(tgt_h);
@@ -331,6 +347,26 @@ struct vkh_runner {
                 VKH_TRY(alloc(w, wsb));
                 gws = GemmWs{w, wsb};
             }
+            concurrent = !lora;
+            if (concurrent) {
+                VKH_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+                ev_layer.assign(L, nullptr);
+                for (int l = 0; l < L; ++l)
+                    VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], hipEventDisableTiming));
+                VKH_HIP(hipEventCreateWithFlags(&ev_side, hipEventDisableTiming));
+                lg.assign(L, LayerGrads{});
+                for (int l = 0; l < L; ++l) {
+                    VKH_TRY(alloc(lg[l].dyb, (size_t)T * D));
+                    VKH_TRY(alloc(lg[l].gub, (size_t)T * 2 * F));
+                    VKH_TRY(alloc(lg[l].midb, (size_t)T * D));
+                    VKH_TRY(alloc(lg[l].qkvb, (size_t)T * qkvd));
+                }
+                if (wsb) {
+                    char *w = nullptr;
+                    VKH_TRY(alloc(w, wsb));
+                    gws2 = GemmWs{w, wsb};
+                }
+            }
         } else {
             VKH_TRY(alloc(fn_out, (size_t)T * D));
         }
@@ -525,12 +561,27 @@ struct vkh_runner {
     }
     // dW[N, K] = dy[T, N]^T x[T, K] (overwrite)
     vkh_status linear_dw(Mat dy, Mat x, const Span &w, int N, int K) {
+        return linear_dw_on(dy, x, w, N, K, gws, cur);
+    }
+    vkh_status linear_dw_on(Mat dy, Mat x, const Span &w, int N, int K, const GemmWs &ws,
+                            hipStream_t st) {
         if (lora) return VKH_OK;  // base weights frozen
         if (b16())
             VKH_HIP(g16_tn((const bf16 *)dy.p, dy.ld, (const bf16 *)x.p, x.ld, Gd(w), K, T, N, K, 1.f,
-                           0.f, gws, cur));
+                           0.f, ws, st));
         else
-            VKH_HIP(gemm_tn(pr, dy, x, Gd(w), K, T, N, K, 1.f, 0.f, cur));
+            VKH_HIP(gemm_tn(pr, dy, x, Gd(w), K, T, N, K, 1.f, 0.f, st));
+        return VKH_OK;
+    }
+    // The four weight-gradient GEMMs of layer l on the side stream (concurrent mode).
+    vkh_status layer_dw_side(int l) {
+        Acts &a = acts[l];
+        LayerSpans &s = ls[l];
+        const LayerGrads &g = lg[l];
+        VKH_TRY(linear_dw_on(matb(g.dyb, D), m_gated(a), s.t[8], D, F, gws2, side));
+        VKH_TRY(linear_dw_on(matb(g.gub, 2 * F), m_n2(a), s.t[6], 2 * F, D, gws2, side));
+        VKH_TRY(linear_dw_on(matb(g.midb, D), m_attn(a), s.t[4], D, qd, gws2, side));
+        VKH_TRY(linear_dw_on(matb(g.qkvb, qkvd), m_n1(a), s.t[1], qkvd, D, gws2, side));
         return VKH_OK;
     }
 
@@ -626,6 +677,14 @@ struct vkh_runner {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const float *x_in = l == 0 ? x_emb : acts[l - 1].y;
+        // concurrent mode: this layer's own gradient copies; dW is deferred to the side stream
+        bf16 *d_gub = concurrent ? lg[l].gub : this->d_gub;
+        bf16 *d_midb = concurrent ? lg[l].midb : this->d_midb;
+        bf16 *d_qkvb = concurrent ? lg[l].qkvb : this->d_qkvb;
+        auto linear_dw = [&](Mat dy_, Mat x_, const Span &w_, int N_, int K_) -> vkh_status {
+            if (concurrent) return VKH_OK;
+            return this->linear_dw(dy_, x_, w_, N_, K_);
+        };
         const Mat mdy = b16() ? matb(dyb, D) : matf(dy, D);
         // transformer.zig:1967-2070 (order), train_decoder.zig:340-498 (math)
         // down: d_gated = dy W_down;  dW_down = dy^T gated
@@ -695,7 +754,9 @@ struct vkh_runner {
         return VKH_OK;
     }
 
-    vkh_status forward_backward_enqueue() {
+    // with_adam: the concurrent mode applies Adam inside the backward (per layer
+    // on the side stream); otherwise the caller enqueues adam_enqueue() after.
+    vkh_status forward_backward_enqueue(bool with_adam) {
         VKH_TRY(forward_all());
         const CceShape cs{T, V, D, 0.f, 0.f};
         // head backward: dh and dW_lm (tied: the embed grad slot)
@@ -710,11 +771,22 @@ struct vkh_runner {
                                 cce_work, cur));
             VKH_HIP(cce_backward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, dz, d_fn, dw_lm, 0.f, cur));
         }
-        VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), dx[0], dxb[0], nullptr,
-                                 Gd(final_norm), partial, T, D, cfg.rms_eps, 0, cur));
+        VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), dx[0],
+                                 concurrent ? lg[L - 1].dyb : dxb[0], nullptr, Gd(final_norm),
+                                 partial, T, D, cfg.rms_eps, 0, cur));
         int c = 0;
         for (int l = L - 1; l >= 0; --l) {
-            VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
+            if (concurrent) {
+                VKH_TRY(layer_backward(l, dx[c], lg[l].dyb, dx[c ^ 1], l > 0 ? lg[l - 1].dyb : nullptr));
+                // layer l's gradient inputs are final: its dW GEMMs (and, with Adam,
+                // its update) run on the side stream while the main stream goes on
+                VKH_HIP(hipEventRecord(ev_layer[l], cur));
+                VKH_HIP(hipStreamWaitEvent(side, ev_layer[l], 0));
+                VKH_TRY(layer_dw_side(l));
+                if (with_adam) VKH_TRY(adam_span(ls[l].t[0].off, layer_end(l), side));
+            } else {
+                VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
+            }
             c ^= 1;
         }
         if (!lora) {
@@ -722,6 +794,29 @@ struct vkh_runner {
             if (!tied) VKH_HIP(fill_f32(dE, embed.numel, 0.f, cur));
             VKH_HIP(embedding_backward(dx[c], tok_d, dE, T, D, V, tied, embed_work, cur));
         }
+        if (concurrent) {
+            // embed, final norm, lm_head: the span before layer 0
+            if (with_adam) VKH_TRY(adam_span(0, ls[0].t[0].off, cur));
+            VKH_HIP(hipEventRecord(ev_side, side));
+            VKH_HIP(hipStreamWaitEvent(cur, ev_side, 0));
+        }
+        return VKH_OK;
+    }
+
+    // end (arena offset) of layer l's tensors
+    size_t layer_end(int l) const {
+        const LayerSpans &s = ls[l];
+        const Span &last = s.t[10].numel ? s.t[10] : s.t[8];
+        return last.off + last.numel;
+    }
+
+    // Adam over the arena range [b, e) of a full fine-tune (adam_step.comp:45-61)
+    vkh_status adam_span(size_t b, size_t e, hipStream_t st) {
+        const float t = (float)step_t;
+        const float bc1 = 1.0f - powf(cfg.beta1, t);
+        const float bc2 = 1.0f - powf(cfg.beta2, t);
+        VKH_HIP(adam_step(P + b, G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
+                          cfg.eps_adam, bc1, bc2, 0.f, b16() ? Pb + b : nullptr, st));
         return VKH_OK;
     }
 
@@ -774,10 +869,10 @@ struct vkh_runner {
     }
 
     vkh_status step_enqueue(bool with_adam) {
-        VKH_TRY(forward_backward_enqueue());
+        VKH_TRY(forward_backward_enqueue(with_adam));
         VKH_TRY(record_loss());
         if (with_adam) {
-            VKH_TRY(adam_enqueue());
+            if (!concurrent) VKH_TRY(adam_enqueue());
             step_t += 1;  // transformer.zig:1318
         }
         return VKH_OK;
@@ -1196,8 +1291,8 @@ vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
             if (us >= budget.microseconds && n > 0) break;
             if (budget.microseconds == 0) break;
         }
-        st = r->forward_backward_enqueue();
-        if (st == VKH_OK) st = r->adam_enqueue();
+        st = r->forward_backward_enqueue(true);
+        if (st == VKH_OK && !r->concurrent) st = r->adam_enqueue();
         if (st != VKH_OK) break;
         r->step_t += 1;
         ++n;
