@@ -406,18 +406,24 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
         wait_vm0();
         __syncthreads();  // slab kt landed for every wave; slab kt-1's buffer is free
         if (kt + 1 < nk) issue(kt + 1, smem + ((kt + 1) & 1) * STAGE);
+        // Both k-steps' fragments are requested before the first MFMA, so the
+        // LDS latency of the second set hides behind the first set's MFMAs.
+        bf16x8 af[2][TM], bfr[2][TN];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-            bf16x8 af[TM], bfr[TN];
 #pragma unroll
-            for (int i = 0; i < TM; ++i) af[i] = frag16<LA, BM>(cur, wm * WM + 16 * i, ks, lane);
+            for (int i = 0; i < TM; ++i) af[ks][i] = frag16<LA, BM>(cur, wm * WM + 16 * i, ks, lane);
 #pragma unroll
-            for (int j = 0; j < TN; ++j) bfr[j] = frag16<LB, BN>(cur + ABYTES, wn * WN + 16 * j, ks, lane);
+            for (int j = 0; j < TN; ++j)
+                bfr[ks][j] = frag16<LB, BN>(cur + ABYTES, wn * WN + 16 * j, ks, lane);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
             for (int i = 0; i < TM; ++i)
 #pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
-        }
+                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[ks][i], bfr[ks][j], acc[i][j]);
     }
     __syncthreads();  // the caller may reuse smem
 }

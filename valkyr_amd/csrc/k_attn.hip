@@ -249,6 +249,69 @@ __global__ void fa_bw_d_k(AttnShape s, const float *o, long ldo, const float *do
     if (lane == 0) d[t * s.n_heads + h] = (float)acc;
 }
 
+// Several (row, head) items per wave for head_dim 64 / 128: LPH = head_dim / 8
+// lanes per item, 8 elements (two float4 of O and of dO) per lane, the fp64
+// dot product reduced inside a DPP row; the next item's loads are issued
+// before the current one is reduced.
+template <int CTRL>
+VKH_DEV double dppd(double v) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+template <int LPH>
+__global__ __launch_bounds__(NT) void fa_bw_d8_k(AttnShape s, const float *o, long ldo,
+                                                  const float *dout, long lddo, float *d,
+                                                  bf16 *dout16, long lddo16) {
+    constexpr int G = 64 / LPH;
+    const int lane = threadIdx.x % 64, j = lane % LPH, g = lane / LPH;
+    const long rows = (long)s.n_batch * s.n_q * s.n_heads;
+    const long stride = (long)gridDim.x * (NT / 64) * G;
+    const int hd = s.head_dim;
+    struct It { float4 o0, o1, d0, d1; };
+    auto fetch = [&](long it, It &x) {
+        if (it < rows) {
+            const long t = it / s.n_heads;
+            const int h = (int)(it % s.n_heads);
+            const float4 *op = reinterpret_cast<const float4 *>(o + t * ldo + h * hd + 8 * j);
+            const float4 *dp = reinterpret_cast<const float4 *>(dout + t * lddo + h * hd + 8 * j);
+            x.o0 = op[0]; x.o1 = op[1]; x.d0 = dp[0]; x.d1 = dp[1];
+        } else {
+            x.o0 = x.o1 = x.d0 = x.d1 = make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    long it = ((long)blockIdx.x * (NT / 64) + threadIdx.x / 64) * G + g;
+    const long wave_first = it - g;
+    It cur;
+    fetch(it, cur);
+    for (long wb = wave_first; wb < rows; wb += stride, it += stride) {
+        It nxt;
+        if (wb + stride < rows) fetch(it + stride, nxt);
+        float dv[8] = {cur.d0.x, cur.d0.y, cur.d0.z, cur.d0.w, cur.d1.x, cur.d1.y, cur.d1.z, cur.d1.w};
+        const float ov[8] = {cur.o0.x, cur.o0.y, cur.o0.z, cur.o0.w, cur.o1.x, cur.o1.y, cur.o1.z, cur.o1.w};
+        const long t = it / s.n_heads;
+        const int h = (int)(it % s.n_heads);
+        if (dout16) {
+            // D must pair with the dO the MFMA kernels see
+            const bf16x8 r = cvt8(dv[0], dv[1], dv[2], dv[3], dv[4], dv[5], dv[6], dv[7]);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) dv[i] = (float)r[i];
+            if (it < rows) *reinterpret_cast<bf16x8 *>(dout16 + t * lddo16 + h * hd + 8 * j) = r;
+        }
+        double acc = 0;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) acc += (double)ov[i] * (double)dv[i];
+        acc += dppd<0xB1>(acc);
+        acc += dppd<0x4E>(acc);
+        acc += dppd<0x141>(acc);
+        if constexpr (LPH == 16) acc += dppd<0x140>(acc);
+        if (j == 0 && it < rows) d[t * s.n_heads + h] = (float)acc;
+        if (wb + stride < rows) cur = nxt;
+    }
+}
+
 // ── backward: dK, dV (fa_bw_dkv.comp) ────────────────────────────────
 // Block: 128 keys of one kv head and sequence; 4 waves x 32 keys, K and V
 // fragments resident in registers; loops over the heads of the GQA group
@@ -743,13 +806,14 @@ __global__ __launch_bounds__(NT, 1) void fa_bwd_dkv2_k(AttnShape s, AttnPtrs p, 
 // this kernel (b128 rows, transposing b64): both run at the speed of a
 // padded-pitch layout (no bank conflicts), where an unswizzled 256-byte pitch
 // is 4x (b128) and 2.3x (transposing) slower.
-// The next tile's DMA is in flight during the current tile (double buffer);
-// there are two barriers per tile (P ready, tile done).
+// The next two tiles' DMA is in flight during the current tile (three
+// buffers); there are two barriers per tile (P ready, tile done).
 
 namespace dkv3 {
 constexpr int NT3 = 512, BN = 128, BM = 64, HD = 128, DS = HD / 32, DSUB = HD / 16;
 constexpr int QS = BM / 16, QST = BM / 32;
 constexpr int TILE = BM * HD * 2;  // bytes of one Q or dO tile
+constexpr int NBUF = 3;            // tile buffers (two DMA batches in flight)
 
 VKH_DEV int swz(int r) { return r & 15; }
 
@@ -817,9 +881,9 @@ VKH_DEV bf16x8 frag_t(const char *tile, int c0, int k0, int g, int l16) {
 
 __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnPtrs p, bf16 *dsw) {
     using namespace dkv3;
-    __shared__ __attribute__((aligned(16))) char Qs[2][TILE];
-    __shared__ __attribute__((aligned(16))) char Os[2][TILE];
-    __shared__ float Ls[2][BM], Dd[2][BM];
+    __shared__ __attribute__((aligned(16))) char Qs[NBUF][TILE];
+    __shared__ __attribute__((aligned(16))) char Os[NBUF][TILE];
+    __shared__ float Ls[NBUF][BM], Dd[NBUF][BM];
     __shared__ __attribute__((aligned(16))) f32x4 Pex[4][8][64];  // [pair][word/4][lane]
 
     // blockIdx.x = (kv head, sequence), blockIdx.y = key tile: under a causal
@@ -885,12 +949,24 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
         if (wave == 1) dma4_async(rd, Dd[buf], (unsigned)(((q0 + lane) * s.n_heads + h) * 4));
     };
 
-    if (niter > 0 && pw) dma(0, 0);
+    // Three tile buffers, two tiles in flight: at the top of iteration `it` a
+    // P wave waits until only the newest batch (tile it + 1) is outstanding.
+    if (pw) {
+        if (niter > 0) dma(0, 0);
+        if (niter > 1) dma(1, 1);
+    }
     for (int it = 0; it < niter; ++it) {
-        const int buf = it & 1;
-        if (pw) wait_vm0();
-        lds_barrier();  // tile `it` landed; everyone is done with buffer buf ^ 1 and Pex
-        if (it + 1 < niter && pw) dma(it + 1, buf ^ 1);
+        const int buf = it % NBUF;
+        if (pw) {
+            if (it + 1 < niter) {
+                if (wave < 2) __builtin_amdgcn_s_waitcnt(0x0f70 | 9);  // 8 tile + 1 lse/D load
+                else __builtin_amdgcn_s_waitcnt(0x0f70 | 8);
+            } else {
+                wait_vm0();
+            }
+        }
+        lds_barrier();  // tile `it` landed; everyone is done with buffer (it + 2) % 3 and Pex
+        if (it + 2 < niter && pw) dma(it + 2, (it + 2) % NBUF);
         const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
         const char *Qb = Qs[buf], *Ob = Os[buf];
         const bool edge = (s.causal && kw0 + 31 > q0) || !keys_ok;
@@ -1220,6 +1296,19 @@ hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *do
                    float *d, bf16 *dout_bf16, long lddo16, hipStream_t st) {
     const long rows = (long)s.n_batch * s.n_q * s.n_heads;
     if (rows <= 0) return hipSuccess;
+    const bool al = ((uintptr_t)o & 15) == 0 && ((uintptr_t)dout & 15) == 0 && ldo % 4 == 0 &&
+                    lddo % 4 == 0 && (!dout_bf16 || (((uintptr_t)dout_bf16 & 15) == 0 && lddo16 % 8 == 0));
+    if ((s.head_dim == 128 || s.head_dim == 64) && al) {
+        const int lph = s.head_dim / 8, per_block = (NT / 64) * (64 / lph);
+        const long grid = std::min<long>(4096, (rows + 2L * per_block - 1) / (2L * per_block));
+        if (lph == 16)
+            hipLaunchKernelGGL(fa_bw_d8_k<16>, dim3((unsigned)grid), dim3(NT), 0, st, s, o, ldo, dout,
+                               lddo, d, dout_bf16, lddo16);
+        else
+            hipLaunchKernelGGL(fa_bw_d8_k<8>, dim3((unsigned)grid), dim3(NT), 0, st, s, o, ldo, dout,
+                               lddo, d, dout_bf16, lddo16);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(fa_bw_d_k, dim3(rows_grid(rows)), dim3(NT), 0, st, s, o, ldo, dout, lddo, d,
                        dout_bf16, lddo16);
     return hipGetLastError();
