@@ -1083,6 +1083,162 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
     }
 }
 
+// ── forward v3 (head_dim 128): DMA-staged K / V tiles ────────────────────
+// One (q tile of 128 rows, head, sequence) per block, 4 waves x 32 queries,
+// Q fragments in registers.  64-key K and V tiles arrive by DMA into the
+// swizzled LDS layout of the backward kernel (two buffers, the next tile in
+// flight while the current one computes, one barrier per tile); K feeds the
+// score MFMAs as row fragments and V^T comes straight from the row-major V
+// tile through the transposing LDS read (no transposed staging copy).
+__global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, long ldq,
+                                                     const bf16 *k, long ldk, const bf16 *v,
+                                                     long ldv, float *o, long ldo, float *lse,
+                                                     bf16 *ob, long ldob) {
+    using namespace dkv3;
+    constexpr int FBM = 128, FBN = 64, KT = FBN * HD * 2;
+    __shared__ __attribute__((aligned(16))) char Ks[2][KT];
+    __shared__ __attribute__((aligned(16))) char Vs[2][KT];
+
+    const int nqt = (s.n_q + FBM - 1) / FBM;
+    // blockIdx.x = (head, sequence), blockIdx.y = q tile, heaviest (last) first
+    const int qt = s.causal ? nqt - 1 - (int)blockIdx.y : (int)blockIdx.y;
+    const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
+    const int kvh = h / (s.n_heads / s.n_kv_heads);
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int q0 = qt * FBM, qw0 = q0 + wave * 32;
+    const int off = s.n_kv - s.n_q;
+    const bf16 *qb = q + (long)b * s.n_q * ldq + h * HD;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+
+    bf16x8 qf[2][DS];
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int qr = qw0 + 16 * qs + c16;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+            qf[qs][ds] = qr < s.n_q ? ld_frag(qb + (long)qr * ldq + 32 * ds + 8 * g) : bf16x8{};
+    }
+    wait_vm0();  // Q fragments are in registers before any DMA is queued
+    f32x4 oacc[DSUB][2];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i) oacc[i][0] = oacc[i][1] = f32x4{0, 0, 0, 0};
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+
+    int kend = s.n_kv;
+    if (s.causal) kend = min(s.n_kv, q0 + FBM + off);
+    const int nkt = (kend + FBN - 1) / FBN;
+    const sgpr4 rk = rsrc4(k + (long)b * s.n_kv * ldk, (unsigned)((long)s.n_kv * ldk * 2));
+    const sgpr4 rv = rsrc4(v + (long)b * s.n_kv * ldv, (unsigned)((long)s.n_kv * ldv * 2));
+    // wave w moves rows 16 w .. 16 w + 15 of the K and V tiles (keys past
+    // n_kv read as zero through the buffer bound)
+    auto dma = [&](int kt, int buf) {
+        const int k0 = kt * FBN;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int r = 16 * wave + 4 * i + g;
+            const int c = c16 ^ swz(r);
+            dma16_async(rk, Ks[buf] + (16 * wave + 4 * i) * HD * 2,
+                        (unsigned)(((k0 + r) * (int)ldk + kvh * HD + 8 * c) * 2));
+            dma16_async(rv, Vs[buf] + (16 * wave + 4 * i) * HD * 2,
+                        (unsigned)(((k0 + r) * (int)ldv + kvh * HD + 8 * c) * 2));
+        }
+    };
+    if (nkt > 0) dma(0, 0);
+    const int wave_last_q = min(qw0 + 31, s.n_q - 1);
+    for (int kt = 0; kt < nkt; ++kt) {
+        const int k0 = kt * FBN, buf = kt & 1;
+        wait_vm0();
+        lds_barrier();  // tile kt landed; everyone is done with buffer buf ^ 1
+        if (kt + 1 < nkt) dma(kt + 1, buf ^ 1);
+        // keys beyond this wave's last visible key are masked; skip if all are
+        if (s.causal && k0 > wave_last_q + off) continue;
+        const char *Kb = Ks[buf], *Vb = Vs[buf];
+
+        f32x4 st[4][2];
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) st[ks][0] = st[ks][1] = f32x4{0, 0, 0, 0};
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds)
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks) {
+                const bf16x8 kf = frag_row(Kb, 16 * ks + c16, 32 * ds + 8 * g);
+                st[ks][0] = mfma16x16x32(kf, qf[0][ds], st[ks][0]);
+                st[ks][1] = mfma16x16x32(kf, qf[1][ds], st[ks][1]);
+            }
+        const bool edge = (s.causal && k0 + FBN - 1 > qw0 + off) || k0 + FBN > s.n_kv;
+        bf16x8 pf[2][2];
+#pragma unroll
+        for (int qs = 0; qs < 2; ++qs) {
+            const int qa = qw0 + 16 * qs + c16;
+            float mt = -INFINITY;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    float x = st[ks][qs][r] * c2;
+                    if (edge) {
+                        const int ka = k0 + 16 * ks + 4 * g + r;
+                        if (ka >= s.n_kv || (s.causal && ka > qa + off)) x = -INFINITY;
+                    }
+                    st[ks][qs][r] = x;
+                    mt = fmaxf(mt, x);
+                }
+            mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+            mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+            const float mn = fmaxf(m[qs], mt);
+            const float so = (m[qs] == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(m[qs] - mn);
+            float lt = 0.f;
+#pragma unroll
+            for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float x = st[ks][qs][r];
+                    const float pv = (x == -INFINITY) ? 0.f : __builtin_amdgcn_exp2f(x - mn);
+                    st[ks][qs][r] = pv;
+                    lt += pv;
+                }
+            lt += __shfl_xor(lt, 16, 64);
+            lt += __shfl_xor(lt, 32, 64);
+            l[qs] = l[qs] * so + lt;
+            m[qs] = mn;
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) oacc[i][qs] *= so;
+            pf[qs][0] = frag_acc(st[0][qs], st[1][qs]);
+            pf[qs][1] = frag_acc(st[2][qs], st[3][qs]);
+        }
+#pragma unroll
+        for (int kst = 0; kst < 2; ++kst)
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) {
+                const bf16x8 vf = frag_t(Vb, 16 * i, 32 * kst, g, c16);
+                oacc[i][0] = mfma16x16x32(vf, pf[0][kst], oacc[i][0]);
+                oacc[i][1] = mfma16x16x32(vf, pf[1][kst], oacc[i][1]);
+            }
+    }
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs) {
+        const int qa = qw0 + 16 * qs + c16;
+        if (qa >= s.n_q) continue;
+        const float inv = l[qs] > 0.f ? 1.0f / l[qs] : 0.f;
+        float *orow = o + ((long)b * s.n_q + qa) * ldo + h * HD;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = oacc[i][qs];
+            const float4 ov = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
+            *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) = ov;
+            if (ob) {
+                bf16x4 bv;
+                bv[0] = (bf16)ov.x; bv[1] = (bf16)ov.y; bv[2] = (bf16)ov.z; bv[3] = (bf16)ov.w;
+                *reinterpret_cast<bf16x4 *>(ob + ((long)b * s.n_q + qa) * ldob + h * HD + 16 * i + 4 * g) = bv;
+            }
+        }
+        if (lse && g == 0)
+            lse[((long)b * s.n_q + qa) * s.n_heads + h] =
+                l[qs] > 0.f ? (m[qs] + log2f(l[qs])) * LN2 : -INFINITY;
+    }
+}
+
 // dQ[q, :] = inv_sqrt_dim * sum_{k visible} dS[q, k] K[k, :]: one 128 x HD
 // output tile per (q tile, head, sequence) on the GEMM tile routine (A = dS
 // from its transposed [k][q] store, B = K rows; both MN-major).
@@ -1277,7 +1433,12 @@ hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k
         if (!bf16_ok(s)) return hipErrorInvalidValue;
         if (ob && (ldob % 4 || ((uintptr_t)ob & 7u))) return hipErrorInvalidValue;
         dim3 grid(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
-        if (s.head_dim == 128)
+        const bool dma_ok = ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 && ldk % 8 == 0 &&
+                            ldv % 8 == 0 && (long)s.n_kv * std::max(ldk, ldv) * 2 < (1L << 31);
+        if (s.head_dim == 128 && dma_ok)
+            hipLaunchKernelGGL(fa_fwd3_k, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
+                               (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
+        else if (s.head_dim == 128)
             hipLaunchKernelGGL(fa_fwd_bf16_k<128>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
                                (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
         else
