@@ -787,6 +787,15 @@ hipError_t by_lph(int hd, F &&f) {
 }  // namespace
 
 size_t rmsnorm_partial_floats(int rows, int dim) { return (size_t)rms_grid(rows) * dim; }
+int rmsnorm_partial_rows(int rows) { return rms_grid(rows); }
+
+hipError_t column_sums(const float *partial, int nparts, long stride, int dim, float *out,
+                       hipStream_t st) {
+    if (dim <= 0) return hipSuccess;
+    hipLaunchKernelGGL(colsum_k, dim3(ceil_div(dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
+                       partial, nparts, stride, dim, out);
+    return hipGetLastError();
+}
 
 hipError_t rmsnorm_forward(const float *x, const float *w, void *y, DType ydt, int rows, int dim,
                            float eps, int gemma_quirk, hipStream_t st) {
@@ -885,7 +894,7 @@ hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv
 hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const float *qkv,
                                 long ld_qkv, const float *wq, const float *wk, float *dwq,
                                 float *dwk, float *partial, const float2 *rope_tab,
-                                bf16 *outb, long ldb, hipStream_t st) {
+                                bf16 *outb, long ldb, hipStream_t st, int *nparts) {
     if (L.n_rows <= 0) return hipSuccess;
     if (!qkv_shape_ok(L, ld, ld_qkv) || (outb && ldb % 4) || !al16(dqkv) || !al16(qkv) ||
         ((uintptr_t)outb & 7u) || (L.qk_norm && (!al16(wq) || !al16(wk))))
@@ -910,6 +919,7 @@ hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const 
             return hipGetLastError();
         });
     if (e != hipSuccess) return e;
+    if (nparts) *nparts = grid;
     if (L.qk_norm && dwq && dwk) {
         hipLaunchKernelGGL(colsum_k, dim3(ceil_div(L.head_dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
                            (const float *)partial, grid, (long)2 * L.head_dim, L.head_dim, dwq);

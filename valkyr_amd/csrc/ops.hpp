@@ -79,6 +79,13 @@ hipError_t rmsnorm_backward(const float *dy, const float *x, const float *w, flo
                             bf16 *dxb, const float *residual, float *dw, float *partial, int rows,
                             int dim, float eps, int gemma_quirk, hipStream_t st);
 size_t rmsnorm_partial_floats(int rows, int dim);
+// Rows of per-block partial sums rmsnorm_backward writes for `rows` rows.
+int rmsnorm_partial_rows(int rows);
+// out[c] = sum over b < nparts of partial[b * stride + c], c < dim, summed in a
+// fixed order (the gain-gradient reduction of the norm backwards; callers
+// that pass dw = nullptr there run it themselves, e.g. on another stream).
+hipError_t column_sums(const float *partial, int nparts, long stride, int dim, float *out,
+                       hipStream_t st);
 
 // RoPE cos/sin table [seq_len][rotary_dim/2] as float2, built on the host
 // with the fp32 formula of qk_rope_partial_batched.comp:76-81.
@@ -104,10 +111,12 @@ hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv
 // Backward of the above on the fused d_qkv buffer: d(post-rope) ->
 // d(pre-norm) for the q/k columns, in place, or (outb non-null) written with
 // the v columns to the bf16 copy outb; dwq/dwk reduced gains (overwrite).
+// nparts (optional) receives the number of partial rows written (q gains in
+// columns [0, hd), k gains in [hd, 2 hd), row stride 2 hd).
 hipError_t qkv_prepare_backward(const QkvLayout &L, float *dqkv, long ld, const float *qkv,
                                 long ld_qkv, const float *wq, const float *wk, float *dwq,
                                 float *dwk, float *partial, const float2 *rope_tab,
-                                bf16 *outb, long ldb, hipStream_t st);
+                                bf16 *outb, long ldb, hipStream_t st, int *nparts = nullptr);
 size_t qkv_partial_floats(const QkvLayout &L);
 
 // ── embedding backward (k_embed.hip) ─────────────────────────────────

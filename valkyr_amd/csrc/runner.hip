@@ -96,11 +96,14 @@ struct vkh_runner {
     // stream's backward, reading per-layer copies of the bf16 gradients.
     struct LayerGrads {
         bf16 *dyb = nullptr, *gub = nullptr, *midb = nullptr, *qkvb = nullptr;
+        // norm-gain partial sums (n1, n2, q/k norm), reduced on the side stream
+        float *pn1 = nullptr, *pn2 = nullptr, *pqk = nullptr;
+        int qk_parts = 0;
     };
     bool concurrent = false;
     hipStream_t side = nullptr;
     std::vector<hipEvent_t> ev_layer;
-    hipEvent_t ev_side = nullptr;
+    hipEvent_t ev_side = nullptr, ev_head = nullptr, ev_lm = nullptr;
     std::vector<LayerGrads> lg;
     GemmWs gws2{nullptr, 0};
     std::vector<Acts> acts;
@@ -128,6 +131,8 @@ struct vkh_runner {
         if (side) (void)hipStreamSynchronize(side);
         for (hipEvent_t e : ev_layer) (void)hipEventDestroy(e);
         if (ev_side) (void)hipEventDestroy(ev_side);
+        if (ev_head) (void)hipEventDestroy(ev_head);
+        if (ev_lm) (void)hipEventDestroy(ev_lm);
         if (side) (void)hipStreamDestroy(side);
         for (void *p : allocs) (void)hipFree(p);
         if (tok_h) (void)hipHostFree(tok_h);
@@ -354,12 +359,17 @@ struct vkh_runner {
                 for (int l = 0; l < L; ++l)
                     VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], hipEventDisableTiming));
                 VKH_HIP(hipEventCreateWithFlags(&ev_side, hipEventDisableTiming));
+                VKH_HIP(hipEventCreateWithFlags(&ev_head, hipEventDisableTiming));
+                VKH_HIP(hipEventCreateWithFlags(&ev_lm, hipEventDisableTiming));
                 lg.assign(L, LayerGrads{});
                 for (int l = 0; l < L; ++l) {
                     VKH_TRY(alloc(lg[l].dyb, (size_t)T * D));
                     VKH_TRY(alloc(lg[l].gub, (size_t)T * 2 * F));
                     VKH_TRY(alloc(lg[l].midb, (size_t)T * D));
                     VKH_TRY(alloc(lg[l].qkvb, (size_t)T * qkvd));
+                    VKH_TRY(alloc(lg[l].pn1, rmsnorm_partial_floats(T, D)));
+                    VKH_TRY(alloc(lg[l].pn2, rmsnorm_partial_floats(T, D)));
+                    if (cfg.qk_norm) VKH_TRY(alloc(lg[l].pqk, qkv_partial_floats(qkv_layout())));
                 }
                 if (wsb) {
                     char *w = nullptr;
@@ -582,6 +592,14 @@ struct vkh_runner {
         VKH_TRY(linear_dw_on(matb(g.gub, 2 * F), m_n2(a), s.t[6], 2 * F, D, gws2, side));
         VKH_TRY(linear_dw_on(matb(g.midb, D), m_attn(a), s.t[4], D, qd, gws2, side));
         VKH_TRY(linear_dw_on(matb(g.qkvb, qkvd), m_n1(a), s.t[1], qkvd, D, gws2, side));
+        // norm-gain gradients from the partial sums the main stream wrote
+        const int rp = rmsnorm_partial_rows(T);
+        VKH_HIP(column_sums(g.pn2, rp, D, D, Gd(s.t[5]), side));
+        VKH_HIP(column_sums(g.pn1, rp, D, D, Gd(s.t[0]), side));
+        if (cfg.qk_norm) {
+            VKH_HIP(column_sums(g.pqk, g.qk_parts, 2L * hd, hd, Gd(s.t[9]), side));
+            VKH_HIP(column_sums(g.pqk + hd, g.qk_parts, 2L * hd, hd, Gd(s.t[10]), side));
+        }
         return VKH_OK;
     }
 
@@ -705,8 +723,9 @@ struct vkh_runner {
         if (proj_lora(4)) VKH_TRY(lora_bwd(l, 4, mdgu, m_n2(a), d_n, D));
         if (proj_lora(5)) VKH_TRY(lora_bwd(l, 5, shift(mdgu, F), m_n2(a), d_n, D));
         // n2: d_mid = rmsnorm_bw(d_n2) + dy
-        VKH_HIP(rmsnorm_backward(d_n, a.mid, W(s.t[5]), d_mid, d_midb, dy, Gd(s.t[5]), partial, T, D,
-                                 cfg.rms_eps, 0, cur));
+        VKH_HIP(rmsnorm_backward(d_n, a.mid, W(s.t[5]), d_mid, d_midb, dy,
+                                 concurrent ? nullptr : Gd(s.t[5]), concurrent ? lg[l].pn2 : partial,
+                                 T, D, cfg.rms_eps, 0, cur));
         const Mat mdmid = b16() ? matb(d_midb, D) : matf(d_mid, D);
         // o: d_attn_out = d_mid W_o; dW_o = d_mid^T attn_out
         VKH_TRY(linear_dx(mdmid, s.t[4], d_attn_out, qd, D, qd));
@@ -736,11 +755,14 @@ struct vkh_runner {
         }
         // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
         const QkvLayout ql = qkv_layout();
+        const bool qk_side = concurrent && cfg.qk_norm;
         VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                      cfg.qk_norm ? W(s.t[10]) : nullptr,
-                                     cfg.qk_norm ? Gd(s.t[9]) : nullptr,
-                                     cfg.qk_norm ? Gd(s.t[10]) : nullptr, partial, rope_tab,
-                                     b16() ? d_qkvb : nullptr, qkvd, cur));
+                                     cfg.qk_norm && !qk_side ? Gd(s.t[9]) : nullptr,
+                                     cfg.qk_norm && !qk_side ? Gd(s.t[10]) : nullptr,
+                                     qk_side ? lg[l].pqk : partial, rope_tab,
+                                     b16() ? d_qkvb : nullptr, qkvd, cur,
+                                     qk_side ? &lg[l].qk_parts : nullptr));
         const Mat mdqkv = b16() ? matb(d_qkvb, qkvd) : matf(d_qkv, qkvd);
         // q/k/v (one [qkvd, D] matrix): d_n1 = d_qkv W_qkv; dW_qkv = d_qkv^T n1
         VKH_TRY(linear_dx(mdqkv, s.t[1], d_n, D, qkvd, D));
@@ -749,8 +771,9 @@ struct vkh_runner {
         if (proj_lora(1)) VKH_TRY(lora_bwd(l, 1, shift(mdqkv, qd), m_n1(a), d_n, D));
         if (proj_lora(2)) VKH_TRY(lora_bwd(l, 2, shift(mdqkv, qd + kvd), m_n1(a), d_n, D));
         // n1: d_x_in = rmsnorm_bw(d_n1) + d_mid
-        VKH_HIP(rmsnorm_backward(d_n, x_in, W(s.t[0]), dxo, dxob, d_mid, Gd(s.t[0]), partial, T, D,
-                                 cfg.rms_eps, 0, cur));
+        VKH_HIP(rmsnorm_backward(d_n, x_in, W(s.t[0]), dxo, dxob, d_mid,
+                                 concurrent ? nullptr : Gd(s.t[0]), concurrent ? lg[l].pn1 : partial,
+                                 T, D, cfg.rms_eps, 0, cur));
         return VKH_OK;
     }
 
@@ -764,8 +787,16 @@ struct vkh_runner {
         if (b16()) {
             VKH_HIP(cce_forward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
                                   cce_work, cur));
-            VKH_HIP(cce_backward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, (bf16 *)dz, d_fn, dw_lm,
-                                   0.f, gws, cur));
+            VKH_HIP(cce_backward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, (bf16 *)dz, d_fn,
+                                   concurrent ? nullptr : dw_lm, 0.f, gws, cur));
+            if (concurrent && dw_lm) {
+                // dW_lm = dz^T h on the side stream; the tied embedding scatter
+                // below adds into the same gradient and waits for it
+                VKH_HIP(hipEventRecord(ev_head, cur));
+                VKH_HIP(hipStreamWaitEvent(side, ev_head, 0));
+                VKH_HIP(g16_tn((const bf16 *)dz, V, fn_outb, D, dw_lm, D, T, V, D, 1.f, 0.f, gws2, side));
+                VKH_HIP(hipEventRecord(ev_lm, side));
+            }
         } else {
             VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
                                 cce_work, cur));
@@ -791,6 +822,7 @@ struct vkh_runner {
         }
         if (!lora) {
             float *dE = Gd(embed);
+            if (concurrent) VKH_HIP(hipStreamWaitEvent(cur, ev_lm, 0));
             if (!tied) VKH_HIP(fill_f32(dE, embed.numel, 0.f, cur));
             VKH_HIP(embedding_backward(dx[c], tok_d, dE, T, D, V, tied, embed_work, cur));
         }
