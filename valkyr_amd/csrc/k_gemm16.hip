@@ -5,7 +5,7 @@
 //
 // Tile plan (measured on MI355X with DMA staging, T = 2048-token step shapes):
 //   * >= 512 tiles of 256 x 256       -> 256 x 256, 8 waves (vocab-sized GEMMs)
-//   * >= 512 tiles of 128 x 128       -> 128 x 128
+//   * >= 512 tiles of 128 x 128       -> 128 x 128, 8 waves of 64 x 32
 //   * K >= 16384 and < 256 such tiles -> 128 x 128 split-K, up to 4 ways (head dh)
 //   * < 384 tiles of 128 x 64, K >= 2048 -> 128 x 64 split-K 2 ways
 //   * otherwise                       -> 128 x 64
@@ -23,8 +23,9 @@ namespace {
 using TBig = Tile16<256, 256, 2, 4>;
 using T128 = Tile16<128, 128, 2, 2>;
 using T128x64 = Tile16<128, 64, 2, 2>;
+using T128w8 = Tile16<128, 128, 2, 4>;   // 8 waves of 64 x 32
 
-enum class Pick { Big, T128, T128x64 };
+enum class Pick { Big, T128, T128x64, T128w8 };
 struct Plan {
     Pick tile;
     int splits;
@@ -32,15 +33,18 @@ struct Plan {
 
 size_t ws_for(const Plan &p, const GemmShape &s) {
     if (p.splits <= 1) return 0;
-    return p.tile == Pick::T128 ? gemm16_ws_bytes<T128>(s, p.splits)
-                                : gemm16_ws_bytes<T128x64>(s, p.splits);
+    switch (p.tile) {
+    case Pick::T128: return gemm16_ws_bytes<T128>(s, p.splits);
+    case Pick::T128w8: return gemm16_ws_bytes<T128w8>(s, p.splits);
+    default: return gemm16_ws_bytes<T128x64>(s, p.splits);
+    }
 }
 
 Plan plan(const GemmShape &s, size_t ws_bytes) {
     auto tiles = [&](int bm, int bn) { return (long)ceil_div(s.M, bm) * (long)ceil_div(s.N, bn); };
     if (tiles(256, 256) >= 512) return {Pick::Big, 1};
     const long t128 = tiles(128, 128), t64 = tiles(128, 64);
-    if (t128 >= 512) return {Pick::T128, 1};
+    if (t128 >= 512) return {Pick::T128w8, 1};
     const int nk = (s.K + 63) / 64;
     Plan p{Pick::T128x64, 1};
     if (s.K >= 16384 && t128 < 256)
@@ -59,6 +63,7 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
     switch (p.tile) {
     case Pick::Big: return launch_gemm16<TBig, LA, LB>(a, b, s, e, sk, st);
     case Pick::T128: return launch_gemm16<T128, LA, LB>(a, b, s, e, sk, st);
+    case Pick::T128w8: return launch_gemm16<T128w8, LA, LB>(a, b, s, e, sk, st);
     default: return launch_gemm16<T128x64, LA, LB>(a, b, s, e, sk, st);
     }
 }
