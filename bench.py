@@ -288,7 +288,7 @@ def main():
         "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (config 2)",
                    "ms": round(fa["ms"], 4), "tflops": round(fa["tflops"], 1),
                    "frac_bf16_peak": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4)},
-        "roofline": {"kernel": "attention backward, config 2: fa_bw_d_k + fa_bwd_dkv2_k + "
+        "roofline": {"kernel": "attention backward, config 2: fa_bw_d8_k + fa_bwd_dkv3_k + "
                                "fa_dq_gemm_k (one call)", "bound": "mfma",
                      "achieved": round(fa["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4),
