@@ -18,14 +18,13 @@
 //     position c ^ (r & 7), so the 16-byte fragment reads of 8 consecutive
 //     lanes (8 consecutive rows, same logical chunk) and the staging writes
 //     (8 chunks of one row) each touch all 32 banks exactly once.
-//   * Global -> LDS by DMA (buffer_load ... lds, see gemm16_tile_dma), two
-//     LDS buffers, one barrier per slab: slab k+1 streams in while slab k's
-//     MFMAs run.  Loads go through buffer resources: out-of-range rows and k
-//     are returned as zero by the hardware range check, so edges need no
-//     branches.  (gemm16_tile is the earlier register-staged form.)
+//   * Global -> LDS by DMA (buffer_load ... lds, see gemm16_tile_dma), two or
+//     three LDS buffers (Tile16::ST), one barrier per slab: the next one or
+//     two slabs stream in while a slab's MFMAs run.  Loads go through buffer
+//     resources: out-of-range rows and k are returned as zero by the
+//     hardware range check, so edges need no branches.
 //   * MN-major operands stay k-row-major in LDS and their MFMA fragments are
-//     read with the transposing LDS load ds_read_b64_tr_b16 (the register-
-//     staged form transposes 8x8 / 4x8 bf16 blocks in registers instead).
+//     read with the transposing LDS load ds_read_b64_tr_b16.
 //   * Block ids are regrouped so each XCD (8 on MI355X, round-robin dispatch)
 //     gets a contiguous band of tiles that share operand panels in its L2.
 #pragma once
@@ -46,139 +45,26 @@ struct Op16 {
 
 constexpr unsigned kOOB = 0x80000000u;  // any offset >= bytes reads as zero
 
-VKH_DEV __amdgpu_buffer_rsrc_t make_rsrc(const Op16 &o) {
-    return __builtin_amdgcn_make_buffer_rsrc((void *)o.p, (short)0, (int)o.bytes, 0x00020000);
+// Buffer resource as four SGPR words (base, base_hi | stride 0, num_records,
+// flags), the form inline assembly takes.
+typedef int sgpr4 __attribute__((ext_vector_type(4)));
+VKH_DEV sgpr4 rsrc4(const void *base, unsigned bytes) {
+    const unsigned long a = (unsigned long)base;
+    sgpr4 r;
+    r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
+    r[1] = __builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32) & 0xffff);
+    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
+    r[3] = 0x00020000;
+    return r;
 }
+VKH_DEV sgpr4 rsrc4(const Op16 &o) { return rsrc4(o.p, o.bytes); }
 
-VKH_DEV u32x4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
-}
-
-// byte offset of chunk c (0..7) of LDS row r
-VKH_DEV int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
-
-// K-major operand: R rows x 64 k per slab, one 16-byte chunk per unit.
-template <int R, int NT>
-struct Ld16K {
-    static constexpr int PER = R * 8 / NT;
-    static_assert(PER >= 1 && (R * 8) % NT == 0, "tile / thread mismatch");
-    u32x4 v[PER];
-    unsigned base[PER];  // byte offset of the chunk at k = 0, or kOOB
-
-    VKH_DEV void setup(const Op16 &o, int row0, int rmax, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT, row = u >> 3, c = u & 7;
-            const int gr = row0 + row;
-            base[i] = gr < rmax ? (unsigned)(((long)gr * o.ld + c * 8) * 2) : kOOB;
-        }
-    }
-    VKH_DEV void load(__amdgpu_buffer_rsrc_t rs, long, int k0, int kmax, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int c = (tid + i * NT) & 7;
-            const bool ok = base[i] != kOOB && k0 + c * 8 < kmax;
-            v[i] = buf_load16(rs, ok ? base[i] + (unsigned)k0 * 2 : kOOB);
-        }
-    }
-    VKH_DEV void store(char *lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT;
-            *reinterpret_cast<u32x4 *>(lds + swz(u >> 3, u & 7)) = v[i];
-        }
-    }
-};
-
-// element j (0..7) of an 8 x bf16 chunk, as the low 16 bits
-template <int J>
-VKH_DEV unsigned half_of(const u32x4 &x) {
-    return J & 1 ? (x[J >> 1] >> 16) : (x[J >> 1] & 0xffffu);
-}
-
-// MN-major operand: storage rows are k.  A unit is KR consecutive k rows of
-// one 8-wide r chunk (KR = 8, 4 or 2, so that every thread owns whole
-// units); it is transposed to 8 r rows of KR k values.
-template <int R, int NT>
-struct Ld16MN {
-    static constexpr int KR = (64 * R / 8) / NT >= 8 ? 8 : (64 * R / 8) / NT >= 4 ? 4 : 2;
-    static constexpr int KB = 64 / KR;  // k blocks per slab
-    static constexpr int UNITS = KB * (R / 8);
-    static constexpr int PER = UNITS / NT;
-    static_assert(PER >= 1 && UNITS % NT == 0, "tile / thread mismatch");
-    u32x4 v[PER][KR];
-    unsigned base[PER];  // byte offset of (k = kb * KR, r chunk) at k0 = 0, or kOOB
-
-    VKH_DEV void setup(const Op16 &o, int row0, int rmax, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT, kb = u % KB, rb = u / KB;
-            const int gr = row0 + rb * 8;
-            base[i] = gr < rmax ? (unsigned)(((long)kb * KR * o.ld + gr) * 2) : kOOB;
-        }
-    }
-    VKH_DEV void load(__amdgpu_buffer_rsrc_t rs, long ld, int k0, int kmax, int tid) {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int kb = (tid + i * NT) % KB;
-#pragma unroll
-            for (int q = 0; q < KR; ++q) {
-                const int k = k0 + kb * KR + q;
-                const bool ok = base[i] != kOOB && k < kmax;
-                v[i][q] = buf_load16(rs, ok ? base[i] + (unsigned)(((long)k0 + q) * ld * 2) : kOOB);
-            }
-        }
-    }
-    template <int J>
-    VKH_DEV void store_row(char *lds, int i, int rb, int kb) const {
-        const int r = rb * 8 + J;
-        const int kpos = kb * KR;
-        char *dst = lds + swz(r, kpos >> 3) + (kpos & 7) * 2;
-        if constexpr (KR == 8) {
-            u32x4 o;
-#pragma unroll
-            for (int w = 0; w < 4; ++w)
-                o[w] = half_of<J>(v[i][2 * w]) | (half_of<J>(v[i][2 * w + 1]) << 16);
-            *reinterpret_cast<u32x4 *>(dst) = o;
-        } else if constexpr (KR == 4) {
-            u32x2 o;
-#pragma unroll
-            for (int w = 0; w < 2; ++w)
-                o[w] = half_of<J>(v[i][2 * w]) | (half_of<J>(v[i][2 * w + 1]) << 16);
-            *reinterpret_cast<u32x2 *>(dst) = o;
-        } else {
-            *reinterpret_cast<unsigned *>(dst) = half_of<J>(v[i][0]) | (half_of<J>(v[i][1]) << 16);
-        }
-    }
-    VKH_DEV void store(char *lds, int tid) const {
-#pragma unroll
-        for (int i = 0; i < PER; ++i) {
-            const int u = tid + i * NT, kb = u % KB, rb = u / KB;
-            store_row<0>(lds, i, rb, kb); store_row<1>(lds, i, rb, kb);
-            store_row<2>(lds, i, rb, kb); store_row<3>(lds, i, rb, kb);
-            store_row<4>(lds, i, rb, kb); store_row<5>(lds, i, rb, kb);
-            store_row<6>(lds, i, rb, kb); store_row<7>(lds, i, rb, kb);
-        }
-    }
-};
-
-template <Lay L, int R, int NT>
-struct Ld16Sel;
-template <int R, int NT>
-struct Ld16Sel<Lay::K, R, NT> {
-    using T = Ld16K<R, NT>;
-};
-template <int R, int NT>
-struct Ld16Sel<Lay::MN, R, NT> {
-    using T = Ld16MN<R, NT>;
-};
-
-// PF = number of K slabs in flight in registers while one computes (1 or 2).
-template <int BM_, int BN_, int WGM_, int WGN_, int PF_ = 1>
+// ST = LDS slab buffers (2: one slab in flight while one computes; 3: two).
+template <int BM_, int BN_, int WGM_, int WGN_, int ST_ = 2>
 struct Tile16 {
-    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, PF = PF_;
+    static constexpr int BM = BM_, BN = BN_, WGM = WGM_, WGN = WGN_, ST = ST_;
     static constexpr int NT = 64 * WGM * WGN;
-    static constexpr int LDS = 2 * (BM + BN) * 128;
+    static constexpr int LDS = ST * (BM + BN) * 128;
 };
 
 // Split-K: `splits` blocks share one output tile, each contracting a
@@ -192,117 +78,6 @@ struct SplitK {
     int splits;
     f32x4 *ws;  // [tiles][splits][BM * BN / 4]
 };
-
-// One block's BM x BN output tile over the K slabs [kbase, kbase + 64 nk):
-// acc (per wave, accumulator layout) += A(m0.., k) B(n0.., k).  `smem` must
-// hold 2 (BM + BN) 128 bytes.  Shared by the GEMM kernels and the attention
-// dQ kernel.
-template <class Cfg, Lay LA, Lay LB, int TM, int TN>
-VKH_DEV void gemm16_tile(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
-                         int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem) {
-    constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
-    constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
-    static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
-    constexpr int ABYTES = BM * 128, BBYTES = BN * 128, STAGE = ABYTES + BBYTES;
-    const int tid = threadIdx.x;
-    const int lane = tid % 64, wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a), rb = make_rsrc(b);
-    // register staging sets (the second is used only with PF == 2)
-    typename Ld16Sel<LA, BM, NT>::T la0, la1;
-    typename Ld16Sel<LB, BN, NT>::T lb0, lb1;
-    la0.setup(a, m0, M, tid);
-    lb0.setup(b, n0, N, tid);
-    if constexpr (Cfg::PF == 2) {
-        la1.setup(a, m0, M, tid);
-        lb1.setup(b, n0, N, tid);
-    }
-    // per-lane fragment offsets: row fr of each 16-row group, chunk (4 ks + fg)
-    const int fr = lane % 16, fg = lane / 16;
-    const int sw = fg ^ (fr & 7);
-    const int a_lane = (wm * WM + fr) * 128, b_lane = (wn * WN + fr) * 128;
-
-    auto compute = [&](const char *sa) {
-        const char *sb = sa + ABYTES;
-#pragma unroll
-        for (int ks = 0; ks < 2; ++ks) {
-            const int coff = (((ks << 2) ^ sw) << 4);
-            bf16x8 af[TM], bfr[TN];
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-                af[i] = *reinterpret_cast<const bf16x8 *>(sa + a_lane + i * 16 * 128 + coff);
-#pragma unroll
-            for (int j = 0; j < TN; ++j)
-                bfr[j] = *reinterpret_cast<const bf16x8 *>(sb + b_lane + j * 16 * 128 + coff);
-#pragma unroll
-            for (int i = 0; i < TM; ++i)
-#pragma unroll
-                for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[i], bfr[j], acc[i][j]);
-        }
-    };
-    char *const lds0 = smem, *const lds1 = smem + STAGE;
-
-    if constexpr (Cfg::PF == 1) {
-        la0.load(ra, a.ld, kbase, Kmax, tid);
-        lb0.load(rb, b.ld, kbase, Kmax, tid);
-        la0.store(lds0, tid);
-        lb0.store(lds0 + ABYTES, tid);
-        __syncthreads();
-        for (int kt = 0; kt < nk; ++kt) {
-            if (kt + 1 < nk) {
-                la0.load(ra, a.ld, kbase + (kt + 1) * 64, Kmax, tid);
-                lb0.load(rb, b.ld, kbase + (kt + 1) * 64, Kmax, tid);
-            }
-            compute(kt & 1 ? lds1 : lds0);
-            if (kt + 1 < nk) {
-                char *nxt = kt & 1 ? lds0 : lds1;
-                la0.store(nxt, tid);
-                lb0.store(nxt + ABYTES, tid);
-            }
-            __syncthreads();
-        }
-    } else {
-        // Invariant at an even step kt: lds0 holds slab kt, set 1 holds slab
-        // kt+1 and set 0 slab kt+2 (both in flight); odd steps swap roles.
-        la0.load(ra, a.ld, kbase, Kmax, tid);
-        lb0.load(rb, b.ld, kbase, Kmax, tid);
-        if (nk > 1) {
-            la1.load(ra, a.ld, kbase + 64, Kmax, tid);
-            lb1.load(rb, b.ld, kbase + 64, Kmax, tid);
-        }
-        la0.store(lds0, tid);
-        lb0.store(lds0 + ABYTES, tid);
-        if (nk > 2) {
-            la0.load(ra, a.ld, kbase + 128, Kmax, tid);
-            lb0.load(rb, b.ld, kbase + 128, Kmax, tid);
-        }
-        __syncthreads();
-        for (int kt = 0; kt < nk; kt += 2) {
-            compute(lds0);
-            if (kt + 1 < nk) {
-                la1.store(lds1, tid);
-                lb1.store(lds1 + ABYTES, tid);
-            }
-            if (kt + 3 < nk) {
-                la1.load(ra, a.ld, kbase + (kt + 3) * 64, Kmax, tid);
-                lb1.load(rb, b.ld, kbase + (kt + 3) * 64, Kmax, tid);
-            }
-            __syncthreads();
-            if (kt + 1 >= nk) break;
-            compute(lds1);
-            if (kt + 2 < nk) {
-                la0.store(lds0, tid);
-                lb0.store(lds0 + ABYTES, tid);
-            }
-            if (kt + 4 < nk) {
-                la0.load(ra, a.ld, kbase + (kt + 4) * 64, Kmax, tid);
-                lb0.load(rb, b.ld, kbase + (kt + 4) * 64, Kmax, tid);
-            }
-            __syncthreads();
-        }
-    }
-
-}
 
 // ── DMA staging: global -> LDS without registers ─────────────────────
 //
@@ -333,13 +108,38 @@ VKH_DEV int mn_swz(int k) {
     else return 2 * (((k >> 1) & 1) | (((k >> 3) & 1) << 1));
 }
 
-VKH_DEV void dma16(__amdgpu_buffer_rsrc_t rs, char *lds_wave_base, unsigned voff) {
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void_t *)lds_wave_base, 16, voff, 0, 0, 0);
+// 16-byte global -> LDS DMA of one wave (lane l lands at lds + 16 l; the LDS
+// address is wave-uniform and goes to M0).  Issued as inline assembly so the
+// compiler's wait-count tracking does not treat later LDS reads as possible
+// aliases of the in-flight slab (it would wait for the DMA before reading the
+// current one); the slab loops wait for their DMA explicitly (vmcnt) before
+// the barrier that publishes a slab.
+VKH_DEV void dma16_async(const sgpr4 &rs, const void *lds, unsigned voff) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (int)(unsigned)(unsigned long)(const __attribute__((address_space(3))) char *)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs)
+                 : "memory");
 }
+VKH_DEV void dma4_async(const sgpr4 &rs, const void *lds, unsigned voff) {
+    const unsigned m0 = __builtin_amdgcn_readfirstlane(
+        (int)(unsigned)(unsigned long)(const __attribute__((address_space(3))) char *)lds);
+    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
+                 :
+                 : "s"(m0), "v"(voff), "s"(rs)
+                 : "memory");
+}
+
+// Block barrier for LDS hand-offs: this wave's LDS operations complete, then
+// s_barrier (no wait on outstanding global operations, unlike __syncthreads'
+// fence).  The memory clobber keeps the compiler from moving memory accesses
+// across it.
+VKH_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // Issue this wave's share of one slab of an operand tile (R x 64).
 template <Lay L, int R, int NW>
-VKH_DEV void dma_tile(__amdgpu_buffer_rsrc_t rs, const Op16 &o, char *tile, int r0, int rmax, int k0,
+VKH_DEV void dma_tile(const sgpr4 &rs, const Op16 &o, char *tile, int r0, int rmax, int k0,
                       int kmax, int wave, int lane) {
     constexpr int PW = R / 8 / NW;  // 1 KB instructions per wave
     static_assert(PW >= 1 && PW * NW * 8 == R, "tile / wave mismatch");
@@ -361,7 +161,7 @@ VKH_DEV void dma_tile(__amdgpu_buffer_rsrc_t rs, const Op16 &o, char *tile, int 
             const int gk = k0 + k, gm = r0 + 8 * c;
             off = (gk < kmax && gm < rmax) ? (unsigned)(((long)gk * o.ld + gm) * 2) : kOOB;
         }
-        dma16(rs, dst, off);
+        dma16_async(rs, dst, off);
     }
 }
 
@@ -386,26 +186,38 @@ VKH_DEV bf16x8 frag16(const char *tile, int row16, int ks, int lane) {
 
 VKH_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0), exp/lgkm untouched
 
+// One block's BM x BN output tile over the K slabs [kbase, kbase + 64 nk):
+// acc (per wave, accumulator layout) += A(m0.., k) B(n0.., k).  `smem` must
+// hold Cfg::LDS bytes.  Shared by the GEMM kernels and the attention dQ kernel.
 template <class Cfg, Lay LA, Lay LB, int TM, int TN>
 VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
                              int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem) {
-    constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::WGM * Cfg::WGN;
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::WGM * Cfg::WGN, ST = Cfg::ST;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
     static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
+    static_assert(ST == 2 || ST == 3, "slab buffers");
     constexpr int ABYTES = BM * 128, BBYTES = BN * 128, STAGE = ABYTES + BBYTES;
+    // DMA instructions one wave issues per slab (the newest slab's count)
+    constexpr int PER_SLAB = BM / 8 / NW + BN / 8 / NW;
+    static_assert(PER_SLAB <= 15, "vmcnt immediate");
     const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
     const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
-    const __amdgpu_buffer_rsrc_t ra = make_rsrc(a), rb = make_rsrc(b);
-    auto issue = [&](int kt, char *stage) {
+    const sgpr4 ra = rsrc4(a), rb = rsrc4(b);
+    auto issue = [&](int kt) {
+        char *stage = smem + (kt % ST) * STAGE;
         dma_tile<LA, BM, NW>(ra, a, stage, m0, M, kbase + kt * 64, Kmax, wave, lane);
         dma_tile<LB, BN, NW>(rb, b, stage + ABYTES, n0, N, kbase + kt * 64, Kmax, wave, lane);
     };
-    if (nk > 0) issue(0, smem);
+    // ST - 1 slabs in flight ahead of the one computing
+    for (int j = 0; j < ST - 1 && j < nk; ++j) issue(j);
     for (int kt = 0; kt < nk; ++kt) {
-        char *cur = smem + (kt & 1) * STAGE;
-        wait_vm0();
-        __syncthreads();  // slab kt landed for every wave; slab kt-1's buffer is free
-        if (kt + 1 < nk) issue(kt + 1, smem + ((kt + 1) & 1) * STAGE);
+        const char *cur = smem + (kt % ST) * STAGE;
+        // slab kt is this wave's oldest outstanding DMA batch: with a newer
+        // batch in flight, wait until only that one remains
+        if (ST == 3 && kt + 1 < nk) __builtin_amdgcn_s_waitcnt(0x0f70 | PER_SLAB);
+        else wait_vm0();
+        lds_barrier();  // slab kt landed for every wave; slab kt-1's buffer is free
+        if (kt + ST - 1 < nk) issue(kt + ST - 1);
         // Both k-steps' fragments are requested before the first MFMA, so the
         // LDS latency of the second set hides behind the first set's MFMAs.
         bf16x8 af[2][TM], bfr[2][TN];
@@ -425,7 +237,7 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
 #pragma unroll
                 for (int j = 0; j < TN; ++j) acc[i][j] = mfma16x16x32(af[ks][i], bfr[ks][j], acc[i][j]);
     }
-    __syncthreads();  // the caller may reuse smem
+    lds_barrier();  // the caller may reuse smem
 }
 
 template <class Cfg, Lay LA, Lay LB, class Epi>
@@ -434,7 +246,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
     constexpr int TM = WM / 16, TN = WN / 16;
-    __shared__ __attribute__((aligned(16))) char smem[2 * (BM + BN) * 128];
+    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
 
     const int tid = threadIdx.x;
     const int lane = tid % 64, wave = tid / 64;

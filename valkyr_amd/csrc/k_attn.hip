@@ -817,46 +817,6 @@ constexpr int NBUF = 3;            // tile buffers (two DMA batches in flight)
 
 VKH_DEV int swz(int r) { return r & 15; }
 
-// Block barrier for LDS hand-offs only: this wave's LDS operations complete,
-// then s_barrier.  (__syncthreads would also wait for the in-flight tile DMA
-// and the dS stores, which the next tile's barrier covers.)  The memory
-// clobber keeps the compiler from moving memory accesses across it.
-VKH_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
-
-// Buffer resource as four SGPR words (base, base_hi, num_records, flags).
-typedef int sgpr4 __attribute__((ext_vector_type(4)));
-VKH_DEV sgpr4 rsrc4(const void *base, unsigned bytes) {
-    const unsigned long a = (unsigned long)base;
-    sgpr4 r;
-    r[0] = __builtin_amdgcn_readfirstlane((int)(unsigned)a);
-    r[1] = __builtin_amdgcn_readfirstlane((int)(unsigned)(a >> 32) & 0xffff);
-    r[2] = __builtin_amdgcn_readfirstlane((int)bytes);
-    r[3] = 0x00020000;
-    return r;
-}
-
-// 16-byte global -> LDS DMA of one wave (lane l lands at lds + 16 l).  Issued
-// as inline assembly so the compiler's wait-count tracking does not treat
-// every later LDS read as a possible alias of the in-flight tile (it would
-// wait for the DMA before the current tile's reads); the tile loop waits for
-// the DMA explicitly (vmcnt(0) before the barrier that publishes the tile).
-VKH_DEV void dma16_async(const sgpr4 &rs, const void *lds, unsigned voff) {
-    const unsigned m0 = __builtin_amdgcn_readfirstlane(
-        (int)(unsigned)(unsigned long)(const __attribute__((address_space(3))) char *)lds);
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, 0 offen lds"
-                 :
-                 : "s"(m0), "v"(voff), "s"(rs)
-                 : "memory");
-}
-VKH_DEV void dma4_async(const sgpr4 &rs, const void *lds, unsigned voff) {
-    const unsigned m0 = __builtin_amdgcn_readfirstlane(
-        (int)(unsigned)(unsigned long)(const __attribute__((address_space(3))) char *)lds);
-    asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dword %1, %2, 0 offen lds"
-                 :
-                 : "s"(m0), "v"(voff), "s"(rs)
-                 : "memory");
-}
-
 // byte offset of (row r, element col) in a swizzled tile
 VKH_DEV int toff(int r, int col) { return r * (HD * 2) + (((col >> 3) ^ swz(r)) << 4) + (col & 7) * 2; }
 
@@ -1246,7 +1206,7 @@ template <int HD>
 __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, const bf16 *dsw) {
     using Cfg = Tile16<128, HD, 2, 2>;
     constexpr int TM = 128 / 2 / 16, TN = HD / 2 / 16;
-    __shared__ __attribute__((aligned(16))) char smem[2 * (128 + HD) * 128];
+    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
     const int qt = s.causal ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;
     const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int kvh = h / (s.n_heads / s.n_kv_heads);

@@ -23,7 +23,9 @@ namespace {
 using TBig = Tile16<256, 256, 2, 4>;
 using T128 = Tile16<128, 128, 2, 2>;
 using T128x64 = Tile16<128, 64, 2, 2>;
-using T128w8 = Tile16<128, 128, 2, 4>;   // 8 waves of 64 x 32
+using T128w8 = Tile16<128, 128, 2, 4>;  // 8 waves of 64 x 32
+// (Three slab buffers were measured slower for these tiles: the larger LDS
+// footprint drops a block per CU.)
 
 enum class Pick { Big, T128, T128x64, T128w8 };
 struct Plan {
