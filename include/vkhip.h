@@ -74,7 +74,14 @@ typedef enum vkh_status {
     VKH_ERR_LORA_CHECKPOINT_CONFIG_SIZE_MISMATCH = 47,
     VKH_ERR_LORA_CHECKPOINT_CONFIG_MISMATCH = 48,
     VKH_ERR_LORA_CHECKPOINT_EMPTY = 49,
-    VKH_ERR_IO = 50
+    VKH_ERR_IO = 50,
+    /* dataset / fine-tune loop: train/dataset.zig:52-62, :140; commands/finetune.zig:132-135 */
+    VKH_ERR_INPUT_IDS_LEN = 60,
+    VKH_ERR_TARGET_IDS_LEN = 61,
+    VKH_ERR_BATCH_INDEX_OUT_OF_RANGE = 62,
+    VKH_ERR_EMPTY_DATASET = 63,
+    VKH_ERR_DATASET_TOO_SHORT = 64,
+    VKH_ERR_BATCH_IDX_OUT_OF_RANGE = 65
 } vkh_status;
 
 typedef enum vkh_precision {
@@ -239,6 +246,59 @@ vkh_status vkh_runner_set_loss_target(vkh_runner *r, float target);
  * is reported once its copy has landed. */
 vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
                                        vkh_train_budget budget, vkh_tick_result *out);
+
+/* ── host feed: packed token stream and the fine-tune loop ───────────── */
+
+/* train/dataset.zig Dataset: examples packed into one stream with `eos_id`
+ * between them (none after the last), read as sliding windows of n_pos + 1
+ * tokens: batch idx = (packed[idx .. idx + n_pos], packed[idx + 1 .. idx + n_pos
+ * + 1]), num_batches = len - n_pos (0 when len <= n_pos).  Token ids only:
+ * the tokenizer is not part of this library. */
+typedef struct vkh_dataset vkh_dataset;
+
+/* buildFromExamples (dataset.zig:76-96) on already-tokenized examples. */
+vkh_status vkh_dataset_from_examples(const uint32_t *const *examples, const size_t *lens,
+                                     size_t n_examples, uint32_t n_pos, uint32_t eos_id,
+                                     vkh_dataset **out);
+/* buildFromJsonl (dataset.zig:98-148) with the token ids of a line in an
+ * integer array field "ids" (the reference tokenizes a "text" field): empty or
+ * whitespace-only lines, lines that do not parse as a JSON object and objects
+ * without an "ids" array of integers in [0, 2^32) are skipped; EOS goes
+ * between accepted lines.  VKH_ERR_EMPTY_DATASET when no line is usable. */
+vkh_status vkh_dataset_from_jsonl(const char *path, uint32_t n_pos, uint32_t eos_id,
+                                  vkh_dataset **out);
+void vkh_dataset_destroy(vkh_dataset *d);
+size_t vkh_dataset_num_batches(const vkh_dataset *d); /* numBatches (dataset.zig:42-47) */
+size_t vkh_dataset_packed_len(const vkh_dataset *d);
+/* the packed stream itself (n = packed_len) */
+vkh_status vkh_dataset_packed(const vkh_dataset *d, uint32_t *out, size_t n);
+/* batch (dataset.zig:50-66): errors InputIdsLen, TargetIdsLen, BatchIndexOutOfRange. */
+vkh_status vkh_dataset_batch(const vkh_dataset *d, size_t idx, uint32_t *input_ids, size_t n_input,
+                             uint32_t *target_ids, size_t n_target);
+/* n_seqs windows for one batched step (the n_seqs extension): window s is
+ * batch (idx + s * stride) mod num_batches, written at offset s * n_pos. */
+vkh_status vkh_dataset_batch_seqs(const vkh_dataset *d, size_t idx, size_t stride, uint32_t n_seqs,
+                                  uint32_t *input_ids, uint32_t *target_ids);
+
+/* computeMeanCe (commands/finetune.zig:256-268): mean over rows of
+ * log-sum-exp(logits[p]) - logits[p][target[p]], fp64 accumulation. */
+float vkh_mean_ce(const float *logits, const uint32_t *target_ids, size_t n_rows, size_t vocab);
+
+typedef struct vkh_finetune_result {
+    float ce_initial;   /* on the batch at batch_idx, before the first step */
+    float ce_final;     /* same batch after the last step */
+    double total_ms;    /* wall time of the step loop */
+    double mean_step_ms;
+} vkh_finetune_result;
+
+/* The training loop of commands/finetune.zig:155-196: CE on batch `batch_idx`
+ * (forward_logits + vkh_mean_ce), n_steps Runner steps on batch `batch_idx`
+ * or, with rotate, on (step + batch_idx) mod num_batches, then CE again on
+ * `batch_idx`.  With n_seqs > 1 each step trains on n_seqs windows n_pos apart
+ * (vkh_dataset_batch_seqs).  Errors: DatasetTooShort (no batch),
+ * BatchIdxOutOfRange, and the Runner's own. */
+vkh_status vkh_runner_finetune(vkh_runner *r, const vkh_dataset *d, uint32_t batch_idx,
+                               uint32_t n_steps, uint32_t rotate, vkh_finetune_result *out);
 
 /* ── kernels (device pointers; enqueue on `stream`) ─────────────────── */
 

@@ -309,3 +309,42 @@ def test_nonfinite_weights_give_nonfinite_loss():
     r.set(0, 0, 1, w)
     loss = r.forward_backward(tok, tgt)
     assert not np.isfinite(loss)
+
+
+def test_finetune_loop_matches_manual_steps():
+    """vkh_runner_finetune (commands/finetune.zig:155-196) against the same loop
+    driven step by step from the host: identical weights and CE values."""
+    from valkyr_amd.dataset import Dataset, finetune, mean_ce
+
+    note("finetune loop")
+    cfg = dict(CONFIG1, n_seqs=2, seq_len=64)
+    m, r1, _, _, _ = build_pair(0, n_seqs=2, seq_len=64)
+    _, r2, _, _, _ = build_pair(0, n_seqs=2, seq_len=64)
+    rng = np.random.default_rng(3)
+    ex = [rng.integers(0, cfg["vocab_size"], rng.integers(20, 200)).tolist() for _ in range(12)]
+    ds = Dataset.from_examples(ex, n_pos=64, eos_id=1)
+    nb = ds.num_batches()
+    res = finetune(r1, ds, batch_idx=5, n_steps=4, rotate=True)
+    # the same loop by hand on the second runner
+    V, T = cfg["vocab_size"], 128
+    tok, tgt = ds.batch_seqs(5, 64, 2)
+    ce0 = mean_ce(r2.forward_logits(tok), tgt, V)
+    for step in range(4):
+        a, b = ds.batch_seqs((step + 5) % nb, 64, 2)
+        r2.step(a, b)
+    ce1 = mean_ce(r2.forward_logits(tok), tgt, V)
+    note(f"  CE {res['ce_initial']:.4f} -> {res['ce_final']:.4f} (manual {ce0:.4f} -> {ce1:.4f}), "
+         f"{res['mean_step_ms']:.2f} ms/step")
+    assert res["ce_initial"] == ce0 and res["ce_final"] == ce1
+    assert res["ce_final"] < res["ce_initial"]
+    for k in tensor_keys(cfg):
+        assert np.array_equal(r1.get(0, *k), r2.get(0, *k)), k
+    # errors of finetune.zig:132-135
+    import valkyr_amd as v
+    short = Dataset.from_examples([[1, 2, 3]], n_pos=64, eos_id=1)
+    with pytest.raises(v.VkhError) as e:
+        finetune(r1, short, 0, 1)
+    assert e.value.name == "DatasetTooShort"
+    with pytest.raises(v.VkhError) as e:
+        finetune(r1, ds, nb, 1)
+    assert e.value.name == "BatchIdxOutOfRange"

@@ -6,9 +6,10 @@ fallback: without the built library, `lib()` raises MissingLibraryError.
 """
 from ._lib import (Config, MissingLibraryError, VkhError, check, device_count, lib)  # noqa: F401
 from .runner import Runner, make_config  # noqa: F401
+from .dataset import Dataset, finetune, mean_ce  # noqa: F401
 
 __all__ = ["Config", "MissingLibraryError", "VkhError", "Runner", "make_config", "lib", "check",
-           "device_count", "build"]
+           "device_count", "build", "Dataset", "finetune", "mean_ce"]
 
 
 def build(jobs: int = 8) -> str:

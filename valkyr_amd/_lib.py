@@ -38,6 +38,8 @@ STATUS = {
     43: "CheckpointConfigMismatch", 44: "EndOfStream", 45: "InvalidLoraCheckpointMagic",
     46: "UnsupportedLoraCheckpointVersion", 47: "LoraCheckpointConfigSizeMismatch",
     48: "LoraCheckpointConfigMismatch", 49: "LoraCheckpointEmpty", 50: "IoError",
+    60: "InputIdsLen", 61: "TargetIdsLen", 62: "BatchIndexOutOfRange", 63: "EmptyDataset",
+    64: "DatasetTooShort", 65: "BatchIdxOutOfRange",
 }
 
 
@@ -103,6 +105,11 @@ class TickResult(C.Structure):
                 ("last_loss", C.c_float), ("idle", C.c_uint32), ("elapsed_us", C.c_uint64)]
 
 
+class FinetuneResult(C.Structure):
+    _fields_ = [("ce_initial", C.c_float), ("ce_final", C.c_float), ("total_ms", C.c_double),
+                ("mean_step_ms", C.c_double)]
+
+
 P = C.c_void_p
 U32 = C.c_uint32
 SZ = C.c_size_t
@@ -138,6 +145,16 @@ SIGNATURES = [
     ("vkh_runner_upload_train_batch", ST, [P, P, SZ, P, SZ]),
     ("vkh_runner_set_loss_target", ST, [P, F]),
     ("vkh_runner_tick_frame_train", ST, [P, P, TrainBudget, C.POINTER(TickResult)]),
+    ("vkh_dataset_from_examples", ST, [P, P, SZ, U32, U32, C.POINTER(P)]),
+    ("vkh_dataset_from_jsonl", ST, [C.c_char_p, U32, U32, C.POINTER(P)]),
+    ("vkh_dataset_destroy", None, [P]),
+    ("vkh_dataset_num_batches", SZ, [P]),
+    ("vkh_dataset_packed_len", SZ, [P]),
+    ("vkh_dataset_packed", ST, [P, P, SZ]),
+    ("vkh_dataset_batch", ST, [P, SZ, P, SZ, P, SZ]),
+    ("vkh_dataset_batch_seqs", ST, [P, SZ, SZ, U32, P, P]),
+    ("vkh_mean_ce", F, [P, P, SZ, SZ]),
+    ("vkh_runner_finetune", ST, [P, P, U32, U32, U32, C.POINTER(FinetuneResult)]),
     ("vkh_fa_forward", ST, [C.POINTER(AttnParams), P, P, P, P, P, P]),
     ("vkh_fa_bw_d", ST, [C.POINTER(AttnParams), P, P, P, P, P]),
     ("vkh_fa_bw_dq", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P]),

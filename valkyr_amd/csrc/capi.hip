@@ -132,6 +132,12 @@ const char *vkh_status_name(vkh_status s) {
     case VKH_ERR_LORA_CHECKPOINT_CONFIG_MISMATCH: return "LoraCheckpointConfigMismatch";
     case VKH_ERR_LORA_CHECKPOINT_EMPTY: return "LoraCheckpointEmpty";
     case VKH_ERR_IO: return "IoError";
+    case VKH_ERR_INPUT_IDS_LEN: return "InputIdsLen";
+    case VKH_ERR_TARGET_IDS_LEN: return "TargetIdsLen";
+    case VKH_ERR_BATCH_INDEX_OUT_OF_RANGE: return "BatchIndexOutOfRange";
+    case VKH_ERR_EMPTY_DATASET: return "EmptyDataset";
+    case VKH_ERR_DATASET_TOO_SHORT: return "DatasetTooShort";
+    case VKH_ERR_BATCH_IDX_OUT_OF_RANGE: return "BatchIdxOutOfRange";
     }
     return "Unknown";
 }
