@@ -15,7 +15,11 @@ reference path) timed on this host on a bounded sample and scaled to
 tokens/s of the same step (see `sample`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
-                       [--no-cpu-baseline] [--fa-reps R] [--only all|step|fa] [--calib-copy]
+                       [--no-cpu-baseline] [--fa-reps R] [--only all|step|fa|mlp]
+                       [--calib-copy]
+
+`mlp_runner` times the tiny-MLP TrainingRunner (train/runner.zig): the
+reference's `--train-demo` loop and tickFrameTrain on batches.
 """
 from __future__ import annotations
 
@@ -219,6 +223,72 @@ def cpu_baseline(args):
                 seconds_measured=round(t_fb1 + t_fb2 + t_adam1, 1))
 
 
+def bench_mlp(args):
+    """The tiny-MLP TrainingRunner (train/runner.zig): the reference's
+    `--train-demo` loop (4 -> 16 -> 4, one-sample tickStep with the prediction
+    read back, 600 steps; docs/embedding.md:894-897 quotes ~730 steps/s on an
+    RTX 3090, Debug build) and tickFrameTrain throughput on batches, timed with
+    HIP events on the stream the steps are enqueued on."""
+    import valkyr_amd as v
+    from valkyr_amd.device import Event, Stream
+
+    out = {}
+    with v.TrainingRunner(4, 16, 4, 0.05, init_seed=0xDEDEDED0) as r:
+        x, t = np.empty(4, np.float32), np.empty(4, np.float32)
+
+        def demo(steps):
+            for k in range(steps):
+                tt = k * 0.05
+                x[:] = (math.sin(tt), math.cos(tt), math.sin(2 * tt), math.cos(2 * tt))
+                t[:] = (0.5 + 0.5 * math.sin(tt), 0.5 + 0.5 * math.cos(tt),
+                        0.5 + 0.333 * math.sin(3 * tt), 0.0)
+                pred = r.tick_step(x, t)
+            return float(0.5 * np.sum((pred - t) ** 2))
+
+        demo(50)
+        t0 = time.perf_counter()
+        last = demo(600)
+        dt = time.perf_counter() - t0
+        out["train_demo"] = {"config": "4-16-4 sgd lr 0.05, 600 blocking tick_step",
+                             "steps_s": round(600 / dt, 1), "us_per_step": round(dt / 600 * 1e6, 2),
+                             "last_loss": round(last, 6),
+                             "reference_steps_s": 730, "reference_hw": "RTX 3090, Debug build"}
+    s = Stream()
+    for name, (I, H, O, N, opt) in {"uv_grid": (5, 16, 3, 256, "adam"),
+                                    "large_batch": (32, 64, 32, 16384, "sgd")}.items():
+        with v.TrainingRunner(I, H, O, 5e-3, max_batch_size=N, optimizer=opt) as r:
+            X = np.random.default_rng(1).uniform(-1, 1, N * I).astype(np.float32)
+            T = np.random.default_rng(2).uniform(0, 1, N * O).astype(np.float32)
+            r.upload_train_batch(X, T)
+            r.tick_frame_train(N, steps=8, stream=s)
+            s.synchronize()
+            K = 256 if N <= 1024 else 32
+            e0, e1 = Event(), Event()
+            e0.record(s)
+            res = r.tick_frame_train(N, steps=K, stream=s)
+            e1.record(s)
+            s.synchronize()
+            ms = e0.elapsed_ms(e1)
+            out[name] = {"config": f"{I}-{H}-{O} {opt} batch {N}, tick_frame_train steps={K}",
+                         "device_us_per_step": round(ms * 1e3 / K, 2),
+                         "host_enqueue_us_per_step": round(res.elapsed_us / K, 2),
+                         "samples_s": round(N * K / (ms * 1e-3), 1)}
+    # the C oracle on the same demo step, one core (the tiny case is latency
+    # work: a CPU core beats any GPU round trip here)
+    try:
+        import oracle as O
+
+        m = O.Mlp(4, 16, 4, seed=0xDEDEDED0)
+        xs, ts = np.zeros(4, np.float32), np.zeros(4, np.float32)
+        t0 = time.perf_counter()
+        for k in range(2000):
+            m.train_step(xs, ts, 0.05)
+        out["train_demo"]["cpu_oracle_steps_s"] = round(2000 / (time.perf_counter() - t0), 1)
+    except Exception as e:  # the oracle is optional on the GPU box
+        out["train_demo"]["cpu_oracle_steps_s"] = f"unavailable: {e}"
+    return out
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -227,7 +297,7 @@ def main():
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--fa-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="all", choices=["all", "step", "fa"],
+    ap.add_argument("--only", default="all", choices=["all", "step", "fa", "mlp"],
                     help="run only the step or only the attention benchmark (profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the benchmarks, run a copy-type kernel of known size "
@@ -253,6 +323,9 @@ def main():
         print(json.dumps({"fa_bwd_ms": round(fa["ms"], 4), "fa_bwd_tflops": round(fa["tflops"], 1)}),
               flush=True)
         return
+    if args.only == "mlp":
+        print(json.dumps({"mlp_runner": bench_mlp(args)}), flush=True)
+        return
     st = bench_step(args, None)
     if args.only == "step":
         print(json.dumps({"ms_per_step": round(st["ms"], 3), "tokens_s": round(st["tokens_s"], 1)}),
@@ -261,6 +334,7 @@ def main():
     fa = bench_fa_bwd(args)
     if args.calib_copy:
         calib_copy()
+    mlp = bench_mlp(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     peak = BF16_PEAK_TFLOPS if args.precision == "bf16" else FP32_PEAK_TFLOPS
     mfu = st["flops"] / (st["ms"] * 1e-3) / 1e12 / peak
@@ -296,6 +370,7 @@ def main():
                      "traffic_unit": "bytes per call (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "calibrated; profiles/fa_bwd_config2_traffic.md)"},
         "cpu_baseline": cpu,
+        "mlp_runner": mlp,
     }
     print(json.dumps(out), flush=True)
 

@@ -81,7 +81,18 @@ typedef enum vkh_status {
     VKH_ERR_BATCH_INDEX_OUT_OF_RANGE = 62,
     VKH_ERR_EMPTY_DATASET = 63,
     VKH_ERR_DATASET_TOO_SHORT = 64,
-    VKH_ERR_BATCH_IDX_OUT_OF_RANGE = 65
+    VKH_ERR_BATCH_IDX_OUT_OF_RANGE = 65,
+    /* tiny-MLP TrainingRunner (train/runner.zig) */
+    VKH_ERR_HIDDEN_DIM_EXCEEDS_MAX = 70,
+    VKH_ERR_X_DIM_MISMATCH = 71,
+    VKH_ERR_TARGET_DIM_MISMATCH = 72,
+    VKH_ERR_OUT_DIM_MISMATCH = 73,
+    VKH_ERR_BATCH_SIZE_NOT_CONFIGURED = 74,
+    VKH_ERR_BATCH_SIZE_EXCEEDS_MAX = 75,
+    VKH_ERR_X_BATCH_DIM_MISMATCH = 76,
+    VKH_ERR_TARGET_BATCH_DIM_MISMATCH = 77,
+    VKH_ERR_OUT_BATCH_DIM_MISMATCH = 78,
+    VKH_ERR_OUTPUT_TOO_LARGE = 79
 } vkh_status;
 
 typedef enum vkh_precision {
@@ -299,6 +310,113 @@ typedef struct vkh_finetune_result {
  * BatchIdxOutOfRange, and the Runner's own. */
 vkh_status vkh_runner_finetune(vkh_runner *r, const vkh_dataset *d, uint32_t batch_idx,
                                uint32_t n_steps, uint32_t rotate, vkh_finetune_result *out);
+
+/* ── tiny-MLP TrainingRunner (train/runner.zig; oracle cpu/train.zig) ───
+ * Linear -> ReLU -> Linear trained in place on the GPU, one runner per
+ * trained function.  Parameters, gradients and Adam moments are each one fp32
+ * blob [W1 (H x I) | b1 (H) | W2 (O x H) | b2 (O)], W row-major with
+ * y = W x + b.  Batches are sample-major [N, dim]. */
+#define VKH_MLP_MAX_HIDDEN 64 /* MLP2_MAX_HIDDEN, runner.zig:128 */
+
+typedef enum vkh_mlp_optimizer { VKH_MLP_SGD = 0, VKH_MLP_ADAM = 1 } vkh_mlp_optimizer;
+typedef enum vkh_mlp_loss { VKH_MLP_MSE = 0, VKH_MLP_CROSS_ENTROPY = 1 } vkh_mlp_loss;
+typedef enum vkh_mlp_decay {
+    VKH_MLP_DECAY_NONE = 0,
+    VKH_MLP_DECAY_LOSS_TARGET = 1 /* idle while last loss <= decay_target */
+} vkh_mlp_decay;
+
+/* Mlp2Config (runner.zig:70-123); defaults from vkh_mlp_config_default. */
+typedef struct vkh_mlp_config {
+    uint32_t dim_in, dim_hidden, dim_out;
+    float lr;                /* mutable later: vkh_mlp_set_lr */
+    float init_scale;        /* W ~ U(-init_scale, init_scale); 0.3 */
+    uint32_t max_batch_size; /* 0 disables the batched surface */
+    uint64_t init_seed;      /* Zig DefaultPrng seed of Mlp.init; 0xCAFE */
+    uint32_t optimizer;      /* vkh_mlp_optimizer; SGD */
+    float adam_beta1, adam_beta2, adam_eps; /* 0.9, 0.999, 1e-8 */
+    uint32_t loss;           /* vkh_mlp_loss; MSE */
+    uint32_t decay;          /* vkh_mlp_decay; NONE */
+    float decay_target;      /* LossDecay.loss_target.target */
+    float weight_decay;      /* decoupled, W1 / W2 only; mutable: vkh_mlp_set_weight_decay */
+} vkh_mlp_config;
+
+typedef struct vkh_mlp vkh_mlp;
+
+void vkh_mlp_config_default(vkh_mlp_config *c, uint32_t dim_in, uint32_t dim_hidden,
+                            uint32_t dim_out, float lr);
+/* TrainingRunner.init (runner.zig:329-544): weights from Mlp.init(seed),
+ * biases and Adam moments zero.  HiddenDimExceedsMax when dim_hidden > 64. */
+vkh_status vkh_mlp_create(const vkh_mlp_config *cfg, vkh_mlp **out);
+void vkh_mlp_destroy(vkh_mlp *m); /* deinit (runner.zig:546-592) */
+vkh_status vkh_mlp_get_config(const vkh_mlp *m, vkh_mlp_config *out);
+vkh_status vkh_mlp_set_lr(vkh_mlp *m, float lr);            /* runner.lr */
+float vkh_mlp_get_lr(const vkh_mlp *m);
+vkh_status vkh_mlp_set_weight_decay(vkh_mlp *m, float wd);  /* runner.weight_decay */
+uint32_t vkh_mlp_adam_step(const vkh_mlp *m);               /* runner.adam_step */
+
+/* Standalone (blocking) calls.  Lengths are element counts of the caller's
+ * slices; mismatches return the reference's error names. */
+/* tickStep (runner.zig:598-620): one-sample MSE + SGD step; out_pred (may be
+ * NULL) gets the prediction before the update.  XDimMismatch,
+ * TargetDimMismatch, OutDimMismatch. */
+vkh_status vkh_mlp_tick_step(vkh_mlp *m, const float *x, size_t x_len, const float *target,
+                             size_t target_len, float *out_pred, size_t out_len);
+/* tickPredict (runner.zig:626-637). */
+vkh_status vkh_mlp_tick_predict(vkh_mlp *m, const float *x, size_t x_len, float *out_pred,
+                                size_t out_len);
+/* tickPredictBatch (runner.zig:705-733): BatchSizeNotConfigured,
+ * XBatchDimMismatch, BatchSizeExceedsMax, OutBatchDimMismatch. */
+vkh_status vkh_mlp_tick_predict_batch(vkh_mlp *m, const float *x_batch, size_t x_len,
+                                      float *out_y, size_t out_len);
+/* tickStepBatch (runner.zig:746-763): one step on the mean gradient of the
+ * batch with the configured loss and optimizer.  TargetBatchDimMismatch too. */
+vkh_status vkh_mlp_tick_step_batch(vkh_mlp *m, const float *x_batch, size_t x_len,
+                                   const float *target_batch, size_t target_len);
+
+/* Cooperative (attach) calls: enqueue on the caller's stream (NULL: the
+ * runner's own) and return without waiting. */
+/* uploadTrainBatch / uploadPredictInputs (runner.zig:784-803): blocking
+ * copies into the runner's batch buffers; call them when no enqueued work
+ * still reads the previous batch. */
+vkh_status vkh_mlp_upload_train_batch(vkh_mlp *m, const float *x_batch, size_t x_len,
+                                      const float *target_batch, size_t target_len);
+vkh_status vkh_mlp_upload_predict_inputs(vkh_mlp *m, const float *x_batch, size_t x_len);
+/* tickStepRecord / tickPredictRecord (runner.zig:655-678). */
+vkh_status vkh_mlp_tick_step_record(vkh_mlp *m, vkh_stream stream, const float *x, size_t x_len,
+                                    const float *target, size_t target_len);
+vkh_status vkh_mlp_tick_predict_record(vkh_mlp *m, vkh_stream stream, const float *x,
+                                       size_t x_len);
+/* tickStepBatchRecord / tickPredictBatchRecord (runner.zig:768-773, :1001-1021). */
+vkh_status vkh_mlp_tick_step_batch_record(vkh_mlp *m, vkh_stream stream, uint32_t n_samples);
+vkh_status vkh_mlp_tick_predict_batch_record(vkh_mlp *m, vkh_stream stream, uint32_t n_samples);
+/* recordPredictReadback / readPredictStaging (runner.zig:815-863): y_batch to
+ * pinned staging, read after the stream is synchronized.  OutputTooLarge. */
+vkh_status vkh_mlp_record_predict_readback(vkh_mlp *m, vkh_stream stream, uint32_t n_samples);
+vkh_status vkh_mlp_read_predict_staging(vkh_mlp *m, float *out_y, size_t out_len);
+/* tickFrameTrain (runner.zig:904-986): up to `budget` steps on the uploaded
+ * batch; with VKH_MLP_DECAY_LOSS_TARGET the previous tick's loss gates
+ * training (idle when <= decay_target) and a fresh loss evaluation is
+ * enqueued every tick.  last_loss is reported only under that policy. */
+vkh_status vkh_mlp_tick_frame_train(vkh_mlp *m, vkh_stream stream, vkh_train_budget budget,
+                                    uint32_t n_samples, vkh_tick_result *out);
+/* getLastLoss (runner.zig:991-993). */
+vkh_status vkh_mlp_get_last_loss(const vkh_mlp *m, float *loss, uint32_t *has_loss);
+
+/* Device buffers, for GPU-resident consumers of the predictions (the
+ * reference binds runner.y / y_batch as shader inputs) and for tests. */
+typedef enum vkh_mlp_buffer_id {
+    VKH_MLP_BUF_PARAMS = 0, VKH_MLP_BUF_GRADS = 1, VKH_MLP_BUF_ADAM_M = 2,
+    VKH_MLP_BUF_ADAM_V = 3, VKH_MLP_BUF_Y = 4, VKH_MLP_BUF_X_BATCH = 5,
+    VKH_MLP_BUF_Y_BATCH = 6, VKH_MLP_BUF_X_TRAIN = 7, VKH_MLP_BUF_TARGET = 8,
+    VKH_MLP_BUF_H_PRE_TRAIN = 9, VKH_MLP_BUF_H_TRAIN = 10, VKH_MLP_BUF_Y_TRAIN = 11,
+    VKH_MLP_BUF_DY_TRAIN = 12, VKH_MLP_BUF_DH_PRE_TRAIN = 13
+} vkh_mlp_buffer_id;
+vkh_status vkh_mlp_buffer(vkh_mlp *m, uint32_t which, float **dptr, size_t *numel);
+/* blocking copy of the first numel floats, after the device is idle */
+vkh_status vkh_mlp_read_buffer(vkh_mlp *m, uint32_t which, float *host, size_t numel);
+/* readWeights (runner.zig:684-689). */
+vkh_status vkh_mlp_read_weights(vkh_mlp *m, float *w1, size_t w1_len, float *b1, size_t b1_len,
+                                float *w2, size_t w2_len, float *b2, size_t b2_len);
 
 /* ── kernels (device pointers; enqueue on `stream`) ─────────────────── */
 

@@ -109,6 +109,23 @@ def _declare(L):
     d("orc_model_step_t", C.c_uint32, C.c_void_p)
     d("orc_model_forward_logits", None, C.c_void_p, U32P, F32P)
     d("orc_now_seconds", C.c_double)
+    U64P = np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")
+    d("orc_zig_prng_seed", None, U64P, C.c_uint64)
+    d("orc_zig_prng_next", C.c_uint64, U64P)
+    d("orc_zig_float32", C.c_float, U64P)
+    d("orc_splitmix64", C.c_uint64, C.POINTER(C.c_uint64))
+    d("orc_mlp_param_count", SZ, SZ, SZ, SZ)
+    d("orc_mlp_init", None, F32P, SZ, SZ, SZ, C.c_float, C.c_uint64)
+    d("orc_mlp_forward", None, F32P, SZ, SZ, SZ, F32P, F32P, F32P, F32P)
+    d("orc_mse_loss", C.c_float, F32P, F32P, SZ)
+    d("orc_mse_loss_grad", None, F32P, F32P, F32P, SZ)
+    d("orc_mlp_backward", None, F32P, SZ, SZ, SZ, F32P, F32P, F32P, F32P, F32P)
+    d("orc_sgd_step", None, F32P, F32P, SZ, C.c_float, C.c_float)
+    d("orc_mlp_train_step", C.c_float, F32P, F32P, SZ, SZ, SZ, F32P, F32P, C.c_float)
+    d("orc_softmax_ce_grad_row", None, F32P, F32P, F32P, SZ)
+    d("orc_mlp_batch_loss", C.c_float, F32P, SZ, SZ, SZ, F32P, F32P, SZ, C.c_int)
+    d("orc_mlp_batch_step", None, F32P, F32P, C.c_void_p, C.c_void_p, SZ, SZ, SZ, F32P, F32P,
+      SZ, C.c_int, C.c_int, C.c_float, C.c_float, C.c_float, C.c_float, C.c_float, C.c_uint32)
 
 
 def _ptr(a):
@@ -397,3 +414,95 @@ class Model:
         out = np.empty(self.T * self.cfg.vocab_size, np.float32)
         lib().orc_model_forward_logits(self._h, np.ascontiguousarray(tokens, np.uint32), out)
         return out
+
+
+# ── tiny-MLP TrainingRunner (cpu/train.zig; runner.zig batched semantics) ──
+
+def splitmix64_stream(seed, n):
+    st = C.c_uint64(seed)
+    return [lib().orc_splitmix64(C.byref(st)) for _ in range(n)]
+
+
+class ZigPrng:
+    """std.Random.DefaultPrng (xoshiro256++ seeded by SplitMix64)."""
+
+    def __init__(self, seed=None, state=None):
+        self.s = np.zeros(4, np.uint64)
+        if state is not None:
+            self.s[:] = np.asarray(state, np.uint64)
+        else:
+            lib().orc_zig_prng_seed(self.s, seed)
+
+    def next(self):
+        return int(lib().orc_zig_prng_next(self.s))
+
+    def float32(self):
+        return np.float32(lib().orc_zig_float32(self.s))
+
+
+class Mlp:
+    """Parameter blob [W1 (H x I) | b1 | W2 (O x H) | b2] plus its views."""
+
+    def __init__(self, dim_in, dim_hidden, dim_out, init_scale=0.3, seed=0xCAFE, params=None):
+        self.I, self.H, self.O = dim_in, dim_hidden, dim_out
+        self.n = int(lib().orc_mlp_param_count(self.I, self.H, self.O))
+        if params is None:
+            self.P = np.empty(self.n, np.float32)
+            lib().orc_mlp_init(self.P, self.I, self.H, self.O, init_scale, seed)
+        else:
+            self.P = f32(params).reshape(-1).copy()
+            assert self.P.size == self.n
+        self.G = np.zeros(self.n, np.float32)
+        self.M = np.zeros(self.n, np.float32)
+        self.V = np.zeros(self.n, np.float32)
+
+    def spans(self):
+        I, H, O = self.I, self.H, self.O
+        o = np.cumsum([0, H * I, H, O * H, O])
+        return {k: slice(o[i], o[i + 1]) for i, k in enumerate(("w1", "b1", "w2", "b2"))}
+
+    def view(self, name, which="P"):
+        return getattr(self, which)[self.spans()[name]]
+
+    def forward(self, x):
+        x = f32(x).reshape(-1)
+        hp, h, y = (np.empty(self.H, np.float32), np.empty(self.H, np.float32),
+                    np.empty(self.O, np.float32))
+        lib().orc_mlp_forward(self.P, self.I, self.H, self.O, x, hp, h, y)
+        return hp, h, y
+
+    def backward(self, x, h_pre, h, dy):
+        lib().orc_mlp_backward(self.P, self.I, self.H, self.O, f32(x).reshape(-1), f32(h_pre),
+                               f32(h), f32(dy), self.G)
+        return self.G
+
+    def train_step(self, x, t, lr):
+        return lib().orc_mlp_train_step(self.P, self.G, self.I, self.H, self.O,
+                                        f32(x).reshape(-1), f32(t).reshape(-1), lr)
+
+    def batch_loss(self, x, t, n, cross_entropy=False):
+        return lib().orc_mlp_batch_loss(self.P, self.I, self.H, self.O, f32(x).reshape(-1),
+                                        f32(t).reshape(-1), n, int(cross_entropy))
+
+    def batch_step(self, x, t, n, lr, cross_entropy=False, adam=False, weight_decay=0.0,
+                   beta1=0.9, beta2=0.999, eps=1e-8, t_step=1):
+        lib().orc_mlp_batch_step(self.P, self.G, _ptr(self.M), _ptr(self.V), self.I, self.H,
+                                 self.O, f32(x).reshape(-1), f32(t).reshape(-1), n,
+                                 int(cross_entropy), int(adam), lr, weight_decay, beta1, beta2,
+                                 eps, t_step)
+
+
+def mse_loss(y, t):
+    y, t = f32(y).reshape(-1), f32(t).reshape(-1)
+    return lib().orc_mse_loss(y, t, y.size)
+
+
+def softmax_ce_grad_row(y, t):
+    y, t = f32(y).reshape(-1), f32(t).reshape(-1)
+    d = np.empty_like(y)
+    lib().orc_softmax_ce_grad_row(d, y, t, y.size)
+    return d
+
+
+def sgd_step(p, g, lr, wd=0.0):
+    lib().orc_sgd_step(p.reshape(-1), f32(g).reshape(-1), p.size, lr, wd)

@@ -1152,3 +1152,221 @@ double orc_now_seconds(void) {
     clock_gettime(CLOCK_MONOTONIC, &ts);
     return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
 }
+
+/* ══ Tiny-MLP TrainingRunner (src/cpu/train.zig; src/train/runner.zig) ══════
+ *
+ * Parameters travel as one blob [W1 (H x I) | b1 (H) | W2 (O x H) | b2 (O)],
+ * row-major, y = W x + b (cpu/train.zig:25-41). */
+
+/* Zig 0.14 std.Random.DefaultPrng = Xoshiro256++ (Blackman & Vigna), seeded
+ * by four SplitMix64 outputs (std/Random/Xoshiro256.zig init/seed). */
+void orc_zig_prng_seed(uint64_t s[4], uint64_t seed) {
+    uint64_t sm = seed;
+    for (int i = 0; i < 4; ++i) s[i] = orc_splitmix64(&sm);
+}
+
+static uint64_t rotl64(uint64_t x, int k) { return (x << k) | (x >> (64 - k)); }
+
+uint64_t orc_zig_prng_next(uint64_t s[4]) {
+    const uint64_t r = rotl64(s[0] + s[3], 23) + s[0];
+    const uint64_t t = s[1] << 17;
+    s[2] ^= s[0];
+    s[3] ^= s[1];
+    s[1] ^= s[2];
+    s[0] ^= s[3];
+    s[2] ^= t;
+    s[3] = rotl64(s[3], 45);
+    return r;
+}
+
+/* std.Random.float(f32): 23 low bits of one u64 draw are the mantissa; the
+ * count of leading zeros of that draw (extended by further draws while the
+ * top 41 bits are all zero) picks the exponent 2^-(1+lz), so the result is
+ * in [0, 1) with every representable value reachable. */
+float orc_zig_float32(uint64_t s[4]) {
+    const uint64_t r = orc_zig_prng_next(s);
+    unsigned lz = r ? (unsigned)__builtin_clzll(r) : 64u;
+    if (lz >= 41) {
+        const uint64_t r2 = orc_zig_prng_next(s);
+        lz = 41 + (r2 ? (unsigned)__builtin_clzll(r2) : 64u);
+        if (lz == 41 + 64) {
+            const uint32_t r3 = (uint32_t)orc_zig_prng_next(s);
+            lz += (unsigned)__builtin_clz(r3 | 0x7FFu);
+        }
+    }
+    const uint32_t bits = ((uint32_t)(126 - lz) << 23) | (uint32_t)(r & 0x7FFFFFu);
+    float f;
+    memcpy(&f, &bits, 4);
+    return f;
+}
+
+size_t orc_mlp_param_count(size_t I, size_t H, size_t O) { return H * I + H + O * H + O; }
+
+/* Mlp.init (cpu/train.zig:47-81): W1 then W2 drawn as (u*2 - 1)*scale with
+ * u = rng.float(f32) from DefaultPrng(seed); biases zero. */
+void orc_mlp_init(float *P, size_t I, size_t H, size_t O, float init_scale, uint64_t seed) {
+    uint64_t s[4];
+    orc_zig_prng_seed(s, seed);
+    float *w1 = P, *b1 = P + H * I, *w2 = b1 + H, *b2 = w2 + O * H;
+    for (size_t k = 0; k < H * I; ++k) w1[k] = (orc_zig_float32(s) * 2.0f - 1.0f) * init_scale;
+    for (size_t k = 0; k < O * H; ++k) w2[k] = (orc_zig_float32(s) * 2.0f - 1.0f) * init_scale;
+    memset(b1, 0, H * sizeof(float));
+    memset(b2, 0, O * sizeof(float));
+}
+
+/* forward (cpu/train.zig:146-173). */
+void orc_mlp_forward(const float *P, size_t I, size_t H, size_t O, const float *x, float *h_pre,
+                     float *h, float *y) {
+    const float *w1 = P, *b1 = P + H * I, *w2 = b1 + H, *b2 = w2 + O * H;
+    for (size_t i = 0; i < H; ++i) {
+        float acc = b1[i];
+        for (size_t j = 0; j < I; ++j) acc += w1[i * I + j] * x[j];
+        h_pre[i] = acc;
+        h[i] = acc > 0 ? acc : 0;
+    }
+    for (size_t i = 0; i < O; ++i) {
+        float acc = b2[i];
+        for (size_t j = 0; j < H; ++j) acc += w2[i * H + j] * h[j];
+        y[i] = acc;
+    }
+}
+
+/* mseLoss / mseLossGrad (cpu/train.zig:180-196): L = 1/2 sum (y - t)^2. */
+float orc_mse_loss(const float *y, const float *t, size_t n) {
+    float acc = 0;
+    for (size_t i = 0; i < n; ++i) {
+        const float d = y[i] - t[i];
+        acc += d * d;
+    }
+    return 0.5f * acc;
+}
+
+void orc_mse_loss_grad(float *dy, const float *y, const float *t, size_t n) {
+    for (size_t i = 0; i < n; ++i) dy[i] = y[i] - t[i];
+}
+
+/* backward (cpu/train.zig:214-254): overwrites G (blob layout). */
+void orc_mlp_backward(const float *P, size_t I, size_t H, size_t O, const float *x,
+                      const float *h_pre, const float *h, const float *dy, float *G) {
+    const float *w2 = P + H * I + H;
+    float *dw1 = G, *db1 = G + H * I, *dw2 = db1 + H, *db2 = dw2 + O * H;
+    for (size_t i = 0; i < O; ++i) {
+        db2[i] = dy[i];
+        for (size_t j = 0; j < H; ++j) dw2[i * H + j] = dy[i] * h[j];
+    }
+    float *dh = (float *)calloc(H ? H : 1, sizeof(float));
+    for (size_t i = 0; i < O; ++i)
+        for (size_t j = 0; j < H; ++j) dh[j] += dy[i] * w2[i * H + j];
+    for (size_t j = 0; j < H; ++j) {
+        const float mask = h_pre[j] > 0 ? 1.0f : 0.0f;
+        const float dpre = dh[j] * mask;
+        db1[j] = dpre;
+        for (size_t k = 0; k < I; ++k) dw1[j * I + k] = dpre * x[k];
+    }
+    free(dh);
+}
+
+/* sgd_step.comp:15-25 (decoupled weight decay on the W spans only, as the
+ * runner pushes weight_decay = 0 for biases, runner.zig:1178-1186);
+ * cpu/train.zig:261-270 is the weight_decay = 0 case. */
+void orc_sgd_step(float *p, const float *g, size_t n, float lr, float weight_decay) {
+    for (size_t i = 0; i < n; ++i) {
+        float v = p[i];
+        if (weight_decay > 0.0f) v = v * (1.0f - lr * weight_decay);
+        p[i] = v - lr * g[i];
+    }
+}
+
+/* trainStep (cpu/train.zig:280-306): forward, MSE, backward, SGD; returns the
+ * loss before the update.  `G` receives the gradients. */
+float orc_mlp_train_step(float *P, float *G, size_t I, size_t H, size_t O, const float *x,
+                         const float *t, float lr) {
+    float *buf = (float *)malloc((2 * H + 2 * O + 1) * sizeof(float));
+    float *h_pre = buf, *h = buf + H, *y = h + H, *dy = y + O;
+    orc_mlp_forward(P, I, H, O, x, h_pre, h, y);
+    const float loss = orc_mse_loss(y, t, O);
+    orc_mse_loss_grad(dy, y, t, O);
+    orc_mlp_backward(P, I, H, O, x, h_pre, h, dy, G);
+    orc_sgd_step(P, G, orc_mlp_param_count(I, H, O), lr, 0.0f);
+    free(buf);
+    return loss;
+}
+
+/* Stable softmax cross-entropy gradient of one row, before the 1/N of the
+ * batch mean (softmax_ce_loss_grad_batched.comp:30-60): dy = softmax(y) - t. */
+void orc_softmax_ce_grad_row(float *dy, const float *y, const float *t, size_t n) {
+    float m = y[0];
+    for (size_t i = 1; i < n; ++i) m = y[i] > m ? y[i] : m;
+    float sum_e = 0;
+    for (size_t i = 0; i < n; ++i) sum_e += expf(y[i] - m);
+    for (size_t i = 0; i < n; ++i) dy[i] = expf(y[i] - m) / sum_e - t[i];
+}
+
+/* Batch loss of the loss-target gate: mlp2_mse_loss_batched.comp (1/2 sum of
+ * squares over N x O, / N) and mlp2_ce_loss_batched.comp (-sum t log softmax,
+ * / N), sequential fp32 as in the shaders. */
+float orc_mlp_batch_loss(const float *P, size_t I, size_t H, size_t O, const float *x,
+                         const float *t, size_t N, int cross_entropy) {
+    float *buf = (float *)malloc((2 * H + O) * sizeof(float));
+    float *h_pre = buf, *h = buf + H, *y = h + H;
+    float total = 0;
+    for (size_t n = 0; n < N; ++n) {
+        orc_mlp_forward(P, I, H, O, x + n * I, h_pre, h, y);
+        const float *tn = t + n * O;
+        if (!cross_entropy) {
+            for (size_t o = 0; o < O; ++o) {
+                const float d = y[o] - tn[o];
+                total += d * d;
+            }
+        } else {
+            float m = y[0];
+            for (size_t o = 1; o < O; ++o) m = y[o] > m ? y[o] : m;
+            float sum_e = 0;
+            for (size_t o = 0; o < O; ++o) sum_e += expf(y[o] - m);
+            const float log_z = m + logf(sum_e);
+            for (size_t o = 0; o < O; ++o) total -= tn[o] * (y[o] - log_z);
+        }
+    }
+    free(buf);
+    return cross_entropy ? total / (float)N : (total * 0.5f) / (float)N;
+}
+
+/* One batched step with the runner's semantics (runner.zig:1053-1220), in
+ * the form of the reference's own CPU check (smoke/training.zig:1576-1612,
+ * :2066-2101): per-sample gradients summed over the batch, times 1/N, then
+ * SGD or Adam (adam_step.comp form, t = the 1-based step) with decoupled
+ * weight decay on W1 and W2 only.  G receives the mean gradient; M and V may
+ * be NULL for SGD. */
+void orc_mlp_batch_step(float *P, float *G, float *M, float *V, size_t I, size_t H, size_t O,
+                        const float *x, const float *t, size_t N, int cross_entropy, int adam,
+                        float lr, float weight_decay, float beta1, float beta2, float eps,
+                        uint32_t t_step) {
+    const size_t np = orc_mlp_param_count(I, H, O);
+    float *gs = (float *)malloc(np * sizeof(float));
+    float *buf = (float *)malloc((2 * H + 2 * O) * sizeof(float));
+    float *h_pre = buf, *h = buf + H, *y = h + H, *dy = y + O;
+    memset(G, 0, np * sizeof(float));
+    for (size_t n = 0; n < N; ++n) {
+        orc_mlp_forward(P, I, H, O, x + n * I, h_pre, h, y);
+        if (cross_entropy)
+            orc_softmax_ce_grad_row(dy, y, t + n * O, O);
+        else
+            orc_mse_loss_grad(dy, y, t + n * O, O);
+        orc_mlp_backward(P, I, H, O, x + n * I, h_pre, h, dy, gs);
+        for (size_t k = 0; k < np; ++k) G[k] += gs[k];
+    }
+    const float inv_n = 1.0f / (float)N;
+    for (size_t k = 0; k < np; ++k) G[k] *= inv_n;
+    /* spans: W1, b1, W2, b2 */
+    const size_t off[5] = {0, H * I, H * I + H, H * I + H + O * H, np};
+    for (int s = 0; s < 4; ++s) {
+        const size_t a = off[s], n = off[s + 1] - off[s];
+        const float wd = (s == 0 || s == 2) ? weight_decay : 0.0f;
+        if (adam)
+            orc_adam_step(P + a, G + a, M + a, V + a, n, lr, beta1, beta2, eps, t_step, wd);
+        else
+            orc_sgd_step(P + a, G + a, n, lr, wd);
+    }
+    free(buf);
+    free(gs);
+}

@@ -168,6 +168,30 @@ uint32_t orc_model_step_t(const orc_model *m);
 /* forward only: logits [T, vocab] (runner forwardLogits). */
 void orc_model_forward_logits(orc_model *m, const uint32_t *tokens, float *logits);
 
+/* ── tiny-MLP TrainingRunner (cpu/train.zig, runner.zig) ────────────────────
+ * Parameter blob: [W1 (H x I) | b1 (H) | W2 (O x H) | b2 (O)]. */
+void orc_zig_prng_seed(uint64_t s[4], uint64_t seed);
+uint64_t orc_zig_prng_next(uint64_t s[4]);
+float orc_zig_float32(uint64_t s[4]);
+size_t orc_mlp_param_count(size_t I, size_t H, size_t O);
+void orc_mlp_init(float *P, size_t I, size_t H, size_t O, float init_scale, uint64_t seed);
+void orc_mlp_forward(const float *P, size_t I, size_t H, size_t O, const float *x, float *h_pre,
+                     float *h, float *y);
+float orc_mse_loss(const float *y, const float *t, size_t n);
+void orc_mse_loss_grad(float *dy, const float *y, const float *t, size_t n);
+void orc_mlp_backward(const float *P, size_t I, size_t H, size_t O, const float *x,
+                      const float *h_pre, const float *h, const float *dy, float *G);
+void orc_sgd_step(float *p, const float *g, size_t n, float lr, float weight_decay);
+float orc_mlp_train_step(float *P, float *G, size_t I, size_t H, size_t O, const float *x,
+                         const float *t, float lr);
+void orc_softmax_ce_grad_row(float *dy, const float *y, const float *t, size_t n);
+float orc_mlp_batch_loss(const float *P, size_t I, size_t H, size_t O, const float *x,
+                         const float *t, size_t N, int cross_entropy);
+void orc_mlp_batch_step(float *P, float *G, float *M, float *V, size_t I, size_t H, size_t O,
+                        const float *x, const float *t, size_t N, int cross_entropy, int adam,
+                        float lr, float weight_decay, float beta1, float beta2, float eps,
+                        uint32_t t_step);
+
 /* time helpers for the CPU baseline */
 double orc_now_seconds(void);
 

@@ -54,7 +54,8 @@ def test_config_struct_layout_matches_header(tmp_path):
     structs = {"vkh_config": L.Config, "vkh_attn_params": L.AttnParams,
                "vkh_cce_params": L.CceParams, "vkh_rope_params": L.RopeParams,
                "vkh_train_budget": L.TrainBudget, "vkh_tick_result": L.TickResult,
-               "vkh_init_weights": L.InitWeights, "vkh_layer_weights": L.LayerWeights}
+               "vkh_init_weights": L.InitWeights, "vkh_layer_weights": L.LayerWeights,
+               "vkh_mlp_config": L.MlpConfig}
     body = "\n".join(f'printf("%s %zu\\n", "{n}", sizeof({n}));' for n in structs)
     src = tmp_path / "s.c"
     src.write_text(f'#include <stdio.h>\n#include "vkhip.h"\nint main(void){{ {body} return 0; }}\n')
@@ -99,3 +100,21 @@ def test_runner_without_device_reports_no_device():
     with pytest.raises(v.VkhError) as e:
         v.Runner(cfg)
     assert e.value.name == "NoDevice"
+
+
+def test_mlp_config_checks_before_device():
+    """runner.zig:329: HiddenDimExceedsMax comes before any device work."""
+    import valkyr_amd as v
+
+    with pytest.raises(v.VkhError) as e:
+        v.TrainingRunner(4, 65, 3, 0.1)
+    assert e.value.name == "HiddenDimExceedsMax"
+    with pytest.raises(v.VkhError) as e:
+        v.TrainingRunner(0, 8, 3, 0.1)
+    assert e.value.name == "InvalidArgument"
+    c = v.make_mlp_config(4, 8, 3, 0.05)
+    # Mlp2Config defaults (runner.zig:70-123)
+    assert (c.init_seed, c.max_batch_size, c.optimizer, c.loss, c.decay) == (0xCAFE, 0, 0, 0, 0)
+    assert abs(c.init_scale - 0.3) < 1e-7 and abs(c.adam_beta1 - 0.9) < 1e-7
+    assert abs(c.adam_beta2 - 0.999) < 1e-7 and abs(c.adam_eps - 1e-8) < 1e-15
+    assert c.weight_decay == 0.0

@@ -7,9 +7,11 @@ fallback: without the built library, `lib()` raises MissingLibraryError.
 from ._lib import (Config, MissingLibraryError, VkhError, check, device_count, lib)  # noqa: F401
 from .runner import Runner, make_config  # noqa: F401
 from .dataset import Dataset, finetune, mean_ce  # noqa: F401
+from .mlp import TrainingRunner, make_mlp_config  # noqa: F401
 
 __all__ = ["Config", "MissingLibraryError", "VkhError", "Runner", "make_config", "lib", "check",
-           "device_count", "build", "Dataset", "finetune", "mean_ce"]
+           "device_count", "build", "Dataset", "finetune", "mean_ce", "TrainingRunner",
+           "make_mlp_config"]
 
 
 def build(jobs: int = 8) -> str:

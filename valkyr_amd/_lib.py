@@ -39,7 +39,10 @@ STATUS = {
     46: "UnsupportedLoraCheckpointVersion", 47: "LoraCheckpointConfigSizeMismatch",
     48: "LoraCheckpointConfigMismatch", 49: "LoraCheckpointEmpty", 50: "IoError",
     60: "InputIdsLen", 61: "TargetIdsLen", 62: "BatchIndexOutOfRange", 63: "EmptyDataset",
-    64: "DatasetTooShort", 65: "BatchIdxOutOfRange",
+    64: "DatasetTooShort", 65: "BatchIdxOutOfRange", 70: "HiddenDimExceedsMax",
+    71: "XDimMismatch", 72: "TargetDimMismatch", 73: "OutDimMismatch",
+    74: "BatchSizeNotConfigured", 75: "BatchSizeExceedsMax", 76: "XBatchDimMismatch",
+    77: "TargetBatchDimMismatch", 78: "OutBatchDimMismatch", 79: "OutputTooLarge",
 }
 
 
@@ -110,6 +113,18 @@ class FinetuneResult(C.Structure):
                 ("mean_step_ms", C.c_double)]
 
 
+class MlpConfig(C.Structure):
+    """vkh_mlp_config: Mlp2Config (runner.zig:70-123)."""
+
+    _fields_ = [
+        ("dim_in", C.c_uint32), ("dim_hidden", C.c_uint32), ("dim_out", C.c_uint32),
+        ("lr", C.c_float), ("init_scale", C.c_float), ("max_batch_size", C.c_uint32),
+        ("init_seed", C.c_uint64), ("optimizer", C.c_uint32), ("adam_beta1", C.c_float),
+        ("adam_beta2", C.c_float), ("adam_eps", C.c_float), ("loss", C.c_uint32),
+        ("decay", C.c_uint32), ("decay_target", C.c_float), ("weight_decay", C.c_float),
+    ]
+
+
 P = C.c_void_p
 U32 = C.c_uint32
 SZ = C.c_size_t
@@ -155,6 +170,31 @@ SIGNATURES = [
     ("vkh_dataset_batch_seqs", ST, [P, SZ, SZ, U32, P, P]),
     ("vkh_mean_ce", F, [P, P, SZ, SZ]),
     ("vkh_runner_finetune", ST, [P, P, U32, U32, U32, C.POINTER(FinetuneResult)]),
+    ("vkh_mlp_config_default", None, [C.POINTER(MlpConfig), U32, U32, U32, F]),
+    ("vkh_mlp_create", ST, [C.POINTER(MlpConfig), C.POINTER(P)]),
+    ("vkh_mlp_destroy", None, [P]),
+    ("vkh_mlp_get_config", ST, [P, C.POINTER(MlpConfig)]),
+    ("vkh_mlp_set_lr", ST, [P, F]),
+    ("vkh_mlp_get_lr", F, [P]),
+    ("vkh_mlp_set_weight_decay", ST, [P, F]),
+    ("vkh_mlp_adam_step", U32, [P]),
+    ("vkh_mlp_tick_step", ST, [P, P, SZ, P, SZ, P, SZ]),
+    ("vkh_mlp_tick_predict", ST, [P, P, SZ, P, SZ]),
+    ("vkh_mlp_tick_predict_batch", ST, [P, P, SZ, P, SZ]),
+    ("vkh_mlp_tick_step_batch", ST, [P, P, SZ, P, SZ]),
+    ("vkh_mlp_upload_train_batch", ST, [P, P, SZ, P, SZ]),
+    ("vkh_mlp_upload_predict_inputs", ST, [P, P, SZ]),
+    ("vkh_mlp_tick_step_record", ST, [P, P, P, SZ, P, SZ]),
+    ("vkh_mlp_tick_predict_record", ST, [P, P, P, SZ]),
+    ("vkh_mlp_tick_step_batch_record", ST, [P, P, U32]),
+    ("vkh_mlp_tick_predict_batch_record", ST, [P, P, U32]),
+    ("vkh_mlp_record_predict_readback", ST, [P, P, U32]),
+    ("vkh_mlp_read_predict_staging", ST, [P, P, SZ]),
+    ("vkh_mlp_tick_frame_train", ST, [P, P, TrainBudget, U32, C.POINTER(TickResult)]),
+    ("vkh_mlp_get_last_loss", ST, [P, C.POINTER(F), C.POINTER(U32)]),
+    ("vkh_mlp_buffer", ST, [P, U32, C.POINTER(P), C.POINTER(SZ)]),
+    ("vkh_mlp_read_buffer", ST, [P, U32, P, SZ]),
+    ("vkh_mlp_read_weights", ST, [P, P, SZ, P, SZ, P, SZ, P, SZ]),
     ("vkh_fa_forward", ST, [C.POINTER(AttnParams), P, P, P, P, P, P]),
     ("vkh_fa_bw_d", ST, [C.POINTER(AttnParams), P, P, P, P, P]),
     ("vkh_fa_bw_dq", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P]),

@@ -138,6 +138,16 @@ const char *vkh_status_name(vkh_status s) {
     case VKH_ERR_EMPTY_DATASET: return "EmptyDataset";
     case VKH_ERR_DATASET_TOO_SHORT: return "DatasetTooShort";
     case VKH_ERR_BATCH_IDX_OUT_OF_RANGE: return "BatchIdxOutOfRange";
+    case VKH_ERR_HIDDEN_DIM_EXCEEDS_MAX: return "HiddenDimExceedsMax";
+    case VKH_ERR_X_DIM_MISMATCH: return "XDimMismatch";
+    case VKH_ERR_TARGET_DIM_MISMATCH: return "TargetDimMismatch";
+    case VKH_ERR_OUT_DIM_MISMATCH: return "OutDimMismatch";
+    case VKH_ERR_BATCH_SIZE_NOT_CONFIGURED: return "BatchSizeNotConfigured";
+    case VKH_ERR_BATCH_SIZE_EXCEEDS_MAX: return "BatchSizeExceedsMax";
+    case VKH_ERR_X_BATCH_DIM_MISMATCH: return "XBatchDimMismatch";
+    case VKH_ERR_TARGET_BATCH_DIM_MISMATCH: return "TargetBatchDimMismatch";
+    case VKH_ERR_OUT_BATCH_DIM_MISMATCH: return "OutBatchDimMismatch";
+    case VKH_ERR_OUTPUT_TOO_LARGE: return "OutputTooLarge";
     }
     return "Unknown";
 }
