@@ -14,6 +14,13 @@
  * `src/train/transformer.zig`).  Loop orders and the fp64 accumulators are
  * kept where the Zig has them; every function cites the file:line it follows.
  *
+ * It also restates the tiny-MLP trainer (`src/cpu/train.zig` and the batched
+ * semantics of `src/train/runner.zig`), including `Mlp.init`'s generator:
+ * Zig 0.14's DefaultPrng (xoshiro256++ seeded by SplitMix64, pinned by the
+ * published vectors of both) and `Random.float(f32)`.  Parity unpinned: which
+ * bits of the draw `Random.float(f32)` uses for the mantissa (restated from
+ * Zig's std source; no Zig toolchain or Zig-written vector exists here).
+ *
  * Extensions over the reference (documented where they appear):
  *   - a batch axis: T = n_seqs * seq_len rows; attention is block-diagonal
  *     per sequence and the RoPE position of row r is r % seq_len;
