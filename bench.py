@@ -15,11 +15,13 @@ reference path) timed on this host on a bounded sample and scaled to
 tokens/s of the same step (see `sample`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
-                       [--no-cpu-baseline] [--fa-reps R] [--only all|step|fa|mlp]
-                       [--calib-copy]
+                       [--no-cpu-baseline] [--fa-reps R]
+                       [--only all|step|fa|mlp|config4|config5] [--calib-copy]
 
 `mlp_runner` times the tiny-MLP TrainingRunner (train/runner.zig): the
-reference's `--train-demo` loop and tickFrameTrain on batches.
+reference's `--train-demo` loop and tickFrameTrain on batches.  `--only config4`
+/ `--only config5` run the metric's Qwen3-4B LoRA and Qwen3-8B long-context
+configurations at full size (memory, step time, size-independent checks).
 """
 from __future__ import annotations
 
@@ -44,6 +46,18 @@ QWEN3_06B = dict(dim=1024, n_heads=16, n_kv_heads=8, head_dim=128, ff_dim=3072, 
                  n_layers=28, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=128,
                  rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
                  n_seqs=4, tied_embeddings=1)
+
+
+# configs 4 and 5 of the metric (parity / capacity cases, not the headline line)
+QWEN3_4B_LORA = dict(dim=2560, n_heads=32, n_kv_heads=8, head_dim=128, ff_dim=9728, n_pos=2048,
+                     n_layers=36, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=128,
+                     rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
+                     n_seqs=1, tied_embeddings=1, lora_targets=0xF, lora_rank=16,
+                     lora_alpha=32.0, lora_lr_b_scale=1.0)
+QWEN3_8B = dict(dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, ff_dim=12288, n_pos=8192,
+                n_layers=36, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=128,
+                rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
+                n_seqs=1, tied_embeddings=0)
 
 
 def step_flops(c) -> float:
@@ -223,6 +237,82 @@ def cpu_baseline(args):
                 seconds_measured=round(t_fb1 + t_fb2 + t_adam1, 1))
 
 
+def bench_config(name, args):
+    """Config 4 (Qwen3-4B shape, frozen bf16-operand base + LoRA r16 on q/k/v/o, 1 x 2048)
+    or config 5 (Qwen3-8B shape, full fine-tune, 1 x 8192, untied head) at full size:
+    device memory, step time, and the size-independent checks the shapes allow (loss of a
+    random init = ln V within 0.5; for LoRA at step 1: B = 0 makes every dA exactly zero,
+    dB non-zero, A and the frozen base unchanged bit for bit)."""
+    import valkyr_amd as v
+    from valkyr_amd.runner import GRAD, PARAM, Q, DOWN, lora_a, lora_b
+
+    c = dict(QWEN3_4B_LORA if name == "config4" else QWEN3_8B)
+    lora = bool(c.get("lora_targets"))
+    T = c["n_pos"] * c["n_seqs"]
+    out = {"shape": {k: c[k] for k in ("dim", "n_heads", "n_kv_heads", "head_dim", "ff_dim",
+                                       "n_layers", "vocab_size")},
+           "tokens_per_step": T}
+    try:
+        r = v.Runner(v.make_config(**c, precision=1))
+    except v.VkhError as e:
+        out["error"] = f"{e.name}: {e.message}"
+        return out
+    r.init_random(seed=20261202, std=0.02, lora_std=0.02)
+    out["trainable_params"] = r.param_count()
+    out["device_gib"] = round(r.device_bytes() / 2**30, 1)
+    rng = np.random.default_rng(2)
+    tok = rng.integers(0, c["vocab_size"], T, dtype=np.uint32)
+    tgt = rng.integers(0, c["vocab_size"], T, dtype=np.uint32)
+    print(f"[bench] {name}: {out['trainable_params']:,} trainable params, "
+          f"{out['device_gib']} GiB", file=sys.stderr, flush=True)
+    checks = {}
+    L = c["n_layers"]
+    if lora:
+        a0 = {(l, p): r.get(PARAM, l, lora_a(p)) for l in (0, L - 1) for p in range(4)}
+        w0 = {(l, w): r.get(PARAM, l, w) for l, w in ((0, Q), (L - 1, DOWN))}
+    t0 = time.perf_counter()
+    r.step(tok, tgt)
+    first_s = time.perf_counter() - t0
+    loss0 = r.last_loss()
+    # after the unit-gain final RMSNorm every logit of a N(0, std^2) head is
+    # N(0, D std^2): the mean CE of a random init is ln V + D std^2 / 2, and the
+    # target logits' mean over T tokens adds noise of std sqrt(D std^2 / T)
+    var = c["dim"] * 0.02 ** 2
+    want = math.log(c["vocab_size"]) + var / 2
+    checks["loss_init"] = round(loss0, 4)
+    checks["loss_init_closed_form"] = round(want, 4)
+    ok = math.isfinite(loss0) and abs(loss0 - want) < 4 * math.sqrt(var / T) + 0.01
+    if lora:
+        dA_zero = all(not r.get(GRAD, l, lora_a(p)).any() for l in range(L) for p in range(4))
+        dB_live = all(r.get(GRAD, l, lora_b(p)).any() for l in (0, L - 1) for p in range(4))
+        a_same = all(np.array_equal(r.get(PARAM, l, lora_a(p)), a) for (l, p), a in a0.items())
+        w_same = all(np.array_equal(r.get(PARAM, l, w), x) for (l, w), x in w0.items())
+        checks.update(dA_exactly_zero_at_step1=dA_zero, dB_nonzero=dB_live,
+                      A_unchanged=a_same, frozen_base_unchanged=w_same)
+        ok = ok and dA_zero and dB_live and a_same and w_same
+    else:
+        g = r.get(GRAD, 0, Q)
+        checks["grad_layer0_q_finite_nonzero"] = bool(np.isfinite(g).all() and g.any())
+        ok = ok and checks["grad_layer0_q_finite_nonzero"]
+    checks["all_passed"] = bool(ok)
+    K = max(1, min(args.steps, 10 if name == "config4" else 3))
+    r.step_async(tok, tgt)
+    r.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(K):
+        r.step_async(tok, tgt)
+    r.synchronize()
+    wall = time.perf_counter() - t0
+    loss1 = r.last_loss()
+    r.close()
+    out.update(steps=K, ms_per_step=round(1000 * wall / K, 2), tokens_s=round(T * K / wall, 1),
+               first_step_s=round(first_s, 2), loss=[round(loss0, 4), round(loss1, 4)],
+               checks=checks)
+    print(f"[bench] {name}: {out['ms_per_step']} ms/step, {out['tokens_s']:,.0f} tok/s, "
+          f"checks {checks}", file=sys.stderr, flush=True)
+    return out
+
+
 def bench_mlp(args):
     """The tiny-MLP TrainingRunner (train/runner.zig): the reference's
     `--train-demo` loop (4 -> 16 -> 4, one-sample tickStep with the prediction
@@ -297,7 +387,8 @@ def main():
     ap.add_argument("--precision", default="bf16", choices=["bf16", "fp32"])
     ap.add_argument("--fa-reps", type=int, default=50)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--only", default="all", choices=["all", "step", "fa", "mlp"],
+    ap.add_argument("--only", default="all",
+                    choices=["all", "step", "fa", "mlp", "config4", "config5"],
                     help="run only the step or only the attention benchmark (profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the benchmarks, run a copy-type kernel of known size "
@@ -325,6 +416,9 @@ def main():
         return
     if args.only == "mlp":
         print(json.dumps({"mlp_runner": bench_mlp(args)}), flush=True)
+        return
+    if args.only in ("config4", "config5"):
+        print(json.dumps({args.only: bench_config(args.only, args)}), flush=True)
         return
     st = bench_step(args, None)
     if args.only == "step":
