@@ -8,8 +8,9 @@
 
 One JSON line on stdout.  `roofline` is the FA-2 backward (fa_bw_d + dK/dV +
 dQ kernels) at config 2 (B=4, S=2048, 16/8 heads, hd 128, causal, bf16
-operands), timed with HIP events on the stream it runs on; its algorithmic
-work is 10 * B * Hq * hd * S(S+1)/2 = 171.88 GFLOP per call.
+Q/K/V/dO and bf16 O from the forward), timed with HIP events on the stream it
+runs on; its algorithmic work is 10 * B * Hq * hd * S(S+1)/2 = 171.88 GFLOP
+per call.
 `cpu_baseline` is the C oracle (a scalar restatement of valkyr's CPU
 reference path) timed on this host on a bounded sample and scaled to
 tokens/s of the same step (see `sample`).
@@ -126,19 +127,22 @@ def bench_fa_bwd(args):
     q = DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(nq, np.float32)))
     k = DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(nk, np.float32)))
     vv = DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(nk, np.float32)))
-    dout = DeviceBuffer.from_numpy((0.1 * rng.standard_normal(nq)).astype(np.float32))
+    # config 2: dO ~N(0, 1e-2) in bf16; O (bf16) and LSE from the forward of the same inputs
+    dout16 = DeviceBuffer.from_numpy(
+        f32_to_bf16_bits((0.1 * rng.standard_normal(nq)).astype(np.float32)))
     o = DeviceBuffer(nq * 4)
+    o16 = DeviceBuffer(nq * 2)
     lse = DeviceBuffer(B * S * H * 4)
     d = DeviceBuffer(B * S * H * 4)
-    dout16 = DeviceBuffer(nq * 2)
     dq, dk, dv = DeviceBuffer(nq * 4), DeviceBuffer(nk * 4), DeviceBuffer(nk * 4)
     p = K.attn_params(S, S, H, Hkv, hd, True, B, K.BF16)
     ws = DeviceBuffer(max(K.fa_backward_workspace_bytes(p), 4))  # bf16 dS
     s = Stream()
     K.fa_forward(p, q, k, vv, o, lse, stream=s)  # O and LSE of the same inputs
+    K.cast_f32_to_bf16(o, o16, nq, stream=s)
 
     def once():
-        K.fa_bw_d(p, o, dout, d, dout16, stream=s)
+        K.fa_bw_d_bf16(p, o16, dout16, d, stream=s)
         K.fa_backward(p, q, k, vv, dout16, lse, d, dq, dk, dv, ws, stream=s)
 
     for _ in range(10):  # clocks settle over the first calls
@@ -456,8 +460,8 @@ def main():
         "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (config 2)",
                    "ms": round(fa["ms"], 4), "tflops": round(fa["tflops"], 1),
                    "frac_bf16_peak": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4)},
-        "roofline": {"kernel": "attention backward, config 2: fa_bw_d8_k + fa_bwd_dkv3_k + "
-                               "fa_dq_gemm_k (one call)", "bound": "mfma",
+        "roofline": {"kernel": "attention backward, config 2: fa_bw_d8_k<bf16> + "
+                               "fa_bwd_dkv3_k + fa_dq_gemm_k (one call)", "bound": "mfma",
                      "achieved": round(fa["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa_bwd_config2_traffic.md"),

@@ -437,6 +437,11 @@ vkh_status vkh_fa_forward(const vkh_attn_params *p, const void *q, const void *k
  * fp32 and `dout_bf16` (if non-NULL) receives its bf16 copy, D pairing with it. */
 vkh_status vkh_fa_bw_d(const vkh_attn_params *p, const float *o, const float *dout, float *d,
                        void *dout_bf16, vkh_stream stream);
+/* shaders/fa_bw_d.comp with O and dO stored in bf16 (the operand precision of
+ * the bf16 attention path: config 2's bf16 dO, the forward's bf16 O): D[t, h] =
+ * sum_d O * dO, fp32 out; head_dim 64 or 128. */
+vkh_status vkh_fa_bw_d_bf16(const vkh_attn_params *p, const void *o_bf16, const void *dout_bf16,
+                            float *d, vkh_stream stream);
 /* shaders/fa_bw_dq.comp: dQ fp32 (overwrite). */
 vkh_status vkh_fa_bw_dq(const vkh_attn_params *p, const void *q, const void *k, const void *v,
                         const void *dout, const float *lse, const float *d, float *dq,

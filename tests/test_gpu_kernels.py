@@ -351,6 +351,24 @@ FA_BF16_CASES = [  # (n, H, Hkv, hd, causal, B)
 ]
 
 
+@pytest.mark.parametrize("hd,rows", [(128, 4 * 2048 * 16), (64, 3 * 100 * 4)])
+def test_fa_bw_d_bf16_inputs(hd, rows):
+    """D = rowsum(O dO) from bf16 O and dO (fa_bw_d.comp with bf16 storage) vs
+    the oracle's fp64 row dot of the same bf16 values; the first case is
+    config 2's full size."""
+    from valkyr_amd import kernels as K
+
+    H = 16 if hd == 128 else 4
+    n = rows // H
+    note(f"fa_bw_d bf16 inputs hd={hd} rows={rows}")
+    o16, o_r = bf16_dev(O.normal(n * H * hd, 111))
+    d16, d_r = bf16_dev(O.normal(n * H * hd, 112, 0.1))
+    p = K.attn_params(n, n, H, H, hd, True, 1, K.BF16)
+    bd = zeros(n * H)
+    K.fa_bw_d_bf16(p, o16, d16, bd)
+    assert rel_l2(O.fa_bw_d(o_r, d_r, n, H, hd), host(bd)) < 1e-6
+
+
 @pytest.mark.parametrize("case", FA_BF16_CASES)
 def test_flash_attention_bf16_mfma(case):
     """MFMA kernels vs the oracle on the same bf16-rounded Q/K/V/dO."""

@@ -197,6 +197,7 @@ SIGNATURES = [
     ("vkh_mlp_read_weights", ST, [P, P, SZ, P, SZ, P, SZ, P, SZ]),
     ("vkh_fa_forward", ST, [C.POINTER(AttnParams), P, P, P, P, P, P]),
     ("vkh_fa_bw_d", ST, [C.POINTER(AttnParams), P, P, P, P, P]),
+    ("vkh_fa_bw_d_bf16", ST, [C.POINTER(AttnParams), P, P, P, P]),
     ("vkh_fa_bw_dq", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P]),
     ("vkh_fa_bw_dkv", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P, P]),
     ("vkh_fa_backward_workspace_bytes", SZ, [C.POINTER(AttnParams)]),

@@ -176,6 +176,18 @@ vkh_status vkh_fa_bw_d(const vkh_attn_params *p, const float *o, const float *do
     return VKH_OK;
 }
 
+vkh_status vkh_fa_bw_d_bf16(const vkh_attn_params *p, const void *o_bf16, const void *dout_bf16,
+                            float *d, vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(o_bf16 && dout_bf16 && d, "null pointer");
+    if (p->head_dim != 64 && p->head_dim != 128)
+        return fail(VKH_ERR_UNSUPPORTED, "bf16 D preprocess needs head_dim 64 or 128");
+    const AttnShape s = attn_shape(p);
+    const long ld = (long)p->n_heads * p->head_dim;
+    VKH_HIP(fa_bw_d_bf16(s, (const bf16 *)o_bf16, ld, (const bf16 *)dout_bf16, ld, d, S(stream)));
+    return VKH_OK;
+}
+
 static AttnPtrs attn_ptrs(const vkh_attn_params *p, const void *q, const void *k, const void *v,
                           const void *dout, const float *lse, const float *d) {
     AttnPtrs a{};

@@ -211,7 +211,7 @@ __global__ __launch_bounds__(NT, 2) void fa_fwd_bf16_k(AttnShape s, const bf16 *
         for (int i = 0; i < DSUB; ++i) {
             const f32x4 a = oacc[i][qs];
             const float4 ov = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-            *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) = ov;
+            if (o) *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) = ov;
             if (ob) {
                 bf16x4 bv;
                 bv[0] = (bf16)ov.x; bv[1] = (bf16)ov.y; bv[2] = (bf16)ov.z; bv[3] = (bf16)ov.w;
@@ -261,9 +261,24 @@ VKH_DEV double dppd(double v) {
     return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
 }
 
-template <int LPH>
-__global__ __launch_bounds__(NT) void fa_bw_d8_k(AttnShape s, const float *o, long ldo,
-                                                  const float *dout, long lddo, float *d,
+// Eight elements of an fp32 or bf16 row, widened to fp32.
+VKH_DEV void load_row8(const float *p, float4 &a, float4 &b) {
+    a = reinterpret_cast<const float4 *>(p)[0];
+    b = reinterpret_cast<const float4 *>(p)[1];
+}
+VKH_DEV void load_row8(const bf16 *p, float4 &a, float4 &b) {
+    const bf16x8 v = *reinterpret_cast<const bf16x8 *>(p);
+    a = make_float4((float)v[0], (float)v[1], (float)v[2], (float)v[3]);
+    b = make_float4((float)v[4], (float)v[5], (float)v[6], (float)v[7]);
+}
+
+// D = rowsum(O * dO), LPH lanes per (row, head) with 8 elements each.  TI is
+// the storage type of O and dO: fp32 (the reference's FaBwDPush layout; with
+// dout16 the bf16 copy of dO the MFMA kernels read is written here too) or
+// bf16 (both already in the operand precision: half the bytes to read).
+template <int LPH, class TI>
+__global__ __launch_bounds__(NT) void fa_bw_d8_k(AttnShape s, const TI *o, long ldo,
+                                                  const TI *dout, long lddo, float *d,
                                                   bf16 *dout16, long lddo16) {
     constexpr int G = 64 / LPH;
     const int lane = threadIdx.x % 64, j = lane % LPH, g = lane / LPH;
@@ -275,9 +290,8 @@ __global__ __launch_bounds__(NT) void fa_bw_d8_k(AttnShape s, const float *o, lo
         if (it < rows) {
             const long t = it / s.n_heads;
             const int h = (int)(it % s.n_heads);
-            const float4 *op = reinterpret_cast<const float4 *>(o + t * ldo + h * hd + 8 * j);
-            const float4 *dp = reinterpret_cast<const float4 *>(dout + t * lddo + h * hd + 8 * j);
-            x.o0 = op[0]; x.o1 = op[1]; x.d0 = dp[0]; x.d1 = dp[1];
+            load_row8(o + t * ldo + h * hd + 8 * j, x.o0, x.o1);
+            load_row8(dout + t * lddo + h * hd + 8 * j, x.d0, x.d1);
         } else {
             x.o0 = x.o1 = x.d0 = x.d1 = make_float4(0.f, 0.f, 0.f, 0.f);
         }
@@ -1186,7 +1200,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, 
         for (int i = 0; i < DSUB; ++i) {
             const f32x4 a = oacc[i][qs];
             const float4 ov = make_float4(a[0] * inv, a[1] * inv, a[2] * inv, a[3] * inv);
-            *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) = ov;
+            if (o) *reinterpret_cast<float4 *>(orow + 16 * i + 4 * g) = ov;
             if (ob) {
                 bf16x4 bv;
                 bv[0] = (bf16)ov.x; bv[1] = (bf16)ov.y; bv[2] = (bf16)ov.z; bv[3] = (bf16)ov.w;
@@ -1423,15 +1437,33 @@ hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *do
         const int lph = s.head_dim / 8, per_block = (NT / 64) * (64 / lph);
         const long grid = std::min<long>(4096, (rows + 2L * per_block - 1) / (2L * per_block));
         if (lph == 16)
-            hipLaunchKernelGGL(fa_bw_d8_k<16>, dim3((unsigned)grid), dim3(NT), 0, st, s, o, ldo, dout,
-                               lddo, d, dout_bf16, lddo16);
+            hipLaunchKernelGGL((fa_bw_d8_k<16, float>), dim3((unsigned)grid), dim3(NT), 0, st, s, o,
+                               ldo, dout, lddo, d, dout_bf16, lddo16);
         else
-            hipLaunchKernelGGL(fa_bw_d8_k<8>, dim3((unsigned)grid), dim3(NT), 0, st, s, o, ldo, dout,
-                               lddo, d, dout_bf16, lddo16);
+            hipLaunchKernelGGL((fa_bw_d8_k<8, float>), dim3((unsigned)grid), dim3(NT), 0, st, s, o,
+                               ldo, dout, lddo, d, dout_bf16, lddo16);
         return hipGetLastError();
     }
     hipLaunchKernelGGL(fa_bw_d_k, dim3(rows_grid(rows)), dim3(NT), 0, st, s, o, ldo, dout, lddo, d,
                        dout_bf16, lddo16);
+    return hipGetLastError();
+}
+
+hipError_t fa_bw_d_bf16(const AttnShape &s, const bf16 *o, long ldo, const bf16 *dout, long lddo,
+                        float *d, hipStream_t st) {
+    const long rows = (long)s.n_batch * s.n_q * s.n_heads;
+    if (rows <= 0) return hipSuccess;
+    if ((s.head_dim != 128 && s.head_dim != 64) || ((uintptr_t)o & 15) || ((uintptr_t)dout & 15) ||
+        ldo % 8 || lddo % 8)
+        return hipErrorInvalidValue;
+    const int lph = s.head_dim / 8, per_block = (NT / 64) * (64 / lph);
+    const long grid = std::min<long>(4096, (rows + 2L * per_block - 1) / (2L * per_block));
+    if (lph == 16)
+        hipLaunchKernelGGL((fa_bw_d8_k<16, bf16>), dim3((unsigned)grid), dim3(NT), 0, st, s, o, ldo,
+                           dout, lddo, d, (bf16 *)nullptr, 0L);
+    else
+        hipLaunchKernelGGL((fa_bw_d8_k<8, bf16>), dim3((unsigned)grid), dim3(NT), 0, st, s, o, ldo,
+                           dout, lddo, d, (bf16 *)nullptr, 0L);
     return hipGetLastError();
 }
 

@@ -105,6 +105,14 @@ hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx,
     return run16<Lay::K, Lay::MN>(a, b, GemmShape{M, K, N}, e, ws, st);
 }
 
+hipError_t g16_nn_bf16(const bf16 *dy, long lddy, const bf16 *w, long ldw, bf16 *dx, long lddx,
+                       int M, int N, int K, const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op(dy, lddy, M, N, a) || !make_op(w, ldw, N, K, b)) return hipErrorInvalidValue;
+    EpiStoreBf16 e{dx, lddx, 1.f};
+    return run16<Lay::K, Lay::MN>(a, b, GemmShape{M, K, N}, e, ws, st);
+}
+
 hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw, long lddw, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
     // C[n, k'] = sum_m dy[m, n] x[m, k']: both operands MN-major over m

@@ -42,6 +42,9 @@ hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, lo
                   const GemmWs &ws, hipStream_t st);
 hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
+// dx as bf16 (the operand precision of the next kernel), no split-K / fp32 copy.
+hipError_t g16_nn_bf16(const bf16 *dy, long lddy, const bf16 *w, long ldw, bf16 *dx, long lddx,
+                       int M, int N, int K, const GemmWs &ws, hipStream_t st);
 hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw, long lddw, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
 size_t g16_ws_bytes_for(int M, int N, int K);
@@ -154,6 +157,9 @@ hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k
 // D = rowsum(O * dO); optionally also writes dO as bf16 (dout_bf16, ld lddo16)
 hipError_t fa_bw_d(const AttnShape &s, const float *o, long ldo, const float *dout, long lddo,
                    float *d, bf16 *dout_bf16, long lddo16, hipStream_t st);
+// D = rowsum(O * dO) from bf16 O and dO (head_dim 64 / 128, 16-byte aligned).
+hipError_t fa_bw_d_bf16(const AttnShape &s, const bf16 *o, long ldo, const bf16 *dout, long lddo,
+                        float *d, hipStream_t st);
 hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 // Fused bf16 backward: dK/dV and bf16 dS into ds_ws (fa_bw_ws_bytes), then

@@ -320,7 +320,9 @@ struct vkh_runner {
             char *qa = nullptr;
             VKH_TRY(alloc(qa, (size_t)T * qkvd * asz));
             a.qkv_attn = qa;
-            VKH_TRY(alloc(a.attn_out, (size_t)T * qd));
+            // the fp32 O feeds only the fp32 path: the bf16 path keeps O in
+            // bf16 (the O projection's operand and the D preprocess's input)
+            if (!(b16() && adt == DType::BF16)) VKH_TRY(alloc(a.attn_out, (size_t)T * qd));
             VKH_TRY(alloc(a.lse, (size_t)T * H));
             VKH_TRY(alloc(a.mid, (size_t)T * D));
             VKH_TRY(alloc(a.gu, (size_t)T * 2 * F));
@@ -642,8 +644,9 @@ struct vkh_runner {
         const size_t es = adt == DType::BF16 ? 2 : 4;
         const char *qa = (const char *)a.qkv_attn;
         const bool ob = b16() && adt == DType::BF16;
-        VKH_HIP(fa_forward(as, qa, qkvd, qa + qd * es, qkvd, qa + (qd + kvd) * es, qkvd, a.attn_out,
-                           qd, a.lse, adt, ob ? a.attn_b : nullptr, qd, cur));
+        VKH_HIP(fa_forward(as, qa, qkvd, qa + qd * es, qkvd, qa + (qd + kvd) * es, qkvd,
+                           ob ? nullptr : a.attn_out, qd, a.lse, adt, ob ? a.attn_b : nullptr, qd,
+                           cur));
         if (b16() && !ob) VKH_HIP(cast_f32_to_bf16(a.attn_out, a.attn_b, (size_t)T * qd, cur));
         // mid = x_in + attn_out W_o^T (+ LoRA)
         const Mat att = m_attn(a);
@@ -727,13 +730,25 @@ struct vkh_runner {
                                  concurrent ? nullptr : Gd(s.t[5]), concurrent ? lg[l].pn2 : partial,
                                  T, D, cfg.rms_eps, 0, cur));
         const Mat mdmid = b16() ? matb(d_midb, D) : matf(d_mid, D);
-        // o: d_attn_out = d_mid W_o; dW_o = d_mid^T attn_out
-        VKH_TRY(linear_dx(mdmid, s.t[4], d_attn_out, qd, D, qd));
+        // o: d_attn_out = d_mid W_o; dW_o = d_mid^T attn_out.  On the bf16
+        // attention path without a LoRA term on o, dO goes straight to bf16 (the
+        // attention kernels' operand) and D = rowsum(O dO) reads both in bf16.
+        const AttnShape as = attn_shape();
+        const bool do_bf16 = b16() && adt == DType::BF16 && !proj_lora(3);
+        if (do_bf16)
+            VKH_HIP(g16_nn_bf16((const bf16 *)mdmid.p, mdmid.ld, Wb(s.t[4]), qd, dout16, qd, T, D,
+                                qd, gws, cur));
+        else
+            VKH_TRY(linear_dx(mdmid, s.t[4], d_attn_out, qd, D, qd));
         VKH_TRY(linear_dw(mdmid, m_attn(a), s.t[4], D, qd));
         if (proj_lora(3)) VKH_TRY(lora_bwd(l, 3, mdmid, m_attn(a), d_attn_out, qd));
         // attention: D, dK/dV, dQ into the fused d_qkv buffer
-        const AttnShape as = attn_shape();
-        VKH_HIP(fa_bw_d(as, a.attn_out, qd, d_attn_out, qd, fa_d, dout16, qd, cur));
+        if (b16() && adt == DType::BF16) {
+            if (!do_bf16) VKH_HIP(cast_f32_to_bf16(d_attn_out, dout16, (size_t)T * qd, cur));
+            VKH_HIP(fa_bw_d_bf16(as, a.attn_b, qd, dout16, qd, fa_d, cur));
+        } else {
+            VKH_HIP(fa_bw_d(as, a.attn_out, qd, d_attn_out, qd, fa_d, dout16, qd, cur));
+        }
         const size_t es = adt == DType::BF16 ? 2 : 4;
         const char *qa = (const char *)a.qkv_attn;
         AttnPtrs ap;

@@ -45,6 +45,11 @@ def fa_bw_d(p, o, dout, d, dout_bf16=None, stream=None):
     check(lib().vkh_fa_bw_d(C.byref(p), _p(o), _p(dout), _p(d), _p(dout_bf16), _s(stream)))
 
 
+def fa_bw_d_bf16(p, o16, dout16, d, stream=None):
+    """D = rowsum(O dO) with O and dO stored in bf16."""
+    check(lib().vkh_fa_bw_d_bf16(C.byref(p), _p(o16), _p(dout16), _p(d), _s(stream)))
+
+
 def fa_bw_dq(p, q, k, v, dout, lse, d, dq, stream=None):
     check(lib().vkh_fa_bw_dq(C.byref(p), _p(q), _p(k), _p(v), _p(dout), _p(lse), _p(d), _p(dq),
                              _s(stream)))
