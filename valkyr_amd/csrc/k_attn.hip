@@ -1003,8 +1003,10 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
             }
         } else {
             // dS = P (dP - D), stored as bf16 dS^T; dK^T += Q^T dS
-            bf16 *dsr = dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv +
-                        (long)(kw0 + c16) * s.n_q + q0 + 4 * g;
+            // wave-uniform base plus a 32-bit lane offset (a 64-bit per-lane
+            // pointer here does not fit the register budget: it was spilled)
+            bf16 *dsr = dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv + (long)kw0 * s.n_q + q0;
+            dsr += c16 * s.n_q + 4 * g;
             const long ds_ks = 16L * s.n_q;
 #pragma unroll
             for (int qs = 0; qs < QS; ++qs) {
