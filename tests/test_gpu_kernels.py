@@ -186,7 +186,7 @@ def test_gemm_bf16_rounding_within_north_star_tolerance():
 # ragged edges, and the generic fallback (K not a multiple of 8).
 GEMM16_SHAPES = [(2048, 16384, 256), (2048, 3072, 512), (1024, 1024, 8192), (2048, 1024, 1024),
                  (1000, 520, 1000), (72, 40, 24), (130, 66, 1001), (2048, 4096, 256),
-                 (2040, 4100, 200)]
+                 (2040, 4100, 200), (2048, 1024, 2048), (2000, 1000, 3000), (2048, 3072, 1024)]
 
 
 @pytest.mark.parametrize("shape", GEMM16_SHAPES)

@@ -189,9 +189,13 @@ VKH_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0), ex
 // One block's BM x BN output tile over the K slabs [kbase, kbase + 64 nk):
 // acc (per wave, accumulator layout) += A(m0.., k) B(n0.., k).  `smem` must
 // hold Cfg::LDS bytes.  Shared by the GEMM kernels and the attention dQ kernel.
+// `wave` is the wave's index among the Cfg::WGM x Cfg::WGN waves that share
+// this tile (-1: threadIdx.x / 64, the whole block).  Every wave of the
+// workgroup must run the same number of slabs: the routine's barriers are
+// workgroup-wide.
 template <class Cfg, Lay LA, Lay LB, int TM, int TN>
 VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
-                             int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem) {
+                             int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem, int wave_in = -1) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::WGM * Cfg::WGN, ST = Cfg::ST;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
     static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
@@ -200,7 +204,8 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
     // DMA instructions one wave issues per slab (the newest slab's count)
     constexpr int PER_SLAB = BM / 8 / NW + BN / 8 / NW;
     static_assert(PER_SLAB <= 15, "vmcnt immediate");
-    const int lane = threadIdx.x % 64, wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const int lane = threadIdx.x % 64;
+    const int wave = __builtin_amdgcn_readfirstlane(wave_in < 0 ? (int)threadIdx.x / 64 : wave_in);
     const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
     const sgpr4 ra = rsrc4(a), rb = rsrc4(b);
     auto issue = [&](int kt) {
@@ -281,6 +286,69 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
     }
     FragPos fp{m0 + wm * WM, n0 + wn * WN, lane};
     epi.template apply<TM, TN>(acc, fp, s);
+}
+
+// Two wave groups per block on one output tile (split-K inside the block):
+// group 0 runs the first half of the K slabs, group 1 the second (padded with
+// zero-filled slabs so both run the same count), each in its own LDS region;
+// group 1 then hands its accumulators over through LDS and group 0 adds them
+// (first half + second half, a fixed order) and runs the epilogue.  For
+// shapes with too few tiles to fill the chip this doubles the waves per CU
+// without the partial round trip and the second launch of split-K.
+template <class Cfg, Lay LA, Lay LB, class Epi>
+__global__ __launch_bounds__(2 * Cfg::NT, 1) void gemm16_ks2_kernel(Op16 a, Op16 b, GemmShape s,
+                                                                   Epi epi) {
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
+    constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    static_assert(BM * BN * 4 <= Cfg::LDS, "hand-over buffer");
+    __shared__ __attribute__((aligned(16))) char smem[2 * Cfg::LDS];
+
+    const int tid = threadIdx.x, grp = tid / NT, gt = tid % NT;
+    const int lane = gt % 64, wave = gt / 64;
+    const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+
+    const int nbm = (s.M + BM - 1) / BM, nbn = (s.N + BN - 1) / BN;
+    const int nb = nbm * nbn;
+    int bid = blockIdx.x;
+    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+    const int bm = bid % nbm, bn = bid / nbm;
+    const int m0 = bm * BM, n0 = bn * BN;
+
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    const int nkh = ((s.K + 63) / 64 + 1) / 2;
+    gemm16_tile_dma<Cfg, LA, LB, TM, TN>(a, b, m0, n0, s.M, s.N, grp * nkh * 64, nkh, s.K, acc,
+                                         smem + grp * Cfg::LDS, wave);
+    f32x4 *hand = reinterpret_cast<f32x4 *>(smem);  // both groups are past their last slab
+    if (grp == 1) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) hand[(i * TN + j) * NT + gt] = acc[i][j];
+    }
+    lds_barrier();
+    if (grp == 1) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] += hand[(i * TN + j) * NT + gt];
+    FragPos fp{m0 + wm * WM, n0 + wn * WN, lane};
+    epi.template apply<TM, TN>(acc, fp, s);
+}
+
+template <class Cfg, Lay LA, Lay LB, class Epi>
+hipError_t launch_gemm16_ks2(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &epi,
+                             hipStream_t st) {
+    if (s.M <= 0 || s.N <= 0) return hipSuccess;
+    const unsigned tiles = ceil_div(s.M, Cfg::BM) * ceil_div(s.N, Cfg::BN);
+    hipLaunchKernelGGL((gemm16_ks2_kernel<Cfg, LA, LB, Epi>), dim3(tiles), dim3(2 * Cfg::NT), 0, st,
+                       a, b, s, epi);
+    return hipGetLastError();
 }
 
 // One block per output tile: sum the split partials in order, then the epilogue.

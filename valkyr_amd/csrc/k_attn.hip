@@ -1218,17 +1218,18 @@ __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, 
 // dQ[q, :] = inv_sqrt_dim * sum_{k visible} dS[q, k] K[k, :]: one 128 x HD
 // output tile per (q tile, head, sequence) on the GEMM tile routine (A = dS
 // from its transposed [k][q] store, B = K rows; both MN-major).
-template <int HD>
-__global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, const bf16 *dsw) {
-    using Cfg = Tile16<128, HD, 2, 2>;
-    constexpr int TM = 128 / 2 / 16, TN = HD / 2 / 16;
+template <int HD, int BMQ = 128, int WGM = 2, int WGN = 2>
+__global__ __launch_bounds__(WGM * WGN * 64, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p,
+                                                                  const bf16 *dsw) {
+    using Cfg = Tile16<BMQ, HD, WGM, WGN>;
+    constexpr int TM = BMQ / WGM / 16, TN = HD / WGN / 16;
     __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
     const int qt = s.causal ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;
     const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int kvh = h / (s.n_heads / s.n_kv_heads);
-    const int q0 = qt * 128;
+    const int q0 = qt * BMQ;
     const int off = s.n_kv - s.n_q;
-    const int kend = s.causal ? min(s.n_kv, q0 + 128 + off) : s.n_kv;
+    const int kend = s.causal ? min(s.n_kv, q0 + BMQ + off) : s.n_kv;
     // A(q, k) = dS^T[k][q]: MN-major
     const Op16 a{dsw + ((long)b * s.n_heads + h) * s.n_q * s.n_kv, s.n_q,
                  (unsigned)((size_t)s.n_q * s.n_kv * 2)};
@@ -1242,7 +1243,7 @@ __global__ __launch_bounds__(NT, 1) void fa_dq_gemm_k(AttnShape s, AttnPtrs p, c
     gemm16_tile_dma<Cfg, Lay::MN, Lay::MN, TM, TN>(a, bk, q0, 0, s.n_q, HD, 0, (kend + 63) / 64, kend,
                                               acc, smem);
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
-    const int row0 = q0 + (wave / 2) * 64, col0 = (wave % 2) * (HD / 2);
+    const int row0 = q0 + (wave / WGN) * (BMQ / WGM), col0 = (wave % WGN) * (HD / WGN);
     const float sc_ = s.inv_sqrt_dim;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
@@ -1508,7 +1509,10 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipSt
     dim3 gq(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
     if (s.head_dim == 128) {
         hipLaunchKernelGGL(fa_bwd_dkv3_k, gkv, dim3(dkv3::NT3), 0, st, s, p, ds_ws);
-        hipLaunchKernelGGL(fa_dq_gemm_k<128>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);
+        constexpr int DQ_BM = 128, DQ_WGM = 2, DQ_WGN = 2;
+        const dim3 gq2(s.n_heads * s.n_batch, (s.n_q + DQ_BM - 1) / DQ_BM);
+        hipLaunchKernelGGL((fa_dq_gemm_k<128, DQ_BM, DQ_WGM, DQ_WGN>), gq2,
+                           dim3(DQ_WGM * DQ_WGN * 64), 0, st, s, p, (const bf16 *)ds_ws);
     } else {
         hipLaunchKernelGGL((fa_bwd_dkv2_k<64, FA_BM>), gkv, dim3(NT), 0, st, s, p, ds_ws);
         hipLaunchKernelGGL(fa_dq_gemm_k<64>, gq, dim3(NT), 0, st, s, p, (const bf16 *)ds_ws);

@@ -27,7 +27,9 @@ using T128w8 = Tile16<128, 128, 2, 4>;  // 8 waves of 64 x 32
 // (Three slab buffers were measured slower for these tiles: the larger LDS
 // footprint drops a block per CU.)
 
-enum class Pick { Big, T128, T128x64, T128w8 };
+constexpr bool kUseKs2 = true;
+
+enum class Pick { Big, T128, T128x64, T128w8, T128x64ks2 };
 struct Plan {
     Pick tile;
     int splits;
@@ -52,7 +54,9 @@ Plan plan(const GemmShape &s, size_t ws_bytes) {
     if (s.K >= 16384 && t128 < 256)
         p = Plan{Pick::T128, (int)std::min<long>(4, std::max<long>(1, 512 / t128))};
     else if (t64 < 384 && s.K >= 2048)
-        p = Plan{Pick::T128x64, 2};
+        // two wave groups in one block for K up to 4096 (measured faster than
+        // split-K + reduce there; slower at K = 6144)
+        p = (kUseKs2 && s.K <= 4096) ? Plan{Pick::T128x64ks2, 1} : Plan{Pick::T128x64, 2};
     while (p.splits > 1 && (nk / p.splits < 8 || ws_for(p, s) > ws_bytes)) --p.splits;
     return p;
 }
@@ -66,6 +70,7 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
     case Pick::Big: return launch_gemm16<TBig, LA, LB>(a, b, s, e, sk, st);
     case Pick::T128: return launch_gemm16<T128, LA, LB>(a, b, s, e, sk, st);
     case Pick::T128w8: return launch_gemm16<T128w8, LA, LB>(a, b, s, e, sk, st);
+    case Pick::T128x64ks2: return launch_gemm16_ks2<T128x64, LA, LB>(a, b, s, e, st);
     default: return launch_gemm16<T128x64, LA, LB>(a, b, s, e, sk, st);
     }
 }
