@@ -54,9 +54,11 @@ Plan plan(const GemmShape &s, size_t ws_bytes) {
     if (s.K >= 16384 && t128 < 256)
         p = Plan{Pick::T128, (int)std::min<long>(4, std::max<long>(1, 512 / t128))};
     else if (t64 < 384 && s.K >= 2048)
-        // two wave groups in one block for K up to 4096 (measured faster than
-        // split-K + reduce there; slower at K = 6144)
-        p = (kUseKs2 && s.K <= 4096) ? Plan{Pick::T128x64ks2, 1} : Plan{Pick::T128x64, 2};
+        // two wave groups in one block: alone, faster than split-K + reduce up
+        // to K = 4096 and slower at 6144, but in the two-stream step faster
+        // for every such shape (22.2 vs 22.5 ms with split-K kept at 6144 and
+        // for the weight gradients, 22.8 ms with split-K everywhere)
+        p = kUseKs2 ? Plan{Pick::T128x64ks2, 1} : Plan{Pick::T128x64, 2};
     while (p.splits > 1 && (nk / p.splits < 8 || ws_for(p, s) > ws_bytes)) --p.splits;
     return p;
 }
