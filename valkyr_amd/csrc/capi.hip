@@ -245,9 +245,10 @@ vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *
         return VKH_OK;
     }
     void *ws = workspace;
-    if (!ws) VKH_HIP(hipMallocAsync(&ws, fa_bw_ws_bytes(s), st));
+    const size_t wsb = fa_bw_ws_bytes(s);  // 0: the recompute kernels need none
+    if (!ws && wsb) VKH_HIP(hipMallocAsync(&ws, wsb, st));
     const hipError_t e = fa_bw_fused(s, a, (bf16 *)ws, st);
-    if (!workspace) (void)hipFreeAsync(ws, st);
+    if (!workspace && wsb) (void)hipFreeAsync(ws, st);
     if (e != hipSuccess) return hip_fail(e, "fa_backward");
     return VKH_OK;
 }

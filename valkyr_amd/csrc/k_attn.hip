@@ -891,7 +891,12 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
     for (int i = 0; i < DSUB; ++i) acc[i][0] = acc[i][1] = f32x4{0, 0, 0, 0};
 
     // (query head, q tile) iterations; the fused path has n_q % 64 == 0 and
-    // n_q == n_kv when causal
+    // n_q == n_kv when causal.  Every key block walks the q tiles from the
+    // last one down, heads inner: the co-resident blocks of one (sequence,
+    // KV head), which sit on one XCD, then read the same Q / dO tile at about
+    // the same time, so a tile comes from HBM once and from that XCD's L2 for
+    // the others (walking up from each block's own diagonal, they read
+    // different tiles and miss L2).
     const int qstart = s.causal ? k0 / BM * BM : 0;
     const int nqt = s.n_q > qstart ? (s.n_q - qstart) / BM : 0;
     const int niter = hpk * nqt;
@@ -909,7 +914,7 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
     // Instruction i of P wave w fills tile rows 16 w + 4 i + g; lane (g, c16)
     // fetches the logical chunk stored at physical chunk c16 of its row.
     auto dma = [&](int it, int buf) {
-        const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+        const int h = kvh * hpk + it % hpk, q0 = qstart + (nqt - 1 - it / hpk) * BM;
         const int r = q0 + 16 * wave + g;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
@@ -941,7 +946,7 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
         }
         lds_barrier();  // tile `it` landed; everyone is done with buffer (it + 2) % 3 and Pex
         if (it + 2 < niter && pw) dma(it + 2, (it + 2) % NBUF);
-        const int h = kvh * hpk + it / nqt, q0 = qstart + (it % nqt) * BM;
+        const int h = kvh * hpk + it % hpk, q0 = qstart + (nqt - 1 - it / hpk) * BM;
         const char *Qb = Qs[buf], *Ob = Os[buf];
         const bool edge = (s.causal && kw0 + 31 > q0) || !keys_ok;
         f32x4 sc[QS][2];
@@ -1054,6 +1059,468 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
         for (int i = 0; i < DSUB; ++i) {
             const f32x4 a = acc[i][ks];
             *reinterpret_cast<float4 *>(out + 16 * i + 4 * g) =
+                make_float4(a[0] * sc_, a[1] * sc_, a[2] * sc_, a[3] * sc_);
+        }
+    }
+}
+
+// ── backward v4 (head_dim 128, an even number of query heads per KV head) ──
+//
+// Two kernels that each form S and dP themselves (seven score-sized products
+// per (query, key) pair instead of five), so nothing of size
+// [heads, n_q, n_kv] goes through HBM and neither kernel issues a global
+// store inside its tile loop: the tile DMA is then the only vector-memory
+// traffic there, and the waits for it can be counted exactly.
+//
+// Both run one wave per SIMD with 64 keys (dK/dV) or 64 queries (dQ) per
+// wave held in registers, so every MFMA operand fragment read from LDS feeds
+// four MFMAs: half the LDS bytes per flop of a 32-row wave tile.  The
+// accumulators (2 x 64 x 128 fp32 for dK/dV, 64 x 128 for dQ) live in AGPRs.
+
+#ifdef DKV4_SB
+#define DKV4_PHASE() __builtin_amdgcn_sched_barrier(0)
+#else
+#define DKV4_PHASE()
+#endif
+namespace dkv4 {
+constexpr int NT = 256, HD = 128, BM = 32, KW = 64, BN = 128;
+constexpr int KS = KW / 16, DS = HD / 32, DSUB = HD / 16, QS = BM / 16;
+constexpr int TILE = BM * HD * 2;           // 8 KB: one Q or dO tile
+constexpr int NBUF = 3;                     // tile buffers (two DMA batches in flight)
+constexpr int STREAM = NBUF * 2 * TILE;     // 48 KB: one head group's Q / dO tiles
+constexpr int XSLOT = DSUB * KS * 64 * 16;  // 32 KB: one wave's dK^T or dV^T
+constexpr int LDS = 4 * XSLOT;              // tile streams + V slices in the loop, the exchange after
+static_assert(2 * STREAM + 2 * KW * HD * 2 <= LDS, "tile streams and V slices exceed the LDS arena");
+}  // namespace dkv4
+
+// dK / dV.  Block = 128 keys of one (sequence, KV head); 4 waves = 2 key
+// slices of 64 x 2 head groups.  Wave (slice, group) holds K and V of its 64
+// keys in VGPRs and, per 32-query tile of a head of its group (heads
+// kvh * hpk + group, + 2, ...), computes
+//   S = Q K^T, dP = dO V^T            (A = Q / dO rows from LDS, b128)
+//   P = exp2(S c - lse), dS = P (dP - D)
+//   dV^T += dO^T P, dK^T += Q^T dS    (A = transposing LDS reads)
+// P and dS are used straight from the accumulators as the B operands of the
+// last two products (contraction rows in frag_acc order).  The two waves of a
+// slice then sum their partial dK / dV through LDS: group 0 keeps dV and adds
+// group 1's, group 1 keeps dK and adds group 0's.
+// Each head group streams its Q / dO tiles through three LDS buffers (two
+// tiles in flight); the slice-0 wave moves Q and lse, the slice-1 wave dO and
+// D.  Tiles are visited from the last query down, heads inner, so the blocks
+// of one (sequence, KV head), which sit on one XCD, read a tile at about the
+// same time and share it in L2.  Under a causal mask the heaviest key blocks
+// (lowest keys) have the lowest block ids and start first.
+__global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPtrs p) {
+    using namespace dkv4;
+    using dkv3::frag_row;
+    using dkv3::frag_t;
+    __shared__ __attribute__((aligned(16))) char smem[LDS];
+    __shared__ __attribute__((aligned(16))) float Ls[2][NBUF][64], Dd[2][NBUF][64];
+
+    const int kt = (int)blockIdx.y;
+    const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
+    const int hpk = s.n_heads / s.n_kv_heads, nh = hpk / 2;
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int sl = wave & 1, hg = wave >> 1;  // key slice, head group
+    const int k0 = kt * BN, kw0 = k0 + sl * KW;
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+
+    // K and V of the slice as B operands: lane (g, c16) holds key 16 ks + c16,
+    // d = 32 ds + 8 g .. + 7 (n_kv is a multiple of 128: no edge)
+    bf16x8 kr[KS][DS];
+    {
+        const bf16 *kb = (const bf16 *)p.k + ((long)b * s.n_kv + kw0 + c16) * p.ldk + kvh * HD + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) kr[ks][ds] = ld_frag(kb + 16L * ks * p.ldk + 32 * ds);
+    }
+    // V of the slice (64 rows, swizzled like the tiles) by DMA from the group-0 wave
+    char *vsl = smem + 2 * STREAM + sl * KW * HD * 2;
+    if (hg == 0) {
+        const sgpr4 rv = rsrc4((const bf16 *)p.v + (long)b * s.n_kv * p.ldv,
+                               (unsigned)((long)s.n_kv * p.ldv * 2));
+#pragma unroll
+        for (int i = 0; i < KW / 4; ++i) {
+            const int r = 4 * i + g;
+            const int col = kvh * HD + 8 * (c16 ^ dkv3::swz(r));
+            dma16_async(rv, vsl + 4 * i * HD * 2, (unsigned)(((kw0 + r) * (int)p.ldv + col) * 2));
+        }
+    }
+    wait_vm0();  // K in registers and V in LDS before any tile DMA is queued
+    __syncthreads();
+    f32x4 dvt[DSUB][KS], dkt[DSUB][KS];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) dvt[i][ks] = dkt[i][ks] = f32x4{0, 0, 0, 0};
+
+    // causal: n_q == n_kv, so queries below k0 see none of the block's keys
+    const int qstart = s.causal ? k0 : 0;
+    const int nqt = (s.n_q - qstart) / BM;
+    const int niter = nh * nqt;
+    char *strm = smem + hg * STREAM;
+
+    // this wave's DMA share: slice 0 moves Q and lse, slice 1 dO and D
+    const sgpr4 rt = sl ? rsrc4((const bf16 *)p.dout + (long)b * s.n_q * p.lddo,
+                                (unsigned)((long)s.n_q * p.lddo * 2))
+                        : rsrc4((const bf16 *)p.q + (long)b * s.n_q * p.ldq,
+                                (unsigned)((long)s.n_q * p.ldq * 2));
+    const int ldt = (int)(sl ? p.lddo : p.ldq);
+    const sgpr4 rs = rsrc4((sl ? p.d : p.lse) + (long)b * s.n_q * s.n_heads,
+                           (unsigned)((long)s.n_q * s.n_heads * 4));
+    float(*stat)[NBUF][64] = sl ? Dd : Ls;
+    auto tile_of = [&](int it, int &h, int &q0) {
+        h = kvh * hpk + hg + 2 * (it % nh);
+        q0 = qstart + (nqt - 1 - it / nh) * BM;
+    };
+    // 9 vector-memory operations per wave and tile: instruction i fills tile
+    // rows 4 i .. 4 i + 3, lane (g, c16) row 4 i + g at physical chunk c16
+    // (the lane id is laundered so the per-lane offsets are recomputed here,
+    // a few VALU operations, instead of being held in registers across the
+    // loop: spilled, their reloads would wait for the tile DMA in flight)
+    auto dma = [&](int it, int buf) {
+        int h, q0;
+        tile_of(it, h, q0);
+        int ln = lane;
+        asm volatile("" : "+v"(ln));
+        const int lg = ln >> 4, l16 = ln & 15;
+        char *dst = strm + buf * 2 * TILE + sl * TILE;
+#pragma unroll
+        for (int i = 0; i < BM / 4; ++i) {
+            const int r = 4 * i + lg;
+            const int col = h * HD + 8 * (l16 ^ dkv3::swz(r));
+            dma16_async(rt, dst + 4 * i * HD * 2, (unsigned)(((q0 + r) * ldt + col) * 2));
+        }
+        dma4_async(rs, stat[hg][buf], (unsigned)(((q0 + ln) * s.n_heads + h) * 4));
+    };
+
+    if (niter > 0) dma(0, 0);
+    if (niter > 1) dma(1, 1);
+    // The tile loop is unrolled over the three buffers, so every LDS address
+    // is a per-lane base plus a compile-time offset (no per-tile VALU adds).
+    auto step = [&](const int it, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        if (it + 1 < niter) __builtin_amdgcn_s_waitcnt(0x0f70 | 9);  // tile it+1 may stay in flight
+        else wait_vm0();
+        lds_barrier();  // tile `it` landed; everyone is done with buffer (it + 2) % 3
+        if (it + 2 < niter) dma(it + 2, (buf + 2) % NBUF);
+        int h, q0;
+        tile_of(it, h, q0);
+        (void)h;
+        const char *Qb = strm + buf * 2 * TILE, *Ob = Qb + TILE;
+        // P = 0 where key kw0 + 16 ks + c16 lies above query q0 + 16 qs + 4 g + r,
+        // i.e. 16 ks - r > lim[qs] (branch-free compare against a per-lane limit)
+        const bool diag = s.causal && kw0 + KW - 1 > q0;
+        int lim[QS];
+        float lq[QS][4], dq[QS][4];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs) {
+            lim[qs] = s.causal ? q0 + 16 * qs + 4 * g - kw0 - c16 : (1 << 30);
+            const float4 l4 = *reinterpret_cast<const float4 *>(&Ls[hg][buf][16 * qs + 4 * g]);
+            const float4 d4 = *reinterpret_cast<const float4 *>(&Dd[hg][buf][16 * qs + 4 * g]);
+            const float ls[4] = {l4.x, l4.y, l4.z, l4.w}, dv_[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                // a fully masked row (lse = -inf) gets P = 0
+                lq[qs][r] = ls[r] == -INFINITY ? INFINITY : ls[r] * LOG2E;
+                dq[qs][r] = dv_[r];
+            }
+        }
+        f32x4 sc[QS][KS], dp[QS][KS];
+#pragma unroll
+        for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) sc[qs][ks] = dp[qs][ks] = f32x4{0, 0, 0, 0};
+        // Each phase walks its 8 A fragments with the next fragment's LDS read
+        // issued before this one's MFMAs; the softmax and dS arithmetic of one
+        // (qs, ks) tile rides along with each step of the following phase.
+        bf16x8 fr[2];
+        fr[0] = frag_row(Qb, c16, 8 * g);
+        // S = Q K^T; f = (ds, qs) = (f / 2, f % 2)
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+            const int ds = f / 2, qs = f % 2, n = f + 1;
+            fr[n & 1] = n < 8 ? frag_row(Qb, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
+                              : frag_row(Ob, c16, 8 * g);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) sc[qs][ks] = mfma16x16x32(fr[f & 1], kr[ks][ds], sc[qs][ks]);
+        }
+        // dP = dO V^T (V from LDS), with P = exp2(S c - lse) of tile (f / 4, f % 4)
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+            const int ds = f / 2, qs = f % 2, n = f + 1;
+            fr[n & 1] = n < 8 ? frag_row(Ob, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
+                              : frag_t(Ob, 0, 0, g, c16);
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+                dp[qs][ks] = mfma16x16x32(fr[f & 1], frag_row(vsl, 16 * ks + c16, 32 * ds + 8 * g), dp[qs][ks]);
+            const int qs2 = f / 4, ks2 = f % 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) sc[qs2][ks2][r] = __builtin_amdgcn_exp2f(sc[qs2][ks2][r] * c2 - lq[qs2][r]);
+        }
+        if (diag) {  // keys above a query of the tile (uniform; no MFMA inside)
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (16 * ks - r > lim[qs]) sc[qs][ks][r] = 0.f;
+        }
+        // dV^T += dO^T P, with dS = P (dP - D) of tile (i / 4, i % 4)
+        {
+            bf16x8 pb[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) pb[ks] = frag_acc(sc[0][ks], sc[1][ks]);
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) {
+                const int n = i + 1;
+                fr[n & 1] = n < DSUB ? frag_t(Ob, 16 * n, 0, g, c16) : frag_t(Qb, 0, 0, g, c16);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) dvt[i][ks] = mfma16x16x32(fr[i & 1], pb[ks], dvt[i][ks]);
+                const int qs2 = i / 4, ks2 = i % 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    dp[qs2][ks2][r] = sc[qs2][ks2][r] * (dp[qs2][ks2][r] - dq[qs2][r]);
+            }
+        }
+        // dK^T += Q^T dS
+        {
+            bf16x8 sb[KS];
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) sb[ks] = frag_acc(dp[0][ks], dp[1][ks]);
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) {
+                if (i + 1 < DSUB) fr[(i + 1) & 1] = frag_t(Qb, 16 * (i + 1), 0, g, c16);
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) dkt[i][ks] = mfma16x16x32(fr[i & 1], sb[ks], dkt[i][ks]);
+            }
+        }
+        // keep the loop-carried accumulators in AGPRs (the MFMA accumulate file)
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(dvt[i][ks]), "+a"(dkt[i][ks]));
+    };
+    for (int it0 = 0; it0 < niter; it0 += NBUF) {
+        step(it0, std::integral_constant<int, 0>{});
+        if (it0 + 1 < niter) step(it0 + 1, std::integral_constant<int, 1>{});
+        if (it0 + 2 < niter) step(it0 + 2, std::integral_constant<int, 2>{});
+    }
+    // head-group exchange through the (now idle) tile arena
+    wait_vm0();
+    __syncthreads();
+    f32x4 *xs = reinterpret_cast<f32x4 *>(smem + (sl * 2 + hg) * XSLOT);
+    const f32x4 *xp = reinterpret_cast<const f32x4 *>(smem + (sl * 2 + (1 - hg)) * XSLOT);
+    // group 0 hands over dK^T and keeps dV^T; group 1 the other way round
+    auto give = [&](const f32x4 (&a)[DSUB][KS]) {
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) xs[(i * KS + ks) * 64 + lane] = a[i][ks];
+    };
+    auto keep = [&](const f32x4 (&a)[DSUB][KS], float *base, long ld, float sc_) {
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) {
+            float *out = base + ((long)b * s.n_kv + kw0 + 16 * ks + c16) * ld + kvh * HD;
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i) {
+                const f32x4 v = a[i][ks] + xp[(i * KS + ks) * 64 + lane];
+                *reinterpret_cast<float4 *>(out + 16 * i + 4 * g) =
+                    make_float4(v[0] * sc_, v[1] * sc_, v[2] * sc_, v[3] * sc_);
+            }
+        }
+    };
+    if (hg == 0) give(dkt);
+    else give(dvt);
+    __syncthreads();
+    if (hg == 0) keep(dvt, p.dv, p.lddv, 1.0f);
+    else keep(dkt, p.dk, p.lddk, s.inv_sqrt_dim);
+}
+
+namespace dq4 {
+constexpr int NT = 256, HD = 128, QW = 64, BQ = 4 * QW, BN = 32;
+constexpr int QSUB = QW / 16, KS = BN / 16, DS = HD / 32, DSUB = HD / 16;
+constexpr int TILE = BN * HD * 2;  // 8 KB: one K or V tile
+constexpr int NBUF = 3;
+}  // namespace dq4
+
+// dQ.  Block = 256 queries of one (sequence, head); wave w owns the 16-row
+// query sub-tiles Q0 + 64 j + 16 w (j = 0..3), interleaved so that under a
+// causal mask every wave has work until the block's last key tile.  Q and dO
+// of those rows sit in VGPRs as B operands; per 32-key tile (K and V by DMA,
+// three buffers)
+//   S^T = K Q^T, dP^T = V dO^T         (A = K / V rows from LDS, b128)
+//   P^T = exp2(S^T c - lse), dS^T = P^T (dP^T - D)   (lse, D: one query per lane)
+//   dQ^T += K^T dS^T                   (A = transposing reads of the K tile)
+// Key tiles ascend from 0, so all query blocks of a (sequence, head) read
+// the same K / V tile at about the same time; the heaviest query blocks
+// (highest queries) start first.
+__global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs p) {
+    using namespace dq4;
+    using dkv3::frag_row;
+    using dkv3::frag_t;
+    __shared__ __attribute__((aligned(16))) char Kt[NBUF][TILE];
+    __shared__ __attribute__((aligned(16))) char Vt[NBUF][TILE];
+
+    const int qblk = s.causal ? (int)gridDim.y - 1 - (int)blockIdx.y : (int)blockIdx.y;
+    const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
+    const int kvh = h / (s.n_heads / s.n_kv_heads);
+    const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
+    const int q00 = qblk * BQ + 16 * wave;  // first row of sub-tile j is q00 + 64 j
+    const float c2 = s.inv_sqrt_dim * LOG2E;
+
+    bf16x8 qr[QSUB][DS], orr[QSUB][DS];
+    float lq[QSUB], dd[QSUB];
+#pragma unroll
+    for (int j = 0; j < QSUB; ++j) {
+        const int q = q00 + 64 * j + c16;
+        const bool ok = q < s.n_q;
+        const long t = (long)b * s.n_q + q;
+        const bf16 *qp = (const bf16 *)p.q + t * p.ldq + h * HD + 8 * g;
+        const bf16 *op = (const bf16 *)p.dout + t * p.lddo + h * HD + 8 * g;
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) {
+            qr[j][ds] = ok ? ld_frag(qp + 32 * ds) : bf16x8{};
+            orr[j][ds] = ok ? ld_frag(op + 32 * ds) : bf16x8{};
+        }
+        const float l = ok ? p.lse[t * s.n_heads + h] : -INFINITY;
+        // rows past n_q and fully masked rows (lse = -inf) get P = 0
+        lq[j] = l == -INFINITY ? INFINITY : l * LOG2E;
+        dd[j] = ok ? p.d[t * s.n_heads + h] : 0.f;
+    }
+    wait_vm0();
+#ifdef DQ4_QA
+#pragma unroll
+    for (int j = 0; j < QSUB; ++j)
+#pragma unroll
+        for (int ds = 0; ds < DS; ++ds) asm volatile("" : "+a"(qr[j][ds]), "+a"(orr[j][ds]));
+#endif
+    f32x4 acc[DSUB][QSUB];
+#pragma unroll
+    for (int i = 0; i < DSUB; ++i)
+#pragma unroll
+        for (int j = 0; j < QSUB; ++j) acc[i][j] = f32x4{0, 0, 0, 0};
+
+    const int kend = s.causal ? min(s.n_kv, qblk * BQ + BQ) : s.n_kv;
+    const int ntl = (kend + BN - 1) / BN;
+    const sgpr4 rk = rsrc4((const bf16 *)p.k + (long)b * s.n_kv * p.ldk,
+                           (unsigned)((long)s.n_kv * p.ldk * 2));
+    const sgpr4 rv = rsrc4((const bf16 *)p.v + (long)b * s.n_kv * p.ldv,
+                           (unsigned)((long)s.n_kv * p.ldv * 2));
+    // wave w moves rows 8 w .. 8 w + 7 of the K and V tiles (4 operations)
+    auto dma = [&](int t, int buf) {
+        const int kk = t * BN;
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+            const int r = 8 * wave + 4 * i + g;
+            const int col = kvh * HD + 8 * (c16 ^ dkv3::swz(r));
+            const int lo = (8 * wave + 4 * i) * HD * 2;
+            dma16_async(rk, Kt[buf] + lo, (unsigned)(((kk + r) * (int)p.ldk + col) * 2));
+            dma16_async(rv, Vt[buf] + lo, (unsigned)(((kk + r) * (int)p.ldv + col) * 2));
+        }
+    };
+    if (ntl > 0) dma(0, 0);
+    if (ntl > 1) dma(1, 1);
+    // The tile loop is unrolled over the three buffers, so every LDS address
+    // is a per-lane base plus a compile-time offset (no per-tile VALU adds).
+    auto step = [&](const int t, auto bufc) {
+        constexpr int buf = decltype(bufc)::value;
+        if (t + 1 < ntl) __builtin_amdgcn_s_waitcnt(0x0f70 | 4);
+        else wait_vm0();
+        lds_barrier();
+        if (t + 2 < ntl) dma(t + 2, (buf + 2) % NBUF);
+        const int kk = t * BN;
+        const char *Kb = Kt[buf], *Vb = Vt[buf];
+        // P = 0 where key kk + 16 ks + 4 g + r lies above query q00 + 64 j + c16,
+        // i.e. 16 ks + r > lim[j] (branch-free compare against a per-lane limit)
+        int lim[QSUB];
+#pragma unroll
+        for (int j = 0; j < QSUB; ++j)
+            lim[j] = min(s.causal ? q00 + 64 * j + c16 - kk - 4 * g : (1 << 30), s.n_kv - 1 - kk - 4 * g);
+        const bool diag = (s.causal && kk + BN - 1 > q00) || kk + BN > s.n_kv;
+        f32x4 st[KS][QSUB], dpt[KS][QSUB];
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int j = 0; j < QSUB; ++j) st[ks][j] = dpt[ks][j] = f32x4{0, 0, 0, 0};
+        // Each phase walks its 8 operand fragments f = (ds, ks) = (f / 2, f % 2)
+        // with the next fragment's LDS read issued before this one's MFMAs.
+        bf16x8 fr[2];
+        fr[0] = frag_row(Kb, c16, 8 * g);
+        // S^T = K Q^T
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+            const int ds = f / 2, ks = f % 2, n = f + 1;
+            fr[n & 1] = n < 8 ? frag_row(Kb, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
+                              : frag_row(Vb, c16, 8 * g);
+#pragma unroll
+            for (int j = 0; j < QSUB; ++j) st[ks][j] = mfma16x16x32(fr[f & 1], qr[j][ds], st[ks][j]);
+        }
+        // dP^T = V dO^T, with P^T = exp2(S^T c - lse) of one (ks, j) tile per step
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+            const int ds = f / 2, ks = f % 2, n = f + 1;
+            fr[n & 1] = n < 8 ? frag_row(Vb, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
+                              : frag_t(Kb, 0, 0, g, c16);
+#pragma unroll
+            for (int j = 0; j < QSUB; ++j) dpt[ks][j] = mfma16x16x32(fr[f & 1], orr[j][ds], dpt[ks][j]);
+            const int ks2 = f / 4, j2 = f % 4;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) st[ks2][j2][r] = __builtin_amdgcn_exp2f(st[ks2][j2][r] * c2 - lq[j2]);
+        }
+        if (diag) {  // keys above a query of this wave (uniform; no MFMA inside)
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int j = 0; j < QSUB; ++j)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (16 * ks + r > lim[j]) st[ks][j][r] = 0.f;
+        }
+#ifdef DQ4_QA
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+            for (int j = 0; j < QSUB; ++j) asm volatile("" : "+v"(dpt[ks][j]));
+#endif
+        // dS^T = P^T (dP^T - D) -> bf16 B operands (contraction = keys)
+        bf16x8 sb[QSUB];
+#pragma unroll
+        for (int j = 0; j < QSUB; ++j) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) dpt[ks][j][r] = st[ks][j][r] * (dpt[ks][j][r] - dd[j]);
+            sb[j] = frag_acc(dpt[0][j], dpt[1][j]);
+        }
+        // dQ^T += K^T dS^T
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            if (i + 1 < DSUB) fr[(i + 1) & 1] = frag_t(Kb, 16 * (i + 1), 0, g, c16);
+#pragma unroll
+            for (int j = 0; j < QSUB; ++j) acc[i][j] = mfma16x16x32(fr[i & 1], sb[j], acc[i][j]);
+        }
+    };
+    for (int t0 = 0; t0 < ntl; t0 += NBUF) {
+        step(t0, std::integral_constant<int, 0>{});
+        if (t0 + 1 < ntl) step(t0 + 1, std::integral_constant<int, 1>{});
+        if (t0 + 2 < ntl) step(t0 + 2, std::integral_constant<int, 2>{});
+    }
+    // acc[i][j][r] = dQ^T[16 i + 4 g + r][q00 + 64 j + c16]
+#pragma unroll
+    for (int j = 0; j < QSUB; ++j) {
+        const int q = q00 + 64 * j + c16;
+        if (q >= s.n_q) continue;
+        float *dqr = p.dq + ((long)b * s.n_q + q) * p.lddq + h * HD;
+        const float sc_ = s.inv_sqrt_dim;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) {
+            const f32x4 a = acc[i][j];
+            *reinterpret_cast<float4 *>(dqr + 16 * i + 4 * g) =
                 make_float4(a[0] * sc_, a[1] * sc_, a[2] * sc_, a[3] * sc_);
         }
     }
@@ -1498,13 +1965,34 @@ bool fa_bw_fused_ok(const AttnShape &s) {
            s.n_heads % s.n_kv_heads == 0;
 }
 
+// The recompute kernels (fa_bwd_dkv4_k + fa_bwd_dq4_k): head_dim 128, an even
+// number of query heads per KV head, 128-key blocks; no dS workspace.
+static bool fa_bw_v4_ok(const AttnShape &s) {
+    return fa_bw_fused_ok(s) && s.head_dim == 128 && (s.n_heads / s.n_kv_heads) % 2 == 0 &&
+           s.n_kv % 128 == 0;
+}
+
 size_t fa_bw_ws_bytes(const AttnShape &s) {
+    if (fa_bw_v4_ok(s)) return 0;
     return (size_t)s.n_batch * s.n_heads * s.n_q * s.n_kv * sizeof(bf16);
 }
 
 hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipStream_t st) {
     if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
-    if (p.dt != DType::BF16 || !fa_bw_fused_ok(s) || !ds_ws) return hipErrorInvalidValue;
+    if (p.dt != DType::BF16 || !fa_bw_fused_ok(s)) return hipErrorInvalidValue;
+    if (fa_bw_v4_ok(s)) {
+        // the DMA offsets are 32-bit: rows of the q / k / v / dO views must fit
+        if ((long)s.n_q * std::max(p.ldq, p.lddo) * 2 >= (1l << 31) ||
+            (long)s.n_kv * std::max(p.ldk, p.ldv) * 2 >= (1l << 31))
+            return hipErrorInvalidValue;
+        hipLaunchKernelGGL(fa_bwd_dkv4_k, dim3(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN),
+                           dim3(dkv4::NT), 0, st, s, p);
+        hipLaunchKernelGGL(fa_bwd_dq4_k,
+                           dim3(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ),
+                           dim3(dq4::NT), 0, st, s, p);
+        return hipGetLastError();
+    }
+    if (!ds_ws) return hipErrorInvalidValue;
     dim3 gkv(s.n_kv_heads * s.n_batch, (s.n_kv + 127) / 128);
     dim3 gq(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
     if (s.head_dim == 128) {

@@ -89,7 +89,8 @@ struct vkh_runner {
     bool shadow_dirty = true;
     bf16 *fn_outb = nullptr, *d_gub = nullptr, *d_midb = nullptr, *d_qkvb = nullptr,
          *dxb[2] = {nullptr, nullptr};
-    bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward
+    bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward (when it needs one)
+    bool attn_fused = false;  // bf16 attention backward on fa_bw_fused
     GemmWs gws{nullptr, 0};
     // Concurrent weight gradients (bf16 full fine-tune): each layer's dW GEMMs
     // and its Adam update run on a second stream one layer behind the main
@@ -340,7 +341,8 @@ struct vkh_runner {
             VKH_TRY(alloc(d_qkvb, (size_t)T * qkvd));
             VKH_TRY(alloc(dxb[0], (size_t)T * D));
             VKH_TRY(alloc(dxb[1], (size_t)T * D));
-            if (adt == DType::BF16 && fa_bw_fused_ok(attn_shape()))
+            attn_fused = adt == DType::BF16 && fa_bw_fused_ok(attn_shape());
+            if (attn_fused && fa_bw_ws_bytes(attn_shape()))
                 VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape()) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
             size_t wsb = 0;
@@ -762,7 +764,7 @@ struct vkh_runner {
         ap.dk = d_qkv + qd; ap.lddk = qkvd;
         ap.dv = d_qkv + qd + kvd; ap.lddv = qkvd;
         ap.dt = adt;
-        if (attn_ds) {
+        if (attn_fused) {
             VKH_HIP(fa_bw_fused(as, ap, attn_ds, cur));
         } else {
             VKH_HIP(fa_bw_dkv(as, ap, cur));
