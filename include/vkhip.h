@@ -454,11 +454,15 @@ vkh_status vkh_fa_bw_dkv(const vkh_attn_params *p, const void *q, const void *k,
 /* The FA-2 backward of one attention call after vkh_fa_bw_d (the
  * fa_bw_dkv.comp + fa_bw_dq.comp pair of the reference's attention
  * backward): dK, dV, dQ fp32 (overwrite).  With bf16 operands (head_dim 64 or
- * 128, n_q and n_kv multiples of 64, self-attention when causal) dK/dV write
- * dS = P (dP - D) once as bf16 into `workspace` and dQ = dS K is a GEMM, so
- * S and dP are formed once instead of twice; other shapes run the two
- * kernels above.  `workspace` may be NULL (allocated per call on the stream)
- * or hold vkh_fa_backward_workspace_bytes(p) bytes. */
+ * 128, n_q and n_kv multiples of 64, self-attention when causal):
+ *   - head_dim 128, an even number of query heads per KV head and n_kv a
+ *     multiple of 128: a dK/dV kernel and a dQ kernel that each form S and
+ *     dP themselves (no workspace: vkh_fa_backward_workspace_bytes is 0);
+ *   - otherwise dK/dV write dS = P (dP - D) once as bf16 into `workspace` and
+ *     dQ = dS K is a GEMM.
+ * Other shapes run the two kernels above.  `workspace` may be NULL (allocated
+ * per call on the stream when needed) or hold
+ * vkh_fa_backward_workspace_bytes(p) bytes. */
 size_t vkh_fa_backward_workspace_bytes(const vkh_attn_params *p);
 vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *k, const void *v,
                            const void *dout, const float *lse, const float *d, float *dq,

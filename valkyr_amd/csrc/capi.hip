@@ -225,7 +225,7 @@ vkh_status vkh_fa_bw_dkv(const vkh_attn_params *p, const void *q, const void *k,
 size_t vkh_fa_backward_workspace_bytes(const vkh_attn_params *p) {
     if (!p || check_attn(p) != VKH_OK) return 0;
     const AttnShape s = attn_shape(p);
-    return p->dtype == VKH_BF16 && fa_bw_fused_ok(s) ? fa_bw_ws_bytes(s) : 0;
+    return p->dtype == VKH_BF16 && fa_bw_fused_ok(s) ? fa_bw_ws_bytes(s, fa_bw_v4_ok(s)) : 0;
 }
 
 vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *k, const void *v,
@@ -245,9 +245,11 @@ vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *
         return VKH_OK;
     }
     void *ws = workspace;
-    const size_t wsb = fa_bw_ws_bytes(s);  // 0: the recompute kernels need none
+    // the recompute kernels whenever the shape allows (they need no workspace)
+    const bool v4 = fa_bw_v4_ok(s);
+    const size_t wsb = fa_bw_ws_bytes(s, v4);
     if (!ws && wsb) VKH_HIP(hipMallocAsync(&ws, wsb, st));
-    const hipError_t e = fa_bw_fused(s, a, (bf16 *)ws, st);
+    const hipError_t e = fa_bw_fused(s, a, (bf16 *)ws, v4, st);
     if (!workspace && wsb) (void)hipFreeAsync(ws, st);
     if (e != hipSuccess) return hip_fail(e, "fa_backward");
     return VKH_OK;

@@ -1967,20 +1967,30 @@ bool fa_bw_fused_ok(const AttnShape &s) {
 
 // The recompute kernels (fa_bwd_dkv4_k + fa_bwd_dq4_k): head_dim 128, an even
 // number of query heads per KV head, 128-key blocks; no dS workspace.
-static bool fa_bw_v4_ok(const AttnShape &s) {
+bool fa_bw_v4_ok(const AttnShape &s) {
     return fa_bw_fused_ok(s) && s.head_dim == 128 && (s.n_heads / s.n_kv_heads) % 2 == 0 &&
            s.n_kv % 128 == 0;
 }
 
-size_t fa_bw_ws_bytes(const AttnShape &s) {
-    if (fa_bw_v4_ok(s)) return 0;
+// They run one block per CU, so they pay off when the dK/dV grid covers the
+// chip (>= 256 blocks: B = 4 x 2048 keys x 8 KV heads, or 8192 keys); the
+// training step's B = 4 x 512 keys (128 blocks) is faster on the
+// two-waves-per-SIMD kernel plus the dS GEMM, whose idle CUs the step's
+// weight-gradient stream fills.
+bool fa_bw_v4_preferred(const AttnShape &s) {
+    return fa_bw_v4_ok(s) && (long)s.n_batch * s.n_kv_heads * (s.n_kv / 128) >= 256;
+}
+
+size_t fa_bw_ws_bytes(const AttnShape &s, bool v4) {
+    if (v4) return 0;
     return (size_t)s.n_batch * s.n_heads * s.n_q * s.n_kv * sizeof(bf16);
 }
 
-hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipStream_t st) {
+hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool v4, hipStream_t st) {
     if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
-    if (p.dt != DType::BF16 || !fa_bw_fused_ok(s)) return hipErrorInvalidValue;
-    if (fa_bw_v4_ok(s)) {
+    if (p.dt != DType::BF16 || !fa_bw_fused_ok(s) || (v4 && !fa_bw_v4_ok(s)))
+        return hipErrorInvalidValue;
+    if (v4) {
         // the DMA offsets are 32-bit: rows of the q / k / v / dO views must fit
         if ((long)s.n_q * std::max(p.ldq, p.lddo) * 2 >= (1l << 31) ||
             (long)s.n_kv * std::max(p.ldk, p.ldv) * 2 >= (1l << 31))

@@ -162,12 +162,17 @@ hipError_t fa_bw_d_bf16(const AttnShape &s, const bf16 *o, long ldo, const bf16 
                         float *d, hipStream_t st);
 hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
-// Fused bf16 backward: dK/dV and bf16 dS into ds_ws (fa_bw_ws_bytes), then
-// dQ = dS K.  Requires fa_bw_fused_ok(s) (bf16 head_dim 64/128, n_q and n_kv
-// multiples of 64, self-attention when causal).
+// Fused bf16 backward.  Requires fa_bw_fused_ok(s) (bf16 head_dim 64/128, n_q
+// and n_kv multiples of 64, self-attention when causal).  v4 (requires
+// fa_bw_v4_ok: head_dim 128, even GQA group, n_kv % 128 == 0): dK/dV and dQ
+// kernels that each recompute S and dP, no workspace.  Otherwise dK/dV writes
+// bf16 dS into ds_ws (fa_bw_ws_bytes) and dQ = dS K is a GEMM.
+// fa_bw_v4_preferred: the shapes on which v4 is the faster of the two.
 bool fa_bw_fused_ok(const AttnShape &s);
-size_t fa_bw_ws_bytes(const AttnShape &s);
-hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, hipStream_t st);
+bool fa_bw_v4_ok(const AttnShape &s);
+bool fa_bw_v4_preferred(const AttnShape &s);
+size_t fa_bw_ws_bytes(const AttnShape &s, bool v4);
+hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool v4, hipStream_t st);
 
 // ── cut cross-entropy (k_cce.hip) ────────────────────────────────────
 struct CceShape {

@@ -91,6 +91,7 @@ struct vkh_runner {
          *dxb[2] = {nullptr, nullptr};
     bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward (when it needs one)
     bool attn_fused = false;  // bf16 attention backward on fa_bw_fused
+    bool attn_v4 = false;     // ... on its recompute kernels (no dS workspace)
     GemmWs gws{nullptr, 0};
     // Concurrent weight gradients (bf16 full fine-tune): each layer's dW GEMMs
     // and its Adam update run on a second stream one layer behind the main
@@ -342,8 +343,9 @@ struct vkh_runner {
             VKH_TRY(alloc(dxb[0], (size_t)T * D));
             VKH_TRY(alloc(dxb[1], (size_t)T * D));
             attn_fused = adt == DType::BF16 && fa_bw_fused_ok(attn_shape());
-            if (attn_fused && fa_bw_ws_bytes(attn_shape()))
-                VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape()) / sizeof(bf16)));
+            attn_v4 = attn_fused && fa_bw_v4_preferred(attn_shape());
+            if (attn_fused && fa_bw_ws_bytes(attn_shape(), attn_v4))
+                VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape(), attn_v4) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
             size_t wsb = 0;
             auto need = [&](int m, int n, int k) { wsb = std::max(wsb, g16_ws_bytes_for(m, n, k)); };
@@ -765,7 +767,7 @@ struct vkh_runner {
         ap.dv = d_qkv + qd + kvd; ap.lddv = qkvd;
         ap.dt = adt;
         if (attn_fused) {
-            VKH_HIP(fa_bw_fused(as, ap, attn_ds, cur));
+            VKH_HIP(fa_bw_fused(as, ap, attn_ds, attn_v4, cur));
         } else {
             VKH_HIP(fa_bw_dkv(as, ap, cur));
             VKH_HIP(fa_bw_dq(as, ap, cur));
