@@ -464,7 +464,7 @@ def main():
                    "ms": round(fa["ms"], 4), "tflops": round(fa["tflops"], 1),
                    "frac_bf16_peak": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4)},
         "roofline": {"kernel": "attention backward, config 2: fa_bw_d8_k<bf16> + "
-                               "fa_bwd_dkv3_k + fa_dq_gemm_k (one call)", "bound": "mfma",
+                               "fa_bwd_dkv4_k + fa_bwd_dq4_k (one call)", "bound": "mfma",
                      "achieved": round(fa["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa_bwd_config2_traffic.md"),
