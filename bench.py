@@ -17,8 +17,11 @@ tokens/s of the same step (see `sample`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
                        [--no-cpu-baseline] [--fa-reps R]
-                       [--only all|step|fa|mlp|config4|config5] [--calib-copy]
+                       [--only all|step|fa|mlp|bw|config4|config5] [--calib-copy]
 
+`bandwidth_kernels` times the HBM-bound backward kernels alone through the C ABI at
+config-3 shapes (RMSNorm, SwiGLU, RoPE backward, Adam, embedding backward) against
+the 8 TB/s HBM peak.
 `mlp_runner` times the tiny-MLP TrainingRunner (train/runner.zig): the
 reference's `--train-demo` loop and tickFrameTrain on batches.  `--only config4`
 / `--only config5` run the metric's Qwen3-4B LoRA and Qwen3-8B long-context
@@ -161,6 +164,108 @@ def bench_fa_bwd(args):
     tflops = flops / (ms * 1e-3) / 1e12
     print(f"[bench] fa-bwd {ms:.3f} ms, {tflops:.1f} TFLOP/s", file=sys.stderr, flush=True)
     return dict(ms=ms, flops=flops, tflops=tflops)
+
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
+
+
+def bench_bandwidth(args):
+    """The bandwidth-bound backward kernels alone, through the C ABI, at config-3 shapes.
+
+    Each kernel cycles through enough independent buffer sets that the data
+    cannot stay in the 256 MB Infinity Cache (>= 768 MB per kernel), so the
+    rate is an HBM rate; HIP events on the launch stream around R calls.
+    `bytes` is each call's algorithmic traffic (compulsory reads + writes,
+    fp32), `frac` the fraction of the 8 TB/s HBM peak."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import DeviceBuffer, Event, Stream
+
+    T, D, F, H, Hkv, hd = 2048, 1024, 3072, 16, 8, 128
+    rng = np.random.default_rng(11)
+    s = Stream()
+
+    def sets_for(nbytes):
+        return max(2, int(np.ceil(768e6 / nbytes)))
+
+    def rand_like(n, nsets, scale=1.0):
+        host = (scale * rng.standard_normal(n)).astype(np.float32)
+        first = DeviceBuffer.from_numpy(host)
+        out = [first]
+        for _ in range(nsets - 1):
+            b = DeviceBuffer(n * 4)
+            K.scale(first, b, n, 1.0, stream=s)
+            out.append(b)
+        return out
+
+    def timed(call, nsets, reps):
+        for i in range(2 * nsets):
+            call(i % nsets)
+        s.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for i in range(reps):
+            call(i % nsets)
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    res = {}
+
+    def row(name, ms, nbytes, shape):
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"shape": shape, "us": round(ms * 1e3, 2), "bytes": int(nbytes),
+                     "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4)}
+        print(f"[bench] {name}: {ms * 1e3:.1f} us, {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%})",
+              file=sys.stderr, flush=True)
+
+    # RMSNorm backward with residual add and gain gradient: dy, x, res in; dx out
+    n = T * D
+    nb = 4 * n * 4
+    k = sets_for(nb)
+    dy, x, res_, dx = rand_like(n, k), rand_like(n, k), rand_like(n, k), rand_like(n, k)
+    w = DeviceBuffer.from_numpy(np.ones(D, np.float32))
+    dw = DeviceBuffer(D * 4)
+    ms = timed(lambda i: K.rmsnorm_backward(dy[i], x[i], w, dx[i], dw, T, D, 1e-6, residual=res_[i],
+                                            stream=s), k, 8 * k)
+    row("rmsnorm_backward", ms, nb + 2 * D * 4, f"[{T}, {D}] + residual, gain gradient")
+    del dy, x, res_, dx
+    # SwiGLU backward: d_gated, pre_gate, up in; d_pre_gate, d_up out
+    n = T * F
+    nb = 5 * n * 4
+    k = sets_for(nb)
+    dg, pg, up, dpg, dup = (rand_like(n, k) for _ in range(5))
+    ms = timed(lambda i: K.swiglu_backward(dg[i], pg[i], up[i], dpg[i], dup[i], n, stream=s), k, 4 * k)
+    row("swiglu_backward", ms, nb, f"[{T}, {F}]")
+    del dg, pg, up, dpg, dup
+    # RoPE backward over q and k (qk_rope_backward_batched): in and out
+    nq, nk = T * H * hd, T * Hkv * hd
+    nb = 2 * (nq + nk) * 4
+    k = sets_for(nb)
+    rp = K.rope_params(T, H, Hkv, hd, hd, 1e6, seq_len=512)
+    dqo, dqi, dko, dki = rand_like(nq, k), rand_like(nq, k), rand_like(nk, k), rand_like(nk, k)
+    ms = timed(lambda i: K.qk_rope_backward(rp, dqo[i], dqi[i], dko[i], dki[i], stream=s), k, 8 * k)
+    row("qk_rope_backward", ms, nb, f"q [{T}, {H}, {hd}] + k [{T}, {Hkv}, {hd}], seq 512")
+    del dqo, dqi, dko, dki
+    # Adam over a 128 Mi-parameter span: p, g, m, v in; p, m, v out
+    n = 128 << 20
+    nb = 7 * n * 4
+    pp, gg = rand_like(n, 1, 0.02), rand_like(n, 1, 1e-3)
+    mm, vv = DeviceBuffer.zeros(n * 4), DeviceBuffer.zeros(n * 4)
+    ms = timed(lambda i: K.adam_step(pp[0], gg[0], mm, vv, n, 1e-4, 0.9, 0.999, 1e-8, 1, stream=s),
+               1, 5)
+    row("adam_step", ms, nb, f"{n} params")
+    del pp, gg, mm, vv
+    # Embedding backward (accumulate into dE): dy read, touched dE rows read + written
+    V = 151936
+    ids_h = rng.integers(0, V, T).astype(np.uint32)
+    distinct = len(np.unique(ids_h))
+    nb = T * D * 4 + 2 * distinct * D * 4
+    ids = DeviceBuffer.from_numpy(ids_h)
+    dyb = rand_like(T * D, 1)
+    dE = DeviceBuffer.zeros(V * D * 4)
+    ms = timed(lambda i: K.embedding_backward(dyb[0], ids, dE, T, D, V, stream=s), 1, 20)
+    row("embedding_backward", ms, nb, f"{T} ids into [{V}, {D}], accumulate")
+    return res
 
 
 def calib_copy():
@@ -395,7 +500,7 @@ def main():
     ap.add_argument("--fa-warmup", type=int, default=150)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--only", default="all",
-                    choices=["all", "step", "fa", "mlp", "config4", "config5"],
+                    choices=["all", "step", "fa", "mlp", "bw", "config4", "config5"],
                     help="run only the step or only the attention benchmark (profiling runs)")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the benchmarks, run a copy-type kernel of known size "
@@ -424,6 +529,9 @@ def main():
     if args.only == "mlp":
         print(json.dumps({"mlp_runner": bench_mlp(args)}), flush=True)
         return
+    if args.only == "bw":
+        print(json.dumps({"bandwidth": bench_bandwidth(args)}), flush=True)
+        return
     if args.only in ("config4", "config5"):
         print(json.dumps({args.only: bench_config(args.only, args)}), flush=True)
         return
@@ -436,6 +544,7 @@ def main():
     if args.calib_copy:
         calib_copy()
     mlp = bench_mlp(args)
+    bw = bench_bandwidth(args)
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     peak = BF16_PEAK_TFLOPS if args.precision == "bf16" else FP32_PEAK_TFLOPS
     mfu = st["flops"] / (st["ms"] * 1e-3) / 1e12 / peak
@@ -471,6 +580,7 @@ def main():
                      "traffic_unit": "bytes per call (rocprofv3 FETCH_SIZE + WRITE_SIZE, "
                                      "calibrated; profiles/fa_bwd_config2_traffic.md)"},
         "cpu_baseline": cpu,
+        "bandwidth_kernels": bw,
         "mlp_runner": mlp,
     }
     print(json.dumps(out), flush=True)

@@ -68,7 +68,7 @@ def test_swiglu_forward_backward():
         assert grel(du_ref, host(bdu)) < 1e-6
 
 
-@pytest.mark.parametrize("rot", [128, 64])
+@pytest.mark.parametrize("rot", [128, 64, 36])  # 36: the scalar (non-float4) path
 def test_qk_rope_forward_backward(rot):
     from valkyr_amd import kernels as K
 

@@ -5,6 +5,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -53,6 +54,60 @@ static vkh_status rope_table_cached(int seq_len, int rot, float theta, const flo
     *out = d;
     return VKH_OK;
 }
+
+// Scratch memory of the standalone entry points (gain partials, sort work,
+// split-K partials): one buffer per device, grown on demand and reused, so a
+// call does not allocate.  Uses are ordered on the device: each use records
+// an event on its stream and the next use makes its stream wait for that
+// event, so calls on different streams never share the buffer at the same
+// time.  The mutex is held while a call enqueues its work.
+struct DevScratch {
+    void *p = nullptr;
+    size_t bytes = 0;
+    hipEvent_t done = nullptr;
+    bool used = false;
+};
+
+class ScratchLease {
+  public:
+    ~ScratchLease() {
+        if (d_) {
+            (void)hipEventRecord(d_->done, st_);
+            d_->used = true;
+        }
+    }
+    vkh_status acquire(size_t bytes, hipStream_t st, void **out) {
+        static std::mutex mu;
+        static std::map<int, DevScratch> per_dev;
+        lk_ = std::unique_lock<std::mutex>(mu);
+        int dev = 0;
+        VKH_HIP(hipGetDevice(&dev));
+        DevScratch &d = per_dev[dev];
+        if (!d.done) VKH_HIP(hipEventCreateWithFlags(&d.done, hipEventDisableTiming));
+        if (d.bytes < bytes) {
+            if (d.p) {
+                VKH_HIP(hipEventSynchronize(d.done));
+                VKH_HIP(hipFree(d.p));
+                d.p = nullptr;
+                d.bytes = 0;
+            }
+            const size_t nb = std::max(bytes, (size_t)1 << 20);
+            VKH_HIP(hipMalloc(&d.p, nb));
+            d.bytes = nb;
+        } else if (d.used) {
+            VKH_HIP(hipStreamWaitEvent(st, d.done, 0));
+        }
+        d_ = &d;
+        st_ = st;
+        *out = d.p;
+        return VKH_OK;
+    }
+
+  private:
+    std::unique_lock<std::mutex> lk_;
+    DevScratch *d_ = nullptr;
+    hipStream_t st_ = nullptr;
+};
 
 }  // namespace vkh
 
@@ -283,9 +338,9 @@ extern "C++" {
 template <class F>
 static vkh_status with_g16_ws(int M, int N, int K, hipStream_t st, const char *what, F &&f) {
     GemmWs ws{nullptr, g16_ws_bytes_for(M, N, K)};
-    if (ws.bytes) VKH_HIP(hipMallocAsync(&ws.p, ws.bytes, st));
+    ScratchLease lease;
+    if (ws.bytes) VKH_TRY(lease.acquire(ws.bytes, st, &ws.p));
     const hipError_t e = f(ws);
-    if (ws.p) (void)hipFreeAsync(ws.p, st);
     if (e != hipSuccess) return hip_fail(e, what);
     return VKH_OK;
 }
@@ -401,11 +456,11 @@ vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w,
     CHECK_ARG(dy && x && w && dx, "null pointer");
     if (dim > 4096) return fail(VKH_ERR_UNSUPPORTED, "rmsnorm_backward dim > 4096");
     hipStream_t st = S(stream);
-    float *partial = nullptr;
-    VKH_HIP(hipMallocAsync((void **)&partial, rmsnorm_partial_floats(n_rows, dim) * 4 + 16, st));
-    hipError_t e = rmsnorm_backward(dy, x, w, dx, nullptr, residual, dw, partial, n_rows, dim, eps,
-                                    gq ? 1 : 0, st);
-    (void)hipFreeAsync(partial, st);
+    void *partial = nullptr;
+    ScratchLease lease;
+    VKH_TRY(lease.acquire(rmsnorm_partial_floats(n_rows, dim) * 4 + 16, st, &partial));
+    hipError_t e = rmsnorm_backward(dy, x, w, dx, nullptr, residual, dw, (float *)partial, n_rows,
+                                    dim, eps, gq ? 1 : 0, st);
     if (e != hipSuccess) return hip_fail(e, "rmsnorm_backward");
     return VKH_OK;
 }
@@ -464,9 +519,9 @@ vkh_status vkh_embedding_backward(const float *dy, const uint32_t *ids, float *d
     if (n_pos > (uint32_t)kEmbedBwMaxPos) return fail(VKH_ERR_UNSUPPORTED, "n_pos > %d", kEmbedBwMaxPos);
     hipStream_t st = S(stream);
     void *work = nullptr;
-    VKH_HIP(hipMallocAsync(&work, embed_bw_work_bytes(n_pos), st));
+    ScratchLease lease;
+    VKH_TRY(lease.acquire(embed_bw_work_bytes(n_pos), st, &work));
     hipError_t e = embedding_backward(dy, ids, dE, n_pos, dim, vocab, true, work, st);
-    (void)hipFreeAsync(work, st);
     if (e != hipSuccess) return hip_fail(e, "embedding_backward");
     return VKH_OK;
 }

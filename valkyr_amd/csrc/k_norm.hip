@@ -167,14 +167,15 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
     for (int c = threadIdx.x; c < dim; c += NT) partial[(long)blockIdx.x * dim + c] = red[c];
 }
 
-// out[c] = sum_b partial[b * stride + c].  A block owns 16 columns; its 16
+// out[c] = sum_b partial[b * stride + c].  A block owns 4 columns; its 64
 // row groups each sum a strided subset of the partial rows with four
-// independent accumulators, then the groups are combined in LDS in a fixed
-// order, so the result does not depend on scheduling.
-constexpr int CS_COLS = 16, CS_GROUPS = 16;
+// independent accumulators, then the groups are combined in LDS by a
+// fixed-shape pairwise tree, so the result does not depend on scheduling.
+// (Many narrow blocks: the partials sit in L2 and the sum is latency-bound.)
+constexpr int CS_COLS = 4, CS_GROUPS = 64;
 __global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *partial, int nparts,
                                                               long stride, int dim, float *out) {
-    __shared__ float sh[CS_GROUPS][CS_COLS + 1];
+    __shared__ float sh[CS_GROUPS][CS_COLS];
     const int cl = threadIdx.x % CS_COLS, g = threadIdx.x / CS_COLS;
     const int c = blockIdx.x * CS_COLS + cl;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -190,19 +191,63 @@ __global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *part
     }
     sh[g][cl] = (a0 + a1) + (a2 + a3);
     __syncthreads();
-    if (g == 0 && c < dim) {
-        float s = 0.f;
 #pragma unroll
-        for (int i = 0; i < CS_GROUPS; ++i) s += sh[i][cl];
-        out[c] = s;
+    for (int s = CS_GROUPS / 2; s > 0; s >>= 1) {
+        if (g < s) sh[g][cl] += sh[g + s][cl];
+        __syncthreads();
     }
+    if (g == 0 && c < dim) out[c] = sh[0][cl];
 }
 
 // ── RoPE ─────────────────────────────────────────────────────────────
 
 // qk_rope_partial_batched.comp / qk_rope_backward_batched.comp with the
 // cos/sin of (position, pair) taken from a table built by the same fp32
-// formula.  One thread per element of the combined [rows, Hq + Hkv, hd].
+// formula.  One block per row (position p = row % seq_len); each thread
+// rotates four consecutive elements of a head (32-bit index arithmetic, float4
+// loads and stores), the partner quad i +- half is read again from cache.
+// Scalar form for rows or rotary widths that are not multiples of 4.
+__global__ __launch_bounds__(NT) void qk_rope4_k(const float *q_in, long ldq_in, float *q_out,
+                                                 long ldq_out, const float *k_in, long ldk_in,
+                                                 float *k_out, long ldk_out, int n_rows, int hq,
+                                                 int hkv, int hd, int rot, int seq_len,
+                                                 const float2 *tab, int backward) {
+    const int half = rot / 2, qpr = hd / 4, nq4 = (hq + hkv) * qpr;
+    for (int p = blockIdx.x; p < n_rows; p += gridDim.x) {
+        const float2 *tr = tab + (long)(p % seq_len) * half;
+        for (int u = threadIdx.x; u < nq4; u += NT) {
+            const int h = u / qpr, i = 4 * (u - h * qpr);
+            const bool is_q = h < hq;
+            const float *in = (is_q ? q_in + (long)p * ldq_in : k_in + (long)p * ldk_in) +
+                              (is_q ? h : h - hq) * hd;
+            float *out = (is_q ? q_out + (long)p * ldq_out : k_out + (long)p * ldk_out) +
+                         (is_q ? h : h - hq) * hd;
+            const float4 x = *reinterpret_cast<const float4 *>(in + i);
+            if (i >= rot) {
+                *reinterpret_cast<float4 *>(out + i) = x;
+                continue;
+            }
+            const bool lower = i < half;
+            const int j = lower ? i : i - half;
+            const float4 y = *reinterpret_cast<const float4 *>(in + (lower ? i + half : i - half));
+            const float4 c01 = *reinterpret_cast<const float4 *>(tr + j);
+            const float4 c23 = *reinterpret_cast<const float4 *>(tr + j + 2);
+            const float xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
+            const float cs[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
+            float o[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // lower half: a = x, b = y; upper half: a = y (pair's low), b = x
+                if (!backward)
+                    o[e] = lower ? xs[e] * cs[e] - ys[e] * sn[e] : ys[e] * sn[e] + xs[e] * cs[e];
+                else
+                    o[e] = lower ? cs[e] * xs[e] + sn[e] * ys[e] : -sn[e] * ys[e] + cs[e] * xs[e];
+            }
+            *reinterpret_cast<float4 *>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
+        }
+    }
+}
+
 __global__ void qk_rope_k(const float *q_in, long ldq_in, float *q_out, long ldq_out,
                           const float *k_in, long ldk_in, float *k_out, long ldk_out, int n_rows,
                           int hq, int hkv, int hd, int rot, int seq_len, const float2 *tab,
@@ -737,7 +782,10 @@ __global__ __launch_bounds__(NT) void qkv_bwd8_k(QkvLayout L, float *dqkv, long 
         partial[(long)blockIdx.x * 2 * hd + c] = red[c / hd][c % hd];
 }
 
-constexpr int kRmsMaxBlocks = 512, kQkvMaxBlocks = 512;
+// Grid caps.  The Q/K-norm backward has one gain partial (2 x head_dim floats)
+// per block; 2048 blocks give each wave about two grid-stride items (at 512,
+// eight serially dependent ones made the kernel latency-bound).
+constexpr int kRmsMaxBlocks = 512, kQkvMaxBlocks = 2048;
 
 inline int rms_grid(int rows) { return std::max(1, std::min(kRmsMaxBlocks, (rows + NW - 1) / NW)); }
 
@@ -842,6 +890,16 @@ hipError_t qk_rope(const float *q_in, long ldq_in, float *q_out, long ldq_out, c
                    bool backward, hipStream_t st) {
     if (n_rows <= 0) return hipSuccess;
     if (rotary_dim > head_dim || (rotary_dim & 1) || seq_len <= 0) return hipErrorInvalidValue;
+    const bool v4 = head_dim % 4 == 0 && rotary_dim % 8 == 0 && al16(q_in) && al16(q_out) &&
+                    al16(k_in) && al16(k_out) && al16(tab) && ldq_in % 4 == 0 &&
+                    ldq_out % 4 == 0 && ldk_in % 4 == 0 && ldk_out % 4 == 0;
+    if (v4) {
+        hipLaunchKernelGGL(qk_rope4_k, dim3((unsigned)std::min(n_rows, 65535)), dim3(NT), 0, st,
+                           q_in, ldq_in, q_out, ldq_out, k_in, ldk_in, k_out, ldk_out, n_rows,
+                           n_q_heads, n_kv_heads, head_dim, rotary_dim, seq_len, tab,
+                           backward ? 1 : 0);
+        return hipGetLastError();
+    }
     const long total = (long)n_rows * (n_q_heads + n_kv_heads) * head_dim;
     long g = (total + NT - 1) / NT;
     if (g > 4096) g = 4096;

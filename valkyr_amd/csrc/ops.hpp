@@ -125,7 +125,8 @@ size_t qkv_partial_floats(const QkvLayout &L);
 // ── embedding backward (k_embed.hip) ─────────────────────────────────
 // out[tok] = (accumulate ? out[tok] : 0) + sum over positions p with
 // ids[p] == tok of dy[p] (position order).  Rows of untouched tokens are not
-// written.  `work` must hold embed_bw_work_bytes(n_pos) bytes.
+// written.  `work` is not used (embed_bw_work_bytes is a 16-byte placeholder,
+// kept so callers that pass a buffer stay valid).
 hipError_t embedding_backward(const float *dy, const uint32_t *ids, float *out, int n_pos,
                               int dim, int vocab, bool accumulate, void *work, hipStream_t st);
 size_t embed_bw_work_bytes(int n_pos);
