@@ -65,6 +65,7 @@ struct DevScratch {
     void *p = nullptr;
     size_t bytes = 0;
     hipEvent_t done = nullptr;
+    hipStream_t last = nullptr;  // stream of the last use (same stream: ordered already)
     bool used = false;
 };
 
@@ -94,9 +95,10 @@ class ScratchLease {
             const size_t nb = std::max(bytes, (size_t)1 << 20);
             VKH_HIP(hipMalloc(&d.p, nb));
             d.bytes = nb;
-        } else if (d.used) {
-            VKH_HIP(hipStreamWaitEvent(st, d.done, 0));
+        } else if (d.used && d.last != st) {
+            VKH_HIP(hipStreamWaitEvent(st, d.done, 0));  // a use on another stream
         }
+        d.last = st;
         d_ = &d;
         st_ = st;
         *out = d.p;

@@ -46,6 +46,38 @@ VKH_DEV void store4<bf16>(bf16 *p, float a, float b, float c, float d) {
 // ── RMSNorm: one wave per row, lane l holds columns 4 l + 256 j ─────────
 
 // C4 = float4 chunks per lane (dim <= 256 * C4)
+template <int CTRL>
+VKH_DEV double dpp_d(double v) {
+    const long long b = __builtin_bit_cast(long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xf, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xf, 0xf, false);
+    return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
+}
+
+template <int LPH>
+VKH_DEV double grp_sum(double v) {
+    v += dpp_d<0xB1>(v);   // quad_perm [1,0,3,2]
+    v += dpp_d<0x4E>(v);   // quad_perm [2,3,0,1]
+    v += dpp_d<0x141>(v);  // row_half_mirror: the other quad of the 8 lanes
+    if constexpr (LPH == 16) v += dpp_d<0x140>(v);  // row_mirror: the other 8 lanes
+    return v;
+}
+
+// Sum over the 64 lanes of a wave: DPP row sums, then the four row results
+// combined in a fixed order (no LDS round trips, unlike shuffles).
+VKH_DEV double wave_sum_dpp(double v) {
+    v = grp_sum<16>(v);
+    const long long b = __builtin_bit_cast(long long, v);
+    double r[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+        const unsigned lo = (unsigned)__builtin_amdgcn_readlane((int)b, 16 * k);
+        const unsigned hi = (unsigned)__builtin_amdgcn_readlane((int)(b >> 32), 16 * k);
+        r[k] = __builtin_bit_cast(double, ((long long)hi << 32) | (long long)lo);
+    }
+    return (r[0] + r[1]) + (r[2] + r[3]);
+}
+
 template <typename TO, int C4>
 __global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float *w, TO *y, int rows,
                                                      int dim, float eps, int gq) {
@@ -64,7 +96,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_fwd_k(const float *x, const float 
             ss += (double)xv[j].z * (double)xv[j].z;
             ss += (double)xv[j].w * (double)xv[j].w;
         }
-        ss = wave_sum(ss);
+        ss = wave_sum_dpp(ss);
         const double m = ss / (double)dim;
         const float ri = 1.0f / sqrtf((float)m + eps);
 #pragma unroll
@@ -122,8 +154,8 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
                 A += (double)ds[q] * (double)gs[q] * xd;
             }
         }
-        ss = wave_sum(ss);
-        A = wave_sum(A);
+        ss = wave_sum_dpp(ss);
+        A = wave_sum_dpp(A);
         const double m = ss / (double)dim;
         const float ri = 1.0f / sqrtf((float)m + eps);
         const float ri3_over_D = ri * ri * ri / ri3_div;
@@ -524,23 +556,6 @@ __global__ __launch_bounds__(NT) void qkv_bwd_k(QkvLayout L, float *dqkv, long l
 // RoPE at LPH = 16, the partner element i +- 64 sits in lane j ^ 8 of the
 // same row (row rotate by 8).  Requires rotary_dim % 16 == 0 so a lane's 8
 // elements are all on one side of the rotation.
-
-template <int CTRL>
-VKH_DEV double dpp_d(double v) {
-    const long long b = __builtin_bit_cast(long long, v);
-    const int lo = __builtin_amdgcn_update_dpp(0, (int)b, CTRL, 0xf, 0xf, false);
-    const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTRL, 0xf, 0xf, false);
-    return __builtin_bit_cast(double, ((long long)hi << 32) | (long long)(unsigned)lo);
-}
-
-template <int LPH>
-VKH_DEV double grp_sum(double v) {
-    v += dpp_d<0xB1>(v);   // quad_perm [1,0,3,2]
-    v += dpp_d<0x4E>(v);   // quad_perm [2,3,0,1]
-    v += dpp_d<0x141>(v);  // row_half_mirror: the other quad of the 8 lanes
-    if constexpr (LPH == 16) v += dpp_d<0x140>(v);  // row_mirror: the other 8 lanes
-    return v;
-}
 
 VKH_DEV void ld8(const float *p, float (&v)[8]) {
     const float4 a = reinterpret_cast<const float4 *>(p)[0];
