@@ -199,15 +199,14 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
     for (int c = threadIdx.x; c < dim; c += NT) partial[(long)blockIdx.x * dim + c] = red[c];
 }
 
-// out[c] = sum_b partial[b * stride + c].  A block owns 4 columns; its 64
+// out[c] = sum_b partial[b * stride + c].  A block owns 16 columns; its 16
 // row groups each sum a strided subset of the partial rows with four
-// independent accumulators, then the groups are combined in LDS by a
-// fixed-shape pairwise tree, so the result does not depend on scheduling.
-// (Many narrow blocks: the partials sit in L2 and the sum is latency-bound.)
-constexpr int CS_COLS = 4, CS_GROUPS = 64;
+// independent accumulators, then the groups are combined in LDS in a fixed
+// order, so the result does not depend on scheduling.
+constexpr int CS_COLS = 16, CS_GROUPS = 16;
 __global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *partial, int nparts,
                                                               long stride, int dim, float *out) {
-    __shared__ float sh[CS_GROUPS][CS_COLS];
+    __shared__ float sh[CS_GROUPS][CS_COLS + 1];
     const int cl = threadIdx.x % CS_COLS, g = threadIdx.x / CS_COLS;
     const int c = blockIdx.x * CS_COLS + cl;
     float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
@@ -223,12 +222,12 @@ __global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *part
     }
     sh[g][cl] = (a0 + a1) + (a2 + a3);
     __syncthreads();
+    if (g == 0 && c < dim) {
+        float s = 0.f;
 #pragma unroll
-    for (int s = CS_GROUPS / 2; s > 0; s >>= 1) {
-        if (g < s) sh[g][cl] += sh[g + s][cl];
-        __syncthreads();
+        for (int i = 0; i < CS_GROUPS; ++i) s += sh[i][cl];
+        out[c] = s;
     }
-    if (g == 0 && c < dim) out[c] = sh[0][cl];
 }
 
 // ── RoPE ─────────────────────────────────────────────────────────────
@@ -797,10 +796,10 @@ __global__ __launch_bounds__(NT) void qkv_bwd8_k(QkvLayout L, float *dqkv, long 
         partial[(long)blockIdx.x * 2 * hd + c] = red[c / hd][c % hd];
 }
 
-// Grid caps.  The Q/K-norm backward has one gain partial (2 x head_dim floats)
-// per block; 2048 blocks give each wave about two grid-stride items (at 512,
-// eight serially dependent ones made the kernel latency-bound).
-constexpr int kRmsMaxBlocks = 512, kQkvMaxBlocks = 2048;
+// Grid caps (the gain partials are one row per block; in the training step
+// a larger Q/K-norm backward grid made its column sums on the side stream
+// slower than it made the kernel faster).
+constexpr int kRmsMaxBlocks = 512, kQkvMaxBlocks = 512;
 
 inline int rms_grid(int rows) { return std::max(1, std::min(kRmsMaxBlocks, (rows + NW - 1) / NW)); }
 
