@@ -1341,14 +1341,15 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
 }
 
 namespace dq4 {
-constexpr int NT = 256, HD = 128, QW = 64, BQ = 4 * QW, BN = 32;
-constexpr int QSUB = QW / 16, KS = BN / 16, DS = HD / 32, DSUB = HD / 16;
+constexpr int HD = 128, BQ = 256, BN = 32;
+constexpr int KS = BN / 16, DS = HD / 32, DSUB = HD / 16;
 constexpr int TILE = BN * HD * 2;  // 8 KB: one K or V tile
 constexpr int NBUF = 3;
 }  // namespace dq4
 
-// dQ.  Block = 256 queries of one (sequence, head); wave w owns the 16-row
-// query sub-tiles Q0 + 64 j + 16 w (j = 0..3), interleaved so that under a
+// dQ.  Block = 256 queries of one (sequence, head) on NWV waves (4: one wave
+// per SIMD, 64 queries each; 8: two per SIMD, 32 queries each); wave w owns
+// the 16-row query sub-tiles Q0 + 16 (NWV j + w), interleaved so that under a
 // causal mask every wave has work until the block's last key tile.  Q and dO
 // of those rows sit in VGPRs as B operands; per 32-key tile (K and V by DMA,
 // three buffers)
@@ -1358,8 +1359,12 @@ constexpr int NBUF = 3;
 // Key tiles ascend from 0, so all query blocks of a (sequence, head) read
 // the same K / V tile at about the same time; the heaviest query blocks
 // (highest queries) start first.
-__global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs p) {
+template <int NWV>
+__global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs p) {
     using namespace dq4;
+    constexpr int QSUB = BQ / 16 / NWV;  // 16-row query sub-tiles per wave
+    constexpr int QST = 16 * NWV;        // row stride between a wave's sub-tiles
+    constexpr int RPW = BN / NWV;        // K / V tile rows each wave moves by DMA
     using dkv3::frag_row;
     using dkv3::frag_t;
     __shared__ __attribute__((aligned(16))) char Kt[NBUF][TILE];
@@ -1370,14 +1375,14 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
     const int kvh = h / (s.n_heads / s.n_kv_heads);
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int q00 = qblk * BQ + 16 * wave;  // first row of sub-tile j is q00 + 64 j
+    const int q00 = qblk * BQ + 16 * wave;  // first row of sub-tile j is q00 + QST j
     const float c2 = s.inv_sqrt_dim * LOG2E;
 
     bf16x8 qr[QSUB][DS], orr[QSUB][DS];
     float lq[QSUB], dd[QSUB];
 #pragma unroll
     for (int j = 0; j < QSUB; ++j) {
-        const int q = q00 + 64 * j + c16;
+        const int q = q00 + QST * j + c16;
         const bool ok = q < s.n_q;
         const long t = (long)b * s.n_q + q;
         const bf16 *qp = (const bf16 *)p.q + t * p.ldq + h * HD + 8 * g;
@@ -1393,12 +1398,6 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
         dd[j] = ok ? p.d[t * s.n_heads + h] : 0.f;
     }
     wait_vm0();
-#ifdef DQ4_QA
-#pragma unroll
-    for (int j = 0; j < QSUB; ++j)
-#pragma unroll
-        for (int ds = 0; ds < DS; ++ds) asm volatile("" : "+a"(qr[j][ds]), "+a"(orr[j][ds]));
-#endif
     f32x4 acc[DSUB][QSUB];
 #pragma unroll
     for (int i = 0; i < DSUB; ++i)
@@ -1411,14 +1410,15 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
                            (unsigned)((long)s.n_kv * p.ldk * 2));
     const sgpr4 rv = rsrc4((const bf16 *)p.v + (long)b * s.n_kv * p.ldv,
                            (unsigned)((long)s.n_kv * p.ldv * 2));
-    // wave w moves rows 8 w .. 8 w + 7 of the K and V tiles (4 operations)
+    // wave w moves rows RPW w .. RPW w + RPW - 1 of the K and V tiles
+    // (RPW / 2 operations)
     auto dma = [&](int t, int buf) {
         const int kk = t * BN;
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
-            const int r = 8 * wave + 4 * i + g;
+        for (int i = 0; i < RPW / 4; ++i) {
+            const int r = RPW * wave + 4 * i + g;
             const int col = kvh * HD + 8 * (c16 ^ dkv3::swz(r));
-            const int lo = (8 * wave + 4 * i) * HD * 2;
+            const int lo = (RPW * wave + 4 * i) * HD * 2;
             dma16_async(rk, Kt[buf] + lo, (unsigned)(((kk + r) * (int)p.ldk + col) * 2));
             dma16_async(rv, Vt[buf] + lo, (unsigned)(((kk + r) * (int)p.ldv + col) * 2));
         }
@@ -1429,7 +1429,7 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
     // is a per-lane base plus a compile-time offset (no per-tile VALU adds).
     auto step = [&](const int t, auto bufc) {
         constexpr int buf = decltype(bufc)::value;
-        if (t + 1 < ntl) __builtin_amdgcn_s_waitcnt(0x0f70 | 4);
+        if (t + 1 < ntl) __builtin_amdgcn_s_waitcnt(0x0f70 | (RPW / 2));
         else wait_vm0();
         lds_barrier();
         if (t + 2 < ntl) dma(t + 2, (buf + 2) % NBUF);
@@ -1440,7 +1440,7 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
         int lim[QSUB];
 #pragma unroll
         for (int j = 0; j < QSUB; ++j)
-            lim[j] = min(s.causal ? q00 + 64 * j + c16 - kk - 4 * g : (1 << 30), s.n_kv - 1 - kk - 4 * g);
+            lim[j] = min(s.causal ? q00 + QST * j + c16 - kk - 4 * g : (1 << 30), s.n_kv - 1 - kk - 4 * g);
         const bool diag = (s.causal && kk + BN - 1 > q00) || kk + BN > s.n_kv;
         f32x4 st[KS][QSUB], dpt[KS][QSUB];
 #pragma unroll
@@ -1468,9 +1468,15 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
                               : frag_t(Kb, 0, 0, g, c16);
 #pragma unroll
             for (int j = 0; j < QSUB; ++j) dpt[ks][j] = mfma16x16x32(fr[f & 1], orr[j][ds], dpt[ks][j]);
-            const int ks2 = f / 4, j2 = f % 4;
+            // the KS * QSUB score tiles spread evenly over the 8 steps
+            constexpr int EVERY = 8 / (KS * QSUB);
+            static_assert(EVERY >= 1 && EVERY * KS * QSUB == 8, "exp schedule");
+            if (f % EVERY == 0) {
+                const int t2 = f / EVERY, ks2 = t2 / QSUB, j2 = t2 % QSUB;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) st[ks2][j2][r] = __builtin_amdgcn_exp2f(st[ks2][j2][r] * c2 - lq[j2]);
+                for (int r = 0; r < 4; ++r)
+                    st[ks2][j2][r] = __builtin_amdgcn_exp2f(st[ks2][j2][r] * c2 - lq[j2]);
+            }
         }
         if (diag) {  // keys above a query of this wave (uniform; no MFMA inside)
 #pragma unroll
@@ -1481,12 +1487,6 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
                     for (int r = 0; r < 4; ++r)
                         if (16 * ks + r > lim[j]) st[ks][j][r] = 0.f;
         }
-#ifdef DQ4_QA
-#pragma unroll
-        for (int ks = 0; ks < KS; ++ks)
-#pragma unroll
-            for (int j = 0; j < QSUB; ++j) asm volatile("" : "+v"(dpt[ks][j]));
-#endif
         // dS^T = P^T (dP^T - D) -> bf16 B operands (contraction = keys)
         bf16x8 sb[QSUB];
 #pragma unroll
@@ -1513,7 +1513,7 @@ __global__ __launch_bounds__(dq4::NT, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs
     // acc[i][j][r] = dQ^T[16 i + 4 g + r][q00 + 64 j + c16]
 #pragma unroll
     for (int j = 0; j < QSUB; ++j) {
-        const int q = q00 + 64 * j + c16;
+        const int q = q00 + QST * j + c16;
         if (q >= s.n_q) continue;
         float *dqr = p.dq + ((long)b * s.n_q + q) * p.lddq + h * HD;
         const float sc_ = s.inv_sqrt_dim;
@@ -1997,9 +1997,10 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
             return hipErrorInvalidValue;
         hipLaunchKernelGGL(fa_bwd_dkv4_k, dim3(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN),
                            dim3(dkv4::NT), 0, st, s, p);
-        hipLaunchKernelGGL(fa_bwd_dq4_k,
+        constexpr int DQ_WAVES = 8;
+        hipLaunchKernelGGL(fa_bwd_dq4_k<DQ_WAVES>,
                            dim3(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ),
-                           dim3(dq4::NT), 0, st, s, p);
+                           dim3(DQ_WAVES * 64), 0, st, s, p);
         return hipGetLastError();
     }
     if (!ds_ws) return hipErrorInvalidValue;
