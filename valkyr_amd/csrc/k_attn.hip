@@ -1083,14 +1083,13 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
 #define DKV4_PHASE()
 #endif
 namespace dkv4 {
-constexpr int NT = 256, HD = 128, BM = 32, KW = 64, BN = 128;
-constexpr int KS = KW / 16, DS = HD / 32, DSUB = HD / 16, QS = BM / 16;
+constexpr int HD = 128, BM = 32, BN = 128;
+constexpr int DS = HD / 32, DSUB = HD / 16, QS = BM / 16;
 constexpr int TILE = BM * HD * 2;           // 8 KB: one Q or dO tile
 constexpr int NBUF = 3;                     // tile buffers (two DMA batches in flight)
 constexpr int STREAM = NBUF * 2 * TILE;     // 48 KB: one head group's Q / dO tiles
-constexpr int XSLOT = DSUB * KS * 64 * 16;  // 32 KB: one wave's dK^T or dV^T
-constexpr int LDS = 4 * XSLOT;              // tile streams + V slices in the loop, the exchange after
-static_assert(2 * STREAM + 2 * KW * HD * 2 <= LDS, "tile streams and V slices exceed the LDS arena");
+constexpr int LDS = 128 * 1024;            // tile streams + V in the loop, the exchange after
+static_assert(2 * STREAM + BN * HD * 2 <= LDS, "tile streams and V slices exceed the LDS arena");
 }  // namespace dkv4
 
 // dK / dV.  Block = 128 keys of one (sequence, KV head); 4 waves = 2 key
@@ -1110,8 +1109,14 @@ static_assert(2 * STREAM + 2 * KW * HD * 2 <= LDS, "tile streams and V slices ex
 // of one (sequence, KV head), which sit on one XCD, read a tile at about the
 // same time and share it in L2.  Under a causal mask the heaviest key blocks
 // (lowest keys) have the lowest block ids and start first.
-__global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPtrs p) {
+template <int NWV>
+__global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPtrs p) {
     using namespace dkv4;
+    constexpr int NS = NWV / 2;                 // key slices per head group
+    constexpr int KW = BN / NS, KS = KW / 16;   // keys per wave, 16-key sub-tiles
+    constexpr int XSLOT = DSUB * KS * 64 * 16;  // one wave's dK^T or dV^T
+    static_assert(NWV * XSLOT <= LDS, "exchange exceeds the LDS arena");
+    constexpr int RP = BM / (NS / 2);           // Q or dO tile rows each wave moves
     using dkv3::frag_row;
     using dkv3::frag_t;
     __shared__ __attribute__((aligned(16))) char smem[LDS];
@@ -1122,7 +1127,11 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     const int hpk = s.n_heads / s.n_kv_heads, nh = hpk / 2;
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int sl = wave & 1, hg = wave >> 1;  // key slice, head group
+    const int sl = wave % NS, hg = wave / NS;  // key slice, head group
+    // DMA share: the first half of a group's waves moves Q (and lse), the
+    // second half dO (and D), RP rows each
+    const bool tdo = sl >= NS / 2;
+    const int part = sl % (NS / 2);
     const int k0 = kt * BN, kw0 = k0 + sl * KW;
     const float c2 = s.inv_sqrt_dim * LOG2E;
 
@@ -1163,14 +1172,13 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     char *strm = smem + hg * STREAM;
 
     // this wave's DMA share: slice 0 moves Q and lse, slice 1 dO and D
-    const sgpr4 rt = sl ? rsrc4((const bf16 *)p.dout + (long)b * s.n_q * p.lddo,
+    const sgpr4 rt = tdo ? rsrc4((const bf16 *)p.dout + (long)b * s.n_q * p.lddo,
                                 (unsigned)((long)s.n_q * p.lddo * 2))
                         : rsrc4((const bf16 *)p.q + (long)b * s.n_q * p.ldq,
                                 (unsigned)((long)s.n_q * p.ldq * 2));
-    const int ldt = (int)(sl ? p.lddo : p.ldq);
-    const sgpr4 rs = rsrc4((sl ? p.d : p.lse) + (long)b * s.n_q * s.n_heads,
+    const int ldt = (int)(tdo ? p.lddo : p.ldq);
+    const sgpr4 rs = rsrc4((tdo ? p.d : p.lse) + (long)b * s.n_q * s.n_heads,
                            (unsigned)((long)s.n_q * s.n_heads * 4));
-    float(*stat)[NBUF][64] = sl ? Dd : Ls;
     auto tile_of = [&](int it, int &h, int &q0) {
         h = kvh * hpk + hg + 2 * (it % nh);
         q0 = qstart + (nqt - 1 - it / nh) * BM;
@@ -1186,14 +1194,18 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
         int ln = lane;
         asm volatile("" : "+v"(ln));
         const int lg = ln >> 4, l16 = ln & 15;
-        char *dst = strm + buf * 2 * TILE + sl * TILE;
+        char *dst = strm + buf * 2 * TILE + (tdo ? TILE : 0);
 #pragma unroll
-        for (int i = 0; i < BM / 4; ++i) {
-            const int r = 4 * i + lg;
+        for (int i = 0; i < RP / 4; ++i) {
+            const int r = part * RP + 4 * i + lg;
             const int col = h * HD + 8 * (l16 ^ dkv3::swz(r));
-            dma16_async(rt, dst + 4 * i * HD * 2, (unsigned)(((q0 + r) * ldt + col) * 2));
+            dma16_async(rt, dst + (part * RP + 4 * i) * HD * 2, (unsigned)(((q0 + r) * ldt + col) * 2));
         }
-        dma4_async(rs, stat[hg][buf], (unsigned)(((q0 + ln) * s.n_heads + h) * 4));
+        if (part == 0) {  // uniform; each branch names its LDS array (no generic pointer)
+            const unsigned so = (unsigned)(((q0 + ln) * s.n_heads + h) * 4);
+            if (tdo) dma4_async(rs, Dd[hg][buf], so);
+            else dma4_async(rs, Ls[hg][buf], so);
+        }
     };
 
     if (niter > 0) dma(0, 0);
@@ -1202,8 +1214,12 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     // is a per-lane base plus a compile-time offset (no per-tile VALU adds).
     auto step = [&](const int it, auto bufc) {
         constexpr int buf = decltype(bufc)::value;
-        if (it + 1 < niter) __builtin_amdgcn_s_waitcnt(0x0f70 | 9);  // tile it+1 may stay in flight
-        else wait_vm0();
+        if (it + 1 < niter) {  // tile it+1 (RP / 4 rows + the stats wave's dword) may stay in flight
+            if (part == 0) __builtin_amdgcn_s_waitcnt(0x0f70 | (RP / 4 + 1));
+            else __builtin_amdgcn_s_waitcnt(0x0f70 | (RP / 4));
+        } else {
+            wait_vm0();
+        }
         lds_barrier();  // tile `it` landed; everyone is done with buffer (it + 2) % 3
         if (it + 2 < niter) dma(it + 2, (buf + 2) % NBUF);
         int h, q0;
@@ -1214,20 +1230,15 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
         // i.e. 16 ks - r > lim[qs] (branch-free compare against a per-lane limit)
         const bool diag = s.causal && kw0 + KW - 1 > q0;
         int lim[QS];
-        float lq[QS][4], dq[QS][4];
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs) {
-            lim[qs] = s.causal ? q0 + 16 * qs + 4 * g - kw0 - c16 : (1 << 30);
-            const float4 l4 = *reinterpret_cast<const float4 *>(&Ls[hg][buf][16 * qs + 4 * g]);
-            const float4 d4 = *reinterpret_cast<const float4 *>(&Dd[hg][buf][16 * qs + 4 * g]);
-            const float ls[4] = {l4.x, l4.y, l4.z, l4.w}, dv_[4] = {d4.x, d4.y, d4.z, d4.w};
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                // a fully masked row (lse = -inf) gets P = 0
-                lq[qs][r] = ls[r] == -INFINITY ? INFINITY : ls[r] * LOG2E;
-                dq[qs][r] = dv_[r];
-            }
-        }
+        for (int qs = 0; qs < QS; ++qs) lim[qs] = s.causal ? q0 + 16 * qs + 4 * g - kw0 - c16 : (1 << 30);
+        // lse and D of this lane's query rows q0 + 16 qs + 4 g + r, read from LDS
+        // where they are used (not held across the tile)
+        auto lse2 = [&](int qs, int r) {
+            const float l = Ls[hg][buf][16 * qs + 4 * g + r];
+            return l == -INFINITY ? INFINITY : l * LOG2E;  // fully masked row: P = 0
+        };
+        auto dval = [&](int qs, int r) { return Dd[hg][buf][16 * qs + 4 * g + r]; };
         f32x4 sc[QS][KS], dp[QS][KS];
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs)
@@ -1256,9 +1267,15 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
                 dp[qs][ks] = mfma16x16x32(fr[f & 1], frag_row(vsl, 16 * ks + c16, 32 * ds + 8 * g), dp[qs][ks]);
-            const int qs2 = f / 4, ks2 = f % 4;
+            // the QS * KS score tiles spread evenly over the 8 steps
+            constexpr int EVERY = 8 / (QS * KS);
+            static_assert(EVERY >= 1 && EVERY * QS * KS == 8, "exp schedule");
+            if (f % EVERY == 0) {
+                const int t2 = f / EVERY, qs2 = t2 / KS, ks2 = t2 % KS;
 #pragma unroll
-            for (int r = 0; r < 4; ++r) sc[qs2][ks2][r] = __builtin_amdgcn_exp2f(sc[qs2][ks2][r] * c2 - lq[qs2][r]);
+                for (int r = 0; r < 4; ++r)
+                    sc[qs2][ks2][r] = __builtin_amdgcn_exp2f(sc[qs2][ks2][r] * c2 - lse2(qs2, r));
+            }
         }
         if (diag) {  // keys above a query of the tile (uniform; no MFMA inside)
 #pragma unroll
@@ -1280,10 +1297,14 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
                 fr[n & 1] = n < DSUB ? frag_t(Ob, 16 * n, 0, g, c16) : frag_t(Qb, 0, 0, g, c16);
 #pragma unroll
                 for (int ks = 0; ks < KS; ++ks) dvt[i][ks] = mfma16x16x32(fr[i & 1], pb[ks], dvt[i][ks]);
-                const int qs2 = i / 4, ks2 = i % 4;
+                constexpr int EVERY = DSUB / (QS * KS);
+                static_assert(EVERY >= 1 && EVERY * QS * KS == DSUB, "dS schedule");
+                if (i % EVERY == 0) {
+                    const int t2 = i / EVERY, qs2 = t2 / KS, ks2 = t2 % KS;
 #pragma unroll
-                for (int r = 0; r < 4; ++r)
-                    dp[qs2][ks2][r] = sc[qs2][ks2][r] * (dp[qs2][ks2][r] - dq[qs2][r]);
+                    for (int r = 0; r < 4; ++r)
+                        dp[qs2][ks2][r] = sc[qs2][ks2][r] * (dp[qs2][ks2][r] - dval(qs2, r));
+                }
             }
         }
         // dK^T += Q^T dS
@@ -1298,11 +1319,15 @@ __global__ __launch_bounds__(dkv4::NT, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
                 for (int ks = 0; ks < KS; ++ks) dkt[i][ks] = mfma16x16x32(fr[i & 1], sb[ks], dkt[i][ks]);
             }
         }
-        // keep the loop-carried accumulators in AGPRs (the MFMA accumulate file)
+        // keep the loop-carried accumulators in AGPRs (the MFMA accumulate
+        // file) when one wave holds the whole register file; with two waves
+        // per SIMD the compiler's own split spills less
+        if constexpr (NWV == 4) {
 #pragma unroll
-        for (int i = 0; i < DSUB; ++i)
+            for (int i = 0; i < DSUB; ++i)
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(dvt[i][ks]), "+a"(dkt[i][ks]));
+                for (int ks = 0; ks < KS; ++ks) asm volatile("" : "+a"(dvt[i][ks]), "+a"(dkt[i][ks]));
+        }
     };
     for (int it0 = 0; it0 < niter; it0 += NBUF) {
         step(it0, std::integral_constant<int, 0>{});
@@ -1995,8 +2020,10 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
         if ((long)s.n_q * std::max(p.ldq, p.lddo) * 2 >= (1l << 31) ||
             (long)s.n_kv * std::max(p.ldk, p.ldv) * 2 >= (1l << 31))
             return hipErrorInvalidValue;
-        hipLaunchKernelGGL(fa_bwd_dkv4_k, dim3(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN),
-                           dim3(dkv4::NT), 0, st, s, p);
+        constexpr int DKV_WAVES = 8;
+        hipLaunchKernelGGL(fa_bwd_dkv4_k<DKV_WAVES>,
+                           dim3(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN),
+                           dim3(DKV_WAVES * 64), 0, st, s, p);
         constexpr int DQ_WAVES = 8;
         hipLaunchKernelGGL(fa_bwd_dq4_k<DQ_WAVES>,
                            dim3(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ),
