@@ -1997,13 +1997,12 @@ bool fa_bw_v4_ok(const AttnShape &s) {
            s.n_kv % 128 == 0;
 }
 
-// They run one block per CU, so they pay off when the dK/dV grid covers the
-// chip (>= 256 blocks: B = 4 x 2048 keys x 8 KV heads, or 8192 keys); the
-// training step's B = 4 x 512 keys (128 blocks) is faster on the
-// two-waves-per-SIMD kernel plus the dS GEMM, whose idle CUs the step's
-// weight-gradient stream fills.
+// They pay off once the dK/dV grid gives every CU a block (>= 128 blocks of 8
+// waves: the training step's B = 4 x 512 keys x 8 KV heads measured 22.16 ms
+// against 22.37 ms on the dS-GEMM path; config 2's 512 blocks 0.266 against
+// 0.327 ms); below that the two-kernel dS path keeps more blocks in flight.
 bool fa_bw_v4_preferred(const AttnShape &s) {
-    return fa_bw_v4_ok(s) && (long)s.n_batch * s.n_kv_heads * (s.n_kv / 128) >= 256;
+    return fa_bw_v4_ok(s) && (long)s.n_batch * s.n_kv_heads * (s.n_kv / 128) >= 128;
 }
 
 size_t fa_bw_ws_bytes(const AttnShape &s, bool v4) {
