@@ -52,6 +52,31 @@ def test_rmsnorm_forward_backward_fused_dw():
         assert rel_l2(dw_ref, dw) < 1e-5
 
 
+def test_rmsnorm_backward_scratch_shared_across_streams():
+    """The standalone entry points share one scratch buffer per device (gain
+    partials here); calls enqueued back to back on two streams, with no host
+    synchronisation between them, must each see their own partials."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import Stream
+
+    rows, dim = 2048, 1024
+    note("rmsnorm backward on two streams sharing the scratch")
+    s1, s2 = Stream(), Stream()
+    cases = []
+    for seed in (11, 21, 31, 41):
+        x, w = O.normal(rows * dim, seed), O.uniform(dim, seed + 1, 0.5, 1.5)
+        dy = O.normal(rows * dim, seed + 2)
+        cases.append((x, w, dy, O.rmsnorm_backward(dy, x, w, 1e-6)))
+    bufs = [(dev(x), dev(w), dev(dy), zeros(rows * dim), zeros(dim)) for x, w, dy, _ in cases]
+    for i, (bx, bw, bdy, bdx, bdw) in enumerate(bufs):
+        K.rmsnorm_backward(bdy, bx, bw, bdx, bdw, rows, dim, 1e-6, stream=(s1 if i % 2 else s2))
+    s1.synchronize()
+    s2.synchronize()
+    for (x, w, dy, (dx_ref, dw_ref)), (_, _, _, bdx, bdw) in zip(cases, bufs):
+        assert grel(dx_ref, host(bdx)) < 1e-5
+        assert rel_l2(dw_ref, host(bdw)) < 1e-5
+
+
 def test_swiglu_forward_backward():
     from valkyr_amd import kernels as K
 
