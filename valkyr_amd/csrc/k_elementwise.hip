@@ -204,9 +204,9 @@ VKH_DEV void adam4(f32x4 &p, const f32x4 &g, f32x4 &m, f32x4 &v, float lr, float
 }
 
 // Streaming update: every byte is touched once, so loads and stores are
-// non-temporal, and two grid-stride iterations are in flight per thread.
+// non-temporal, and ADAM_U grid-stride iterations are in flight per thread.
 // pb (optional): bf16 copy of the updated parameters (the GEMM operand shadow).
-constexpr int ADAM_GRID = 256 * 32;
+constexpr int ADAM_GRID = 256 * 32, ADAM_U = 2;  // 4 in flight measured no faster
 
 __global__ __launch_bounds__(NT) void adam_k(float *p_, const float *g_, float *m_, float *v_,
                                               bf16 *pb, size_t n, float lr, float b1, float b2,
@@ -217,10 +217,10 @@ __global__ __launch_bounds__(NT) void adam_k(float *p_, const float *g_, float *
           *v = reinterpret_cast<f32x4 *>(v_);
     const f32x4 *g = reinterpret_cast<const f32x4 *>(g_);
     size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x;
-    for (; i + stride < n4; i += 2 * stride) {
-        f32x4 pp[2], gg[2], mm[2], vv[2];
+    for (; i + (ADAM_U - 1) * stride < n4; i += ADAM_U * stride) {
+        f32x4 pp[ADAM_U], gg[ADAM_U], mm[ADAM_U], vv[ADAM_U];
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < ADAM_U; ++u) {
             const size_t j = i + u * stride;
             pp[u] = __builtin_nontemporal_load(&p[j]);
             gg[u] = __builtin_nontemporal_load(&g[j]);
@@ -228,7 +228,7 @@ __global__ __launch_bounds__(NT) void adam_k(float *p_, const float *g_, float *
             vv[u] = __builtin_nontemporal_load(&v[j]);
         }
 #pragma unroll
-        for (int u = 0; u < 2; ++u) {
+        for (int u = 0; u < ADAM_U; ++u) {
             const size_t j = i + u * stride;
             adam4(pp[u], gg[u], mm[u], vv[u], lr, b1, b2, eps, bc1, bc2, wd);
             __builtin_nontemporal_store(pp[u], &p[j]);
