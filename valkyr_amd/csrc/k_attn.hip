@@ -1072,16 +1072,13 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
 // store inside its tile loop: the tile DMA is then the only vector-memory
 // traffic there, and the waits for it can be counted exactly.
 //
-// Both run one wave per SIMD with 64 keys (dK/dV) or 64 queries (dQ) per
-// wave held in registers, so every MFMA operand fragment read from LDS feeds
-// four MFMAs: half the LDS bytes per flop of a 32-row wave tile.  The
-// accumulators (2 x 64 x 128 fp32 for dK/dV, 64 x 128 for dQ) live in AGPRs.
-
-#ifdef DKV4_SB
-#define DKV4_PHASE() __builtin_amdgcn_sched_barrier(0)
-#else
-#define DKV4_PHASE()
-#endif
+// Both are templates on the wave count NWV of a block.  NWV = 4: one wave
+// per SIMD with 64 keys (dK/dV) or 64 queries (dQ) per wave in registers, so
+// every MFMA operand fragment read from LDS feeds four MFMAs (half the LDS
+// bytes per flop of a 32-row wave tile), accumulators in AGPRs.  NWV = 8: two
+// waves per SIMD with 32 each, so one wave's softmax / dS arithmetic overlaps
+// the other wave's MFMAs; on MI355X the 8-wave forms are the faster ones and
+// are the ones launched.
 namespace dkv4 {
 constexpr int HD = 128, BM = 32, BN = 128;
 constexpr int DS = HD / 32, DSUB = HD / 16, QS = BM / 16;
@@ -1092,10 +1089,10 @@ constexpr int LDS = 128 * 1024;            // tile streams + V in the loop, the 
 static_assert(2 * STREAM + BN * HD * 2 <= LDS, "tile streams and V slices exceed the LDS arena");
 }  // namespace dkv4
 
-// dK / dV.  Block = 128 keys of one (sequence, KV head); 4 waves = 2 key
-// slices of 64 x 2 head groups.  Wave (slice, group) holds K and V of its 64
-// keys in VGPRs and, per 32-query tile of a head of its group (heads
-// kvh * hpk + group, + 2, ...), computes
+// dK / dV.  Block = 128 keys of one (sequence, KV head); NWV waves = NWV / 2
+// key slices x 2 head groups.  Wave (slice, group) holds K of its slice in
+// VGPRs (V of the block's keys sits in LDS) and, per 32-query tile of a head
+// of its group (heads kvh * hpk + group, + 2, ...), computes
 //   S = Q K^T, dP = dO V^T            (A = Q / dO rows from LDS, b128)
 //   P = exp2(S c - lse), dS = P (dP - D)
 //   dV^T += dO^T P, dK^T += Q^T dS    (A = transposing LDS reads)
@@ -1104,8 +1101,8 @@ static_assert(2 * STREAM + BN * HD * 2 <= LDS, "tile streams and V slices exceed
 // slice then sum their partial dK / dV through LDS: group 0 keeps dV and adds
 // group 1's, group 1 keeps dK and adds group 0's.
 // Each head group streams its Q / dO tiles through three LDS buffers (two
-// tiles in flight); the slice-0 wave moves Q and lse, the slice-1 wave dO and
-// D.  Tiles are visited from the last query down, heads inner, so the blocks
+// tiles in flight); the first half of the group's waves moves Q (and lse),
+// the second half dO (and D).  Tiles are visited from the last query down, heads inner, so the blocks
 // of one (sequence, KV head), which sit on one XCD, read a tile at about the
 // same time and share it in L2.  Under a causal mask the heaviest key blocks
 // (lowest keys) have the lowest block ids and start first.
