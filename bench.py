@@ -139,7 +139,7 @@ def bench_fa_bwd(args):
     d = DeviceBuffer(B * S * H * 4)
     dq, dk, dv = DeviceBuffer(nq * 4), DeviceBuffer(nk * 4), DeviceBuffer(nk * 4)
     p = K.attn_params(S, S, H, Hkv, hd, True, B, K.BF16)
-    ws = DeviceBuffer(max(K.fa_backward_workspace_bytes(p), 4))  # bf16 dS
+    ws = DeviceBuffer(max(K.fa_backward_workspace_bytes(p), 4))  # bf16 dS if the shape needs it
     s = Stream()
     K.fa_forward(p, q, k, vv, o, lse, stream=s)  # O and LSE of the same inputs
     K.cast_f32_to_bf16(o, o16, nq, stream=s)
