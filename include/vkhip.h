@@ -15,7 +15,10 @@
  *   - Streams: `vkh_stream` is a `hipStream_t` (NULL = the runner's own
  *     stream for runner calls, the null stream for kernel calls).  Kernel
  *     entry points only enqueue; runner `step`/`forward_logits`/checkpoint
- *     calls are blocking like the reference's.
+ *     calls are blocking like the reference's.  A runner orders its own work
+ *     across streams: work enqueued on a caller stream (step_async,
+ *     tick_frame_train) completes before any later runner call reads or
+ *     writes the same memory, on any stream or from the host.
  *   - Layout: weights are [N, K] row-major with y = x W^T; activations are
  *     [T, dim] with T = n_seqs * n_pos rows; Q, O, dO are [T, n_heads, head_dim]
  *     and K, V are [T, n_kv_heads, head_dim]; LSE and D are [T, n_heads].
@@ -204,6 +207,19 @@ vkh_status vkh_runner_get_config(const vkh_runner *r, vkh_config *out);
 size_t vkh_runner_param_count(const vkh_runner *r);          /* trainable params */
 size_t vkh_runner_device_bytes(const vkh_runner *r);
 
+/* Which attention-backward kernels the runner's step uses (fixed at create
+ * from the shape and precision): the recompute MFMA kernels (bf16, head_dim
+ * 128, an even GQA group, n_pos a multiple of 128 and at least 128 key blocks
+ * of 128), the MFMA kernels with a bf16 dS workspace (other bf16 shapes with
+ * n_pos a multiple of 64), or the per-row kernels (fp32 precision and the
+ * remaining shapes). */
+typedef enum vkh_attn_bw_path {
+    VKH_ATTN_BW_ROWWISE = 0,
+    VKH_ATTN_BW_DS_GEMM = 1,
+    VKH_ATTN_BW_RECOMPUTE = 2
+} vkh_attn_bw_path;
+uint32_t vkh_runner_attention_backward_path(const vkh_runner *r);
+
 /* Tensor access (host <-> device copies, blocking). */
 vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int which,
                                    size_t *numel);
@@ -216,13 +232,33 @@ vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int 
                                         float **dptr, size_t *numel);
 
 /* Checkpoints, byte layout of transformer.zig:157-205, :1390-1655:
- * 16-byte header {magic, version 1, step_t, cfg_size} + config bytes +
- * positional fp32 blobs (.vkpt: (param, m, v) per tensor in collectBlobs
- * order; .lvkpt: (A, mA, vA, B, mB, vB) per enabled projection and layer). */
+ * 16-byte header {magic, version 1, step_t, cfg_size = 80} + the 80 bytes of
+ * the reference's `Config` (VKH_CHECKPOINT_CONFIG_BYTES, see
+ * vkh_checkpoint_config_encode) + positional fp32 blobs (.vkpt: (param, m, v)
+ * per tensor in collectBlobs order, lm_head included: a tied runner writes
+ * its embedding's blobs there and loads only files whose lm_head equals the
+ * embedding; .lvkpt: (A, mA, vA, B, mB, vB) per enabled projection and
+ * layer).  Loading compares the shape fields of cfgShapeMatches
+ * (transformer.zig:197-205) and restores step_t, lr, beta1, beta2, eps_adam
+ * (and lora_alpha, lora_lr_b_scale from .lvkpt). */
 vkh_status vkh_runner_save_checkpoint(vkh_runner *r, const char *path);
 vkh_status vkh_runner_load_checkpoint(vkh_runner *r, const char *path);
 vkh_status vkh_runner_save_lora_checkpoint(vkh_runner *r, const char *path);
 vkh_status vkh_runner_load_lora_checkpoint(vkh_runner *r, const char *path);
+
+/* The checkpoint config block: std.mem.asBytes(&cfg) of the reference's
+ * auto-layout `Config` (transformer.zig:31-77), fields ordered by descending
+ * alignment with declaration order kept among equals: offsets 0-28 dim,
+ * n_heads, n_kv_heads, head_dim, ff_dim, n_pos, n_layers, vocab_size (u32);
+ * 32 rms_eps (f32); 36 rotary_dim (u32); 40 rope_theta, 44 lr, 48 beta1,
+ * 52 beta2, 56 eps_adam (f32); 60 lora_targets, 64 lora_rank (u32);
+ * 68 lora_alpha, 72 lora_lr_b_scale (f32); 76 causal, 77 qk_norm (bool, one
+ * byte); 78-79 padding (written as zero).  Host-only: no device work.
+ * decode fills the reference's fields and sets the extensions to n_seqs = 1,
+ * untied, fp32 precision. */
+#define VKH_CHECKPOINT_CONFIG_BYTES 80
+vkh_status vkh_checkpoint_config_encode(const vkh_config *cfg, void *out, size_t out_len);
+vkh_status vkh_checkpoint_config_decode(const void *in, size_t in_len, vkh_config *out);
 
 /* ── cooperative per-frame API (shape of runner.zig:129-176, :904-986) ── */
 typedef enum vkh_budget_mode {
@@ -253,8 +289,13 @@ vkh_status vkh_runner_upload_train_batch(vkh_runner *r, const uint32_t *token_id
  * (target <= 0 disables). */
 vkh_status vkh_runner_set_loss_target(vkh_runner *r, float target);
 /* runner.zig:904 tickFrameTrain: enqueue up to the budget of steps on the
- * caller's stream and return without waiting; the loss of the previous tick
- * is reported once its copy has landed. */
+ * caller's stream and return without waiting; the loss staged by an earlier
+ * tick is reported once its copy has landed.  A budget of 0 steps or 0 us
+ * returns idle with the cached loss (runner.zig:924-926); an unknown mode is
+ * VKH_ERR_INVALID_ARGUMENT.  With a loss target (> 0), a tick whose cached
+ * loss is <= target is idle (no steps) and every tick enqueues a fresh loss
+ * evaluation (forward + CE) of the staged batch, so a newly uploaded batch
+ * above the target resumes training (runner.zig:948-973). */
 vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
                                        vkh_train_budget budget, vkh_tick_result *out);
 

@@ -59,6 +59,8 @@ def _declare(L):
         f.restype = res
         f.argtypes = list(args)
 
+    d("orc_set_threads", None, C.c_int)
+    d("orc_get_threads", C.c_int)
     d("orc_fill_normal", None, F32P, SZ, C.c_uint64, C.c_float, C.c_float)
     d("orc_fill_uniform", None, F32P, SZ, C.c_uint64, C.c_float, C.c_float)
     d("orc_fill_ids", None, U32P, SZ, C.c_uint64, C.c_uint32)
@@ -107,6 +109,7 @@ def _declare(L):
     d("orc_model_adam", None, C.c_void_p)
     d("orc_model_step", C.c_float, C.c_void_p, U32P, U32P)
     d("orc_model_step_t", C.c_uint32, C.c_void_p)
+    d("orc_model_set_step_t", None, C.c_void_p, C.c_uint32)
     d("orc_model_forward_logits", None, C.c_void_p, U32P, F32P)
     d("orc_now_seconds", C.c_double)
     U64P = np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")
@@ -133,6 +136,16 @@ def _ptr(a):
 
 
 # ── array helpers ────────────────────────────────────────────────────────
+
+def set_threads(n: int) -> None:
+    """OpenMP threads of the oracle's parallel loops (results are identical
+    for every thread count: only independent outputs run in parallel)."""
+    lib().orc_set_threads(int(n))
+
+
+def get_threads() -> int:
+    return int(lib().orc_get_threads())
+
 
 def normal(n, seed, std=1.0, mean=0.0):
     x = np.empty(int(n), np.float32)
@@ -409,6 +422,10 @@ class Model:
     @property
     def step_t(self):
         return lib().orc_model_step_t(self._h)
+
+    @step_t.setter
+    def step_t(self, t):
+        lib().orc_model_set_step_t(self._h, int(t))
 
     def forward_logits(self, tokens):
         out = np.empty(self.T * self.cfg.vocab_size, np.float32)

@@ -10,8 +10,32 @@
 #include <stdlib.h>
 #include <string.h>
 #include <time.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
 
 #define NEG_INF (-INFINITY)
+
+/* ── threads ───────────────────────────────────────────────────────────────
+ * Parallel loops run only over outputs that are independent of each other,
+ * and every accumulation keeps the sequential loop's order, so any thread
+ * count gives bit-identical results. */
+
+void orc_set_threads(int n) {
+#ifdef _OPENMP
+    omp_set_num_threads(n > 0 ? n : 1);
+#else
+    (void)n;
+#endif
+}
+
+int orc_get_threads(void) {
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
 
 /* ── generator ─────────────────────────────────────────────────────────── */
 
@@ -26,9 +50,15 @@ static double u01(uint64_t *s) { /* (0, 1) exclusive of 0 */
     return ((double)(orc_splitmix64(s) >> 11) + 0.5) * (1.0 / 9007199254740992.0);
 }
 
+/* The j-th draw (0-based) of a SplitMix64 stream started at `seed` is the
+ * mix of seed + (j + 1) * gamma, so the Box-Muller pairs can be formed in
+ * any order: the values are those of the sequential stream. */
 void orc_fill_normal(float *x, size_t n, uint64_t seed, float mean, float stddev) {
-    uint64_t s = seed;
-    for (size_t i = 0; i < n; i += 2) {
+    const long long npairs = (long long)((n + 1) / 2);
+#pragma omp parallel for schedule(static)
+    for (long long p = 0; p < npairs; ++p) {
+        const size_t i = 2 * (size_t)p;
+        uint64_t s = seed + 0x9E3779B97F4A7C15ull * (uint64_t)i;
         double u1 = u01(&s), u2 = u01(&s);
         double r = sqrt(-2.0 * log(u1));
         double a = 6.283185307179586 * u2;
@@ -314,14 +344,20 @@ void orc_flash_attention_forward(const float *Q, const float *K, const float *V,
                                  size_t Br, size_t Bc, float *out, float *lse) {
     size_t hpk = n_heads / n_kv_heads;
     float inv_sqrt_d = 1.0f / sqrtf((float)head_dim);
+    /* every (query block, head) is independent: parallel over them */
+    const long long n_qb = (long long)((n_q + Br - 1) / Br), n_work = n_qb * (long long)n_heads;
+#pragma omp parallel
+    {
     float *s_tile = malloc(Br * Bc * sizeof(float));
     float *p_tile = malloc(Br * Bc * sizeof(float));
     float *o_acc = malloc(Br * head_dim * sizeof(float));
     float *m_acc = malloc(Br * sizeof(float));
     float *l_acc = malloc(Br * sizeof(float));
-    for (size_t qb = 0; qb < n_q; qb += Br) {
+#pragma omp for schedule(dynamic, 1)
+    for (long long wi = 0; wi < n_work; ++wi) {
+        const size_t qb = (size_t)(wi / (long long)n_heads) * Br, h = (size_t)(wi % (long long)n_heads);
         size_t qe = qb + Br < n_q ? qb + Br : n_q, qlen = qe - qb;
-        for (size_t h = 0; h < n_heads; ++h) {
+        {
             size_t kv_h = h / hpk;
             for (size_t qi = 0; qi < qlen; ++qi) { m_acc[qi] = NEG_INF; l_acc[qi] = 0.0f; }
             for (size_t i = 0; i < qlen * head_dim; ++i) o_acc[i] = 0.0f;
@@ -375,6 +411,7 @@ void orc_flash_attention_forward(const float *Q, const float *K, const float *V,
         }
     }
     free(s_tile); free(p_tile); free(o_acc); free(m_acc); free(l_acc);
+    }
 }
 
 void orc_flash_attention_backward(const float *Q, const float *K, const float *V,
@@ -387,9 +424,13 @@ void orc_flash_attention_backward(const float *Q, const float *K, const float *V
     memset(dQ, 0, n_q * n_heads * head_dim * sizeof(float));
     memset(dK, 0, n_kv * n_kv_heads * head_dim * sizeof(float));
     memset(dV, 0, n_kv * n_kv_heads * head_dim * sizeof(float));
+    /* The KV heads are independent.  Within one, dK / dV rows take their
+     * terms in the sequential loop's order (q ascending, then the group's
+     * heads ascending), and dQ[q, h] its terms k ascending. */
+#pragma omp parallel for schedule(static, 1)
+    for (size_t kv_h = 0; kv_h < n_kv_heads; ++kv_h)
     for (size_t q = 0; q < n_q; ++q)
-        for (size_t h = 0; h < n_heads; ++h) {
-            size_t kv_h = h / hpk;
+        for (size_t h = kv_h * hpk; h < (kv_h + 1) * hpk; ++h) {
             size_t o_off = q * n_heads * head_dim + h * head_dim;
             float lse_qh = lse[q * n_heads + h];
             if (lse_qh == NEG_INF) continue;
@@ -432,134 +473,194 @@ void orc_fa_bw_d(const float *O, const float *dO, size_t n_q, size_t n_heads,
 
 void orc_matmul_nt(float *out, const float *x, const float *W, size_t M, size_t N,
                    size_t K) {
-    for (size_t m = 0; m < M; ++m) {
-        const float *xr = x + m * K;
-        for (size_t n = 0; n < N; ++n) {
-            const float *wr = W + n * K;
-            float acc = 0;
-            for (size_t k = 0; k < K; ++k) acc += xr[k] * wr[k];
-            out[m * N + n] = acc;
-        }
+    /* every output is its own fp32 k-ascending sum: parallel over outputs */
+    const long long MN = (long long)M * (long long)N;
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < MN; ++i) {
+        const size_t m = (size_t)i / N, n = (size_t)i % N;
+        const float *xr = x + m * K, *wr = W + n * K;
+        float acc = 0;
+        for (size_t k = 0; k < K; ++k) acc += xr[k] * wr[k];
+        out[m * N + n] = acc;
     }
 }
 
 void orc_linear_backward(const float *dout, const float *x, const float *W, size_t M,
                          size_t N, size_t K, float *dx, float *dW) {
     if (dx) {
-        /* dx[m,k] = sum_n dout[m,n] W[n,k]; fp64 per output, n ascending. */
-        double *acc = malloc(K * sizeof(double));
-        for (size_t m = 0; m < M; ++m) {
-            for (size_t k = 0; k < K; ++k) acc[k] = 0;
-            for (size_t n = 0; n < N; ++n) {
-                double g = dout[m * N + n];
-                const float *wr = W + n * K;
-                for (size_t k = 0; k < K; ++k) acc[k] += g * (double)wr[k];
+        /* dx[m,k] = sum_n dout[m,n] W[n,k]; fp64 per output, n ascending
+         * (rows of dx are independent). */
+#pragma omp parallel
+        {
+            double *acc = malloc(K * sizeof(double));
+#pragma omp for schedule(static)
+            for (size_t m = 0; m < M; ++m) {
+                for (size_t k = 0; k < K; ++k) acc[k] = 0;
+                for (size_t n = 0; n < N; ++n) {
+                    double g = dout[m * N + n];
+                    const float *wr = W + n * K;
+                    for (size_t k = 0; k < K; ++k) acc[k] += g * (double)wr[k];
+                }
+                for (size_t k = 0; k < K; ++k) dx[m * K + k] = (float)acc[k];
             }
-            for (size_t k = 0; k < K; ++k) dx[m * K + k] = (float)acc[k];
+            free(acc);
         }
-        free(acc);
     }
     if (dW) {
-        /* dW[n,k] += sum_m dout[m,n] x[m,k]; fp64 per output, m ascending. */
-        double *acc = malloc(K * sizeof(double));
-        for (size_t n = 0; n < N; ++n) {
-            for (size_t k = 0; k < K; ++k) acc[k] = 0;
-            for (size_t m = 0; m < M; ++m) {
-                double g = dout[m * N + n];
-                const float *xr = x + m * K;
-                for (size_t k = 0; k < K; ++k) acc[k] += g * (double)xr[k];
+        /* dW[n,k] += sum_m dout[m,n] x[m,k]; fp64 per output, m ascending
+         * (rows of dW are independent). */
+#pragma omp parallel
+        {
+            double *acc = malloc(K * sizeof(double));
+#pragma omp for schedule(static)
+            for (size_t n = 0; n < N; ++n) {
+                for (size_t k = 0; k < K; ++k) acc[k] = 0;
+                for (size_t m = 0; m < M; ++m) {
+                    double g = dout[m * N + n];
+                    const float *xr = x + m * K;
+                    for (size_t k = 0; k < K; ++k) acc[k] += g * (double)xr[k];
+                }
+                for (size_t k = 0; k < K; ++k) dW[n * K + k] += (float)acc[k];
             }
-            for (size_t k = 0; k < K; ++k) dW[n * K + k] += (float)acc[k];
+            free(acc);
         }
-        free(acc);
     }
 }
 
 /* ── cut cross-entropy: src/cpu/cce.zig:89-268 ─────────────────────────── */
 
+/* Rows are taken CCE_RB at a time; the logits of a block are formed vocab
+ * row by vocab row (z_t[v * nr + r], each an fp64 dot rounded to fp32 as in
+ * cce.zig), so the head matrix streams once per block.  The per-row online
+ * softmax then walks the chunks exactly as cce.zig does. */
+#define CCE_RB 32
+
+static void cce_logits_block(const float *h, const float *w_lm, size_t r0, size_t nr,
+                             size_t vocab, size_t dim, float *z_t) {
+#pragma omp parallel for schedule(static)
+    for (size_t v = 0; v < vocab; ++v) {
+        const float *wr = w_lm + v * dim;
+        for (size_t r = 0; r < nr; ++r) {
+            const float *hr = h + (r0 + r) * dim;
+            double s = 0;
+            for (size_t k = 0; k < dim; ++k) s += (double)hr[k] * (double)wr[k];
+            z_t[v * nr + r] = (float)s;
+        }
+    }
+}
+
 float orc_cce_forward(const float *h, const float *w_lm, const uint32_t *tgt, size_t n,
                       size_t vocab, size_t dim, size_t chunk, float z_loss_scale,
                       float label_smoothing, float *lse_out, float *loss_row_out) {
-    double total_loss = 0;
     float eps = label_smoothing;
     float t_scale = 1.0f - eps;
-    float *z = malloc(chunk * sizeof(float));
-    for (size_t row = 0; row < n; ++row) {
-        const float *hr = h + row * dim;
-        float m = NEG_INF;
-        double d_acc = 0, z_sum = 0;
-        float z_target = 0;
-        size_t t = tgt[row];
-        for (size_t c0 = 0; c0 < vocab; c0 += chunk) {
-            size_t c1 = c0 + chunk < vocab ? c0 + chunk : vocab, len = c1 - c0;
-            float chunk_max = NEG_INF;
-            for (size_t o = 0; o < len; ++o) {
-                const float *wr = w_lm + (c0 + o) * dim;
-                double s = 0;
-                for (size_t k = 0; k < dim; ++k) s += (double)hr[k] * (double)wr[k];
-                float zi = (float)s;
-                z[o] = zi;
-                if (zi > chunk_max) chunk_max = zi;
-                z_sum += (double)zi;
+    float *z_t = malloc((size_t)CCE_RB * vocab * sizeof(float));
+    double *row_loss = malloc(n * sizeof(double));
+    for (size_t r0 = 0; r0 < n; r0 += CCE_RB) {
+        const size_t nr = r0 + CCE_RB < n ? CCE_RB : n - r0;
+        cce_logits_block(h, w_lm, r0, nr, vocab, dim, z_t);
+#pragma omp parallel for schedule(static)
+        for (size_t r = 0; r < nr; ++r) {
+            const size_t row = r0 + r;
+            float m = NEG_INF;
+            double d_acc = 0, z_sum = 0;
+            float z_target = 0;
+            size_t t = tgt[row];
+            for (size_t c0 = 0; c0 < vocab; c0 += chunk) {
+                size_t c1 = c0 + chunk < vocab ? c0 + chunk : vocab;
+                float chunk_max = NEG_INF;
+                for (size_t v = c0; v < c1; ++v) {
+                    float zi = z_t[v * nr + r];
+                    if (zi > chunk_max) chunk_max = zi;
+                    z_sum += (double)zi;
+                }
+                float m_new = m > chunk_max ? m : chunk_max;
+                double chunk_sum = 0;
+                for (size_t v = c0; v < c1; ++v) chunk_sum += exp((double)z_t[v * nr + r] - (double)m_new);
+                double rescale = isinf(m) ? 0.0 : exp((double)m - (double)m_new);
+                d_acc = d_acc * rescale + chunk_sum;
+                m = m_new;
+                if (t >= c0 && t < c1) z_target = z_t[t * nr + r];
             }
-            float m_new = m > chunk_max ? m : chunk_max;
-            double chunk_sum = 0;
-            for (size_t o = 0; o < len; ++o) chunk_sum += exp((double)z[o] - (double)m_new);
-            double rescale = isinf(m) ? 0.0 : exp((double)m - (double)m_new);
-            d_acc = d_acc * rescale + chunk_sum;
-            m = m_new;
-            if (t >= c0 && t < c1) z_target = z[t - c0];
+            float lse = (float)(log(d_acc) + (double)m);
+            lse_out[row] = lse;
+            double z_mean = z_sum / (double)vocab;
+            double ce = (double)lse - (double)t_scale * (double)z_target - (double)eps * z_mean;
+            double zp = (double)z_loss_scale * (double)lse * (double)lse;
+            if (loss_row_out) loss_row_out[row] = (float)(ce + zp);
+            row_loss[row] = ce + zp;
         }
-        float lse = (float)(log(d_acc) + (double)m);
-        lse_out[row] = lse;
-        double z_mean = z_sum / (double)vocab;
-        double ce = (double)lse - (double)t_scale * (double)z_target - (double)eps * z_mean;
-        double zp = (double)z_loss_scale * (double)lse * (double)lse;
-        if (loss_row_out) loss_row_out[row] = (float)(ce + zp);
-        total_loss += ce + zp;
     }
-    free(z);
+    double total_loss = 0;
+    for (size_t row = 0; row < n; ++row) total_loss += row_loss[row];
+    free(z_t);
+    free(row_loss);
     return (float)(total_loss / (double)n);
 }
 
+/* dh[row, :] accumulates dz * W[v, :] with v ascending and dW[v, :]
+ * accumulates dz * h[row, :] with rows ascending, in fp32, as cce.zig's
+ * row-by-row loop does; the block structure only changes which of these
+ * independent sums is advanced when. */
 void orc_cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
                       const float *lse, size_t n, size_t vocab, size_t dim, size_t chunk,
                       float z_loss_scale, float label_smoothing, float *d_h, float *dW) {
+    (void)chunk; /* the chunking of cce.zig does not change any value here */
     memset(d_h, 0, n * dim * sizeof(float));
     float inv_n = 1.0f / (float)n;
     float eps = label_smoothing;
     float eps_over_v = eps / (float)vocab;
     float t_scale = 1.0f - eps;
-    float *z = malloc(chunk * sizeof(float));
-    for (size_t row = 0; row < n; ++row) {
-        const float *hr = h + row * dim;
-        float *dhr = d_h + row * dim;
-        float lse_row = lse[row];
-        size_t t = tgt[row];
-        float softmax_factor = 1.0f + 2.0f * z_loss_scale * lse_row;
-        for (size_t c0 = 0; c0 < vocab; c0 += chunk) {
-            size_t c1 = c0 + chunk < vocab ? c0 + chunk : vocab, len = c1 - c0;
-            for (size_t o = 0; o < len; ++o) {
-                const float *wr = w_lm + (c0 + o) * dim;
-                double s = 0;
-                for (size_t k = 0; k < dim; ++k) s += (double)hr[k] * (double)wr[k];
-                z[o] = (float)s;
+    float *z_t = malloc((size_t)CCE_RB * vocab * sizeof(float));
+    for (size_t r0 = 0; r0 < n; r0 += CCE_RB) {
+        const size_t nr = r0 + CCE_RB < n ? CCE_RB : n - r0;
+        cce_logits_block(h, w_lm, r0, nr, vocab, dim, z_t);
+        /* z -> dz in place */
+#pragma omp parallel for schedule(static)
+        for (size_t v = 0; v < vocab; ++v)
+            for (size_t r = 0; r < nr; ++r) {
+                const size_t row = r0 + r;
+                float lse_row = lse[row];
+                float softmax_factor = 1.0f + 2.0f * z_loss_scale * lse_row;
+                float p = (float)exp((double)z_t[v * nr + r] - (double)lse_row);
+                float ti = (v == tgt[row]) ? t_scale : 0.0f;
+                z_t[v * nr + r] = (softmax_factor * p - ti - eps_over_v) * inv_n;
             }
-            for (size_t o = 0; o < len; ++o) {
-                size_t vi = c0 + o;
-                float p = (float)exp((double)z[o] - (double)lse_row);
-                float ti = (vi == t) ? t_scale : 0.0f;
-                float dz = (softmax_factor * p - ti - eps_over_v) * inv_n;
-                const float *wr = w_lm + vi * dim;
-                float *dwr = dW ? dW + vi * dim : NULL;
-                for (size_t k = 0; k < dim; ++k) {
-                    dhr[k] += dz * wr[k];
-                    if (dwr) dwr[k] += dz * hr[k];
+        /* dh: each thread owns whole rows and walks the vocabulary in tiles
+         * of 64 head rows (reused from cache by all its rows) */
+#pragma omp parallel
+        {
+            size_t ra = 0, rb = nr;
+#ifdef _OPENMP
+            const size_t nt = (size_t)omp_get_num_threads(), ti = (size_t)omp_get_thread_num();
+            ra = nr * ti / nt;
+            rb = nr * (ti + 1) / nt;
+#endif
+            for (size_t v0 = 0; v0 < vocab && ra < rb; v0 += 64) {
+                const size_t v1 = v0 + 64 < vocab ? v0 + 64 : vocab;
+                for (size_t r = ra; r < rb; ++r) {
+                    float *dhr = d_h + (r0 + r) * dim;
+                    for (size_t v = v0; v < v1; ++v) {
+                        const float dz = z_t[v * nr + r];
+                        const float *wr = w_lm + v * dim;
+                        for (size_t k = 0; k < dim; ++k) dhr[k] += dz * wr[k];
+                    }
+                }
+            }
+        }
+        if (dW) {
+#pragma omp parallel for schedule(static)
+            for (size_t v = 0; v < vocab; ++v) {
+                float *dwr = dW + v * dim;
+                for (size_t r = 0; r < nr; ++r) {
+                    const float dz = z_t[v * nr + r];
+                    const float *hr = h + (r0 + r) * dim;
+                    for (size_t k = 0; k < dim; ++k) dwr[k] += dz * hr[k];
                 }
             }
         }
     }
-    free(z);
+    free(z_t);
 }
 
 float orc_softmax_ce_loss(const float *logits, const uint32_t *tgt, size_t n_pos,
@@ -670,6 +771,7 @@ void orc_adam_step(float *param, const float *grad, float *m, float *v, size_t n
     float t_f = (float)t;
     float bc1 = 1.0f - powf(beta1, t_f);
     float bc2 = 1.0f - powf(beta2, t_f);
+#pragma omp parallel for schedule(static)
     for (size_t i = 0; i < n; ++i) {
         float g = grad[i];
         float nm = beta1 * m[i] + (1.0f - beta1) * g;
@@ -847,6 +949,9 @@ float *orc_model_tensor(orc_model *m, int kind, int layer, int which, size_t *nu
 }
 
 uint32_t orc_model_step_t(const orc_model *m) { return m->step_t; }
+
+/* step_t as a checkpoint restores it (transformer.zig:1444) */
+void orc_model_set_step_t(orc_model *m, uint32_t t) { m->step_t = t; }
 
 void orc_model_init_random(orc_model *m, uint64_t seed, float std, float lora_std) {
     const orc_model_config *c = &m->cfg;

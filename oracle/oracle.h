@@ -38,6 +38,11 @@
 extern "C" {
 #endif
 
+/* ── threads (OpenMP over independent outputs; results do not depend on the
+ * thread count) ─────────────────────────────────────────────────────────── */
+void orc_set_threads(int n);
+int orc_get_threads(void);
+
 /* ── seeded generator (SplitMix64 + Box-Muller) ─────────────────────────── */
 uint64_t orc_splitmix64(uint64_t *state);
 void orc_fill_normal(float *x, size_t n, uint64_t seed, float mean, float stddev);
@@ -172,6 +177,7 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
 void orc_model_adam(orc_model *m);
 float orc_model_step(orc_model *m, const uint32_t *tokens, const uint32_t *targets);
 uint32_t orc_model_step_t(const orc_model *m);
+void orc_model_set_step_t(orc_model *m, uint32_t t);
 /* forward only: logits [T, vocab] (runner forwardLogits). */
 void orc_model_forward_logits(orc_model *m, const uint32_t *tokens, float *logits);
 

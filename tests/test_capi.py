@@ -118,3 +118,42 @@ def test_mlp_config_checks_before_device():
     assert abs(c.init_scale - 0.3) < 1e-7 and abs(c.adam_beta1 - 0.9) < 1e-7
     assert abs(c.adam_beta2 - 0.999) < 1e-7 and abs(c.adam_eps - 1e-8) < 1e-15
     assert c.weight_decay == 0.0
+
+
+def test_checkpoint_config_block_layout():
+    """The .vkpt / .lvkpt config block is the reference's `Config` as bytes
+    (transformer.zig:31-77, :1405-1406): an auto-layout Zig struct, so its
+    nineteen 4-byte fields in declaration order, then causal and qk_norm as
+    one byte each, then two bytes of padding (80 bytes).  Checked against a
+    block packed here field by field, both ways."""
+    import struct
+
+    import valkyr_amd as v
+    from valkyr_amd.runner import checkpoint_config_bytes, checkpoint_config_from_bytes
+
+    cfg = v.make_config(dim=1024, n_heads=16, n_kv_heads=8, head_dim=128, ff_dim=3072, n_pos=512,
+                        n_layers=28, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=96,
+                        rope_theta=1e6, qk_norm=1, lr=3e-4, beta1=0.85, beta2=0.995,
+                        eps_adam=1e-7, lora_targets=0x15, lora_rank=8, lora_alpha=16.0,
+                        lora_lr_b_scale=4.0, n_seqs=4, tied_embeddings=1, precision=1)
+    fields = (1024, 16, 8, 128, 3072, 512, 28, 151936, 1e-6, 96, 1e6, 3e-4, 0.85, 0.995, 1e-7,
+              0x15, 8, 16.0, 4.0, 1, 1)
+    want = struct.pack("<8If If 4f 2I 2f 2B 2x", *fields)
+    assert len(want) == 80
+    assert checkpoint_config_bytes(cfg) == want
+    back = checkpoint_config_from_bytes(want)
+    for name in ("dim", "n_heads", "n_kv_heads", "head_dim", "ff_dim", "n_pos", "n_layers",
+                 "vocab_size", "rotary_dim", "lora_targets", "lora_rank", "causal", "qk_norm"):
+        assert getattr(back, name) == getattr(cfg, name), name
+    for name in ("rms_eps", "rope_theta", "lr", "beta1", "beta2", "eps_adam", "lora_alpha",
+                 "lora_lr_b_scale"):
+        assert getattr(back, name) == getattr(cfg, name), name
+    # the extensions are not in the reference's block
+    assert (back.n_seqs, back.tied_embeddings, back.precision) == (1, 0, 0)
+    # bool bytes: causal off, qk_norm off
+    off = struct.pack("<8If If 4f 2I 2f 2B 2x", *(fields[:19] + (0, 0)))
+    c2 = checkpoint_config_from_bytes(off)
+    assert c2.causal == 0 and c2.qk_norm == 0
+    with pytest.raises(v.VkhError) as e:
+        checkpoint_config_from_bytes(want + b"\0\0\0\0")
+    assert e.value.name == "CheckpointConfigSizeMismatch"

@@ -1,9 +1,15 @@
-"""The metric's configs 4 and 5 at full size through the C ABI, held to the
-size-independent properties those shapes allow (no oracle runs at this size):
+"""The metric's configs 3, 4 and 5 at full size through the C ABI, held to the
+size-independent properties those shapes allow (no oracle runs at this size;
+config 3's widths are held to the oracle at 2 layers in test_gpu_runner.py):
 
 * the loss of a random init: after the unit-gain final RMSNorm every logit of
   a N(0, s^2) head is N(0, D s^2), so the mean CE is ln V + D s^2 / 2 up to the
   target logits' sampling noise, std sqrt(D s^2 / T);
+* config 3 (Qwen3-0.6B shape, 4 x 512, 28 layers, tied 151936 vocabulary):
+  the step takes the recompute attention backward, gradients of sampled
+  tensors are finite and non-zero, the bf16-operand gradients agree with the
+  fp32-precision runner's on the same weights, and the loss falls over
+  repeated steps on one batch;
 * config 4 (Qwen3-4B shape, LoRA r16 on q/k/v/o, frozen base): at step 1
   B = 0 makes every dA exactly zero (lora.zig:449-505), dB is live, and A and
   the frozen base weights are unchanged bit for bit after the update;
@@ -25,6 +31,8 @@ pytestmark = pytest.mark.gpu
 BASE = dict(head_dim=128, n_heads=32, n_kv_heads=8, vocab_size=151936, rms_eps=1e-6, causal=1,
             rotary_dim=128, rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999,
             eps_adam=1e-8, n_seqs=1)
+CONFIG3 = dict(BASE, n_heads=16, dim=1024, ff_dim=3072, n_pos=512, n_seqs=4, n_layers=28,
+               tied_embeddings=1)
 CONFIG4 = dict(BASE, dim=2560, ff_dim=9728, n_pos=2048, n_layers=36, tied_embeddings=1,
                lora_targets=0xF, lora_rank=16, lora_alpha=32.0, lora_lr_b_scale=1.0)
 CONFIG5 = dict(BASE, dim=4096, ff_dim=12288, n_pos=8192, n_layers=36, tied_embeddings=0)
@@ -37,11 +45,11 @@ def _gpu():
     assert v.device_count() > 0, "no GPU visible"
 
 
-def runner(c):
+def runner(c, precision=1):
     import valkyr_amd as v
 
     try:
-        r = v.Runner(v.make_config(**c, precision=1))
+        r = v.Runner(v.make_config(**c, precision=precision))
     except v.VkhError as e:
         if e.name == "OutOfMemory":
             pytest.skip(f"not enough device memory: {e.message}")
@@ -62,6 +70,39 @@ def loss_closed_form_ok(c, loss):
     want = math.log(c["vocab_size"]) + var / 2
     note(f"  loss {loss:.4f}, closed form {want:.4f} +- {math.sqrt(var / T):.4f}")
     return abs(loss - want) < 4 * math.sqrt(var / T) + 0.01
+
+
+def test_config3_qwen3_06b_full_size():
+    from helpers import rel_l2
+    from valkyr_amd.runner import DOWN, GATE, GRAD, K, N1, N2, O, Q, Q_NORM, UP
+
+    c = CONFIG3
+    note("config 3 full size: Qwen3-0.6B shape, 4 x 512, 28 layers, tied vocabulary")
+    sampled = [(-1, 0), (-1, 1), (0, Q), (0, N1), (0, DOWN), (9, K), (13, N2), (13, UP),
+               (20, Q_NORM), (27, O), (27, GATE)]
+    tok, tgt = batch(c, 3)
+    with runner(c) as r:
+        assert r.param_count() == 596_049_920
+        assert r.attention_backward_path() == "recompute"
+        loss = r.forward_backward(tok, tgt)  # first-step gradients, no update
+        assert loss_closed_form_ok(c, loss)
+        g16 = {k: r.get(GRAD, *k) for k in sampled}
+        for k, g in g16.items():
+            assert np.isfinite(g).all() and g.any(), k
+        with runner(c, precision=0) as r32:  # same seed: same fp32 weights
+            loss32 = r32.forward_backward(tok, tgt)
+            note(f"  first-step loss bf16 {loss:.5f}, fp32 {loss32:.5f}")
+            assert abs(loss - loss32) < 1e-3 * loss32
+            errs = {k: rel_l2(r32.get(GRAD, *k), g16[k]) for k in sampled}
+        note("  bf16 vs fp32 gradient rel-L2: " + ", ".join(f"{k}: {e:.2e}" for k, e in errs.items()))
+        assert max(errs.values()) < 5e-2, errs
+        losses = []
+        for _ in range(4):
+            r.step(tok, tgt)
+            losses.append(r.last_loss())
+        note(f"  losses over 4 steps on one batch: {losses}")
+        assert all(np.isfinite(losses)) and losses[-1] < losses[0] and losses[0] == loss
+        assert r.step_t == 5
 
 
 def test_config4_qwen3_4b_lora_first_step():

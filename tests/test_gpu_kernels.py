@@ -489,3 +489,28 @@ def test_flash_attention_bf16_full_size_invariants():
         dd = (pr * dp).sum()
         dq_ref = sc * ((pr * (dp - dd)) @ k5[b, :qi + 1, kv])
         assert rel_l2(dq_ref, dq.reshape(B, S, H, hd)[b, qi, h]) < 1e-2
+    # closed-form dK / dV rows at sampled keys (a key-row permutation or a row
+    # written to the wrong key would pass the sums above):
+    #   dV[j] = sum_{h in group} sum_{q >= j} P[q, j] dO[q, h]
+    #   dK[j] = sc sum_{h in group} sum_{q >= j} P[q, j] (dP[q, j] - D[q, h]) Q[q, h]
+    dk5 = dk.reshape(B, S, Hkv, hd)
+    dv5 = dv.reshape(B, S, Hkv, hd)
+    mask = np.tril(np.ones((S, S), bool))
+    for _ in range(3):
+        b, kv = rng.integers(B), rng.integers(Hkv)
+        keys = [0, int(rng.integers(1, S - 1)), int(rng.integers(S // 2, S - 1)), S - 1]
+        dv_ref = np.zeros((len(keys), hd))
+        dk_ref = np.zeros((len(keys), hd))
+        for h in range(kv * hpk, (kv + 1) * hpk):
+            s_ = (q5[b, :, h] @ k5[b, :, kv].T) * sc
+            s_ = np.where(mask, s_, -np.inf)
+            P = np.exp(s_ - s_.max(1, keepdims=True))
+            P /= P.sum(1, keepdims=True)
+            dP = do5[b, :, h] @ v5[b, :, kv].T
+            Dq = (P * dP).sum(1, keepdims=True)
+            dS = P * (dP - Dq)
+            dv_ref += P[:, keys].T @ do5[b, :, h]
+            dk_ref += sc * (dS[:, keys].T @ q5[b, :, h])
+        for i, j in enumerate(keys):
+            assert rel_l2(dv_ref[i], dv5[b, j, kv]) < 1e-2, ("dV", b, kv, j)
+            assert rel_l2(dk_ref[i], dk5[b, j, kv]) < 1e-2, ("dK", b, kv, j)

@@ -551,3 +551,37 @@ def test_model_lora_freezes_base():
     for k, v in before.items():
         assert np.array_equal(v, m.tensor(O.Model.PARAM, *k)), k
     assert np.any(m.tensor(O.Model.PARAM, 0, 17) != 0)  # B moved
+
+
+def test_thread_count_does_not_change_results():
+    """The oracle's OpenMP loops run only over independent outputs with every
+    sum in the sequential order: a whole step (tied head, bf16 operands, GQA
+    4:1, two sequences) and the CCE with z-loss and label smoothing give the
+    same bits on 1 thread and on all threads."""
+    cfg = dict(dim=64, n_heads=8, n_kv_heads=2, head_dim=16, ff_dim=96, seq_len=40, n_seqs=2,
+               n_layers=2, vocab_size=1100, rms_eps=1e-6, causal=1, rotary_dim=16,
+               rope_theta=1e6, qk_norm=1, lr=1e-3, beta1=0.9, beta2=0.999, eps_adam=1e-8,
+               lora_targets=0, lora_rank=0, lora_alpha=0.0, lora_lr_b_scale=1.0,
+               tied_embeddings=1, bf16_operands=1)
+    nthreads = O.get_threads()
+    outs = []
+    try:
+        for t in (1, max(nthreads, 4)):
+            O.set_threads(t)
+            m = O.Model(**cfg)
+            m.init_random(5, std=0.05)
+            tok, tgt = O.ids(80, 1, 1100), O.ids(80, 2, 1100)
+            loss = [m.step(tok, tgt) for _ in range(2)]
+            snap = [np.float32(x) for x in loss]
+            for kind in range(4):
+                snap += [m.tensor(kind, -1, 0).copy(), m.tensor(kind, 1, 1).copy(),
+                         m.tensor(kind, 0, 10).copy()]
+            h, w, tg = O.normal(70 * 48, 3), O.normal(900 * 48, 4, 0.1), O.ids(70, 5, 900)
+            l, lse, lr_ = O.cce_forward(h, w, tg, 70, 900, 48, chunk=256, z_loss=1e-3, ls=0.1)
+            dh, dW = O.cce_backward(h, w, tg, lse, 70, 900, 48, chunk=256, z_loss=1e-3, ls=0.1)
+            snap += [np.float32(l), lse, lr_, dh, dW]
+            outs.append(snap)
+    finally:
+        O.set_threads(nthreads)
+    for a, b in zip(*outs):
+        assert np.array_equal(a, b)

@@ -157,6 +157,9 @@ SIGNATURES = [
     ("vkh_runner_load_checkpoint", ST, [P, C.c_char_p]),
     ("vkh_runner_save_lora_checkpoint", ST, [P, C.c_char_p]),
     ("vkh_runner_load_lora_checkpoint", ST, [P, C.c_char_p]),
+    ("vkh_runner_attention_backward_path", U32, [P]),
+    ("vkh_checkpoint_config_encode", ST, [C.POINTER(Config), P, SZ]),
+    ("vkh_checkpoint_config_decode", ST, [P, SZ, C.POINTER(Config)]),
     ("vkh_runner_upload_train_batch", ST, [P, P, SZ, P, SZ]),
     ("vkh_runner_set_loss_target", ST, [P, F]),
     ("vkh_runner_tick_frame_train", ST, [P, P, TrainBudget, C.POINTER(TickResult)]),

@@ -122,15 +122,25 @@ struct vkh_runner {
     float *loss_h = nullptr;
     hipEvent_t upload_done = nullptr, loss_ready = nullptr;
     hipStream_t own = nullptr, cur = nullptr;
+    // Ordering across streams: every enqueue ends by recording ev_done on the
+    // stream it used; an enqueue on another stream first waits for it, and
+    // host-side reads and writes of runner memory wait for it.
+    hipEvent_t ev_done = nullptr;
+    hipStream_t last_st = nullptr;
     uint32_t step_t = 1;  // transformer.zig:940
     float loss_target = 0.f;
     bool loss_pending = false, batch_ready = false;
+    // the tick API's cached last loss (runner.zig:932-945)
+    bool has_last = false;
+    float last_loss_v = 0.f;
     size_t dev_bytes = 0;
     std::vector<void *> allocs;
 
     ~vkh_runner() {
+        if (ev_done && last_st) (void)hipEventSynchronize(ev_done);
         if (own) (void)hipStreamSynchronize(own);
         if (side) (void)hipStreamSynchronize(side);
+        if (ev_done) (void)hipEventDestroy(ev_done);
         for (hipEvent_t e : ev_layer) (void)hipEventDestroy(e);
         if (ev_side) (void)hipEventDestroy(ev_side);
         if (ev_head) (void)hipEventDestroy(ev_head);
@@ -279,6 +289,7 @@ struct vkh_runner {
         cur = own;
         VKH_HIP(hipEventCreateWithFlags(&upload_done, hipEventDisableTiming));
         VKH_HIP(hipEventCreateWithFlags(&loss_ready, hipEventDisableTiming));
+        VKH_HIP(hipEventCreateWithFlags(&ev_done, hipEventDisableTiming));
         VKH_HIP(hipHostMalloc((void **)&tok_h, (size_t)T * 4, hipHostMallocDefault));
         VKH_HIP(hipHostMalloc((void **)&tgt_h, (size_t)T * 4, hipHostMallocDefault));
         VKH_HIP(hipHostMalloc((void **)&loss_h, 16, hipHostMallocDefault));
@@ -511,6 +522,7 @@ struct vkh_runner {
     }
 
     vkh_status init_random(uint64_t seed, float std_, float lora_std) {
+        VKH_TRY(host_wait());
         shadow_dirty = true;
         auto normal = [&](const Span &s, uint64_t tag, float sd) -> vkh_status {
             if (!s.numel) return VKH_OK;
@@ -919,6 +931,45 @@ struct vkh_runner {
         return VKH_OK;
     }
 
+    // Start enqueueing on stream s after the runner's last work, whichever
+    // stream that went to (on the same stream the wait is already implied;
+    // it is issued anyway, so a caller stream destroyed and re-created at the
+    // same address cannot skip it).
+    vkh_status begin_on(hipStream_t s) {
+        cur = s;
+        if (last_st) VKH_HIP(hipStreamWaitEvent(s, ev_done, 0));
+        return VKH_OK;
+    }
+    // Close an enqueue: later work on any stream (or the host) orders after it.
+    vkh_status end_on() {
+        hipStream_t s = cur;
+        cur = own;
+        VKH_HIP(hipEventRecord(ev_done, s));
+        last_st = s;
+        return VKH_OK;
+    }
+    // Before the host reads or writes runner memory.
+    vkh_status host_wait() {
+        if (last_st) VKH_HIP(hipEventSynchronize(ev_done));
+        VKH_HIP(hipStreamSynchronize(own));
+        return VKH_OK;
+    }
+
+    // Forward + CE loss of the staged batch into the loss staging (the
+    // loss evaluation runner.zig:967-973 records every tick under a loss
+    // target, so a new batch whose loss is above the target resumes training).
+    vkh_status loss_eval_enqueue() {
+        VKH_TRY(forward_all());
+        const CceShape cs{T, V, D, 0.f, 0.f};
+        if (b16())
+            VKH_HIP(cce_forward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
+                                  cce_work, cur));
+        else
+            VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
+                                cce_work, cur));
+        return record_loss();
+    }
+
     vkh_status step_enqueue(bool with_adam) {
         VKH_TRY(forward_backward_enqueue(with_adam));
         VKH_TRY(record_loss());
@@ -940,39 +991,82 @@ struct CkptHeader {
 };
 static_assert(sizeof(CkptHeader) == 16, "checkpoint header is 16 bytes");
 
+// The config block is std.mem.asBytes(&cfg) of the reference's `Config`
+// (transformer.zig:31-77, written at :1405-1406).  `Config` is an auto-layout
+// Zig struct: the compiler orders its fields by descending alignment, keeping
+// declaration order among equals, so the nineteen 4-byte fields come first in
+// declaration order, then the two bools (causal, qk_norm), then two bytes of
+// padding: @sizeOf(Config) = 80.  Padding is written as zero.
+constexpr uint32_t kZigCfgSize = 80;
+
+void put32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
+void putf(uint8_t *p, float v) { memcpy(p, &v, 4); }
+uint32_t get32(const uint8_t *p) { uint32_t v; memcpy(&v, p, 4); return v; }
+float getf(const uint8_t *p) { float v; memcpy(&v, p, 4); return v; }
+
+void zig_cfg_encode(const vkh_config &c, uint8_t *o) {
+    memset(o, 0, kZigCfgSize);
+    put32(o + 0, c.dim); put32(o + 4, c.n_heads); put32(o + 8, c.n_kv_heads);
+    put32(o + 12, c.head_dim); put32(o + 16, c.ff_dim); put32(o + 20, c.n_pos);
+    put32(o + 24, c.n_layers); put32(o + 28, c.vocab_size); putf(o + 32, c.rms_eps);
+    put32(o + 36, c.rotary_dim); putf(o + 40, c.rope_theta); putf(o + 44, c.lr);
+    putf(o + 48, c.beta1); putf(o + 52, c.beta2); putf(o + 56, c.eps_adam);
+    put32(o + 60, c.lora_targets); put32(o + 64, c.lora_rank); putf(o + 68, c.lora_alpha);
+    putf(o + 72, c.lora_lr_b_scale);
+    o[76] = c.causal ? 1 : 0;
+    o[77] = c.qk_norm ? 1 : 0;
+}
+
+// Fills the reference's fields; the extensions (n_seqs, tied_embeddings,
+// precision) are left as they are in `c`.
+void zig_cfg_decode(const uint8_t *o, vkh_config &c) {
+    c.dim = get32(o + 0); c.n_heads = get32(o + 4); c.n_kv_heads = get32(o + 8);
+    c.head_dim = get32(o + 12); c.ff_dim = get32(o + 16); c.n_pos = get32(o + 20);
+    c.n_layers = get32(o + 24); c.vocab_size = get32(o + 28); c.rms_eps = getf(o + 32);
+    c.rotary_dim = get32(o + 36); c.rope_theta = getf(o + 40); c.lr = getf(o + 44);
+    c.beta1 = getf(o + 48); c.beta2 = getf(o + 52); c.eps_adam = getf(o + 56);
+    c.lora_targets = get32(o + 60); c.lora_rank = get32(o + 64); c.lora_alpha = getf(o + 68);
+    c.lora_lr_b_scale = getf(o + 72);
+    c.causal = o[76] != 0;
+    c.qk_norm = o[77] != 0;
+}
+
 // transformer.zig:197-205 cfgShapeMatches
 bool shape_matches(const vkh_config &a, const vkh_config &b) {
     return a.dim == b.dim && a.n_heads == b.n_heads && a.n_kv_heads == b.n_kv_heads &&
            a.head_dim == b.head_dim && a.ff_dim == b.ff_dim && a.n_pos == b.n_pos &&
            a.n_layers == b.n_layers && a.vocab_size == b.vocab_size && a.rms_eps == b.rms_eps &&
-           a.causal == b.causal && a.rotary_dim == b.rotary_dim &&
-           a.rope_theta == b.rope_theta && a.qk_norm == b.qk_norm &&
-           a.lora_targets == b.lora_targets && a.lora_rank == b.lora_rank &&
-           (a.n_seqs ? a.n_seqs : 1) == (b.n_seqs ? b.n_seqs : 1) &&
-           a.tied_embeddings == b.tied_embeddings;
+           (a.causal != 0) == (b.causal != 0) && a.rotary_dim == b.rotary_dim &&
+           a.rope_theta == b.rope_theta && (a.qk_norm != 0) == (b.qk_norm != 0) &&
+           a.lora_targets == b.lora_targets && a.lora_rank == b.lora_rank;
 }
 
 struct Blob {
-    float *dev;  // nullptr => zeros (m/v of frozen tensors)
+    float *dev;   // nullptr => zeros (m/v of frozen tensors)
     size_t numel;
+    int alias;    // >= 0: the tied lm_head, the same memory as blob `alias`
 };
 
 }  // namespace
 
 namespace vkh {
 
+// transformer.zig:1586-1655 collectBlobs.  A tied runner has one embedding
+// matrix; its lm_head blobs are the embedding's (param, m, v) again, which is
+// how the reference itself represents a tied head (load_real.zig:14-19 copies
+// embed_tokens into a separate lm_head), so the file loads in the reference.
 static void collect_blobs(vkh_runner *r, std::vector<Blob> &out) {
-    auto add3 = [&](const Span &s) {
-        out.push_back({r->P + s.off, s.numel});
-        out.push_back({r->ptr(VKH_ADAM_M, s), s.numel});
-        out.push_back({r->ptr(VKH_ADAM_V, s), s.numel});
+    auto add3 = [&](const Span &s, int alias) {
+        out.push_back({r->P + s.off, s.numel, alias});
+        out.push_back({r->ptr(VKH_ADAM_M, s), s.numel, alias < 0 ? -1 : alias + 1});
+        out.push_back({r->ptr(VKH_ADAM_V, s), s.numel, alias < 0 ? -1 : alias + 2});
     };
-    add3(r->embed);
-    add3(r->final_norm);
-    if (!r->tied) add3(r->lm_head);
+    add3(r->embed, -1);
+    add3(r->final_norm, -1);
+    add3(r->lm_head, r->tied ? 0 : -1);
     for (int l = 0; l < r->L; ++l) {
-        for (int t = 0; t < 9; ++t) add3(r->ls[l].t[t]);
-        if (r->cfg.qk_norm) { add3(r->ls[l].t[9]); add3(r->ls[l].t[10]); }
+        for (int t = 0; t < 9; ++t) add3(r->ls[l].t[t], -1);
+        if (r->cfg.qk_norm) { add3(r->ls[l].t[9], -1); add3(r->ls[l].t[10], -1); }
     }
 }
 
@@ -981,27 +1075,29 @@ static void collect_lora_blobs(vkh_runner *r, std::vector<Blob> &out) {
         if (!r->proj_lora(p)) continue;
         for (int l = 0; l < r->L; ++l) {
             const Span &a = r->ls[l].la[p], &b = r->ls[l].lb[p];
-            out.push_back({r->P + a.off, a.numel});
-            out.push_back({r->ptr(VKH_ADAM_M, a), a.numel});
-            out.push_back({r->ptr(VKH_ADAM_V, a), a.numel});
-            out.push_back({r->P + b.off, b.numel});
-            out.push_back({r->ptr(VKH_ADAM_M, b), b.numel});
-            out.push_back({r->ptr(VKH_ADAM_V, b), b.numel});
+            out.push_back({r->P + a.off, a.numel, -1});
+            out.push_back({r->ptr(VKH_ADAM_M, a), a.numel, -1});
+            out.push_back({r->ptr(VKH_ADAM_V, a), a.numel, -1});
+            out.push_back({r->P + b.off, b.numel, -1});
+            out.push_back({r->ptr(VKH_ADAM_M, b), b.numel, -1});
+            out.push_back({r->ptr(VKH_ADAM_V, b), b.numel, -1});
         }
     }
 }
 
 static vkh_status save_blobs(vkh_runner *r, const char *path, const char magic[4],
                              const std::vector<Blob> &blobs) {
-    VKH_HIP(hipStreamSynchronize(r->own));
+    VKH_TRY(r->host_wait());
     FILE *f = fopen(path, "wb");
     if (!f) return fail(VKH_ERR_IO, "cannot open %s for writing", path);
     CkptHeader h;
     memcpy(h.magic, magic, 4);
     h.version = 1;
     h.step_t = r->step_t;
-    h.cfg_size = sizeof(vkh_config);
-    bool ok = fwrite(&h, sizeof(h), 1, f) == 1 && fwrite(&r->cfg, sizeof(vkh_config), 1, f) == 1;
+    h.cfg_size = kZigCfgSize;
+    uint8_t cb[kZigCfgSize];
+    zig_cfg_encode(r->cfg, cb);
+    bool ok = fwrite(&h, sizeof(h), 1, f) == 1 && fwrite(cb, kZigCfgSize, 1, f) == 1;
     std::vector<float> buf;
     for (const Blob &b : blobs) {
         if (!ok) break;
@@ -1021,21 +1117,25 @@ static vkh_status load_blobs(vkh_runner *r, const char *path, const char magic[4
     FILE *f = fopen(path, "rb");
     if (!f) return fail(VKH_ERR_IO, "cannot open %s", path);
     CkptHeader h;
-    vkh_config saved;
+    uint8_t cb[kZigCfgSize];
+    vkh_config saved = r->cfg;
     vkh_status st = VKH_OK;
+    const vkh_status mismatch =
+        lora_file ? VKH_ERR_LORA_CHECKPOINT_CONFIG_MISMATCH : VKH_ERR_CHECKPOINT_CONFIG_MISMATCH;
     if (fread(&h, sizeof(h), 1, f) != 1) st = fail(VKH_ERR_END_OF_STREAM, "truncated header");
     else if (memcmp(h.magic, magic, 4) != 0)
         st = fail(lora_file ? VKH_ERR_INVALID_LORA_CHECKPOINT_MAGIC : VKH_ERR_INVALID_CHECKPOINT_MAGIC, "bad magic");
     else if (h.version != 1)
         st = fail(lora_file ? VKH_ERR_UNSUPPORTED_LORA_CHECKPOINT_VERSION : VKH_ERR_UNSUPPORTED_CHECKPOINT_VERSION,
                   "version %u", h.version);
-    else if (h.cfg_size != sizeof(vkh_config))
+    else if (h.cfg_size != kZigCfgSize)
         st = fail(lora_file ? VKH_ERR_LORA_CHECKPOINT_CONFIG_SIZE_MISMATCH : VKH_ERR_CHECKPOINT_CONFIG_SIZE_MISMATCH,
-                  "cfg_size %u", h.cfg_size);
-    else if (fread(&saved, sizeof(saved), 1, f) != 1) st = fail(VKH_ERR_END_OF_STREAM, "truncated config");
-    else if (!shape_matches(saved, r->cfg))
-        st = fail(lora_file ? VKH_ERR_LORA_CHECKPOINT_CONFIG_MISMATCH : VKH_ERR_CHECKPOINT_CONFIG_MISMATCH,
-                  "config shape mismatch");
+                  "cfg_size %u != %u", h.cfg_size, kZigCfgSize);
+    else if (fread(cb, kZigCfgSize, 1, f) != 1) st = fail(VKH_ERR_END_OF_STREAM, "truncated config");
+    else {
+        zig_cfg_decode(cb, saved);
+        if (!shape_matches(saved, r->cfg)) st = fail(mismatch, "config shape mismatch");
+    }
     std::vector<std::vector<float>> data;
     if (st == VKH_OK) {
         data.resize(blobs.size());
@@ -1048,10 +1148,15 @@ static vkh_status load_blobs(vkh_runner *r, const char *path, const char magic[4
         }
     }
     fclose(f);
+    // a tied runner holds one matrix: the file's lm_head must be its embedding
+    for (size_t i = 0; st == VKH_OK && i < blobs.size(); ++i)
+        if (blobs[i].alias >= 0 && data[i] != data[(size_t)blobs[i].alias])
+            st = fail(mismatch, "the file's lm_head differs from its embedding (untied) but the "
+                                "runner ties them");
     if (st != VKH_OK) return st;
-    VKH_HIP(hipStreamSynchronize(r->own));
+    VKH_TRY(r->host_wait());
     for (size_t i = 0; i < blobs.size(); ++i)
-        if (blobs[i].dev)
+        if (blobs[i].dev && blobs[i].alias < 0)
             VKH_HIP(hipMemcpy(blobs[i].dev, data[i].data(), blobs[i].numel * 4, hipMemcpyHostToDevice));
     // transformer.zig:1444-1448, :1538-1544
     r->step_t = h.step_t;
@@ -1108,14 +1213,15 @@ static vkh_status run_step(vkh_runner *r, const uint32_t *tok, size_t nt, const 
                            size_t ng, hipStream_t st, bool adam, bool wait) {
     if (!r) return fail(VKH_ERR_INVALID_ARGUMENT, "null runner");
     VKH_TRY(r->check_ids(tok, nt, tgt, ng));
-    r->cur = st ? st : r->own;
+    VKH_TRY(r->begin_on(st ? st : r->own));
     vkh_status s = r->upload_ids(tok, tgt);
     if (s == VKH_OK) s = r->step_enqueue(adam);
+    const vkh_status se = r->end_on();
+    if (s == VKH_OK) s = se;
     if (s == VKH_OK && wait) {
-        hipError_t e = hipStreamSynchronize(r->cur);
+        hipError_t e = hipEventSynchronize(r->ev_done);
         if (e != hipSuccess) s = hip_fail(e, "step");
     }
-    r->cur = r->own;
     return s;
 }
 
@@ -1146,8 +1252,7 @@ vkh_status vkh_runner_last_loss(vkh_runner *r, float *loss) {
 
 vkh_status vkh_runner_synchronize(vkh_runner *r) {
     if (!r) return fail(VKH_ERR_INVALID_ARGUMENT, "null runner");
-    VKH_HIP(hipStreamSynchronize(r->own));
-    return VKH_OK;
+    return r->host_wait();
 }
 
 vkh_status vkh_runner_forward_logits(vkh_runner *r, const uint32_t *token_ids, size_t n_tokens,
@@ -1155,9 +1260,12 @@ vkh_status vkh_runner_forward_logits(vkh_runner *r, const uint32_t *token_ids, s
     if (!r || !out_logits) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
     VKH_TRY(r->check_ids(token_ids, n_tokens, nullptr, 0));
     if (out_len != (size_t)r->T * r->V) return fail(VKH_ERR_OUT_LOGITS_LEN, "out_logits len %zu", out_len);
-    r->cur = r->own;
-    VKH_TRY(r->upload_ids(token_ids, nullptr));
-    VKH_TRY(r->forward_all());
+    VKH_TRY(r->begin_on(r->own));
+    vkh_status s = r->upload_ids(token_ids, nullptr);
+    if (s == VKH_OK) s = r->forward_all();
+    const vkh_status se = r->end_on();
+    if (s == VKH_OK) s = se;
+    if (s != VKH_OK) return s;
     float *logits = nullptr;
     VKH_HIP(hipMallocAsync((void **)&logits, (size_t)r->T * r->V * 4, r->own));
     hipError_t e =
@@ -1168,6 +1276,7 @@ vkh_status vkh_runner_forward_logits(vkh_runner *r, const uint32_t *token_ids, s
     if (e == hipSuccess)
         e = hipMemcpyAsync(out_logits, logits, (size_t)r->T * r->V * 4, hipMemcpyDeviceToHost, r->own);
     (void)hipFreeAsync(logits, r->own);
+    if (e == hipSuccess) e = hipEventRecord(r->ev_done, r->own);
     if (e == hipSuccess) e = hipStreamSynchronize(r->own);
     if (e != hipSuccess) return hip_fail(e, "forward_logits");
     return VKH_OK;
@@ -1211,6 +1320,13 @@ size_t vkh_runner_param_count(const vkh_runner *r) {
 
 size_t vkh_runner_device_bytes(const vkh_runner *r) { return r ? r->dev_bytes : 0; }
 
+uint32_t vkh_runner_attention_backward_path(const vkh_runner *r) {
+    if (!r) return VKH_ATTN_BW_ROWWISE;
+    if (r->attn_v4) return VKH_ATTN_BW_RECOMPUTE;
+    if (r->attn_fused) return VKH_ATTN_BW_DS_GEMM;
+    return VKH_ATTN_BW_ROWWISE;
+}
+
 vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int which,
                                    size_t *numel) {
     if (!r || !numel) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
@@ -1246,7 +1362,7 @@ vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, 
     size_t n = 0;
     VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n));
     if (numel != n || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
-    VKH_HIP(hipStreamSynchronize(r->own));
+    VKH_TRY(r->host_wait());
     VKH_HIP(hipMemcpy(host, d, n * 4, hipMemcpyDeviceToHost));
     return VKH_OK;
 }
@@ -1257,7 +1373,7 @@ vkh_status vkh_runner_set_tensor(vkh_runner *r, int kind, int layer, int which,
     size_t n = 0;
     VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n));
     if (numel != n || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
-    VKH_HIP(hipStreamSynchronize(r->own));
+    VKH_TRY(r->host_wait());
     VKH_HIP(hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice));
     if (kind == VKH_PARAM) r->shadow_dirty = true;
     return VKH_OK;
@@ -1300,8 +1416,11 @@ vkh_status vkh_runner_upload_train_batch(vkh_runner *r, const uint32_t *token_id
                                          size_t n_targets) {
     if (!r) return fail(VKH_ERR_INVALID_ARGUMENT, "null runner");
     VKH_TRY(r->check_ids(token_ids, n_tokens, target_ids, n_targets));
-    r->cur = r->own;
-    VKH_TRY(r->upload_ids(token_ids, target_ids));
+    VKH_TRY(r->begin_on(r->own));
+    vkh_status s = r->upload_ids(token_ids, target_ids);
+    const vkh_status se = r->end_on();
+    if (s == VKH_OK) s = se;
+    if (s != VKH_OK) return s;
     VKH_HIP(hipStreamSynchronize(r->own));
     r->batch_ready = true;
     return VKH_OK;
@@ -1313,47 +1432,78 @@ vkh_status vkh_runner_set_loss_target(vkh_runner *r, float target) {
     return VKH_OK;
 }
 
+// runner.zig:904-986 tickFrameTrain over the transformer step: up to the
+// budget of steps on the staged batch, enqueued on the caller's stream.  The
+// loss reported is the one staged by an earlier tick, once its copy has
+// landed.  With a loss target, that loss gates training (idle while it is at
+// or below the target) and every tick enqueues a fresh loss evaluation of the
+// staged batch after its steps, so uploading a batch whose loss is above the
+// target resumes training; without one, the loss of the tick's last step is
+// staged.
 vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
                                        vkh_train_budget budget, vkh_tick_result *out) {
     if (!r || !out) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
-    if (!r->batch_ready) return fail(VKH_ERR_INVALID_ARGUMENT, "no train batch uploaded");
-    const auto t0 = std::chrono::steady_clock::now();
     memset(out, 0, sizeof(*out));
-    // runner.zig:932-945: last frame's loss, if it has landed
+    if (!r->batch_ready) return fail(VKH_ERR_INVALID_ARGUMENT, "no train batch uploaded");
+    if (budget.mode > VKH_BUDGET_EITHER) return fail(VKH_ERR_INVALID_ARGUMENT, "unknown budget mode %u", budget.mode);
+    const auto t0 = std::chrono::steady_clock::now();
     if (r->loss_pending && hipEventQuery(r->loss_ready) == hipSuccess) {
-        out->has_loss = 1;
-        out->last_loss = r->loss_h[0];
+        r->last_loss_v = r->loss_h[0];
+        r->has_last = true;
     }
-    // runner.zig:948-956: loss-target gate
-    if (out->has_loss && r->loss_target > 0.f && out->last_loss <= r->loss_target) {
+    out->has_loss = r->has_last ? 1u : 0u;
+    out->last_loss = r->has_last ? r->last_loss_v : 0.f;
+    const uint32_t max_steps = budget.mode == VKH_BUDGET_MICROSECONDS ? UINT32_MAX : budget.steps;
+    const uint64_t us_cap = budget.mode == VKH_BUDGET_STEPS ? UINT64_MAX : budget.microseconds;
+    if (max_steps == 0 || us_cap == 0) {  // runner.zig:924-926
         out->idle = 1;
         return VKH_OK;
     }
-    r->cur = stream ? (hipStream_t)stream : r->own;
+    const bool decay = r->loss_target > 0.f;
+    const bool should_train = !decay || !r->has_last || r->last_loss_v > r->loss_target;
+    VKH_TRY(r->begin_on(stream ? (hipStream_t)stream : r->own));
     vkh_status st = VKH_OK;
-    const bool by_steps = budget.mode != VKH_BUDGET_MICROSECONDS;
-    const bool by_time = budget.mode != VKH_BUDGET_STEPS;
     uint32_t n = 0;
-    for (;;) {
-        if (by_steps && n >= budget.steps) break;
-        if (by_time) {
-            const uint64_t us = (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(
-                                    std::chrono::steady_clock::now() - t0).count();
-            if (us >= budget.microseconds && n > 0) break;
-            if (budget.microseconds == 0) break;
-        }
+    while (should_train && n < max_steps) {
         st = r->forward_backward_enqueue(true);
         if (st == VKH_OK && !r->concurrent) st = r->adam_enqueue();
         if (st != VKH_OK) break;
         r->step_t += 1;
         ++n;
+        const uint64_t us = (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(
+                                std::chrono::steady_clock::now() - t0).count();
+        if (us >= us_cap) break;
     }
-    if (st == VKH_OK && n > 0) st = r->record_loss();  // runner.zig:975-977
-    r->cur = r->own;
+    if (st == VKH_OK) {
+        if (decay) st = r->loss_eval_enqueue();
+        else if (n > 0) st = r->record_loss();
+    }
+    const vkh_status se = r->end_on();
+    if (st == VKH_OK) st = se;
     out->steps_completed = n;
+    out->idle = should_train ? 0u : 1u;
     out->elapsed_us = (uint64_t)std::chrono::duration_cast<std::chrono::microseconds>(
                           std::chrono::steady_clock::now() - t0).count();
     return st;
+}
+
+// The checkpoint config block (the reference's Config bytes) as a codec, for
+// hosts and tests that read or write checkpoint files themselves.
+vkh_status vkh_checkpoint_config_encode(const vkh_config *cfg, void *out, size_t out_len) {
+    if (!cfg || !out) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
+    if (out_len < kZigCfgSize) return fail(VKH_ERR_INVALID_ARGUMENT, "out_len %zu < %u", out_len, kZigCfgSize);
+    zig_cfg_encode(*cfg, (uint8_t *)out);
+    return VKH_OK;
+}
+
+vkh_status vkh_checkpoint_config_decode(const void *in, size_t in_len, vkh_config *out) {
+    if (!in || !out) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
+    if (in_len != kZigCfgSize)
+        return fail(VKH_ERR_CHECKPOINT_CONFIG_SIZE_MISMATCH, "in_len %zu != %u", in_len, kZigCfgSize);
+    memset(out, 0, sizeof(*out));
+    out->n_seqs = 1;
+    zig_cfg_decode((const uint8_t *)in, *out);
+    return VKH_OK;
 }
 
 }  // extern "C"

@@ -56,6 +56,24 @@ class TickResultPy:
     elapsed_us: int
 
 
+CHECKPOINT_CONFIG_BYTES = 80
+
+
+def checkpoint_config_bytes(cfg: Config) -> bytes:
+    """The 80-byte config block a .vkpt / .lvkpt carries (the reference's
+    `Config` bytes, transformer.zig:31-77, :1405-1406)."""
+    buf = (C.c_uint8 * CHECKPOINT_CONFIG_BYTES)()
+    check(lib().vkh_checkpoint_config_encode(C.byref(cfg), buf, CHECKPOINT_CONFIG_BYTES))
+    return bytes(buf)
+
+
+def checkpoint_config_from_bytes(data: bytes) -> Config:
+    cfg = Config()
+    buf = (C.c_uint8 * len(data)).from_buffer_copy(data)
+    check(lib().vkh_checkpoint_config_decode(buf, len(data), C.byref(cfg)))
+    return cfg
+
+
 def make_config(**kw) -> Config:
     """vkh_config with the reference's defaults (transformer.zig:31-77)."""
     d = dict(rms_eps=1e-5, causal=1, rotary_dim=0, rope_theta=10000.0, qk_norm=0, lr=1e-2,
@@ -207,6 +225,11 @@ class Runner:
         p, n = C.c_void_p(), C.c_size_t()
         check(lib().vkh_runner_tensor_device_ptr(self._h, kind, layer, which, C.byref(p), C.byref(n)))
         return p.value, n.value
+
+    def attention_backward_path(self) -> str:
+        """'recompute', 'ds_gemm' or 'rowwise': the step's attention backward."""
+        return {0: "rowwise", 1: "ds_gemm", 2: "recompute"}[
+            int(lib().vkh_runner_attention_backward_path(self._h))]
 
     # ── checkpoints ──────────────────────────────────────────────────
     def save_checkpoint(self, path: str):
