@@ -84,12 +84,18 @@ def _declare(L):
       SZ, SZ, F32P, F32P)
     d("orc_flash_attention_backward", None, F32P, F32P, F32P, F32P, F32P, F32P, SZ, SZ,
       SZ, SZ, SZ, C.c_int, F32P, F32P, F32P)
+    d("orc_flash_attention_forward_bf16ops", None, F32P, F32P, F32P, SZ, SZ, SZ, SZ, SZ,
+      C.c_int, F32P, F32P)
+    d("orc_flash_attention_backward_bf16ops", None, F32P, F32P, F32P, F32P, F32P, F32P, SZ, SZ,
+      SZ, SZ, SZ, C.c_int, F32P, F32P, F32P)
     d("orc_fa_bw_d", None, F32P, F32P, SZ, SZ, SZ, F32P)
     d("orc_matmul_nt", None, F32P, F32P, F32P, SZ, SZ, SZ)
     d("orc_linear_backward", None, F32P, F32P, F32P, SZ, SZ, SZ, C.c_void_p, C.c_void_p)
     d("orc_cce_forward", C.c_float, F32P, F32P, U32P, SZ, SZ, SZ, SZ, C.c_float, C.c_float,
       F32P, F32P)
     d("orc_cce_backward", None, F32P, F32P, U32P, F32P, SZ, SZ, SZ, SZ, C.c_float,
+      C.c_float, F32P, C.c_void_p)
+    d("orc_cce_backward_bf16ops", None, F32P, F32P, U32P, F32P, SZ, SZ, SZ, C.c_float,
       C.c_float, F32P, C.c_void_p)
     d("orc_softmax_ce_loss", C.c_float, F32P, U32P, SZ, SZ)
     d("orc_softmax_ce_loss_grad", None, F32P, F32P, U32P, SZ, SZ)
@@ -271,23 +277,32 @@ def swiglu_backward(dg, pg, up):
     return dpg, dup
 
 
-def flash_forward(Q, K, V, n_q, n_kv, H, Hkv, hd, causal, Br=16, Bc=16):
+def flash_forward(Q, K, V, n_q, n_kv, H, Hkv, hd, causal, Br=16, Bc=16, bf16_ops=False):
+    """flash_attn.zig forward; bf16_ops: the MFMA kernels' operand rounding
+    (P to bf16 where it multiplies V, 64-key tiles; Br / Bc ignored)."""
     Q, K, V = f32(Q), f32(K), f32(V)
     out = np.empty(n_q * H * hd, np.float32)
     lse = np.empty(n_q * H, np.float32)
-    lib().orc_flash_attention_forward(Q.reshape(-1), K.reshape(-1), V.reshape(-1), n_q, n_kv,
-                                      H, Hkv, hd, int(causal), Br, Bc, out, lse)
+    if bf16_ops:
+        lib().orc_flash_attention_forward_bf16ops(Q.reshape(-1), K.reshape(-1), V.reshape(-1),
+                                                  n_q, n_kv, H, Hkv, hd, int(causal), out, lse)
+    else:
+        lib().orc_flash_attention_forward(Q.reshape(-1), K.reshape(-1), V.reshape(-1), n_q,
+                                          n_kv, H, Hkv, hd, int(causal), Br, Bc, out, lse)
     return out, lse
 
 
-def flash_backward(Q, K, V, O, dO, lse, n_q, n_kv, H, Hkv, hd, causal):
+def flash_backward(Q, K, V, O, dO, lse, n_q, n_kv, H, Hkv, hd, causal, bf16_ops=False):
+    """flash_attn.zig backward; bf16_ops: P and the unscaled dS rounded to bf16
+    where they meet dO / Q / K, 1/sqrt(d) applied to the accumulated dQ, dK."""
     Q, K, V, O, dO, lse = (f32(a) for a in (Q, K, V, O, dO, lse))
     dQ = np.empty(n_q * H * hd, np.float32)
     dK = np.empty(n_kv * Hkv * hd, np.float32)
     dV = np.empty_like(dK)
-    lib().orc_flash_attention_backward(Q.reshape(-1), K.reshape(-1), V.reshape(-1),
-                                       O.reshape(-1), dO.reshape(-1), lse.reshape(-1), n_q,
-                                       n_kv, H, Hkv, hd, int(causal), dQ, dK, dV)
+    fn = (lib().orc_flash_attention_backward_bf16ops if bf16_ops
+          else lib().orc_flash_attention_backward)
+    fn(Q.reshape(-1), K.reshape(-1), V.reshape(-1), O.reshape(-1), dO.reshape(-1),
+       lse.reshape(-1), n_q, n_kv, H, Hkv, hd, int(causal), dQ, dK, dV)
     return dQ, dK, dV
 
 
@@ -324,13 +339,19 @@ def cce_forward(h, w, tgt, n, vocab, dim, chunk=1024, z_loss=0.0, ls=0.0):
     return loss, lse, loss_row
 
 
-def cce_backward(h, w, tgt, lse, n, vocab, dim, chunk=1024, z_loss=0.0, ls=0.0, want_dw=True):
+def cce_backward(h, w, tgt, lse, n, vocab, dim, chunk=1024, z_loss=0.0, ls=0.0, want_dw=True,
+                 bf16_ops=False):
+    """cce.zig backward; bf16_ops: dz rounded to bf16 before both products."""
     h, w, lse = f32(h), f32(w), f32(lse)
     tgt = np.ascontiguousarray(tgt, np.uint32)
     dh = np.empty(n * dim, np.float32)
     dW = np.zeros(vocab * dim, np.float32) if want_dw else None
-    lib().orc_cce_backward(h.reshape(-1), w.reshape(-1), tgt, lse, n, vocab, dim,
-                           min(chunk, vocab), z_loss, ls, dh, _ptr(dW))
+    if bf16_ops:
+        lib().orc_cce_backward_bf16ops(h.reshape(-1), w.reshape(-1), tgt, lse, n, vocab, dim,
+                                       z_loss, ls, dh, _ptr(dW))
+    else:
+        lib().orc_cce_backward(h.reshape(-1), w.reshape(-1), tgt, lse, n, vocab, dim,
+                               min(chunk, vocab), z_loss, ls, dh, _ptr(dW))
     return dh, dW
 
 

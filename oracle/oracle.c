@@ -338,10 +338,15 @@ void orc_swiglu_backward(const float *d_gated, const float *pre_gate, const floa
 
 /* ── FlashAttention: src/cpu/flash_attn.zig:91-376 ─────────────────────── */
 
-void orc_flash_attention_forward(const float *Q, const float *K, const float *V,
-                                 size_t n_q, size_t n_kv, size_t n_heads,
-                                 size_t n_kv_heads, size_t head_dim, int causal,
-                                 size_t Br, size_t Bc, float *out, float *lse) {
+static float bf16r(float x) { return orc_bf16_to_f32(orc_f32_to_bf16(x)); }
+
+/* bf16_ops: the bf16-operand model of the MFMA kernels.  Every product's
+ * operands are bf16, including the probabilities: P is formed in fp32 (l sums
+ * the fp32 values) and rounded to bf16 where it multiplies V. */
+static void flash_forward(const float *Q, const float *K, const float *V, size_t n_q,
+                          size_t n_kv, size_t n_heads, size_t n_kv_heads, size_t head_dim,
+                          int causal, size_t Br, size_t Bc, int bf16_ops, float *out,
+                          float *lse) {
     size_t hpk = n_heads / n_kv_heads;
     float inv_sqrt_d = 1.0f / sqrtf((float)head_dim);
     /* every (query block, head) is independent: parallel over them */
@@ -394,6 +399,7 @@ void orc_flash_attention_forward(const float *Q, const float *K, const float *V,
                     for (size_t ki = 0; ki < klen; ++ki) {
                         float p = p_tile[qi * Bc + ki];
                         if (p == 0.0f) continue;
+                        if (bf16_ops) p = bf16r(p);
                         size_t v_off = (kb + ki) * n_kv_heads * head_dim + kv_h * head_dim;
                         for (size_t d = 0; d < head_dim; ++d) o_acc[qi * head_dim + d] += p * V[v_off + d];
                     }
@@ -414,11 +420,21 @@ void orc_flash_attention_forward(const float *Q, const float *K, const float *V,
     }
 }
 
-void orc_flash_attention_backward(const float *Q, const float *K, const float *V,
-                                  const float *O, const float *dO, const float *lse,
-                                  size_t n_q, size_t n_kv, size_t n_heads,
-                                  size_t n_kv_heads, size_t head_dim, int causal,
-                                  float *dQ, float *dK, float *dV) {
+void orc_flash_attention_forward(const float *Q, const float *K, const float *V,
+                                 size_t n_q, size_t n_kv, size_t n_heads,
+                                 size_t n_kv_heads, size_t head_dim, int causal,
+                                 size_t Br, size_t Bc, float *out, float *lse) {
+    flash_forward(Q, K, V, n_q, n_kv, n_heads, n_kv_heads, head_dim, causal, Br, Bc, 0, out, lse);
+}
+
+/* bf16_ops: P rounds to bf16 where it multiplies dO (dV), and the unscaled
+ * dS = P (dP - D) rounds to bf16 where it multiplies Q and K (dK, dQ); the
+ * 1/sqrt(d) scale is applied to the accumulated dQ and dK, which is where the
+ * MFMA kernels apply it. */
+static void flash_backward(const float *Q, const float *K, const float *V, const float *O,
+                           const float *dO, const float *lse, size_t n_q, size_t n_kv,
+                           size_t n_heads, size_t n_kv_heads, size_t head_dim, int causal,
+                           int bf16_ops, float *dQ, float *dK, float *dV) {
     size_t hpk = n_heads / n_kv_heads;
     float inv_sqrt_d = 1.0f / sqrtf((float)head_dim);
     memset(dQ, 0, n_q * n_heads * head_dim * sizeof(float));
@@ -446,16 +462,47 @@ void orc_flash_attention_backward(const float *Q, const float *K, const float *V
                 float S = (float)s * inv_sqrt_d;
                 float P = expf(S - lse_qh);
                 if (P == 0.0f) continue;
-                for (size_t d = 0; d < head_dim; ++d) dV[k_off + d] += P * dO[o_off + d];
+                const float Pv = bf16_ops ? bf16r(P) : P;
+                for (size_t d = 0; d < head_dim; ++d) dV[k_off + d] += Pv * dO[o_off + d];
                 double dP = 0;
                 for (size_t d = 0; d < head_dim; ++d) dP += (double)dO[o_off + d] * (double)V[k_off + d];
-                float dS_scaled = P * ((float)dP - D_f32) * inv_sqrt_d;
+                float dS_scaled = bf16_ops ? bf16r(P * ((float)dP - D_f32))
+                                           : P * ((float)dP - D_f32) * inv_sqrt_d;
                 for (size_t d = 0; d < head_dim; ++d) {
                     dQ[o_off + d] += dS_scaled * K[k_off + d];
                     dK[k_off + d] += dS_scaled * Q[o_off + d];
                 }
             }
         }
+    if (bf16_ops) {
+        for (size_t i = 0; i < n_q * n_heads * head_dim; ++i) dQ[i] *= inv_sqrt_d;
+        for (size_t i = 0; i < n_kv * n_kv_heads * head_dim; ++i) dK[i] *= inv_sqrt_d;
+    }
+}
+
+void orc_flash_attention_backward(const float *Q, const float *K, const float *V,
+                                  const float *O, const float *dO, const float *lse,
+                                  size_t n_q, size_t n_kv, size_t n_heads,
+                                  size_t n_kv_heads, size_t head_dim, int causal,
+                                  float *dQ, float *dK, float *dV) {
+    flash_backward(Q, K, V, O, dO, lse, n_q, n_kv, n_heads, n_kv_heads, head_dim, causal, 0, dQ,
+                   dK, dV);
+}
+
+void orc_flash_attention_forward_bf16ops(const float *Q, const float *K, const float *V,
+                                         size_t n_q, size_t n_kv, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, int causal,
+                                         float *out, float *lse) {
+    flash_forward(Q, K, V, n_q, n_kv, n_heads, n_kv_heads, head_dim, causal, 16, 64, 1, out, lse);
+}
+
+void orc_flash_attention_backward_bf16ops(const float *Q, const float *K, const float *V,
+                                          const float *O, const float *dO, const float *lse,
+                                          size_t n_q, size_t n_kv, size_t n_heads,
+                                          size_t n_kv_heads, size_t head_dim, int causal,
+                                          float *dQ, float *dK, float *dV) {
+    flash_backward(Q, K, V, O, dO, lse, n_q, n_kv, n_heads, n_kv_heads, head_dim, causal, 1, dQ,
+                   dK, dV);
 }
 
 void orc_fa_bw_d(const float *O, const float *dO, size_t n_q, size_t n_heads,
@@ -602,10 +649,10 @@ float orc_cce_forward(const float *h, const float *w_lm, const uint32_t *tgt, si
  * accumulates dz * h[row, :] with rows ascending, in fp32, as cce.zig's
  * row-by-row loop does; the block structure only changes which of these
  * independent sums is advanced when. */
-void orc_cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
-                      const float *lse, size_t n, size_t vocab, size_t dim, size_t chunk,
-                      float z_loss_scale, float label_smoothing, float *d_h, float *dW) {
-    (void)chunk; /* the chunking of cce.zig does not change any value here */
+static void cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
+                         const float *lse, size_t n, size_t vocab, size_t dim,
+                         float z_loss_scale, float label_smoothing, int bf16_ops, float *d_h,
+                         float *dW) {
     memset(d_h, 0, n * dim * sizeof(float));
     float inv_n = 1.0f / (float)n;
     float eps = label_smoothing;
@@ -624,7 +671,9 @@ void orc_cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
                 float softmax_factor = 1.0f + 2.0f * z_loss_scale * lse_row;
                 float p = (float)exp((double)z_t[v * nr + r] - (double)lse_row);
                 float ti = (v == tgt[row]) ? t_scale : 0.0f;
-                z_t[v * nr + r] = (softmax_factor * p - ti - eps_over_v) * inv_n;
+                const float dz = (softmax_factor * p - ti - eps_over_v) * inv_n;
+                /* bf16 operands: dz is an operand of both products */
+                z_t[v * nr + r] = bf16_ops ? orc_bf16_to_f32(orc_f32_to_bf16(dz)) : dz;
             }
         /* dh: each thread owns whole rows and walks the vocabulary in tiles
          * of 64 head rows (reused from cache by all its rows) */
@@ -661,6 +710,21 @@ void orc_cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
         }
     }
     free(z_t);
+}
+
+void orc_cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
+                      const float *lse, size_t n, size_t vocab, size_t dim, size_t chunk,
+                      float z_loss_scale, float label_smoothing, float *d_h, float *dW) {
+    (void)chunk; /* the chunking of cce.zig does not change any value here */
+    cce_backward(h, w_lm, tgt, lse, n, vocab, dim, z_loss_scale, label_smoothing, 0, d_h, dW);
+}
+
+/* The bf16-operand model of the MFMA path: dz rounds to bf16 (the operand
+ * of dh = dz W and dW = dz^T h); h and W are expected already rounded. */
+void orc_cce_backward_bf16ops(const float *h, const float *w_lm, const uint32_t *tgt,
+                              const float *lse, size_t n, size_t vocab, size_t dim,
+                              float z_loss_scale, float label_smoothing, float *d_h, float *dW) {
+    cce_backward(h, w_lm, tgt, lse, n, vocab, dim, z_loss_scale, label_smoothing, 1, d_h, dW);
 }
 
 float orc_softmax_ce_loss(const float *logits, const uint32_t *tgt, size_t n_pos,
@@ -1067,10 +1131,11 @@ static void layer_forward(orc_model *m, int l, const float *x_in, scratch_t *sc)
     const float *qq = maybe_bf16(m, a->q, T * m->qd, &sc[0]);
     const float *kk = maybe_bf16(m, a->k, T * m->kvd, &sc[1]);
     const float *vv = maybe_bf16(m, a->v, T * m->kvd, &sc[2]);
+    /* bf16 operands: the kernels' 64-key tiles and bf16 P (flash_forward) */
     for (uint32_t b = 0; b < c->n_seqs; ++b)
-        orc_flash_attention_forward(qq + b * S * m->qd, kk + b * S * m->kvd, vv + b * S * m->kvd,
-                                    S, S, H, Hkv, hd, c->causal != 0, 16, 16,
-                                    a->attn_out + b * S * m->qd, a->lse + b * S * H);
+        flash_forward(qq + b * S * m->qd, kk + b * S * m->kvd, vv + b * S * m->kvd, S, S, H, Hkv,
+                      hd, c->causal != 0, 16, c->bf16_operands ? 64 : 16, c->bf16_operands != 0,
+                      a->attn_out + b * S * m->qd, a->lse + b * S * H);
     float *o = malloc(T * D * sizeof(float));
     proj_forward(m, l, 3, a->attn_out, P + s->t[4].off, o, &sc[0], &sc[1]);
     for (size_t i = 0; i < T * D; ++i) a->mid[i] = x_in[i] + o[i];
@@ -1118,11 +1183,13 @@ static void layer_backward(orc_model *m, int l, const float *x_in, const float *
     const float *kk = maybe_bf16(m, a->k, T * m->kvd, &sc[1]);
     const float *vv = maybe_bf16(m, a->v, T * m->kvd, &sc[2]);
     const float *dd = maybe_bf16(m, d_attn_out, T * m->qd, &sc[3]);
+    /* bf16 operands: D = rowsum(O dO) over the bf16 O the kernels keep */
+    const float *oo = maybe_bf16(m, a->attn_out, T * m->qd, &sc[4]);
     for (uint32_t b = 0; b < c->n_seqs; ++b)
-        orc_flash_attention_backward(qq + b * S * m->qd, kk + b * S * m->kvd, vv + b * S * m->kvd,
-                                     a->attn_out + b * S * m->qd, dd + b * S * m->qd,
-                                     a->lse + b * S * H, S, S, H, Hkv, hd, c->causal != 0,
-                                     dQ + b * S * m->qd, dK + b * S * m->kvd, dV + b * S * m->kvd);
+        flash_backward(qq + b * S * m->qd, kk + b * S * m->kvd, vv + b * S * m->kvd,
+                       oo + b * S * m->qd, dd + b * S * m->qd, a->lse + b * S * H, S, S, H, Hkv,
+                       hd, c->causal != 0, c->bf16_operands != 0, dQ + b * S * m->qd,
+                       dK + b * S * m->kvd, dV + b * S * m->kvd);
     float *dQ2 = malloc(T * m->qd * sizeof(float)), *dK2 = malloc(T * m->kvd * sizeof(float));
     if (c->rotary_dim > 0) {
         orc_rope_backward_batched(dQ2, dQ, T, H, hd, c->rotary_dim, c->rope_theta, S);
@@ -1169,7 +1236,7 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
     float *P = m->arena[ORC_PARAM], *G = m->arena[ORC_GRAD];
     size_t T = m->T, D = c->dim, V = c->vocab_size;
     int lora = c->lora_targets != 0;
-    scratch_t sc[4] = {{0}};
+    scratch_t sc[5] = {{0}};
     model_forward(m, tokens, sc);
     const float *hh = maybe_bf16(m, m->fn_out, T * D, &sc[0]);
     const float *ww = maybe_bf16(m, P + m->lm_head.off, V * D, &sc[1]);
@@ -1182,7 +1249,7 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
         dW_lm = c->tied_embeddings ? calloc(V * D, sizeof(float)) : G + m->lm_head.off;
         if (!c->tied_embeddings) memset(dW_lm, 0, V * D * sizeof(float));
     }
-    orc_cce_backward(hh, ww, targets, m->lse, T, V, D, chunk, 0, 0, d_fn, dW_lm);
+    cce_backward(hh, ww, targets, m->lse, T, V, D, 0, 0, c->bf16_operands != 0, d_fn, dW_lm);
     float *d_y = malloc(T * D * sizeof(float)), *d_x = malloc(T * D * sizeof(float));
     float *dw_fn = G + m->final_norm.off;
     if (!lora) memset(dw_fn, 0, D * sizeof(float));
@@ -1203,7 +1270,7 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
         }
     }
     free(d_fn); free(d_y); free(d_x);
-    for (int k = 0; k < 4; ++k) free(sc[k].buf);
+    for (int k = 0; k < 5; ++k) free(sc[k].buf);
     return loss;
 }
 
@@ -1242,14 +1309,14 @@ float orc_model_step(orc_model *m, const uint32_t *tokens, const uint32_t *targe
 }
 
 void orc_model_forward_logits(orc_model *m, const uint32_t *tokens, float *logits) {
-    scratch_t sc[4] = {{0}};
+    scratch_t sc[5] = {{0}};
     model_forward(m, tokens, sc);
     const orc_model_config *c = &m->cfg;
     const float *hh = maybe_bf16(m, m->fn_out, m->T * c->dim, &sc[0]);
     const float *ww = maybe_bf16(m, m->arena[ORC_PARAM] + m->lm_head.off,
                                  (size_t)c->vocab_size * c->dim, &sc[1]);
     orc_matmul_nt(logits, hh, ww, m->T, c->vocab_size, c->dim);
-    for (int k = 0; k < 4; ++k) free(sc[k].buf);
+    for (int k = 0; k < 5; ++k) free(sc[k].buf);
 }
 
 double orc_now_seconds(void) {

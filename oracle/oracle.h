@@ -93,6 +93,20 @@ void orc_flash_attention_backward(const float *Q, const float *K, const float *V
                                   size_t n_q, size_t n_kv, size_t n_heads,
                                   size_t n_kv_heads, size_t head_dim, int causal,
                                   float *dQ, float *dK, float *dV);
+/* The same with the bf16-operand model of the MFMA kernels (an extension:
+ * the reference is fp32 throughout): P rounds to bf16 where it multiplies V
+ * (forward, 64-key tiles) and dO (dV); the unscaled dS = P (dP - D) rounds to
+ * bf16 where it multiplies Q and K, and 1/sqrt(d) scales the accumulated dQ
+ * and dK.  Inputs are expected already rounded to bf16. */
+void orc_flash_attention_forward_bf16ops(const float *Q, const float *K, const float *V,
+                                         size_t n_q, size_t n_kv, size_t n_heads,
+                                         size_t n_kv_heads, size_t head_dim, int causal,
+                                         float *out, float *lse);
+void orc_flash_attention_backward_bf16ops(const float *Q, const float *K, const float *V,
+                                          const float *O, const float *dO, const float *lse,
+                                          size_t n_q, size_t n_kv, size_t n_heads,
+                                          size_t n_kv_heads, size_t head_dim, int causal,
+                                          float *dQ, float *dK, float *dV);
 /* FA-2 preprocess of fa_bw_d.comp: D[q,h] = sum_d O*dO (fp64 as in
  * flash_attn.zig:330-334). */
 void orc_fa_bw_d(const float *O, const float *dO, size_t n_q, size_t n_heads,
@@ -113,6 +127,10 @@ void orc_cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
                       const float *lse, size_t n, size_t vocab, size_t dim, size_t chunk,
                       float z_loss_scale, float label_smoothing, float *d_h,
                       float *dW /* accumulated, nullable */);
+/* bf16-operand model of the MFMA path: dz rounded to bf16 before dh and dW. */
+void orc_cce_backward_bf16ops(const float *h, const float *w_lm, const uint32_t *tgt,
+                              const float *lse, size_t n, size_t vocab, size_t dim,
+                              float z_loss_scale, float label_smoothing, float *d_h, float *dW);
 /* train_decoder.zig:738-785: materialised softmax-CE loss and d_logits. */
 float orc_softmax_ce_loss(const float *logits, const uint32_t *tgt, size_t n_pos,
                           size_t vocab);

@@ -421,6 +421,20 @@ def test_flash_attention_bf16_mfma(case):
     note(f"  rel-L2 O={e[0]:.2e} dQ={e[1]:.2e} dK={e[2]:.2e} dV={e[3]:.2e}")
     assert max(abs(lse_r - lse)) < 2e-2
     assert all(x < BF16_TOL for x in e), e
+    # the oracle's bf16-operand model (P and dS rounded where the MFMAs take
+    # them) on the same O / lse / D inputs
+    m16 = []
+    for b in range(B):
+        sq = slice(b * n * H * hd, (b + 1) * n * H * hd)
+        sk = slice(b * n * Hkv * hd, (b + 1) * n * Hkv * hd)
+        m16.append(O.flash_backward(Qr[sq], Kr[sk], Vr[sk], o_r[sq], dOr[sq],
+                                    lse_r[b * n * H:(b + 1) * n * H], n, n, H, Hkv, hd, causal,
+                                    bf16_ops=True))
+    dq16, dk16, dv16 = (np.concatenate([x[i] for x in m16]) for i in range(3))
+    e16 = [rel_l2(dq16, dq), rel_l2(dk16, dk), rel_l2(dv16, dv)]
+    note(f"  vs the bf16-operand oracle dQ={e16[0]:.2e} dK={e16[1]:.2e} dV={e16[2]:.2e}")
+    # same roundings at the same points: only fp32 summation order differs
+    assert all(x < 1e-4 for x in e16), e16
     # the fused backward (bf16 dS workspace + dQ GEMM where the shape allows)
     ws_bytes = K.fa_backward_workspace_bytes(p)
     note(f"  fused path: workspace {ws_bytes} bytes")

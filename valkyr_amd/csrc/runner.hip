@@ -120,7 +120,9 @@ struct vkh_runner {
     uint32_t *tok_d = nullptr, *tgt_d = nullptr;
     uint32_t *tok_h = nullptr, *tgt_h = nullptr;
     float *loss_h = nullptr;
-    hipEvent_t upload_done = nullptr, loss_ready = nullptr;
+    // loss staging (pinned): slot 0 for step / forward_backward, slot 1 for
+    // the tick API's gate, each with its own event
+    hipEvent_t upload_done = nullptr, loss_ready = nullptr, tick_loss_ready = nullptr;
     hipStream_t own = nullptr, cur = nullptr;
     // Ordering across streams: every enqueue ends by recording ev_done on the
     // stream it used; an enqueue on another stream first waits for it, and
@@ -129,7 +131,7 @@ struct vkh_runner {
     hipStream_t last_st = nullptr;
     uint32_t step_t = 1;  // transformer.zig:940
     float loss_target = 0.f;
-    bool loss_pending = false, batch_ready = false;
+    bool loss_pending = false, tick_loss_pending = false, batch_ready = false;
     // the tick API's cached last loss (runner.zig:932-945)
     bool has_last = false;
     float last_loss_v = 0.f;
@@ -152,6 +154,7 @@ struct vkh_runner {
         if (loss_h) (void)hipHostFree(loss_h);
         if (upload_done) (void)hipEventDestroy(upload_done);
         if (loss_ready) (void)hipEventDestroy(loss_ready);
+        if (tick_loss_ready) (void)hipEventDestroy(tick_loss_ready);
         if (own) (void)hipStreamDestroy(own);
     }
 
@@ -289,6 +292,7 @@ struct vkh_runner {
         cur = own;
         VKH_HIP(hipEventCreateWithFlags(&upload_done, hipEventDisableTiming));
         VKH_HIP(hipEventCreateWithFlags(&loss_ready, hipEventDisableTiming));
+        VKH_HIP(hipEventCreateWithFlags(&tick_loss_ready, hipEventDisableTiming));
         VKH_HIP(hipEventCreateWithFlags(&ev_done, hipEventDisableTiming));
         VKH_HIP(hipHostMalloc((void **)&tok_h, (size_t)T * 4, hipHostMallocDefault));
         VKH_HIP(hipHostMalloc((void **)&tgt_h, (size_t)T * 4, hipHostMallocDefault));
@@ -930,6 +934,14 @@ struct vkh_runner {
         loss_pending = true;
         return VKH_OK;
     }
+    // the tick API's staging: only ticks write it, so the gate sees what
+    // earlier ticks measured whatever other calls ran in between
+    vkh_status record_tick_loss() {
+        VKH_HIP(hipMemcpyAsync(loss_h + 1, loss_mean, 4, hipMemcpyDeviceToHost, cur));
+        VKH_HIP(hipEventRecord(tick_loss_ready, cur));
+        tick_loss_pending = true;
+        return VKH_OK;
+    }
 
     // Start enqueueing on stream s after the runner's last work, whichever
     // stream that went to (on the same stream the wait is already implied;
@@ -967,7 +979,7 @@ struct vkh_runner {
         else
             VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
                                 cce_work, cur));
-        return record_loss();
+        return record_tick_loss();
     }
 
     vkh_status step_enqueue(bool with_adam) {
@@ -1447,8 +1459,8 @@ vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
     if (!r->batch_ready) return fail(VKH_ERR_INVALID_ARGUMENT, "no train batch uploaded");
     if (budget.mode > VKH_BUDGET_EITHER) return fail(VKH_ERR_INVALID_ARGUMENT, "unknown budget mode %u", budget.mode);
     const auto t0 = std::chrono::steady_clock::now();
-    if (r->loss_pending && hipEventQuery(r->loss_ready) == hipSuccess) {
-        r->last_loss_v = r->loss_h[0];
+    if (r->tick_loss_pending && hipEventQuery(r->tick_loss_ready) == hipSuccess) {
+        r->last_loss_v = r->loss_h[1];
         r->has_last = true;
     }
     out->has_loss = r->has_last ? 1u : 0u;
@@ -1476,7 +1488,7 @@ vkh_status vkh_runner_tick_frame_train(vkh_runner *r, vkh_stream stream,
     }
     if (st == VKH_OK) {
         if (decay) st = r->loss_eval_enqueue();
-        else if (n > 0) st = r->record_loss();
+        else if (n > 0) st = r->record_tick_loss();
     }
     const vkh_status se = r->end_on();
     if (st == VKH_OK) st = se;
