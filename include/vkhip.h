@@ -569,6 +569,17 @@ vkh_status vkh_rmsnorm_forward(const float *x, const float *w, float *y, uint32_
 vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w, float *dx,
                                 const float *residual, float *dw, uint32_t n_rows, uint32_t dim,
                                 float eps, uint32_t gemma_quirk, vkh_stream stream);
+/* No counterpart in the reference: vkh_rmsnorm_backward for callers that
+ * cannot allocate (code under HIP graph capture, serving loops, harnesses that
+ * forbid hipMalloc).  Same kernels and results (bit for bit); the gain-gradient
+ * partials live in a fixed 8 MiB per-device array inside the library instead
+ * of memory it allocates, so the call allocates nothing.  Limit: dim <= 4096
+ * (VKH_ERR_UNSUPPORTED beyond).  Calls on one GPU share that array: calls that
+ * may overlap in time on one GPU (different streams without ordering) race. */
+vkh_status vkh_rmsnorm_backward_noalloc(const float *dy, const float *x, const float *w,
+                                        float *dx, const float *residual, float *dw,
+                                        uint32_t n_rows, uint32_t dim, float eps,
+                                        uint32_t gemma_quirk, vkh_stream stream);
 /* shaders/swiglu_forward.comp / swiglu_backward.comp (SwigluPush {n}) */
 vkh_status vkh_swiglu_forward(const float *pre_gate, const float *up, float *gated, size_t n,
                               vkh_stream stream);

@@ -217,6 +217,7 @@ SIGNATURES = [
     ("vkh_cce_backward", ST, [C.POINTER(CceParams), P, P, P, P, P, P, U32, P]),
     ("vkh_rmsnorm_forward", ST, [P, P, P, U32, U32, F, U32, P]),
     ("vkh_rmsnorm_backward", ST, [P, P, P, P, P, P, U32, U32, F, U32, P]),
+    ("vkh_rmsnorm_backward_noalloc", ST, [P, P, P, P, P, P, U32, U32, F, U32, P]),
     ("vkh_swiglu_forward", ST, [P, P, P, SZ, P]),
     ("vkh_swiglu_backward", ST, [P, P, P, P, P, SZ, P]),
     ("vkh_qk_rope_forward", ST, [C.POINTER(RopeParams), P, P, P, P, P]),

@@ -467,6 +467,58 @@ vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w,
     return VKH_OK;
 }
 
+// ── the allocation-free RMSNorm backward ───────────────────────────────
+// The gain-gradient partials (one row of `dim` floats per block of the
+// backward kernel, at most 512 blocks and dim <= 4096) live in a fixed device
+// array instead of the lease above, so a call allocates nothing (for callers
+// under graph capture or in loops that must not call hipMalloc).  Each GPU
+// holds its own copy for the life of the process; its device address is
+// looked up once per device and only that address is handed to kernels.
+// Every block overwrites its whole partial row before the column sum reads
+// it, so nothing needs clearing between calls.
+constexpr size_t kNoAllocPartialFloats = 512 * 4096;  // 8 MiB
+static __device__ __align__(256) float scratch[kNoAllocPartialFloats];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float *g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+static vkh_status noalloc_scratch(float **out) {
+    int dev = 0;
+    VKH_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices) return fail(VKH_ERR_UNSUPPORTED, "device index %d >= %d", dev, kMaxDevices);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void *p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+        if (!p) return fail(VKH_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+        g_scratch_ptr[dev] = (float *)p;
+    }
+    *out = g_scratch_ptr[dev];
+    return VKH_OK;
+}
+
+vkh_status vkh_rmsnorm_backward_noalloc(const float *dy, const float *x, const float *w,
+                                        float *dx, const float *residual, float *dw,
+                                        uint32_t n_rows, uint32_t dim, float eps, uint32_t gq,
+                                        vkh_stream stream) {
+    CHECK_ARG(dy && x && w && dx, "null pointer");
+    if (dim > 4096) return fail(VKH_ERR_UNSUPPORTED, "rmsnorm_backward_noalloc: dim %u > 4096", dim);
+    const size_t need = rmsnorm_partial_floats((int)n_rows, (int)dim);
+    if (need > kNoAllocPartialFloats)
+        return fail(VKH_ERR_UNSUPPORTED, "rmsnorm_backward_noalloc: %zu partial floats > %zu",
+                    need, kNoAllocPartialFloats);
+    float *partial = nullptr;
+    VKH_TRY(noalloc_scratch(&partial));
+    hipError_t e = rmsnorm_backward(dy, x, w, dx, nullptr, residual, dw, partial, n_rows, dim, eps,
+                                    gq ? 1 : 0, S(stream));
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm_backward_noalloc");
+    return VKH_OK;
+}
+
 vkh_status vkh_swiglu_forward(const float *pg, const float *up, float *g, size_t n,
                               vkh_stream stream) {
     CHECK_ARG(pg && up && g, "null pointer");

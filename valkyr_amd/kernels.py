@@ -137,6 +137,14 @@ def rmsnorm_backward(dy, x, w, dx, dw=None, n_rows=0, dim=0, eps=1e-6, gemma_qui
                                      dim, eps, int(gemma_quirk), _s(stream)))
 
 
+def rmsnorm_backward_noalloc(dy, x, w, dx, dw=None, n_rows=0, dim=0, eps=1e-6,
+                             gemma_quirk=False, residual=None, stream=None):
+    """vkh_rmsnorm_backward with the gain partials in the library's fixed
+    per-device array: no allocation; calls on one GPU must not overlap."""
+    check(lib().vkh_rmsnorm_backward_noalloc(_p(dy), _p(x), _p(w), _p(dx), _p(residual), _p(dw),
+                                             n_rows, dim, eps, int(gemma_quirk), _s(stream)))
+
+
 def swiglu_forward(pre_gate, up, gated, n, stream=None):
     check(lib().vkh_swiglu_forward(_p(pre_gate), _p(up), _p(gated), n, _s(stream)))
 
