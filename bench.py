@@ -11,9 +11,13 @@ dQ kernels) at config 2 (B=4, S=2048, 16/8 heads, hd 128, causal, bf16
 Q/K/V/dO and bf16 O from the forward), timed with HIP events on the stream it
 runs on; its algorithmic work is 10 * B * Hq * hd * S(S+1)/2 = 171.88 GFLOP
 per call.
-`cpu_baseline` is the C oracle (a scalar restatement of valkyr's CPU
-reference path) timed on this host on a bounded sample and scaled to
-tokens/s of the same step (see `sample`).
+`reference_precision_step` is the same step with fp32 operands throughout (the
+reference's own precision).
+`cpu_baseline` is the C oracle (a restatement of valkyr's CPU reference path,
+fp64 accumulators) timed on this host on a bounded sample, each cost timed
+directly, scaled to tokens/s of the same step (see `sample`): all host threads
+(`value`, OpenMP over independent outputs, same bits as one thread) and one
+thread (`single_thread`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
                        [--no-cpu-baseline] [--fa-reps R]
@@ -78,12 +82,15 @@ def step_flops(c) -> float:
     return gemm + cce + attn
 
 
-def bench_step(args, dev_info):
+def bench_step(args, dev_info, precision=None, steps=None, warmup=None):
     import valkyr_amd as v
     from valkyr_amd.device import Event
 
     c = dict(QWEN3_06B)
-    prec = 1 if args.precision == "bf16" else 0
+    precision = precision or args.precision
+    steps = steps or args.steps
+    warmup = args.warmup if warmup is None else warmup
+    prec = 1 if precision == "bf16" else 0
     cfg = v.make_config(**c, precision=prec)
     r = v.Runner(cfg)
     r.init_random(seed=20261201, std=0.02)
@@ -93,7 +100,7 @@ def bench_step(args, dev_info):
     tgt = rng.integers(0, c["vocab_size"], T, dtype=np.uint32)
     print(f"[bench] runner ready: {r.param_count():,} params, "
           f"{r.device_bytes() / 2**30:.1f} GiB device memory", file=sys.stderr, flush=True)
-    for _ in range(args.warmup):
+    for _ in range(warmup):
         r.step_async(tok, tgt)
     r.synchronize()
     loss0 = r.last_loss()
@@ -101,7 +108,7 @@ def bench_step(args, dev_info):
     r.synchronize()
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(args.steps):
+    for _ in range(steps):
         r.step_async(tok, tgt)
     r.synchronize()
     e1.record()
@@ -109,10 +116,10 @@ def bench_step(args, dev_info):
     t1 = time.perf_counter()
     wall = t1 - t0
     loss1 = r.last_loss()
-    ms = 1000.0 * wall / args.steps
-    tokens_s = T * args.steps / wall
+    ms = 1000.0 * wall / steps
+    tokens_s = T * steps / wall
     flops = step_flops(c)
-    print(f"[bench] step {ms:.2f} ms, {tokens_s:,.0f} tok/s, loss {loss0:.4f} -> {loss1:.4f}",
+    print(f"[bench] {precision} step {ms:.2f} ms, {tokens_s:,.0f} tok/s, loss {loss0:.4f} -> {loss1:.4f}",
           file=sys.stderr, flush=True)
     r.close()
     return dict(ms=ms, tokens_s=tokens_s, T=T, flops=flops, loss_first=loss0, loss_last=loss1,
@@ -296,56 +303,95 @@ def measured_traffic(name):
 
 
 def cpu_baseline(args):
-    """The C oracle (single thread) on a bounded sample of the step, scaled to tokens/s.
+    """valkyr's CPU reference path (the C oracle: a restatement of src/cpu/*.zig with its
+    fp64 accumulators, parallel only over independent outputs, so every thread count gives
+    the same bits) on this host, scaled to tokens/s of the config-3 step.
 
-    Sample: the config-3 model shape with 1 and 2 layers at T = 16 tokens
-    (one sequence), full 151936 vocab, tied embeddings; per-layer and
-    per-head costs per token come from the two timings, Adam from the
-    1-layer model's optimizer step scaled by parameter count.  Extrapolated:
-    t(step) = 2048 * (28 * c_layer + c_head) + t_adam(596M params)."""
+    Each cost is timed directly, not as a difference of two runs: the oracle model keeps
+    per-phase wall clocks.  Sample: the config-3 widths with 2 layers and the full tied
+    151936 vocabulary on one sequence of 32 tokens (16 for the one-thread figure; one
+    warm-up pass, then timed passes);
+    the causal attention at the real sequence length timed separately on one 256-position
+    sequence (16/8 heads of 128) and scaled by (512 / 256)^2; Adam over the sample's
+    187 M parameters scaled to 596 M.  Extrapolated per step:
+      t = 28 * (2048 * c_layer + 4 * t_attn(512)) + 2048 * c_head + t_adam(596 M),
+    with c_layer the per-token layer cost net of attention.  Reported for all host threads
+    (value) and for one thread (the reference oracle is single-threaded scalar code)."""
     import oracle as O
 
     c = dict(QWEN3_06B)
-    Ts = 16
+    Sa, L = 256, 2
+    T = c["n_pos"] * c["n_seqs"]
+    n_full = 596_049_920
+    H, Hkv, hd = c["n_heads"], c["n_kv_heads"], c["head_dim"]
+    qa, ka, va = O.normal(Sa * H * hd, 21), O.normal(Sa * Hkv * hd, 22), O.normal(Sa * Hkv * hd, 23)
+    doa = O.normal(Sa * H * hd, 24, 0.1)
+    all_threads = O.get_threads()
 
-    def model(nl):
-        m = O.Model(dim=c["dim"], n_heads=c["n_heads"], n_kv_heads=c["n_kv_heads"],
-                    head_dim=c["head_dim"], ff_dim=c["ff_dim"], seq_len=Ts, n_seqs=1,
-                    n_layers=nl, vocab_size=c["vocab_size"], rms_eps=c["rms_eps"], causal=1,
-                    rotary_dim=c["rotary_dim"], rope_theta=c["rope_theta"], qk_norm=1, lr=1e-4,
-                    beta1=0.9, beta2=0.999, eps_adam=1e-8, lora_targets=0, lora_rank=0,
-                    lora_alpha=0.0, lora_lr_b_scale=1.0, tied_embeddings=1, bf16_operands=0)
+    def model(Ts):
+        m = O.Model(dim=c["dim"], n_heads=H, n_kv_heads=Hkv, head_dim=hd, ff_dim=c["ff_dim"],
+                    seq_len=Ts, n_seqs=1, n_layers=L, vocab_size=c["vocab_size"],
+                    rms_eps=c["rms_eps"], causal=1, rotary_dim=c["rotary_dim"],
+                    rope_theta=c["rope_theta"], qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999,
+                    eps_adam=1e-8, lora_targets=0, lora_rank=0, lora_alpha=0.0,
+                    lora_lr_b_scale=1.0, tied_embeddings=1, bf16_operands=0)
         m.init_random(3, std=0.02)
         return m
 
-    tok = O.ids(Ts, 11, c["vocab_size"])
-    tgt = O.ids(Ts, 12, c["vocab_size"])
-    m1 = model(1)
-    t0 = O.now()
-    m1.forward_backward(tok, tgt)
-    t_fb1 = O.now() - t0
-    t0 = O.now()
-    m1.adam()
-    t_adam1 = O.now() - t0
-    n1 = sum(m1.tensor(0, l, w).size for l, w in [(-1, 0), (-1, 1)] + [(0, i) for i in range(11)])
-    del m1
-    m2 = model(2)
-    t0 = O.now()
-    m2.forward_backward(tok, tgt)
-    t_fb2 = O.now() - t0
-    del m2
-    c_layer = max(t_fb2 - t_fb1, 1e-9) / Ts
-    c_head = max(t_fb1 / Ts - c_layer, 0.0)
-    T = c["n_pos"] * c["n_seqs"]
-    n_full = 596_049_920
-    t_step = T * (c["n_layers"] * c_layer + c_head) + t_adam1 * n_full / n1
-    return dict(value=T / t_step, unit="tokens/s", cores=1, kind="port",
-                sample=(f"C oracle (src/cpu/*.zig restatement, 1 thread, fp64 accumulators) on the "
-                        f"config-3 shape at T={Ts}: 1-layer fwd+bwd {t_fb1:.1f} s, 2-layer "
-                        f"{t_fb2:.1f} s, Adam over {n1:,} params {t_adam1:.2f} s; scaled to 28 "
-                        f"layers x 2048 tokens + Adam over {n_full:,} params "
-                        f"= {t_step:,.0f} s/step (extrapolated)"),
-                seconds_measured=round(t_fb1 + t_fb2 + t_adam1, 1))
+    def measure(threads, reps, Ts):
+        O.set_threads(all_threads)
+        m = model(Ts)
+        n_sample = sum(m.tensor(0, l, w).size for l, w in [(-1, 0), (-1, 1)] +
+                       [(l, i) for l in range(L) for i in range(11)])
+        tok, tgt = O.ids(Ts, 11, c["vocab_size"]), O.ids(Ts, 12, c["vocab_size"])
+        m.forward_backward(tok, tgt)  # warm-up: first touch of the sample's memory
+        m.adam()
+        O.set_threads(threads)
+        runs = []
+        for _ in range(reps):
+            m.reset_phases()
+            m.forward_backward(tok, tgt)
+            m.adam()
+            ph = m.phase_seconds()
+            t0 = O.now()
+            o, lse = O.flash_forward(qa, ka, va, Sa, Sa, H, Hkv, hd, True)
+            O.flash_backward(qa, ka, va, o, doa, lse, Sa, Sa, H, Hkv, hd, True)
+            ph["attn_256"] = O.now() - t0
+            runs.append(ph)
+        del m
+        ph = {k: float(np.median([r[k] for r in runs])) for k in runs[0]}
+        c_layer = (ph["layer_fwd"] + ph["layer_bwd"] - ph["attn_fwd"] - ph["attn_bwd"]) / (L * Ts)
+        t_attn512 = ph["attn_256"] * (c["n_pos"] / Sa) ** 2
+        c_head = ph["head"] / Ts
+        t_adam = ph["adam"] * n_full / n_sample
+        t_step = c["n_layers"] * (T * c_layer + c["n_seqs"] * t_attn512) + T * c_head + t_adam
+        return dict(tokens_s=T / t_step, s_per_step=t_step, per_token_layer_s=c_layer,
+                    attn_seq512_s=t_attn512, per_token_head_s=c_head, adam_596m_s=t_adam,
+                    measured_s=sum(sum(r.values()) for r in runs), runs=reps, tokens=Ts,
+                    n_sample=n_sample)
+
+    try:
+        multi = measure(all_threads, 3, 32)
+        single = measure(1, 1, 16)
+    finally:
+        O.set_threads(all_threads)
+    return dict(value=round(multi["tokens_s"], 3), unit="tokens/s", cores=all_threads,
+                kind="port",
+                sample=(f"C oracle (src/cpu/*.zig restatement, fp64 accumulators, OpenMP over "
+                        f"independent outputs) on this host: config-3 widths, {L} layers, tied "
+                        f"151936 vocabulary, 32 tokens (median of {multi['runs']} passes; 16 tokens, "
+                        f"1 pass on 1 thread) + causal "
+                        f"attention on one {Sa}-position sequence scaled by (512/{Sa})^2, Adam "
+                        f"scaled from {multi['n_sample']:,} to {n_full:,} params; per step = 28 layers x "
+                        f"2048 tokens (extrapolated): {multi['s_per_step']:,.0f} s on "
+                        f"{all_threads} threads, {single['s_per_step']:,.0f} s on 1 thread"),
+                single_thread={"value": round(single["tokens_s"], 3), "cores": 1,
+                               "s_per_step": round(single["s_per_step"], 1)},
+                all_threads={k: (round(v, 6) if isinstance(v, float) else v)
+                             for k, v in multi.items()},
+                single_thread_detail={k: (round(v, 6) if isinstance(v, float) else v)
+                                      for k, v in single.items()},
+                seconds_measured=round(multi["measured_s"] + single["measured_s"], 1))
 
 
 def bench_config(name, args):
@@ -540,6 +586,8 @@ def main():
         print(json.dumps({"ms_per_step": round(st["ms"], 3), "tokens_s": round(st["tokens_s"], 1)}),
               flush=True)
         return
+    # the same step at the reference's own precision (fp32 operands throughout)
+    st32 = bench_step(args, None, precision="fp32", steps=max(3, args.steps // 4), warmup=2)
     fa = bench_fa_bwd(args)
     if args.calib_copy:
         calib_copy()
@@ -567,6 +615,14 @@ def main():
                    "master_weights": "fp32", "optimizer": "adam",
                    "parallelism": "single GPU"},
         "step_tflops": round(st["flops"] / (st["ms"] * 1e-3) / 1e12, 1),
+        "reference_precision_step": {
+            "dtype": "fp32", "note": "config 3 with fp32 operands on v_mfma_f32_16x16x4_f32 "
+                                     "(the reference computes in fp32 throughout)",
+            "ms_per_step": round(st32["ms"], 3), "tokens_s": round(st32["tokens_s"], 1),
+            "steps": max(3, args.steps // 4),
+            "tflops": round(st32["flops"] / (st32["ms"] * 1e-3) / 1e12, 1),
+            "frac_fp32_peak": round(st32["flops"] / (st32["ms"] * 1e-3) / 1e12 / FP32_PEAK_TFLOPS, 4),
+            "loss": [round(st32["loss_first"], 4), round(st32["loss_last"], 4)]},
         "step_mfu": round(mfu, 4),
         "loss": [round(st["loss_first"], 4), round(st["loss_last"], 4)],
         "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (config 2)",

@@ -116,6 +116,8 @@ def _declare(L):
     d("orc_model_step", C.c_float, C.c_void_p, U32P, U32P)
     d("orc_model_step_t", C.c_uint32, C.c_void_p)
     d("orc_model_set_step_t", None, C.c_void_p, C.c_uint32)
+    d("orc_model_phase_seconds", None, C.c_void_p, np.ctypeslib.ndpointer(dtype=np.float64, flags="C_CONTIGUOUS"))
+    d("orc_model_reset_phases", None, C.c_void_p)
     d("orc_model_forward_logits", None, C.c_void_p, U32P, F32P)
     d("orc_now_seconds", C.c_double)
     U64P = np.ctypeslib.ndpointer(dtype=np.uint64, flags="C_CONTIGUOUS")
@@ -447,6 +449,19 @@ class Model:
     @step_t.setter
     def step_t(self, t):
         lib().orc_model_set_step_t(self._h, int(t))
+
+    PHASES = ("layer_fwd", "layer_bwd", "attn_fwd", "attn_bwd", "head", "adam")
+
+    def phase_seconds(self):
+        """Wall seconds per phase since the last reset_phases(): layer forwards
+        and backwards (attention included), the attention inside them, the head
+        (embedding, final norm, CCE, tied sum) and Adam."""
+        out = np.zeros(len(self.PHASES), np.float64)
+        lib().orc_model_phase_seconds(self._h, out)
+        return dict(zip(self.PHASES, out.tolist()))
+
+    def reset_phases(self):
+        lib().orc_model_reset_phases(self._h)
 
     def forward_logits(self, tokens):
         out = np.empty(self.T * self.cfg.vocab_size, np.float32)

@@ -889,7 +889,24 @@ struct orc_model {
     float *x_emb, *fn_out, *lse, *loss_row;
     uint32_t step_t;
     uint32_t *tokens;
+    /* wall seconds spent per phase since the last reset (ORC_PHASE_*) */
+    double phase_s[ORC_N_PHASES];
+    float *dW_lm_tied; /* the tied head's dW_lm, kept between steps (zeroed per step) */
 };
+
+static double now_s(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (double)ts.tv_sec + 1e-9 * (double)ts.tv_nsec;
+}
+
+void orc_model_phase_seconds(const orc_model *m, double *out) {
+    for (int i = 0; i < ORC_N_PHASES; ++i) out[i] = m->phase_s[i];
+}
+
+void orc_model_reset_phases(orc_model *m) {
+    for (int i = 0; i < ORC_N_PHASES; ++i) m->phase_s[i] = 0;
+}
 
 static void proj_shape(const orc_model *m, int p, size_t *N, size_t *K) {
     const orc_model_config *c = &m->cfg;
@@ -988,6 +1005,7 @@ void orc_model_destroy(orc_model *m) {
     free(m->acts); free(m->ls);
     for (int k = 0; k < 4; ++k) free(m->arena[k]);
     free(m->x_emb); free(m->fn_out); free(m->lse); free(m->loss_row); free(m->tokens);
+    free(m->dW_lm_tied);
     free(m);
 }
 
@@ -1132,10 +1150,12 @@ static void layer_forward(orc_model *m, int l, const float *x_in, scratch_t *sc)
     const float *kk = maybe_bf16(m, a->k, T * m->kvd, &sc[1]);
     const float *vv = maybe_bf16(m, a->v, T * m->kvd, &sc[2]);
     /* bf16 operands: the kernels' 64-key tiles and bf16 P (flash_forward) */
+    const double ta = now_s();
     for (uint32_t b = 0; b < c->n_seqs; ++b)
         flash_forward(qq + b * S * m->qd, kk + b * S * m->kvd, vv + b * S * m->kvd, S, S, H, Hkv,
                       hd, c->causal != 0, 16, c->bf16_operands ? 64 : 16, c->bf16_operands != 0,
                       a->attn_out + b * S * m->qd, a->lse + b * S * H);
+    m->phase_s[ORC_PHASE_ATTN_FWD] += now_s() - ta;
     float *o = malloc(T * D * sizeof(float));
     proj_forward(m, l, 3, a->attn_out, P + s->t[4].off, o, &sc[0], &sc[1]);
     for (size_t i = 0; i < T * D; ++i) a->mid[i] = x_in[i] + o[i];
@@ -1185,11 +1205,13 @@ static void layer_backward(orc_model *m, int l, const float *x_in, const float *
     const float *dd = maybe_bf16(m, d_attn_out, T * m->qd, &sc[3]);
     /* bf16 operands: D = rowsum(O dO) over the bf16 O the kernels keep */
     const float *oo = maybe_bf16(m, a->attn_out, T * m->qd, &sc[4]);
+    const double ta = now_s();
     for (uint32_t b = 0; b < c->n_seqs; ++b)
         flash_backward(qq + b * S * m->qd, kk + b * S * m->kvd, vv + b * S * m->kvd,
                        oo + b * S * m->qd, dd + b * S * m->qd, a->lse + b * S * H, S, S, H, Hkv,
                        hd, c->causal != 0, c->bf16_operands != 0, dQ + b * S * m->qd,
                        dK + b * S * m->kvd, dV + b * S * m->kvd);
+    m->phase_s[ORC_PHASE_ATTN_BWD] += now_s() - ta;
     float *dQ2 = malloc(T * m->qd * sizeof(float)), *dK2 = malloc(T * m->kvd * sizeof(float));
     if (c->rotary_dim > 0) {
         orc_rope_backward_batched(dQ2, dQ, T, H, hd, c->rotary_dim, c->rope_theta, S);
@@ -1224,10 +1246,15 @@ static void model_forward(orc_model *m, const uint32_t *tokens, scratch_t *sc) {
     float *P = m->arena[ORC_PARAM];
     size_t T = m->T, D = c->dim;
     memcpy(m->tokens, tokens, T * sizeof(uint32_t));
+    double t0 = now_s();
     orc_embedding_forward(P + m->embed.off, tokens, T, D, m->x_emb);
+    double t1 = now_s();
     for (uint32_t l = 0; l < c->n_layers; ++l)
         layer_forward(m, l, l == 0 ? m->x_emb : m->acts[l - 1].y, sc);
+    double t2 = now_s();
     orc_rmsnorm_forward(m->acts[c->n_layers - 1].y, P + m->final_norm.off, T, D, c->rms_eps, 0, m->fn_out);
+    m->phase_s[ORC_PHASE_LAYER_FWD] += t2 - t1;
+    m->phase_s[ORC_PHASE_HEAD] += (t1 - t0) + (now_s() - t2);
 }
 
 float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
@@ -1238,6 +1265,7 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
     int lora = c->lora_targets != 0;
     scratch_t sc[5] = {{0}};
     model_forward(m, tokens, sc);
+    double t0 = now_s();
     const float *hh = maybe_bf16(m, m->fn_out, T * D, &sc[0]);
     const float *ww = maybe_bf16(m, P + m->lm_head.off, V * D, &sc[1]);
     size_t chunk = V < 1024 ? V : 1024;
@@ -1246,8 +1274,9 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
     float *d_fn = malloc(T * D * sizeof(float));
     float *dW_lm = NULL;
     if (!lora) {
-        dW_lm = c->tied_embeddings ? calloc(V * D, sizeof(float)) : G + m->lm_head.off;
-        if (!c->tied_embeddings) memset(dW_lm, 0, V * D * sizeof(float));
+        if (c->tied_embeddings && !m->dW_lm_tied) m->dW_lm_tied = malloc(V * D * sizeof(float));
+        dW_lm = c->tied_embeddings ? m->dW_lm_tied : G + m->lm_head.off;
+        memset(dW_lm, 0, V * D * sizeof(float));
     }
     cce_backward(hh, ww, targets, m->lse, T, V, D, 0, 0, c->bf16_operands != 0, d_fn, dW_lm);
     float *d_y = malloc(T * D * sizeof(float)), *d_x = malloc(T * D * sizeof(float));
@@ -1255,10 +1284,12 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
     if (!lora) memset(dw_fn, 0, D * sizeof(float));
     orc_rmsnorm_backward(d_fn, m->acts[c->n_layers - 1].y, P + m->final_norm.off, T, D,
                          c->rms_eps, 0, d_y, lora ? NULL : dw_fn);
+    double t1 = now_s();
     for (int l = (int)c->n_layers - 1; l >= 0; --l) {
         layer_backward(m, l, l == 0 ? m->x_emb : m->acts[l - 1].y, d_y, d_x, sc);
         float *t = d_y; d_y = d_x; d_x = t;
     }
+    double t2 = now_s();
     if (!lora) {
         float *dE = G + m->embed.off;
         memset(dE, 0, V * D * sizeof(float));
@@ -1266,11 +1297,12 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
         if (c->tied_embeddings) {
             /* tied: grad = dE (position-order row sums) + dW_lm */
             for (size_t i = 0; i < V * D; ++i) dE[i] = dW_lm[i] + dE[i];
-            free(dW_lm);
         }
     }
     free(d_fn); free(d_y); free(d_x);
     for (int k = 0; k < 5; ++k) free(sc[k].buf);
+    m->phase_s[ORC_PHASE_LAYER_BWD] += t2 - t1;
+    m->phase_s[ORC_PHASE_HEAD] += (t1 - t0) + (now_s() - t2);
     return loss;
 }
 
@@ -1286,6 +1318,7 @@ static void adam_span(orc_model *m, span sp, float lr) {
  * lr * lora_lr_b_scale) when LoRA is active. */
 void orc_model_adam(orc_model *m) {
     const orc_model_config *c = &m->cfg;
+    const double t0 = now_s();
     if (!c->lora_targets) {
         adam_span(m, m->embed, c->lr);
         for (uint32_t l = 0; l < c->n_layers; ++l)
@@ -1299,6 +1332,7 @@ void orc_model_adam(orc_model *m) {
                 adam_span(m, m->ls[l].lora_b[p], c->lr * c->lora_lr_b_scale);
             }
     }
+    m->phase_s[ORC_PHASE_ADAM] += now_s() - t0;
     m->step_t += 1;
 }
 

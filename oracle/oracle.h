@@ -196,6 +196,15 @@ void orc_model_adam(orc_model *m);
 float orc_model_step(orc_model *m, const uint32_t *tokens, const uint32_t *targets);
 uint32_t orc_model_step_t(const orc_model *m);
 void orc_model_set_step_t(orc_model *m, uint32_t t);
+/* Wall seconds spent per phase since the last reset (timing for the CPU
+ * baseline): layer forwards and backwards (attention included), the attention
+ * inside them, the head (embedding, final norm, CCE, tied sum) and Adam. */
+enum {
+    ORC_PHASE_LAYER_FWD = 0, ORC_PHASE_LAYER_BWD = 1, ORC_PHASE_ATTN_FWD = 2,
+    ORC_PHASE_ATTN_BWD = 3, ORC_PHASE_HEAD = 4, ORC_PHASE_ADAM = 5, ORC_N_PHASES = 6
+};
+void orc_model_phase_seconds(const orc_model *m, double *out);
+void orc_model_reset_phases(orc_model *m);
 /* forward only: logits [T, vocab] (runner forwardLogits). */
 void orc_model_forward_logits(orc_model *m, const uint32_t *tokens, float *logits);
 
