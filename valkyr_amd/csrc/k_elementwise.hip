@@ -77,23 +77,43 @@ __global__ void cast_bf16_k(const float *in, bf16 *out, size_t n, bool vec) {
 // sigmoid(z) = 1 / (1 + exp(-z))  (train_transformer.zig:832-834)
 __device__ __forceinline__ float sigmoidf_(float z) { return 1.0f / (1.0f + expf(-z)); }
 
+// Streaming kernels give each block one contiguous chunk (SW_U float4 per
+// thread, all loads issued before any store, non-temporal): on MI355X that
+// pattern measured 6.2 TB/s for a 1 GB copy against 5.0-5.3 TB/s for a
+// grid-stride loop.  The SwiGLU kernels take one row chunk per block
+// (blockIdx.y = row), so rows with their own leading dimensions need no
+// index division.
+constexpr int SW_U = 4;
+
+VKH_DEV float4 ldnt4(const float *p) {
+    const f32x4 v = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(p));
+    return make_float4(v.x, v.y, v.z, v.w);
+}
+
 // swiglu_forward.comp / train_transformer.zig:839-851
 template <typename TO>
-__global__ void swiglu_fwd_k(const float *pg, long ldpg, const float *up, long ldup, TO *g,
-                             long ldg, int rows, int cols4) {
-    const size_t n = (size_t)rows * cols4;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        const long r = (long)(i / cols4);
-        const int c = (int)(i % cols4) * 4;
-        float4 z = *reinterpret_cast<const float4 *>(pg + r * ldpg + c);
-        float4 u = *reinterpret_cast<const float4 *>(up + r * ldup + c);
+__global__ __launch_bounds__(NT) void swiglu_fwd_k(const float *pg, long ldpg, const float *up,
+                                                    long ldup, TO *g, long ldg, int cols4) {
+    const long r = blockIdx.y;
+    const int c0 = (int)blockIdx.x * NT * SW_U + (int)threadIdx.x;
+    float4 z[SW_U], u[SW_U];
+#pragma unroll
+    for (int k = 0; k < SW_U; ++k) {
+        const int c = 4 * (c0 + k * NT);
+        if (c0 + k * NT < cols4) {
+            z[k] = ldnt4(pg + r * ldpg + c);
+            u[k] = ldnt4(up + r * ldup + c);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < SW_U; ++k) {
+        if (c0 + k * NT >= cols4) continue;
         float4 o;
-        o.x = z.x * sigmoidf_(z.x) * u.x;
-        o.y = z.y * sigmoidf_(z.y) * u.y;
-        o.z = z.z * sigmoidf_(z.z) * u.z;
-        o.w = z.w * sigmoidf_(z.w) * u.w;
-        st4(g + r * ldg + c, o);
+        o.x = z[k].x * sigmoidf_(z[k].x) * u[k].x;
+        o.y = z[k].y * sigmoidf_(z[k].y) * u[k].y;
+        o.z = z[k].z * sigmoidf_(z[k].z) * u[k].z;
+        o.w = z[k].w * sigmoidf_(z[k].w) * u[k].w;
+        st4(g + r * ldg + 4 * (c0 + k * NT), o);
     }
 }
 
@@ -107,22 +127,30 @@ __device__ __forceinline__ void swiglu_bw1(float dg, float z, float u, float &dz
 
 // swiglu_backward.comp / train_transformer.zig:857-875
 template <typename TO>
-__global__ void swiglu_bwd_k(const float *dg, long lddg, const float *pg, long ldpg,
-                             const float *up, long ldup, TO *dpg, long lddpg, TO *dup,
-                             long lddup, int rows, int cols4) {
-    const size_t n = (size_t)rows * cols4;
-    const size_t stride = (size_t)gridDim.x * blockDim.x;
-    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
-        const long r = (long)(i / cols4);
-        const int c = (int)(i % cols4) * 4;
-        float4 d = *reinterpret_cast<const float4 *>(dg + r * lddg + c);
-        float4 z = *reinterpret_cast<const float4 *>(pg + r * ldpg + c);
-        float4 u = *reinterpret_cast<const float4 *>(up + r * ldup + c);
+__global__ __launch_bounds__(NT) void swiglu_bwd_k(const float *dg, long lddg, const float *pg,
+                                                    long ldpg, const float *up, long ldup, TO *dpg,
+                                                    long lddpg, TO *dup, long lddup, int cols4) {
+    const long r = blockIdx.y;
+    const int c0 = (int)blockIdx.x * NT * SW_U + (int)threadIdx.x;
+    float4 d[SW_U], z[SW_U], u[SW_U];
+#pragma unroll
+    for (int k = 0; k < SW_U; ++k) {
+        const int c = 4 * (c0 + k * NT);
+        if (c0 + k * NT < cols4) {
+            d[k] = ldnt4(dg + r * lddg + c);
+            z[k] = ldnt4(pg + r * ldpg + c);
+            u[k] = ldnt4(up + r * ldup + c);
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < SW_U; ++k) {
+        if (c0 + k * NT >= cols4) continue;
+        const int c = 4 * (c0 + k * NT);
         float4 oz, ou;
-        swiglu_bw1(d.x, z.x, u.x, oz.x, ou.x);
-        swiglu_bw1(d.y, z.y, u.y, oz.y, ou.y);
-        swiglu_bw1(d.z, z.z, u.z, oz.z, ou.z);
-        swiglu_bw1(d.w, z.w, u.w, oz.w, ou.w);
+        swiglu_bw1(d[k].x, z[k].x, u[k].x, oz.x, ou.x);
+        swiglu_bw1(d[k].y, z[k].y, u[k].y, oz.y, ou.y);
+        swiglu_bw1(d[k].z, z[k].z, u[k].z, oz.z, ou.z);
+        swiglu_bw1(d[k].w, z[k].w, u[k].w, oz.w, ou.w);
         st4(dpg + r * lddpg + c, oz);
         st4(dup + r * lddup + c, ou);
     }
@@ -204,9 +232,146 @@ VKH_DEV void adam4(f32x4 &p, const f32x4 &g, f32x4 &m, f32x4 &v, float lr, float
 }
 
 // Streaming update: every byte is touched once, so loads and stores are
-// non-temporal, and ADAM_U grid-stride iterations are in flight per thread.
-// pb (optional): bf16 copy of the updated parameters (the GEMM operand shadow).
-constexpr int ADAM_GRID = 256 * 32, ADAM_U = 2;  // 4 in flight measured no faster
+// non-temporal.  Each block updates one contiguous chunk of NT * ADAM_U
+// float4 (all loads issued before the first store), the pattern that
+// measured fastest for large streams on MI355X.  pb (optional): bf16 copy of
+// the updated parameters (the GEMM operand shadow).
+constexpr int ADAM_U = 4;
+
+__global__ __launch_bounds__(NT) void adam_chunk_k(float *p_, const float *g_, float *m_,
+                                                    float *v_, bf16 *pb, size_t n, float lr,
+                                                    float b1, float b2, float eps, float bc1,
+                                                    float bc2, float wd) {
+    const size_t n4 = n / 4;
+    f32x4 *p = reinterpret_cast<f32x4 *>(p_), *m = reinterpret_cast<f32x4 *>(m_),
+          *v = reinterpret_cast<f32x4 *>(v_);
+    const f32x4 *g = reinterpret_cast<const f32x4 *>(g_);
+    const size_t base = (size_t)blockIdx.x * (NT * ADAM_U) + threadIdx.x;
+    f32x4 pp[ADAM_U], gg[ADAM_U], mm[ADAM_U], vv[ADAM_U];
+#pragma unroll
+    for (int u = 0; u < ADAM_U; ++u) {
+        const size_t j = base + (size_t)u * NT;
+        if (j < n4) {
+            pp[u] = __builtin_nontemporal_load(&p[j]);
+            gg[u] = __builtin_nontemporal_load(&g[j]);
+            mm[u] = __builtin_nontemporal_load(&m[j]);
+            vv[u] = __builtin_nontemporal_load(&v[j]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < ADAM_U; ++u) {
+        const size_t j = base + (size_t)u * NT;
+        if (j >= n4) continue;
+        adam4(pp[u], gg[u], mm[u], vv[u], lr, b1, b2, eps, bc1, bc2, wd);
+        __builtin_nontemporal_store(pp[u], &p[j]);
+        __builtin_nontemporal_store(mm[u], &m[j]);
+        __builtin_nontemporal_store(vv[u], &v[j]);
+        if (pb) {
+            bf16x4 b;
+            b[0] = (bf16)pp[u].x; b[1] = (bf16)pp[u].y; b[2] = (bf16)pp[u].z; b[3] = (bf16)pp[u].w;
+            __builtin_nontemporal_store(b, reinterpret_cast<bf16x4 *>(pb) + j);
+        }
+    }
+    // the last n % 4 elements
+    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) {
+        const size_t k = 4 * n4 + threadIdx.x;
+        adam1(p_[k], g_[k], m_[k], v_[k], lr, b1, b2, eps, bc1, bc2, wd);
+        if (pb) pb[k] = (bf16)p_[k];
+    }
+}
+
+// Adam over a span that holds norm gains whose gradients are still per-block
+// partial sums (the RMSNorm backward kernels' [nparts][stride] partials):
+// blocks [0, nchunk) run the chunked update on every other element; each
+// following block takes GN_COLS columns of one gain, sums their partials in
+// the column-sum kernel's order (GN_GROUPS strided groups, four accumulators,
+// then the groups in order), stores the gradient and updates those elements.
+constexpr int GN_COLS = 16, GN_GROUPS = 16;
+static_assert(GN_COLS * GN_GROUPS == NT, "gain block shape");
+
+__global__ __launch_bounds__(NT) void adam_gains_k(float *p_, float *g_, float *m_, float *v_,
+                                                    bf16 *pb, size_t n, unsigned nchunk,
+                                                    AdamGains gs, float lr, float b1, float b2,
+                                                    float eps, float bc1, float bc2, float wd) {
+    if (blockIdx.x < nchunk) {
+        const size_t n4 = n / 4;
+        f32x4 *p = reinterpret_cast<f32x4 *>(p_), *m = reinterpret_cast<f32x4 *>(m_),
+              *v = reinterpret_cast<f32x4 *>(v_);
+        const f32x4 *g = reinterpret_cast<const f32x4 *>(g_);
+        const size_t base = (size_t)blockIdx.x * (NT * ADAM_U) + threadIdx.x;
+        auto gain_elem = [&](size_t j) {
+            bool in = false;
+#pragma unroll
+            for (int i = 0; i < kAdamMaxGains; ++i)
+                in |= i < gs.n && 4 * j - gs.g[i].off < (size_t)gs.g[i].dim;
+            return in;
+        };
+        f32x4 pp[ADAM_U], gg[ADAM_U], mm[ADAM_U], vv[ADAM_U];
+#pragma unroll
+        for (int u = 0; u < ADAM_U; ++u) {
+            const size_t j = base + (size_t)u * NT;
+            if (j < n4 && !gain_elem(j)) {
+                pp[u] = __builtin_nontemporal_load(&p[j]);
+                gg[u] = __builtin_nontemporal_load(&g[j]);
+                mm[u] = __builtin_nontemporal_load(&m[j]);
+                vv[u] = __builtin_nontemporal_load(&v[j]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < ADAM_U; ++u) {
+            const size_t j = base + (size_t)u * NT;
+            if (j >= n4 || gain_elem(j)) continue;
+            adam4(pp[u], gg[u], mm[u], vv[u], lr, b1, b2, eps, bc1, bc2, wd);
+            __builtin_nontemporal_store(pp[u], &p[j]);
+            __builtin_nontemporal_store(mm[u], &m[j]);
+            __builtin_nontemporal_store(vv[u], &v[j]);
+            if (pb) {
+                bf16x4 b;
+                b[0] = (bf16)pp[u].x; b[1] = (bf16)pp[u].y; b[2] = (bf16)pp[u].z; b[3] = (bf16)pp[u].w;
+                __builtin_nontemporal_store(b, reinterpret_cast<bf16x4 *>(pb) + j);
+            }
+        }
+        return;
+    }
+    // a gain block: which gain, which columns
+    unsigned blk = blockIdx.x - nchunk;
+    int gi = 0;
+    for (; gi < gs.n; ++gi) {
+        const unsigned nb = (gs.g[gi].dim + GN_COLS - 1) / GN_COLS;
+        if (blk < nb) break;
+        blk -= nb;
+    }
+    if (gi >= gs.n) return;
+    const AdamGain G = gs.g[gi];
+    __shared__ float sh[GN_GROUPS][GN_COLS + 1];
+    const int cl = threadIdx.x % GN_COLS, grp = threadIdx.x / GN_COLS;
+    const int c = (int)blk * GN_COLS + cl;
+    float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+    if (c < (int)G.dim) {
+        int b = grp;
+        for (; b + 3 * GN_GROUPS < G.nparts; b += 4 * GN_GROUPS) {
+            a0 += G.partial[(long)b * G.stride + c];
+            a1 += G.partial[(long)(b + GN_GROUPS) * G.stride + c];
+            a2 += G.partial[(long)(b + 2 * GN_GROUPS) * G.stride + c];
+            a3 += G.partial[(long)(b + 3 * GN_GROUPS) * G.stride + c];
+        }
+        for (; b < G.nparts; b += GN_GROUPS) a0 += G.partial[(long)b * G.stride + c];
+    }
+    sh[grp][cl] = (a0 + a1) + (a2 + a3);
+    __syncthreads();
+    if (grp == 0 && c < (int)G.dim) {
+        float sum = 0.f;
+#pragma unroll
+        for (int i = 0; i < GN_GROUPS; ++i) sum += sh[i][cl];
+        const size_t k = G.off + c;
+        g_[k] = sum;
+        adam1(p_[k], sum, m_[k], v_[k], lr, b1, b2, eps, bc1, bc2, wd);
+        if (pb) pb[k] = (bf16)p_[k];
+    }
+}
+
+// Unaligned spans: a grid-stride loop over scalars and float4 where aligned.
+constexpr int ADAM_GRID = 256 * 32;
 
 __global__ __launch_bounds__(NT) void adam_k(float *p_, const float *g_, float *m_, float *v_,
                                               bf16 *pb, size_t n, float lr, float b1, float b2,
@@ -297,19 +462,21 @@ hipError_t swiglu_forward(const float *pg, long ldpg, const float *up, long ldup
                           long ldg, DType gdt, int rows, int cols, hipStream_t st) {
     if (rows <= 0 || cols <= 0) return hipSuccess;
     const bool v4 = (cols % 4 == 0) && (ldpg % 4 == 0) && (ldup % 4 == 0) && (ldg % 4 == 0) &&
-                    al16(pg) && al16(up) && ((uintptr_t)g & (gdt == DType::F32 ? 15u : 7u)) == 0;
-    const unsigned gv = grid_for((size_t)rows * cols / 4), gs = grid_for((size_t)rows * cols);
+                    al16(pg) && al16(up) && ((uintptr_t)g & (gdt == DType::F32 ? 15u : 7u)) == 0 &&
+                    rows <= 65535;
+    const unsigned gs = grid_for((size_t)rows * cols);
+    const dim3 gv((unsigned)ceil_div(cols / 4, NT * SW_U), (unsigned)rows);
     if (gdt == DType::F32) {
         if (v4)
-            hipLaunchKernelGGL(swiglu_fwd_k<float>, dim3(gv), dim3(NT), 0, st, pg, ldpg, up, ldup,
-                               (float *)g, ldg, rows, cols / 4);
+            hipLaunchKernelGGL(swiglu_fwd_k<float>, gv, dim3(NT), 0, st, pg, ldpg, up, ldup,
+                               (float *)g, ldg, cols / 4);
         else
             hipLaunchKernelGGL(swiglu_fwd_s<float>, dim3(gs), dim3(NT), 0, st, pg, ldpg, up, ldup,
                                (float *)g, ldg, rows, cols);
     } else {
         if (v4)
-            hipLaunchKernelGGL(swiglu_fwd_k<bf16>, dim3(gv), dim3(NT), 0, st, pg, ldpg, up, ldup,
-                               (bf16 *)g, ldg, rows, cols / 4);
+            hipLaunchKernelGGL(swiglu_fwd_k<bf16>, gv, dim3(NT), 0, st, pg, ldpg, up, ldup,
+                               (bf16 *)g, ldg, cols / 4);
         else
             hipLaunchKernelGGL(swiglu_fwd_s<bf16>, dim3(gs), dim3(NT), 0, st, pg, ldpg, up, ldup,
                                (bf16 *)g, ldg, rows, cols);
@@ -324,19 +491,20 @@ hipError_t swiglu_backward(const float *dg, long lddg, const float *pg, long ldp
     const uintptr_t om = odt == DType::F32 ? 15u : 7u;
     const bool v4 = (cols % 4 == 0) && (lddg % 4 == 0) && (ldpg % 4 == 0) && (ldup % 4 == 0) &&
                     (lddpg % 4 == 0) && (lddup % 4 == 0) && al16(dg) && al16(pg) && al16(up) &&
-                    ((uintptr_t)dpg & om) == 0 && ((uintptr_t)dup & om) == 0;
-    const unsigned gv = grid_for((size_t)rows * cols / 4), gs = grid_for((size_t)rows * cols);
+                    ((uintptr_t)dpg & om) == 0 && ((uintptr_t)dup & om) == 0 && rows <= 65535;
+    const unsigned gs = grid_for((size_t)rows * cols);
+    const dim3 gv((unsigned)ceil_div(cols / 4, NT * SW_U), (unsigned)rows);
     if (odt == DType::F32) {
         if (v4)
-            hipLaunchKernelGGL(swiglu_bwd_k<float>, dim3(gv), dim3(NT), 0, st, dg, lddg, pg, ldpg,
-                               up, ldup, (float *)dpg, lddpg, (float *)dup, lddup, rows, cols / 4);
+            hipLaunchKernelGGL(swiglu_bwd_k<float>, gv, dim3(NT), 0, st, dg, lddg, pg, ldpg,
+                               up, ldup, (float *)dpg, lddpg, (float *)dup, lddup, cols / 4);
         else
             hipLaunchKernelGGL(swiglu_bwd_s<float>, dim3(gs), dim3(NT), 0, st, dg, lddg, pg, ldpg,
                                up, ldup, (float *)dpg, lddpg, (float *)dup, lddup, rows, cols);
     } else {
         if (v4)
-            hipLaunchKernelGGL(swiglu_bwd_k<bf16>, dim3(gv), dim3(NT), 0, st, dg, lddg, pg, ldpg,
-                               up, ldup, (bf16 *)dpg, lddpg, (bf16 *)dup, lddup, rows, cols / 4);
+            hipLaunchKernelGGL(swiglu_bwd_k<bf16>, gv, dim3(NT), 0, st, dg, lddg, pg, ldpg,
+                               up, ldup, (bf16 *)dpg, lddpg, (bf16 *)dup, lddup, cols / 4);
         else
             hipLaunchKernelGGL(swiglu_bwd_s<bf16>, dim3(gs), dim3(NT), 0, st, dg, lddg, pg, ldpg,
                                up, ldup, (bf16 *)dpg, lddpg, (bf16 *)dup, lddup, rows, cols);
@@ -353,11 +521,39 @@ hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int
     return hipGetLastError();
 }
 
+hipError_t adam_step_gains(float *p, float *g, float *m, float *v, size_t n, float lr, float beta1,
+                           float beta2, float eps, float bc1, float bc2, float wd, bf16 *pb,
+                           const AdamGains &gs, hipStream_t st) {
+    if (!n) return hipSuccess;
+    const bool vec = al16(p) && al16(g) && al16(m) && al16(v) && ((uintptr_t)pb & 7u) == 0 &&
+                     n % 4 == 0;
+    unsigned gain_blocks = 0;
+    for (int i = 0; i < gs.n; ++i) {
+        // whole float4 vectors inside the span
+        if (gs.g[i].off % 4 || gs.g[i].dim % 4 || gs.g[i].off + gs.g[i].dim > n) return hipErrorInvalidValue;
+        gain_blocks += ceil_div(gs.g[i].dim, GN_COLS);
+    }
+    if (!vec || gs.n > kAdamMaxGains) return hipErrorInvalidValue;
+    const size_t nchunk = std::max<size_t>(1, (n / 4 + NT * ADAM_U - 1) / (NT * ADAM_U));
+    if (nchunk + gain_blocks >= (1u << 31)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(adam_gains_k, dim3((unsigned)(nchunk + gain_blocks)), dim3(NT), 0, st, p, g,
+                       m, v, pb, n, (unsigned)nchunk, gs, lr, beta1, beta2, eps, bc1, bc2, wd);
+    return hipGetLastError();
+}
+
 hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,
                      float beta1, float beta2, float eps, float bc1, float bc2, float wd,
                      bf16 *pb, hipStream_t st) {
     if (!n) return hipSuccess;
     const bool vec = al16(p) && al16(g) && al16(m) && al16(v) && ((uintptr_t)pb & 7u) == 0;
+    if (vec) {
+        const size_t blocks = std::max<size_t>(1, (n / 4 + NT * ADAM_U - 1) / (NT * ADAM_U));
+        if (blocks < (1u << 31)) {
+            hipLaunchKernelGGL(adam_chunk_k, dim3((unsigned)blocks), dim3(NT), 0, st, p, g, m, v, pb,
+                               n, lr, beta1, beta2, eps, bc1, bc2, wd);
+            return hipGetLastError();
+        }
+    }
     size_t grid = (n / 4 + NT - 1) / NT;
     grid = grid < 1 ? 1 : (grid > ADAM_GRID ? ADAM_GRID : grid);
     hipLaunchKernelGGL(adam_k, dim3((unsigned)grid), dim3(NT), 0, st, p, g, m, v, pb, n, lr,

@@ -72,6 +72,25 @@ hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int
 hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,
                      float beta1, float beta2, float eps, float bc1, float bc2, float wd,
                      bf16 *pb, hipStream_t st);
+// Up to kAdamMaxGains norm gains inside an Adam span whose gradients are still
+// RMSNorm-backward partial sums: gradient = column sums of partial[nparts][stride]
+// (the column-sum kernel's order), stored into g, then the update.  Gains must
+// cover whole float4 vectors (offsets and lengths multiples of 4).
+constexpr int kAdamMaxGains = 4;
+struct AdamGain {
+    size_t off;           // element offset from the span start
+    unsigned dim;
+    const float *partial;
+    int nparts;
+    long stride;
+};
+struct AdamGains {
+    AdamGain g[kAdamMaxGains];
+    int n;
+};
+hipError_t adam_step_gains(float *p, float *g, float *m, float *v, size_t n, float lr, float beta1,
+                           float beta2, float eps, float bc1, float bc2, float wd, bf16 *pb,
+                           const AdamGains &gs, hipStream_t st);
 
 // y (fp32 or bf16 per ydt) = rmsnorm(x) * w
 hipError_t rmsnorm_forward(const float *x, const float *w, void *y, DType ydt, int rows, int dim,

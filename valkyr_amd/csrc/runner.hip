@@ -605,8 +605,10 @@ struct vkh_runner {
             VKH_HIP(gemm_tn(pr, dy, x, Gd(w), K, T, N, K, 1.f, 0.f, st));
         return VKH_OK;
     }
-    // The four weight-gradient GEMMs of layer l on the side stream (concurrent mode).
-    vkh_status layer_dw_side(int l) {
+    // The four weight-gradient GEMMs of layer l on the side stream (concurrent
+    // mode); with gains_in_adam the norm-gain gradients are left as partials
+    // for adam_layer_side to reduce.
+    vkh_status layer_dw_side(int l, bool gains_in_adam) {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const LayerGrads &g = lg[l];
@@ -614,6 +616,7 @@ struct vkh_runner {
         VKH_TRY(linear_dw_on(matb(g.gub, 2 * F), m_n2(a), s.t[6], 2 * F, D, gws2, side));
         VKH_TRY(linear_dw_on(matb(g.midb, D), m_attn(a), s.t[4], D, qd, gws2, side));
         VKH_TRY(linear_dw_on(matb(g.qkvb, qkvd), m_n1(a), s.t[1], qkvd, D, gws2, side));
+        if (gains_in_adam) return VKH_OK;
         // norm-gain gradients from the partial sums the main stream wrote
         const int rp = rmsnorm_partial_rows(T);
         VKH_HIP(column_sums(g.pn2, rp, D, D, Gd(s.t[5]), side));
@@ -848,8 +851,8 @@ struct vkh_runner {
                 // its update) run on the side stream while the main stream goes on
                 VKH_HIP(hipEventRecord(ev_layer[l], cur));
                 VKH_HIP(hipStreamWaitEvent(side, ev_layer[l], 0));
-                VKH_TRY(layer_dw_side(l));
-                if (with_adam) VKH_TRY(adam_span(ls[l].t[0].off, layer_end(l), side));
+                VKH_TRY(layer_dw_side(l, with_adam));
+                if (with_adam) VKH_TRY(adam_layer_side(l));
             } else {
                 VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
             }
@@ -867,6 +870,31 @@ struct vkh_runner {
             VKH_HIP(hipEventRecord(ev_side, side));
             VKH_HIP(hipStreamWaitEvent(cur, ev_side, 0));
         }
+        return VKH_OK;
+    }
+
+    // Adam over layer l's span on the side stream, reducing its norm-gain
+    // partials (n1, n2, q/k norm) inside the same launch.
+    vkh_status adam_layer_side(int l) {
+        const LayerSpans &ss = ls[l];
+        const LayerGrads &g = lg[l];
+        const size_t b = ss.t[0].off, e = layer_end(l);
+        const int rp = rmsnorm_partial_rows(T);
+        AdamGains gs{};
+        auto add = [&](const Span &sp, const float *part, int nparts, long stride) {
+            gs.g[gs.n++] = AdamGain{sp.off - b, (unsigned)sp.numel, part, nparts, stride};
+        };
+        add(ss.t[0], g.pn1, rp, D);
+        add(ss.t[5], g.pn2, rp, D);
+        if (cfg.qk_norm) {
+            add(ss.t[9], g.pqk, g.qk_parts, 2L * hd);
+            add(ss.t[10], g.pqk + hd, g.qk_parts, 2L * hd);
+        }
+        const float t = (float)step_t;
+        const float bc1 = 1.0f - powf(cfg.beta1, t);
+        const float bc2 = 1.0f - powf(cfg.beta2, t);
+        VKH_HIP(adam_step_gains(P + b, G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
+                                cfg.eps_adam, bc1, bc2, 0.f, b16() ? Pb + b : nullptr, gs, side));
         return VKH_OK;
     }
 
