@@ -137,6 +137,26 @@ VKH_DEV void dma4_async(const sgpr4 &rs, const void *lds, unsigned voff) {
 // across it.
 VKH_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// Byte offset (into the operand) of the 16 bytes lane `lane` moves for 1 KB
+// piece `ins` of an operand tile's slab (R rows x 64 k at k0); the piece
+// lands at tile + 1024 ins + 16 lane.  kOOB past the edges.
+template <Lay L, int R>
+VKH_DEV unsigned tile_off(const Op16 &o, int ins, int lane, int r0, int rmax, int k0, int kmax) {
+    if constexpr (L == Lay::K) {
+        const int r = ins * 8 + lane / 8, c = (lane % 8) ^ ((lane / 8) & 7);
+        const int gr = r0 + r, gk = k0 + 8 * c;
+        return (gr < rmax && gk < kmax) ? (unsigned)(((long)gr * o.ld + gk) * 2) : kOOB;
+    } else {
+        constexpr int CPR = R / 8;        // 16-byte chunks per k row
+        static_assert(R == 64 || R % 128 == 0, "MN tile width");
+        constexpr int RPI = 64 / CPR;     // k rows per instruction
+        const int k = ins * RPI + lane / CPR, pch = lane % CPR;
+        const int c = pch ^ mn_swz<R>(k);
+        const int gk = k0 + k, gm = r0 + 8 * c;
+        return (gk < kmax && gm < rmax) ? (unsigned)(((long)gk * o.ld + gm) * 2) : kOOB;
+    }
+}
+
 // Issue this wave's share of one slab of an operand tile (R x 64).
 template <Lay L, int R, int NW>
 VKH_DEV void dma_tile(const sgpr4 &rs, const Op16 &o, char *tile, int r0, int rmax, int k0,
@@ -146,22 +166,7 @@ VKH_DEV void dma_tile(const sgpr4 &rs, const Op16 &o, char *tile, int r0, int rm
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
         const int ins = wave * PW + j;
-        char *dst = tile + ins * 1024;
-        unsigned off;
-        if constexpr (L == Lay::K) {
-            const int r = ins * 8 + lane / 8, c = (lane % 8) ^ ((lane / 8) & 7);
-            const int gr = r0 + r, gk = k0 + 8 * c;
-            off = (gr < rmax && gk < kmax) ? (unsigned)(((long)gr * o.ld + gk) * 2) : kOOB;
-        } else {
-            constexpr int CPR = R / 8;        // 16-byte chunks per k row
-        static_assert(R == 64 || R % 128 == 0, "MN tile width");
-            constexpr int RPI = 64 / CPR;     // k rows per instruction
-            const int k = ins * RPI + lane / CPR, pch = lane % CPR;
-            const int c = pch ^ mn_swz<R>(k);
-            const int gk = k0 + k, gm = r0 + 8 * c;
-            off = (gk < kmax && gm < rmax) ? (unsigned)(((long)gk * o.ld + gm) * 2) : kOOB;
-        }
-        dma16_async(rs, dst, off);
+        dma16_async(rs, tile + ins * 1024, tile_off<L, R>(o, ins, lane, r0, rmax, k0, kmax));
     }
 }
 

@@ -25,7 +25,10 @@ using T128 = Tile16<128, 128, 2, 2>;
 using T128x64 = Tile16<128, 64, 2, 2>;
 using T128w8 = Tile16<128, 128, 2, 4>;  // 8 waves of 64 x 32
 // (Three slab buffers were measured slower for these tiles: the larger LDS
-// footprint drops a block per CU.)
+// footprint drops a block per CU.  Staging the slabs through VGPRs two slabs
+// ahead, which doubles the time a load has to arrive without more LDS, was
+// measured equal on every per-layer shape alone and in the step: slab
+// latency is not what bounds these GEMMs.)
 
 constexpr bool kUseKs2 = true;
 
