@@ -151,9 +151,8 @@ def bench_fa_bwd(args):
     K.fa_forward(p, q, k, vv, o, lse, stream=s)  # O and LSE of the same inputs
     K.cast_f32_to_bf16(o, o16, nq, stream=s)
 
-    def once():
-        K.fa_bw_d_bf16(p, o16, dout16, d, stream=s)
-        K.fa_backward(p, q, k, vv, dout16, lse, d, dq, dk, dv, ws, stream=s)
+    def once():  # D preprocess + dK/dV + dQ
+        K.fa_backward_from_o(p, q, k, vv, o16, dout16, lse, d, dq, dk, dv, ws, stream=s)
 
     # the GPU clock ramps up over the first ~100 back-to-back calls (0.39 ms ->
     # 0.33 ms per call); the timed calls measure the settled state, as in training
@@ -628,8 +627,9 @@ def main():
         "fa_bwd": {"config": "B=4 S=2048 Hq=16 Hkv=8 hd=128 causal bf16 (config 2)",
                    "ms": round(fa["ms"], 4), "tflops": round(fa["tflops"], 1),
                    "frac_bf16_peak": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4)},
-        "roofline": {"kernel": "attention backward, config 2: fa_bw_d8_k<bf16> + "
-                               "fa_bwd_dkv4_k + fa_bwd_dq4_k (one call)", "bound": "mfma",
+        "roofline": {"kernel": "attention backward, config 2: fa_bwd_dq4_k (with the D "
+                               "preprocess) + fa_bwd_dkv4_k (one vkh_fa_backward_from_o call)",
+                     "bound": "mfma",
                      "achieved": round(fa["tflops"], 1), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(fa["tflops"] / BF16_PEAK_TFLOPS, 4),
                      "traffic": measured_traffic("fa_bwd_config2_traffic.md"),

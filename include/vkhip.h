@@ -508,6 +508,16 @@ size_t vkh_fa_backward_workspace_bytes(const vkh_attn_params *p);
 vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *k, const void *v,
                            const void *dout, const float *lse, const float *d, float *dq,
                            float *dk, float *dv, void *workspace, vkh_stream stream);
+/* The three shaders of the reference's attention backward recorded back to
+ * back (fa_bw_d.comp, fa_bw_dkv.comp, fa_bw_dq.comp; transformer.zig:2004-2050)
+ * from bf16 O and dO: D = rowsum(O dO) is written to `d` and dK, dV, dQ as in
+ * vkh_fa_backward.  On the recompute path the dQ kernel forms D itself (no
+ * separate pass); other shapes run vkh_fa_bw_d_bf16 then vkh_fa_backward.
+ * bf16 operands only. */
+vkh_status vkh_fa_backward_from_o(const vkh_attn_params *p, const void *q, const void *k,
+                                  const void *v, const void *o_bf16, const void *dout_bf16,
+                                  const float *lse, float *d, float *dq, float *dk, float *dv,
+                                  void *workspace, vkh_stream stream);
 
 /* shaders/matmul_nt_v2.comp (MatmulPush {m, n, k}): y[M,N] = x[M,K] w[N,K]^T. */
 vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,

@@ -448,6 +448,38 @@ def test_flash_attention_bf16_mfma(case):
     assert all(x < BF16_TOL for x in f), f
     # same dS values and products, only the dQ summation order differs
     assert all(x < 1e-5 for x in g), g
+    _check_from_o(p, qb, kb, vb, o, dob16, lse_r, dO.size, ws)
+
+
+def _check_from_o(p, qb, kb, vb, o, dob16, lse, n_do, ws):
+    """vkh_fa_backward_from_o (D formed from the bf16 O inside the backward)
+    vs the two calls it replaces, fa_bw_d_bf16 then fa_backward, on the same
+    bf16 O: D to fp64-dot accuracy, dQ / dK / dV equal up to summation order."""
+    from valkyr_amd import kernels as K
+
+    o16, o_r = bf16_dev(o)
+    lse_b = dev(lse)
+    n_rows = lse.size
+    d_ref = zeros(n_rows)
+    K.fa_bw_d_bf16(p, o16, dob16, d_ref)
+    dq0, dk0, dv0 = zeros(o.size), zeros(_kv_numel(p)), zeros(_kv_numel(p))
+    K.fa_backward(p, qb, kb, vb, dob16, lse_b, d_ref, dq0, dk0, dv0, ws)
+    d1 = zeros(n_rows)
+    dq1, dk1, dv1 = zeros(o.size), zeros(_kv_numel(p)), zeros(_kv_numel(p))
+    K.fa_backward_from_o(p, qb, kb, vb, o16, dob16, lse_b, d1, dq1, dk1, dv1, ws)
+    from valkyr_amd.device import bf16_bits_to_f32
+
+    dO_r = bf16_bits_to_f32(host(dob16, n_do, np.uint16))
+    d_np = O.fa_bw_d(o_r, dO_r, n_rows // p.n_heads, p.n_heads, p.head_dim)
+    e = [rel_l2(d_np, host(d1)), rel_l2(host(dq0), host(dq1)), rel_l2(host(dk0), host(dk1)),
+         rel_l2(host(dv0), host(dv1))]
+    note(f"  from_o vs two calls: D={e[0]:.1e} dQ={e[1]:.1e} dK={e[2]:.1e} dV={e[3]:.1e}")
+    assert e[0] < 1e-6 and rel_l2(d_np, host(d_ref)) < 1e-6
+    assert all(x < 1e-5 for x in e[1:]), e
+
+
+def _kv_numel(p):
+    return p.n_batch * p.n_kv * p.n_kv_heads * p.head_dim
 
 
 def test_flash_attention_bf16_full_size_invariants():
@@ -477,6 +509,7 @@ def test_flash_attention_bf16_full_size_invariants():
     bdq, bdk, bdv = zeros(Q.size), zeros(Kk.size), zeros(Kk.size)
     K.fa_backward(p, qb, kb, vb, dob16, blse, bd, bdq, bdk, bdv)
     o, lse, dq, dk, dv = host(bo), host(blse), host(bdq), host(bdk), host(bdv)
+    _check_from_o(p, qb, kb, vb, o, dob16, lse, dO.size, None)
     hpk = H // Hkv
     dv4 = dv.reshape(B, S, Hkv, hd).astype(np.float64)
     dO4 = dOr.reshape(B, S, Hkv, hpk, hd).astype(np.float64)

@@ -205,6 +205,7 @@ SIGNATURES = [
     ("vkh_fa_bw_dkv", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P, P]),
     ("vkh_fa_backward_workspace_bytes", SZ, [C.POINTER(AttnParams)]),
     ("vkh_fa_backward", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P, P, P, P]),
+    ("vkh_fa_backward_from_o", ST, [C.POINTER(AttnParams), P, P, P, P, P, P, P, P, P, P, P, P]),
     ("vkh_matmul_nt", ST, [P, P, P, U32, U32, U32, U32, P]),
     ("vkh_linear_backward_dx", ST, [P, P, P, U32, U32, U32, U32, P]),
     ("vkh_linear_backward_dw", ST, [P, P, P, U32, U32, U32, U32, P]),

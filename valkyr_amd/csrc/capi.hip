@@ -312,6 +312,33 @@ vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *
     return VKH_OK;
 }
 
+// The whole attention backward from bf16 O: the D preprocess and the two
+// gradient kernels.  On the recompute path the dQ kernel forms D itself (no
+// separate pass) and the dK/dV kernel reads it; other shapes run the D kernel
+// and then vkh_fa_backward.
+vkh_status vkh_fa_backward_from_o(const vkh_attn_params *p, const void *q, const void *k,
+                                  const void *v, const void *o_bf16, const void *dout_bf16,
+                                  const float *lse, float *d, float *dq, float *dk, float *dv,
+                                  void *workspace, vkh_stream stream) {
+    VKH_TRY(check_attn(p));
+    CHECK_ARG(q && k && v && o_bf16 && dout_bf16 && lse && d && dq && dk && dv, "null pointer");
+    if (p->dtype != VKH_BF16) return fail(VKH_ERR_INVALID_ARGUMENT, "fa_backward_from_o takes bf16 operands");
+    const AttnShape s = attn_shape(p);
+    if (fa_bw_fused_ok(s) && fa_bw_v4_ok(s)) {
+        AttnPtrs a = attn_ptrs(p, q, k, v, dout_bf16, lse, d);
+        a.dq = dq;
+        a.dk = dk;
+        a.dv = dv;
+        a.o16 = o_bf16;
+        a.ldo16 = (long)p->n_heads * p->head_dim;
+        const hipError_t e = fa_bw_fused(s, a, nullptr, true, S(stream));
+        if (e != hipSuccess) return hip_fail(e, "fa_backward_from_o");
+        return VKH_OK;
+    }
+    VKH_TRY(vkh_fa_bw_d_bf16(p, o_bf16, dout_bf16, d, stream));
+    return vkh_fa_backward(p, q, k, v, dout_bf16, lse, d, dq, dk, dv, workspace, stream);
+}
+
 // ── GEMMs ──────────────────────────────────────────────────────────────
 
 vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,

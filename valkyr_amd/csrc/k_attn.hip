@@ -1381,7 +1381,10 @@ constexpr int NBUF = 3;
 // Key tiles ascend from 0, so all query blocks of a (sequence, head) read
 // the same K / V tile at about the same time; the heaviest query blocks
 // (highest queries) start first.
-template <int NWV>
+// WITH_D: D = rowsum(O dO) of the block's rows is formed here from bf16 O (the
+// lane's 32 products in fp64, then the row's four lanes) and stored to p.d
+// for the dK/dV kernel, which then runs after this one; no separate pass.
+template <int NWV, bool WITH_D>
 __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs p) {
     using namespace dq4;
     constexpr int QSUB = BQ / 16 / NWV;  // 16-row query sub-tiles per wave
@@ -1417,7 +1420,22 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
         const float l = ok ? p.lse[t * s.n_heads + h] : -INFINITY;
         // rows past n_q and fully masked rows (lse = -inf) get P = 0
         lq[j] = l == -INFINITY ? INFINITY : l * LOG2E;
-        dd[j] = ok ? p.d[t * s.n_heads + h] : 0.f;
+        if constexpr (WITH_D) {
+            const bf16 *opo = (const bf16 *)p.o16 + t * p.ldo16 + h * HD + 8 * g;
+            double acc = 0;
+#pragma unroll
+            for (int ds = 0; ds < DS; ++ds) {
+                const bf16x8 ov = ok ? ld_frag(opo + 32 * ds) : bf16x8{};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) acc += (double)(float)ov[e] * (double)(float)orr[j][ds][e];
+            }
+            acc += __shfl_xor(acc, 16, 64);
+            acc += __shfl_xor(acc, 32, 64);
+            dd[j] = ok ? (float)acc : 0.f;
+            if (ok && g == 0) p.d[t * s.n_heads + h] = dd[j];
+        } else {
+            dd[j] = ok ? p.d[t * s.n_heads + h] : 0.f;
+        }
     }
     wait_vm0();
     f32x4 acc[DSUB][QSUB];
@@ -2016,14 +2034,17 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
         if ((long)s.n_q * std::max(p.ldq, p.lddo) * 2 >= (1l << 31) ||
             (long)s.n_kv * std::max(p.ldk, p.ldv) * 2 >= (1l << 31))
             return hipErrorInvalidValue;
-        constexpr int DKV_WAVES = 8;
-        hipLaunchKernelGGL(fa_bwd_dkv4_k<DKV_WAVES>,
-                           dim3(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN),
-                           dim3(DKV_WAVES * 64), 0, st, s, p);
-        constexpr int DQ_WAVES = 8;
-        hipLaunchKernelGGL(fa_bwd_dq4_k<DQ_WAVES>,
-                           dim3(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ),
-                           dim3(DQ_WAVES * 64), 0, st, s, p);
+        if (p.o16 && (long)s.n_q * p.ldo16 * 2 >= (1l << 31)) return hipErrorInvalidValue;
+        constexpr int DKV_WAVES = 8, DQ_WAVES = 8;
+        const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
+        const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
+        if (p.o16) {  // dQ forms D, then dK/dV reads it
+            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            hipLaunchKernelGGL(fa_bwd_dkv4_k<DKV_WAVES>, gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+        } else {
+            hipLaunchKernelGGL(fa_bwd_dkv4_k<DKV_WAVES>, gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+        }
         return hipGetLastError();
     }
     if (!ds_ws) return hipErrorInvalidValue;

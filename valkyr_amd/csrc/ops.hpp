@@ -169,6 +169,9 @@ struct AttnPtrs {
     float *dk; long lddk;
     float *dv; long lddv;
     DType dt;
+    // bf16 O: when set on the recompute path, the dQ kernel forms
+    // D = rowsum(O dO) for its rows itself (written to d) and runs first
+    const void *o16 = nullptr; long ldo16 = 0;
 };
 // ob (optional, bf16 operands only): bf16 copy of O for the output projection.
 hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,

@@ -768,7 +768,8 @@ struct vkh_runner {
         // attention: D, dK/dV, dQ into the fused d_qkv buffer
         if (b16() && adt == DType::BF16) {
             if (!do_bf16) VKH_HIP(cast_f32_to_bf16(d_attn_out, dout16, (size_t)T * qd, cur));
-            VKH_HIP(fa_bw_d_bf16(as, a.attn_b, qd, dout16, qd, fa_d, cur));
+            // the recompute kernels form D themselves (from the bf16 O below)
+            if (!attn_v4) VKH_HIP(fa_bw_d_bf16(as, a.attn_b, qd, dout16, qd, fa_d, cur));
         } else {
             VKH_HIP(fa_bw_d(as, a.attn_out, qd, d_attn_out, qd, fa_d, dout16, qd, cur));
         }
@@ -785,6 +786,10 @@ struct vkh_runner {
         ap.dk = d_qkv + qd; ap.lddk = qkvd;
         ap.dv = d_qkv + qd + kvd; ap.lddv = qkvd;
         ap.dt = adt;
+        if (attn_v4) {
+            ap.o16 = a.attn_b;
+            ap.ldo16 = qd;
+        }
         if (attn_fused) {
             VKH_HIP(fa_bw_fused(as, ap, attn_ds, attn_v4, cur));
         } else {

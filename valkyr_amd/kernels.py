@@ -72,6 +72,14 @@ def fa_backward(p, q, k, v, dout, lse, d, dq, dk, dv, workspace=None, stream=Non
                                 _p(dq), _p(dk), _p(dv), _p(workspace), _s(stream)))
 
 
+def fa_backward_from_o(p, q, k, v, o16, dout16, lse, d, dq, dk, dv, workspace=None, stream=None):
+    """D = rowsum(O dO) (written to d) and dK, dV, dQ from bf16 O and dO in one
+    call; on the recompute path the dQ kernel forms D itself."""
+    check(lib().vkh_fa_backward_from_o(C.byref(p), _p(q), _p(k), _p(v), _p(o16), _p(dout16),
+                                       _p(lse), _p(d), _p(dq), _p(dk), _p(dv), _p(workspace),
+                                       _s(stream)))
+
+
 def matmul_nt(x, w, y, M, N, K, precision=PRECISION_FP32, stream=None):
     """matmul_nt_v2.comp: y[M,N] = x[M,K] w[N,K]^T."""
     check(lib().vkh_matmul_nt(_p(x), _p(w), _p(y), M, N, K, precision, _s(stream)))
