@@ -6,8 +6,8 @@
   weights / accumulation / Adam), synthetic random-init weights and
   uniform token ids.
 
-One JSON line on stdout.  `roofline` is the FA-2 backward (fa_bw_d + dK/dV +
-dQ kernels) at config 2 (B=4, S=2048, 16/8 heads, hd 128, causal, bf16
+One JSON line on stdout.  `roofline` is the FA-2 backward (the D row-dot
+preprocess + dK/dV + dQ, one call) at config 2 (B=4, S=2048, 16/8 heads, hd 128, causal, bf16
 Q/K/V/dO and bf16 O from the forward), timed with HIP events on the stream it
 runs on; its algorithmic work is 10 * B * Hq * hd * S(S+1)/2 = 171.88 GFLOP
 per call.
@@ -20,16 +20,18 @@ directly, scaled to tokens/s of the same step (see `sample`): all host threads
 thread (`single_thread`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
-                       [--no-cpu-baseline] [--fa-reps R]
+                       [--no-cpu-baseline] [--no-configs] [--fa-reps R]
                        [--only all|step|fa|mlp|bw|config4|config5] [--calib-copy]
 
 `bandwidth_kernels` times the HBM-bound backward kernels alone through the C ABI at
 config-3 shapes (RMSNorm, SwiGLU, RoPE backward, Adam, embedding backward) against
 the 8 TB/s HBM peak.
 `mlp_runner` times the tiny-MLP TrainingRunner (train/runner.zig): the
-reference's `--train-demo` loop and tickFrameTrain on batches.  `--only config4`
-/ `--only config5` run the metric's Qwen3-4B LoRA and Qwen3-8B long-context
-configurations at full size (memory, step time, size-independent checks).
+reference's `--train-demo` loop and tickFrameTrain on batches.  `configs` runs
+the metric's Qwen3-4B LoRA (config 4) and Qwen3-8B long-context full fine-tune
+with per-layer activation recompute (config 5) at full size: device memory,
+step time, TFLOP/s of the step's algorithmic work, size-independent checks
+(`--only config4` / `--only config5` run one alone, `--no-configs` skips them).
 """
 from __future__ import annotations
 
@@ -65,21 +67,29 @@ QWEN3_4B_LORA = dict(dim=2560, n_heads=32, n_kv_heads=8, head_dim=128, ff_dim=97
 QWEN3_8B = dict(dim=4096, n_heads=32, n_kv_heads=8, head_dim=128, ff_dim=12288, n_pos=8192,
                 n_layers=36, vocab_size=151936, rms_eps=1e-6, causal=1, rotary_dim=128,
                 rope_theta=1e6, qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8,
-                n_seqs=1, tied_embeddings=0)
+                n_seqs=1, tied_embeddings=0, recompute=1)
 
 
 def step_flops(c) -> float:
-    """Algorithmic FLOP of one step (6 * tokens * matmul params + CCE + attention)."""
+    """Algorithmic FLOP of one step: 6 * tokens * matmul params (4 with a frozen
+    base: no weight gradients), the CCE head (6 T V D; 4 when frozen), causal
+    attention (forward 2 GEMMs, backward 5), and each LoRA adapter's six rank-r
+    products (6 T r (K + N)).  Activation recompute is not counted: it is work
+    the step repeats, not work the model needs."""
     T = c["n_pos"] * c["n_seqs"]
     D, F, V, L = c["dim"], c["ff_dim"], c["vocab_size"], c["n_layers"]
     qd, kvd = c["n_heads"] * c["head_dim"], c["n_kv_heads"] * c["head_dim"]
     p_mat = L * (D * (qd + 2 * kvd) + qd * D + 3 * D * F)
-    gemm = 6.0 * T * p_mat
-    cce = 6.0 * T * V * D
+    lora = c.get("lora_targets", 0)
+    gemm = (4.0 if lora else 6.0) * T * p_mat
+    cce = (4.0 if lora else 6.0) * T * V * D
     S, H, hd = c["n_pos"], c["n_heads"], c["head_dim"]
     causal_pairs = c["n_seqs"] * S * (S + 1) / 2
     attn = L * H * hd * causal_pairs * (4 + 10)  # fwd 2 GEMMs (4), bwd 5 GEMMs (10)
-    return gemm + cce + attn
+    nk = [(qd, D), (kvd, D), (kvd, D), (D, qd), (F, D), (F, D), (D, F)]  # (N, K) per projection
+    adapters = sum(6.0 * T * c["lora_rank"] * (n + k) for p, (n, k) in enumerate(nk)
+                   if lora & (1 << p)) * L
+    return gemm + cce + attn + adapters
 
 
 def bench_step(args, dev_info, precision=None, steps=None, warmup=None):
@@ -395,7 +405,8 @@ def cpu_baseline(args):
 
 def bench_config(name, args):
     """Config 4 (Qwen3-4B shape, frozen bf16-operand base + LoRA r16 on q/k/v/o, 1 x 2048)
-    or config 5 (Qwen3-8B shape, full fine-tune, 1 x 8192, untied head) at full size:
+    or config 5 (Qwen3-8B shape, full fine-tune with per-layer activation recompute,
+    1 x 8192, untied head) at full size:
     device memory, step time, and the size-independent checks the shapes allow (loss of a
     random init = ln V within 0.5; for LoRA at step 1: B = 0 makes every dA exactly zero,
     dB non-zero, A and the frozen base unchanged bit for bit)."""
@@ -461,9 +472,14 @@ def bench_config(name, args):
     wall = time.perf_counter() - t0
     loss1 = r.last_loss()
     r.close()
+    tflops = step_flops(c) / (wall / K) / 1e12
     out.update(steps=K, ms_per_step=round(1000 * wall / K, 2), tokens_s=round(T * K / wall, 1),
+               tflops=round(tflops, 1), frac_bf16_peak=round(tflops / BF16_PEAK_TFLOPS, 4),
                first_step_s=round(first_s, 2), loss=[round(loss0, 4), round(loss1, 4)],
                checks=checks)
+    if c.get("recompute"):
+        out["activation_recompute"] = "per layer (each layer keeps its input; forward rerun " \
+                                      "before its backward; not counted in tflops)"
     print(f"[bench] {name}: {out['ms_per_step']} ms/step, {out['tokens_s']:,.0f} tok/s, "
           f"checks {checks}", file=sys.stderr, flush=True)
     return out
@@ -544,6 +560,8 @@ def main():
     ap.add_argument("--fa-reps", type=int, default=100)
     ap.add_argument("--fa-warmup", type=int, default=150)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the full-size config 4 / config 5 steps")
     ap.add_argument("--only", default="all",
                     choices=["all", "step", "fa", "mlp", "bw", "config4", "config5"],
                     help="run only the step or only the attention benchmark (profiling runs)")
@@ -592,6 +610,7 @@ def main():
         calib_copy()
     mlp = bench_mlp(args)
     bw = bench_bandwidth(args)
+    cfgs = {} if args.no_configs else {n: bench_config(n, args) for n in ("config4", "config5")}
     cpu = None if args.no_cpu_baseline else cpu_baseline(args)
     peak = BF16_PEAK_TFLOPS if args.precision == "bf16" else FP32_PEAK_TFLOPS
     mfu = st["flops"] / (st["ms"] * 1e-3) / 1e12 / peak
@@ -638,6 +657,7 @@ def main():
         "cpu_baseline": cpu,
         "bandwidth_kernels": bw,
         "mlp_runner": mlp,
+        "configs": cfgs,
     }
     print(json.dumps(out), flush=True)
 

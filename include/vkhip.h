@@ -112,7 +112,7 @@ enum {
     VKH_LORA_ALL_ATTN = 0xFu, VKH_LORA_ALL_FFN = 0x70u, VKH_LORA_ALL = 0x7Fu
 };
 
-/* transformer.zig:31-77 (Config) plus three extensions at the end. */
+/* transformer.zig:31-77 (Config) plus four extensions at the end. */
 typedef struct vkh_config {
     uint32_t dim, n_heads, n_kv_heads, head_dim, ff_dim;
     uint32_t n_pos;            /* positions per sequence */
@@ -129,7 +129,9 @@ typedef struct vkh_config {
     uint32_t n_seqs;           /* sequences per step (0 means 1); T = n_seqs * n_pos */
     uint32_t tied_embeddings;  /* lm_head aliases embed; grad = dE + dW_lm */
     uint32_t precision;        /* vkh_precision */
-    uint32_t reserved;
+    uint32_t recompute;        /* 1: per-layer activation recompute -- each layer keeps only
+                                  its input, and its forward runs again just before its
+                                  backward (same kernels, so the same gradients bit for bit) */
 } vkh_config;
 
 /* A borrowed host fp32 tensor (a Zig slice: pointer + element count). */

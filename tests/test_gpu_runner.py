@@ -154,6 +154,65 @@ def test_step_parity_bf16(variant):
         assert rel_l2(m.tensor(0, *k), r.get(0, *k)) < 1e-2
 
 
+# Per-layer activation recompute (config 5's mode) at 5 layers, so that the
+# two shared activation sets, the two gradient-copy sets and the three-deep
+# dy ring are all reused: the same kernels run on the same inputs, so every
+# gradient, moment and weight must equal the stored-activation runner's bit
+# for bit, through forward_backward and three Adam steps.
+RECOMPUTE_MODE_BASE = dict(dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ff_dim=768, n_pos=128,
+                           n_layers=5, vocab_size=4096, rms_eps=1e-6, causal=1, rotary_dim=64,
+                           rope_theta=1e6, qk_norm=1, lr=1e-3)
+LORA_QV = dict(lora_targets=0x5 | 0x40, lora_rank=8, lora_alpha=16.0)
+
+
+@pytest.mark.parametrize("precision,over", [
+    (0, {}), (1, {}), (1, dict(tied_embeddings=1, n_seqs=2, n_pos=64)), (0, LORA_QV),
+    (1, LORA_QV),
+    (1, dict(head_dim=128, n_heads=16, n_kv_heads=8, rotary_dim=128, n_seqs=16, n_pos=128,
+             ff_dim=512, vocab_size=1024, n_layers=4))])
+def test_activation_recompute_bit_identical(precision, over):
+    import valkyr_amd as v
+    from valkyr_amd.runner import ADAM_M, ADAM_V, GRAD, PARAM
+
+    c = dict(RECOMPUTE_MODE_BASE, **over)
+    note(f"activation recompute precision={precision} {over}")
+    lora = bool(c.get("lora_targets"))
+    L = c["n_layers"]
+    T = c["n_pos"] * c.get("n_seqs", 1)
+    with v.Runner(v.make_config(**c, precision=precision)) as a, \
+            v.Runner(v.make_config(**c, precision=precision, recompute=1)) as b:
+        for r in (a, b):
+            r.init_random(seed=21, std=0.02, lora_std=0.02)
+        note(f"  device bytes stored {a.device_bytes():,}, recompute {b.device_bytes():,}")
+        assert b.device_bytes() < a.device_bytes()
+        if over.get("head_dim") == 128:
+            assert b.attention_backward_path() == "recompute"
+        cf = {**c, "tied_embeddings": c.get("tied_embeddings", 0),
+              "qk_norm": c["qk_norm"]}
+        base = tensor_keys(cf)
+        trainable = lora_keys(cf) if lora else base
+        tok, tgt = O.ids(T, 5, c["vocab_size"]), O.ids(T, 6, c["vocab_size"])
+
+        def same(kind, keys, what):
+            for k in keys:
+                x, y = a.get(kind, *k), b.get(kind, *k)
+                assert np.array_equal(x, y), (what, k, rel_l2(x, y))
+
+        la, lb = a.forward_backward(tok, tgt), b.forward_backward(tok, tgt)
+        assert la == lb, (la, lb)
+        same(GRAD, trainable, "grad")
+        for i in range(3):
+            tok, tgt = O.ids(T, 7 + i, c["vocab_size"]), O.ids(T, 17 + i, c["vocab_size"])
+            a.step(tok, tgt)
+            b.step(tok, tgt)
+            assert a.last_loss() == b.last_loss()
+        same(GRAD, trainable, "grad after steps")
+        same(ADAM_M, trainable, "adam m")
+        same(ADAM_V, trainable, "adam v")
+        same(PARAM, base + (lora_keys(cf) if lora else []), "param")
+        note(f"  loss {la:.5f} -> {b.last_loss():.5f}, identical")
+
+
 # Qwen3-0.6B widths (config 3) at 2 layers and 128 positions: dim 1024, 16/8
 # heads of 128, QK-norm, FFN 3072, the full 151936 vocabulary with tied
 # embeddings, theta 1e6, eps 1e-6.  This pins the CCE's dh and dW over the full

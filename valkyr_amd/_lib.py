@@ -58,7 +58,7 @@ class Config(C.Structure):
         ("beta2", C.c_float), ("eps_adam", C.c_float), ("lora_targets", C.c_uint32),
         ("lora_rank", C.c_uint32), ("lora_alpha", C.c_float), ("lora_lr_b_scale", C.c_float),
         ("n_seqs", C.c_uint32), ("tied_embeddings", C.c_uint32), ("precision", C.c_uint32),
-        ("reserved", C.c_uint32),
+        ("recompute", C.c_uint32),
     ]
 
 

@@ -103,6 +103,17 @@ struct vkh_runner {
         int qk_parts = 0;
     };
     bool concurrent = false;
+    // Per-layer activation recompute: each layer keeps its output y (the next
+    // layer's input); the other activations live in kActSets sets shared in
+    // turn (layer l in set l % kActSets), and a layer's forward runs again
+    // just before its backward when later layers have reused its set.  The
+    // side stream's gradient copies are shared the same way (kGradSets sets,
+    // kDyRing for dy, which the layer above writes), and before layer l
+    // writes any of them the main stream waits for the side stream to finish
+    // layer l + 2, their previous user (ev_sdone).
+    static constexpr int kActSets = 2, kGradSets = 2, kDyRing = 3;
+    bool recompute = false;
+    std::vector<hipEvent_t> ev_sdone;
     hipStream_t side = nullptr;
     std::vector<hipEvent_t> ev_layer;
     hipEvent_t ev_side = nullptr, ev_head = nullptr, ev_lm = nullptr;
@@ -144,6 +155,7 @@ struct vkh_runner {
         if (side) (void)hipStreamSynchronize(side);
         if (ev_done) (void)hipEventDestroy(ev_done);
         for (hipEvent_t e : ev_layer) (void)hipEventDestroy(e);
+        for (hipEvent_t e : ev_sdone) (void)hipEventDestroy(e);
         if (ev_side) (void)hipEventDestroy(ev_side);
         if (ev_head) (void)hipEventDestroy(ev_head);
         if (ev_lm) (void)hipEventDestroy(ev_lm);
@@ -320,9 +332,17 @@ struct vkh_runner {
         }
 
         const size_t asz = adt == DType::BF16 ? 2 : 4;
+        recompute = cfg.recompute != 0;
+        concurrent = b16() && !lora;
+        const int n_sets = recompute ? std::min(L, kActSets) : L;
         acts.assign(L, Acts{});
         for (int l = 0; l < L; ++l) {
             Acts &a = acts[l];
+            if (l >= n_sets) {  // recompute: set l % n_sets, own output
+                a = acts[l % n_sets];
+                VKH_TRY(alloc(a.y, (size_t)T * D));
+                continue;
+            }
             if (b16()) {
                 VKH_TRY(alloc(a.n1b, (size_t)T * D));
                 VKH_TRY(alloc(a.attn_b, (size_t)T * qd));
@@ -352,11 +372,13 @@ struct vkh_runner {
         VKH_TRY(alloc(x_emb, (size_t)T * D));
         if (b16()) {
             VKH_TRY(alloc(fn_outb, (size_t)T * D));
-            VKH_TRY(alloc(d_gub, (size_t)T * 2 * F));
-            VKH_TRY(alloc(d_midb, (size_t)T * D));
-            VKH_TRY(alloc(d_qkvb, (size_t)T * qkvd));
-            VKH_TRY(alloc(dxb[0], (size_t)T * D));
-            VKH_TRY(alloc(dxb[1], (size_t)T * D));
+            if (!concurrent) {  // concurrent mode uses the per-layer copies (lg)
+                VKH_TRY(alloc(d_gub, (size_t)T * 2 * F));
+                VKH_TRY(alloc(d_midb, (size_t)T * D));
+                VKH_TRY(alloc(d_qkvb, (size_t)T * qkvd));
+                VKH_TRY(alloc(dxb[0], (size_t)T * D));
+                VKH_TRY(alloc(dxb[1], (size_t)T * D));
+            }
             attn_fused = adt == DType::BF16 && fa_bw_fused_ok(attn_shape());
             attn_v4 = attn_fused && fa_bw_v4_preferred(attn_shape());
             if (attn_fused && fa_bw_ws_bytes(attn_shape(), attn_v4))
@@ -373,18 +395,31 @@ struct vkh_runner {
                 VKH_TRY(alloc(w, wsb));
                 gws = GemmWs{w, wsb};
             }
-            concurrent = !lora;
             if (concurrent) {
                 VKH_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
                 ev_layer.assign(L, nullptr);
                 for (int l = 0; l < L; ++l)
                     VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], hipEventDisableTiming));
+                if (recompute) {
+                    ev_sdone.assign(L, nullptr);
+                    for (int l = 0; l < L; ++l)
+                        VKH_HIP(hipEventCreateWithFlags(&ev_sdone[l], hipEventDisableTiming));
+                }
                 VKH_HIP(hipEventCreateWithFlags(&ev_side, hipEventDisableTiming));
                 VKH_HIP(hipEventCreateWithFlags(&ev_head, hipEventDisableTiming));
                 VKH_HIP(hipEventCreateWithFlags(&ev_lm, hipEventDisableTiming));
                 lg.assign(L, LayerGrads{});
+                const int n_g = recompute ? std::min(L, kGradSets) : L;
+                const int n_dy = recompute ? std::min(L, kDyRing) : L;
                 for (int l = 0; l < L; ++l) {
-                    VKH_TRY(alloc(lg[l].dyb, (size_t)T * D));
+                    if (l < n_dy) VKH_TRY(alloc(lg[l].dyb, (size_t)T * D));
+                    else lg[l].dyb = lg[l % n_dy].dyb;
+                    if (l >= n_g) {
+                        const LayerGrads &o = lg[l % n_g];
+                        lg[l].gub = o.gub; lg[l].midb = o.midb; lg[l].qkvb = o.qkvb;
+                        lg[l].pn1 = o.pn1; lg[l].pn2 = o.pn2; lg[l].pqk = o.pqk;
+                        continue;
+                    }
                     VKH_TRY(alloc(lg[l].gub, (size_t)T * 2 * F));
                     VKH_TRY(alloc(lg[l].midb, (size_t)T * D));
                     VKH_TRY(alloc(lg[l].qkvb, (size_t)T * qkvd));
@@ -564,10 +599,18 @@ struct vkh_runner {
     vkh_status lora_fwd(int l, int p, Mat x, float *y, long ldy) {
         int N, K;
         proj_shape(p, N, K);
-        float *A = W(ls[l].la[p]), *Bm = W(ls[l].lb[p]);
+        float *Bm = W(ls[l].lb[p]);
         float *inter = acts[l].inter[p];
-        VKH_HIP(gemm_nt(pr, x, matf(A, K), inter, R, T, R, K, nullptr, 0, 1.f, 0.f, cur));
+        VKH_TRY(lora_inter(l, p, x));
         VKH_HIP(gemm_nt(pr, matf(inter, R), matf(Bm, R), y, ldy, T, N, R, nullptr, 0, aor, 1.f, cur));
+        return VKH_OK;
+    }
+    // inter = x A^T, the rank-r intermediate the LoRA backward reads (dB)
+    vkh_status lora_inter(int l, int p, Mat x) {
+        int N, K;
+        proj_shape(p, N, K);
+        VKH_HIP(gemm_nt(pr, x, matf(W(ls[l].la[p]), K), acts[l].inter[p], R, T, R, K, nullptr, 0,
+                        1.f, 0.f, cur));
         return VKH_OK;
     }
 
@@ -646,7 +689,9 @@ struct vkh_runner {
         return VKH_OK;
     }
 
-    vkh_status layer_forward(int l) {
+    // need_y = false (a recompute before the backward): stop before the down
+    // projection, whose output y the layer keeps anyway.
+    vkh_status layer_forward(int l, bool need_y = true) {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const float *x_in = l == 0 ? x_emb : acts[l - 1].y;
@@ -683,8 +728,9 @@ struct vkh_runner {
         if (proj_lora(5)) VKH_TRY(lora_fwd(l, 5, n2, a.gu + F, 2 * F));
         VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F, b16() ? (void *)a.gatedb : (void *)a.gated,
                                F, odt, T, F, cur));
-        // y = mid + gated W_down^T (+ LoRA)
         const Mat gt = m_gated(a);
+        if (!need_y) return proj_lora(6) ? lora_inter(l, 6, gt) : VKH_OK;
+        // y = mid + gated W_down^T (+ LoRA)
         VKH_TRY(linear_fwd(gt, s.t[8], a.y, D, D, F, a.mid, D));
         if (proj_lora(6)) VKH_TRY(lora_fwd(l, 6, gt, a.y, D));
         return VKH_OK;
@@ -850,6 +896,12 @@ struct vkh_runner {
                                  partial, T, D, cfg.rms_eps, 0, cur));
         int c = 0;
         for (int l = L - 1; l >= 0; --l) {
+            if (recompute) {
+                // shared sets: the side stream is done with layer l + 2's
+                if (concurrent && l + 2 < L) VKH_HIP(hipStreamWaitEvent(cur, ev_sdone[l + 2], 0));
+                // the set holds layer l + kActSets's activations: run l's forward again
+                if (l + kActSets < L) VKH_TRY(layer_forward(l, false));
+            }
             if (concurrent) {
                 VKH_TRY(layer_backward(l, dx[c], lg[l].dyb, dx[c ^ 1], l > 0 ? lg[l - 1].dyb : nullptr));
                 // layer l's gradient inputs are final: its dW GEMMs (and, with Adam,
@@ -858,6 +910,7 @@ struct vkh_runner {
                 VKH_HIP(hipStreamWaitEvent(side, ev_layer[l], 0));
                 VKH_TRY(layer_dw_side(l, with_adam));
                 if (with_adam) VKH_TRY(adam_layer_side(l));
+                if (recompute) VKH_HIP(hipEventRecord(ev_sdone[l], side));
             } else {
                 VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
             }

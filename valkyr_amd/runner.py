@@ -78,7 +78,7 @@ def make_config(**kw) -> Config:
     """vkh_config with the reference's defaults (transformer.zig:31-77)."""
     d = dict(rms_eps=1e-5, causal=1, rotary_dim=0, rope_theta=10000.0, qk_norm=0, lr=1e-2,
              beta1=0.9, beta2=0.999, eps_adam=1e-8, lora_targets=0, lora_rank=0, lora_alpha=0.0,
-             lora_lr_b_scale=1.0, n_seqs=1, tied_embeddings=0, precision=0, reserved=0)
+             lora_lr_b_scale=1.0, n_seqs=1, tied_embeddings=0, precision=0, recompute=0)
     d.update(kw)
     return Config(**d)
 
