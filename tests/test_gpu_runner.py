@@ -265,27 +265,42 @@ def test_step_bf16_vs_pure_fp32_oracle():
     compare(m, rb, tensor_keys(cfg), 1, 5e-2, "grad bf16-vs-fp32")
 
 
-def test_lora_step_parity():
-    """Config-4 shape class: LoRA r=16 on q/k/v/o, B=0 init, frozen base."""
-    note("lora step")
-    over = dict(lora_targets=0xF, lora_rank=16, lora_alpha=32.0, lora_lr_b_scale=1.0)
-    m, r, tok, tgt, cfg = build_pair(0, **over)
+@pytest.mark.parametrize("precision,over", [
+    (0, dict(lora_targets=0xF)), (1, dict(lora_targets=0xF)),
+    (1, dict(lora_targets=0x7F, n_layers=3)), (0, dict(lora_targets=0x55, lora_rank=8)),
+    (1, dict(HD128, lora_targets=0xF))])
+def test_lora_step_parity(precision, over):
+    """Config-4 shape class: LoRA r=16 on q/k/v/o (and every projection, and
+    a rank-8 subset), B = 0 init, frozen base.  fp32: every adapter gradient
+    within 1e-3; bf16: against the oracle with bf16 base-GEMM operands and fp32
+    adapter factors (the rank-r kernels' numerics) within 1e-2."""
+    note(f"lora step precision={precision} {over}")
+    over = dict(dict(lora_rank=16, lora_alpha=32.0, lora_lr_b_scale=1.0), **over)
+    m, r, tok, tgt, cfg = build_pair(precision, **over)
+    tol, ltol = (1e-3, 1e-5) if precision == 0 else (1e-2, 1e-3)
     lk = lora_keys(cfg)
     loss_ref = m.forward_backward(tok, tgt)
     loss = r.forward_backward(tok, tgt)
-    assert abs(loss - loss_ref) < 1e-5 * abs(loss_ref)
+    assert abs(loss - loss_ref) < ltol * abs(loss_ref)
     for (l, w) in lk:
         if w % 2 == 0:  # dA == 0 exactly at B = 0 (lora.zig:449-505)
             assert np.all(r.get(1, l, w) == 0)
-    compare(m, r, [k for k in lk if k[1] % 2 == 1], 1, 1e-3, "dB")
+    compare(m, r, [k for k in lk if k[1] % 2 == 1], 1, tol, "dB")
     base_before = r.get(0, 0, 1).copy()
     m.adam()
     r.step(tok, tgt)
+    if precision == 1:
+        # Adam at t = 1 moves each entry by about lr * sign(g): where dB is
+        # near zero, the bf16-level difference in dB flips the step, so the
+        # oracle continues from the runner's updated adapters (step-2
+        # gradients from identical weights)
+        for k in lk:
+            m.tensor(0, *k)[:] = r.get(0, *k)
     # second step: B != 0, dA flows; frozen base unchanged bit-for-bit
     loss_ref = m.forward_backward(tok, tgt)
     loss = r.forward_backward(tok, tgt)
-    assert abs(loss - loss_ref) < 1e-5 * abs(loss_ref)
-    compare(m, r, lk, 1, 1e-3, "lora grad step 2")
+    assert abs(loss - loss_ref) < ltol * abs(loss_ref)
+    compare(m, r, lk, 1, tol, "lora grad step 2")
     assert np.array_equal(base_before, r.get(0, 0, 1))
 
 

@@ -411,6 +411,16 @@ vkh_status vkh_lora_forward(const float *x, const float *w, const float *a, cons
     const Precision pr = PR(precision);
     hipStream_t st = S(stream);
     VKH_HIP(gemm_nt(pr, matf(x, K), matf(w, K), y, N, M, N, K, nullptr, 0, 1.f, 0.f, st));
+    // rank-r kernels (fp32 factors and products) where the shape allows
+    LoraSegs sa, sb;
+    sa.n = sb.n = 1;
+    sa.s[0] = LoraSeg{0, (int)K, a, 1, (long)K, inter, (long)r};
+    sb.s[0] = LoraSeg{0, (int)N, b, (long)r, 1, inter, (long)r};
+    if (lora_fast_ok(DType::F32, x, K, (int)r, sa) && lora_update_ok(y, N, (int)r, sb)) {
+        VKH_HIP(lora_rows(DType::F32, x, K, (int)M, (int)r, sa, 1.f, st));
+        VKH_HIP(lora_update(y, N, (int)M, (int)r, sb, aor, st));
+        return VKH_OK;
+    }
     VKH_HIP(gemm_nt(pr, matf(x, K), matf(a, K), inter, r, M, r, K, nullptr, 0, 1.f, 0.f, st));
     VKH_HIP(gemm_nt(pr, matf(inter, r), matf(b, r), y, N, M, N, r, nullptr, 0, aor, 1.f, st));
     return VKH_OK;
@@ -425,7 +435,25 @@ vkh_status vkh_lora_backward(const float *dy, const float *x, const float *w, co
     const Precision pr = PR(precision);
     hipStream_t st = S(stream);
     float *dyB = nullptr;
-    VKH_HIP(hipMallocAsync((void **)&dyB, (size_t)M * r * 4, st));
+    VKH_HIP(hipMallocAsync((void **)&dyB, (size_t)M * r * 4 + 256, st));
+    LoraSegs sb, sa, sdA, sdB;
+    sb.n = sa.n = sdA.n = sdB.n = 1;
+    sb.s[0] = LoraSeg{0, (int)N, b, (long)r, 1, dyB, (long)r};
+    sa.s[0] = LoraSeg{0, (int)K, a, 1, (long)K, dyB, (long)r};
+    sdA.s[0] = LoraSeg{0, (int)K, nullptr, 1, 1, dyB, (long)r, dA, 1, (long)K};
+    sdB.s[0] = LoraSeg{0, (int)N, nullptr, 1, 1, (float *)inter, (long)r, dB, (long)r, 1};
+    if (lora_fast_ok(DType::F32, dy, N, (int)r, sb) && lora_fast_ok(DType::F32, x, K, (int)r, sdA) &&
+        lora_fast_ok(DType::F32, dy, N, (int)r, sdB) && (!dx || lora_update_ok(dx, K, (int)r, sa))) {
+        // rank-r kernels (fp32 factors and products)
+        hipError_t e = lora_rows(DType::F32, dy, N, (int)M, (int)r, sb, 1.f, st);
+        if (e == hipSuccess && dx) e = gemm_nn(pr, matf(dy, N), matf(w, K), dx, K, M, N, K, 1.f, 0.f, st);
+        if (e == hipSuccess && dx) e = lora_update(dx, K, (int)M, (int)r, sa, aor, st);
+        if (e == hipSuccess) e = lora_cols(DType::F32, x, K, (int)M, (int)r, sdA, aor, st);
+        if (e == hipSuccess) e = lora_cols(DType::F32, dy, N, (int)M, (int)r, sdB, aor, st);
+        (void)hipFreeAsync(dyB, st);
+        if (e != hipSuccess) return hip_fail(e, "lora_backward");
+        return VKH_OK;
+    }
     hipError_t e = gemm_nn(pr, matf(dy, N), matf(b, r), dyB, r, M, N, r, 1.f, 0.f, st);
     if (e == hipSuccess && dx) e = gemm_nn(pr, matf(dy, N), matf(w, K), dx, K, M, N, K, 1.f, 0.f, st);
     if (e == hipSuccess && dx) e = gemm_nn(pr, matf(dyB, r), matf(a, K), dx, K, M, r, K, aor, 1.f, st);

@@ -49,6 +49,37 @@ hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
 size_t g16_ws_bytes_for(int M, int N, int K);
 
+// ── LoRA rank-r products (k_lora.hip) ───────────────────────────────────
+// One adapter of a launch: its columns [col, col + ncols) of the shared X
+// (or of Y for the update), its factor F(c, i) = f[c * fsc + i * fsi] (A^T:
+// fsc = 1, fsi = K; B: fsc = r, fsi = 1), its [T, r] operand u, and for
+// lora_cols the gradient g(c, i) = g[c * gsc + i * gsi].
+struct LoraSeg {
+    long col = 0;
+    int ncols = 0;
+    const float *f = nullptr;
+    long fsc = 1, fsi = 1;
+    float *u = nullptr;
+    long ldu = 0;
+    float *g = nullptr;
+    long gsc = 1, gsi = 1;
+};
+struct LoraSegs {
+    LoraSeg s[3];
+    int n = 0;
+};
+// U_s = alpha X[:, cols_s] F_s            (X fp32 or bf16, [T, ldx])
+hipError_t lora_rows(DType xt, const void *x, long ldx, int T, int r, const LoraSegs &g,
+                     float alpha, hipStream_t st);
+// g_s = alpha X[:, cols_s]^T U_s          (overwrite)
+hipError_t lora_cols(DType xt, const void *x, long ldx, int T, int r, const LoraSegs &g,
+                     float alpha, hipStream_t st);
+// Y[:, cols_s] += alpha U_s F_s^T          (every adapter whose columns hold c)
+hipError_t lora_update(float *y, long ldy, int T, int r, const LoraSegs &g, float alpha,
+                       hipStream_t st);
+bool lora_fast_ok(DType xt, const void *x, long ldx, int r, const LoraSegs &g);
+bool lora_update_ok(const float *y, long ldy, int r, const LoraSegs &g);
+
 // bf16-output forward GEMM (used for LoRA intermediates and bf16 copies)
 hipError_t gemm_nt_bf16out(Mat x, Mat w, bf16 *y, long ldy, int M, int N, int K, float alpha,
                            hipStream_t st);

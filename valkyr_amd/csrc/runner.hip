@@ -462,7 +462,7 @@ struct vkh_runner {
         char *ew = nullptr;
         VKH_TRY(alloc(ew, embed_bw_work_bytes(T)));
         embed_work = ew;
-        if (lora) VKH_TRY(alloc(dyB, (size_t)T * R));
+        if (lora) VKH_TRY(alloc(dyB, (size_t)3 * T * R));  // dy B of up to three adapters
         VKH_TRY(alloc(tok_d, T));
         VKH_TRY(alloc(tgt_d, T));
         if (cfg.rotary_dim > 0) {
@@ -605,6 +605,38 @@ struct vkh_runner {
         VKH_HIP(gemm_nt(pr, matf(inter, R), matf(Bm, R), y, ldy, T, N, R, nullptr, 0, aor, 1.f, cur));
         return VKH_OK;
     }
+    // column of projection p in its fused output (and fused gradient)
+    long proj_col(int p) const {
+        return p == 1 ? qd : p == 2 ? qd + kvd : p == 5 ? F : 0;
+    }
+    // The LoRA terms of the targets among projections `ps`, which share the
+    // input x: inter_p = x A_p^T (one launch), then, with need_y, y[:, col_p
+    // ..] += aor inter_p B_p^T (one launch); the rank-r kernels where the
+    // shapes allow, else the general GEMMs per projection.
+    vkh_status lora_fwd_group(int l, std::initializer_list<int> ps, Mat x, float *y, long ldy,
+                              bool need_y = true) {
+        LoraSegs sa, sb;
+        for (int p : ps) {
+            if (!proj_lora(p)) continue;
+            int N, K;
+            proj_shape(p, N, K);
+            float *inter = acts[l].inter[p];
+            sa.s[sa.n++] = LoraSeg{0, K, W(ls[l].la[p]), 1, (long)K, inter, (long)R};
+            sb.s[sb.n++] = LoraSeg{proj_col(p), N, W(ls[l].lb[p]), (long)R, 1, inter, (long)R};
+        }
+        if (!sa.n) return VKH_OK;
+        if (lora_fast_ok(x.dt, x.p, x.ld, R, sa) && (!need_y || lora_update_ok(y, ldy, R, sb))) {
+            VKH_HIP(lora_rows(x.dt, x.p, x.ld, T, R, sa, 1.f, cur));
+            if (need_y) VKH_HIP(lora_update(y, ldy, T, R, sb, aor, cur));
+            return VKH_OK;
+        }
+        for (int p : ps) {
+            if (!proj_lora(p)) continue;
+            if (need_y) VKH_TRY(lora_fwd(l, p, x, y + proj_col(p), ldy));
+            else VKH_TRY(lora_inter(l, p, x));
+        }
+        return VKH_OK;
+    }
     // inter = x A^T, the rank-r intermediate the LoRA backward reads (dB)
     vkh_status lora_inter(int l, int p, Mat x) {
         int N, K;
@@ -701,9 +733,7 @@ struct vkh_runner {
                                 cfg.rms_eps, 0, cur));
         const Mat n1 = m_n1(a);
         VKH_TRY(linear_fwd(n1, s.t[1], a.qkv, qkvd, qkvd, D, nullptr, 0));
-        if (proj_lora(0)) VKH_TRY(lora_fwd(l, 0, n1, a.qkv, qkvd));
-        if (proj_lora(1)) VKH_TRY(lora_fwd(l, 1, n1, a.qkv + qd, qkvd));
-        if (proj_lora(2)) VKH_TRY(lora_fwd(l, 2, n1, a.qkv + qd + kvd, qkvd));
+        VKH_TRY(lora_fwd_group(l, {0, 1, 2}, n1, a.qkv, qkvd));
         const QkvLayout ql = qkv_layout();
         VKH_HIP(qkv_prepare_forward(ql, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                     cfg.qk_norm ? W(s.t[10]) : nullptr, a.qkv_attn, qkvd, adt,
@@ -719,20 +749,19 @@ struct vkh_runner {
         // mid = x_in + attn_out W_o^T (+ LoRA)
         const Mat att = m_attn(a);
         VKH_TRY(linear_fwd(att, s.t[4], a.mid, D, D, qd, x_in, D));
-        if (proj_lora(3)) VKH_TRY(lora_fwd(l, 3, att, a.mid, D));
+        VKH_TRY(lora_fwd_group(l, {3}, att, a.mid, D));
         VKH_HIP(rmsnorm_forward(a.mid, W(s.t[5]), b16() ? (void *)a.n2b : (void *)a.n2, odt, T, D,
                                 cfg.rms_eps, 0, cur));
         const Mat n2 = m_n2(a);
         VKH_TRY(linear_fwd(n2, s.t[6], a.gu, 2 * F, 2 * F, D, nullptr, 0));
-        if (proj_lora(4)) VKH_TRY(lora_fwd(l, 4, n2, a.gu, 2 * F));
-        if (proj_lora(5)) VKH_TRY(lora_fwd(l, 5, n2, a.gu + F, 2 * F));
+        VKH_TRY(lora_fwd_group(l, {4, 5}, n2, a.gu, 2 * F));
         VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F, b16() ? (void *)a.gatedb : (void *)a.gated,
                                F, odt, T, F, cur));
         const Mat gt = m_gated(a);
-        if (!need_y) return proj_lora(6) ? lora_inter(l, 6, gt) : VKH_OK;
+        if (!need_y) return lora_fwd_group(l, {6}, gt, nullptr, 0, false);
         // y = mid + gated W_down^T (+ LoRA)
         VKH_TRY(linear_fwd(gt, s.t[8], a.y, D, D, F, a.mid, D));
-        if (proj_lora(6)) VKH_TRY(lora_fwd(l, 6, gt, a.y, D));
+        VKH_TRY(lora_fwd_group(l, {6}, gt, a.y, D));
         return VKH_OK;
     }
 
@@ -761,6 +790,39 @@ struct vkh_runner {
         return VKH_OK;
     }
 
+    // LoRA backward of the targets among projections `ps`, which share the
+    // input x; dy is their fused output gradient (projection p at column
+    // proj_col(p)).  dy B for all of them, dx += aor (dy B) A, dA and dB:
+    // one launch each on the rank-r kernels where the shapes allow.
+    vkh_status lora_bwd_group(int l, std::initializer_list<int> ps, Mat dy, Mat x, float *dxo,
+                              long lddx) {
+        LoraSegs sb, sa, sda, sdb;
+        for (int p : ps) {
+            if (!proj_lora(p)) continue;
+            int N, K;
+            proj_shape(p, N, K);
+            float *db = dyB + (size_t)sb.n * T * R;
+            float *dA = G + (ls[l].la[p].off - tb), *dB = G + (ls[l].lb[p].off - tb);
+            sb.s[sb.n++] = LoraSeg{proj_col(p), N, W(ls[l].lb[p]), (long)R, 1, db, (long)R};
+            sa.s[sa.n++] = LoraSeg{0, K, W(ls[l].la[p]), 1, (long)K, db, (long)R};
+            sda.s[sda.n++] = LoraSeg{0, K, nullptr, 1, 1, db, (long)R, dA, 1, (long)K};
+            sdb.s[sdb.n++] = LoraSeg{proj_col(p), N, nullptr, 1, 1, acts[l].inter[p], (long)R, dB,
+                                     (long)R, 1};
+        }
+        if (!sb.n) return VKH_OK;
+        if (lora_fast_ok(dy.dt, dy.p, dy.ld, R, sb) && lora_fast_ok(x.dt, x.p, x.ld, R, sda) &&
+            lora_fast_ok(dy.dt, dy.p, dy.ld, R, sdb) && (!dxo || lora_update_ok(dxo, lddx, R, sa))) {
+            VKH_HIP(lora_rows(dy.dt, dy.p, dy.ld, T, R, sb, 1.f, cur));
+            if (dxo) VKH_HIP(lora_update(dxo, lddx, T, R, sa, aor, cur));
+            VKH_HIP(lora_cols(x.dt, x.p, x.ld, T, R, sda, aor, cur));
+            VKH_HIP(lora_cols(dy.dt, dy.p, dy.ld, T, R, sdb, aor, cur));
+            return VKH_OK;
+        }
+        for (int p : ps)
+            if (proj_lora(p)) VKH_TRY(lora_bwd(l, p, shift(dy, proj_col(p)), x, dxo, lddx));
+        return VKH_OK;
+    }
+
     // dy / dyb: the residual-stream gradient (fp32) and its bf16 copy; the
     // layer input gradient goes to dxo / dxob.
     vkh_status layer_backward(int l, const float *dy, const bf16 *dyb, float *dxo, bf16 *dxob) {
@@ -780,7 +842,7 @@ struct vkh_runner {
         // down: d_gated = dy W_down;  dW_down = dy^T gated
         VKH_TRY(linear_dx(mdy, s.t[8], d_gated, F, D, F));
         VKH_TRY(linear_dw(mdy, m_gated(a), s.t[8], D, F));
-        if (proj_lora(6)) VKH_TRY(lora_bwd(l, 6, mdy, m_gated(a), d_gated, F));
+        VKH_TRY(lora_bwd_group(l, {6}, mdy, m_gated(a), d_gated, F));
         // swiglu: d_gu = [d_gate | d_up] (bf16 copy only in the bf16 precision)
         if (b16())
             VKH_HIP(swiglu_backward(d_gated, F, a.gu, 2 * F, a.gu + F, 2 * F, d_gub, 2 * F, d_gub + F,
@@ -792,8 +854,7 @@ struct vkh_runner {
         // gate/up (one [2F, D] matrix): d_n2 = d_gu W_gu; dW_gu = d_gu^T n2
         VKH_TRY(linear_dx(mdgu, s.t[6], d_n, D, 2 * F, D));
         VKH_TRY(linear_dw(mdgu, m_n2(a), s.t[6], 2 * F, D));
-        if (proj_lora(4)) VKH_TRY(lora_bwd(l, 4, mdgu, m_n2(a), d_n, D));
-        if (proj_lora(5)) VKH_TRY(lora_bwd(l, 5, shift(mdgu, F), m_n2(a), d_n, D));
+        VKH_TRY(lora_bwd_group(l, {4, 5}, mdgu, m_n2(a), d_n, D));
         // n2: d_mid = rmsnorm_bw(d_n2) + dy
         VKH_HIP(rmsnorm_backward(d_n, a.mid, W(s.t[5]), d_mid, d_midb, dy,
                                  concurrent ? nullptr : Gd(s.t[5]), concurrent ? lg[l].pn2 : partial,
@@ -810,7 +871,7 @@ struct vkh_runner {
         else
             VKH_TRY(linear_dx(mdmid, s.t[4], d_attn_out, qd, D, qd));
         VKH_TRY(linear_dw(mdmid, m_attn(a), s.t[4], D, qd));
-        if (proj_lora(3)) VKH_TRY(lora_bwd(l, 3, mdmid, m_attn(a), d_attn_out, qd));
+        VKH_TRY(lora_bwd_group(l, {3}, mdmid, m_attn(a), d_attn_out, qd));
         // attention: D, dK/dV, dQ into the fused d_qkv buffer
         if (b16() && adt == DType::BF16) {
             if (!do_bf16) VKH_HIP(cast_f32_to_bf16(d_attn_out, dout16, (size_t)T * qd, cur));
@@ -856,9 +917,7 @@ struct vkh_runner {
         // q/k/v (one [qkvd, D] matrix): d_n1 = d_qkv W_qkv; dW_qkv = d_qkv^T n1
         VKH_TRY(linear_dx(mdqkv, s.t[1], d_n, D, qkvd, D));
         VKH_TRY(linear_dw(mdqkv, m_n1(a), s.t[1], qkvd, D));
-        if (proj_lora(0)) VKH_TRY(lora_bwd(l, 0, mdqkv, m_n1(a), d_n, D));
-        if (proj_lora(1)) VKH_TRY(lora_bwd(l, 1, shift(mdqkv, qd), m_n1(a), d_n, D));
-        if (proj_lora(2)) VKH_TRY(lora_bwd(l, 2, shift(mdqkv, qd + kvd), m_n1(a), d_n, D));
+        VKH_TRY(lora_bwd_group(l, {0, 1, 2}, mdqkv, m_n1(a), d_n, D));
         // n1: d_x_in = rmsnorm_bw(d_n1) + d_mid
         VKH_HIP(rmsnorm_backward(d_n, x_in, W(s.t[0]), dxo, dxob, d_mid,
                                  concurrent ? nullptr : Gd(s.t[0]), concurrent ? lg[l].pn1 : partial,
