@@ -6,6 +6,8 @@
 // Tile plan (measured on MI355X with DMA staging, T = 2048-token step shapes):
 //   * >= 512 tiles of 256 x 256       -> 256 x 256, 8 waves (vocab-sized GEMMs)
 //   * >= 512 tiles of 128 x 128       -> 128 x 128, 8 waves of 64 x 32
+//   * K >= 16384 and >= 256 tiles of 128 x 128 -> 256 x 256 split-K 3 ways
+//   * K >= 4096 and >= 256 tiles of 128 x 128  -> 128 x 128, 8 waves
 //   * K >= 16384 and < 256 such tiles -> 128 x 128 split-K, up to 4 ways (head dh)
 //   * < 384 tiles of 128 x 64, K >= 2048 -> 128 x 64 split-K 2 ways
 //   * otherwise                       -> 128 x 64
@@ -41,6 +43,7 @@ struct Plan {
 size_t ws_for(const Plan &p, const GemmShape &s) {
     if (p.splits <= 1) return 0;
     switch (p.tile) {
+    case Pick::Big: return gemm16_ws_bytes<TBig>(s, p.splits);
     case Pick::T128: return gemm16_ws_bytes<T128>(s, p.splits);
     case Pick::T128w8: return gemm16_ws_bytes<T128w8>(s, p.splits);
     default: return gemm16_ws_bytes<T128x64>(s, p.splits);
@@ -54,7 +57,16 @@ Plan plan(const GemmShape &s, size_t ws_bytes) {
     if (t128 >= 512) return {Pick::T128w8, 1};
     const int nk = (s.K + 63) / 64;
     Plan p{Pick::T128x64, 1};
-    if (s.K >= 16384 && t128 < 256)
+    if (s.K >= 16384 && t128 >= 256)
+        // a long contraction onto at least a chip-wide wave of 128 x 128 tiles
+        // (Qwen3-4B gate/up dx, K = 19456): 256 x 256 split 3 ways, 199 us
+        // against 236 (128 x 128, 8 waves) and 361 (128 x 64)
+        p = Plan{Pick::Big, 3};
+    else if (s.K >= 4096 && t128 >= 256)
+        // Qwen3-4B o / down forward and q/k/v dx (N = 2560, K = 4096..9728):
+        // 128 x 128 on 8 waves, 50 / 113 / 79 us against 56 / 167 / 104 (128 x 64)
+        p = Plan{Pick::T128w8, 1};
+    else if (s.K >= 16384 && t128 < 256)
         p = Plan{Pick::T128, (int)std::min<long>(4, std::max<long>(1, 512 / t128))};
     else if (t64 < 384 && s.K >= 2048)
         // two wave groups in one block: alone, faster than split-K + reduce up
