@@ -1079,6 +1079,113 @@ __global__ __launch_bounds__(dkv3::NT3, 1) void fa_bwd_dkv3_k(AttnShape s, AttnP
 // waves per SIMD with 32 each, so one wave's softmax / dS arithmetic overlaps
 // the other wave's MFMAs; on MI355X the 8-wave forms are the faster ones and
 // are the ones launched.
+// ── fused q/k gradient epilogue (recompute kernels) ───────────────────
+// The recompute kernels end with dQ / dK rows in the accumulator layout: the
+// four lanes g = 0..3 of one c16 hold a head row (head_dim 128), lane g its
+// elements d = 16 i + 4 g + r in v[i][r].  qk_row_bwd takes such a row back
+// through RoPE (rotary_dim = head_dim: pairs d, d + 64 sit in tiles i, i + 4
+// of the same lane, both rotated by table column d) and the Q/K-RMSNorm
+// (fp64 row sums as in qkv_bwd8_k, combined over the four lanes), and adds
+// the row's gain-gradient terms v_rot * ri * x to dw.  Every lane of the
+// wave calls it (lane shuffles); `ok` masks rows past the sequence.
+VKH_DEV void qk_row_bwd(float (&v)[8][4], float (&dw)[8][4], bool ok, const QkEpi &e,
+                        const float *xrow, const float *gain, int pos, int g) {
+    if (e.rot) {
+        const float2 *tr = e.rope + (long)pos * 64 + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            float4 c01 = make_float4(1.f, 0.f, 1.f, 0.f), c23 = c01;
+            if (ok) {
+                c01 = *reinterpret_cast<const float4 *>(tr + 16 * i);
+                c23 = *reinterpret_cast<const float4 *>(tr + 16 * i + 2);
+            }
+            const float cs[4][2] = {{c01.x, c01.y}, {c01.z, c01.w}, {c23.x, c23.y}, {c23.z, c23.w}};
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float lo = v[i][r], hi = v[i + 4][r];
+                v[i][r] = cs[r][0] * lo + cs[r][1] * hi;
+                v[i + 4][r] = -cs[r][1] * lo + cs[r][0] * hi;
+            }
+        }
+    }
+    if (!gain) return;
+    float x[8][4], gw[8][4];
+    double ss = 0, A = 0;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const float4 xv = ok ? *reinterpret_cast<const float4 *>(xrow + 16 * i + 4 * g)
+                             : make_float4(0.f, 0.f, 0.f, 0.f);
+        const float4 gv = *reinterpret_cast<const float4 *>(gain + 16 * i + 4 * g);
+        x[i][0] = xv.x; x[i][1] = xv.y; x[i][2] = xv.z; x[i][3] = xv.w;
+        gw[i][0] = gv.x; gw[i][1] = gv.y; gw[i][2] = gv.z; gw[i][3] = gv.w;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            ss += (double)x[i][r] * (double)x[i][r];
+            A += (double)v[i][r] * (double)gw[i][r] * (double)x[i][r];
+        }
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    A += __shfl_xor(A, 16, 64);
+    A += __shfl_xor(A, 32, 64);
+    const float ri = 1.0f / sqrtf((float)(ss / 128.0) + e.eps);
+    const float ri3 = ri * ri * ri / 128.0f;
+    const float Af = (float)A;
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            if (ok) dw[i][r] += v[i][r] * ri * x[i][r];
+            v[i][r] = ri * gw[i][r] * v[i][r] - ri3 * x[i][r] * Af;
+        }
+}
+
+VKH_DEV void st_row_bf16(bf16 *row, const float (&v)[8][4], int g) {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        bf16x4 o;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] = (bf16)v[i][r];
+        *reinterpret_cast<bf16x4 *>(row + 16 * i + 4 * g) = o;
+    }
+}
+
+// Gain-gradient partial of a block: dw summed over the 16 rows of each lane
+// group (a fixed xor tree), then over waves 0..nw-1 in order through `red`
+// ([nw][128] floats of LDS); the sum goes to part[0..127].  Every thread of
+// the block calls it (barriers); waves with `mine` false only take part in
+// the barriers.
+VKH_DEV void qk_dw_block(float (&dw)[8][4], float *red, int wave, int nw, bool mine, int lane,
+                         float *part) {
+    if (mine) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float a = dw[i][r];
+                a += __shfl_xor(a, 1, 64);
+                a += __shfl_xor(a, 2, 64);
+                a += __shfl_xor(a, 4, 64);
+                a += __shfl_xor(a, 8, 64);
+                dw[i][r] = a;
+            }
+        if (lane % 16 == 0) {
+            const int g = lane / 16;
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) red[wave * 128 + 16 * i + 4 * g + r] = dw[i][r];
+        }
+    }
+    __syncthreads();
+    const int tid = threadIdx.x;
+    if (tid < 128) {
+        float a = red[tid];
+        for (int w = 1; w < nw; ++w) a += red[w * 128 + tid];
+        part[tid] = a;
+    }
+}
+
 namespace dkv4 {
 constexpr int HD = 128, BM = 32, BN = 128;
 constexpr int DS = HD / 32, DSUB = HD / 16, QS = BM / 16;
@@ -1106,7 +1213,7 @@ static_assert(2 * STREAM + BN * HD * 2 <= LDS, "tile streams and V slices exceed
 // of one (sequence, KV head), which sit on one XCD, read a tile at about the
 // same time and share it in L2.  Under a causal mask the heaviest key blocks
 // (lowest keys) have the lowest block ids and start first.
-template <int NWV>
+template <int NWV, bool QKE>
 __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPtrs p) {
     using namespace dkv4;
     constexpr int NS = NWV / 2;                 // key slices per head group
@@ -1358,8 +1465,40 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     if (hg == 0) give(dkt);
     else give(dvt);
     __syncthreads();
-    if (hg == 0) keep(dvt, p.dv, p.lddv, 1.0f);
-    else keep(dkt, p.dk, p.lddk, s.inv_sqrt_dim);
+    if constexpr (!QKE) {
+        if (hg == 0) keep(dvt, p.dv, p.lddv, 1.0f);
+        else keep(dkt, p.dk, p.lddk, s.inv_sqrt_dim);
+    } else {
+        // bf16 rows of the fused [T, (H + 2 Hkv) hd] gradient: dV as is, dK
+        // back through RoPE and the K-RMSNorm (gain partials per block)
+        __shared__ float red[NS * 128];
+        const QkEpi &e = p.qk;
+        float dw[8][4] = {};
+        const int kcol = s.n_heads * HD + kvh * HD, vcol = kcol + s.n_kv_heads * HD;
+        auto rows = [&](const f32x4(&a)[DSUB][KS], bool is_k) {
+#pragma unroll
+            for (int ks = 0; ks < KS; ++ks) {
+                const int key = kw0 + 16 * ks + c16;
+                const long t = (long)b * s.n_kv + key;
+                const float sc_ = is_k ? s.inv_sqrt_dim : 1.0f;
+                float v[8][4];
+#pragma unroll
+                for (int i = 0; i < DSUB; ++i) {
+                    const f32x4 w = a[i][ks] + xp[(i * KS + ks) * 64 + lane];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) v[i][r] = w[r] * sc_;
+                }
+                if (is_k) qk_row_bwd(v, dw, true, e, e.x + t * e.ldx + kcol, e.gk, key, g);
+                st_row_bf16(e.out + t * e.ldout + (is_k ? kcol : vcol), v, g);
+            }
+        };
+        if (hg == 0) rows(dvt, false);
+        else rows(dkt, true);
+        if (e.gk) {
+            const int blk = blockIdx.y * gridDim.x + blockIdx.x;
+            qk_dw_block(dw, red, sl, NS, hg == 1, lane, e.pk + (long)blk * 128);
+        }
+    }
 }
 
 namespace dq4 {
@@ -1384,7 +1523,7 @@ constexpr int NBUF = 3;
 // WITH_D: D = rowsum(O dO) of the block's rows is formed here from bf16 O (the
 // lane's 32 products in fp64, then the row's four lanes) and stored to p.d
 // for the dK/dV kernel, which then runs after this one; no separate pass.
-template <int NWV, bool WITH_D>
+template <int NWV, bool WITH_D, bool QKE>
 __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs p) {
     using namespace dq4;
     constexpr int QSUB = BQ / 16 / NWV;  // 16-row query sub-tiles per wave
@@ -1551,6 +1690,30 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
         if (t0 + 2 < ntl) step(t0 + 2, std::integral_constant<int, 2>{});
     }
     // acc[i][j][r] = dQ^T[16 i + 4 g + r][q00 + 64 j + c16]
+    if constexpr (QKE) {
+        // bf16 rows of the fused gradient, back through RoPE and the Q-RMSNorm
+        __shared__ float red[NWV * 128];
+        const QkEpi &e = p.qk;
+        float dw[8][4] = {};
+#pragma unroll
+        for (int j = 0; j < QSUB; ++j) {
+            const int q = q00 + QST * j + c16;
+            const bool ok = q < s.n_q;
+            const long t = (long)b * s.n_q + (ok ? q : 0);
+            float v[8][4];
+#pragma unroll
+            for (int i = 0; i < DSUB; ++i)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) v[i][r] = acc[i][j][r] * s.inv_sqrt_dim;
+            qk_row_bwd(v, dw, ok, e, e.x + t * e.ldx + h * HD, e.gq, ok ? q : 0, g);
+            if (ok) st_row_bf16(e.out + t * e.ldout + h * HD, v, g);
+        }
+        if (e.gq) {
+            const int blk = blockIdx.y * gridDim.x + blockIdx.x;
+            qk_dw_block(dw, red, wave, NWV, true, lane, e.pq + (long)blk * 128);
+        }
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < QSUB; ++j) {
         const int q = q00 + QST * j + c16;
@@ -2020,6 +2183,16 @@ bool fa_bw_v4_preferred(const AttnShape &s) {
     return fa_bw_v4_ok(s) && (long)s.n_batch * s.n_kv_heads * (s.n_kv / 128) >= 128;
 }
 
+int fa_bw_v4_q_blocks(const AttnShape &s) {
+    return s.n_heads * s.n_batch * ((s.n_q + dq4::BQ - 1) / dq4::BQ);
+}
+int fa_bw_v4_kv_blocks(const AttnShape &s) { return s.n_kv_heads * s.n_batch * (s.n_kv / dkv4::BN); }
+// The epilogue's row layout assumes head_dim 128 and a rotary span of 0 or
+// the whole head (pairs 64 apart).
+bool fa_bw_qk_epi_ok(const AttnShape &s, int rotary_dim) {
+    return fa_bw_v4_ok(s) && (rotary_dim == 0 || rotary_dim == s.head_dim);
+}
+
 size_t fa_bw_ws_bytes(const AttnShape &s, bool v4) {
     if (v4) return 0;
     return (size_t)s.n_batch * s.n_heads * s.n_q * s.n_kv * sizeof(bf16);
@@ -2038,12 +2211,21 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
         constexpr int DKV_WAVES = 8, DQ_WAVES = 8;
         const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
         const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
-        if (p.o16) {  // dQ forms D, then dK/dV reads it
-            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
-            hipLaunchKernelGGL(fa_bwd_dkv4_k<DKV_WAVES>, gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+        const QkEpi &e = p.qk;
+        if (e.out) {
+            // fused q/k epilogue: dQ forms D (needs bf16 O), then dK/dV
+            if (!p.o16 || !fa_bw_qk_epi_ok(s, e.rot) || !e.x || e.ldout % 8 || e.ldx % 4 ||
+                ((uintptr_t)e.out & 15) || ((uintptr_t)e.x & 15) || (e.rot && !e.rope) ||
+                (bool)e.gq != (bool)e.gk || (e.gq && (!e.pq || !e.pk)))
+                return hipErrorInvalidValue;
+            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true, true>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            hipLaunchKernelGGL((fa_bwd_dkv4_k<DKV_WAVES, true>), gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+        } else if (p.o16) {  // dQ forms D, then dK/dV reads it
+            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            hipLaunchKernelGGL((fa_bwd_dkv4_k<DKV_WAVES, false>), gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
         } else {
-            hipLaunchKernelGGL(fa_bwd_dkv4_k<DKV_WAVES>, gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
-            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            hipLaunchKernelGGL((fa_bwd_dkv4_k<DKV_WAVES, false>), gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, false, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
         }
         return hipGetLastError();
     }

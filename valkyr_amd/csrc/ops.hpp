@@ -188,6 +188,23 @@ struct AttnShape {
     int causal;
     float inv_sqrt_dim;
 };
+// Fused q/k gradient epilogue of the recompute attention backward: dQ, dK
+// and dV leave the kernels as bf16 rows of one [T, (H + 2 Hkv) hd] matrix
+// (q heads, then k, then v), dQ and dK already taken back through RoPE and
+// the Q/K-RMSNorm (the gradient w.r.t. the pre-norm projection output), with
+// the norm-gain gradient as one head_dim row of partial sums per block.
+struct QkEpi {
+    bf16 *out = nullptr;                      // set: the epilogue runs
+    long ldout = 0;
+    const float *x = nullptr;                 // pre-norm q / k rows (same column layout)
+    long ldx = 0;
+    const float *gq = nullptr, *gk = nullptr; // norm gains (null: no Q/K-RMSNorm)
+    float eps = 0.f;
+    const float2 *rope = nullptr;             // [n_pos][head_dim / 2] (cos, sin)
+    int rot = 0;                              // rotary_dim: 0 or head_dim
+    float *pq = nullptr, *pk = nullptr;       // gain partials [blocks][head_dim]
+};
+
 struct AttnPtrs {
     const void *q; long ldq;   // [T, n_heads*hd] rows, elements of dtype dt
     const void *k; long ldk;
@@ -203,6 +220,7 @@ struct AttnPtrs {
     // bf16 O: when set on the recompute path, the dQ kernel forms
     // D = rowsum(O dO) for its rows itself (written to d) and runs first
     const void *o16 = nullptr; long ldo16 = 0;
+    QkEpi qk;  // recompute path only
 };
 // ob (optional, bf16 operands only): bf16 copy of O for the output projection.
 hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
@@ -225,6 +243,11 @@ hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 bool fa_bw_fused_ok(const AttnShape &s);
 bool fa_bw_v4_ok(const AttnShape &s);
 bool fa_bw_v4_preferred(const AttnShape &s);
+// Gain-partial rows the fused q/k epilogue writes (dQ kernel: q gains; dK/dV
+// kernel: k gains), and whether a shape / rotary_dim can take it.
+int fa_bw_v4_q_blocks(const AttnShape &s);
+int fa_bw_v4_kv_blocks(const AttnShape &s);
+bool fa_bw_qk_epi_ok(const AttnShape &s, int rotary_dim);
 size_t fa_bw_ws_bytes(const AttnShape &s, bool v4);
 hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool v4, hipStream_t st);
 

@@ -92,6 +92,7 @@ struct vkh_runner {
     bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward (when it needs one)
     bool attn_fused = false;  // bf16 attention backward on fa_bw_fused
     bool attn_v4 = false;     // ... on its recompute kernels (no dS workspace)
+    bool qk_fused = false;    // ... with RoPE^T / Q/K-norm backward in their epilogues
     GemmWs gws{nullptr, 0};
     // Concurrent weight gradients (bf16 full fine-tune): each layer's dW GEMMs
     // and its Adam update run on a second stream one layer behind the main
@@ -101,6 +102,12 @@ struct vkh_runner {
         // norm-gain partial sums (n1, n2, q/k norm), reduced on the side stream
         float *pn1 = nullptr, *pn2 = nullptr, *pqk = nullptr;
         int qk_parts = 0;
+        // where this step's q / k gain partials went: rows of `stride` floats
+        // (interleaved q|k rows from the Q/K-norm kernel, or the attention
+        // kernels' separate q and k rows)
+        float *pq = nullptr, *pk = nullptr;
+        int q_parts = 0, k_parts = 0;
+        long qk_stride = 0;
     };
     bool concurrent = false;
     // Per-layer activation recompute: each layer keeps its output y (the next
@@ -381,6 +388,7 @@ struct vkh_runner {
             }
             attn_fused = adt == DType::BF16 && fa_bw_fused_ok(attn_shape());
             attn_v4 = attn_fused && fa_bw_v4_preferred(attn_shape());
+            qk_fused = attn_v4 && fa_bw_qk_epi_ok(attn_shape(), (int)cfg.rotary_dim);
             if (attn_fused && fa_bw_ws_bytes(attn_shape(), attn_v4))
                 VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape(), attn_v4) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
@@ -425,7 +433,7 @@ struct vkh_runner {
                     VKH_TRY(alloc(lg[l].qkvb, (size_t)T * qkvd));
                     VKH_TRY(alloc(lg[l].pn1, rmsnorm_partial_floats(T, D)));
                     VKH_TRY(alloc(lg[l].pn2, rmsnorm_partial_floats(T, D)));
-                    if (cfg.qk_norm) VKH_TRY(alloc(lg[l].pqk, qkv_partial_floats(qkv_layout())));
+                    if (cfg.qk_norm) VKH_TRY(alloc(lg[l].pqk, qk_partial_floats()));
                 }
                 if (wsb) {
                     char *w = nullptr;
@@ -450,9 +458,8 @@ struct vkh_runner {
         VKH_TRY(alloc(dx[1], (size_t)T * D));
         VKH_TRY(alloc(d_fn, (size_t)T * D));
         if (adt == DType::BF16) VKH_TRY(alloc(dout16, (size_t)T * qd));
-        QkvLayout ql = qkv_layout();
         size_t pf = rmsnorm_partial_floats(T, D);
-        if (qkv_partial_floats(ql) > pf) pf = qkv_partial_floats(ql);
+        if (qk_partial_floats() > pf) pf = qk_partial_floats();
         VKH_TRY(alloc(partial, pf));
         CceShape cs{T, V, D, 0.f, 0.f};
         VKH_TRY(alloc(cce_work, cce_work_floats(cs)));
@@ -474,6 +481,16 @@ struct vkh_runner {
         }
         VKH_HIP(hipStreamSynchronize(own));
         return VKH_OK;
+    }
+
+    // floats of q / k gain partials one layer's backward writes (either path)
+    size_t qk_partial_floats() const {
+        size_t n = qkv_partial_floats(qkv_layout());
+        if (qk_fused) {
+            const AttnShape as = attn_shape();
+            n = std::max(n, (size_t)(fa_bw_v4_q_blocks(as) + fa_bw_v4_kv_blocks(as)) * hd);
+        }
+        return n;
     }
 
     QkvLayout qkv_layout() const {
@@ -697,8 +714,8 @@ struct vkh_runner {
         VKH_HIP(column_sums(g.pn2, rp, D, D, Gd(s.t[5]), side));
         VKH_HIP(column_sums(g.pn1, rp, D, D, Gd(s.t[0]), side));
         if (cfg.qk_norm) {
-            VKH_HIP(column_sums(g.pqk, g.qk_parts, 2L * hd, hd, Gd(s.t[9]), side));
-            VKH_HIP(column_sums(g.pqk + hd, g.qk_parts, 2L * hd, hd, Gd(s.t[10]), side));
+            VKH_HIP(column_sums(g.pq, g.q_parts, g.qk_stride, hd, Gd(s.t[9]), side));
+            VKH_HIP(column_sums(g.pk, g.k_parts, g.qk_stride, hd, Gd(s.t[10]), side));
         }
         return VKH_OK;
     }
@@ -897,22 +914,51 @@ struct vkh_runner {
             ap.o16 = a.attn_b;
             ap.ldo16 = qd;
         }
-        if (attn_fused) {
-            VKH_HIP(fa_bw_fused(as, ap, attn_ds, attn_v4, cur));
-        } else {
-            VKH_HIP(fa_bw_dkv(as, ap, cur));
-            VKH_HIP(fa_bw_dq(as, ap, cur));
-        }
-        // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
-        const QkvLayout ql = qkv_layout();
         const bool qk_side = concurrent && cfg.qk_norm;
-        VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
-                                     cfg.qk_norm ? W(s.t[10]) : nullptr,
-                                     cfg.qk_norm && !qk_side ? Gd(s.t[9]) : nullptr,
-                                     cfg.qk_norm && !qk_side ? Gd(s.t[10]) : nullptr,
-                                     qk_side ? lg[l].pqk : partial, rope_tab,
-                                     b16() ? d_qkvb : nullptr, qkvd, cur,
-                                     qk_side ? &lg[l].qk_parts : nullptr));
+        float *qkp = qk_side ? lg[l].pqk : partial;
+        if (qk_fused) {
+            // RoPE^T and the Q/K-norm backward in the attention kernels'
+            // epilogues, straight into the bf16 gradient copy
+            QkEpi &e = ap.qk;
+            e.out = d_qkvb; e.ldout = qkvd;
+            e.x = a.qkv; e.ldx = qkvd;
+            e.gq = cfg.qk_norm ? W(s.t[9]) : nullptr;
+            e.gk = cfg.qk_norm ? W(s.t[10]) : nullptr;
+            e.eps = cfg.rms_eps;
+            e.rope = rope_tab; e.rot = (int)cfg.rotary_dim;
+            const int nq = fa_bw_v4_q_blocks(as);
+            e.pq = qkp;
+            e.pk = qkp + (size_t)nq * hd;
+            VKH_HIP(fa_bw_fused(as, ap, attn_ds, true, cur));
+            if (qk_side) {
+                lg[l].pq = e.pq; lg[l].pk = e.pk;
+                lg[l].q_parts = nq; lg[l].k_parts = fa_bw_v4_kv_blocks(as);
+                lg[l].qk_stride = hd;
+            } else if (cfg.qk_norm && !lora) {
+                VKH_HIP(column_sums(e.pq, nq, hd, hd, Gd(s.t[9]), cur));
+                VKH_HIP(column_sums(e.pk, fa_bw_v4_kv_blocks(as), hd, hd, Gd(s.t[10]), cur));
+            }
+        } else {
+            if (attn_fused) {
+                VKH_HIP(fa_bw_fused(as, ap, attn_ds, attn_v4, cur));
+            } else {
+                VKH_HIP(fa_bw_dkv(as, ap, cur));
+                VKH_HIP(fa_bw_dq(as, ap, cur));
+            }
+            // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
+            const QkvLayout ql = qkv_layout();
+            VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
+                                         cfg.qk_norm ? W(s.t[10]) : nullptr,
+                                         cfg.qk_norm && !qk_side ? Gd(s.t[9]) : nullptr,
+                                         cfg.qk_norm && !qk_side ? Gd(s.t[10]) : nullptr, qkp,
+                                         rope_tab, b16() ? d_qkvb : nullptr, qkvd, cur,
+                                         qk_side ? &lg[l].qk_parts : nullptr));
+            if (qk_side) {
+                lg[l].pq = qkp; lg[l].pk = qkp + hd;
+                lg[l].q_parts = lg[l].k_parts = lg[l].qk_parts;
+                lg[l].qk_stride = 2L * hd;
+            }
+        }
         const Mat mdqkv = b16() ? matb(d_qkvb, qkvd) : matf(d_qkv, qkvd);
         // q/k/v (one [qkvd, D] matrix): d_n1 = d_qkv W_qkv; dW_qkv = d_qkv^T n1
         VKH_TRY(linear_dx(mdqkv, s.t[1], d_n, D, qkvd, D));
@@ -1004,8 +1050,8 @@ struct vkh_runner {
         add(ss.t[0], g.pn1, rp, D);
         add(ss.t[5], g.pn2, rp, D);
         if (cfg.qk_norm) {
-            add(ss.t[9], g.pqk, g.qk_parts, 2L * hd);
-            add(ss.t[10], g.pqk + hd, g.qk_parts, 2L * hd);
+            add(ss.t[9], g.pq, g.q_parts, g.qk_stride);
+            add(ss.t[10], g.pk, g.k_parts, g.qk_stride);
         }
         const float t = (float)step_t;
         const float bc1 = 1.0f - powf(cfg.beta1, t);
