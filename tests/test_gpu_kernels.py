@@ -248,6 +248,24 @@ LORA_SHAPES = [(256, 384, 256, 16), (200, 384, 256, 16), (256, 384, 256, 8),
                (512, 1024, 2560, 16), (130, 100, 72, 6)]
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 1023, 4096 * 1024 + 5, 33 * 1024 * 1024])
+def test_scale_add_exact(n):
+    """scale / add_in_place / vec_add (the reference's scale and add shaders):
+    one fp32 rounding per element, so bit-exact against numpy; sizes cover
+    the chunked aligned kernel, its n % 4 tail and the short-vector path."""
+    from valkyr_amd import kernels as K
+
+    x = O.normal(n, 31)
+    y = O.normal(n, 32)
+    bx, by, bo = dev(x), dev(y), zeros(n)
+    K.scale(bx, bo, n, 0.37)
+    assert np.array_equal(host(bo, n), x * np.float32(0.37))
+    K.vec_add(bx, by, bo, n)
+    assert np.array_equal(host(bo, n), x + y)
+    K.add_in_place(bo, bx, n)
+    assert np.array_equal(host(bo, n), (x + y) + x)
+
+
 @pytest.mark.parametrize("prec", [0, 1])
 @pytest.mark.parametrize("shape", LORA_SHAPES)
 def test_lora_forward_backward(prec, shape):

@@ -61,6 +61,31 @@ __global__ void scale_k(const float *in, float *out, size_t n, float s, bool vec
         out[i] = in[i] * s;
 }
 
+// The aligned form: each block streams one contiguous chunk of NT * SC_U
+// float4 (16 KB in, 16 KB out), all loads issued before the stores,
+// non-temporal (the stream is not reused); the last n % 4 elements in block
+// 0.  As a plain read-n / write-n stream it is also the copy ceiling the
+// bandwidth kernels are measured against.
+constexpr int SC_U = 4;
+__global__ __launch_bounds__(NT) void scale_chunk_k(const float *in_, float *out_, size_t n, float s) {
+    const size_t n4 = n / 4;
+    const f32x4 *in = reinterpret_cast<const f32x4 *>(in_);
+    f32x4 *out = reinterpret_cast<f32x4 *>(out_);
+    const size_t base = (size_t)blockIdx.x * (NT * SC_U) + threadIdx.x;
+    f32x4 x[SC_U];
+#pragma unroll
+    for (int u = 0; u < SC_U; ++u) {
+        const size_t j = base + (size_t)u * NT;
+        if (j < n4) x[u] = __builtin_nontemporal_load(&in[j]);
+    }
+#pragma unroll
+    for (int u = 0; u < SC_U; ++u) {
+        const size_t j = base + (size_t)u * NT;
+        if (j < n4) __builtin_nontemporal_store(x[u] * s, &out[j]);
+    }
+    if (blockIdx.x == 0 && threadIdx.x < n - 4 * n4) out_[4 * n4 + threadIdx.x] = in_[4 * n4 + threadIdx.x] * s;
+}
+
 __global__ void cast_bf16_k(const float *in, bf16 *out, size_t n, bool vec) {
     const size_t n4 = vec ? n / 4 : 0;
     const size_t stride = (size_t)gridDim.x * blockDim.x;
@@ -446,6 +471,11 @@ hipError_t vec_add(const float *a, const float *b, float *c, size_t n, hipStream
 
 hipError_t scale(const float *in, float *out, size_t n, float s, hipStream_t st) {
     if (!n) return hipSuccess;
+    const size_t blocks = (n / 4 + NT * SC_U - 1) / (NT * SC_U);
+    if (al16(in) && al16(out) && blocks >= 1 && blocks < (1u << 31)) {
+        hipLaunchKernelGGL(scale_chunk_k, dim3((unsigned)blocks), dim3(NT), 0, st, in, out, n, s);
+        return hipGetLastError();
+    }
     hipLaunchKernelGGL(scale_k, dim3(grid_for(n / 4 + 1)), dim3(NT), 0, st, in, out, n, s,
                        al16(in) && al16(out));
     return hipGetLastError();
