@@ -1362,15 +1362,19 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks) sc[qs][ks] = mfma16x16x32(fr[f & 1], kr[ks][ds], sc[qs][ks]);
         }
-        // dP = dO V^T (V from LDS), with P = exp2(S c - lse) of tile (f / 4, f % 4)
+        // dP = dO V^T (V from LDS, each fragment read once and used for both
+        // query halves), with P = exp2(S c - lse) of tile (f / 4, f % 4)
+        bf16x8 vf[KS];
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
             const int ds = f / 2, qs = f % 2, n = f + 1;
+            if (qs == 0)
+#pragma unroll
+                for (int ks = 0; ks < KS; ++ks) vf[ks] = frag_row(vsl, 16 * ks + c16, 32 * ds + 8 * g);
             fr[n & 1] = n < 8 ? frag_row(Ob, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
                               : frag_t(Ob, 0, 0, g, c16);
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks)
-                dp[qs][ks] = mfma16x16x32(fr[f & 1], frag_row(vsl, 16 * ks + c16, 32 * ds + 8 * g), dp[qs][ks]);
+            for (int ks = 0; ks < KS; ++ks) dp[qs][ks] = mfma16x16x32(fr[f & 1], vf[ks], dp[qs][ks]);
             // the QS * KS score tiles spread evenly over the 8 steps
             constexpr int EVERY = 8 / (QS * KS);
             static_assert(EVERY >= 1 && EVERY * QS * KS == 8, "exp schedule");
@@ -1626,27 +1630,34 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
             for (int j = 0; j < QSUB; ++j) st[ks][j] = dpt[ks][j] = f32x4{0, 0, 0, 0};
-        // Each phase walks its 8 operand fragments f = (ds, ks) = (f / 2, f % 2)
-        // with the next fragment's LDS read issued before this one's MFMAs.
-        bf16x8 fr[2];
-        fr[0] = frag_row(Kb, c16, 8 * g);
+        // The three phases walk 24 operand fragments in one sequence (slots
+        // 0-7: K rows for S^T, f = (ds, ks) = (f / 2, f % 2); 8-15: V rows for
+        // dP^T; 16-23: transposed K for dQ^T), each slot's LDS read issued PD
+        // slots ahead of its MFMAs through a ring of PD + 1 fragments.
+        constexpr int PD = 2, RING = PD + 1;
+        auto ldslot = [&](int n) -> bf16x8 {
+            if (n < 8) return frag_row(Kb, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g);
+            if (n < 16) return frag_row(Vb, 16 * ((n - 8) % 2) + c16, 32 * ((n - 8) / 2) + 8 * g);
+            return frag_t(Kb, 16 * (n - 16), 0, g, c16);
+        };
+        bf16x8 fr[RING];
+#pragma unroll
+        for (int n = 0; n < PD; ++n) fr[n] = ldslot(n);
         // S^T = K Q^T
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            const int ds = f / 2, ks = f % 2, n = f + 1;
-            fr[n & 1] = n < 8 ? frag_row(Kb, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
-                              : frag_row(Vb, c16, 8 * g);
+            const int ds = f / 2, ks = f % 2, n = f;
+            fr[(n + PD) % RING] = ldslot(n + PD);
 #pragma unroll
-            for (int j = 0; j < QSUB; ++j) st[ks][j] = mfma16x16x32(fr[f & 1], qr[j][ds], st[ks][j]);
+            for (int j = 0; j < QSUB; ++j) st[ks][j] = mfma16x16x32(fr[n % RING], qr[j][ds], st[ks][j]);
         }
         // dP^T = V dO^T, with P^T = exp2(S^T c - lse) of one (ks, j) tile per step
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            const int ds = f / 2, ks = f % 2, n = f + 1;
-            fr[n & 1] = n < 8 ? frag_row(Vb, 16 * (n % 2) + c16, 32 * (n / 2) + 8 * g)
-                              : frag_t(Kb, 0, 0, g, c16);
+            const int ds = f / 2, ks = f % 2, n = 8 + f;
+            fr[(n + PD) % RING] = ldslot(n + PD);
 #pragma unroll
-            for (int j = 0; j < QSUB; ++j) dpt[ks][j] = mfma16x16x32(fr[f & 1], orr[j][ds], dpt[ks][j]);
+            for (int j = 0; j < QSUB; ++j) dpt[ks][j] = mfma16x16x32(fr[n % RING], orr[j][ds], dpt[ks][j]);
             // the KS * QSUB score tiles spread evenly over the 8 steps
             constexpr int EVERY = 8 / (KS * QSUB);
             static_assert(EVERY >= 1 && EVERY * KS * QSUB == 8, "exp schedule");
@@ -1679,9 +1690,10 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
         // dQ^T += K^T dS^T
 #pragma unroll
         for (int i = 0; i < DSUB; ++i) {
-            if (i + 1 < DSUB) fr[(i + 1) & 1] = frag_t(Kb, 16 * (i + 1), 0, g, c16);
+            const int n = 16 + i;
+            if (n + PD < 24) fr[(n + PD) % RING] = ldslot(n + PD);
 #pragma unroll
-            for (int j = 0; j < QSUB; ++j) acc[i][j] = mfma16x16x32(fr[i & 1], sb[j], acc[i][j]);
+            for (int j = 0; j < QSUB; ++j) acc[i][j] = mfma16x16x32(fr[n % RING], sb[j], acc[i][j]);
         }
     };
     for (int t0 = 0; t0 < ntl; t0 += NBUF) {
