@@ -46,8 +46,30 @@ VKH_DEV void ld8(float (&v)[8], const float *p) {
 // supplies A[fr][fg] = X[t0 + fr][c + 8 fg + m] and B[fg][fr] =
 // F(c + 8 fg + m, 16 j + fr) for m = 0..7: one 16-byte X load feeds eight
 // MFMAs per row tile.  FK: F(c, i) = f[i * fsi + c] (A's [r, K] layout;
-// 16-byte loads), else f[c * fsc + i] (B's [N, r] layout).
-constexpr int kRowsWaves = 8, kRowsRT = 2;
+// 16-byte loads), else f[c * fsc + i] (B's [N, r] layout).  Each wave keeps
+// kStages column groups of loads in flight (a register ring).
+constexpr int kRowsWaves = 8, kRowsRT = 2, kStages = 4;
+
+// raw 16-byte X load (converted at use)
+template <typename TX> struct Raw16;
+template <> struct Raw16<bf16> {
+    bf16x8 v;
+    VKH_DEV void ld(const bf16 *p) { v = *reinterpret_cast<const bf16x8 *>(p); }
+    VKH_DEV void zero() { v = bf16x8{}; }
+    VKH_DEV float operator[](int e) const { return (float)v[e]; }
+};
+template <> struct Raw16<float> {
+    float4 a, b;
+    VKH_DEV void ld(const float *p) {
+        a = *reinterpret_cast<const float4 *>(p);
+        b = *reinterpret_cast<const float4 *>(p + 4);
+    }
+    VKH_DEV void zero() { a = b = make_float4(0.f, 0.f, 0.f, 0.f); }
+    VKH_DEV float operator[](int e) const {  // e is a compile-time index at every use
+        return e == 0 ? a.x : e == 1 ? a.y : e == 2 ? a.z : e == 3 ? a.w
+             : e == 4 ? b.x : e == 5 ? b.y : e == 6 ? b.z : b.w;
+    }
+};
 
 template <typename TX, int NR, bool FK>
 __global__ __launch_bounds__(kRowsWaves * 64) void lora_rows_k(const TX *__restrict__ x, long ldx,
@@ -83,50 +105,48 @@ __global__ __launch_bounds__(kRowsWaves * 64) void lora_rows_k(const TX *__restr
 #pragma unroll
         for (int j = 0; j < NR; ++j) acc[a][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    auto load = [&](int g, float (&xv)[kRowsRT][8], float (&fv)[NR][8]) {
+    struct Stage {
+        Raw16<TX> x[kRowsRT];
+        float f[NR][8];
+    };
+    auto load = [&](int g, Stage &st) {
         const int c = 32 * g;
 #pragma unroll
         for (int a = 0; a < kRowsRT; ++a) {
-            if (rok[a]) ld8(xv[a], xr[a] + c);
-            else
-#pragma unroll
-                for (int e = 0; e < 8; ++e) xv[a][e] = 0.f;
+            if (rok[a]) st.x[a].ld(xr[a] + c);
+            else st.x[a].zero();
         }
 #pragma unroll
         for (int j = 0; j < NR; ++j) {
             if (!iok[j]) {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) fv[j][e] = 0.f;
+                for (int e = 0; e < 8; ++e) st.f[j][e] = 0.f;
             } else if constexpr (FK) {
-                ld8(fv[j], fp[j] + c);
+                ld8(st.f[j], fp[j] + c);
             } else {
 #pragma unroll
-                for (int e = 0; e < 8; ++e) fv[j][e] = fp[j][(long)(c + e) * s.fsc];
+                for (int e = 0; e < 8; ++e) st.f[j][e] = fp[j][(long)(c + e) * s.fsc];
             }
         }
     };
-    if (g0 < g1) {
-        float xv[kRowsRT][8], fv[NR][8];
-        load(g0, xv, fv);
-        for (int g = g0; g < g1; ++g) {
-            float xn[kRowsRT][8], fn[NR][8];
-            if (g + 1 < g1) load(g + 1, xn, fn);
+    // ring of kStages: group g + kStages - 1 is requested before group g computes
+    Stage st[kStages];
+#pragma unroll
+    for (int k = 0; k < kStages - 1; ++k)
+        if (g0 + k < g1) load(g0 + k, st[k]);
+    for (int g = g0; g < g1; g += kStages) {
+#pragma unroll
+        for (int k = 0; k < kStages; ++k) {
+            const int gg = g + k;
+            if (gg >= g1) break;
+            if (gg + kStages - 1 < g1) load(gg + kStages - 1, st[(k + kStages - 1) % kStages]);
 #pragma unroll
             for (int m = 0; m < 8; ++m)
 #pragma unroll
                 for (int a = 0; a < kRowsRT; ++a)
 #pragma unroll
-                    for (int j = 0; j < NR; ++j) acc[a][j] = mfma16x16x4(xv[a][m], fv[j][m], acc[a][j]);
-            if (g + 1 < g1) {
-#pragma unroll
-                for (int a = 0; a < kRowsRT; ++a)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) xv[a][e] = xn[a][e];
-#pragma unroll
-                for (int j = 0; j < NR; ++j)
-#pragma unroll
-                    for (int e = 0; e < 8; ++e) fv[j][e] = fn[j][e];
-            }
+                    for (int j = 0; j < NR; ++j)
+                        acc[a][j] = mfma16x16x4(st[k].x[a][m], st[k].f[j][m], acc[a][j]);
         }
     }
 #pragma unroll
@@ -167,8 +187,6 @@ template <typename TX, int NR>
 __global__ __launch_bounds__(512) void lora_cols_k(const TX *__restrict__ x, long ldx, int T,
                                                   int r, LoraSegs sg, float alpha) {
     constexpr int US = cols_us<NR>();
-    constexpr int XV = 16 / sizeof(TX);                    // X values per 16-byte load
-    constexpr int XL = kColsRows * kColsCW / XV / 256;     // X loads per thread per chunk
     constexpr int UL = (kColsRows * 16 * NR / 4 + 255) / 256;  // U float4 loads per thread
     __shared__ float xs[2][kColsRows][kXS];
     __shared__ float us[2][kColsRows][US];
@@ -183,61 +201,69 @@ __global__ __launch_bounds__(512) void lora_cols_k(const TX *__restrict__ x, lon
     const int nch = (half + kColsRows - 1) / kColsRows;  // same count for both halves
 
     const TX *xb = x + s.col + c0;
-    float xr[XL][XV];
-    float4 ur[UL];
-    auto load = [&](int ch) {
+    // a chunk's loads, raw (converted when stored to LDS); kStages chunks in
+    // flight per thread (a register ring)
+    constexpr int XE = 8;  // X values per ring entry (bf16: one 16-byte load, fp32: two)
+    constexpr int XN = kColsRows * kColsCW / XE / 256;  // entries per thread per chunk
+    struct Stage {
+        Raw16<TX> x[XN];
+        float4 u[UL];
+    };
+    auto load = [&](int ch, Stage &st) {
         const int r0 = tb + ch * kColsRows;
 #pragma unroll
-        for (int k = 0; k < XL; ++k) {
-            const int e = (ht + 256 * k) * XV, row = e / kColsCW, col = e % kColsCW;
+        for (int k = 0; k < XN; ++k) {
+            const int e = (ht + 256 * k) * XE, row = e / kColsCW, col = e % kColsCW;
             const int t = r0 + row;
-            if (t < te) {
-                if constexpr (XV == 8) ld8(xr[k], xb + (long)t * ldx + col);
-                else {
-                    const float4 v = *reinterpret_cast<const float4 *>(xb + (long)t * ldx + col);
-                    xr[k][0] = v.x; xr[k][1] = v.y; xr[k][2] = v.z; xr[k][3] = v.w;
-                }
-            } else {
-#pragma unroll
-                for (int v = 0; v < XV; ++v) xr[k][v] = 0.f;
-            }
+            if (t < te) st.x[k].ld(xb + (long)t * ldx + col);
+            else st.x[k].zero();
         }
 #pragma unroll
         for (int k = 0; k < UL; ++k) {
             const int e = (ht + 256 * k) * 4, row = e / (16 * NR), col = e % (16 * NR);
             const int t = r0 + row;
-            ur[k] = float4{0.f, 0.f, 0.f, 0.f};
+            st.u[k] = float4{0.f, 0.f, 0.f, 0.f};
             if (row < kColsRows && t < te && col < r)
-                ur[k] = *reinterpret_cast<const float4 *>(s.u + (long)t * s.ldu + col);
+                st.u[k] = *reinterpret_cast<const float4 *>(s.u + (long)t * s.ldu + col);
         }
     };
-    auto store = [&]() {
+    auto store = [&](const Stage &st) {
 #pragma unroll
-        for (int k = 0; k < XL; ++k) {
-            const int e = (ht + 256 * k) * XV, row = e / kColsCW, col = e % kColsCW;
-#pragma unroll
-            for (int v = 0; v < XV; ++v) xs[h][row][col + v] = xr[k][v];
+        for (int k = 0; k < XN; ++k) {
+            const int e = (ht + 256 * k) * XE, row = e / kColsCW, col = e % kColsCW;
+            float4 *d = reinterpret_cast<float4 *>(&xs[h][row][col]);
+            d[0] = make_float4(st.x[k][0], st.x[k][1], st.x[k][2], st.x[k][3]);
+            d[1] = make_float4(st.x[k][4], st.x[k][5], st.x[k][6], st.x[k][7]);
         }
 #pragma unroll
         for (int k = 0; k < UL; ++k) {
             const int e = (ht + 256 * k) * 4, row = e / (16 * NR), col = e % (16 * NR);
-            if (row < kColsRows) *reinterpret_cast<float4 *>(&us[h][row][col]) = ur[k];
+            if (row < kColsRows) *reinterpret_cast<float4 *>(&us[h][row][col]) = st.u[k];
         }
     };
     f32x4 acc[NR];
 #pragma unroll
     for (int j = 0; j < NR; ++j) acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    load(0);
-    for (int ch = 0; ch < nch; ++ch) {
-        __syncthreads();  // the previous chunk's reads are done
-        store();
-        __syncthreads();
-        if (ch + 1 < nch) load(ch + 1);
+    Stage st[kStages];
 #pragma unroll
-        for (int k = 0; k < kColsRows / 4; ++k) {
-            const float a = xs[h][4 * k + fg][16 * q + fr];
+    for (int k = 0; k < kStages - 1; ++k)
+        if (k < nch) load(k, st[k]);
+    // nch is the same for every thread: the barriers below are uniform
+    for (int ch0 = 0; ch0 < nch; ch0 += kStages) {
 #pragma unroll
-            for (int j = 0; j < NR; ++j) acc[j] = mfma16x16x4(a, us[h][4 * k + fg][16 * j + fr], acc[j]);
+        for (int k = 0; k < kStages; ++k) {
+            const int ch = ch0 + k;
+            if (ch >= nch) break;
+            __syncthreads();  // the previous chunk's reads are done
+            store(st[k]);
+            __syncthreads();
+            if (ch + kStages - 1 < nch) load(ch + kStages - 1, st[(k + kStages - 1) % kStages]);
+#pragma unroll
+            for (int kk = 0; kk < kColsRows / 4; ++kk) {
+                const float a = xs[h][4 * kk + fg][16 * q + fr];
+#pragma unroll
+                for (int j = 0; j < NR; ++j) acc[j] = mfma16x16x4(a, us[h][4 * kk + fg][16 * j + fr], acc[j]);
+            }
         }
     }
     __syncthreads();
@@ -262,18 +288,29 @@ __global__ __launch_bounds__(512) void lora_cols_k(const TX *__restrict__ x, lon
 }
 
 // ── lora_update ─────────────────────────────────────────────────────────
-// Thread = 4 rows x 4 consecutive columns of Y (float4 in and out); block =
-// 256 threads = 4 rows x 1024 columns, so U[t][i] is uniform over the block.
-// Adapters whose column range holds the thread's columns add their rank-r
-// product (FK: F(c, i) = f[i * fsi + c], one float4 per i; else
+// Block = kUpdRows rows x 1024 columns of Y; thread = those rows x 4
+// consecutive columns (float4 in and out).  The adapters' U rows of the block
+// go through LDS once (read back as broadcasts); each thread loads its
+// columns' factor values once per 4 rank indices and applies them to all
+// kUpdRows rows.  Adapters whose column range holds the thread's columns add
+// their rank-r product (FK: F(c, i) = f[i * fsi + c], one float4 per i; else
 // f[c * fsc + i], one float4 per column and four i).
-constexpr int kUpdCols = 1024, kUpdRows = 4;
+constexpr int kUpdCols = 1024, kUpdRows = 16;
 
 template <bool FK>
 __global__ __launch_bounds__(256) void lora_update_k(float *__restrict__ y, long ldy, int T, int r,
                                                      LoraSegs sg, float alpha) {
+    __shared__ float4 ush[3][kUpdRows][16];  // U rows t0.. of each adapter (r <= 64)
     const int c = blockIdx.x * kUpdCols + threadIdx.x * 4;
     const int t0 = blockIdx.y * kUpdRows;
+    for (int e = threadIdx.x; e < sg.n * kUpdRows * 16; e += 256) {
+        const int si = e / (kUpdRows * 16), row = (e / 16) % kUpdRows, q4 = e % 16;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t0 + row < T && 4 * q4 < r)
+            v = *reinterpret_cast<const float4 *>(sg.s[si].u + (long)(t0 + row) * sg.s[si].ldu + 4 * q4);
+        ush[si][row][q4] = v;
+    }
+    __syncthreads();
     float acc[kUpdRows][4] = {};
     bool any = false;
     for (int si = 0; si < sg.n; ++si) {
@@ -281,30 +318,33 @@ __global__ __launch_bounds__(256) void lora_update_k(float *__restrict__ y, long
         if (c < s.col || c >= s.col + s.ncols) continue;
         any = true;
         const long cc = c - s.col;
-        const float *u = s.u + (long)t0 * s.ldu;
-        if constexpr (FK) {
-            for (int i = 0; i < r; ++i) {
-                const float4 f = *reinterpret_cast<const float4 *>(s.f + (long)i * s.fsi + cc);
-#pragma unroll
-                for (int a = 0; a < kUpdRows; ++a) {
-                    const float ua = t0 + a < T ? u[(long)a * s.ldu + i] : 0.f;
-                    acc[a][0] += ua * f.x; acc[a][1] += ua * f.y;
-                    acc[a][2] += ua * f.z; acc[a][3] += ua * f.w;
-                }
-            }
-        } else {
-            for (int i = 0; i < r; i += 4) {
-                float4 f[4];
+        for (int i = 0; i < r; i += 4) {
+            // f4[e] = F(cc + 0..3, i + e) as a float4 over the 4 columns
+            float4 f4[4];
+            if constexpr (FK) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e)
-                    f[e] = *reinterpret_cast<const float4 *>(s.f + (cc + e) * s.fsc + i);
+                    f4[e] = *reinterpret_cast<const float4 *>(s.f + (long)(i + e) * s.fsi + cc);
+            } else {
+                float4 fc[4];  // fc[col] = F(cc + col, i .. i + 3)
 #pragma unroll
-                for (int a = 0; a < kUpdRows; ++a) {
-                    if (t0 + a >= T) continue;
-                    const float4 ua = *reinterpret_cast<const float4 *>(u + (long)a * s.ldu + i);
+                for (int col = 0; col < 4; ++col)
+                    fc[col] = *reinterpret_cast<const float4 *>(s.f + (cc + col) * s.fsc + i);
+                f4[0] = make_float4(fc[0].x, fc[1].x, fc[2].x, fc[3].x);
+                f4[1] = make_float4(fc[0].y, fc[1].y, fc[2].y, fc[3].y);
+                f4[2] = make_float4(fc[0].z, fc[1].z, fc[2].z, fc[3].z);
+                f4[3] = make_float4(fc[0].w, fc[1].w, fc[2].w, fc[3].w);
+            }
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        acc[a][e] += ua.x * f[e].x + ua.y * f[e].y + ua.z * f[e].z + ua.w * f[e].w;
+            for (int a = 0; a < kUpdRows; ++a) {
+                const float4 u = ush[si][a][i / 4];
+                const float uu[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[a][0] += uu[e] * f4[e].x;
+                    acc[a][1] += uu[e] * f4[e].y;
+                    acc[a][2] += uu[e] * f4[e].z;
+                    acc[a][3] += uu[e] * f4[e].w;
                 }
             }
         }
