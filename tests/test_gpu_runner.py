@@ -169,7 +169,9 @@ LORA_QV = dict(lora_targets=0x5 | 0x40, lora_rank=8, lora_alpha=16.0)
     (0, {}), (1, {}), (1, dict(tied_embeddings=1, n_seqs=2, n_pos=64)), (0, LORA_QV),
     (1, LORA_QV),
     (1, dict(head_dim=128, n_heads=16, n_kv_heads=8, rotary_dim=128, n_seqs=16, n_pos=128,
-             ff_dim=512, vocab_size=1024, n_layers=4))])
+             ff_dim=512, vocab_size=1024, n_layers=4)),
+    (1, dict(head_dim=128, n_heads=16, n_kv_heads=8, rotary_dim=128, n_seqs=16, n_pos=128,
+             ff_dim=512, vocab_size=1024, n_layers=4, **LORA_QV))])
 def test_activation_recompute_bit_identical(precision, over):
     import valkyr_amd as v
     from valkyr_amd.runner import ADAM_M, ADAM_V, GRAD, PARAM
@@ -268,7 +270,10 @@ def test_step_bf16_vs_pure_fp32_oracle():
 @pytest.mark.parametrize("precision,over", [
     (0, dict(lora_targets=0xF)), (1, dict(lora_targets=0xF)),
     (1, dict(lora_targets=0x7F, n_layers=3)), (0, dict(lora_targets=0x55, lora_rank=8)),
-    (1, dict(HD128, lora_targets=0xF))])
+    (1, dict(HD128, lora_targets=0xF)),
+    # the recompute attention path at a grid that leaves CUs idle: dQ runs on
+    # a second stream beside dK/dV
+    (1, dict(RECOMPUTE, lora_targets=0xF))])
 def test_lora_step_parity(precision, over):
     """Config-4 shape class: LoRA r=16 on q/k/v/o (and every projection, and
     a rank-8 subset), B = 0 init, frozen base.  fp32: every adapter gradient

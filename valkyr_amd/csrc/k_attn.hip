@@ -2195,6 +2195,32 @@ bool fa_bw_v4_preferred(const AttnShape &s) {
     return fa_bw_v4_ok(s) && (long)s.n_batch * s.n_kv_heads * (s.n_kv / 128) >= 128;
 }
 
+// One of the two recompute kernels alone (D already in p.d): which = 0 the
+// dK/dV kernel, 1 the dQ kernel, so a caller can run them on two streams.
+hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipStream_t st) {
+    if (s.n_batch <= 0 || s.n_q <= 0) return hipSuccess;
+    if (p.dt != DType::BF16 || !fa_bw_v4_ok(s) || p.o16) return hipErrorInvalidValue;
+    if ((long)s.n_q * std::max(p.ldq, p.lddo) * 2 >= (1l << 31) ||
+        (long)s.n_kv * std::max(p.ldk, p.ldv) * 2 >= (1l << 31))
+        return hipErrorInvalidValue;
+    const QkEpi &e = p.qk;
+    if (e.out && (!fa_bw_qk_epi_ok(s, e.rot) || !e.x || e.ldout % 8 || e.ldx % 4 ||
+                  ((uintptr_t)e.out & 15) || ((uintptr_t)e.x & 15) || (e.rot && !e.rope) ||
+                  (bool)e.gq != (bool)e.gk || (e.gq && (!e.pq || !e.pk))))
+        return hipErrorInvalidValue;
+    constexpr int W = 8;
+    if (which == 0) {
+        const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
+        if (e.out) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, true>), gkv, dim3(W * 64), 0, st, s, p);
+        else hipLaunchKernelGGL((fa_bwd_dkv4_k<W, false>), gkv, dim3(W * 64), 0, st, s, p);
+    } else {
+        const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
+        if (e.out) hipLaunchKernelGGL((fa_bwd_dq4_k<W, false, true>), gq, dim3(W * 64), 0, st, s, p);
+        else hipLaunchKernelGGL((fa_bwd_dq4_k<W, false, false>), gq, dim3(W * 64), 0, st, s, p);
+    }
+    return hipGetLastError();
+}
+
 int fa_bw_v4_q_blocks(const AttnShape &s) {
     return s.n_heads * s.n_batch * ((s.n_q + dq4::BQ - 1) / dq4::BQ);
 }

@@ -245,6 +245,7 @@ bool fa_bw_v4_ok(const AttnShape &s);
 bool fa_bw_v4_preferred(const AttnShape &s);
 // Gain-partial rows the fused q/k epilogue writes (dQ kernel: q gains; dK/dV
 // kernel: k gains), and whether a shape / rotary_dim can take it.
+hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipStream_t st);
 int fa_bw_v4_q_blocks(const AttnShape &s);
 int fa_bw_v4_kv_blocks(const AttnShape &s);
 bool fa_bw_qk_epi_ok(const AttnShape &s, int rotary_dim);

@@ -93,6 +93,11 @@ struct vkh_runner {
     bool attn_fused = false;  // bf16 attention backward on fa_bw_fused
     bool attn_v4 = false;     // ... on its recompute kernels (no dS workspace)
     bool qk_fused = false;    // ... with RoPE^T / Q/K-norm backward in their epilogues
+    // ... with the dQ kernel on a second stream beside dK/dV (one stream
+    // otherwise: no side stream, and the dK/dV grid leaves CUs idle)
+    bool attn_fork = false;
+    hipStream_t aux = nullptr;
+    hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     GemmWs gws{nullptr, 0};
     // Concurrent weight gradients (bf16 full fine-tune): each layer's dW GEMMs
     // and its Adam update run on a second stream one layer behind the main
@@ -167,6 +172,10 @@ struct vkh_runner {
         if (ev_head) (void)hipEventDestroy(ev_head);
         if (ev_lm) (void)hipEventDestroy(ev_lm);
         if (side) (void)hipStreamDestroy(side);
+        if (aux) (void)hipStreamSynchronize(aux);
+        if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_join) (void)hipEventDestroy(ev_join);
+        if (aux) (void)hipStreamDestroy(aux);
         for (void *p : allocs) (void)hipFree(p);
         if (tok_h) (void)hipHostFree(tok_h);
         if (tgt_h) (void)hipHostFree(tgt_h);
@@ -389,6 +398,12 @@ struct vkh_runner {
             attn_fused = adt == DType::BF16 && fa_bw_fused_ok(attn_shape());
             attn_v4 = attn_fused && fa_bw_v4_preferred(attn_shape());
             qk_fused = attn_v4 && fa_bw_qk_epi_ok(attn_shape(), (int)cfg.rotary_dim);
+            attn_fork = attn_v4 && lora && fa_bw_v4_kv_blocks(attn_shape()) < 256;
+            if (attn_fork) {
+                VKH_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
+                VKH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+                VKH_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
+            }
             if (attn_fused && fa_bw_ws_bytes(attn_shape(), attn_v4))
                 VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape(), attn_v4) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
@@ -892,8 +907,9 @@ struct vkh_runner {
         // attention: D, dK/dV, dQ into the fused d_qkv buffer
         if (b16() && adt == DType::BF16) {
             if (!do_bf16) VKH_HIP(cast_f32_to_bf16(d_attn_out, dout16, (size_t)T * qd, cur));
-            // the recompute kernels form D themselves (from the bf16 O below)
-            if (!attn_v4) VKH_HIP(fa_bw_d_bf16(as, a.attn_b, qd, dout16, qd, fa_d, cur));
+            // the recompute kernels form D themselves (from the bf16 O below),
+            // unless dQ runs beside dK/dV
+            if (!attn_v4 || attn_fork) VKH_HIP(fa_bw_d_bf16(as, a.attn_b, qd, dout16, qd, fa_d, cur));
         } else {
             VKH_HIP(fa_bw_d(as, a.attn_out, qd, d_attn_out, qd, fa_d, dout16, qd, cur));
         }
@@ -910,10 +926,24 @@ struct vkh_runner {
         ap.dk = d_qkv + qd; ap.lddk = qkvd;
         ap.dv = d_qkv + qd + kvd; ap.lddv = qkvd;
         ap.dt = adt;
-        if (attn_v4) {
+        if (attn_v4 && !attn_fork) {
             ap.o16 = a.attn_b;
             ap.ldo16 = qd;
         }
+        // the recompute (or dS-GEMM) kernels; forked: dQ on the second stream
+        auto attn_bw = [&]() -> vkh_status {
+            if (attn_fork) {
+                VKH_HIP(hipEventRecord(ev_fork, cur));
+                VKH_HIP(hipStreamWaitEvent(aux, ev_fork, 0));
+                VKH_HIP(fa_bw_v4_part(as, ap, 1, aux));
+                VKH_HIP(fa_bw_v4_part(as, ap, 0, cur));
+                VKH_HIP(hipEventRecord(ev_join, aux));
+                VKH_HIP(hipStreamWaitEvent(cur, ev_join, 0));
+                return VKH_OK;
+            }
+            VKH_HIP(fa_bw_fused(as, ap, attn_ds, attn_v4, cur));
+            return VKH_OK;
+        };
         const bool qk_side = concurrent && cfg.qk_norm;
         float *qkp = qk_side ? lg[l].pqk : partial;
         if (qk_fused) {
@@ -929,7 +959,7 @@ struct vkh_runner {
             const int nq = fa_bw_v4_q_blocks(as);
             e.pq = qkp;
             e.pk = qkp + (size_t)nq * hd;
-            VKH_HIP(fa_bw_fused(as, ap, attn_ds, true, cur));
+            VKH_TRY(attn_bw());
             if (qk_side) {
                 lg[l].pq = e.pq; lg[l].pk = e.pk;
                 lg[l].q_parts = nq; lg[l].k_parts = fa_bw_v4_kv_blocks(as);
@@ -940,7 +970,7 @@ struct vkh_runner {
             }
         } else {
             if (attn_fused) {
-                VKH_HIP(fa_bw_fused(as, ap, attn_ds, attn_v4, cur));
+                VKH_TRY(attn_bw());
             } else {
                 VKH_HIP(fa_bw_dkv(as, ap, cur));
                 VKH_HIP(fa_bw_dq(as, ap, cur));
