@@ -98,6 +98,12 @@ struct vkh_runner {
     bool attn_fork = false;
     hipStream_t aux = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
+    // LoRA: each layer's adapter gradients dA, dB (lora_cols) run on `aux`
+    // too; what they read (the fused dy copies, dy B, the layer's inputs) is
+    // next overwritten within the layer below's backward, which starts by
+    // waiting for this layer's event (ev_laux[l]).
+    bool lora_aux = false;
+    std::vector<hipEvent_t> ev_laux;
     GemmWs gws{nullptr, 0};
     // Concurrent weight gradients (bf16 full fine-tune): each layer's dW GEMMs
     // and its Adam update run on a second stream one layer behind the main
@@ -175,6 +181,7 @@ struct vkh_runner {
         if (aux) (void)hipStreamSynchronize(aux);
         if (ev_fork) (void)hipEventDestroy(ev_fork);
         if (ev_join) (void)hipEventDestroy(ev_join);
+        for (hipEvent_t e : ev_laux) (void)hipEventDestroy(e);
         if (aux) (void)hipStreamDestroy(aux);
         for (void *p : allocs) (void)hipFree(p);
         if (tok_h) (void)hipHostFree(tok_h);
@@ -399,11 +406,6 @@ struct vkh_runner {
             attn_v4 = attn_fused && fa_bw_v4_preferred(attn_shape());
             qk_fused = attn_v4 && fa_bw_qk_epi_ok(attn_shape(), (int)cfg.rotary_dim);
             attn_fork = attn_v4 && lora && fa_bw_v4_kv_blocks(attn_shape()) < 256;
-            if (attn_fork) {
-                VKH_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
-                VKH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
-                VKH_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
-            }
             if (attn_fused && fa_bw_ws_bytes(attn_shape(), attn_v4))
                 VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape(), attn_v4) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
@@ -484,7 +486,18 @@ struct vkh_runner {
         char *ew = nullptr;
         VKH_TRY(alloc(ew, embed_bw_work_bytes(T)));
         embed_work = ew;
-        if (lora) VKH_TRY(alloc(dyB, (size_t)3 * T * R));  // dy B of up to three adapters
+        if (lora) VKH_TRY(alloc(dyB, (size_t)7 * T * R));  // dy B of each adapter
+        lora_aux = lora;
+        if (attn_fork || lora_aux) {
+            VKH_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
+            VKH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
+            VKH_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
+        }
+        if (lora_aux) {
+            ev_laux.assign(L, nullptr);
+            for (int l = 0; l < L; ++l)
+                VKH_HIP(hipEventCreateWithFlags(&ev_laux[l], hipEventDisableTiming));
+        }
         VKH_TRY(alloc(tok_d, T));
         VKH_TRY(alloc(tgt_d, T));
         if (cfg.rotary_dim > 0) {
@@ -833,7 +846,7 @@ struct vkh_runner {
             if (!proj_lora(p)) continue;
             int N, K;
             proj_shape(p, N, K);
-            float *db = dyB + (size_t)sb.n * T * R;
+            float *db = dyB + (size_t)p * T * R;
             float *dA = G + (ls[l].la[p].off - tb), *dB = G + (ls[l].lb[p].off - tb);
             sb.s[sb.n++] = LoraSeg{proj_col(p), N, W(ls[l].lb[p]), (long)R, 1, db, (long)R};
             sa.s[sa.n++] = LoraSeg{0, K, W(ls[l].la[p]), 1, (long)K, db, (long)R};
@@ -845,9 +858,16 @@ struct vkh_runner {
         if (lora_fast_ok(dy.dt, dy.p, dy.ld, R, sb) && lora_fast_ok(x.dt, x.p, x.ld, R, sda) &&
             lora_fast_ok(dy.dt, dy.p, dy.ld, R, sdb) && (!dxo || lora_update_ok(dxo, lddx, R, sa))) {
             VKH_HIP(lora_rows(dy.dt, dy.p, dy.ld, T, R, sb, 1.f, cur));
+            // dA, dB beside the rest of the backward (ordering: ev_laux)
+            hipStream_t cs = cur;
+            if (lora_aux) {
+                VKH_HIP(hipEventRecord(ev_fork, cur));
+                VKH_HIP(hipStreamWaitEvent(aux, ev_fork, 0));
+                cs = aux;
+            }
+            VKH_HIP(lora_cols(x.dt, x.p, x.ld, T, R, sda, aor, cs));
+            VKH_HIP(lora_cols(dy.dt, dy.p, dy.ld, T, R, sdb, aor, cs));
             if (dxo) VKH_HIP(lora_update(dxo, lddx, T, R, sa, aor, cur));
-            VKH_HIP(lora_cols(x.dt, x.p, x.ld, T, R, sda, aor, cur));
-            VKH_HIP(lora_cols(dy.dt, dy.p, dy.ld, T, R, sdb, aor, cur));
             return VKH_OK;
         }
         for (int p : ps)
@@ -858,6 +878,12 @@ struct vkh_runner {
     // dy / dyb: the residual-stream gradient (fp32) and its bf16 copy; the
     // layer input gradient goes to dxo / dxob.
     vkh_status layer_backward(int l, const float *dy, const bf16 *dyb, float *dxo, bf16 *dxob) {
+        if (lora_aux && l + 1 < L) VKH_HIP(hipStreamWaitEvent(cur, ev_laux[l + 1], 0));
+        VKH_TRY(layer_backward_body(l, dy, dyb, dxo, dxob));
+        if (lora_aux) VKH_HIP(hipEventRecord(ev_laux[l], aux));
+        return VKH_OK;
+    }
+    vkh_status layer_backward_body(int l, const float *dy, const bf16 *dyb, float *dxo, bf16 *dxob) {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const float *x_in = l == 0 ? x_emb : acts[l - 1].y;
@@ -1051,6 +1077,8 @@ struct vkh_runner {
             }
             c ^= 1;
         }
+        // the adapters' last gradients before Adam and the next forward
+        if (lora_aux) VKH_HIP(hipStreamWaitEvent(cur, ev_laux[0], 0));
         if (!lora) {
             float *dE = Gd(embed);
             if (concurrent) VKH_HIP(hipStreamWaitEvent(cur, ev_lm, 0));
