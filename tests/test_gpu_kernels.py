@@ -34,7 +34,10 @@ def _gpu():
 def test_rmsnorm_forward_backward_fused_dw():
     from valkyr_amd import kernels as K
 
-    for rows, dim in ((128, 256), (2048, 1024), (300, 128), (7, 96)):
+    # the wide rows (> 2048: a block per row) at the Qwen3-4B / -8B widths, a
+    # ragged last 1024-column chunk, and more rows than the grid's blocks
+    for rows, dim in ((128, 256), (2048, 1024), (300, 128), (7, 96), (64, 2560), (1100, 4096),
+                      (9, 3000)):
         note(f"rmsnorm rows={rows} dim={dim}")
         x = O.normal(rows * dim, 1)
         w = O.uniform(dim, 2, 0.5, 1.5)
@@ -190,6 +193,38 @@ def test_linear_gemms(prec, shape):
     assert rel_l2(y_ref, host(by)) < tol
     assert rel_l2(dx_ref, host(bdx)) < tol
     assert rel_l2(dW_ref, host(bdW)) < tol
+
+
+def test_bf16_gemms_over_2gib_operand():
+    """The head's dz at 8192 tokens x 151936 vocabulary (2.49 GB of bf16) is
+    past the DMA path's 2 GiB views: dW = dz^T x runs in row chunks that
+    accumulate, dx = dz W in independent row chunks.  Sampled output rows
+    against float64 products of the same bf16 values."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import bf16_bits_to_f32
+
+    M, V, D = 8192, 151936, 64
+    rng = np.random.default_rng(17)
+    note(f"bf16 GEMMs with a [{M}, {V}] operand")
+    dz_bits = (rng.integers(0, 1 << 15, (M, V), dtype=np.uint16) & np.uint16(0x3FFF)) | \
+        np.uint16(0x3C00)  # |values| in [2^-7, 2^0): no overflow, no denormals
+    dz_bits ^= (rng.integers(0, 2, (M, V), dtype=np.uint16) << np.uint16(15))
+    x_bits = O.to_bf16_bits(O.normal(M * D, 18).reshape(M, D))
+    w_bits = O.to_bf16_bits(O.normal(V * D, 19, 0.05).reshape(V, D))
+    bdz, bx, bw = dev(dz_bits), dev(x_bits), dev(w_bits)
+    bdw, bdx = zeros(V * D), zeros(M * D)
+    K.linear_backward_dw_bf16(bdz, bx, bdw, M, V, D)
+    K.linear_backward_dx_bf16(bdz, bw, bdx, M, V, D)
+    dw = host(bdw, V * D).reshape(V, D)
+    dx = host(bdx, M * D).reshape(M, D)
+    xf = bf16_bits_to_f32(x_bits).astype(np.float64)
+    wf = bf16_bits_to_f32(w_bits).astype(np.float64)
+    for v in rng.integers(0, V, 12):
+        ref = bf16_bits_to_f32(dz_bits[:, v]).astype(np.float64) @ xf
+        assert rel_l2(ref, dw[v]) < 1e-5, v
+    for m in list(rng.integers(0, M, 10)) + [M // 2 - 1, M // 2, M - 1]:
+        ref = bf16_bits_to_f32(dz_bits[m]).astype(np.float64) @ wf
+        assert rel_l2(ref, dx[m]) < 1e-5, m
 
 
 def test_gemm_bf16_rounding_within_north_star_tolerance():

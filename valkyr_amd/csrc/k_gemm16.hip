@@ -103,6 +103,15 @@ bool make_op(const bf16 *p, long ld, long rows, long run, Op16 &o) {
 
 Mat matb(const bf16 *p, long ld) { return Mat{p, ld, DType::BF16}; }
 
+// Rows per chunk when a [rows, ld] bf16 operand view reaches 2 GiB (the DMA
+// path's 32-bit offsets): 0 if it fits whole, else a multiple of 64 rows.
+int rows_per_2g_chunk(long rows, long ld, long run) {
+    if (((rows - 1) * ld + run) * 2 < (1l << 31)) return 0;
+    const long fit = ((1l << 31) - 1) / (2 * ld);  // rows whose view fits
+    const long n = (rows + fit - 1) / fit;           // chunks
+    return (int)(((rows + n - 1) / n + 63) / 64 * 64);
+}
+
 }  // namespace
 
 hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
@@ -118,6 +127,15 @@ hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, lo
 
 hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
+    // an over-2 GiB dy (the head's dz at 8192 tokens): independent row chunks
+    if (const int mc = M > 64 ? rows_per_2g_chunk(M, lddy, N) : 0) {
+        for (int m0 = 0; m0 < M; m0 += mc) {
+            const hipError_t e = g16_nn(dy + (long)m0 * lddy, lddy, w, ldw, dx + (long)m0 * lddx,
+                                        lddx, std::min(mc, M - m0), N, K, alpha, beta, ws, st);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     // C[m, k'] = sum_n dy[m, n] W[n, k']: A = dy (K-major over n), B(k', n) = W[n][k'] (MN)
     Op16 a, b;
     if (!make_op(dy, lddy, M, N, a) || !make_op(w, ldw, N, K, b))
@@ -137,6 +155,17 @@ hipError_t g16_nn_bf16(const bf16 *dy, long lddy, const bf16 *w, long ldw, bf16 
 
 hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw, long lddw, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
+    // an over-2 GiB dy (the head's dz at 8192 tokens): the contraction over m in
+    // row chunks, each chunk after the first accumulating (beta = 1)
+    const int ca = M > 64 ? rows_per_2g_chunk(M, lddy, N) : 0, cb = M > 64 ? rows_per_2g_chunk(M, ldx, K) : 0;
+    if (const int mc = (ca && cb) ? std::min(ca, cb) : std::max(ca, cb)) {
+        for (int m0 = 0; m0 < M; m0 += mc) {
+            const hipError_t e = g16_tn(dy + (long)m0 * lddy, lddy, x + (long)m0 * ldx, ldx, dw, lddw,
+                                        std::min(mc, M - m0), N, K, alpha, m0 ? 1.f : beta, ws, st);
+            if (e != hipSuccess) return e;
+        }
+        return hipSuccess;
+    }
     // C[n, k'] = sum_m dy[m, n] x[m, k']: both operands MN-major over m
     Op16 a, b;
     if (!make_op(dy, lddy, M, N, a) || !make_op(x, ldx, M, K, b))

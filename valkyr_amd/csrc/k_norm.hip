@@ -199,6 +199,97 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
     for (int c = threadIdx.x; c < dim; c += NT) partial[(long)blockIdx.x * dim + c] = red[c];
 }
 
+// Wide rows (dim > 2048): one row per block iteration instead of one per
+// wave, so a thread holds 4 columns per 1024 (C4B <= 4 float4 of x, dy,
+// residual, gain and gain-gradient sum) rather than 16 float4 of each, which
+// left one wave per SIMD and spilled.  The row sums (fp64) are combined over
+// the block's four waves in a fixed order through LDS (double-buffered by row
+// parity, one barrier per row); each thread's columns' gain sums are its own,
+// so the block's partial row needs no reduction.  Same grid as rmsnorm_bwd_k
+// (the partial-row count the consumers use).
+template <int C4B>
+__global__ __launch_bounds__(NT) void rmsnorm_bwd_row_k(const float *dy, const float *x,
+                                                         const float *w, float *dx, bf16 *dxb,
+                                                         const float *res, float *partial,
+                                                         int rows, int dim, float eps, int gq) {
+    __shared__ double sred[2][2][NW];
+    const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
+    float4 gain[C4B], dwa[C4B];
+#pragma unroll
+    for (int j = 0; j < C4B; ++j) {
+        const int c = 4 * threadIdx.x + 1024 * j;
+        gain[j] = c < dim ? *reinterpret_cast<const float4 *>(w + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (gq) gain[j] = make_float4(gain[j].x + 1.0f, gain[j].y + 1.0f, gain[j].z + 1.0f, gain[j].w + 1.0f);
+        dwa[j] = make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    const float ri3_div = (float)dim;
+    int par = 0;
+    for (int row = blockIdx.x; row < rows; row += gridDim.x, par ^= 1) {
+        const long ro = (long)row * dim;
+        float4 xv[C4B], dv[C4B], rv[C4B];
+        double ss = 0, A = 0;
+#pragma unroll
+        for (int j = 0; j < C4B; ++j) {
+            const int c = 4 * threadIdx.x + 1024 * j;
+            const bool ok = c < dim;
+            xv[j] = ok ? *reinterpret_cast<const float4 *>(x + ro + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            dv[j] = ok ? *reinterpret_cast<const float4 *>(dy + ro + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+            rv[j] = (ok && res) ? *reinterpret_cast<const float4 *>(res + ro + c) : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+#pragma unroll
+        for (int j = 0; j < C4B; ++j) {
+            const float xs[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            const float ds[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+            const float gs[4] = {gain[j].x, gain[j].y, gain[j].z, gain[j].w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const double xd = xs[q];
+                ss += xd * xd;
+                A += (double)ds[q] * (double)gs[q] * xd;
+            }
+        }
+        ss = wave_sum_dpp(ss);
+        A = wave_sum_dpp(A);
+        if (lane == 0) {
+            sred[par][0][wave] = ss;
+            sred[par][1][wave] = A;
+        }
+        __syncthreads();
+        ss = ((sred[par][0][0] + sred[par][0][1]) + sred[par][0][2]) + sred[par][0][3];
+        A = ((sred[par][1][0] + sred[par][1][1]) + sred[par][1][2]) + sred[par][1][3];
+        const double m = ss / (double)dim;
+        const float ri = 1.0f / sqrtf((float)m + eps);
+        const float ri3_over_D = ri * ri * ri / ri3_div;
+        const float A_f = (float)A;
+#pragma unroll
+        for (int j = 0; j < C4B; ++j) {
+            const int c = 4 * threadIdx.x + 1024 * j;
+            if (c >= dim) continue;
+            const float xs[4] = {xv[j].x, xv[j].y, xv[j].z, xv[j].w};
+            const float ds[4] = {dv[j].x, dv[j].y, dv[j].z, dv[j].w};
+            const float gs[4] = {gain[j].x, gain[j].y, gain[j].z, gain[j].w};
+            float o[4], dw[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                o[q] = ri * gs[q] * ds[q] - ri3_over_D * xs[q] * A_f;
+                dw[q] = ds[q] * ri * xs[q];
+            }
+            if (res) {
+                const float4 r = rv[j];
+                o[0] = o[0] + r.x; o[1] = o[1] + r.y; o[2] = o[2] + r.z; o[3] = o[3] + r.w;
+            }
+            store4<float>(dx + ro + c, o[0], o[1], o[2], o[3]);
+            if (dxb) store4<bf16>(dxb + ro + c, o[0], o[1], o[2], o[3]);
+            dwa[j].x += dw[0]; dwa[j].y += dw[1]; dwa[j].z += dw[2]; dwa[j].w += dw[3];
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < C4B; ++j) {
+        const int c = 4 * threadIdx.x + 1024 * j;
+        if (c < dim) *reinterpret_cast<float4 *>(partial + (long)blockIdx.x * dim + c) = dwa[j];
+    }
+}
+
 // out[c] = sum_b partial[b * stride + c].  A block owns 16 columns; its 16
 // row groups each sum a strided subset of the partial rows with four
 // independent accumulators, then the groups are combined in LDS in a fixed
@@ -885,12 +976,19 @@ hipError_t rmsnorm_backward(const float *dy, const float *x, const float *w, flo
         ((uintptr_t)dxb & 7u) || !al16(residual))
         return hipErrorInvalidValue;
     const int grid = rms_grid(rows);
-    hipError_t e = by_c4(dim, [&](auto c4) {
-        constexpr int C4 = decltype(c4)::value;
-        hipLaunchKernelGGL((rmsnorm_bwd_k<C4>), dim3(grid), dim3(NT), 0, st, dy, x, w, dx, dxb,
+    hipError_t e;
+    if (dim > 2048) {  // wide rows: a block per row (dim <= 4096: 4 float4 per thread)
+        hipLaunchKernelGGL((rmsnorm_bwd_row_k<4>), dim3(grid), dim3(NT), 0, st, dy, x, w, dx, dxb,
                            residual, partial, rows, dim, eps, gemma_quirk);
-        return hipGetLastError();
-    });
+        e = hipGetLastError();
+    } else {
+        e = by_c4(dim, [&](auto c4) {
+            constexpr int C4 = decltype(c4)::value;
+            hipLaunchKernelGGL((rmsnorm_bwd_k<C4>), dim3(grid), dim3(NT), 0, st, dy, x, w, dx, dxb,
+                               residual, partial, rows, dim, eps, gemma_quirk);
+            return hipGetLastError();
+        });
+    }
     if (e != hipSuccess) return e;
     if (dw)
         hipLaunchKernelGGL(colsum_k, dim3(ceil_div(dim, CS_COLS)), dim3(CS_COLS * CS_GROUPS), 0, st,
