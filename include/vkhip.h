@@ -130,8 +130,10 @@ typedef struct vkh_config {
     uint32_t tied_embeddings;  /* lm_head aliases embed; grad = dE + dW_lm */
     uint32_t precision;        /* vkh_precision */
     uint32_t recompute;        /* 1: per-layer activation recompute -- each layer keeps only
-                                  its input, and its forward runs again just before its
-                                  backward (same kernels, so the same gradients bit for bit) */
+                                  its input and its attention output O and LSE; the rest of
+                                  its forward (projections, norms, SwiGLU) runs again just
+                                  before its backward (same kernels, so the same gradients
+                                  bit for bit) */
 } vkh_config;
 
 /* A borrowed host fp32 tensor (a Zig slice: pointer + element count). */

@@ -122,9 +122,10 @@ struct vkh_runner {
     };
     bool concurrent = false;
     // Per-layer activation recompute: each layer keeps its output y (the next
-    // layer's input); the other activations live in kActSets sets shared in
-    // turn (layer l in set l % kActSets), and a layer's forward runs again
-    // just before its backward when later layers have reused its set.  The
+    // layer's input) and its attention output O and LSE; the other activations
+    // live in kActSets sets shared in turn (layer l in set l % kActSets), and
+    // a layer's forward, attention aside, runs again just before its backward
+    // when later layers have reused its set.  The
     // side stream's gradient copies are shared the same way (kGradSets sets,
     // kDyRing for dy, which the layer above writes), and before layer l
     // writes any of them the main stream waits for the side stream to finish
@@ -361,9 +362,15 @@ struct vkh_runner {
         acts.assign(L, Acts{});
         for (int l = 0; l < L; ++l) {
             Acts &a = acts[l];
-            if (l >= n_sets) {  // recompute: set l % n_sets, own output
+            if (l >= n_sets) {
+                // recompute: set l % n_sets, own output y and own attention
+                // output O and LSE (the recompute reruns projections, norms and
+                // SwiGLU, not the attention)
                 a = acts[l % n_sets];
                 VKH_TRY(alloc(a.y, (size_t)T * D));
+                VKH_TRY(alloc(a.lse, (size_t)T * H));
+                if (b16()) VKH_TRY(alloc(a.attn_b, (size_t)T * qd));
+                if (!(b16() && adt == DType::BF16)) VKH_TRY(alloc(a.attn_out, (size_t)T * qd));
                 continue;
             }
             if (b16()) {
@@ -787,10 +794,13 @@ struct vkh_runner {
         const size_t es = adt == DType::BF16 ? 2 : 4;
         const char *qa = (const char *)a.qkv_attn;
         const bool ob = b16() && adt == DType::BF16;
-        VKH_HIP(fa_forward(as, qa, qkvd, qa + qd * es, qkvd, qa + (qd + kvd) * es, qkvd,
-                           ob ? nullptr : a.attn_out, qd, a.lse, adt, ob ? a.attn_b : nullptr, qd,
-                           cur));
-        if (b16() && !ob) VKH_HIP(cast_f32_to_bf16(a.attn_out, a.attn_b, (size_t)T * qd, cur));
+        // a recompute keeps the layer's O and LSE from the forward pass
+        if (need_y) {
+            VKH_HIP(fa_forward(as, qa, qkvd, qa + qd * es, qkvd, qa + (qd + kvd) * es, qkvd,
+                               ob ? nullptr : a.attn_out, qd, a.lse, adt, ob ? a.attn_b : nullptr, qd,
+                               cur));
+            if (b16() && !ob) VKH_HIP(cast_f32_to_bf16(a.attn_out, a.attn_b, (size_t)T * qd, cur));
+        }
         // mid = x_in + attn_out W_o^T (+ LoRA)
         const Mat att = m_attn(a);
         VKH_TRY(linear_fwd(att, s.t[4], a.mid, D, D, qd, x_in, D));
