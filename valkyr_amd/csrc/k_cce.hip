@@ -185,9 +185,10 @@ hipError_t logits16(const CceShape &s, const bf16 *h, const bf16 *w, const Epi &
     }
     const Op16 a{h, s.D, (unsigned)hb}, b{w, s.D, (unsigned)wb};
     const SplitK one{1, nullptr};
+    constexpr int g = tile_group_rows<Lay::K, Lay::K>();
     if ((long)ceil_div(s.N, 256) * ceil_div(s.V, 256) >= 256)
-        return launch_gemm16<Tile16<256, 256, 2, 4>, Lay::K, Lay::K>(a, b, sh, epi, one, st);
-    return launch_gemm16<Tile16<128, 256, 2, 4>, Lay::K, Lay::K>(a, b, sh, epi, one, st);
+        return launch_gemm16<Tile16<256, 256, 2, 4>, Lay::K, Lay::K>(a, b, sh, epi, one, g, st);
+    return launch_gemm16<Tile16<128, 256, 2, 4>, Lay::K, Lay::K>(a, b, sh, epi, one, g, st);
 }
 
 }  // namespace

@@ -38,6 +38,7 @@ enum class Pick { Big, T128, T128x64, T128w8, T128x64ks2 };
 struct Plan {
     Pick tile;
     int splits;
+    bool column_order = false;  // tiles in plain column order (no row groups)
 };
 
 size_t ws_for(const Plan &p, const GemmShape &s) {
@@ -64,8 +65,9 @@ Plan plan(const GemmShape &s, size_t ws_bytes) {
         p = Plan{Pick::Big, 3};
     else if (s.K >= 4096 && t128 >= 256)
         // Qwen3-4B o / down forward and q/k/v dx (N = 2560, K = 4096..9728):
-        // 128 x 128 on 8 waves, 50 / 113 / 79 us against 56 / 167 / 104 (128 x 64)
-        p = Plan{Pick::T128w8, 1};
+        // 128 x 128 on 8 waves, 50 / 113 / 79 us against 56 / 167 / 104 (128 x 64);
+        // in column order (the LoRA step: 66.7 against 68.1 ms with row groups)
+        p = Plan{Pick::T128w8, 1, true};
     else if (s.K >= 16384 && t128 < 256)
         p = Plan{Pick::T128, (int)std::min<long>(4, std::max<long>(1, 512 / t128))};
     else if (t64 < 384 && s.K >= 2048)
@@ -83,12 +85,13 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
                  hipStream_t st) {
     const Plan p = plan(s, ws.p ? ws.bytes : 0);
     const SplitK sk{p.splits, (f32x4 *)ws.p};
+    const int g = p.column_order ? 0 : tile_group_rows<LA, LB>();
     switch (p.tile) {
-    case Pick::Big: return launch_gemm16<TBig, LA, LB>(a, b, s, e, sk, st);
-    case Pick::T128: return launch_gemm16<T128, LA, LB>(a, b, s, e, sk, st);
-    case Pick::T128w8: return launch_gemm16<T128w8, LA, LB>(a, b, s, e, sk, st);
-    case Pick::T128x64ks2: return launch_gemm16_ks2<T128x64, LA, LB>(a, b, s, e, st);
-    default: return launch_gemm16<T128x64, LA, LB>(a, b, s, e, sk, st);
+    case Pick::Big: return launch_gemm16<TBig, LA, LB>(a, b, s, e, sk, g, st);
+    case Pick::T128: return launch_gemm16<T128, LA, LB>(a, b, s, e, sk, g, st);
+    case Pick::T128w8: return launch_gemm16<T128w8, LA, LB>(a, b, s, e, sk, g, st);
+    case Pick::T128x64ks2: return launch_gemm16_ks2<T128x64, LA, LB>(a, b, s, e, g, st);
+    default: return launch_gemm16<T128x64, LA, LB>(a, b, s, e, sk, g, st);
     }
 }
 
