@@ -177,6 +177,29 @@ struct TileCfg {
     static constexpr int BM = BM_, BN = BN_, BK = BK_;
 };
 
+// Output tile (bm, bn) of linear tile index t.  Tiles go in groups of `grp`
+// tile rows (0: all of them), column by column inside a group, so the blocks
+// that run at the same time on one XCD (consecutive t after the XCD
+// regrouping) cover a few rows x a few columns of tiles and share operand
+// panels in that XCD's L2, instead of one column of tiles that each bring
+// their own row panel.  Group height by operand layout, measured on the bf16
+// training step (T = 2048: 8 / 2 rows, 20.2 ms against 21.8 in plain column
+// order) and the 8192-token step (593 against 618 ms): 8 rows when the A
+// operand is K-major (forward, dx), 2 for the weight gradients (both
+// operands MN-major).
+template <Lay LA, Lay LB>
+constexpr int tile_group_rows() {
+    return LA == Lay::MN && LB == Lay::MN ? 2 : 8;
+}
+VKH_DEV void tile_rc(int t, int nbm, int nbn, int grp, int &bm, int &bn) {
+    if (grp <= 0 || grp > nbm) grp = nbm;
+    const int per = grp * nbn;
+    const int g = t / per, r = t - g * per;
+    const int gm = min(grp, nbm - g * grp);
+    bm = g * grp + r % gm;
+    bn = r / gm;
+}
+
 // Fragment coordinates handed to epilogues: accumulator acc[i][j][r] holds
 // C[row0 + 16 i + 4 (lane / 16) + r][col0 + 16 j + lane % 16].
 struct FragPos {
@@ -207,7 +230,8 @@ __global__ __launch_bounds__(256, 2) void gemm_kernel(GemmOperand a, GemmOperand
     const int nb = nbm * nbn;
     int bid = blockIdx.x;
     if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
-    const int bm = bid % nbm, bn = bid / nbm;
+    int bm, bn;
+    tile_rc(bid, nbm, nbn, tile_group_rows<LA, LB>(), bm, bn);
     const int m0 = bm * BM, n0 = bn * BN;
 
     TileLoader<TA, LA, BF16, BM, BK, NT> la;

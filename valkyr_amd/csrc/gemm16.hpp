@@ -193,29 +193,6 @@ VKH_DEV bf16x8 frag16(const char *tile, int row16, int ks, int lane) {
 
 VKH_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0), exp/lgkm untouched
 
-// Output tile (bm, bn) of linear tile index t.  Tiles go in groups of `grp`
-// tile rows (0: all of them), column by column inside a group, so the blocks
-// that run at the same time on one XCD (consecutive t after the XCD
-// regrouping) cover a few rows x a few columns of tiles and share operand
-// panels in that XCD's L2, instead of one column of tiles that each bring
-// their own row panel.
-// Group height by operand layout, measured on the training step (T = 2048:
-// 8 / 2 rows, 20.2 ms against 21.8 in plain column order) and the 8192-token
-// step (593 against 618 ms): 8 rows when the A operand is K-major (forward,
-// dx), 2 for the weight gradients (both operands MN-major).
-template <Lay LA, Lay LB>
-constexpr int tile_group_rows() {
-    return LA == Lay::MN && LB == Lay::MN ? 2 : 8;
-}
-VKH_DEV void tile_rc(int t, int nbm, int nbn, int grp, int &bm, int &bn) {
-    if (grp <= 0 || grp > nbm) grp = nbm;
-    const int per = grp * nbn;
-    const int g = t / per, r = t - g * per;
-    const int gm = min(grp, nbm - g * grp);
-    bm = g * grp + r % gm;
-    bn = r / gm;
-}
-
 // One block's BM x BN output tile over the K slabs [kbase, kbase + 64 nk):
 // acc (per wave, accumulator layout) += A(m0.., k) B(n0.., k).  `smem` must
 // hold Cfg::LDS bytes.  Shared by the GEMM kernels and the attention dQ kernel.
