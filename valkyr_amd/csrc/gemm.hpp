@@ -196,8 +196,10 @@ VKH_DEV void tile_rc(int t, int nbm, int nbn, int grp, int &bm, int &bn) {
     const int per = grp * nbn;
     const int g = t / per, r = t - g * per;
     const int gm = min(grp, nbm - g * grp);
-    bm = g * grp + r % gm;
-    bn = r / gm;
+    // wave-uniform: kept in scalar registers (the tile loops of the largest
+    // kernels have no vector register to spare)
+    bm = __builtin_amdgcn_readfirstlane(g * grp + r % gm);
+    bn = __builtin_amdgcn_readfirstlane(r / gm);
 }
 
 // Fragment coordinates handed to epilogues: accumulator acc[i][j][r] holds
