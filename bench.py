@@ -496,7 +496,8 @@ def bench_config(name, args):
                first_step_s=round(first_s, 2), loss=[round(loss0, 4), round(loss1, 4)],
                checks=checks)
     if c.get("recompute"):
-        out["activation_recompute"] = "per layer (each layer keeps its input; forward rerun " \
+        out["activation_recompute"] = "per layer (each layer keeps its input and its attention " \
+                                      "output O / LSE; projections, norms and SwiGLU rerun " \
                                       "before its backward; not counted in tflops)"
     print(f"[bench] {name}: {out['ms_per_step']} ms/step, {out['tokens_s']:,.0f} tok/s, "
           f"checks {checks}", file=sys.stderr, flush=True)
