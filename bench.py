@@ -21,11 +21,13 @@ thread (`single_thread`).
 
 usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--precision bf16|fp32]
                        [--no-cpu-baseline] [--no-configs] [--fa-reps R]
-                       [--only all|step|fa|mlp|bw|config4|config5] [--calib-copy]
+                       [--only all|step|fa|mlp|bw|gemms|config4|config5] [--calib-copy]
 
 `bandwidth_kernels` times the HBM-bound backward kernels alone through the C ABI at
 config-3 shapes (RMSNorm, SwiGLU, RoPE backward, Adam, embedding backward) against
 the 8 TB/s HBM peak.
+`--only gemms` times the twelve per-layer GEMMs of config 3 alone through the C ABI,
+with hipBLASLt (torch.mm) on the same shapes when torch is importable.
 `mlp_runner` times the tiny-MLP TrainingRunner (train/runner.zig): the
 reference's `--train-demo` loop and tickFrameTrain on batches.  `configs` runs
 the metric's Qwen3-4B LoRA (config 4) and Qwen3-8B long-context full fine-tune
@@ -300,6 +302,113 @@ def bench_bandwidth(args):
     ms = timed(lambda i: K.embedding_backward(dyb[0], ids, dE, T, D, V, stream=s), 1, 20)
     row("embedding_backward", ms, nb, f"{T} ids into [{V}, {D}], accumulate")
     return res
+
+
+# The twelve linear-layer GEMMs of one config-3 layer (T = 2048 tokens): name, kind
+# (nt: y = x W^T forward; dx: dx = dy W; dw: dW = dy^T x), M (tokens), N (outputs), K (inputs)
+LAYER_GEMMS = [("qkv fwd", "nt", 2048, 4096, 1024), ("o fwd", "nt", 2048, 1024, 2048),
+               ("gate/up fwd", "nt", 2048, 6144, 1024), ("down fwd", "nt", 2048, 1024, 3072),
+               ("down dx", "dx", 2048, 1024, 3072), ("gate/up dx", "dx", 2048, 6144, 1024),
+               ("o dx", "dx", 2048, 1024, 2048), ("qkv dx", "dx", 2048, 4096, 1024),
+               ("down dW", "dw", 2048, 1024, 3072), ("gate/up dW", "dw", 2048, 6144, 1024),
+               ("o dW", "dw", 2048, 1024, 2048), ("qkv dW", "dw", 2048, 4096, 1024)]
+
+
+def bench_gemms(args):
+    """The per-layer GEMMs of config 3 alone, through the C ABI (bf16 operands, fp32
+    out; the kernels the step launches, without the second stream sharing the chip),
+    HIP events on the launch stream around 50 calls after 10 warm-up calls.  With
+    --hipblaslt, hipBLASLt (torch.mm, bf16 operands and output) is timed on the same
+    shapes beside them as a library reference point (torch is not imported otherwise,
+    so counter runs of this leg see only the library's kernels)."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import DeviceBuffer, Event, Stream, f32_to_bf16_bits
+
+    rng = np.random.default_rng(5)
+    s = Stream()
+    reps = 50
+
+    def ev_time(call):
+        for _ in range(10):
+            call()
+        s.synchronize()
+        e0, e1 = Event(), Event()
+        e0.record(s)
+        for _ in range(reps):
+            call()
+        e1.record(s)
+        e1.synchronize()
+        return e0.elapsed_ms(e1) / reps
+
+    have_torch = False
+    if args.hipblaslt:
+        try:
+            import torch
+            have_torch = torch.cuda.is_available()
+            if not have_torch:
+                print("[bench] --hipblaslt: torch sees no GPU", file=sys.stderr, flush=True)
+        except Exception as e:
+            print(f"[bench] --hipblaslt: torch unavailable ({e})", file=sys.stderr, flush=True)
+
+    def torch_time(call):
+        for _ in range(10):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            call()
+        e1.record()
+        e1.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    def bf16_buf(n):
+        return DeviceBuffer.from_numpy(f32_to_bf16_bits(rng.standard_normal(n, np.float32)))
+
+    rows, tot, tot_lib = {}, 0.0, 0.0
+    for name, kind, M, N, Kd in LAYER_GEMMS:
+        flops = 2.0 * M * N * Kd
+        if kind == "nt":
+            a, b, y = bf16_buf(M * Kd), bf16_buf(N * Kd), DeviceBuffer(M * N * 4)
+            call = lambda: K.matmul_nt_bf16(a, b, y, M, N, Kd, stream=s)
+        elif kind == "dx":
+            a, b, y = bf16_buf(M * N), bf16_buf(N * Kd), DeviceBuffer(M * Kd * 4)
+            call = lambda: K.linear_backward_dx_bf16(a, b, y, M, N, Kd, stream=s)
+        else:
+            a, b, y = bf16_buf(M * N), bf16_buf(M * Kd), DeviceBuffer(N * Kd * 4)
+            call = lambda: K.linear_backward_dw_bf16(a, b, y, M, N, Kd, stream=s)
+        ms = ev_time(call)
+        tot += ms
+        row = {"M": M, "N": N, "K": Kd, "us": round(ms * 1e3, 1),
+               "TFLOP_s": round(flops / (ms * 1e-3) / 1e12, 1)}
+        if have_torch:
+            dev = torch.device("cuda")
+            g = torch.Generator(device=dev).manual_seed(5)
+            if kind == "nt":
+                ta = torch.randn(M, Kd, device=dev, generator=g).bfloat16()
+                tb = torch.randn(N, Kd, device=dev, generator=g).bfloat16().t()
+            elif kind == "dx":
+                ta = torch.randn(M, N, device=dev, generator=g).bfloat16()
+                tb = torch.randn(N, Kd, device=dev, generator=g).bfloat16()
+            else:
+                ta = torch.randn(M, N, device=dev, generator=g).bfloat16().t()
+                tb = torch.randn(M, Kd, device=dev, generator=g).bfloat16()
+            lms = torch_time(lambda: torch.mm(ta, tb))
+            tot_lib += lms
+            row["hipblaslt_us"] = round(lms * 1e3, 1)
+            del ta, tb
+        rows[name] = row
+        print(f"[bench] gemm {name}: {row}", file=sys.stderr, flush=True)
+        del a, b, y
+    out = {"shapes": rows, "layer_us": round(tot * 1e3, 1),
+           "layer_TFLOP_s": round(sum(2.0 * M * N * Kd for _, _, M, N, Kd in LAYER_GEMMS)
+                                  / (tot * 1e-3) / 1e12, 1)}
+    if have_torch:
+        out["hipblaslt_layer_us"] = round(tot_lib * 1e3, 1)
+    print(f"[bench] per-layer GEMMs alone: {out['layer_us']} us"
+          + (f" (hipBLASLt {out['hipblaslt_layer_us']} us)" if have_torch else ""),
+          file=sys.stderr, flush=True)
+    return out
 
 
 def calib_copy():
@@ -582,8 +691,10 @@ def main():
     ap.add_argument("--no-configs", action="store_true",
                     help="skip the full-size config 4 / config 5 steps")
     ap.add_argument("--only", default="all",
-                    choices=["all", "step", "fa", "mlp", "bw", "config4", "config5"],
+                    choices=["all", "step", "fa", "mlp", "bw", "gemms", "config4", "config5"],
                     help="run only the step or only the attention benchmark (profiling runs)")
+    ap.add_argument("--hipblaslt", action="store_true",
+                    help="--only gemms: also time hipBLASLt (torch.mm) on the same shapes")
     ap.add_argument("--calib-copy", action="store_true",
                     help="after the benchmarks, run a copy-type kernel of known size "
                          "(vkh_scale over 64 Mi floats: 256 MiB read + 256 MiB written, 3x) "
@@ -596,6 +707,11 @@ def main():
               file=sys.stderr)
         sys.exit(2)
 
+    if args.hipblaslt:
+        try:  # before the library loads: torch then sees the GPU
+            import torch  # noqa: F401
+        except Exception:
+            pass
     import valkyr_amd as v
 
     if v.device_count() < 1:
@@ -613,6 +729,9 @@ def main():
         return
     if args.only == "bw":
         print(json.dumps({"bandwidth": bench_bandwidth(args)}), flush=True)
+        return
+    if args.only == "gemms":
+        print(json.dumps({"layer_gemms": bench_gemms(args)}), flush=True)
         return
     if args.only in ("config4", "config5"):
         print(json.dumps({args.only: bench_config(args.only, args)}), flush=True)

@@ -45,35 +45,45 @@ struct EpiCceStats {
     template <int TM, int TN>
     VKH_DEV void apply(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s) const {
         static_assert(TN * 16 == WN, "wave slice width");
-        const int c16 = fp.lane % 16, g = fp.lane / 16;
         const int part = fp.col0 / WN;
         // the last tile's second slice can lie wholly past V: it owns no partial
         if (part >= w.nparts) return;
+        // slices wholly inside the vocabulary (all but the last) skip the
+        // per-column range checks
+        if (fp.col0 + WN <= V) rows<TM, TN, true>(acc, fp, s, part);
+        else rows<TM, TN, false>(acc, fp, s, part);
+    }
+
+    template <int TM, int TN, bool FULL>
+    VKH_DEV void rows(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s,
+                      int part) const {
+        const int c16 = fp.lane % 16, g = fp.lane / 16;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = fp.row0 + 16 * i + 4 * g + r;
                 const bool rok = row < s.M;
-                const uint32_t t = rok ? tgt[row] : 0xffffffffu;
+                // the target column relative to this lane's first column: the
+                // lane of fragment j holds it when tc == 16 j
+                const int tc = rok ? (int)tgt[row] - fp.col0 - c16 : -1;
                 float mx = -INFINITY, zs = 0.f;
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
-                    const int col = fp.col0 + 16 * j + c16;
-                    if (col < V) {
+                    if (FULL || fp.col0 + 16 * j + c16 < V) {
                         const float z = acc[i][j][r];
                         mx = fmaxf(mx, z);
                         zs += z;
-                        if ((uint32_t)col == t) w.zt[row] = z;
+                        if (tc == 16 * j) w.zt[row] = z;
                     }
                 }
                 mx = row16_max(mx);
+                const float mxl = mx * LOG2E;
                 float se = 0.f;
 #pragma unroll
-                for (int j = 0; j < TN; ++j) {
-                    const int col = fp.col0 + 16 * j + c16;
-                    if (col < V) se += exp2f((acc[i][j][r] - mx) * LOG2E);
-                }
+                for (int j = 0; j < TN; ++j)
+                    if (FULL || fp.col0 + 16 * j + c16 < V)
+                        se += __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], LOG2E, -mxl));
                 se = row16_sum(se);
                 zs = row16_sum(zs);
                 if (rok && c16 == 0) {
@@ -96,7 +106,16 @@ struct EpiCceDz {
 
     template <int TM, int TN>
     VKH_DEV void apply(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s) const {
+        if (fp.col0 + 16 * TN <= V) rows<TM, TN, true>(acc, fp, s);
+        else rows<TM, TN, false>(acc, fp, s);
+    }
+
+    // dz = (sf p - eps / V - [v == t] (1 - eps)) / N with p = exp(z - lse),
+    // sf = 1 + 2 lambda_z lse; the 1 / N folded into the coefficients
+    template <int TM, int TN, bool FULL>
+    VKH_DEV void rows(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s) const {
         const int c16 = fp.lane % 16, g = fp.lane / 16;
+        const float off = eps_over_v * inv_n, tsc = t_scale * inv_n;
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -104,16 +123,17 @@ struct EpiCceDz {
                 const int row = fp.row0 + 16 * i + 4 * g + r;
                 if (row >= s.M) continue;
                 const float l = lse[row];
-                const float sf = 1.0f + zl2 * l;
-                const uint32_t t = tgt[row];
+                const float lL2 = l * LOG2E;
+                const float sf = (1.0f + zl2 * l) * inv_n;
+                const int tc = (int)tgt[row] - fp.col0 - c16;
+                TZ *out = dz + (size_t)row * V + fp.col0 + c16;
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
-                    const int col = fp.col0 + 16 * j + c16;
-                    if (col >= V) continue;
-                    const float p = expf(acc[i][j][r] - l);
-                    const float ti = ((uint32_t)col == t) ? t_scale : 0.0f;
-                    const float d = (sf * p - ti - eps_over_v) * inv_n;
-                    dz[(size_t)row * V + col] = (TZ)d;
+                    if (!FULL && fp.col0 + 16 * j + c16 >= V) continue;
+                    const float p = __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], LOG2E, -lL2));
+                    float d = fmaf(sf, p, -off);
+                    if (tc == 16 * j) d -= tsc;
+                    out[16 * j] = (TZ)d;
                 }
             }
     }
