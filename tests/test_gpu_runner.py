@@ -253,6 +253,60 @@ def test_step_parity_qwen3_06b_widths(precision):
             assert rel_l2(du_ref, du) < 1e-2, (k, rel_l2(du_ref, du))
 
 
+@pytest.mark.parametrize("tied", [1, 0], ids=["tied", "untied"])
+def test_split_embedding_update_bit_identical(tied):
+    """The two-stream bf16 step updates the embedding table in two parts: rows
+    no token names on the second stream right after the head's weight
+    gradient, the token rows inside the embedding-backward launch.  Over two
+    steps (the second with non-zero moments) the table's gradient, Adam
+    moments and weights (and the untied head's and the final norm's) equal,
+    bit for bit, one full-table Adam update (the library's own span kernel)
+    applied to the gradient a forward/backward-only pass produces from the
+    same state."""
+    import valkyr_amd as v
+    from valkyr_amd import kernels as K
+    from valkyr_amd.runner import ADAM_M, ADAM_V, GRAD, PARAM
+
+    from helpers import dev, host
+
+    c = dict(dim=256, n_heads=4, n_kv_heads=2, head_dim=64, ff_dim=512, n_pos=128, n_seqs=2,
+             n_layers=2, vocab_size=4096, rms_eps=1e-6, rotary_dim=64, rope_theta=1e6,
+             qk_norm=1, lr=1e-3, tied_embeddings=tied)
+    T, V = 256, 4096
+    keys = [(-1, 0), (-1, 1)] + ([] if tied else [(-1, 2)])
+    with v.Runner(v.make_config(**c, precision=1)) as a, \
+            v.Runner(v.make_config(**c, precision=1)) as b:
+        for r in (a, b):
+            r.init_random(seed=31, std=0.02)
+        for it in range(2):
+            # ids from a narrow range: repeated ids (the owner sums them) and
+            # most of the table untouched
+            tok = (O.ids(T, 40 + it, 97) * 37 + 5).astype(np.uint32) % V
+            tgt = O.ids(T, 50 + it, V)
+            state = {k: [a.get(kind, *k) for kind in (PARAM, ADAM_M, ADAM_V)] for k in keys}
+            t = a.step_t
+            b.step_t = t
+            lb = b.forward_backward(tok, tgt)
+            a.step(tok, tgt)
+            assert a.last_loss() == lb
+            for k in keys:
+                g = b.get(GRAD, *k)
+                assert np.array_equal(a.get(GRAD, *k), g), (it, k, "grad")
+                p, m, vv = (dev(x) for x in state[k])
+                n = g.size
+                K.adam_step(p, dev(g), m, vv, n, c["lr"], 0.9, 0.999, 1e-8, t)
+                for kind, buf in ((PARAM, p), (ADAM_M, m), (ADAM_V, vv)):
+                    want = host(buf, n)
+                    got = a.get(kind, *k)
+                    assert np.array_equal(got, want), (it, k, kind, rel_l2(want, got))
+            # b follows a's state for the next step's gradient
+            for k in [(-1, 0), (-1, 1)] + ([] if tied else [(-1, 2)]) + \
+                    [(l, w) for l in range(2) for w in range(11)]:
+                for kind in (PARAM, ADAM_M, ADAM_V):
+                    b.set(kind, *k, a.get(kind, *k))
+        note(f"  split embedding update tied={tied}: bit-identical over 2 steps")
+
+
 def test_step_bf16_vs_pure_fp32_oracle():
     """bf16-operand GPU path against the unrounded fp32 oracle (reported; 5e-2 bar)."""
     m, r, tok, tgt, cfg = build_pair(0)

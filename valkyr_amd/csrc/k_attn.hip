@@ -1213,7 +1213,10 @@ static_assert(2 * STREAM + BN * HD * 2 <= LDS, "tile streams and V slices exceed
 // of one (sequence, KV head), which sit on one XCD, read a tile at about the
 // same time and share it in L2.  Under a causal mask the heaviest key blocks
 // (lowest keys) have the lowest block ids and start first.
-template <int NWV, bool QKE>
+// NH: query heads per head group (hpk / 2) when known at compile time (1 for
+// GQA 2:1, 2 for 4:1), 0 to read it from the shape; a constant turns the
+// per-tile (head, query tile) split of the iteration index into shifts.
+template <int NWV, bool QKE, int NH = 0>
 __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPtrs p) {
     using namespace dkv4;
     constexpr int NS = NWV / 2;                 // key slices per head group
@@ -1228,7 +1231,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
 
     const int kt = (int)blockIdx.y;
     const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
-    const int hpk = s.n_heads / s.n_kv_heads, nh = hpk / 2;
+    const int hpk = s.n_heads / s.n_kv_heads, nh = NH ? NH : hpk / 2;
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int sl = wave % NS, hg = wave / NS;  // key slice, head group
@@ -1337,11 +1340,10 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
 #pragma unroll
         for (int qs = 0; qs < QS; ++qs) lim[qs] = s.causal ? q0 + 16 * qs + 4 * g - kw0 - c16 : (1 << 30);
         // lse and D of this lane's query rows q0 + 16 qs + 4 g + r, read from LDS
-        // where they are used (not held across the tile)
-        auto lse2 = [&](int qs, int r) {
-            const float l = Ls[hg][buf][16 * qs + 4 * g + r];
-            return l == -INFINITY ? INFINITY : l * LOG2E;  // fully masked row: P = 0
-        };
+        // where they are used (not held across the tile).  Every query row sees
+        // at least one key on this path (causal needs n_q == n_kv, so row q sees
+        // keys 0..q), so its LSE is finite and no empty-row case arises here.
+        auto lse2 = [&](int qs, int r) { return Ls[hg][buf][16 * qs + 4 * g + r] * LOG2E; };
         auto dval = [&](int qs, int r) { return Dd[hg][buf][16 * qs + 4 * g + r]; };
         f32x4 sc[QS][KS], dp[QS][KS];
 #pragma unroll
@@ -2195,6 +2197,17 @@ bool fa_bw_v4_preferred(const AttnShape &s) {
     return fa_bw_v4_ok(s) && (long)s.n_batch * s.n_kv_heads * (s.n_kv / 128) >= 128;
 }
 
+// The dK/dV recompute kernel with the head-group size as a constant where it
+// is one of the common ones.
+template <int W, bool QKE>
+void launch_dkv4(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
+    const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
+    const int nh = s.n_heads / s.n_kv_heads / 2;
+    if (nh == 1) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 1>), gkv, dim3(W * 64), 0, st, s, p);
+    else if (nh == 2) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 2>), gkv, dim3(W * 64), 0, st, s, p);
+    else hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 0>), gkv, dim3(W * 64), 0, st, s, p);
+}
+
 // One of the two recompute kernels alone (D already in p.d): which = 0 the
 // dK/dV kernel, 1 the dQ kernel, so a caller can run them on two streams.
 hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipStream_t st) {
@@ -2210,9 +2223,8 @@ hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipSt
         return hipErrorInvalidValue;
     constexpr int W = 8;
     if (which == 0) {
-        const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
-        if (e.out) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, true>), gkv, dim3(W * 64), 0, st, s, p);
-        else hipLaunchKernelGGL((fa_bwd_dkv4_k<W, false>), gkv, dim3(W * 64), 0, st, s, p);
+        if (e.out) launch_dkv4<W, true>(s, p, st);
+        else launch_dkv4<W, false>(s, p, st);
     } else {
         const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
         if (e.out) hipLaunchKernelGGL((fa_bwd_dq4_k<W, false, true>), gq, dim3(W * 64), 0, st, s, p);
@@ -2247,7 +2259,6 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
             return hipErrorInvalidValue;
         if (p.o16 && (long)s.n_q * p.ldo16 * 2 >= (1l << 31)) return hipErrorInvalidValue;
         constexpr int DKV_WAVES = 8, DQ_WAVES = 8;
-        const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
         const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
         const QkEpi &e = p.qk;
         if (e.out) {
@@ -2257,12 +2268,12 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
                 (bool)e.gq != (bool)e.gk || (e.gq && (!e.pq || !e.pk)))
                 return hipErrorInvalidValue;
             hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true, true>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
-            hipLaunchKernelGGL((fa_bwd_dkv4_k<DKV_WAVES, true>), gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+            launch_dkv4<DKV_WAVES, true>(s, p, st);
         } else if (p.o16) {  // dQ forms D, then dK/dV reads it
             hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
-            hipLaunchKernelGGL((fa_bwd_dkv4_k<DKV_WAVES, false>), gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+            launch_dkv4<DKV_WAVES, false>(s, p, st);
         } else {
-            hipLaunchKernelGGL((fa_bwd_dkv4_k<DKV_WAVES, false>), gkv, dim3(DKV_WAVES * 64), 0, st, s, p);
+            launch_dkv4<DKV_WAVES, false>(s, p, st);
             hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, false, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
         }
         return hipGetLastError();

@@ -3,6 +3,7 @@
 // sized to fill the 256 CUs; fp contraction is disabled so each kernel
 // rounds exactly like the scalar reference formula it restates.
 #include "ops.hpp"
+#include "adam.hpp"
 
 #pragma clang fp contract(off)
 
@@ -231,31 +232,6 @@ __global__ void embed_lookup_k(const float *embed, const uint32_t *ids, float *o
     }
 }
 
-// adam_step.comp:41-62
-__device__ __forceinline__ void adam1(float &p, float g, float &m, float &v, float lr, float b1,
-                                      float b2, float eps, float bc1, float bc2, float wd) {
-    const float nm = b1 * m + (1.0f - b1) * g;
-    const float nv = b2 * v + (1.0f - b2) * g * g;
-    m = nm;
-    v = nv;
-    const float m_hat = nm / bc1;
-    const float v_hat = nv / bc2;
-    float q = p;
-    if (wd > 0.0f) q = q * (1.0f - lr * wd);
-    p = q - lr * m_hat / (sqrtf(v_hat) + eps);
-}
-
-VKH_DEV void adam4(f32x4 &p, const f32x4 &g, f32x4 &m, f32x4 &v, float lr, float b1, float b2,
-                   float eps, float bc1, float bc2, float wd) {
-    float pp[4] = {p.x, p.y, p.z, p.w}, mm[4] = {m.x, m.y, m.z, m.w}, vv[4] = {v.x, v.y, v.z, v.w};
-    const float gg[4] = {g.x, g.y, g.z, g.w};
-#pragma unroll
-    for (int i = 0; i < 4; ++i) adam1(pp[i], gg[i], mm[i], vv[i], lr, b1, b2, eps, bc1, bc2, wd);
-    p = f32x4{pp[0], pp[1], pp[2], pp[3]};
-    m = f32x4{mm[0], mm[1], mm[2], mm[3]};
-    v = f32x4{vv[0], vv[1], vv[2], vv[3]};
-}
-
 // Streaming update: every byte is touched once, so loads and stores are
 // non-temporal.  Each block updates one contiguous chunk of NT * ADAM_U
 // float4 (all loads issued before the first store), the pattern that
@@ -303,6 +279,55 @@ __global__ __launch_bounds__(NT) void adam_chunk_k(float *p_, const float *g_, f
         adam1(p_[k], g_[k], m_[k], v_[k], lr, b1, b2, eps, bc1, bc2, wd);
         if (pb) pb[k] = (bf16)p_[k];
     }
+}
+
+// Adam over the rows of a [rows, dim] table (dim % 4 == 0) whose mark is not
+// `stamp`: the rows a step's tokens touched carry the stamp and are updated
+// by the embedding backward once their gradient is complete, the others as
+// soon as the head's weight gradient is.  Same chunking as adam_chunk_k.
+__global__ __launch_bounds__(NT) void adam_rows_k(float *p_, const float *g_, float *m_, float *v_,
+                                                   bf16 *pb, size_t n, unsigned dim4,
+                                                   const uint32_t *mark, uint32_t stamp,
+                                                   AdamHyper h) {
+    const size_t n4 = n / 4;
+    f32x4 *p = reinterpret_cast<f32x4 *>(p_), *m = reinterpret_cast<f32x4 *>(m_),
+          *v = reinterpret_cast<f32x4 *>(v_);
+    const f32x4 *g = reinterpret_cast<const f32x4 *>(g_);
+    const size_t base = (size_t)blockIdx.x * (NT * ADAM_U) + threadIdx.x;
+    f32x4 pp[ADAM_U], gg[ADAM_U], mm[ADAM_U], vv[ADAM_U];
+    bool on[ADAM_U];
+#pragma unroll
+    for (int u = 0; u < ADAM_U; ++u) {
+        const size_t j = base + (size_t)u * NT;
+        on[u] = j < n4 && mark[j / dim4] != stamp;
+        if (on[u]) {
+            pp[u] = __builtin_nontemporal_load(&p[j]);
+            gg[u] = __builtin_nontemporal_load(&g[j]);
+            mm[u] = __builtin_nontemporal_load(&m[j]);
+            vv[u] = __builtin_nontemporal_load(&v[j]);
+        }
+    }
+#pragma unroll
+    for (int u = 0; u < ADAM_U; ++u) {
+        if (!on[u]) continue;
+        const size_t j = base + (size_t)u * NT;
+        adam4(pp[u], gg[u], mm[u], vv[u], h);
+        __builtin_nontemporal_store(pp[u], &p[j]);
+        __builtin_nontemporal_store(mm[u], &m[j]);
+        __builtin_nontemporal_store(vv[u], &v[j]);
+        if (pb) {
+            bf16x4 b;
+            b[0] = (bf16)pp[u].x; b[1] = (bf16)pp[u].y; b[2] = (bf16)pp[u].z; b[3] = (bf16)pp[u].w;
+            __builtin_nontemporal_store(b, reinterpret_cast<bf16x4 *>(pb) + j);
+        }
+    }
+}
+
+// mark[ids[i]] = stamp (duplicate ids write the same value)
+__global__ void mark_rows_k(const uint32_t *ids, int n, uint32_t *mark, uint32_t rows,
+                            uint32_t stamp) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n && ids[i] < rows) mark[ids[i]] = stamp;
 }
 
 // Adam over a span that holds norm gains whose gradients are still per-block
@@ -588,6 +613,28 @@ hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, flo
     grid = grid < 1 ? 1 : (grid > ADAM_GRID ? ADAM_GRID : grid);
     hipLaunchKernelGGL(adam_k, dim3((unsigned)grid), dim3(NT), 0, st, p, g, m, v, pb, n, lr,
                        beta1, beta2, eps, bc1, bc2, wd, vec);
+    return hipGetLastError();
+}
+
+hipError_t adam_rows_unmarked(float *p, const float *g, float *m, float *v, bf16 *pb, int rows,
+                              int dim, const uint32_t *mark, uint32_t stamp, const AdamHyper &h,
+                              hipStream_t st) {
+    if (rows <= 0 || dim <= 0) return hipSuccess;
+    const size_t n = (size_t)rows * dim;
+    const bool vec = al16(p) && al16(g) && al16(m) && al16(v) && ((uintptr_t)pb & 7u) == 0;
+    if (!vec || dim % 4 || !mark) return hipErrorInvalidValue;
+    const size_t blocks = (n / 4 + NT * ADAM_U - 1) / (NT * ADAM_U);
+    if (blocks >= (1u << 31)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(adam_rows_k, dim3((unsigned)blocks), dim3(NT), 0, st, p, g, m, v, pb, n,
+                       (unsigned)(dim / 4), mark, stamp, h);
+    return hipGetLastError();
+}
+
+hipError_t mark_rows(const uint32_t *ids, int n, uint32_t *mark, int rows, uint32_t stamp,
+                     hipStream_t st) {
+    if (n <= 0) return hipSuccess;
+    hipLaunchKernelGGL(mark_rows_k, dim3(ceil_div(n, NT)), dim3(NT), 0, st, ids, n, mark,
+                       (uint32_t)rows, stamp);
     return hipGetLastError();
 }
 

@@ -13,6 +13,7 @@
 // oracle's, so the result is bit-identical to it; no sort, no atomics, no
 // work buffer.
 #include "ops.hpp"
+#include "adam.hpp"
 
 namespace vkh {
 
@@ -20,10 +21,10 @@ namespace {
 
 constexpr int EO_NT = 256;
 
-template <bool VEC>
+template <bool VEC, bool ADAM>
 __global__ __launch_bounds__(EO_NT) void embed_own_k(const float *dy, const uint32_t *ids, int n,
                                                       int dim, float *out, int vocab,
-                                                      int accumulate) {
+                                                      int accumulate, EmbedAdam ea) {
     __shared__ uint64_t masks[EO_NT / 64];
     __shared__ uint16_t list[kEmbedBwMaxPos];
     const int p = blockIdx.x, lane = threadIdx.x % 64, w = threadIdx.x / 64;
@@ -65,6 +66,21 @@ __global__ __launch_bounds__(EO_NT) void embed_own_k(const float *dy, const uint
                 acc = make_float4(o.x + acc.x, o.y + acc.y, o.z + acc.z, o.w + acc.w);
             }
             reinterpret_cast<float4 *>(orow)[c] = acc;
+            if constexpr (ADAM) {  // the row's gradient is final: its Adam update
+                const size_t j = (size_t)tok * (dim / 4) + c;
+                f32x4 *p = reinterpret_cast<f32x4 *>(ea.p), *m = reinterpret_cast<f32x4 *>(ea.m),
+                      *v = reinterpret_cast<f32x4 *>(ea.v);
+                f32x4 pp = p[j], mm = m[j], vv = v[j];
+                adam4(pp, f32x4{acc.x, acc.y, acc.z, acc.w}, mm, vv, ea.h);
+                p[j] = pp;
+                m[j] = mm;
+                v[j] = vv;
+                if (ea.pb) {
+                    bf16x4 b;
+                    b[0] = (bf16)pp.x; b[1] = (bf16)pp.y; b[2] = (bf16)pp.z; b[3] = (bf16)pp.w;
+                    reinterpret_cast<bf16x4 *>(ea.pb)[j] = b;
+                }
+            }
         }
     } else {
         for (int c = threadIdx.x; c < dim; c += EO_NT) {
@@ -85,12 +101,27 @@ hipError_t embedding_backward(const float *dy, const uint32_t *ids, float *out, 
     if (n_pos <= 0) return hipSuccess;
     if (n_pos > kEmbedBwMaxPos) return hipErrorInvalidValue;
     const bool vec = (dim % 4 == 0) && (((uintptr_t)dy | (uintptr_t)out) & 15u) == 0;
+    const EmbedAdam none{};
     if (vec)
-        hipLaunchKernelGGL(embed_own_k<true>, dim3(n_pos), dim3(EO_NT), 0, st, dy, ids, n_pos, dim,
-                           out, vocab, accumulate ? 1 : 0);
+        hipLaunchKernelGGL((embed_own_k<true, false>), dim3(n_pos), dim3(EO_NT), 0, st, dy, ids,
+                           n_pos, dim, out, vocab, accumulate ? 1 : 0, none);
     else
-        hipLaunchKernelGGL(embed_own_k<false>, dim3(n_pos), dim3(EO_NT), 0, st, dy, ids, n_pos,
-                           dim, out, vocab, accumulate ? 1 : 0);
+        hipLaunchKernelGGL((embed_own_k<false, false>), dim3(n_pos), dim3(EO_NT), 0, st, dy, ids,
+                           n_pos, dim, out, vocab, accumulate ? 1 : 0, none);
+    return hipGetLastError();
+}
+
+hipError_t embedding_backward_adam(const float *dy, const uint32_t *ids, float *out, int n_pos,
+                                   int dim, int vocab, bool accumulate, const EmbedAdam &ea,
+                                   hipStream_t st) {
+    if (n_pos <= 0) return hipSuccess;
+    if (n_pos > kEmbedBwMaxPos) return hipErrorInvalidValue;
+    const uintptr_t a = (uintptr_t)dy | (uintptr_t)out | (uintptr_t)ea.p | (uintptr_t)ea.m |
+                        (uintptr_t)ea.v;
+    if (dim % 4 || (a & 15u) || ((uintptr_t)ea.pb & 7u) || !ea.p || !ea.m || !ea.v)
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL((embed_own_k<true, true>), dim3(n_pos), dim3(EO_NT), 0, st, dy, ids, n_pos,
+                       dim, out, vocab, accumulate ? 1 : 0, ea);
     return hipGetLastError();
 }
 

@@ -4,6 +4,7 @@
 #pragma once
 
 #include "common.hpp"
+#include "adam.hpp"
 
 namespace vkh {
 
@@ -180,6 +181,24 @@ size_t qkv_partial_floats(const QkvLayout &L);
 hipError_t embedding_backward(const float *dy, const uint32_t *ids, float *out, int n_pos,
                               int dim, int vocab, bool accumulate, void *work, hipStream_t st);
 size_t embed_bw_work_bytes(int n_pos);
+// The same scatter, and then the Adam update of every row it wrote (dim % 4
+// == 0, 16-byte aligned rows): for a step whose table gradient is complete
+// once the scatter is (the head's weight gradient came first).
+struct EmbedAdam {
+    float *p, *m, *v;
+    bf16 *pb;  // optional bf16 copy of the updated rows
+    AdamHyper h;
+};
+hipError_t embedding_backward_adam(const float *dy, const uint32_t *ids, float *out, int n_pos,
+                                   int dim, int vocab, bool accumulate, const EmbedAdam &ea,
+                                   hipStream_t st);
+// Adam over the rows of a [rows, dim] table (dim % 4 == 0, 16-byte aligned)
+// whose mark differs from `stamp`; mark_rows stamps the rows named by ids.
+hipError_t adam_rows_unmarked(float *p, const float *g, float *m, float *v, bf16 *pb, int rows,
+                              int dim, const uint32_t *mark, uint32_t stamp, const AdamHyper &h,
+                              hipStream_t st);
+hipError_t mark_rows(const uint32_t *ids, int n, uint32_t *mark, int rows, uint32_t stamp,
+                     hipStream_t st);
 constexpr int kEmbedBwMaxPos = 16384;
 
 // ── attention (k_attn.hip) ───────────────────────────────────────────

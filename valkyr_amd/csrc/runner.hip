@@ -136,6 +136,14 @@ struct vkh_runner {
     hipStream_t side = nullptr;
     std::vector<hipEvent_t> ev_layer;
     hipEvent_t ev_side = nullptr, ev_head = nullptr, ev_lm = nullptr;
+    // Split embedding update (concurrent mode with Adam): rows of the table
+    // that no token of the step names have their final gradient once the
+    // head's weight gradient is written (tied) or are zero (untied), so their
+    // Adam update runs on the side stream right after that GEMM; the rows the
+    // tokens name (stamped in emb_mark with this step's stamp) are updated by
+    // the embedding backward at the end of the step, inside its own launch.
+    uint32_t *emb_mark = nullptr;
+    uint32_t mark_stamp = 0;
     std::vector<LayerGrads> lg;
     GemmWs gws2{nullptr, 0};
     std::vector<Acts> acts;
@@ -440,6 +448,10 @@ struct vkh_runner {
                 VKH_HIP(hipEventCreateWithFlags(&ev_side, hipEventDisableTiming));
                 VKH_HIP(hipEventCreateWithFlags(&ev_head, hipEventDisableTiming));
                 VKH_HIP(hipEventCreateWithFlags(&ev_lm, hipEventDisableTiming));
+                if (embed_split_ok()) {
+                    VKH_TRY(alloc(emb_mark, (size_t)V));
+                    VKH_HIP(fill_f32(reinterpret_cast<float *>(emb_mark), (size_t)V, 0.f, own));
+                }
                 lg.assign(L, LayerGrads{});
                 const int n_g = recompute ? std::min(L, kGradSets) : L;
                 const int n_dy = recompute ? std::min(L, kDyRing) : L;
@@ -1044,17 +1056,26 @@ struct vkh_runner {
         const CceShape cs{T, V, D, 0.f, 0.f};
         // head backward: dh and dW_lm (tied: the embed grad slot)
         float *dw_lm = lora ? nullptr : Gd(lm_head);
+        const bool split = with_adam && embed_split_ok();
         if (b16()) {
             VKH_HIP(cce_forward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
                                   cce_work, cur));
             VKH_HIP(cce_backward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, (bf16 *)dz, d_fn,
                                    concurrent ? nullptr : dw_lm, 0.f, gws, cur));
             if (concurrent && dw_lm) {
+                if (split) {  // this step's token rows, for the split embedding update
+                    if (++mark_stamp == 0) {
+                        VKH_HIP(fill_f32(reinterpret_cast<float *>(emb_mark), (size_t)V, 0.f, cur));
+                        mark_stamp = 1;
+                    }
+                    VKH_HIP(mark_rows(tok_d, T, emb_mark, V, mark_stamp, cur));
+                }
                 // dW_lm = dz^T h on the side stream; the tied embedding scatter
                 // below adds into the same gradient and waits for it
                 VKH_HIP(hipEventRecord(ev_head, cur));
                 VKH_HIP(hipStreamWaitEvent(side, ev_head, 0));
                 VKH_HIP(g16_tn((const bf16 *)dz, V, fn_outb, D, dw_lm, D, T, V, D, 1.f, 0.f, gws2, side));
+                if (split) VKH_TRY(embed_adam_early());
                 VKH_HIP(hipEventRecord(ev_lm, side));
             }
         } else {
@@ -1092,12 +1113,21 @@ struct vkh_runner {
         if (!lora) {
             float *dE = Gd(embed);
             if (concurrent) VKH_HIP(hipStreamWaitEvent(cur, ev_lm, 0));
-            if (!tied) VKH_HIP(fill_f32(dE, embed.numel, 0.f, cur));
-            VKH_HIP(embedding_backward(dx[c], tok_d, dE, T, D, V, tied, embed_work, cur));
+            if (split) {
+                // the scatter completes the token rows' gradient: their update in the same launch
+                const EmbedAdam ea{W(embed), M + embed.off, Vm + embed.off,
+                                   b16() ? Pb + embed.off : nullptr, adam_hyper(cfg.lr)};
+                VKH_HIP(embedding_backward_adam(dx[c], tok_d, dE, T, D, V, tied, ea, cur));
+            } else {
+                if (!tied) VKH_HIP(fill_f32(dE, embed.numel, 0.f, cur));
+                VKH_HIP(embedding_backward(dx[c], tok_d, dE, T, D, V, tied, embed_work, cur));
+            }
         }
         if (concurrent) {
-            // embed, final norm, lm_head: the span before layer 0
-            if (with_adam) VKH_TRY(adam_span(0, ls[0].t[0].off, cur));
+            // embed, final norm, lm_head: the span before layer 0 (split: the
+            // embedding and lm_head are done, the final norm remains)
+            if (split) VKH_TRY(adam_span(final_norm.off, final_norm.off + final_norm.numel, cur));
+            else if (with_adam) VKH_TRY(adam_span(0, ls[0].t[0].off, cur));
             VKH_HIP(hipEventRecord(ev_side, side));
             VKH_HIP(hipStreamWaitEvent(cur, ev_side, 0));
         }
@@ -1134,6 +1164,30 @@ struct vkh_runner {
         const LayerSpans &s = ls[l];
         const Span &last = s.t[10].numel ? s.t[10] : s.t[8];
         return last.off + last.numel;
+    }
+
+    AdamHyper adam_hyper(float lr) const {
+        const float t = (float)step_t;
+        return AdamHyper{lr, cfg.beta1, cfg.beta2, cfg.eps_adam, 1.0f - powf(cfg.beta1, t),
+                         1.0f - powf(cfg.beta2, t), 0.f};
+    }
+    // the split embedding update needs whole float4 rows
+    bool embed_split_ok() const { return concurrent && !lora && D % 4 == 0; }
+
+    // Side stream, after the head's weight-gradient GEMM: Adam over the table
+    // rows no token of this step names (and, untied, over lm_head, whose
+    // gradient is complete, after zeroing the embedding gradient the scatter
+    // writes into).
+    vkh_status embed_adam_early() {
+        const AdamHyper h = adam_hyper(cfg.lr);
+        if (!tied) {
+            VKH_TRY(adam_span(lm_head.off, lm_head.off + lm_head.numel, side));
+            VKH_HIP(fill_f32(Gd(embed), embed.numel, 0.f, side));
+        }
+        VKH_HIP(adam_rows_unmarked(W(embed), Gd(embed), M + embed.off, Vm + embed.off,
+                                   b16() ? Pb + embed.off : nullptr, V, D, emb_mark, mark_stamp, h,
+                                   side));
+        return VKH_OK;
     }
 
     // Adam over the arena range [b, e) of a full fine-tune (adam_step.comp:45-61)
