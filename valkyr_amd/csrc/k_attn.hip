@@ -1345,11 +1345,17 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
         // keys 0..q), so its LSE is finite and no empty-row case arises here.
         auto lse2 = [&](int qs, int r) { return Ls[hg][buf][16 * qs + 4 * g + r] * LOG2E; };
         auto dval = [&](int qs, int r) { return Dd[hg][buf][16 * qs + 4 * g + r]; };
+        // the dP accumulators start at -D, so they end as dP - D
         f32x4 sc[QS][KS], dp[QS][KS];
 #pragma unroll
-        for (int qs = 0; qs < QS; ++qs)
+        for (int qs = 0; qs < QS; ++qs) {
+            const f32x4 nd{-dval(qs, 0), -dval(qs, 1), -dval(qs, 2), -dval(qs, 3)};
 #pragma unroll
-            for (int ks = 0; ks < KS; ++ks) sc[qs][ks] = dp[qs][ks] = f32x4{0, 0, 0, 0};
+            for (int ks = 0; ks < KS; ++ks) {
+                sc[qs][ks] = f32x4{0, 0, 0, 0};
+                dp[qs][ks] = nd;
+            }
+        }
         // Each phase walks its 8 A fragments with the next fragment's LDS read
         // issued before this one's MFMAs; the softmax and dS arithmetic of one
         // (qs, ks) tile rides along with each step of the following phase.
@@ -1396,7 +1402,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
                     for (int r = 0; r < 4; ++r)
                         if (16 * ks - r > lim[qs]) sc[qs][ks][r] = 0.f;
         }
-        // dV^T += dO^T P, with dS = P (dP - D) of tile (i / 4, i % 4)
+        // dV^T += dO^T P, with dS = P (dP - D) of tile (i / 4, i % 4) (dp holds dP - D)
         {
             bf16x8 pb[KS];
 #pragma unroll
@@ -1413,7 +1419,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
                     const int t2 = i / EVERY, qs2 = t2 / KS, ks2 = t2 % KS;
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
-                        dp[qs2][ks2][r] = sc[qs2][ks2][r] * (dp[qs2][ks2][r] - dval(qs2, r));
+                        dp[qs2][ks2][r] = sc[qs2][ks2][r] * dp[qs2][ks2][r];
                 }
             }
         }
@@ -1627,11 +1633,15 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
         for (int j = 0; j < QSUB; ++j)
             lim[j] = min(s.causal ? q00 + QST * j + c16 - kk - 4 * g : (1 << 30), s.n_kv - 1 - kk - 4 * g);
         const bool diag = (s.causal && kk + BN - 1 > q00) || kk + BN > s.n_kv;
+        // the dP^T accumulators start at -D (one query per lane), so they end as dP^T - D
         f32x4 st[KS][QSUB], dpt[KS][QSUB];
 #pragma unroll
         for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-            for (int j = 0; j < QSUB; ++j) st[ks][j] = dpt[ks][j] = f32x4{0, 0, 0, 0};
+            for (int j = 0; j < QSUB; ++j) {
+                st[ks][j] = f32x4{0, 0, 0, 0};
+                dpt[ks][j] = f32x4{-dd[j], -dd[j], -dd[j], -dd[j]};
+            }
         // The three phases walk 24 operand fragments in one sequence (slots
         // 0-7: K rows for S^T, f = (ds, ks) = (f / 2, f % 2); 8-15: V rows for
         // dP^T; 16-23: transposed K for dQ^T), each slot's LDS read issued PD
@@ -1686,7 +1696,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
 #pragma unroll
             for (int ks = 0; ks < KS; ++ks)
 #pragma unroll
-                for (int r = 0; r < 4; ++r) dpt[ks][j][r] = st[ks][j][r] * (dpt[ks][j][r] - dd[j]);
+                for (int r = 0; r < 4; ++r) dpt[ks][j][r] = st[ks][j][r] * dpt[ks][j][r];
             sb[j] = frag_acc(dpt[0][j], dpt[1][j]);
         }
         // dQ^T += K^T dS^T
