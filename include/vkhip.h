@@ -224,7 +224,10 @@ typedef enum vkh_attn_bw_path {
 } vkh_attn_bw_path;
 uint32_t vkh_runner_attention_backward_path(const vkh_runner *r);
 
-/* Tensor access (host <-> device copies, blocking). */
+/* Tensor access (host <-> device copies, blocking).  A LoRA runner in bf16
+ * precision keeps its frozen base matrices (embed, lm_head, q..down) in bf16
+ * only: get returns their bf16 values widened to fp32, set rounds to nearest
+ * even, and tensor_device_ptr refuses them (VKH_ERR_UNSUPPORTED). */
 vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int which,
                                    size_t *numel);
 vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, float *host,

@@ -232,6 +232,21 @@ __global__ void embed_lookup_k(const float *embed, const uint32_t *ids, float *o
     }
 }
 
+// The same lookup from a bf16 table (a frozen bf16 base), widened to fp32
+// (dim % 4 == 0, 8-byte aligned rows).
+__global__ void embed_lookup_bf16_k(const bf16 *embed, const uint32_t *ids, float *out, int n_pos,
+                                    int dim, float scale) {
+    const size_t n4 = (size_t)n_pos * dim / 4;
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    const int d4 = dim / 4;
+    for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n4; i += stride) {
+        const int p = (int)(i / d4), c = (int)(i % d4);
+        const bf16x4 e = reinterpret_cast<const bf16x4 *>(embed + (size_t)ids[p] * dim)[c];
+        reinterpret_cast<float4 *>(out)[i] =
+            make_float4((float)e[0] * scale, (float)e[1] * scale, (float)e[2] * scale, (float)e[3] * scale);
+    }
+}
+
 // Streaming update: every byte is touched once, so loads and stores are
 // non-temporal.  Each block updates one contiguous chunk of NT * ADAM_U
 // float4 (all loads issued before the first store), the pattern that
@@ -573,6 +588,15 @@ hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int
     const bool v4 = (dim % 4 == 0) && al16(embed) && al16(out);
     hipLaunchKernelGGL(embed_lookup_k, dim3(grid_for((size_t)n_pos * dim / (v4 ? 4 : 1))), dim3(NT),
                        0, st, embed, ids, out, n_pos, dim, scale_, v4);
+    return hipGetLastError();
+}
+
+hipError_t embed_lookup_bf16(const bf16 *embed, const uint32_t *ids, float *out, int n_pos,
+                             int dim, float scale_, hipStream_t st) {
+    if (n_pos <= 0 || dim <= 0) return hipSuccess;
+    if (dim % 4 || ((uintptr_t)embed & 7u) || !al16(out)) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(embed_lookup_bf16_k, dim3(grid_for((size_t)n_pos * dim / 4)), dim3(NT), 0, st,
+                       embed, ids, out, n_pos, dim, scale_);
     return hipGetLastError();
 }
 

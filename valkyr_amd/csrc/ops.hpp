@@ -99,6 +99,9 @@ hipError_t swiglu_backward(const float *dg, long lddg, const float *pg, long ldp
                            long lddup, DType odt, int rows, int cols, hipStream_t st);
 hipError_t embed_lookup(const float *embed, const uint32_t *ids, float *out, int n_pos, int dim,
                         float scale, hipStream_t st);
+// the lookup from a bf16 table (dim % 4 == 0), widened to fp32
+hipError_t embed_lookup_bf16(const bf16 *embed, const uint32_t *ids, float *out, int n_pos,
+                             int dim, float scale, hipStream_t st);
 // Adam (adam_step.comp): bc1 = 1 - beta1^t, bc2 = 1 - beta2^t computed by the caller.
 // pb (optional) receives bf16(p) after the update.
 hipError_t adam_step(float *p, const float *g, float *m, float *v, size_t n, float lr,

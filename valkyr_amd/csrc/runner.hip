@@ -45,7 +45,8 @@ struct Acts {
     bf16 *n1b, *attn_b, *n2b, *gatedb;
 };
 
-__global__ void init_normal_k(float *p, size_t n, uint64_t seed, float stddev) {
+template <typename TO>
+__global__ void init_normal_k(TO *p, size_t n, uint64_t seed, float stddev) {
     const size_t stride = (size_t)gridDim.x * blockDim.x;
     for (size_t i = blockIdx.x * (size_t)blockDim.x + threadIdx.x; i < n; i += stride) {
         uint64_t z = seed + 0x9E3779B97F4A7C15ull * (i / 2 + 1);
@@ -56,7 +57,7 @@ __global__ void init_normal_k(float *p, size_t n, uint64_t seed, float stddev) {
         const double u2 = ((double)(z & 0xFFFFFFull) + 0.5) * (1.0 / 16777216.0);
         const double r = sqrt(-2.0 * log(u1));
         const double a = 6.283185307179586 * u2;
-        p[i] = (float)(stddev * r * ((i & 1) ? sin(a) : cos(a)));
+        p[i] = (TO)(float)(stddev * r * ((i & 1) ? sin(a) : cos(a)));
     }
 }
 
@@ -65,6 +66,33 @@ inline uint64_t mix(uint64_t x) {
     x = (x ^ (x >> 30)) * 0xBF58476D1CE4E5B9ull;
     x = (x ^ (x >> 27)) * 0x94D049BB133111EBull;
     return x ^ (x >> 31);
+}
+
+// Host <-> device transfers of a bf16-only tensor as fp32 values: widening
+// is exact; rounding is to nearest even (the device casts' rounding).
+uint16_t bf16_bits_rne(float f) {
+    uint32_t u;
+    memcpy(&u, &f, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);  // NaN stays NaN
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+vkh_status read_bf16_widened(const bf16 *dev, size_t n, float *host) {
+    std::vector<uint16_t> h(n);
+    VKH_HIP(hipMemcpy(h.data(), dev, n * 2, hipMemcpyDeviceToHost));
+    for (size_t i = 0; i < n; ++i) {
+        const uint32_t u = (uint32_t)h[i] << 16;
+        memcpy(&host[i], &u, 4);
+    }
+    return VKH_OK;
+}
+
+vkh_status write_bf16_rounded(bf16 *dev, size_t n, const float *host) {
+    std::vector<uint16_t> h(n);
+    for (size_t i = 0; i < n; ++i) h[i] = bf16_bits_rne(host[i]);
+    VKH_HIP(hipMemcpy(dev, h.data(), n * 2, hipMemcpyHostToDevice));
+    return VKH_OK;
 }
 
 }  // namespace
@@ -83,6 +111,12 @@ struct vkh_runner {
     size_t total = 0, tb = 0, te = 0, lora_a_begin = 0, lora_b_begin = 0;
 
     float *P = nullptr, *G = nullptr, *M = nullptr, *Vm = nullptr;
+    // LoRA in bf16 precision (a frozen bf16 base): the base matrices (embed,
+    // lm_head, the seven projections) are stored in bf16 only, in Pb, and
+    // take the arena offsets below p_lo; P holds fp32 from p_lo on (the norm
+    // gains and the adapters).  Elsewhere p_lo = 0 and everything has fp32.
+    bool fb16 = false;
+    size_t p_lo = 0;
     // bf16 precision: bf16 shadow of P (the GEMM weight operands), refreshed
     // by Adam and re-cast whenever parameters change from the host side
     bf16 *Pb = nullptr;
@@ -233,24 +267,38 @@ struct vkh_runner {
         size_t off = 0;
         auto align = [&]() { off = (off + 63) & ~size_t(63); };
         auto take = [&](Span &s, size_t n) { s.off = off; s.numel = n; off += n; };
+        // fb16: the norm gains go after all matrices (from p_lo on, with fp32)
+        const bool gains_here = !fb16;
         align(); take(embed, (size_t)V * D);
-        align(); take(final_norm, D);
+        if (gains_here) { align(); take(final_norm, D); }
         if (tied) lm_head = embed; else { align(); take(lm_head, (size_t)V * D); }
         ls.assign(L, LayerSpans{});
         for (int l = 0; l < L; ++l) {
             LayerSpans &s = ls[l];
-            align(); take(s.t[0], D);
+            if (gains_here) { align(); take(s.t[0], D); }
             align(); take(s.t[1], (size_t)qd * D);
             take(s.t[2], (size_t)kvd * D);  // k, v directly after q: one [qkvd, D] matrix
             take(s.t[3], (size_t)kvd * D);
             align(); take(s.t[4], (size_t)D * qd);
-            align(); take(s.t[5], D);
+            if (gains_here) { align(); take(s.t[5], D); }
             align(); take(s.t[6], (size_t)F * D);
             take(s.t[7], (size_t)F * D);    // up directly after gate: one [2F, D] matrix
             align(); take(s.t[8], (size_t)D * F);
-            if (cfg.qk_norm) { align(); take(s.t[9], hd); align(); take(s.t[10], hd); }
+            if (gains_here && cfg.qk_norm) { align(); take(s.t[9], hd); align(); take(s.t[10], hd); }
         }
         align();
+        p_lo = 0;
+        if (fb16) {
+            p_lo = off;
+            take(final_norm, D);
+            for (int l = 0; l < L; ++l) {
+                LayerSpans &s = ls[l];
+                align(); take(s.t[0], D);
+                align(); take(s.t[5], D);
+                if (cfg.qk_norm) { align(); take(s.t[9], hd); align(); take(s.t[10], hd); }
+            }
+            align();
+        }
         tb = 0;
         if (lora) {
             // all A tensors, then all B tensors (two Adam spans: lr and lr * b_scale)
@@ -294,12 +342,14 @@ struct vkh_runner {
     }
 
     float *ptr(int kind, const Span &s) const {
-        if (kind == VKH_PARAM) return P + s.off;
+        if (kind == VKH_PARAM) return bf16_only(s) ? nullptr : W(s);
         if (s.off < tb || s.off + s.numel > te) return nullptr;  // not trainable
         float *base = kind == VKH_GRAD ? G : kind == VKH_ADAM_M ? M : Vm;
         return base + (s.off - tb);
     }
-    float *W(const Span &s) const { return P + s.off; }
+    float *Pat(size_t off) const { return P + (off - p_lo); }
+    float *W(const Span &s) const { return Pat(s.off); }
+    bool bf16_only(const Span &s) const { return fb16 && s.numel && s.off < p_lo; }
     const bf16 *Wb(const Span &s) const { return Pb + s.off; }
     bool b16() const { return pr == Precision::BF16; }
     float *Gd(const Span &s) const { return lora ? nullptr : G + (s.off - tb); }
@@ -329,6 +379,7 @@ struct vkh_runner {
         pr = cfg.precision == VKH_PRECISION_BF16 ? Precision::BF16 : Precision::FP32;
         adt = (pr == Precision::BF16 && (hd == 64 || hd == 128)) ? DType::BF16 : DType::F32;
         aor = lora ? cfg.lora_alpha / (float)R : 0.f;
+        fb16 = lora && pr == Precision::BF16;
         qd = H * hd; kvd = Hkv * hd; qkvd = qd + 2 * kvd;
         build_layout();
 
@@ -342,9 +393,12 @@ struct vkh_runner {
         VKH_HIP(hipHostMalloc((void **)&tgt_h, (size_t)T * 4, hipHostMallocDefault));
         VKH_HIP(hipHostMalloc((void **)&loss_h, 16, hipHostMallocDefault));
 
-        VKH_TRY(alloc(P, total));
-        VKH_HIP(hipMemsetAsync(P, 0, total * 4, own));
+        VKH_TRY(alloc(P, total - p_lo));
+        VKH_HIP(hipMemsetAsync(P, 0, (total - p_lo) * 4, own));
         if (b16()) VKH_TRY(alloc(Pb, total));
+        // bf16-only base matrices start at zero like the fp32 ones (the shadow
+        // cast never writes them)
+        if (p_lo) VKH_HIP(hipMemsetAsync(Pb, 0, p_lo * sizeof(bf16), own));
         const size_t nt = te - tb;
         VKH_TRY(alloc(G, nt));
         VKH_TRY(alloc(M, nt));
@@ -354,7 +408,7 @@ struct vkh_runner {
         VKH_HIP(hipMemsetAsync(Vm, 0, nt * 4, own));
         // norm gains start at one
         auto ones = [&](const Span &s) -> vkh_status {
-            if (s.numel) VKH_HIP(fill_f32(P + s.off, s.numel, 1.0f, own));
+            if (s.numel) VKH_HIP(fill_f32(W(s), s.numel, 1.0f, own));
             return VKH_OK;
         };
         VKH_TRY(ones(final_norm));
@@ -556,6 +610,11 @@ struct vkh_runner {
         return s;
     }
 
+    // a bf16-only base matrix from host fp32 values (rounded to nearest even)
+    vkh_status upload_bf16(const Span &s, const float *host) {
+        return write_bf16_rounded(Pb + s.off, s.numel, host);
+    }
+
     vkh_status upload_weights(const vkh_init_weights &w) {
         const size_t qdim = (size_t)qd, kvdim = (size_t)kvd;
         if (w.embed.len != (size_t)V * D) return fail(VKH_ERR_EMBED_SHAPE, "embed len %zu", w.embed.len);
@@ -582,7 +641,9 @@ struct vkh_runner {
             if (proj_lora(p) && w.lora[p] && w.lora_len[p] != (size_t)L)
                 return fail(VKH_ERR_LORA_INIT_LEN, "lora init for projection %d has %zu layers", p, w.lora_len[p]);
         auto up = [&](const Span &s, const vkh_tensor &t) -> vkh_status {
-            if (s.numel && t.data) VKH_HIP(hipMemcpy(P + s.off, t.data, s.numel * 4, hipMemcpyHostToDevice));
+            if (!s.numel || !t.data) return VKH_OK;
+            if (bf16_only(s)) return upload_bf16(s, t.data);
+            VKH_HIP(hipMemcpy(W(s), t.data, s.numel * 4, hipMemcpyHostToDevice));
             return VKH_OK;
         };
         VKH_TRY(up(embed, w.embed));
@@ -617,7 +678,7 @@ struct vkh_runner {
         const float sigma = 1.0f / sqrtf((float)R);
         for (int l = 0; l < L; ++l) {
             const Span &a = ls[l].la[p];
-            hipLaunchKernelGGL(init_normal_k, dim3(256), dim3(256), 0, own, P + a.off, a.numel,
+            hipLaunchKernelGGL(init_normal_k<float>, dim3(256), dim3(256), 0, own, W(a), a.numel,
                                mix(0x10AAFADEull ^ ((uint64_t)p << 32) ^ (uint64_t)l), sigma);
             VKH_HIP(hipGetLastError());
         }
@@ -630,13 +691,17 @@ struct vkh_runner {
         auto normal = [&](const Span &s, uint64_t tag, float sd) -> vkh_status {
             if (!s.numel) return VKH_OK;
             const unsigned g = (unsigned)std::min<size_t>(4096, (s.numel + 255) / 256);
-            hipLaunchKernelGGL(init_normal_k, dim3(g ? g : 1), dim3(256), 0, own, P + s.off, s.numel,
-                               mix(seed ^ mix(tag)), sd);
+            if (bf16_only(s))
+                hipLaunchKernelGGL(init_normal_k<bf16>, dim3(g ? g : 1), dim3(256), 0, own, Pb + s.off,
+                                   s.numel, mix(seed ^ mix(tag)), sd);
+            else
+                hipLaunchKernelGGL(init_normal_k<float>, dim3(g ? g : 1), dim3(256), 0, own, W(s),
+                                   s.numel, mix(seed ^ mix(tag)), sd);
             VKH_HIP(hipGetLastError());
             return VKH_OK;
         };
         auto ones = [&](const Span &s) -> vkh_status {
-            if (s.numel) VKH_HIP(fill_f32(P + s.off, s.numel, 1.0f, own));
+            if (s.numel) VKH_HIP(fill_f32(W(s), s.numel, 1.0f, own));
             return VKH_OK;
         };
         VKH_TRY(normal(embed, 1, std_));
@@ -650,7 +715,7 @@ struct vkh_runner {
         for (int p = 0; p < 7; ++p)
             for (int l = 0; l < L; ++l) {
                 if (ls[l].la[p].numel) VKH_TRY(normal(ls[l].la[p], 500000 + 64 * (uint64_t)p + l, lora_std));
-                if (ls[l].lb[p].numel) VKH_HIP(hipMemsetAsync(P + ls[l].lb[p].off, 0, ls[l].lb[p].numel * 4, own));
+                if (ls[l].lb[p].numel) VKH_HIP(hipMemsetAsync(W(ls[l].lb[p]), 0, ls[l].lb[p].numel * 4, own));
             }
         VKH_HIP(hipStreamSynchronize(own));
         return VKH_OK;
@@ -779,7 +844,7 @@ struct vkh_runner {
 
     vkh_status sync_shadow() {
         if (b16() && shadow_dirty) {
-            VKH_HIP(cast_f32_to_bf16(P, Pb, total, cur));
+            VKH_HIP(cast_f32_to_bf16(P, Pb + p_lo, total - p_lo, cur));
             shadow_dirty = false;
         }
         return VKH_OK;
@@ -834,7 +899,8 @@ struct vkh_runner {
 
     vkh_status forward_all() {
         VKH_TRY(sync_shadow());
-        VKH_HIP(embed_lookup(W(embed), tok_d, x_emb, T, D, 1.0f, cur));
+        if (bf16_only(embed)) VKH_HIP(embed_lookup_bf16(Wb(embed), tok_d, x_emb, T, D, 1.0f, cur));
+        else VKH_HIP(embed_lookup(W(embed), tok_d, x_emb, T, D, 1.0f, cur));
         for (int l = 0; l < L; ++l) VKH_TRY(layer_forward(l));
         VKH_HIP(rmsnorm_forward(acts[L - 1].y, W(final_norm), b16() ? (void *)fn_outb : (void *)fn_out,
                                 b16() ? DType::BF16 : DType::F32, T, D, cfg.rms_eps, 0, cur));
@@ -1154,7 +1220,7 @@ struct vkh_runner {
         const float t = (float)step_t;
         const float bc1 = 1.0f - powf(cfg.beta1, t);
         const float bc2 = 1.0f - powf(cfg.beta2, t);
-        VKH_HIP(adam_step_gains(P + b, G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
+        VKH_HIP(adam_step_gains(Pat(b), G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
                                 cfg.eps_adam, bc1, bc2, 0.f, b16() ? Pb + b : nullptr, gs, side));
         return VKH_OK;
     }
@@ -1195,7 +1261,7 @@ struct vkh_runner {
         const float t = (float)step_t;
         const float bc1 = 1.0f - powf(cfg.beta1, t);
         const float bc2 = 1.0f - powf(cfg.beta2, t);
-        VKH_HIP(adam_step(P + b, G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
+        VKH_HIP(adam_step(Pat(b), G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
                           cfg.eps_adam, bc1, bc2, 0.f, b16() ? Pb + b : nullptr, st));
         return VKH_OK;
     }
@@ -1206,13 +1272,13 @@ struct vkh_runner {
         const float bc2 = 1.0f - powf(cfg.beta2, t);
         bf16 *pb = b16() ? Pb : nullptr;
         if (!lora) {
-            VKH_HIP(adam_step(P, G, M, Vm, total, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2,
+            VKH_HIP(adam_step(Pat(0), G, M, Vm, total, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2,
                               0.f, pb, cur));
         } else {
             const size_t na = lora_b_begin - lora_a_begin, nb = total - lora_b_begin;
-            VKH_HIP(adam_step(P + lora_a_begin, G, M, Vm, na, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam,
+            VKH_HIP(adam_step(Pat(lora_a_begin), G, M, Vm, na, cfg.lr, cfg.beta1, cfg.beta2, cfg.eps_adam,
                               bc1, bc2, 0.f, pb ? pb + lora_a_begin : nullptr, cur));
-            VKH_HIP(adam_step(P + lora_b_begin, G + na, M + na, Vm + na, nb, cfg.lr * cfg.lora_lr_b_scale,
+            VKH_HIP(adam_step(Pat(lora_b_begin), G + na, M + na, Vm + na, nb, cfg.lr * cfg.lora_lr_b_scale,
                               cfg.beta1, cfg.beta2, cfg.eps_adam, bc1, bc2, 0.f,
                               pb ? pb + lora_b_begin : nullptr, cur));
         }
@@ -1367,9 +1433,10 @@ bool shape_matches(const vkh_config &a, const vkh_config &b) {
 }
 
 struct Blob {
-    float *dev;   // nullptr => zeros (m/v of frozen tensors)
+    float *dev;   // nullptr => zeros (m/v of frozen tensors), unless dev16
     size_t numel;
     int alias;    // >= 0: the tied lm_head, the same memory as blob `alias`
+    bf16 *dev16 = nullptr;  // a base matrix stored in bf16 only: widened / rounded
 };
 
 }  // namespace
@@ -1382,7 +1449,8 @@ namespace vkh {
 // embed_tokens into a separate lm_head), so the file loads in the reference.
 static void collect_blobs(vkh_runner *r, std::vector<Blob> &out) {
     auto add3 = [&](const Span &s, int alias) {
-        out.push_back({r->P + s.off, s.numel, alias});
+        if (r->bf16_only(s)) out.push_back({nullptr, s.numel, alias, r->Pb + s.off});
+        else out.push_back({r->W(s), s.numel, alias});
         out.push_back({r->ptr(VKH_ADAM_M, s), s.numel, alias < 0 ? -1 : alias + 1});
         out.push_back({r->ptr(VKH_ADAM_V, s), s.numel, alias < 0 ? -1 : alias + 2});
     };
@@ -1400,10 +1468,10 @@ static void collect_lora_blobs(vkh_runner *r, std::vector<Blob> &out) {
         if (!r->proj_lora(p)) continue;
         for (int l = 0; l < r->L; ++l) {
             const Span &a = r->ls[l].la[p], &b = r->ls[l].lb[p];
-            out.push_back({r->P + a.off, a.numel, -1});
+            out.push_back({r->W(a), a.numel, -1});
             out.push_back({r->ptr(VKH_ADAM_M, a), a.numel, -1});
             out.push_back({r->ptr(VKH_ADAM_V, a), a.numel, -1});
-            out.push_back({r->P + b.off, b.numel, -1});
+            out.push_back({r->W(b), b.numel, -1});
             out.push_back({r->ptr(VKH_ADAM_M, b), b.numel, -1});
             out.push_back({r->ptr(VKH_ADAM_V, b), b.numel, -1});
         }
@@ -1430,6 +1498,9 @@ static vkh_status save_blobs(vkh_runner *r, const char *path, const char magic[4
         if (b.dev) {
             hipError_t e = hipMemcpy(buf.data(), b.dev, b.numel * 4, hipMemcpyDeviceToHost);
             if (e != hipSuccess) { fclose(f); return hip_fail(e, "checkpoint readback"); }
+        } else if (b.dev16) {
+            const vkh_status e = read_bf16_widened(b.dev16, b.numel, buf.data());
+            if (e != VKH_OK) { fclose(f); return e; }
         }
         ok = fwrite(buf.data(), 4, b.numel, f) == b.numel;
     }
@@ -1480,9 +1551,13 @@ static vkh_status load_blobs(vkh_runner *r, const char *path, const char magic[4
                                 "runner ties them");
     if (st != VKH_OK) return st;
     VKH_TRY(r->host_wait());
-    for (size_t i = 0; i < blobs.size(); ++i)
-        if (blobs[i].dev && blobs[i].alias < 0)
+    for (size_t i = 0; i < blobs.size(); ++i) {
+        if (blobs[i].alias >= 0) continue;
+        if (blobs[i].dev)
             VKH_HIP(hipMemcpy(blobs[i].dev, data[i].data(), blobs[i].numel * 4, hipMemcpyHostToDevice));
+        else if (blobs[i].dev16)
+            VKH_TRY(write_bf16_rounded(blobs[i].dev16, blobs[i].numel, data[i].data()));
+    }
     // transformer.zig:1444-1448, :1538-1544
     r->step_t = h.step_t;
     r->cfg.lr = saved.lr;
@@ -1663,11 +1738,13 @@ vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int
 }
 
 static vkh_status tensor_ptr(vkh_runner *r, int kind, int layer, int which, float **dptr,
-                             size_t *numel) {
+                             size_t *numel, bf16 **dptr16 = nullptr) {
     if (!r || !dptr) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
     size_t n = 0;
     VKH_TRY(vkh_runner_tensor_numel(r, kind, layer, which, &n));
-    *dptr = r->ptr(kind, *r->find(layer, which));
+    const Span &s = *r->find(layer, which);
+    *dptr = r->ptr(kind, s);
+    if (dptr16) *dptr16 = kind == VKH_PARAM && r->bf16_only(s) ? r->Pb + s.off : nullptr;
     if (numel) *numel = n;
     return VKH_OK;
 }
@@ -1677,6 +1754,8 @@ static vkh_status tensor_ptr(vkh_runner *r, int kind, int layer, int which, floa
 vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int which,
                                         float **dptr, size_t *numel) {
     VKH_TRY(tensor_ptr(r, kind, layer, which, dptr, numel));
+    if (!*dptr)
+        return fail(VKH_ERR_UNSUPPORTED, "a frozen base matrix of a bf16 LoRA runner has no fp32 copy");
     if (kind == VKH_PARAM) r->shadow_dirty = true;
     return VKH_OK;
 }
@@ -1684,10 +1763,12 @@ vkh_status vkh_runner_tensor_device_ptr(vkh_runner *r, int kind, int layer, int 
 vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, float *host,
                                  size_t numel) {
     float *d = nullptr;
+    bf16 *d16 = nullptr;
     size_t n = 0;
-    VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n));
+    VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n, &d16));
     if (numel != n || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
     VKH_TRY(r->host_wait());
+    if (d16) return read_bf16_widened(d16, n, host);  // bf16-only base matrix
     VKH_HIP(hipMemcpy(host, d, n * 4, hipMemcpyDeviceToHost));
     return VKH_OK;
 }
@@ -1695,10 +1776,12 @@ vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, 
 vkh_status vkh_runner_set_tensor(vkh_runner *r, int kind, int layer, int which,
                                  const float *host, size_t numel) {
     float *d = nullptr;
+    bf16 *d16 = nullptr;
     size_t n = 0;
-    VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n));
+    VKH_TRY(tensor_ptr(r, kind, layer, which, &d, &n, &d16));
     if (numel != n || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
     VKH_TRY(r->host_wait());
+    if (d16) return write_bf16_rounded(d16, n, host);  // bf16-only base matrix
     VKH_HIP(hipMemcpy(d, host, n * 4, hipMemcpyHostToDevice));
     if (kind == VKH_PARAM) r->shadow_dirty = true;
     return VKH_OK;
