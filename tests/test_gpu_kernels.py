@@ -521,6 +521,65 @@ def test_flash_attention_bf16_mfma(case):
     _check_from_o(p, qb, kb, vb, o, dob16, lse_r, dO.size, ws)
 
 
+# n_q != n_kv in bf16 (the reference's causal limit k <= q + (n_kv - n_q),
+# fa_bw_dq.comp / flash_attn.zig:66-68 causalKeyLimit): more keys than queries
+# under the causal mask, and more queries than keys without it; GQA 2:1 and
+# 4:1, head_dim 64 and 128, ragged key tiles.  (Causal with n_q > n_kv is not an
+# input: the reference's limit is unsigned arithmetic and underflows there, and
+# the C ABI refuses it, checked below.)
+FA_BF16_SHIFT_CASES = [  # (n_q, n_kv, H, Hkv, hd, causal, B)
+    (96, 160, 4, 2, 64, True, 1), (64, 192, 8, 2, 128, True, 2), (40, 100, 8, 2, 64, True, 1),
+    (160, 96, 4, 2, 128, False, 1),
+]
+
+
+@pytest.mark.parametrize("case", FA_BF16_SHIFT_CASES)
+def test_flash_attention_bf16_unequal_lengths(case):
+    """bf16 forward and backward through the C ABI with n_q != n_kv against the
+    oracle on the same bf16-rounded Q/K/V/dO (the per-row bf16 kernels take
+    these shapes: the MFMA tile kernels need n_q == n_kv under a causal mask)."""
+    from valkyr_amd import kernels as K
+
+    n_q, n_kv, H, Hkv, hd, causal, B = case
+    note(f"fa bf16 unequal lengths {case}")
+    Q = O.normal(B * n_q * H * hd, 121)
+    Kk = O.normal(B * n_kv * Hkv * hd, 122)
+    Vv = O.normal(B * n_kv * Hkv * hd, 123)
+    dO = O.normal(B * n_q * H * hd, 124, 0.1)
+    qb, Qr = bf16_dev(Q)
+    kb, Kr = bf16_dev(Kk)
+    vb, Vr = bf16_dev(Vv)
+    dob, dOr = bf16_dev(dO)
+    o_r, lse_r, dq_r, dk_r, dv_r = _fa_oracle(Qr, Kr, Vr, dOr, B, n_q, n_kv, H, Hkv, hd, causal)
+    p = K.attn_params(n_q, n_kv, H, Hkv, hd, causal, B, K.BF16)
+    o, lse, d, dq, dk, dv = _run_fa_gpu(p, qb, kb, vb, o_r, dob, dev(dO), lse_r, B, n_q, n_kv, H,
+                                        Hkv, hd)
+    assert max(abs(lse_r - lse)) < 2e-2
+    e = [rel_l2(o_r, o), rel_l2(dq_r, dq), rel_l2(dk_r, dk), rel_l2(dv_r, dv)]
+    note(f"  rel-L2 O={e[0]:.2e} dQ={e[1]:.2e} dK={e[2]:.2e} dV={e[3]:.2e}")
+    assert all(x < BF16_TOL for x in e), e
+    # the one-call backward takes the same shapes
+    ws_bytes = K.fa_backward_workspace_bytes(p)
+    bdq, bdk, bdv = zeros(dq.size), zeros(dk.size), zeros(dv.size)
+    ws = zeros(ws_bytes // 4 + 1) if ws_bytes else None
+    K.fa_backward(p, qb, kb, vb, dob, dev(lse_r), dev(d), bdq, bdk, bdv, ws)
+    f = [rel_l2(dq_r, host(bdq)), rel_l2(dk_r, host(bdk)), rel_l2(dv_r, host(bdv))]
+    note(f"  one-call backward dQ={f[0]:.2e} dK={f[1]:.2e} dV={f[2]:.2e}")
+    assert all(x < BF16_TOL for x in f), f
+
+
+def test_flash_attention_causal_more_queries_than_keys_refused():
+    """Causal attention with n_q > n_kv is refused with InvalidArgument before
+    any launch (the reference's key limit q + (n_kv - n_q) is unsigned)."""
+    from valkyr_amd import VkhError
+    from valkyr_amd import kernels as K
+
+    p = K.attn_params(128, 64, 4, 2, 64, True, 1, K.BF16)
+    q, kv = zeros(128 * 4 * 64), zeros(64 * 2 * 64)
+    with pytest.raises(VkhError, match="InvalidArgument"):
+        K.fa_forward(p, q, kv, kv, zeros(128 * 4 * 64), zeros(128 * 4))
+
+
 def _check_from_o(p, qb, kb, vb, o, dob16, lse, n_do, ws):
     """vkh_fa_backward_from_o (D formed from the bf16 O inside the backward)
     vs the two calls it replaces, fa_bw_d_bf16 then fa_backward, on the same
