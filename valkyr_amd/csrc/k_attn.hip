@@ -1514,14 +1514,14 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
 }
 
 namespace dq4 {
-constexpr int HD = 128, BQ = 256, BN = 32;
+constexpr int HD = 128, BN = 32;
 constexpr int KS = BN / 16, DS = HD / 32, DSUB = HD / 16;
 constexpr int TILE = BN * HD * 2;  // 8 KB: one K or V tile
 constexpr int NBUF = 3;
 }  // namespace dq4
 
-// dQ.  Block = 256 queries of one (sequence, head) on NWV waves (4: one wave
-// per SIMD, 64 queries each; 8: two per SIMD, 32 queries each); wave w owns
+// dQ.  Block = BQ (256 or 128) queries of one (sequence, head) on NWV waves
+// (8: two per SIMD, BQ / 8 queries each); wave w owns
 // the 16-row query sub-tiles Q0 + 16 (NWV j + w), interleaved so that under a
 // causal mask every wave has work until the block's last key tile.  Q and dO
 // of those rows sit in VGPRs as B operands; per 32-key tile (K and V by DMA,
@@ -1535,7 +1535,7 @@ constexpr int NBUF = 3;
 // WITH_D: D = rowsum(O dO) of the block's rows is formed here from bf16 O (the
 // lane's 32 products in fp64, then the row's four lanes) and stored to p.d
 // for the dK/dV kernel, which then runs after this one; no separate pass.
-template <int NWV, bool WITH_D, bool QKE>
+template <int NWV, bool WITH_D, bool QKE, int BQ>
 __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtrs p) {
     using namespace dq4;
     constexpr int QSUB = BQ / 16 / NWV;  // 16-row query sub-tiles per wave
@@ -2218,6 +2218,25 @@ void launch_dkv4(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     else hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 0>), gkv, dim3(W * 64), 0, st, s, p);
 }
 
+// dQ blocks of 256 queries, or of 128 where 256 would leave fewer blocks than
+// CUs: there a causal grid is also short of work at its end, since a block's
+// work grows with its last query (config 3, 4 x 512: 128 blocks of 256 rows,
+// the later block of each sequence twice the earlier)
+int dq4_bq(const AttnShape &s) {
+    const long b256 = (long)s.n_heads * s.n_batch * ((s.n_q + 255) / 256);
+    return b256 < 256 ? 128 : 256;
+}
+template <bool WITH_D, bool QKE>
+void launch_dq4(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
+    constexpr int W = 8;
+    const int bq = dq4_bq(s);
+    const dim3 gq(s.n_heads * s.n_batch, (s.n_q + bq - 1) / bq);
+    if (bq == 128)
+        hipLaunchKernelGGL((fa_bwd_dq4_k<W, WITH_D, QKE, 128>), gq, dim3(W * 64), 0, st, s, p);
+    else
+        hipLaunchKernelGGL((fa_bwd_dq4_k<W, WITH_D, QKE, 256>), gq, dim3(W * 64), 0, st, s, p);
+}
+
 // One of the two recompute kernels alone (D already in p.d): which = 0 the
 // dK/dV kernel, 1 the dQ kernel, so a caller can run them on two streams.
 hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipStream_t st) {
@@ -2236,15 +2255,15 @@ hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipSt
         if (e.out) launch_dkv4<W, true>(s, p, st);
         else launch_dkv4<W, false>(s, p, st);
     } else {
-        const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
-        if (e.out) hipLaunchKernelGGL((fa_bwd_dq4_k<W, false, true>), gq, dim3(W * 64), 0, st, s, p);
-        else hipLaunchKernelGGL((fa_bwd_dq4_k<W, false, false>), gq, dim3(W * 64), 0, st, s, p);
+        if (e.out) launch_dq4<false, true>(s, p, st);
+        else launch_dq4<false, false>(s, p, st);
     }
     return hipGetLastError();
 }
 
 int fa_bw_v4_q_blocks(const AttnShape &s) {
-    return s.n_heads * s.n_batch * ((s.n_q + dq4::BQ - 1) / dq4::BQ);
+    const int bq = dq4_bq(s);
+    return s.n_heads * s.n_batch * ((s.n_q + bq - 1) / bq);
 }
 int fa_bw_v4_kv_blocks(const AttnShape &s) { return s.n_kv_heads * s.n_batch * (s.n_kv / dkv4::BN); }
 // The epilogue's row layout assumes head_dim 128 and a rotary span of 0 or
@@ -2268,8 +2287,7 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
             (long)s.n_kv * std::max(p.ldk, p.ldv) * 2 >= (1l << 31))
             return hipErrorInvalidValue;
         if (p.o16 && (long)s.n_q * p.ldo16 * 2 >= (1l << 31)) return hipErrorInvalidValue;
-        constexpr int DKV_WAVES = 8, DQ_WAVES = 8;
-        const dim3 gq(s.n_heads * s.n_batch, (s.n_q + dq4::BQ - 1) / dq4::BQ);
+        constexpr int DKV_WAVES = 8;
         const QkEpi &e = p.qk;
         if (e.out) {
             // fused q/k epilogue: dQ forms D (needs bf16 O), then dK/dV
@@ -2277,14 +2295,14 @@ hipError_t fa_bw_fused(const AttnShape &s, const AttnPtrs &p, bf16 *ds_ws, bool 
                 ((uintptr_t)e.out & 15) || ((uintptr_t)e.x & 15) || (e.rot && !e.rope) ||
                 (bool)e.gq != (bool)e.gk || (e.gq && (!e.pq || !e.pk)))
                 return hipErrorInvalidValue;
-            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true, true>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            launch_dq4<true, true>(s, p, st);
             launch_dkv4<DKV_WAVES, true>(s, p, st);
         } else if (p.o16) {  // dQ forms D, then dK/dV reads it
-            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, true, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            launch_dq4<true, false>(s, p, st);
             launch_dkv4<DKV_WAVES, false>(s, p, st);
         } else {
             launch_dkv4<DKV_WAVES, false>(s, p, st);
-            hipLaunchKernelGGL((fa_bwd_dq4_k<DQ_WAVES, false, false>), gq, dim3(DQ_WAVES * 64), 0, st, s, p);
+            launch_dq4<false, false>(s, p, st);
         }
         return hipGetLastError();
     }
