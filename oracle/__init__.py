@@ -112,6 +112,10 @@ def _declare(L):
       C.POINTER(C.c_size_t))
     d("orc_model_init_random", None, C.c_void_p, C.c_uint64, C.c_float, C.c_float)
     d("orc_model_forward_backward", C.c_float, C.c_void_p, U32P, U32P)
+    d("orc_model_head_forward_backward", C.c_float, C.c_void_p, F32P, U32P, F32P)
+    d("orc_model_layer_forward_backward", None, C.c_void_p, C.c_int, F32P, F32P, F32P)
+    d("orc_model_embedding_backward", None, C.c_void_p, U32P, F32P)
+    d("orc_model_layer_output", None, C.c_void_p, C.c_int, F32P)
     d("orc_model_adam", None, C.c_void_p)
     d("orc_model_step", C.c_float, C.c_void_p, U32P, U32P)
     d("orc_model_step_t", C.c_uint32, C.c_void_p)
@@ -434,6 +438,36 @@ class Model:
     def forward_backward(self, tokens, targets):
         return lib().orc_model_forward_backward(self._h, np.ascontiguousarray(tokens, np.uint32),
                                                 np.ascontiguousarray(targets, np.uint32))
+
+    # the stages of forward_backward on given inputs (stage-by-stage checks)
+    def head_forward_backward(self, y, targets):
+        """Final norm + CE + their backward from the last layer's output y:
+        returns (loss, gradient at y); writes the final-norm gain and lm_head
+        gradients (tied: kept for embedding_backward)."""
+        y = np.ascontiguousarray(y, np.float32).ravel()
+        d_y = np.empty_like(y)
+        loss = lib().orc_model_head_forward_backward(
+            self._h, y, np.ascontiguousarray(targets, np.uint32), d_y)
+        return loss, d_y
+
+    def layer_forward_backward(self, l, x_in, d_y):
+        """Layer l's forward from x_in and backward from the gradient d_y at
+        its output: writes its gradients, returns the gradient at x_in."""
+        x_in = np.ascontiguousarray(x_in, np.float32).ravel()
+        d_x = np.empty_like(x_in)
+        lib().orc_model_layer_forward_backward(self._h, int(l), x_in,
+                                               np.ascontiguousarray(d_y, np.float32).ravel(), d_x)
+        return d_x
+
+    def layer_output(self, l):
+        """Layer l's output from the last forward (l = -1: the embedding output)."""
+        out = np.empty(self.T * self.cfg.dim, np.float32)
+        lib().orc_model_layer_output(self._h, int(l), out)
+        return out
+
+    def embedding_backward(self, tokens, d_x0):
+        lib().orc_model_embedding_backward(self._h, np.ascontiguousarray(tokens, np.uint32),
+                                           np.ascontiguousarray(d_x0, np.float32).ravel())
 
     def adam(self):
         lib().orc_model_adam(self._h)

@@ -520,11 +520,35 @@ void orc_fa_bw_d(const float *O, const float *dO, size_t n_q, size_t n_heads,
 
 void orc_matmul_nt(float *out, const float *x, const float *W, size_t M, size_t N,
                    size_t K) {
-    /* every output is its own fp32 k-ascending sum: parallel over outputs */
-    const long long MN = (long long)M * (long long)N;
+    /* every output is its own fp32 k-ascending sum: parallel over outputs.
+     * Rows go MM_G at a time over a transposed copy of their x values, so
+     * the MM_G sums of one W row advance together (vectorised across rows,
+     * each still summed in k order). */
+    enum { MM_G = 64 };
+    const size_t ng = M / MM_G;
+    float *xt = malloc((ng ? ng : 1) * K * MM_G * sizeof(float));
 #pragma omp parallel for schedule(static)
-    for (long long i = 0; i < MN; ++i) {
-        const size_t m = (size_t)i / N, n = (size_t)i % N;
+    for (size_t g = 0; g < ng; ++g)
+        for (size_t j = 0; j < MM_G; ++j)
+            for (size_t k = 0; k < K; ++k) xt[(g * K + k) * MM_G + j] = x[(g * MM_G + j) * K + k];
+    const long long tasks = (long long)ng * (long long)N;
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < tasks; ++i) {
+        const size_t g = (size_t)i / N, n = (size_t)i % N;
+        const float *xg = xt + g * K * MM_G, *wr = W + n * K;
+        float acc[MM_G];
+        for (int j = 0; j < MM_G; ++j) acc[j] = 0;
+        for (size_t k = 0; k < K; ++k) {
+            const float w = wr[k];
+            for (int j = 0; j < MM_G; ++j) acc[j] += xg[k * MM_G + j] * w;
+        }
+        for (int j = 0; j < MM_G; ++j) out[(g * MM_G + j) * N + n] = acc[j];
+    }
+    free(xt);
+    const long long rest = (long long)(M - ng * MM_G) * (long long)N;
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < rest; ++i) {
+        const size_t m = ng * MM_G + (size_t)i / N, n = (size_t)i % N;
         const float *xr = x + m * K, *wr = W + n * K;
         float acc = 0;
         for (size_t k = 0; k < K; ++k) acc += xr[k] * wr[k];
@@ -534,21 +558,30 @@ void orc_matmul_nt(float *out, const float *x, const float *W, size_t M, size_t 
 
 void orc_linear_backward(const float *dout, const float *x, const float *W, size_t M,
                          size_t N, size_t K, float *dx, float *dW) {
+    /* LB_G independent outputs rows advance together per streamed row of the
+     * other operand; each output is still its own fp64 sum in the stated order */
+    enum { LB_G = 8 };
     if (dx) {
         /* dx[m,k] = sum_n dout[m,n] W[n,k]; fp64 per output, n ascending
          * (rows of dx are independent). */
+        const size_t nb = (M + LB_G - 1) / LB_G;
 #pragma omp parallel
         {
-            double *acc = malloc(K * sizeof(double));
+            double *acc = malloc(LB_G * K * sizeof(double));
 #pragma omp for schedule(static)
-            for (size_t m = 0; m < M; ++m) {
-                for (size_t k = 0; k < K; ++k) acc[k] = 0;
+            for (size_t b = 0; b < nb; ++b) {
+                const size_t m0 = b * LB_G, mr = m0 + LB_G <= M ? LB_G : M - m0;
+                for (size_t i = 0; i < mr * K; ++i) acc[i] = 0;
                 for (size_t n = 0; n < N; ++n) {
-                    double g = dout[m * N + n];
                     const float *wr = W + n * K;
-                    for (size_t k = 0; k < K; ++k) acc[k] += g * (double)wr[k];
+                    for (size_t r = 0; r < mr; ++r) {
+                        const double g = dout[(m0 + r) * N + n];
+                        double *ar = acc + r * K;
+                        for (size_t k = 0; k < K; ++k) ar[k] += g * (double)wr[k];
+                    }
                 }
-                for (size_t k = 0; k < K; ++k) dx[m * K + k] = (float)acc[k];
+                for (size_t r = 0; r < mr; ++r)
+                    for (size_t k = 0; k < K; ++k) dx[(m0 + r) * K + k] = (float)acc[r * K + k];
             }
             free(acc);
         }
@@ -556,18 +589,24 @@ void orc_linear_backward(const float *dout, const float *x, const float *W, size
     if (dW) {
         /* dW[n,k] += sum_m dout[m,n] x[m,k]; fp64 per output, m ascending
          * (rows of dW are independent). */
+        const size_t nb = (N + LB_G - 1) / LB_G;
 #pragma omp parallel
         {
-            double *acc = malloc(K * sizeof(double));
+            double *acc = malloc(LB_G * K * sizeof(double));
 #pragma omp for schedule(static)
-            for (size_t n = 0; n < N; ++n) {
-                for (size_t k = 0; k < K; ++k) acc[k] = 0;
+            for (size_t b = 0; b < nb; ++b) {
+                const size_t n0 = b * LB_G, nr = n0 + LB_G <= N ? LB_G : N - n0;
+                for (size_t i = 0; i < nr * K; ++i) acc[i] = 0;
                 for (size_t m = 0; m < M; ++m) {
-                    double g = dout[m * N + n];
                     const float *xr = x + m * K;
-                    for (size_t k = 0; k < K; ++k) acc[k] += g * (double)xr[k];
+                    for (size_t r = 0; r < nr; ++r) {
+                        const double g = dout[m * N + n0 + r];
+                        double *ar = acc + r * K;
+                        for (size_t k = 0; k < K; ++k) ar[k] += g * (double)xr[k];
+                    }
                 }
-                for (size_t k = 0; k < K; ++k) dW[n * K + k] += (float)acc[k];
+                for (size_t r = 0; r < nr; ++r)
+                    for (size_t k = 0; k < K; ++k) dW[(n0 + r) * K + k] += (float)acc[r * K + k];
             }
             free(acc);
         }
@@ -579,21 +618,43 @@ void orc_linear_backward(const float *dout, const float *x, const float *W, size
 /* Rows are taken CCE_RB at a time; the logits of a block are formed vocab
  * row by vocab row (z_t[v * nr + r], each an fp64 dot rounded to fp32 as in
  * cce.zig), so the head matrix streams once per block.  The per-row online
- * softmax then walks the chunks exactly as cce.zig does. */
-#define CCE_RB 32
+ * softmax then walks the chunks exactly as cce.zig does.  Within a block, 32
+ * rows' dots advance together over a transposed copy of their h values (32
+ * independent fp64 sums, vectorised across the rows); each is still its own
+ * k-ascending sum, so the values do not depend on the grouping. */
+#define CCE_RB 128
+#define CCE_G 32
 
 static void cce_logits_block(const float *h, const float *w_lm, size_t r0, size_t nr,
                              size_t vocab, size_t dim, float *z_t) {
+    const size_t ng = nr / CCE_G;
+    float *ht = malloc((ng ? ng : 1) * dim * CCE_G * sizeof(float));
+    for (size_t g = 0; g < ng; ++g)
+        for (size_t j = 0; j < CCE_G; ++j) {
+            const float *hr = h + (r0 + g * CCE_G + j) * dim;
+            for (size_t k = 0; k < dim; ++k) ht[(g * dim + k) * CCE_G + j] = hr[k];
+        }
 #pragma omp parallel for schedule(static)
     for (size_t v = 0; v < vocab; ++v) {
         const float *wr = w_lm + v * dim;
-        for (size_t r = 0; r < nr; ++r) {
+        for (size_t g = 0; g < ng; ++g) {
+            const float *hg = ht + g * dim * CCE_G;
+            double s[CCE_G];
+            for (int j = 0; j < CCE_G; ++j) s[j] = 0;
+            for (size_t k = 0; k < dim; ++k) {
+                const double w = (double)wr[k];
+                for (int j = 0; j < CCE_G; ++j) s[j] += (double)hg[k * CCE_G + j] * w;
+            }
+            for (int j = 0; j < CCE_G; ++j) z_t[v * nr + g * CCE_G + j] = (float)s[j];
+        }
+        for (size_t r = ng * CCE_G; r < nr; ++r) {
             const float *hr = h + (r0 + r) * dim;
             double s = 0;
             for (size_t k = 0; k < dim; ++k) s += (double)hr[k] * (double)wr[k];
             z_t[v * nr + r] = (float)s;
         }
     }
+    free(ht);
 }
 
 float orc_cce_forward(const float *h, const float *w_lm, const uint32_t *tgt, size_t n,
@@ -698,13 +759,27 @@ static void cce_backward(const float *h, const float *w_lm, const uint32_t *tgt,
             }
         }
         if (dW) {
+            /* each dW element takes the block's rows in ascending order; 64
+             * columns of a vocabulary row are held in registers across them */
 #pragma omp parallel for schedule(static)
             for (size_t v = 0; v < vocab; ++v) {
                 float *dwr = dW + v * dim;
-                for (size_t r = 0; r < nr; ++r) {
-                    const float dz = z_t[v * nr + r];
+                const float *zr = z_t + v * nr;
+                size_t k0 = 0;
+                for (; k0 + 64 <= dim; k0 += 64) {
+                    float acc[64];
+                    for (int k = 0; k < 64; ++k) acc[k] = dwr[k0 + k];
+                    for (size_t r = 0; r < nr; ++r) {
+                        const float dz = zr[r];
+                        const float *hr = h + (r0 + r) * dim + k0;
+                        for (int k = 0; k < 64; ++k) acc[k] += dz * hr[k];
+                    }
+                    for (int k = 0; k < 64; ++k) dwr[k0 + k] = acc[k];
+                }
+                for (size_t r = 0; r < nr && k0 < dim; ++r) {
+                    const float dz = zr[r];
                     const float *hr = h + (r0 + r) * dim;
-                    for (size_t k = 0; k < dim; ++k) dwr[k] += dz * hr[k];
+                    for (size_t k = k0; k < dim; ++k) dwr[k] += dz * hr[k];
                 }
             }
         }
@@ -1257,20 +1332,22 @@ static void model_forward(orc_model *m, const uint32_t *tokens, scratch_t *sc) {
     m->phase_s[ORC_PHASE_HEAD] += (t1 - t0) + (now_s() - t2);
 }
 
-float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
-                                 const uint32_t *targets) {
+/* The head on the last layer's output y: final RMSNorm, the chunked CE
+ * forward and backward (cce_backward: dh overwritten, dW_lm accumulated into
+ * zero; tied: kept in m->dW_lm_tied for the embedding's sum) and the final
+ * norm's backward, which writes d_y (the gradient at y) and the gain
+ * gradient (transformer.zig:1917-1960). */
+static float head_forward_backward(orc_model *m, const float *y, const uint32_t *targets,
+                                   float *d_y, scratch_t *sc) {
     const orc_model_config *c = &m->cfg;
     float *P = m->arena[ORC_PARAM], *G = m->arena[ORC_GRAD];
     size_t T = m->T, D = c->dim, V = c->vocab_size;
     int lora = c->lora_targets != 0;
-    scratch_t sc[5] = {{0}};
-    model_forward(m, tokens, sc);
-    double t0 = now_s();
+    orc_rmsnorm_forward(y, P + m->final_norm.off, T, D, c->rms_eps, 0, m->fn_out);
     const float *hh = maybe_bf16(m, m->fn_out, T * D, &sc[0]);
     const float *ww = maybe_bf16(m, P + m->lm_head.off, V * D, &sc[1]);
     size_t chunk = V < 1024 ? V : 1024;
     float loss = orc_cce_forward(hh, ww, targets, T, V, D, chunk, 0, 0, m->lse, m->loss_row);
-    /* head backward: cce_backward (dh overwrite, dW_lm accumulate into zero) */
     float *d_fn = malloc(T * D * sizeof(float));
     float *dW_lm = NULL;
     if (!lora) {
@@ -1279,31 +1356,77 @@ float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
         memset(dW_lm, 0, V * D * sizeof(float));
     }
     cce_backward(hh, ww, targets, m->lse, T, V, D, 0, 0, c->bf16_operands != 0, d_fn, dW_lm);
-    float *d_y = malloc(T * D * sizeof(float)), *d_x = malloc(T * D * sizeof(float));
     float *dw_fn = G + m->final_norm.off;
     if (!lora) memset(dw_fn, 0, D * sizeof(float));
-    orc_rmsnorm_backward(d_fn, m->acts[c->n_layers - 1].y, P + m->final_norm.off, T, D,
-                         c->rms_eps, 0, d_y, lora ? NULL : dw_fn);
+    orc_rmsnorm_backward(d_fn, y, P + m->final_norm.off, T, D, c->rms_eps, 0, d_y,
+                         lora ? NULL : dw_fn);
+    free(d_fn);
+    return loss;
+}
+
+/* The embedding gradient from the gradient at the embedding output (the
+ * scatter in position order; tied: plus the head's dW_lm). */
+static void embed_backward(orc_model *m, const uint32_t *tokens, const float *d_x0) {
+    const orc_model_config *c = &m->cfg;
+    if (c->lora_targets) return;
+    float *G = m->arena[ORC_GRAD];
+    size_t T = m->T, D = c->dim, V = c->vocab_size;
+    float *dE = G + m->embed.off;
+    memset(dE, 0, V * D * sizeof(float));
+    orc_embedding_backward(d_x0, tokens, T, V, D, dE);
+    if (c->tied_embeddings) {
+        /* tied: grad = dE (position-order row sums) + dW_lm */
+        const float *dW_lm = m->dW_lm_tied;
+        for (size_t i = 0; i < V * D; ++i) dE[i] = dW_lm[i] + dE[i];
+    }
+}
+
+float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
+                                 const uint32_t *targets) {
+    const orc_model_config *c = &m->cfg;
+    size_t T = m->T, D = c->dim;
+    scratch_t sc[5] = {{0}};
+    model_forward(m, tokens, sc);
+    double t0 = now_s();
+    float *d_y = malloc(T * D * sizeof(float)), *d_x = malloc(T * D * sizeof(float));
+    float loss = head_forward_backward(m, m->acts[c->n_layers - 1].y, targets, d_y, sc);
     double t1 = now_s();
     for (int l = (int)c->n_layers - 1; l >= 0; --l) {
         layer_backward(m, l, l == 0 ? m->x_emb : m->acts[l - 1].y, d_y, d_x, sc);
         float *t = d_y; d_y = d_x; d_x = t;
     }
     double t2 = now_s();
-    if (!lora) {
-        float *dE = G + m->embed.off;
-        memset(dE, 0, V * D * sizeof(float));
-        orc_embedding_backward(d_y, tokens, T, V, D, dE);
-        if (c->tied_embeddings) {
-            /* tied: grad = dE (position-order row sums) + dW_lm */
-            for (size_t i = 0; i < V * D; ++i) dE[i] = dW_lm[i] + dE[i];
-        }
-    }
-    free(d_fn); free(d_y); free(d_x);
+    embed_backward(m, tokens, d_y);
+    free(d_y); free(d_x);
     for (int k = 0; k < 5; ++k) free(sc[k].buf);
     m->phase_s[ORC_PHASE_LAYER_BWD] += t2 - t1;
     m->phase_s[ORC_PHASE_HEAD] += (t1 - t0) + (now_s() - t2);
     return loss;
+}
+
+float orc_model_head_forward_backward(orc_model *m, const float *y, const uint32_t *targets,
+                                      float *d_y) {
+    scratch_t sc[5] = {{0}};
+    float loss = head_forward_backward(m, y, targets, d_y, sc);
+    for (int k = 0; k < 5; ++k) free(sc[k].buf);
+    return loss;
+}
+
+void orc_model_layer_forward_backward(orc_model *m, int l, const float *x_in, const float *d_y,
+                                      float *d_x_in) {
+    scratch_t sc[5] = {{0}};
+    layer_forward(m, l, x_in, sc);
+    layer_backward(m, l, x_in, d_y, d_x_in, sc);
+    for (int k = 0; k < 5; ++k) free(sc[k].buf);
+}
+
+void orc_model_embedding_backward(orc_model *m, const uint32_t *tokens, const float *d_x0) {
+    embed_backward(m, tokens, d_x0);
+}
+
+void orc_model_layer_output(const orc_model *m, int l, float *out) {
+    const float *src = l < 0 ? m->x_emb : m->acts[l].y;
+    memcpy(out, src, m->T * m->cfg.dim * sizeof(float));
 }
 
 static void adam_span(orc_model *m, span sp, float lr) {

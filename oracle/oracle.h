@@ -191,6 +191,21 @@ void orc_model_init_random(orc_model *m, uint64_t seed, float std, float lora_st
 /* forward + CCE loss + backward (grads written, not applied). Returns loss. */
 float orc_model_forward_backward(orc_model *m, const uint32_t *tokens,
                                  const uint32_t *targets);
+/* The stages of orc_model_forward_backward on caller-given inputs (the same
+ * code it runs), for stage-by-stage comparisons: the head on the last layer's
+ * output y (loss returned; writes the gradient at y, the final-norm gain and
+ * lm_head gradients), one layer's forward and backward from its input and the
+ * gradient at its output (writes the layer's gradients and the gradient at
+ * its input; its stored activations are replaced), and the embedding gradient
+ * from the gradient at the embedding output (tied: plus the head's dW_lm from
+ * the last head call). */
+float orc_model_head_forward_backward(orc_model *m, const float *y, const uint32_t *targets,
+                                      float *d_y);
+void orc_model_layer_forward_backward(orc_model *m, int l, const float *x_in, const float *d_y,
+                                      float *d_x_in);
+void orc_model_embedding_backward(orc_model *m, const uint32_t *tokens, const float *d_x0);
+/* Layer l's output y from the last forward (l = -1: the embedding output). */
+void orc_model_layer_output(const orc_model *m, int l, float *out);
 /* Adam over every trainable tensor with t = step_t, then step_t += 1. */
 void orc_model_adam(orc_model *m);
 float orc_model_step(orc_model *m, const uint32_t *tokens, const uint32_t *targets);

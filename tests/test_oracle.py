@@ -680,3 +680,32 @@ def test_bf16_operand_step_sensitivity_floor():
     d16 = max(rel_l2(a, b) for a, b in zip(grads(1, False), grads(1, True)))
     d32 = max(rel_l2(a, b) for a, b in zip(grads(0, False), grads(0, True)))
     assert 3e-3 < d16 < 1e-2 and d32 < 1e-5, (d16, d32)
+
+
+@pytest.mark.parametrize("bf16,tied", [(0, 0), (1, 1)])
+def test_model_stages_compose_to_forward_backward(bf16, tied):
+    """The stage functions (head, one layer, embedding gradient on given
+    inputs) are the code forward_backward runs: chained on a fresh model from
+    the whole run's own layer boundaries they give its loss and every
+    gradient bit for bit (fp32 and the bf16-operand model, tied and untied)."""
+    cfg = dict(dim=128, n_heads=4, n_kv_heads=2, head_dim=32, ff_dim=256, seq_len=32, n_seqs=2,
+               n_layers=3, vocab_size=512, rms_eps=1e-6, causal=1, rotary_dim=32, rope_theta=1e6,
+               qk_norm=1, lr=1e-4, beta1=0.9, beta2=0.999, eps_adam=1e-8, lora_targets=0,
+               lora_rank=0, lora_alpha=0.0, lora_lr_b_scale=1.0, tied_embeddings=tied,
+               bf16_operands=bf16)
+    L, T = 3, 64
+    tok, tgt = O.ids(T, 41, 512), O.ids(T, 42, 512)
+    a, b = O.Model(**cfg), O.Model(**cfg)
+    for m in (a, b):
+        m.init_random(17, std=0.02)
+    loss = a.forward_backward(tok, tgt)
+    xs = [a.layer_output(l - 1) for l in range(L + 1)]  # x(l): input of layer l; x(L): head input
+    loss_b, g = b.head_forward_backward(xs[L], tgt)
+    assert loss_b == loss
+    for l in range(L - 1, -1, -1):
+        g = b.layer_forward_backward(l, xs[l], g)
+    b.embedding_backward(tok, g)
+    keys = [(-1, 0), (-1, 1)] + ([] if tied else [(-1, 2)]) + \
+        [(l, w) for l in range(L) for w in range(11)]
+    for k in keys:
+        assert np.array_equal(a.tensor(1, *k), b.tensor(1, *k)), k
