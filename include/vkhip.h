@@ -223,6 +223,25 @@ typedef enum vkh_attn_bw_path {
     VKH_ATTN_BW_RECOMPUTE = 2
 } vkh_attn_bw_path;
 uint32_t vkh_runner_attention_backward_path(const vkh_runner *r);
+/* The step's attention-backward launch plan (introspection for tests and
+ * tuning; the reference has no counterpart): out[0] the path as above,
+ * out[1] query rows per dQ block (128, or 256 where that still gives at least
+ * one block per CU), out[2] dQ blocks, out[3] dK/dV blocks, out[4] 1 when
+ * RoPE^T and the Q/K-norm backward run in the kernels' epilogues.  out[1..4]
+ * are 0 off the recompute path. */
+vkh_status vkh_runner_attention_backward_plan(const vkh_runner *r, uint32_t out[5]);
+
+/* Stage-by-stage test introspection (the reference has no counterpart).
+ * With capture on, every forward/backward keeps the gradient of the loss at
+ * each layer boundary: L + 1 fp32 [T, dim] tensors, allocated when capture is
+ * first turned on.  vkh_runner_boundary_read copies boundary l in [0, L]:
+ * which = 0 the residual-stream tensor there (l = 0 the embedding output,
+ * 0 < l <= L the output of layer l - 1, so l = L is the head's input), which
+ * = 1 the gradient at it from the last backward run with capture on.
+ * Blocking. */
+vkh_status vkh_runner_set_boundary_capture(vkh_runner *r, uint32_t on);
+vkh_status vkh_runner_boundary_read(vkh_runner *r, uint32_t l, uint32_t which, float *dst,
+                                    size_t numel);
 
 /* Tensor access (host <-> device copies, blocking).  A LoRA runner in bf16
  * precision keeps its frozen base matrices (embed, lm_head, q..down) in bf16
@@ -260,7 +279,10 @@ vkh_status vkh_runner_load_lora_checkpoint(vkh_runner *r, const char *path);
  * 32 rms_eps (f32); 36 rotary_dim (u32); 40 rope_theta, 44 lr, 48 beta1,
  * 52 beta2, 56 eps_adam (f32); 60 lora_targets, 64 lora_rank (u32);
  * 68 lora_alpha, 72 lora_lr_b_scale (f32); 76 causal, 77 qk_norm (bool, one
- * byte); 78-79 padding (written as zero).  Host-only: no device work.
+ * byte); 78-79 padding (written as zero).  That order is inferred from the
+ * Zig compiler's auto-layout rules (the reference's `Config` is not extern,
+ * transformer.zig:190-193) and is unpinned against any reference-written
+ * file.  Host-only: no device work.
  * decode fills the reference's fields and sets the extensions to n_seqs = 1,
  * untied, fp32 precision. */
 #define VKH_CHECKPOINT_CONFIG_BYTES 80
@@ -572,6 +594,40 @@ typedef struct vkh_cce_params {
 vkh_status vkh_cce_forward(const vkh_cce_params *p, const float *h, const float *w,
                            const uint32_t *targets, float *lse, float *loss_row,
                            float *loss_mean, vkh_stream stream);
+/* One adapter of a grouped LoRA call: output columns [col, col + n) of the
+ * group's fused y / dy, input width k, the fp32 factors and per-adapter
+ * buffers. */
+typedef struct vkh_lora_adapter {
+    uint32_t col, n, k;
+    const float *a;  /* A [r, k] */
+    const float *b;  /* B [n, r] */
+    float *inter;    /* x A^T [T, r]: written by the forward, read by the backward */
+    float *dyb;      /* dy B [T, r]: written by the backward */
+    float *da;       /* dA [r, k] (overwrite) */
+    float *db;       /* dB [n, r] (overwrite) */
+} vkh_lora_adapter;
+
+/* train/lora.zig:99-129 (forward) and :137-251 (backward) for up to three
+ * adapters that share one bf16 activation, launched as the training step
+ * launches them on its fused projections (q/k/v on the first norm's output,
+ * gate/up on the second's, o and down alone): x and dy are bf16 [T, *] with
+ * leading dimensions ldx / lddy (in elements), factors, intermediates and
+ * products fp32, fixed summation order.  Forward: inter = x A^T and
+ * y[:, col..col+n) += aor inter B^T.  Backward: dyb = dy B, dx += aor dyb A
+ * (dx may be NULL), dA = aor dyb^T x, dB = aor dy^T inter.  The rank-r
+ * kernels need r a multiple of 4 up to 64, 16-byte aligned rows, and k, n
+ * and col multiples of the kernels' column groups; other shapes return
+ * VKH_ERR_UNSUPPORTED.  The reference has no grouped call: each adapter is
+ * its lora.zig call. */
+vkh_status vkh_lora_group_forward_bf16(const uint16_t *x, uint32_t ldx, uint32_t T, uint32_t r,
+                                       float aor, const vkh_lora_adapter *adapters,
+                                       uint32_t n_adapters, float *y, uint32_t ldy,
+                                       vkh_stream stream);
+vkh_status vkh_lora_group_backward_bf16(const uint16_t *dy, uint32_t lddy, const uint16_t *x,
+                                        uint32_t ldx, uint32_t T, uint32_t r, float aor,
+                                        const vkh_lora_adapter *adapters, uint32_t n_adapters,
+                                        float *dx, uint32_t lddx, vkh_stream stream);
+
 /* shaders/cce_backward_dh.comp + cce_backward_dw.comp in one pass:
  * dh overwritten (if non-NULL); dw += (accumulate_dw) or = dz^T h (if non-NULL). */
 vkh_status vkh_cce_backward(const vkh_cce_params *p, const float *h, const float *w,
@@ -591,12 +647,23 @@ vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w,
  * forbid hipMalloc).  Same kernels and results (bit for bit); the gain-gradient
  * partials live in a fixed 8 MiB per-device array inside the library instead
  * of memory it allocates, so the call allocates nothing.  Limit: dim <= 4096
- * (VKH_ERR_UNSUPPORTED beyond).  Calls on one GPU share that array: calls that
- * may overlap in time on one GPU (different streams without ordering) race. */
+ * (VKH_ERR_UNSUPPORTED beyond).  Calls on one GPU share that array and are
+ * ordered on the device like the allocating form's scratch uses (a call on
+ * another stream waits for the previous call), except while the caller's
+ * stream is being captured into a graph: there the captured launch is not
+ * ordered against other uses of the array, and the caller must not run the
+ * graph while another call on the same GPU may still be in flight (they
+ * race). */
 vkh_status vkh_rmsnorm_backward_noalloc(const float *dy, const float *x, const float *w,
                                         float *dx, const float *residual, float *dw,
                                         uint32_t n_rows, uint32_t dim, float eps,
                                         uint32_t gemma_quirk, vkh_stream stream);
+/* No counterpart in the reference (test introspection): the number of
+ * allocations this library has made in the process so far (device and pinned
+ * host memory, and leases of the shared scratch buffer that the standalone
+ * entry points use), so a test can check that an entry point allocates
+ * nothing. */
+uint64_t vkh_allocation_count(void);
 /* shaders/swiglu_forward.comp / swiglu_backward.comp (SwigluPush {n}) */
 vkh_status vkh_swiglu_forward(const float *pre_gate, const float *up, float *gated, size_t n,
                               vkh_stream stream);

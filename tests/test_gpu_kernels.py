@@ -335,6 +335,62 @@ def test_lora_forward_backward(prec, shape):
         assert e["inter"] < 1e-5 and e["dA"] < 1e-5 and e["dB"] < 1e-5, e
 
 
+# The fused projection groups of one decoder layer with adapters on every
+# projection (LoraTarget.all): (input width k, output width n of each adapter)
+# at dim 256, 4 query / 2 KV heads of 64, FFN 768.
+LORA_GROUPS = {"qkv": (256, [256, 128, 128]), "o": (256, [256]), "gate_up": (256, [768, 768]),
+               "down": (768, [256])}
+
+
+@pytest.mark.parametrize("group", list(LORA_GROUPS))
+def test_lora_group_bf16_matches_oracle(group):
+    """The training step's grouped bf16 LoRA launches (the runner's segment
+    lists and kernel instantiations, through vkh_lora_group_*_bf16) against
+    the oracle's lora.zig restatement on identical inputs: x and dy are the
+    bf16 values the step's kernels read, the factors are non-zero (a step-2
+    state), and factors, intermediates and products are fp32 on both sides,
+    so the rounding points match and only the summation order differs:
+    inter, y, dyb-derived dx, dA and dB within 1e-5."""
+    from valkyr_amd import kernels as K
+
+    T, r, aor = 128, 16, 2.0
+    k, ns = LORA_GROUPS[group]
+    ntot = sum(ns)
+    cols = [sum(ns[:i]) for i in range(len(ns))]
+    note(f"lora group {group}: k={k} n={ns} T={T} r={r}")
+    x16, xr = bf16_dev(O.normal(T * k, 301))
+    dy16, dyr = bf16_dev(O.normal(T * ntot, 302, 0.1))
+    fa = [O.normal(r * k, 303 + i, 0.05) for i in range(len(ns))]
+    fb = [O.normal(n * r, 313 + i, 0.05) for i, n in enumerate(ns)]
+    bufs = [dict(col=c, n=n, k=k, a=dev(a), b=dev(b), inter=zeros(T * r), dyb=zeros(T * r),
+                 da=zeros(r * k), db=zeros(n * r))
+            for c, n, a, b in zip(cols, ns, fa, fb)]
+    ad = K.lora_adapters(bufs)
+    by, bdx = zeros(T * ntot), zeros(T * k)
+    K.lora_group_forward_bf16(x16, k, T, r, aor, ad, by, ntot)
+    K.lora_group_backward_bf16(dy16, ntot, x16, k, T, r, aor, ad, bdx, k)
+    y = host(by).reshape(T, ntot)
+    dx = host(bdx)
+    dx_ref = np.zeros(T * k, np.float64)
+    dy2 = dyr.reshape(T, ntot)
+    errs = {}
+    for i, (c, n) in enumerate(zip(cols, ns)):
+        dyi = np.ascontiguousarray(dy2[:, c:c + n]).ravel()
+        y_ref, inter_ref = O.lora_forward(xr, np.zeros(n * k, np.float32), fa[i], fb[i], T, n, k,
+                                          r, aor)
+        dxi, da_ref, db_ref = O.lora_backward(dyi, xr, np.zeros(n * k, np.float32), fa[i], fb[i],
+                                              inter_ref, T, n, k, r, aor)
+        dx_ref += dxi
+        b = bufs[i]
+        errs[f"inter{i}"] = rel_l2(inter_ref, host(b["inter"]))
+        errs[f"y{i}"] = rel_l2(y_ref, y[:, c:c + n])
+        errs[f"dA{i}"] = rel_l2(da_ref, host(b["da"]))
+        errs[f"dB{i}"] = rel_l2(db_ref, host(b["db"]))
+    errs["dx"] = rel_l2(dx_ref, dx)
+    note("  " + " ".join(f"{n}={e:.1e}" for n, e in errs.items()))
+    assert all(e < 1e-5 for e in errs.values()), errs
+
+
 def test_lora_b_zero_gives_zero_dA_on_gpu():
     from valkyr_amd import kernels as K
 
@@ -605,6 +661,53 @@ def _check_from_o(p, qb, kb, vb, o, dob16, lse, n_do, ws):
     note(f"  from_o vs two calls: D={e[0]:.1e} dQ={e[1]:.1e} dK={e[2]:.1e} dV={e[3]:.1e}")
     assert e[0] < 1e-6 and rel_l2(d_np, host(d_ref)) < 1e-6
     assert all(x < 1e-5 for x in e[1:]), e
+
+
+def test_flash_attention_bf16_config3_shape():
+    """Config 3's attention shape (B = 4 x S = 512, 16/8 heads, hd 128, causal)
+    through the one vkh_fa_backward_from_o call the step makes (the recompute
+    kernels: D formed by the dQ kernel from the bf16 O, 128-query dQ blocks,
+    no workspace) against the oracle on the same bf16 Q/K/V/dO/O: dQ/dK/dV
+    within the bf16 bar of the fp32 oracle, within 1e-4 of its bf16-operand
+    model (P and dS rounded where the MFMAs take them), D to fp64-dot
+    accuracy."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import bf16_bits_to_f32
+
+    B, n, H, Hkv, hd = 4, 512, 16, 8, 128
+    note("fa bf16 config-3 shape, one-call backward from O")
+    Q = O.normal(B * n * H * hd, 131)
+    Kk = O.normal(B * n * Hkv * hd, 132)
+    Vv = O.normal(B * n * Hkv * hd, 133)
+    dO = O.normal(B * n * H * hd, 134, 0.1)
+    qb, Qr = bf16_dev(Q)
+    kb, Kr = bf16_dev(Kk)
+    vb, Vr = bf16_dev(Vv)
+    dob16, dOr = bf16_dev(dO)
+    p = K.attn_params(n, n, H, Hkv, hd, True, B, K.BF16)
+    assert K.fa_backward_workspace_bytes(p) == 0  # the recompute kernels
+    o_r, lse_r, dq_r, dk_r, dv_r = _fa_oracle(Qr, Kr, Vr, dOr, B, n, n, H, Hkv, hd, True)
+    # the backward reads O in bf16: the oracle's models take the same values
+    o16, o16_r = bf16_dev(o_r)
+    d_ref = O.fa_bw_d(o16_r, dOr, B * n, H, hd)
+    bd, bdq, bdk, bdv = zeros(B * n * H), zeros(Q.size), zeros(Kk.size), zeros(Kk.size)
+    K.fa_backward_from_o(p, qb, kb, vb, o16, dob16, dev(lse_r), bd, bdq, bdk, bdv, None)
+    d, dq, dk, dv = host(bd), host(bdq), host(bdk), host(bdv)
+    assert rel_l2(d_ref, d) < 1e-6, rel_l2(d_ref, d)
+    e = [rel_l2(dq_r, dq), rel_l2(dk_r, dk), rel_l2(dv_r, dv)]
+    note(f"  vs the fp32 oracle dQ={e[0]:.2e} dK={e[1]:.2e} dV={e[2]:.2e}")
+    assert all(x < BF16_TOL for x in e), e
+    m16 = []
+    for b in range(B):
+        sq = slice(b * n * H * hd, (b + 1) * n * H * hd)
+        sk = slice(b * n * Hkv * hd, (b + 1) * n * Hkv * hd)
+        m16.append(O.flash_backward(Qr[sq], Kr[sk], Vr[sk], o16_r[sq], dOr[sq],
+                                    lse_r[b * n * H:(b + 1) * n * H], n, n, H, Hkv, hd, True,
+                                    bf16_ops=True))
+    dq16, dk16, dv16 = (np.concatenate([x[i] for x in m16]) for i in range(3))
+    e16 = [rel_l2(dq16, dq), rel_l2(dk16, dk), rel_l2(dv16, dv)]
+    note(f"  vs the bf16-operand oracle dQ={e16[0]:.2e} dK={e16[1]:.2e} dV={e16[2]:.2e}")
+    assert all(x < 1e-4 for x in e16), e16
 
 
 def _kv_numel(p):

@@ -87,6 +87,12 @@ class AttnParams(C.Structure):
                 ("causal", C.c_uint32), ("inv_sqrt_dim", C.c_float), ("dtype", C.c_uint32)]
 
 
+class LoraAdapter(C.Structure):
+    _fields_ = [("col", C.c_uint32), ("n", C.c_uint32), ("k", C.c_uint32),
+                ("a", C.c_void_p), ("b", C.c_void_p), ("inter", C.c_void_p), ("dyb", C.c_void_p),
+                ("da", C.c_void_p), ("db", C.c_void_p)]
+
+
 class CceParams(C.Structure):
     _fields_ = [("n", C.c_uint32), ("vocab", C.c_uint32), ("dim", C.c_uint32),
                 ("z_loss_scale", C.c_float), ("label_smoothing", C.c_float),
@@ -158,6 +164,9 @@ SIGNATURES = [
     ("vkh_runner_save_lora_checkpoint", ST, [P, C.c_char_p]),
     ("vkh_runner_load_lora_checkpoint", ST, [P, C.c_char_p]),
     ("vkh_runner_attention_backward_path", U32, [P]),
+    ("vkh_runner_attention_backward_plan", ST, [P, C.POINTER(C.c_uint32 * 5)]),
+    ("vkh_runner_set_boundary_capture", ST, [P, U32]),
+    ("vkh_runner_boundary_read", ST, [P, U32, U32, P, SZ]),
     ("vkh_checkpoint_config_encode", ST, [C.POINTER(Config), P, SZ]),
     ("vkh_checkpoint_config_decode", ST, [P, SZ, C.POINTER(Config)]),
     ("vkh_runner_upload_train_batch", ST, [P, P, SZ, P, SZ]),
@@ -214,11 +223,14 @@ SIGNATURES = [
     ("vkh_linear_backward_dw_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_lora_forward", ST, [P, P, P, P, P, P, U32, U32, U32, U32, F, U32, P]),
     ("vkh_lora_backward", ST, [P, P, P, P, P, P, P, P, P, U32, U32, U32, U32, F, U32, P]),
+    ("vkh_lora_group_forward_bf16", ST, [P, U32, U32, U32, F, C.POINTER(LoraAdapter), U32, P, U32, P]),
+    ("vkh_lora_group_backward_bf16", ST, [P, U32, P, U32, U32, U32, F, C.POINTER(LoraAdapter), U32, P, U32, P]),
     ("vkh_cce_forward", ST, [C.POINTER(CceParams), P, P, P, P, P, P, P]),
     ("vkh_cce_backward", ST, [C.POINTER(CceParams), P, P, P, P, P, P, U32, P]),
     ("vkh_rmsnorm_forward", ST, [P, P, P, U32, U32, F, U32, P]),
     ("vkh_rmsnorm_backward", ST, [P, P, P, P, P, P, U32, U32, F, U32, P]),
     ("vkh_rmsnorm_backward_noalloc", ST, [P, P, P, P, P, P, U32, U32, F, U32, P]),
+    ("vkh_allocation_count", C.c_uint64, []),
     ("vkh_swiglu_forward", ST, [P, P, P, SZ, P]),
     ("vkh_swiglu_backward", ST, [P, P, P, P, P, SZ, P]),
     ("vkh_qk_rope_forward", ST, [C.POINTER(RopeParams), P, P, P, P, P]),

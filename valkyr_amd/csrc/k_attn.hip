@@ -2265,6 +2265,7 @@ int fa_bw_v4_q_blocks(const AttnShape &s) {
     const int bq = dq4_bq(s);
     return s.n_heads * s.n_batch * ((s.n_q + bq - 1) / bq);
 }
+int fa_bw_v4_q_rows(const AttnShape &s) { return dq4_bq(s); }
 int fa_bw_v4_kv_blocks(const AttnShape &s) { return s.n_kv_heads * s.n_batch * (s.n_kv / dkv4::BN); }
 // The epilogue's row layout assumes head_dim 128 and a rotary span of 0 or
 // the whole head (pairs 64 apart).

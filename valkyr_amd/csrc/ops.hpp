@@ -81,6 +81,25 @@ hipError_t lora_update(float *y, long ldy, int T, int r, const LoraSegs &g, floa
 bool lora_fast_ok(DType xt, const void *x, long ldx, int r, const LoraSegs &g);
 bool lora_update_ok(const float *y, long ldy, int r, const LoraSegs &g);
 
+// One projection group's adapters (train/lora.zig:99-251 for each): up to
+// three adapters that read one activation x [T, k] and own column blocks
+// [col, col + n) of the group's fused output y / gradient dy.
+struct LoraAdapter {
+    long col = 0;
+    int n = 0, k = 0;
+    const float *a = nullptr, *b = nullptr;  // A [r, k], B [n, r]
+    float *inter = nullptr;                  // x A^T [T, r]
+    float *dyb = nullptr;                    // dy B [T, r]
+    float *da = nullptr, *db = nullptr;      // gradients (overwrite)
+};
+// The segment lists the group's launches take: forward rows (inter = x A^T)
+// and update (y += aor inter B^T); backward rows (dyb = dy B), update
+// (dx += aor dyb A), dA = aor dyb^T x and dB = aor dy^T inter.
+struct LoraGroupSegs {
+    LoraSegs fwd_rows, fwd_upd, bwd_rows, bwd_upd, bwd_da, bwd_db;
+};
+LoraGroupSegs lora_group_segs(const LoraAdapter *ad, int na, int r);
+
 // bf16-output forward GEMM (used for LoRA intermediates and bf16 copies)
 hipError_t gemm_nt_bf16out(Mat x, Mat w, bf16 *y, long ldy, int M, int N, int K, float alpha,
                            hipStream_t st);
@@ -269,6 +288,7 @@ bool fa_bw_v4_preferred(const AttnShape &s);
 // kernel: k gains), and whether a shape / rotary_dim can take it.
 hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipStream_t st);
 int fa_bw_v4_q_blocks(const AttnShape &s);
+int fa_bw_v4_q_rows(const AttnShape &s);  // query rows per dQ block
 int fa_bw_v4_kv_blocks(const AttnShape &s);
 bool fa_bw_qk_epi_ok(const AttnShape &s, int rotary_dim);
 size_t fa_bw_ws_bytes(const AttnShape &s, bool v4);

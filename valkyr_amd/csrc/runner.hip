@@ -196,6 +196,10 @@ struct vkh_runner {
     // the tick API's gate, each with its own event
     hipEvent_t upload_done = nullptr, loss_ready = nullptr, tick_loss_ready = nullptr;
     hipStream_t own = nullptr, cur = nullptr;
+    // boundary capture (test introspection): the gradient at each layer
+    // boundary l = 0..L from the last backward, (L + 1) x [T, D] fp32
+    float *bnd_grad = nullptr;
+    bool bnd_capture = false;
     // Ordering across streams: every enqueue ends by recording ev_done on the
     // stream it used; an enqueue on another stream first waits for it, and
     // host-side reads and writes of runner memory wait for it.
@@ -240,6 +244,7 @@ struct vkh_runner {
     vkh_status alloc(T_ *&p, size_t count) {
         const size_t bytes = count * sizeof(T_) + 256;
         void *q = nullptr;
+        note_allocation();
         hipError_t e = hipMalloc(&q, bytes);
         if (e != hipSuccess)
             return fail(VKH_ERR_OUT_OF_MEMORY, "hipMalloc(%zu bytes) failed: %s", bytes,
@@ -389,6 +394,7 @@ struct vkh_runner {
         VKH_HIP(hipEventCreateWithFlags(&loss_ready, hipEventDisableTiming));
         VKH_HIP(hipEventCreateWithFlags(&tick_loss_ready, hipEventDisableTiming));
         VKH_HIP(hipEventCreateWithFlags(&ev_done, hipEventDisableTiming));
+        note_allocation();
         VKH_HIP(hipHostMalloc((void **)&tok_h, (size_t)T * 4, hipHostMallocDefault));
         VKH_HIP(hipHostMalloc((void **)&tgt_h, (size_t)T * 4, hipHostMallocDefault));
         VKH_HIP(hipHostMalloc((void **)&loss_h, 16, hipHostMallocDefault));
@@ -742,18 +748,30 @@ struct vkh_runner {
     // input x: inter_p = x A_p^T (one launch), then, with need_y, y[:, col_p
     // ..] += aor inter_p B_p^T (one launch); the rank-r kernels where the
     // shapes allow, else the general GEMMs per projection.
-    vkh_status lora_fwd_group(int l, std::initializer_list<int> ps, Mat x, float *y, long ldy,
-                              bool need_y = true) {
-        LoraSegs sa, sb;
+    // The adapters of layer l among projections ps (one group of the fused layout).
+    int lora_adapters(int l, std::initializer_list<int> ps, LoraAdapter (&ad)[3]) {
+        int na = 0;
         for (int p : ps) {
             if (!proj_lora(p)) continue;
-            int N, K;
-            proj_shape(p, N, K);
-            float *inter = acts[l].inter[p];
-            sa.s[sa.n++] = LoraSeg{0, K, W(ls[l].la[p]), 1, (long)K, inter, (long)R};
-            sb.s[sb.n++] = LoraSeg{proj_col(p), N, W(ls[l].lb[p]), (long)R, 1, inter, (long)R};
+            LoraAdapter &a = ad[na++];
+            proj_shape(p, a.n, a.k);
+            a.col = proj_col(p);
+            a.a = W(ls[l].la[p]);
+            a.b = W(ls[l].lb[p]);
+            a.inter = acts[l].inter[p];
+            a.dyb = dyB + (size_t)p * T * R;
+            a.da = G + (ls[l].la[p].off - tb);
+            a.db = G + (ls[l].lb[p].off - tb);
         }
-        if (!sa.n) return VKH_OK;
+        return na;
+    }
+    vkh_status lora_fwd_group(int l, std::initializer_list<int> ps, Mat x, float *y, long ldy,
+                              bool need_y = true) {
+        LoraAdapter ad[3];
+        const int na = lora_adapters(l, ps, ad);
+        if (!na) return VKH_OK;
+        const LoraGroupSegs gs = lora_group_segs(ad, na, R);
+        const LoraSegs &sa = gs.fwd_rows, &sb = gs.fwd_upd;
         if (lora_fast_ok(x.dt, x.p, x.ld, R, sa) && (!need_y || lora_update_ok(y, ldy, R, sb))) {
             VKH_HIP(lora_rows(x.dt, x.p, x.ld, T, R, sa, 1.f, cur));
             if (need_y) VKH_HIP(lora_update(y, ldy, T, R, sb, aor, cur));
@@ -929,20 +947,11 @@ struct vkh_runner {
     // one launch each on the rank-r kernels where the shapes allow.
     vkh_status lora_bwd_group(int l, std::initializer_list<int> ps, Mat dy, Mat x, float *dxo,
                               long lddx) {
-        LoraSegs sb, sa, sda, sdb;
-        for (int p : ps) {
-            if (!proj_lora(p)) continue;
-            int N, K;
-            proj_shape(p, N, K);
-            float *db = dyB + (size_t)p * T * R;
-            float *dA = G + (ls[l].la[p].off - tb), *dB = G + (ls[l].lb[p].off - tb);
-            sb.s[sb.n++] = LoraSeg{proj_col(p), N, W(ls[l].lb[p]), (long)R, 1, db, (long)R};
-            sa.s[sa.n++] = LoraSeg{0, K, W(ls[l].la[p]), 1, (long)K, db, (long)R};
-            sda.s[sda.n++] = LoraSeg{0, K, nullptr, 1, 1, db, (long)R, dA, 1, (long)K};
-            sdb.s[sdb.n++] = LoraSeg{proj_col(p), N, nullptr, 1, 1, acts[l].inter[p], (long)R, dB,
-                                     (long)R, 1};
-        }
-        if (!sb.n) return VKH_OK;
+        LoraAdapter ad[3];
+        const int na = lora_adapters(l, ps, ad);
+        if (!na) return VKH_OK;
+        const LoraGroupSegs gs = lora_group_segs(ad, na, R);
+        const LoraSegs &sb = gs.bwd_rows, &sa = gs.bwd_upd, &sda = gs.bwd_da, &sdb = gs.bwd_db;
         if (lora_fast_ok(dy.dt, dy.p, dy.ld, R, sb) && lora_fast_ok(x.dt, x.p, x.ld, R, sda) &&
             lora_fast_ok(dy.dt, dy.p, dy.ld, R, sdb) && (!dxo || lora_update_ok(dxo, lddx, R, sa))) {
             VKH_HIP(lora_rows(dy.dt, dy.p, dy.ld, T, R, sb, 1.f, cur));
@@ -1115,6 +1124,13 @@ struct vkh_runner {
         return VKH_OK;
     }
 
+    vkh_status capture_boundary(int l, const float *g) {
+        if (!bnd_capture) return VKH_OK;
+        VKH_HIP(hipMemcpyAsync(bnd_grad + (size_t)l * T * D, g, (size_t)T * D * 4,
+                               hipMemcpyDeviceToDevice, cur));
+        return VKH_OK;
+    }
+
     // with_adam: the concurrent mode applies Adam inside the backward (per layer
     // on the side stream); otherwise the caller enqueues adam_enqueue() after.
     vkh_status forward_backward_enqueue(bool with_adam) {
@@ -1152,6 +1168,7 @@ struct vkh_runner {
         VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), dx[0],
                                  concurrent ? lg[L - 1].dyb : dxb[0], nullptr, Gd(final_norm),
                                  partial, T, D, cfg.rms_eps, 0, cur));
+        VKH_TRY(capture_boundary(L, dx[0]));
         int c = 0;
         for (int l = L - 1; l >= 0; --l) {
             if (recompute) {
@@ -1172,6 +1189,7 @@ struct vkh_runner {
             } else {
                 VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
             }
+            VKH_TRY(capture_boundary(l, dx[c ^ 1]));
             c ^= 1;
         }
         // the adapters' last gradients before Adam and the next forward
@@ -1387,7 +1405,9 @@ static_assert(sizeof(CkptHeader) == 16, "checkpoint header is 16 bytes");
 // Zig struct: the compiler orders its fields by descending alignment, keeping
 // declaration order among equals, so the nineteen 4-byte fields come first in
 // declaration order, then the two bools (causal, qk_norm), then two bytes of
-// padding: @sizeOf(Config) = 80.  Padding is written as zero.
+// padding: @sizeOf(Config) = 80.  Padding is written as zero.  The order is
+// inferred from those rules, not checked against a reference-written file
+// (none exists); this encoder and zig_cfg_decode are the only places it lives.
 constexpr uint32_t kZigCfgSize = 80;
 
 void put32(uint8_t *p, uint32_t v) { memcpy(p, &v, 4); }
@@ -1667,6 +1687,7 @@ vkh_status vkh_runner_forward_logits(vkh_runner *r, const uint32_t *token_ids, s
     if (s == VKH_OK) s = se;
     if (s != VKH_OK) return s;
     float *logits = nullptr;
+    note_allocation();
     VKH_HIP(hipMallocAsync((void **)&logits, (size_t)r->T * r->V * 4, r->own));
     hipError_t e =
         r->b16() ? g16_nt(r->fn_outb, r->D, r->Wb(r->lm_head), r->D, logits, r->V, r->T, r->V, r->D,
@@ -1727,6 +1748,20 @@ uint32_t vkh_runner_attention_backward_path(const vkh_runner *r) {
     return VKH_ATTN_BW_ROWWISE;
 }
 
+vkh_status vkh_runner_attention_backward_plan(const vkh_runner *r, uint32_t out[5]) {
+    if (!r || !out) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
+    out[0] = vkh_runner_attention_backward_path(r);
+    out[1] = out[2] = out[3] = out[4] = 0;
+    if (r->attn_v4) {
+        const AttnShape s = r->attn_shape();
+        out[1] = (uint32_t)fa_bw_v4_q_rows(s);
+        out[2] = (uint32_t)fa_bw_v4_q_blocks(s);
+        out[3] = (uint32_t)fa_bw_v4_kv_blocks(s);
+        out[4] = r->qk_fused ? 1u : 0u;
+    }
+    return VKH_OK;
+}
+
 vkh_status vkh_runner_tensor_numel(const vkh_runner *r, int kind, int layer, int which,
                                    size_t *numel) {
     if (!r || !numel) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
@@ -1770,6 +1805,32 @@ vkh_status vkh_runner_get_tensor(vkh_runner *r, int kind, int layer, int which, 
     VKH_TRY(r->host_wait());
     if (d16) return read_bf16_widened(d16, n, host);  // bf16-only base matrix
     VKH_HIP(hipMemcpy(host, d, n * 4, hipMemcpyDeviceToHost));
+    return VKH_OK;
+}
+
+vkh_status vkh_runner_set_boundary_capture(vkh_runner *r, uint32_t on) {
+    if (!r) return fail(VKH_ERR_INVALID_ARGUMENT, "null runner");
+    VKH_TRY(r->host_wait());
+    if (on && !r->bnd_grad) VKH_TRY(r->alloc(r->bnd_grad, (size_t)(r->L + 1) * r->T * r->D));
+    r->bnd_capture = on != 0;
+    return VKH_OK;
+}
+
+vkh_status vkh_runner_boundary_read(vkh_runner *r, uint32_t l, uint32_t which, float *host,
+                                    size_t numel) {
+    if (!r || !host) return fail(VKH_ERR_INVALID_ARGUMENT, "null argument");
+    if ((int)l > r->L || which > 1) return fail(VKH_ERR_INVALID_ARGUMENT, "boundary %u / %u", l, which);
+    const size_t n = (size_t)r->T * r->D;
+    if (numel != n) return fail(VKH_ERR_INVALID_ARGUMENT, "numel %zu != %zu", numel, n);
+    const float *src;
+    if (which == 0) {
+        src = l == 0 ? r->x_emb : r->acts[l - 1].y;
+    } else {
+        if (!r->bnd_grad) return fail(VKH_ERR_INVALID_ARGUMENT, "boundary capture was never on");
+        src = r->bnd_grad + (size_t)l * n;
+    }
+    VKH_TRY(r->host_wait());
+    VKH_HIP(hipMemcpy(host, src, n * 4, hipMemcpyDeviceToHost));
     return VKH_OK;
 }
 

@@ -231,6 +231,31 @@ class Runner:
         return {0: "rowwise", 1: "ds_gemm", 2: "recompute"}[
             int(lib().vkh_runner_attention_backward_path(self._h))]
 
+    def set_boundary_capture(self, on: bool = True) -> None:
+        """Keep the gradient at every layer boundary in later backwards
+        (stage-by-stage checks)."""
+        check(lib().vkh_runner_set_boundary_capture(self._h, int(bool(on))))
+
+    def boundary(self, l: int, which: int) -> np.ndarray:
+        """which = 0: the residual-stream tensor at boundary l (0 the
+        embedding output, l the output of layer l - 1); which = 1: the
+        captured gradient at it.  fp32 [T, dim] flattened."""
+        c = self.cfg
+        out = np.empty(c.n_pos * max(1, c.n_seqs) * c.dim, np.float32)
+        check(lib().vkh_runner_boundary_read(self._h, l, which,
+                                             out.ctypes.data_as(C.c_void_p), out.size))
+        return out
+
+    def attention_backward_plan(self) -> dict:
+        """The step's attention-backward launch plan: path, query rows per dQ
+        block, dQ and dK/dV block counts, and whether RoPE^T and the Q/K-norm
+        backward run in the recompute kernels' epilogues."""
+        out = (C.c_uint32 * 5)()
+        check(lib().vkh_runner_attention_backward_plan(self._h, C.byref(out)))
+        return {"path": {0: "rowwise", 1: "ds_gemm", 2: "recompute"}[int(out[0])],
+                "dq_block_rows": int(out[1]), "dq_blocks": int(out[2]),
+                "dkv_blocks": int(out[3]), "qk_epilogue": bool(out[4])}
+
     # ── checkpoints ──────────────────────────────────────────────────
     def save_checkpoint(self, path: str):
         check(lib().vkh_runner_save_checkpoint(self._h, path.encode()))
