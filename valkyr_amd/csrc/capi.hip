@@ -6,6 +6,7 @@
 #include <string.h>
 
 #include <algorithm>
+#include <atomic>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -31,6 +32,9 @@ vkh_status hip_fail(hipError_t e, const char *what) {
     return fail(VKH_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
 }
 
+static std::atomic<uint64_t> g_allocations{0};
+void note_allocation() { g_allocations.fetch_add(1, std::memory_order_relaxed); }
+
 // RoPE tables for the standalone kernel entry points, cached per
 // (device, seq_len, rotary_dim, theta) for the life of the process.
 static vkh_status rope_table_cached(int seq_len, int rot, float theta, const float2 **out) {
@@ -48,6 +52,7 @@ static vkh_status rope_table_cached(int seq_len, int rot, float theta, const flo
     std::vector<float2> tab((size_t)seq_len * (half ? half : 1));
     if (half) rope_table_host(tab.data(), seq_len, rot, theta);
     float2 *d = nullptr;
+    note_allocation();
     VKH_HIP(hipMalloc(&d, tab.size() * sizeof(float2)));
     VKH_HIP(hipMemcpy(d, tab.data(), tab.size() * sizeof(float2), hipMemcpyHostToDevice));
     cache[key] = d;
@@ -78,6 +83,7 @@ class ScratchLease {
         }
     }
     vkh_status acquire(size_t bytes, hipStream_t st, void **out) {
+        note_allocation();
         static std::mutex mu;
         static std::map<int, DevScratch> per_dev;
         lk_ = std::unique_lock<std::mutex>(mu);
@@ -93,6 +99,7 @@ class ScratchLease {
                 d.bytes = 0;
             }
             const size_t nb = std::max(bytes, (size_t)1 << 20);
+            note_allocation();
             VKH_HIP(hipMalloc(&d.p, nb));
             d.bytes = nb;
         } else if (d.used && d.last != st) {
@@ -305,7 +312,10 @@ vkh_status vkh_fa_backward(const vkh_attn_params *p, const void *q, const void *
     // the recompute kernels whenever the shape allows (they need no workspace)
     const bool v4 = fa_bw_v4_ok(s);
     const size_t wsb = fa_bw_ws_bytes(s, v4);
-    if (!ws && wsb) VKH_HIP(hipMallocAsync(&ws, wsb, st));
+    if (!ws && wsb) {
+        note_allocation();
+        VKH_HIP(hipMallocAsync(&ws, wsb, st));
+    }
     const hipError_t e = fa_bw_fused(s, a, (bf16 *)ws, v4, st);
     if (!workspace && wsb) (void)hipFreeAsync(ws, st);
     if (e != hipSuccess) return hip_fail(e, "fa_backward");
@@ -435,6 +445,7 @@ vkh_status vkh_lora_backward(const float *dy, const float *x, const float *w, co
     const Precision pr = PR(precision);
     hipStream_t st = S(stream);
     float *dyB = nullptr;
+    note_allocation();
     VKH_HIP(hipMallocAsync((void **)&dyB, (size_t)M * r * 4 + 256, st));
     LoraSegs sb, sa, sdA, sdB;
     sb.n = sa.n = sdA.n = sdB.n = 1;
@@ -464,6 +475,66 @@ vkh_status vkh_lora_backward(const float *dy, const float *x, const float *w, co
     return VKH_OK;
 }
 
+// The training step's grouped LoRA launches on bf16 activations: the segment
+// lists come from lora_group_segs, as in the runner.
+static vkh_status lora_group_args(const vkh_lora_adapter *ad, uint32_t na, uint32_t r,
+                                  LoraAdapter (&out)[3]) {
+    CHECK_ARG(ad && na >= 1 && na <= 3, "1 to 3 adapters");
+    CHECK_ARG(r > 0, "rank 0");
+    for (uint32_t i = 0; i < na; ++i) {
+        const vkh_lora_adapter &a = ad[i];
+        CHECK_ARG(a.a && a.b && a.inter && a.n && a.k, "adapter: null factor or buffer");
+        out[i] = LoraAdapter{(long)a.col, (int)a.n, (int)a.k, a.a, a.b, a.inter, a.dyb, a.da, a.db};
+    }
+    return VKH_OK;
+}
+
+vkh_status vkh_lora_group_forward_bf16(const uint16_t *x, uint32_t ldx, uint32_t T, uint32_t r,
+                                       float aor, const vkh_lora_adapter *adapters,
+                                       uint32_t n_adapters, float *y, uint32_t ldy,
+                                       vkh_stream stream) {
+    CHECK_ARG(x && y, "null pointer");
+    LoraAdapter ad[3];
+    VKH_TRY(lora_group_args(adapters, n_adapters, r, ad));
+    for (uint32_t i = 0; i < n_adapters; ++i)
+        CHECK_ARG(ad[i].k <= (long)ldx && ad[i].col + ad[i].n <= (long)ldy, "adapter outside the rows");
+    const LoraGroupSegs g = lora_group_segs(ad, (int)n_adapters, (int)r);
+    if (!lora_fast_ok(DType::BF16, x, ldx, (int)r, g.fwd_rows) ||
+        !lora_update_ok(y, ldy, (int)r, g.fwd_upd))
+        return fail(VKH_ERR_UNSUPPORTED, "lora_group_forward_bf16: shape or alignment");
+    hipStream_t st = S(stream);
+    VKH_HIP(lora_rows(DType::BF16, x, ldx, (int)T, (int)r, g.fwd_rows, 1.f, st));
+    VKH_HIP(lora_update(y, ldy, (int)T, (int)r, g.fwd_upd, aor, st));
+    return VKH_OK;
+}
+
+vkh_status vkh_lora_group_backward_bf16(const uint16_t *dy, uint32_t lddy, const uint16_t *x,
+                                        uint32_t ldx, uint32_t T, uint32_t r, float aor,
+                                        const vkh_lora_adapter *adapters, uint32_t n_adapters,
+                                        float *dx, uint32_t lddx, vkh_stream stream) {
+    CHECK_ARG(dy && x, "null pointer");
+    LoraAdapter ad[3];
+    VKH_TRY(lora_group_args(adapters, n_adapters, r, ad));
+    for (uint32_t i = 0; i < n_adapters; ++i) {
+        CHECK_ARG(ad[i].dyb && ad[i].da && ad[i].db, "adapter: null dyb, da or db");
+        CHECK_ARG(ad[i].k <= (long)ldx && ad[i].col + ad[i].n <= (long)lddy &&
+                      (!dx || ad[i].k <= (long)lddx),
+                  "adapter outside the rows");
+    }
+    const LoraGroupSegs g = lora_group_segs(ad, (int)n_adapters, (int)r);
+    if (!lora_fast_ok(DType::BF16, dy, lddy, (int)r, g.bwd_rows) ||
+        !lora_fast_ok(DType::BF16, x, ldx, (int)r, g.bwd_da) ||
+        !lora_fast_ok(DType::BF16, dy, lddy, (int)r, g.bwd_db) ||
+        (dx && !lora_update_ok(dx, lddx, (int)r, g.bwd_upd)))
+        return fail(VKH_ERR_UNSUPPORTED, "lora_group_backward_bf16: shape or alignment");
+    hipStream_t st = S(stream);
+    VKH_HIP(lora_rows(DType::BF16, dy, lddy, (int)T, (int)r, g.bwd_rows, 1.f, st));
+    VKH_HIP(lora_cols(DType::BF16, x, ldx, (int)T, (int)r, g.bwd_da, aor, st));
+    VKH_HIP(lora_cols(DType::BF16, dy, lddy, (int)T, (int)r, g.bwd_db, aor, st));
+    if (dx) VKH_HIP(lora_update(dx, lddx, (int)T, (int)r, g.bwd_upd, aor, st));
+    return VKH_OK;
+}
+
 // ── CCE ────────────────────────────────────────────────────────────────
 
 vkh_status vkh_cce_forward(const vkh_cce_params *p, const float *h, const float *w,
@@ -474,6 +545,7 @@ vkh_status vkh_cce_forward(const vkh_cce_params *p, const float *h, const float 
     const CceShape s{(int)p->n, (int)p->vocab, (int)p->dim, p->z_loss_scale, p->label_smoothing};
     hipStream_t st = S(stream);
     float *work = nullptr;
+    note_allocation();
     VKH_HIP(hipMallocAsync((void **)&work, cce_work_floats(s) * 4, st));
     hipError_t e = cce_forward(PR(p->precision), s, h, w, targets, lse, loss_row, loss_mean, work, st);
     (void)hipFreeAsync(work, st);
@@ -490,6 +562,7 @@ vkh_status vkh_cce_backward(const vkh_cce_params *p, const float *h, const float
     hipStream_t st = S(stream);
     void *dz = nullptr;
     const size_t zb = (size_t)p->n * p->vocab * (p->precision == VKH_PRECISION_BF16 ? 2 : 4);
+    note_allocation();
     VKH_HIP(hipMallocAsync(&dz, zb, st));
     hipError_t e = cce_backward(PR(p->precision), s, h, w, targets, lse, dz, dh, dw,
                                 accumulate_dw ? 1.f : 0.f, st);
@@ -528,31 +601,42 @@ vkh_status vkh_rmsnorm_backward(const float *dy, const float *x, const float *w,
 // array instead of the lease above, so a call allocates nothing (for callers
 // under graph capture or in loops that must not call hipMalloc).  Each GPU
 // holds its own copy for the life of the process; its device address is
-// looked up once per device and only that address is handed to kernels.
-// Every block overwrites its whole partial row before the column sum reads
-// it, so nothing needs clearing between calls.
+// looked up once per device, at the first call on it, and only that address
+// is handed to kernels.  Every block overwrites its whole partial row before
+// the column sum reads it, so nothing needs clearing between calls.
+//
+// Calls share the array, so they are ordered like the lease's uses: an event
+// per device (created with the address lookup; an event holds no device
+// memory) is recorded after each call's launch, and a call on another stream
+// first makes its stream wait for it.  While the caller's stream is being
+// captured into a graph the event is neither waited for nor recorded (a
+// captured stream may not wait on work outside its capture): the caller then
+// orders the graph's launches against other uses of the array itself.
 constexpr size_t kNoAllocPartialFloats = 512 * 4096;  // 8 MiB
 static __device__ __align__(256) float scratch[kNoAllocPartialFloats];
 
 namespace {
 constexpr int kMaxDevices = 64;
+struct NoAllocScratch {
+    float *ptr = nullptr;      // the device address of `scratch` on this device
+    hipEvent_t done = nullptr; // recorded after each uncaptured use
+    hipStream_t last = nullptr;
+    bool used = false;
+};
 std::mutex g_scratch_mu;
-float *g_scratch_ptr[kMaxDevices] = {};
+NoAllocScratch g_scratch[kMaxDevices];
 }  // namespace
 
-static vkh_status noalloc_scratch(float **out) {
-    int dev = 0;
-    VKH_HIP(hipGetDevice(&dev));
-    if (dev < 0 || dev >= kMaxDevices) return fail(VKH_ERR_UNSUPPORTED, "device index %d >= %d", dev, kMaxDevices);
-    std::lock_guard<std::mutex> lk(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
-        void *p = nullptr;
-        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
-        if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
-        if (!p) return fail(VKH_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
-        g_scratch_ptr[dev] = (float *)p;
-    }
-    *out = g_scratch_ptr[dev];
+// Set-up of the current device's array (once per device, with the mutex held).
+static vkh_status noalloc_scratch_setup(int dev) {
+    NoAllocScratch &d = g_scratch[dev];
+    if (d.ptr) return VKH_OK;
+    void *p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (!p) return fail(VKH_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
+    VKH_HIP(hipEventCreateWithFlags(&d.done, hipEventDisableTiming));
+    d.ptr = (float *)p;
     return VKH_OK;
 }
 
@@ -566,13 +650,30 @@ vkh_status vkh_rmsnorm_backward_noalloc(const float *dy, const float *x, const f
     if (need > kNoAllocPartialFloats)
         return fail(VKH_ERR_UNSUPPORTED, "rmsnorm_backward_noalloc: %zu partial floats > %zu",
                     need, kNoAllocPartialFloats);
-    float *partial = nullptr;
-    VKH_TRY(noalloc_scratch(&partial));
-    hipError_t e = rmsnorm_backward(dy, x, w, dx, nullptr, residual, dw, partial, n_rows, dim, eps,
-                                    gq ? 1 : 0, S(stream));
+    int dev = 0;
+    VKH_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= kMaxDevices)
+        return fail(VKH_ERR_UNSUPPORTED, "device index %d >= %d", dev, kMaxDevices);
+    const hipStream_t st = S(stream);
+    std::lock_guard<std::mutex> lk(g_scratch_mu);  // held while the call enqueues
+    VKH_TRY(noalloc_scratch_setup(dev));
+    NoAllocScratch &d = g_scratch[dev];
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    VKH_HIP(hipStreamIsCapturing(st, &cs));
+    const bool captured = cs != hipStreamCaptureStatusNone;
+    if (!captured && d.used && d.last != st) VKH_HIP(hipStreamWaitEvent(st, d.done, 0));
+    hipError_t e = rmsnorm_backward(dy, x, w, dx, nullptr, residual, dw, d.ptr, n_rows, dim, eps,
+                                    gq ? 1 : 0, st);
     if (e != hipSuccess) return hip_fail(e, "rmsnorm_backward_noalloc");
+    if (!captured) {
+        VKH_HIP(hipEventRecord(d.done, st));
+        d.used = true;
+        d.last = st;
+    }
     return VKH_OK;
 }
+
+uint64_t vkh_allocation_count(void) { return g_allocations.load(std::memory_order_relaxed); }
 
 vkh_status vkh_swiglu_forward(const float *pg, const float *up, float *g, size_t n,
                               vkh_stream stream) {
@@ -682,6 +783,7 @@ vkh_status vkh_device_count(int *count) {
 vkh_status vkh_set_device(int device) { VKH_HIP(hipSetDevice(device)); return VKH_OK; }
 vkh_status vkh_malloc(void **ptr, size_t bytes) {
     CHECK_ARG(ptr, "null pointer");
+    note_allocation();
     VKH_HIP(hipMalloc(ptr, bytes ? bytes : 1));
     return VKH_OK;
 }

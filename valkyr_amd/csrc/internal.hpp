@@ -11,6 +11,9 @@ namespace vkh {
 // Records a thread-local message and returns `st`.
 vkh_status fail(vkh_status st, const char *fmt, ...) __attribute__((format(printf, 2, 3)));
 vkh_status hip_fail(hipError_t e, const char *what);
+// Counts one allocation by the library (device or pinned memory, or a lease of
+// the shared scratch buffer); read through vkh_allocation_count.
+void note_allocation();
 
 }  // namespace vkh
 

@@ -402,6 +402,22 @@ hipError_t cols_launch(const TX *x, long ldx, int T, int r, const LoraSegs &g, f
 // Shapes the three kernels take: r <= 64 and a multiple of 4, every adapter's
 // columns a multiple of 64 starting on a 16-byte boundary of X / Y, rows of
 // X, Y and U 16-byte aligned, factor layouts that allow float4 loads.
+LoraGroupSegs lora_group_segs(const LoraAdapter *ad, int na, int r) {
+    LoraGroupSegs g;
+    for (int i = 0; i < na && i < 3; ++i) {
+        const LoraAdapter &a = ad[i];
+        g.fwd_rows.s[g.fwd_rows.n++] = LoraSeg{0, a.k, a.a, 1, (long)a.k, a.inter, (long)r};
+        g.fwd_upd.s[g.fwd_upd.n++] = LoraSeg{a.col, a.n, a.b, (long)r, 1, a.inter, (long)r};
+        g.bwd_rows.s[g.bwd_rows.n++] = LoraSeg{a.col, a.n, a.b, (long)r, 1, a.dyb, (long)r};
+        g.bwd_upd.s[g.bwd_upd.n++] = LoraSeg{0, a.k, a.a, 1, (long)a.k, a.dyb, (long)r};
+        g.bwd_da.s[g.bwd_da.n++] =
+            LoraSeg{0, a.k, nullptr, 1, 1, a.dyb, (long)r, a.da, 1, (long)a.k};
+        g.bwd_db.s[g.bwd_db.n++] =
+            LoraSeg{a.col, a.n, nullptr, 1, 1, a.inter, (long)r, a.db, (long)r, 1};
+    }
+    return g;
+}
+
 bool lora_fast_ok(DType xt, const void *x, long ldx, int r, const LoraSegs &g) {
     if (r < 1 || r > 64 || r % 4 || g.n < 1 || g.n > 3) return false;
     const long xv = xt == DType::BF16 ? 8 : 4;

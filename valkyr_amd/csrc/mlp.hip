@@ -880,6 +880,7 @@ vkh_status vkh_mlp_create(const vkh_mlp_config *cfg, vkh_mlp **out) {
         offs[k] = off;
         off += (slots[k].n * sizeof(float) + 255) & ~(size_t)255;
     }
+    note_allocation();
     hipError_t e = hipMalloc((void **)&m->arena, off ? off : 256);
     if (e != hipSuccess) return bail(hip_fail(e, "hipMalloc (mlp arena)"));
     for (size_t k = 0; k < sizeof(slots) / sizeof(slots[0]); ++k)
@@ -889,6 +890,7 @@ vkh_status vkh_mlp_create(const vkh_mlp_config *cfg, vkh_mlp **out) {
     // pinned staging: x, target, loss, predictions
     m->ystage_n = NB * O;
     const size_t pin_n = I + O + O + 1 + m->ystage_n + (size_t)kRing * (I + O);
+    note_allocation();
     e = hipHostMalloc((void **)&m->pin, pin_n * sizeof(float), hipHostMallocDefault);
     if (e != hipSuccess) return bail(hip_fail(e, "hipHostMalloc (mlp staging)"));
     memset(m->pin, 0, pin_n * sizeof(float));

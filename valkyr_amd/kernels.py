@@ -10,7 +10,7 @@ from __future__ import annotations
 import ctypes as C
 import math
 
-from ._lib import AttnParams, CceParams, RopeParams, check, lib
+from ._lib import AttnParams, CceParams, LoraAdapter, RopeParams, check, lib
 
 F32, BF16 = 0, 1
 PRECISION_FP32, PRECISION_BF16 = 0, 1
@@ -118,6 +118,35 @@ def lora_backward(dy, x, w, a, b, inter, dx, dA, dB, M, N, K, r, alpha_over_r,
                   precision=PRECISION_FP32, stream=None):
     check(lib().vkh_lora_backward(_p(dy), _p(x), _p(w), _p(a), _p(b), _p(inter), _p(dx), _p(dA),
                                   _p(dB), M, N, K, r, alpha_over_r, precision, _s(stream)))
+
+
+def lora_adapters(specs):
+    """ctypes array of vkh_lora_adapter from dicts with keys col, n, k, a, b,
+    inter, dyb, da, db (buffers or None)."""
+    def addr(x):
+        p = _p(x)
+        return None if p is None else p.value
+
+    arr = (LoraAdapter * len(specs))()
+    for i, d in enumerate(specs):
+        arr[i] = LoraAdapter(d["col"], d["n"], d["k"],
+                             *(addr(d.get(f)) for f in ("a", "b", "inter", "dyb", "da", "db")))
+    return arr
+
+
+def lora_group_forward_bf16(x16, ldx, T, r, aor, adapters, y, ldy, stream=None):
+    """The training step's grouped rank-r forward on a bf16 activation:
+    inter = x A^T and y[:, col:col+n] += aor inter B^T for each adapter."""
+    check(lib().vkh_lora_group_forward_bf16(_p(x16), ldx, T, r, aor, adapters, len(adapters),
+                                            _p(y), ldy, _s(stream)))
+
+
+def lora_group_backward_bf16(dy16, lddy, x16, ldx, T, r, aor, adapters, dx=None, lddx=0,
+                             stream=None):
+    """The grouped rank-r backward on bf16 dy and x: dyb = dy B, dA, dB and
+    dx += aor dyb A."""
+    check(lib().vkh_lora_group_backward_bf16(_p(dy16), lddy, _p(x16), ldx, T, r, aor, adapters,
+                                             len(adapters), _p(dx), lddx, _s(stream)))
 
 
 def cce_params(n, vocab, dim, z_loss_scale=0.0, label_smoothing=0.0, precision=PRECISION_FP32):
