@@ -441,7 +441,11 @@ def test_cce_forward_backward(prec, n, V, D, zl, ls):
 FA_F32_CASES = [  # smoke/cpu.zig:909-916 shapes (n_q, n_kv, H, Hkv, hd, causal) + batch
     (4, 4, 4, 2, 16, True, 1), (16, 16, 16, 8, 128, True, 1), (8, 8, 8, 2, 256, True, 1),
     (10, 12, 4, 2, 16, True, 1), (8, 8, 4, 1, 16, True, 1), (4, 8, 4, 2, 16, False, 1),
-    (128, 128, 4, 2, 64, True, 3),
+    # the fp32 matrix-core kernels (head_dim 64 / 128, whole 64-row tiles): GQA 2:1
+    # and 4:1, non-causal with more keys and with more queries, config 3's shape
+    (128, 128, 4, 2, 64, True, 3), (256, 256, 16, 8, 128, True, 2),
+    (192, 192, 8, 2, 64, True, 1), (128, 256, 4, 2, 128, False, 1),
+    (256, 128, 8, 2, 64, False, 2), (512, 512, 16, 8, 128, True, 4),
 ]
 
 

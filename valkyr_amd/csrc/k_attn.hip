@@ -2117,6 +2117,9 @@ hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k
                                (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
     } else {
         if (s.head_dim > 64 * MAXE || ob) return hipErrorInvalidValue;
+        if (fa_f32m_fwd(s, (const float *)q, ldq, (const float *)k, ldk, (const float *)v, ldv, o,
+                        ldo, lse, st))
+            return hipGetLastError();
         hipLaunchKernelGGL(fa_fwd_f32_k, dim3(rows_grid((long)s.n_batch * s.n_q * s.n_heads)),
                            dim3(NT), 0, st, s, (const float *)q, ldq, (const float *)k, ldk,
                            (const float *)v, ldv, o, ldo, lse);
@@ -2176,6 +2179,7 @@ hipError_t fa_bw_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
             hipLaunchKernelGGL(fa_bwd_dq_bf16_k<64>, grid, dim3(NT), 0, st, s, p);
     } else {
         if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
+        if (fa_f32m_dq(s, p, st)) return hipGetLastError();
         hipLaunchKernelGGL(fa_bwd_dq_f32_k, dim3(rows_grid((long)s.n_batch * s.n_q * s.n_heads)),
                            dim3(NT), 0, st, s, p);
     }
@@ -2335,6 +2339,7 @@ hipError_t fa_bw_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
             hipLaunchKernelGGL(fa_bwd_dkv_bf16_k<64>, grid, dim3(NT), 0, st, s, p);
     } else {
         if (s.head_dim > 64 * MAXE) return hipErrorInvalidValue;
+        if (fa_f32m_dkv(s, p, st)) return hipGetLastError();
         hipLaunchKernelGGL(fa_bwd_dkv_f32_k,
                            dim3(rows_grid((long)s.n_batch * s.n_kv * s.n_kv_heads)), dim3(NT), 0,
                            st, s, p);

@@ -263,6 +263,15 @@ struct AttnPtrs {
     const void *o16 = nullptr; long ldo16 = 0;
     QkEpi qk;  // recompute path only
 };
+// fp32 attention on the matrix cores (k_attn_f32.hip) for the shapes
+// fa_f32m_ok accepts; each launcher returns false, launching nothing, for a
+// shape or alignment it does not take (the caller then uses the per-row
+// kernels).
+bool fa_f32m_ok(const AttnShape &s);
+bool fa_f32m_fwd(const AttnShape &s, const float *q, long ldq, const float *k, long ldk,
+                 const float *v, long ldv, float *o, long ldo, float *lse, hipStream_t st);
+bool fa_f32m_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
+bool fa_f32m_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 // ob (optional, bf16 operands only): bf16 copy of O for the output projection.
 hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
                       const void *v, long ldv, float *o, long ldo, float *lse, DType dt,
