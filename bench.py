@@ -728,7 +728,10 @@ def main():
         print(json.dumps({"mlp_runner": bench_mlp(args)}), flush=True)
         return
     if args.only == "bw":
-        print(json.dumps({"bandwidth": bench_bandwidth(args)}), flush=True)
+        bw = bench_bandwidth(args)
+        if args.calib_copy:
+            calib_copy()
+        print(json.dumps({"bandwidth": bw}), flush=True)
         return
     if args.only == "gemms":
         print(json.dumps({"layer_gemms": bench_gemms(args)}), flush=True)

@@ -56,8 +56,8 @@ def test_rmsnorm_forward_backward_fused_dw():
 
 
 def test_rmsnorm_backward_scratch_shared_across_streams():
-    """The standalone entry points share one scratch buffer per device (gain
-    partials here); calls enqueued back to back on two streams, with no host
+    """The standalone entry points keep their scratch (gain partials here) per
+    stream; calls enqueued back to back on two streams, with no host
     synchronisation between them, must each see their own partials."""
     from valkyr_amd import kernels as K
     from valkyr_amd.device import Stream

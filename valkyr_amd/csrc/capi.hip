@@ -7,6 +7,7 @@
 
 #include <algorithm>
 #include <atomic>
+#include <iterator>
 #include <map>
 #include <mutex>
 #include <tuple>
@@ -60,62 +61,66 @@ static vkh_status rope_table_cached(int seq_len, int rot, float theta, const flo
     return VKH_OK;
 }
 
-// Scratch memory of the standalone entry points (gain partials, sort work,
-// split-K partials): one buffer per device, grown on demand and reused, so a
-// call does not allocate.  Uses are ordered on the device: each use records
-// an event on its stream and the next use makes its stream wait for that
-// event, so calls on different streams never share the buffer at the same
-// time.  The mutex is held while a call enqueues its work.
-struct DevScratch {
-    void *p = nullptr;
-    size_t bytes = 0;
-    hipEvent_t done = nullptr;
-    hipStream_t last = nullptr;  // stream of the last use (same stream: ordered already)
-    bool used = false;
-};
-
+// Scratch memory of the standalone entry points (gain partials, split-K
+// partials): one buffer per (device, stream), grown on demand and reused, so
+// a call does not allocate once its stream's buffer is large enough.  Calls
+// on one stream are ordered by the stream; calls on different streams use
+// different buffers, so no event is recorded or waited for per call (an
+// event record costs a few microseconds of device time).  Streams are told
+// apart by hipStreamGetId, which is unique for the life of the process, so a
+// stream created after another was destroyed never inherits its buffer.  A
+// buffer is replaced only after its stream has drained; at most kMaxStreams
+// buffers are kept, and making room for another waits for the whole device.
 class ScratchLease {
   public:
-    ~ScratchLease() {
-        if (d_) {
-            (void)hipEventRecord(d_->done, st_);
-            d_->used = true;
-        }
-    }
     vkh_status acquire(size_t bytes, hipStream_t st, void **out) {
         note_allocation();
+        constexpr size_t kMaxStreams = 64;
+        struct Buf {
+            void *p = nullptr;
+            size_t bytes = 0;
+        };
         static std::mutex mu;
-        static std::map<int, DevScratch> per_dev;
-        lk_ = std::unique_lock<std::mutex>(mu);
+        static std::map<std::pair<int, unsigned long long>, Buf> per_stream;
+        lk_ = std::unique_lock<std::mutex>(mu);  // held until the call has enqueued its work
         int dev = 0;
         VKH_HIP(hipGetDevice(&dev));
-        DevScratch &d = per_dev[dev];
-        if (!d.done) VKH_HIP(hipEventCreateWithFlags(&d.done, hipEventDisableTiming));
-        if (d.bytes < bytes) {
-            if (d.p) {
-                VKH_HIP(hipEventSynchronize(d.done));
-                VKH_HIP(hipFree(d.p));
-                d.p = nullptr;
-                d.bytes = 0;
+        unsigned long long sid = 0;
+        VKH_HIP(hipStreamGetId(st, &sid));
+        const auto key = std::make_pair(dev, sid);
+        auto it = per_stream.find(key);
+        if (it == per_stream.end()) {
+            if (per_stream.size() >= kMaxStreams) {
+                // every stream's work done: any kept buffer may go
+                VKH_HIP(hipDeviceSynchronize());
+                for (auto &kv : per_stream) {
+                    if (kv.first.first != dev) continue;
+                    VKH_HIP(hipFree(kv.second.p));
+                }
+                for (auto i = per_stream.begin(); i != per_stream.end();)
+                    i = i->first.first == dev ? per_stream.erase(i) : std::next(i);
+            }
+            it = per_stream.emplace(key, Buf{}).first;
+        }
+        Buf &b = it->second;
+        if (b.bytes < bytes) {
+            if (b.p) {
+                VKH_HIP(hipStreamSynchronize(st));  // its earlier uses are done
+                VKH_HIP(hipFree(b.p));
+                b.p = nullptr;
+                b.bytes = 0;
             }
             const size_t nb = std::max(bytes, (size_t)1 << 20);
             note_allocation();
-            VKH_HIP(hipMalloc(&d.p, nb));
-            d.bytes = nb;
-        } else if (d.used && d.last != st) {
-            VKH_HIP(hipStreamWaitEvent(st, d.done, 0));  // a use on another stream
+            VKH_HIP(hipMalloc(&b.p, nb));
+            b.bytes = nb;
         }
-        d.last = st;
-        d_ = &d;
-        st_ = st;
-        *out = d.p;
+        *out = b.p;
         return VKH_OK;
     }
 
   private:
     std::unique_lock<std::mutex> lk_;
-    DevScratch *d_ = nullptr;
-    hipStream_t st_ = nullptr;
 };
 
 }  // namespace vkh
@@ -635,7 +640,7 @@ static vkh_status noalloc_scratch_setup(int dev) {
     const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
     if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
     if (!p) return fail(VKH_ERR_HIP, "hipGetSymbolAddress(scratch) returned null");
-    VKH_HIP(hipEventCreateWithFlags(&d.done, hipEventDisableTiming));
+    VKH_HIP(hipEventCreateWithFlags(&d.done, hipEventDisableTiming | hipEventDisableSystemFence));
     d.ptr = (float *)p;
     return VKH_OK;
 }
@@ -727,11 +732,8 @@ vkh_status vkh_embedding_backward(const float *dy, const uint32_t *ids, float *d
                                   vkh_stream stream) {
     CHECK_ARG(dy && ids && dE, "null pointer");
     if (n_pos > (uint32_t)kEmbedBwMaxPos) return fail(VKH_ERR_UNSUPPORTED, "n_pos > %d", kEmbedBwMaxPos);
-    hipStream_t st = S(stream);
-    void *work = nullptr;
-    ScratchLease lease;
-    VKH_TRY(lease.acquire(embed_bw_work_bytes(n_pos), st, &work));
-    hipError_t e = embedding_backward(dy, ids, dE, n_pos, dim, vocab, true, work, st);
+    // the owner kernels need no work buffer (no lease, no ordering event)
+    hipError_t e = embedding_backward(dy, ids, dE, n_pos, dim, vocab, true, nullptr, S(stream));
     if (e != hipSuccess) return hip_fail(e, "embedding_backward");
     return VKH_OK;
 }

@@ -118,7 +118,7 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
                                                      const float *w, float *dx, bf16 *dxb,
                                                      const float *res, float *partial, int rows,
                                                      int dim, float eps, int gq) {
-    __shared__ float red[256 * C4];
+    __shared__ float4 red[NW][64 * C4];
     const int lane = threadIdx.x % 64, wave = threadIdx.x / 64;
     const int nw = gridDim.x * NW;
     float4 gain[C4], dwa[C4];
@@ -182,21 +182,19 @@ __global__ __launch_bounds__(NT) void rmsnorm_bwd_k(const float *dy, const float
             dwa[j].x += dw[0]; dwa[j].y += dw[1]; dwa[j].z += dw[2]; dwa[j].w += dw[3];
         }
     }
-    // combine the waves' gain partials in a fixed order: ((w0 + w1) + w2) + w3
-    for (int wv = 0; wv < NW; ++wv) {
-        if (wave == wv) {
+    // combine the waves' gain partials in a fixed order, ((w0 + w1) + w2) + w3,
+    // after one barrier: each wave leaves its sums in its own LDS slot
 #pragma unroll
-            for (int j = 0; j < C4; ++j) {
-                const int c = 4 * lane + 256 * j;
-                if (c >= dim) continue;
-                float4 a = dwa[j];
-                if (wv > 0) a = make_float4(red[c] + a.x, red[c + 1] + a.y, red[c + 2] + a.z, red[c + 3] + a.w);
-                red[c] = a.x; red[c + 1] = a.y; red[c + 2] = a.z; red[c + 3] = a.w;
-            }
-        }
-        __syncthreads();
+    for (int j = 0; j < C4; ++j) red[wave][64 * j + lane] = dwa[j];
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * C4; i += NT) {
+        const int c = 4 * (i % 64) + 256 * (i / 64);
+        if (c >= dim) continue;
+        const float4 a = red[0][i], b = red[1][i], e = red[2][i], d = red[3][i];
+        *reinterpret_cast<float4 *>(partial + (long)blockIdx.x * dim + c) =
+            make_float4(((a.x + b.x) + e.x) + d.x, ((a.y + b.y) + e.y) + d.y,
+                        ((a.z + b.z) + e.z) + d.z, ((a.w + b.w) + e.w) + d.w);
     }
-    for (int c = threadIdx.x; c < dim; c += NT) partial[(long)blockIdx.x * dim + c] = red[c];
 }
 
 // Wide rows (dim > 2048): one row per block iteration instead of one per
@@ -325,48 +323,56 @@ __global__ __launch_bounds__(CS_COLS *CS_GROUPS) void colsum_k(const float *part
 
 // qk_rope_partial_batched.comp / qk_rope_backward_batched.comp with the
 // cos/sin of (position, pair) taken from a table built by the same fp32
-// formula.  One block per row (position p = row % seq_len); each thread
-// rotates four consecutive elements of a head (32-bit index arithmetic, float4
-// loads and stores), the partner quad i +- half is read again from cache.
+// formula (position p = row % seq_len).
 // Scalar form for rows or rotary widths that are not multiples of 4.
-__global__ __launch_bounds__(NT) void qk_rope4_k(const float *q_in, long ldq_in, float *q_out,
-                                                 long ldq_out, const float *k_in, long ldk_in,
-                                                 float *k_out, long ldk_out, int n_rows, int hq,
-                                                 int hkv, int hd, int rot, int seq_len,
-                                                 const float2 *tab, int backward) {
-    const int half = rot / 2, qpr = hd / 4, nq4 = (hq + hkv) * qpr;
-    for (int p = blockIdx.x; p < n_rows; p += gridDim.x) {
-        const float2 *tr = tab + (long)(p % seq_len) * half;
-        for (int u = threadIdx.x; u < nq4; u += NT) {
-            const int h = u / qpr, i = 4 * (u - h * qpr);
-            const bool is_q = h < hq;
-            const float *in = (is_q ? q_in + (long)p * ldq_in : k_in + (long)p * ldk_in) +
-                              (is_q ? h : h - hq) * hd;
-            float *out = (is_q ? q_out + (long)p * ldq_out : k_out + (long)p * ldk_out) +
-                         (is_q ? h : h - hq) * hd;
-            const float4 x = *reinterpret_cast<const float4 *>(in + i);
-            if (i >= rot) {
-                *reinterpret_cast<float4 *>(out + i) = x;
-                continue;
-            }
-            const bool lower = i < half;
-            const int j = lower ? i : i - half;
-            const float4 y = *reinterpret_cast<const float4 *>(in + (lower ? i + half : i - half));
-            const float4 c01 = *reinterpret_cast<const float4 *>(tr + j);
-            const float4 c23 = *reinterpret_cast<const float4 *>(tr + j + 2);
-            const float xs[4] = {x.x, x.y, x.z, x.w}, ys[4] = {y.x, y.y, y.z, y.w};
-            const float cs[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
-            float o[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                // lower half: a = x, b = y; upper half: a = y (pair's low), b = x
-                if (!backward)
-                    o[e] = lower ? xs[e] * cs[e] - ys[e] * sn[e] : ys[e] * sn[e] + xs[e] * cs[e];
-                else
-                    o[e] = lower ? cs[e] * xs[e] + sn[e] * ys[e] : -sn[e] * ys[e] + cs[e] * xs[e];
-            }
-            *reinterpret_cast<float4 *>(out + i) = make_float4(o[0], o[1], o[2], o[3]);
+// One thread per (row, head, 4-element group of the rotary half) and per
+// 4-element group of the non-rotary tail: the pair (i, i + half) is loaded
+// once (two float4) and both rotated outputs are written, so every element
+// is read from memory once; the cos / sin of the row's position come from
+// the table (L2).  32-bit index arithmetic over the flattened work.
+__global__ __launch_bounds__(NT) void qk_rope_pair_k(const float *q_in, long ldq_in, float *q_out,
+                                                     long ldq_out, const float *k_in, long ldk_in,
+                                                     float *k_out, long ldk_out, int n_rows, int hq,
+                                                     int hkv, int hd, int rot, int seq_len,
+                                                     const float2 *tab, int backward) {
+    const int half = rot / 2, npair = half / 4, per_head = npair + (hd - rot) / 4;
+    const int heads = hq + hkv, total = n_rows * heads * per_head;
+    for (int u = blockIdx.x * NT + threadIdx.x; u < total; u += gridDim.x * NT) {
+        const int k = u % per_head, rh = u / per_head, h = rh % heads, p = rh / heads;
+        const bool is_q = h < hq;
+        const float *in = (is_q ? q_in + (long)p * ldq_in : k_in + (long)p * ldk_in) +
+                          (is_q ? h : h - hq) * hd;
+        float *out = (is_q ? q_out + (long)p * ldq_out : k_out + (long)p * ldk_out) +
+                     (is_q ? h : h - hq) * hd;
+        if (k >= npair) {  // beyond the rotary span: copied
+            const int i = rot + 4 * (k - npair);
+            __builtin_nontemporal_store(__builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(in + i)),
+                                        reinterpret_cast<f32x4 *>(out + i));
+            continue;
         }
+        const int i = 4 * k;
+        // streamed once: non-temporal, so the table keeps its place in the caches
+        const f32x4 lo = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(in + i));
+        const f32x4 hi = __builtin_nontemporal_load(reinterpret_cast<const f32x4 *>(in + i + half));
+        const float2 *tr = tab + (long)(p % seq_len) * half + i;
+        const float4 c01 = *reinterpret_cast<const float4 *>(tr);
+        const float4 c23 = *reinterpret_cast<const float4 *>(tr + 2);
+        const float xl[4] = {lo[0], lo[1], lo[2], lo[3]}, xh[4] = {hi[0], hi[1], hi[2], hi[3]};
+        const float cs[4] = {c01.x, c01.z, c23.x, c23.z}, sn[4] = {c01.y, c01.w, c23.y, c23.w};
+        float ol[4], oh[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            if (!backward) {
+                ol[e] = xl[e] * cs[e] - xh[e] * sn[e];
+                oh[e] = xl[e] * sn[e] + xh[e] * cs[e];
+            } else {
+                ol[e] = cs[e] * xl[e] + sn[e] * xh[e];
+                oh[e] = -sn[e] * xl[e] + cs[e] * xh[e];
+            }
+        }
+        __builtin_nontemporal_store(f32x4{ol[0], ol[1], ol[2], ol[3]}, reinterpret_cast<f32x4 *>(out + i));
+        __builtin_nontemporal_store(f32x4{oh[0], oh[1], oh[2], oh[3]},
+                                    reinterpret_cast<f32x4 *>(out + i + half));
     }
 }
 
@@ -1005,11 +1011,12 @@ hipError_t qk_rope(const float *q_in, long ldq_in, float *q_out, long ldq_out, c
     const bool v4 = head_dim % 4 == 0 && rotary_dim % 8 == 0 && al16(q_in) && al16(q_out) &&
                     al16(k_in) && al16(k_out) && al16(tab) && ldq_in % 4 == 0 &&
                     ldq_out % 4 == 0 && ldk_in % 4 == 0 && ldk_out % 4 == 0;
-    if (v4) {
-        hipLaunchKernelGGL(qk_rope4_k, dim3((unsigned)std::min(n_rows, 65535)), dim3(NT), 0, st,
-                           q_in, ldq_in, q_out, ldq_out, k_in, ldk_in, k_out, ldk_out, n_rows,
-                           n_q_heads, n_kv_heads, head_dim, rotary_dim, seq_len, tab,
-                           backward ? 1 : 0);
+    const long units = (long)n_rows * (n_q_heads + n_kv_heads) * (rotary_dim / 8 + (head_dim - rotary_dim) / 4);
+    if (v4 && units < (1L << 31)) {
+        const long g = std::min<long>(16384, (units + NT - 1) / NT);
+        hipLaunchKernelGGL(qk_rope_pair_k, dim3((unsigned)g), dim3(NT), 0, st, q_in, ldq_in, q_out,
+                           ldq_out, k_in, ldk_in, k_out, ldk_out, n_rows, n_q_heads, n_kv_heads,
+                           head_dim, rotary_dim, seq_len, tab, backward ? 1 : 0);
         return hipGetLastError();
     }
     const long total = (long)n_rows * (n_q_heads + n_kv_heads) * head_dim;

@@ -24,6 +24,12 @@
 
 #include "internal.hpp"
 
+// Events that only order one stream after another on this device (waited for
+// with hipStreamWaitEvent, never by the host): no timing and no system-scope
+// fence, which makes each record cheaper; events the host waits on before
+// reading pinned memory keep the fence.
+constexpr unsigned kOrderEvent = hipEventDisableTiming | hipEventDisableSystemFence;
+
 using namespace vkh;
 
 namespace {
@@ -499,15 +505,15 @@ struct vkh_runner {
                 VKH_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
                 ev_layer.assign(L, nullptr);
                 for (int l = 0; l < L; ++l)
-                    VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], hipEventDisableTiming));
+                    VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], kOrderEvent));
                 if (recompute) {
                     ev_sdone.assign(L, nullptr);
                     for (int l = 0; l < L; ++l)
-                        VKH_HIP(hipEventCreateWithFlags(&ev_sdone[l], hipEventDisableTiming));
+                        VKH_HIP(hipEventCreateWithFlags(&ev_sdone[l], kOrderEvent));
                 }
-                VKH_HIP(hipEventCreateWithFlags(&ev_side, hipEventDisableTiming));
-                VKH_HIP(hipEventCreateWithFlags(&ev_head, hipEventDisableTiming));
-                VKH_HIP(hipEventCreateWithFlags(&ev_lm, hipEventDisableTiming));
+                VKH_HIP(hipEventCreateWithFlags(&ev_side, kOrderEvent));
+                VKH_HIP(hipEventCreateWithFlags(&ev_head, kOrderEvent));
+                VKH_HIP(hipEventCreateWithFlags(&ev_lm, kOrderEvent));
                 if (embed_split_ok()) {
                     VKH_TRY(alloc(emb_mark, (size_t)V));
                     VKH_HIP(fill_f32(reinterpret_cast<float *>(emb_mark), (size_t)V, 0.f, own));
@@ -569,13 +575,13 @@ struct vkh_runner {
         lora_aux = lora;
         if (attn_fork || lora_aux) {
             VKH_HIP(hipStreamCreateWithFlags(&aux, hipStreamNonBlocking));
-            VKH_HIP(hipEventCreateWithFlags(&ev_fork, hipEventDisableTiming));
-            VKH_HIP(hipEventCreateWithFlags(&ev_join, hipEventDisableTiming));
+            VKH_HIP(hipEventCreateWithFlags(&ev_fork, kOrderEvent));
+            VKH_HIP(hipEventCreateWithFlags(&ev_join, kOrderEvent));
         }
         if (lora_aux) {
             ev_laux.assign(L, nullptr);
             for (int l = 0; l < L; ++l)
-                VKH_HIP(hipEventCreateWithFlags(&ev_laux[l], hipEventDisableTiming));
+                VKH_HIP(hipEventCreateWithFlags(&ev_laux[l], kOrderEvent));
         }
         VKH_TRY(alloc(tok_d, T));
         VKH_TRY(alloc(tgt_d, T));
@@ -1462,6 +1468,7 @@ struct Blob {
 }  // namespace
 
 namespace vkh {
+
 
 // transformer.zig:1586-1655 collectBlobs.  A tied runner has one embedding
 // matrix; its lm_head blobs are the embedding's (param, m, v) again, which is
