@@ -174,6 +174,16 @@ RECOMPUTE = dict(HD128, n_heads=16, n_kv_heads=8, n_seqs=16, seq_len=128, n_laye
                  ff_dim=512, vocab_size=1024)
 
 
+# GQA 4:1 on the recompute path with 128 dK/dV blocks (fewer than the CUs): the
+# dK/dV launch splits each block's head group over two blocks and a combine
+# kernel adds the halves before the epilogue (config 4's case at 1 x 2048);
+# with a 64-wide rotary span the fused epilogue is off and the combine writes
+# fp32 dK / dV
+RECOMPUTE_GQA4 = dict(HD128, n_heads=16, n_kv_heads=4, n_seqs=16, seq_len=256, n_layers=1,
+                      dim=256, ff_dim=512, vocab_size=1024)
+RECOMPUTE_GQA4_ROT64 = dict(RECOMPUTE_GQA4, rotary_dim=64)
+SPLIT_VARIANTS = (RECOMPUTE_GQA4, RECOMPUTE_GQA4_ROT64)
+
 # The fused q/k epilogue's other branches: RoPE^T without the Q/K-norm
 # backward (a Llama-style hd-128 model), and the Q/K-norm backward without RoPE.
 RECOMPUTE_NO_QK_NORM = dict(RECOMPUTE, qk_norm=0)
@@ -182,9 +192,10 @@ RECOMPUTE_VARIANTS = (RECOMPUTE, RECOMPUTE_NO_QK_NORM, RECOMPUTE_NO_ROPE)
 
 
 @pytest.mark.parametrize("variant", [{}, HD128, RECOMPUTE, RECOMPUTE_NO_QK_NORM,
-                                     RECOMPUTE_NO_ROPE],
+                                     RECOMPUTE_NO_ROPE, RECOMPUTE_GQA4, RECOMPUTE_GQA4_ROT64],
                          ids=["config1", "hd128", "recompute", "recompute-no-qk-norm",
-                              "recompute-no-rope"])
+                              "recompute-no-rope", "recompute-gqa4-split",
+                              "recompute-gqa4-split-rot64"])
 def test_step_parity_bf16(variant):
     """bf16-operand step vs the oracle with the same operand rounding (every
     MFMA operand, the attention P and dS and the CCE dz included), every
@@ -200,6 +211,12 @@ def test_step_parity_bf16(variant):
         plan = r.attention_backward_plan()
         note(f"  attention backward plan {plan}")
         assert plan["qk_epilogue"], plan
+    if any(variant is x for x in SPLIT_VARIANTS):
+        plan = r.attention_backward_plan()
+        note(f"  attention backward plan {plan}")
+        # 16 sequences x 4 KV heads x 2 key blocks = 128, launched as 2 x 128
+        assert plan["path"] == "recompute" and plan["dkv_blocks"] == 256, plan
+        assert plan["qk_epilogue"] == (variant is RECOMPUTE_GQA4), plan
     keys = tensor_keys(cfg)
     loss_ref = m.forward_backward(tok, tgt)
     loss = r.forward_backward(tok, tgt)
@@ -231,7 +248,10 @@ LORA_QV = dict(lora_targets=0x5 | 0x40, lora_rank=8, lora_alpha=16.0)
     (1, dict(head_dim=128, n_heads=16, n_kv_heads=8, rotary_dim=128, n_seqs=16, n_pos=128,
              ff_dim=512, vocab_size=1024, n_layers=4)),
     (1, dict(head_dim=128, n_heads=16, n_kv_heads=8, rotary_dim=128, n_seqs=16, n_pos=128,
-             ff_dim=512, vocab_size=1024, n_layers=4, **LORA_QV))])
+             ff_dim=512, vocab_size=1024, n_layers=4, **LORA_QV)),
+    # GQA 4:1 with the split dK/dV launch
+    (1, dict(head_dim=128, n_heads=16, n_kv_heads=4, rotary_dim=128, n_seqs=16, n_pos=256,
+             ff_dim=512, vocab_size=1024, n_layers=4))])
 def test_activation_recompute_bit_identical(precision, over):
     import valkyr_amd as v
     from valkyr_amd.runner import ADAM_M, ADAM_V, GRAD, PARAM
@@ -442,8 +462,8 @@ def test_step_bf16_vs_pure_fp32_oracle():
     (1, dict(lora_targets=0x7F, n_layers=3)), (0, dict(lora_targets=0x55, lora_rank=8)),
     (1, dict(HD128, lora_targets=0xF)),
     # the recompute attention path at a grid that leaves CUs idle: dQ runs on
-    # a second stream beside dK/dV
-    (1, dict(RECOMPUTE, lora_targets=0xF))])
+    # a second stream beside dK/dV (and with GQA 4:1, the split dK/dV launch)
+    (1, dict(RECOMPUTE, lora_targets=0xF)), (1, dict(RECOMPUTE_GQA4, lora_targets=0xF))])
 def test_lora_step_parity(precision, over):
     """Config-4 shape class: LoRA r=16 on q/k/v/o (and every projection, and
     a rank-8 subset), B = 0 init, frozen base.  fp32: every adapter gradient

@@ -1216,7 +1216,12 @@ static_assert(2 * STREAM + BN * HD * 2 <= LDS, "tile streams and V slices exceed
 // NH: query heads per head group (hpk / 2) when known at compile time (1 for
 // GQA 2:1, 2 for 4:1), 0 to read it from the shape; a constant turns the
 // per-tile (head, query tile) split of the iteration index into shifts.
-template <int NWV, bool QKE, int NH = 0>
+// PARTS = 2: the block's query heads are split between two blocks (blockIdx.z),
+// each summing half of every head group's heads and writing its raw dK / dV
+// (fp32, dK scaled) into its own slice of p.split_ws; fa_dkv_combine_k adds the
+// two slices in part order and runs the epilogue.  That doubles the grid where
+// the (sequence, KV head, key block) grid alone leaves CUs idle.
+template <int NWV, bool QKE, int NH = 0, int PARTS = 1>
 __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPtrs p) {
     using namespace dkv4;
     constexpr int NS = NWV / 2;                 // key slices per head group
@@ -1230,8 +1235,11 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     __shared__ __attribute__((aligned(16))) float Ls[2][NBUF][64], Dd[2][NBUF][64];
 
     const int kt = (int)blockIdx.y;
+    static_assert(PARTS == 1 || !QKE, "a split launch leaves the epilogue to the combine kernel");
     const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
-    const int hpk = s.n_heads / s.n_kv_heads, nh = NH ? NH : hpk / 2;
+    const int hpk = s.n_heads / s.n_kv_heads;
+    const int nh = (NH ? NH : hpk / 2) / PARTS;  // this block's heads per head group
+    const int zp = PARTS > 1 ? (int)blockIdx.z : 0;  // this block's half of the heads
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int sl = wave % NS, hg = wave / NS;  // key slice, head group
@@ -1287,7 +1295,7 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     const sgpr4 rs = rsrc4((tdo ? p.d : p.lse) + (long)b * s.n_q * s.n_heads,
                            (unsigned)((long)s.n_q * s.n_heads * 4));
     auto tile_of = [&](int it, int &h, int &q0) {
-        h = kvh * hpk + hg + 2 * (it % nh);
+        h = kvh * hpk + hg + 2 * (zp * nh + it % nh);
         q0 = qstart + (nqt - 1 - it / nh) * BM;
     };
     // 9 vector-memory operations per wave and tile: instruction i fills tile
@@ -1477,7 +1485,12 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
     if (hg == 0) give(dkt);
     else give(dvt);
     __syncthreads();
-    if constexpr (!QKE) {
+    if constexpr (PARTS > 1) {
+        const long R = (long)s.n_batch * s.n_kv, kvd = (long)s.n_kv_heads * HD;
+        float *wk = p.split_ws + (long)zp * 2 * R * kvd, *wv = wk + R * kvd;
+        if (hg == 0) keep(dvt, wv, kvd, 1.0f);
+        else keep(dkt, wk, kvd, s.inv_sqrt_dim);
+    } else if constexpr (!QKE) {
         if (hg == 0) keep(dvt, p.dv, p.lddv, 1.0f);
         else keep(dkt, p.dk, p.lddk, s.inv_sqrt_dim);
     } else {
@@ -1509,6 +1522,62 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dkv4_k(AttnShape s, AttnPt
         if (e.gk) {
             const int blk = blockIdx.y * gridDim.x + blockIdx.x;
             qk_dw_block(dw, red, sl, NS, hg == 1, lane, e.pk + (long)blk * 128);
+        }
+    }
+}
+
+// The two slices of a split dK / dV launch (p.split_ws: [part][dK, dV][rows][kvd]
+// fp32) added in part order, then written as the unsplit kernel writes them:
+// with the fused epilogue (QKE) dV as bf16 and dK through RoPE^T and the
+// K-RMSNorm backward as bf16 into the gradient rows, the gain gradient as one
+// 128-wide partial row per block; otherwise fp32 dK and dV.  Block = 64 rows
+// of one KV head, 4 waves of 16 rows in the accumulator row layout
+// (lane (g, c) holds elements 16 i + 4 g + r of row c).
+template <bool QKE>
+__global__ __launch_bounds__(256) void fa_dkv_combine_k(AttnShape s, AttnPtrs p) {
+    constexpr int HD = 128;
+    __shared__ float red[4 * HD];
+    const int kvh = blockIdx.y;
+    const int lane = threadIdx.x % 64, g = lane / 16, c16 = lane % 16;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / 64);
+    const long R = (long)s.n_batch * s.n_kv, kvd = (long)s.n_kv_heads * HD;
+    const long t = (long)blockIdx.x * 64 + 16 * wave + c16;  // row b * n_kv + key
+    const bool ok = t < R;
+    const long tt = ok ? t : 0;
+    const float *k0 = p.split_ws + tt * kvd + kvh * HD + 4 * g, *k1 = k0 + 2 * R * kvd;
+    const float *v0 = k0 + R * kvd, *v1 = k1 + R * kvd;
+    float vk[8][4], vv[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        float4 a = make_float4(0.f, 0.f, 0.f, 0.f), bb = a, c = a, d = a;
+        if (ok) {
+            a = *reinterpret_cast<const float4 *>(k0 + 16 * i);
+            bb = *reinterpret_cast<const float4 *>(k1 + 16 * i);
+            c = *reinterpret_cast<const float4 *>(v0 + 16 * i);
+            d = *reinterpret_cast<const float4 *>(v1 + 16 * i);
+        }
+        vk[i][0] = a.x + bb.x; vk[i][1] = a.y + bb.y; vk[i][2] = a.z + bb.z; vk[i][3] = a.w + bb.w;
+        vv[i][0] = c.x + d.x; vv[i][1] = c.y + d.y; vv[i][2] = c.z + d.z; vv[i][3] = c.w + d.w;
+    }
+    if constexpr (QKE) {
+        const QkEpi &e = p.qk;
+        float dw[8][4] = {};
+        const int kcol = s.n_heads * HD + kvh * HD, vcol = kcol + s.n_kv_heads * HD;
+        const int pos = (int)(tt % s.n_kv);
+        qk_row_bwd(vk, dw, ok, e, e.x + tt * e.ldx + kcol, e.gk, pos, g);
+        if (ok) {
+            st_row_bf16(e.out + tt * e.ldout + kcol, vk, g);
+            st_row_bf16(e.out + tt * e.ldout + vcol, vv, g);
+        }
+        if (e.gk && e.pk)  // uniform
+            qk_dw_block(dw, red, wave, 4, true, lane,
+                        e.pk + ((long)blockIdx.y * gridDim.x + blockIdx.x) * HD);
+    } else if (ok) {
+        float *dk = p.dk + t * p.lddk + kvh * HD + 4 * g, *dv = p.dv + t * p.lddv + kvh * HD + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            *reinterpret_cast<float4 *>(dk + 16 * i) = make_float4(vk[i][0], vk[i][1], vk[i][2], vk[i][3]);
+            *reinterpret_cast<float4 *>(dv + 16 * i) = make_float4(vv[i][0], vv[i][1], vv[i][2], vv[i][3]);
         }
     }
 }
@@ -2215,8 +2284,17 @@ bool fa_bw_v4_preferred(const AttnShape &s) {
 // is one of the common ones.
 template <int W, bool QKE>
 void launch_dkv4(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
-    const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
     const int nh = s.n_heads / s.n_kv_heads / 2;
+    if (p.split_ws && fa_bw_v4_split(s)) {
+        // two blocks per (sequence, KV head, key block), then their sum and the epilogue
+        const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN, 2);
+        if (nh == 2) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, false, 2, 2>), gkv, dim3(W * 64), 0, st, s, p);
+        else hipLaunchKernelGGL((fa_bwd_dkv4_k<W, false, 0, 2>), gkv, dim3(W * 64), 0, st, s, p);
+        const dim3 gc((unsigned)(((long)s.n_batch * s.n_kv + 63) / 64), s.n_kv_heads);
+        hipLaunchKernelGGL(fa_dkv_combine_k<QKE>, gc, dim3(256), 0, st, s, p);
+        return;
+    }
+    const dim3 gkv(s.n_kv_heads * s.n_batch, s.n_kv / dkv4::BN);
     if (nh == 1) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 1>), gkv, dim3(W * 64), 0, st, s, p);
     else if (nh == 2) hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 2>), gkv, dim3(W * 64), 0, st, s, p);
     else hipLaunchKernelGGL((fa_bwd_dkv4_k<W, QKE, 0>), gkv, dim3(W * 64), 0, st, s, p);
@@ -2271,6 +2349,23 @@ int fa_bw_v4_q_blocks(const AttnShape &s) {
 }
 int fa_bw_v4_q_rows(const AttnShape &s) { return dq4_bq(s); }
 int fa_bw_v4_kv_blocks(const AttnShape &s) { return s.n_kv_heads * s.n_batch * (s.n_kv / dkv4::BN); }
+// The split dK/dV launch: where the (sequence, KV head, key block) grid has
+// fewer blocks than CUs and each head group holds an even number of query
+// heads to divide (config 4: 128 blocks of 4-head groups at 1 x 2048 -> 256).
+bool fa_bw_v4_split(const AttnShape &s) {
+    return fa_bw_v4_ok(s) && (s.n_heads / s.n_kv_heads / 2) % 2 == 0 && fa_bw_v4_kv_blocks(s) < 256;
+}
+size_t fa_bw_v4_split_ws_floats(const AttnShape &s) {
+    return fa_bw_v4_split(s) ? (size_t)4 * s.n_batch * s.n_kv * s.n_kv_heads * dkv4::HD : 0;
+}
+int fa_bw_v4_kv_launch_blocks(const AttnShape &s, bool split) {
+    return split && fa_bw_v4_split(s) ? 2 * fa_bw_v4_kv_blocks(s) : fa_bw_v4_kv_blocks(s);
+}
+int fa_bw_v4_k_gain_parts(const AttnShape &s, bool split) {
+    if (split && fa_bw_v4_split(s))
+        return (int)(((long)s.n_batch * s.n_kv + 63) / 64) * s.n_kv_heads;
+    return fa_bw_v4_kv_blocks(s);
+}
 // The epilogue's row layout assumes head_dim 128 and a rotary span of 0 or
 // the whole head (pairs 64 apart).
 bool fa_bw_qk_epi_ok(const AttnShape &s, int rotary_dim) {

@@ -115,7 +115,128 @@ int rows_per_2g_chunk(long rows, long ld, long run) {
     return (int)(((rows + n - 1) / n + 63) / 64 * 64);
 }
 
+// ── LoRA term in the epilogue ──────────────────────────────────────────
+// EpiLora<Base> adds rank-r LoRA products (train/lora.zig:99-251) to the tile
+// before Base stores it:
+//   C[t, col_s + c] = acc + alpha sum_i U_s[t, i] F_s(c, i)
+// for every adapter s whose columns [col_s, col_s + ncols) hold c: the
+// forward's y += aor inter B^T, or the backward's dx += aor (dy B) A summed
+// over the adapters of one shared input.  The output is then written once,
+// instead of stored by the GEMM, read back and stored again by a separate
+// update pass.  The products run on v_mfma_f32_16x16x4_f32 in the
+// accumulator layout: lane (g, c) supplies A[c][k] = alpha U_s[row0 + 16 i + c][k]
+// and B[k][c] = F_s(col0 + 16 j + c - col_s, k) for the contraction index
+// k = 16 kb + 4 g + e at step e, so the results land on acc[i][j] where Base
+// reads them.  Base's own alpha must be 1 (the linear layers' products).
+template <class Base>
+struct EpiLora {
+    Base base;
+    LoraSegs sg;
+    int r;
+    float alpha;
+
+    template <int TM, int TN>
+    VKH_DEV void apply(const f32x4 (&acc_in)[TM][TN], const FragPos &fp, const GemmShape &s) const {
+        f32x4 acc[TM][TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) acc[i][j] = acc_in[i][j];
+        const int g = fp.lane / 16, c = fp.lane % 16;
+        for (int si = 0; si < sg.n; ++si) {
+            const LoraSeg &q = sg.s[si];
+            // wave-uniform: none of the wave's columns in this adapter's range
+            if (fp.col0 + 16 * TN <= q.col || fp.col0 >= q.col + q.ncols) continue;
+            for (int kb = 0; kb < r; kb += 16) {
+                const int k = kb + 4 * g;
+                const bool kok = k < r;  // r is a multiple of 4
+                f32x4 ua[TM];
+#pragma unroll
+                for (int i = 0; i < TM; ++i) {
+                    const int row = fp.row0 + 16 * i + c;
+                    float4 t = make_float4(0.f, 0.f, 0.f, 0.f);
+                    if (kok && row < s.M) t = *reinterpret_cast<const float4 *>(q.u + (long)row * q.ldu + k);
+                    ua[i] = f32x4{alpha * t.x, alpha * t.y, alpha * t.z, alpha * t.w};
+                }
+#pragma unroll
+                for (int j = 0; j < TN; ++j) {
+                    const long cb = fp.col0 + 16 * j;  // wave-uniform
+                    if (cb < q.col || cb >= q.col + q.ncols) continue;
+                    const long cc = cb + c - q.col;
+                    f32x4 fb = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (kok) {
+                        if (q.fsc == 1) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) fb[e] = q.f[(long)(k + e) * q.fsi + cc];
+                        } else {
+                            const float4 t = *reinterpret_cast<const float4 *>(q.f + cc * q.fsc + k);
+                            fb = f32x4{t.x, t.y, t.z, t.w};
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < TM; ++i)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) acc[i][j] = mfma16x16x4(ua[i][e], fb[e], acc[i][j]);
+                }
+            }
+        }
+        base.template apply<TM, TN>(acc, fp, s);
+    }
+};
+
+bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
+
+// The adapters' layout rules of EpiLora on an output of n_out columns:
+// 16-column blocks, whole 16-byte U rows and factor reads, r <= 64.
+bool lora_epi_ok(const LoraSegs &g, int r, int n_out) {
+    if (r < 1 || r > 64 || r % 4 || g.n < 1 || g.n > 3) return false;
+    for (int i = 0; i < g.n; ++i) {
+        const LoraSeg &q = g.s[i];
+        if (q.col < 0 || q.col % 16 || q.ncols <= 0 || q.ncols % 16 || q.col + q.ncols > n_out) return false;
+        if (!q.u || !al16(q.u) || q.ldu % 4 || q.ldu < r || !q.f) return false;
+        if (q.fsc != 1 && (!al16(q.f) || q.fsc % 4 || q.fsi != 1)) return false;
+    }
+    return true;
+}
+
 }  // namespace
+
+bool g16_lora_ok(const bf16 *a, long lda, long arows, long arun, const bf16 *b, long ldb, long brows,
+                 long brun, const LoraSegs &g, int r, int n_out) {
+    Op16 oa, ob;
+    return make_op(a, lda, arows, arun, oa) && make_op(b, ldb, brows, brun, ob) &&
+           lora_epi_ok(g, r, n_out);
+}
+
+hipError_t g16_nt_lora(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
+                       int N, int K, const float *R, long ldr, const LoraSegs &g, int r,
+                       float alpha, const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op(x, ldx, M, K, a) || !make_op(w, ldw, N, K, b) || !lora_epi_ok(g, r, N))
+        return hipErrorInvalidValue;
+    EpiLora<EpiStore> e{EpiStore{y, ldy, R, ldr, 1.f, 0.f}, g, r, alpha};
+    return run16<Lay::K, Lay::K>(a, b, GemmShape{M, N, K}, e, ws, st);
+}
+
+hipError_t g16_nn_lora(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx,
+                       int M, int N, int K, const LoraSegs &g, int r, float alpha, const GemmWs &ws,
+                       hipStream_t st) {
+    Op16 a, b;
+    if (!make_op(dy, lddy, M, N, a) || !make_op(w, ldw, N, K, b) || !lora_epi_ok(g, r, K))
+        return hipErrorInvalidValue;
+    EpiLora<EpiStore> e{EpiStore{dx, lddx, nullptr, 0, 1.f, 0.f}, g, r, alpha};
+    return run16<Lay::K, Lay::MN>(a, b, GemmShape{M, K, N}, e, ws, st);
+}
+
+hipError_t g16_nn_bf16_lora(const bf16 *dy, long lddy, const bf16 *w, long ldw, bf16 *dx,
+                            long lddx, int M, int N, int K, const LoraSegs &g, int r, float alpha,
+                            const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op(dy, lddy, M, N, a) || !make_op(w, ldw, N, K, b) || !lora_epi_ok(g, r, K))
+        return hipErrorInvalidValue;
+    EpiLora<EpiStoreBf16> e{EpiStoreBf16{dx, lddx, 1.f}, g, r, alpha};
+    return run16<Lay::K, Lay::MN>(a, b, GemmShape{M, K, N}, e, ws, st);
+}
 
 hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
                   int N, int K, const float *R, long ldr, float alpha, float beta,

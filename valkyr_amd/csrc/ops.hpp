@@ -80,6 +80,23 @@ hipError_t lora_update(float *y, long ldy, int T, int r, const LoraSegs &g, floa
                        hipStream_t st);
 bool lora_fast_ok(DType xt, const void *x, long ldx, int r, const LoraSegs &g);
 bool lora_update_ok(const float *y, long ldy, int r, const LoraSegs &g);
+// The bf16-operand GEMMs with lora_update's term added in their epilogue
+// (k_gemm16.hip): the output written once, U_s and F_s as for lora_update
+// (alpha the LoRA scale; the base product unscaled).  g16_lora_ok: both
+// operands ([arows, arun] and [brows, brun] views) and the adapters fit the
+// fused form on an output of n_out columns; the entry points return
+// hipErrorInvalidValue where it does not.
+bool g16_lora_ok(const bf16 *a, long lda, long arows, long arun, const bf16 *b, long ldb, long brows,
+                 long brun, const LoraSegs &g, int r, int n_out);
+hipError_t g16_nt_lora(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
+                       int N, int K, const float *R, long ldr, const LoraSegs &g, int r,
+                       float alpha, const GemmWs &ws, hipStream_t st);
+hipError_t g16_nn_lora(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx,
+                       int M, int N, int K, const LoraSegs &g, int r, float alpha, const GemmWs &ws,
+                       hipStream_t st);
+hipError_t g16_nn_bf16_lora(const bf16 *dy, long lddy, const bf16 *w, long ldw, bf16 *dx,
+                            long lddx, int M, int N, int K, const LoraSegs &g, int r, float alpha,
+                            const GemmWs &ws, hipStream_t st);
 
 // One projection group's adapters (train/lora.zig:99-251 for each): up to
 // three adapters that read one activation x [T, k] and own column blocks
@@ -262,6 +279,9 @@ struct AttnPtrs {
     // D = rowsum(O dO) for its rows itself (written to d) and runs first
     const void *o16 = nullptr; long ldo16 = 0;
     QkEpi qk;  // recompute path only
+    // recompute path: workspace of fa_bw_v4_split_ws_floats(s) floats; when set
+    // on a shape fa_bw_v4_split accepts, the dK / dV launch is split in two
+    float *split_ws = nullptr;
 };
 // fp32 attention on the matrix cores (k_attn_f32.hip) for the shapes
 // fa_f32m_ok accepts; each launcher returns false, launching nothing, for a
@@ -298,6 +318,11 @@ bool fa_bw_v4_preferred(const AttnShape &s);
 hipError_t fa_bw_v4_part(const AttnShape &s, const AttnPtrs &p, int which, hipStream_t st);
 int fa_bw_v4_q_blocks(const AttnShape &s);
 int fa_bw_v4_q_rows(const AttnShape &s);  // query rows per dQ block
+bool fa_bw_v4_split(const AttnShape &s);
+size_t fa_bw_v4_split_ws_floats(const AttnShape &s);
+// dK/dV blocks launched, and K-gain partial rows written, with or without the split
+int fa_bw_v4_kv_launch_blocks(const AttnShape &s, bool split);
+int fa_bw_v4_k_gain_parts(const AttnShape &s, bool split);
 int fa_bw_v4_kv_blocks(const AttnShape &s);
 bool fa_bw_qk_epi_ok(const AttnShape &s, int rotary_dim);
 size_t fa_bw_ws_bytes(const AttnShape &s, bool v4);

@@ -132,6 +132,7 @@ struct vkh_runner {
     bf16 *attn_ds = nullptr;  // bf16 dS of the fused attention backward (when it needs one)
     bool attn_fused = false;  // bf16 attention backward on fa_bw_fused
     bool attn_v4 = false;     // ... on its recompute kernels (no dS workspace)
+    float *attn_split = nullptr;  // ... with the dK/dV launch split in two (its workspace)
     bool qk_fused = false;    // ... with RoPE^T / Q/K-norm backward in their epilogues
     // ... with the dQ kernel on a second stream beside dK/dV (one stream
     // otherwise: no side stream, and the dK/dV grid leaves CUs idle)
@@ -487,6 +488,8 @@ struct vkh_runner {
             attn_v4 = attn_fused && fa_bw_v4_preferred(attn_shape());
             qk_fused = attn_v4 && fa_bw_qk_epi_ok(attn_shape(), (int)cfg.rotary_dim);
             attn_fork = attn_v4 && lora && fa_bw_v4_kv_blocks(attn_shape()) < 256;
+            if (attn_v4 && fa_bw_v4_split(attn_shape()))
+                VKH_TRY(alloc(attn_split, fa_bw_v4_split_ws_floats(attn_shape())));
             if (attn_fused && fa_bw_ws_bytes(attn_shape(), attn_v4))
                 VKH_TRY(alloc(attn_ds, fa_bw_ws_bytes(attn_shape(), attn_v4) / sizeof(bf16)));
             // split-K workspace: the largest the planner asks for over the step's GEMMs
@@ -601,7 +604,7 @@ struct vkh_runner {
         size_t n = qkv_partial_floats(qkv_layout());
         if (qk_fused) {
             const AttnShape as = attn_shape();
-            n = std::max(n, (size_t)(fa_bw_v4_q_blocks(as) + fa_bw_v4_kv_blocks(as)) * hd);
+            n = std::max(n, (size_t)(fa_bw_v4_q_blocks(as) + fa_bw_v4_k_gain_parts(as, attn_split)) * hd);
         }
         return n;
     }
@@ -790,6 +793,69 @@ struct vkh_runner {
         }
         return VKH_OK;
     }
+    // y = x W^T (+ Rr) with the LoRA terms of the targets among `ps`: in the
+    // bf16 precision the update rides in the GEMM's epilogue (inter first,
+    // then one GEMM), else the GEMM and lora_fwd_group's update pass.
+    vkh_status linear_fwd_lora(int l, std::initializer_list<int> ps, Mat x, const Span &w, float *y,
+                               long ldy, int N, int K, const float *Rr, long ldr) {
+        LoraAdapter ad[3];
+        const int na = b16() ? lora_adapters(l, ps, ad) : 0;
+        if (na) {
+            const LoraGroupSegs gs = lora_group_segs(ad, na, R);
+            if (lora_fast_ok(x.dt, x.p, x.ld, R, gs.fwd_rows) &&
+                g16_lora_ok((const bf16 *)x.p, x.ld, T, K, Wb(w), K, N, K, gs.fwd_upd, R, N)) {
+                VKH_HIP(lora_rows(x.dt, x.p, x.ld, T, R, gs.fwd_rows, 1.f, cur));
+                VKH_HIP(g16_nt_lora((const bf16 *)x.p, x.ld, Wb(w), K, y, ldy, T, N, K, Rr, ldr,
+                                    gs.fwd_upd, R, aor, gws, cur));
+                return VKH_OK;
+            }
+        }
+        VKH_TRY(linear_fwd(x, w, y, ldy, N, K, Rr, ldr));
+        return lora_fwd_group(l, ps, x, y, ldy);
+    }
+    // Whether dx_lora can fuse the LoRA dx term of `ps` into the dx GEMM.
+    bool dx_lora_fused(int l, std::initializer_list<int> ps, Mat dy, Mat x, const Span &w, int N,
+                       int K) {
+        LoraAdapter ad[3];
+        const int na = b16() ? lora_adapters(l, ps, ad) : 0;
+        if (!na) return false;
+        const LoraGroupSegs gs = lora_group_segs(ad, na, R);
+        return lora_fast_ok(dy.dt, dy.p, dy.ld, R, gs.bwd_rows) &&
+               lora_fast_ok(x.dt, x.p, x.ld, R, gs.bwd_da) &&
+               lora_fast_ok(dy.dt, dy.p, dy.ld, R, gs.bwd_db) &&
+               g16_lora_ok((const bf16 *)dy.p, dy.ld, T, N, Wb(w), K, N, K, gs.bwd_upd, R, K);
+    }
+    // dx = dy W plus the LoRA backward of the targets among `ps` (dx term,
+    // dA, dB): where dx_lora_fused holds, dy B first, dA / dB on the side
+    // stream, and the dx term in the dx GEMM's epilogue (fp32 dx, or bf16
+    // into dxb); otherwise the GEMM then lora_bwd_group (fp32 dx only).
+    vkh_status dx_lora(int l, std::initializer_list<int> ps, Mat dy, Mat x, const Span &w, float *dx,
+                       bf16 *dxb, long lddx, int N, int K) {
+        if (!dx_lora_fused(l, ps, dy, x, w, N, K)) {
+            if (dxb) return fail(VKH_ERR_UNSUPPORTED, "bf16 dx with an unfused LoRA term");
+            VKH_TRY(linear_dx(dy, w, dx, lddx, N, K));
+            return lora_bwd_group(l, ps, dy, x, dx, lddx);
+        }
+        LoraAdapter ad[3];
+        const int na = lora_adapters(l, ps, ad);
+        const LoraGroupSegs gs = lora_group_segs(ad, na, R);
+        VKH_HIP(lora_rows(dy.dt, dy.p, dy.ld, T, R, gs.bwd_rows, 1.f, cur));
+        hipStream_t cs = cur;
+        if (lora_aux) {
+            VKH_HIP(hipEventRecord(ev_fork, cur));
+            VKH_HIP(hipStreamWaitEvent(aux, ev_fork, 0));
+            cs = aux;
+        }
+        VKH_HIP(lora_cols(x.dt, x.p, x.ld, T, R, gs.bwd_da, aor, cs));
+        VKH_HIP(lora_cols(dy.dt, dy.p, dy.ld, T, R, gs.bwd_db, aor, cs));
+        if (dxb)
+            VKH_HIP(g16_nn_bf16_lora((const bf16 *)dy.p, dy.ld, Wb(w), K, dxb, lddx, T, N, K,
+                                     gs.bwd_upd, R, aor, gws, cur));
+        else
+            VKH_HIP(g16_nn_lora((const bf16 *)dy.p, dy.ld, Wb(w), K, dx, lddx, T, N, K, gs.bwd_upd, R,
+                                aor, gws, cur));
+        return VKH_OK;
+    }
     // inter = x A^T, the rank-r intermediate the LoRA backward reads (dB)
     vkh_status lora_inter(int l, int p, Mat x) {
         int N, K;
@@ -885,8 +951,7 @@ struct vkh_runner {
         VKH_HIP(rmsnorm_forward(x_in, W(s.t[0]), b16() ? (void *)a.n1b : (void *)a.n1, odt, T, D,
                                 cfg.rms_eps, 0, cur));
         const Mat n1 = m_n1(a);
-        VKH_TRY(linear_fwd(n1, s.t[1], a.qkv, qkvd, qkvd, D, nullptr, 0));
-        VKH_TRY(lora_fwd_group(l, {0, 1, 2}, n1, a.qkv, qkvd));
+        VKH_TRY(linear_fwd_lora(l, {0, 1, 2}, n1, s.t[1], a.qkv, qkvd, qkvd, D, nullptr, 0));
         const QkvLayout ql = qkv_layout();
         VKH_HIP(qkv_prepare_forward(ql, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                     cfg.qk_norm ? W(s.t[10]) : nullptr, a.qkv_attn, qkvd, adt,
@@ -904,20 +969,17 @@ struct vkh_runner {
         }
         // mid = x_in + attn_out W_o^T (+ LoRA)
         const Mat att = m_attn(a);
-        VKH_TRY(linear_fwd(att, s.t[4], a.mid, D, D, qd, x_in, D));
-        VKH_TRY(lora_fwd_group(l, {3}, att, a.mid, D));
+        VKH_TRY(linear_fwd_lora(l, {3}, att, s.t[4], a.mid, D, D, qd, x_in, D));
         VKH_HIP(rmsnorm_forward(a.mid, W(s.t[5]), b16() ? (void *)a.n2b : (void *)a.n2, odt, T, D,
                                 cfg.rms_eps, 0, cur));
         const Mat n2 = m_n2(a);
-        VKH_TRY(linear_fwd(n2, s.t[6], a.gu, 2 * F, 2 * F, D, nullptr, 0));
-        VKH_TRY(lora_fwd_group(l, {4, 5}, n2, a.gu, 2 * F));
+        VKH_TRY(linear_fwd_lora(l, {4, 5}, n2, s.t[6], a.gu, 2 * F, 2 * F, D, nullptr, 0));
         VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F, b16() ? (void *)a.gatedb : (void *)a.gated,
                                F, odt, T, F, cur));
         const Mat gt = m_gated(a);
         if (!need_y) return lora_fwd_group(l, {6}, gt, nullptr, 0, false);
         // y = mid + gated W_down^T (+ LoRA)
-        VKH_TRY(linear_fwd(gt, s.t[8], a.y, D, D, F, a.mid, D));
-        VKH_TRY(lora_fwd_group(l, {6}, gt, a.y, D));
+        VKH_TRY(linear_fwd_lora(l, {6}, gt, s.t[8], a.y, D, D, F, a.mid, D));
         return VKH_OK;
     }
 
@@ -1001,9 +1063,8 @@ struct vkh_runner {
         const Mat mdy = b16() ? matb(dyb, D) : matf(dy, D);
         // transformer.zig:1967-2070 (order), train_decoder.zig:340-498 (math)
         // down: d_gated = dy W_down;  dW_down = dy^T gated
-        VKH_TRY(linear_dx(mdy, s.t[8], d_gated, F, D, F));
+        VKH_TRY(dx_lora(l, {6}, mdy, m_gated(a), s.t[8], d_gated, nullptr, F, D, F));
         VKH_TRY(linear_dw(mdy, m_gated(a), s.t[8], D, F));
-        VKH_TRY(lora_bwd_group(l, {6}, mdy, m_gated(a), d_gated, F));
         // swiglu: d_gu = [d_gate | d_up] (bf16 copy only in the bf16 precision)
         if (b16())
             VKH_HIP(swiglu_backward(d_gated, F, a.gu, 2 * F, a.gu + F, 2 * F, d_gub, 2 * F, d_gub + F,
@@ -1013,9 +1074,8 @@ struct vkh_runner {
                                     2 * F, DType::F32, T, F, cur));
         const Mat mdgu = b16() ? matb(d_gub, 2 * F) : matf(d_gu, 2 * F);
         // gate/up (one [2F, D] matrix): d_n2 = d_gu W_gu; dW_gu = d_gu^T n2
-        VKH_TRY(linear_dx(mdgu, s.t[6], d_n, D, 2 * F, D));
+        VKH_TRY(dx_lora(l, {4, 5}, mdgu, m_n2(a), s.t[6], d_n, nullptr, D, 2 * F, D));
         VKH_TRY(linear_dw(mdgu, m_n2(a), s.t[6], 2 * F, D));
-        VKH_TRY(lora_bwd_group(l, {4, 5}, mdgu, m_n2(a), d_n, D));
         // n2: d_mid = rmsnorm_bw(d_n2) + dy
         VKH_HIP(rmsnorm_backward(d_n, a.mid, W(s.t[5]), d_mid, d_midb, dy,
                                  concurrent ? nullptr : Gd(s.t[5]), concurrent ? lg[l].pn2 : partial,
@@ -1025,14 +1085,16 @@ struct vkh_runner {
         // attention path without a LoRA term on o, dO goes straight to bf16 (the
         // attention kernels' operand) and D = rowsum(O dO) reads both in bf16.
         const AttnShape as = attn_shape();
-        const bool do_bf16 = b16() && adt == DType::BF16 && !proj_lora(3);
-        if (do_bf16)
+        const bool o_lora = proj_lora(3);
+        const bool do_bf16 = b16() && adt == DType::BF16 &&
+                             (!o_lora || dx_lora_fused(l, {3}, mdmid, m_attn(a), s.t[4], D, qd));
+        if (do_bf16 && !o_lora)
             VKH_HIP(g16_nn_bf16((const bf16 *)mdmid.p, mdmid.ld, Wb(s.t[4]), qd, dout16, qd, T, D,
                                 qd, gws, cur));
         else
-            VKH_TRY(linear_dx(mdmid, s.t[4], d_attn_out, qd, D, qd));
+            VKH_TRY(dx_lora(l, {3}, mdmid, m_attn(a), s.t[4], d_attn_out, do_bf16 ? dout16 : nullptr,
+                            qd, D, qd));
         VKH_TRY(linear_dw(mdmid, m_attn(a), s.t[4], D, qd));
-        VKH_TRY(lora_bwd_group(l, {3}, mdmid, m_attn(a), d_attn_out, qd));
         // attention: D, dK/dV, dQ into the fused d_qkv buffer
         if (b16() && adt == DType::BF16) {
             if (!do_bf16) VKH_HIP(cast_f32_to_bf16(d_attn_out, dout16, (size_t)T * qd, cur));
@@ -1055,6 +1117,7 @@ struct vkh_runner {
         ap.dk = d_qkv + qd; ap.lddk = qkvd;
         ap.dv = d_qkv + qd + kvd; ap.lddv = qkvd;
         ap.dt = adt;
+        ap.split_ws = attn_split;
         if (attn_v4 && !attn_fork) {
             ap.o16 = a.attn_b;
             ap.ldo16 = qd;
@@ -1091,11 +1154,11 @@ struct vkh_runner {
             VKH_TRY(attn_bw());
             if (qk_side) {
                 lg[l].pq = e.pq; lg[l].pk = e.pk;
-                lg[l].q_parts = nq; lg[l].k_parts = fa_bw_v4_kv_blocks(as);
+                lg[l].q_parts = nq; lg[l].k_parts = fa_bw_v4_k_gain_parts(as, attn_split);
                 lg[l].qk_stride = hd;
             } else if (cfg.qk_norm && !lora) {
                 VKH_HIP(column_sums(e.pq, nq, hd, hd, Gd(s.t[9]), cur));
-                VKH_HIP(column_sums(e.pk, fa_bw_v4_kv_blocks(as), hd, hd, Gd(s.t[10]), cur));
+                VKH_HIP(column_sums(e.pk, fa_bw_v4_k_gain_parts(as, attn_split), hd, hd, Gd(s.t[10]), cur));
             }
         } else {
             if (attn_fused) {
@@ -1120,9 +1183,8 @@ struct vkh_runner {
         }
         const Mat mdqkv = b16() ? matb(d_qkvb, qkvd) : matf(d_qkv, qkvd);
         // q/k/v (one [qkvd, D] matrix): d_n1 = d_qkv W_qkv; dW_qkv = d_qkv^T n1
-        VKH_TRY(linear_dx(mdqkv, s.t[1], d_n, D, qkvd, D));
+        VKH_TRY(dx_lora(l, {0, 1, 2}, mdqkv, m_n1(a), s.t[1], d_n, nullptr, D, qkvd, D));
         VKH_TRY(linear_dw(mdqkv, m_n1(a), s.t[1], qkvd, D));
-        VKH_TRY(lora_bwd_group(l, {0, 1, 2}, mdqkv, m_n1(a), d_n, D));
         // n1: d_x_in = rmsnorm_bw(d_n1) + d_mid
         VKH_HIP(rmsnorm_backward(d_n, x_in, W(s.t[0]), dxo, dxob, d_mid,
                                  concurrent ? nullptr : Gd(s.t[0]), concurrent ? lg[l].pn1 : partial,
@@ -1763,7 +1825,7 @@ vkh_status vkh_runner_attention_backward_plan(const vkh_runner *r, uint32_t out[
         const AttnShape s = r->attn_shape();
         out[1] = (uint32_t)fa_bw_v4_q_rows(s);
         out[2] = (uint32_t)fa_bw_v4_q_blocks(s);
-        out[3] = (uint32_t)fa_bw_v4_kv_blocks(s);
+        out[3] = (uint32_t)fa_bw_v4_kv_launch_blocks(s, r->attn_split != nullptr);
         out[4] = r->qk_fused ? 1u : 0u;
     }
     return VKH_OK;
