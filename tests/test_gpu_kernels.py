@@ -195,6 +195,37 @@ def test_linear_gemms(prec, shape):
     assert rel_l2(dW_ref, host(bdW)) < tol
 
 
+# fp32 operands on the DMA-staged kernels (precision FP32): shapes that reach
+# each tile plan in the forward, dx and dW layouts (256 x 256; 128 x 128 on 8
+# waves; 128 x 64 with the in-block split of K; plain 128 x 64), ragged edges
+# at multiples of 4, and a shape whose extents are not multiples of 4 (the
+# generic kernel).
+GEMM32_SHAPES = [(4096, 4096, 256), (2048, 2048, 512), (2048, 512, 4096), (1000, 520, 1000),
+                 (2040, 1028, 516), (72, 40, 24), (130, 66, 1001)]
+
+
+@pytest.mark.parametrize("shape", GEMM32_SHAPES)
+def test_linear_gemms_fp32_dma(shape):
+    from valkyr_amd import kernels as K
+
+    M, N, Kd = shape
+    note(f"gemm fp32 M={M} N={N} K={Kd}")
+    rng = np.random.default_rng(M + N + Kd)
+    x = rng.standard_normal((M, Kd), dtype=np.float32)
+    W = (0.05 * rng.standard_normal((N, Kd))).astype(np.float32)
+    dy = rng.standard_normal((M, N), dtype=np.float32)
+    x64, W64, dy64 = x.astype(np.float64), W.astype(np.float64), dy.astype(np.float64)
+    bx, bW, bdy = dev(x.ravel()), dev(W.ravel()), dev(dy.ravel())
+    by, bdx, bdW = zeros(M * N), zeros(M * Kd), zeros(N * Kd)
+    K.matmul_nt(bx, bW, by, M, N, Kd, 0)
+    K.linear_backward_dx(bdy, bW, bdx, M, N, Kd, 0)
+    K.linear_backward_dw(bdy, bx, bdW, M, N, Kd, 0)
+    tol = 1e-5  # fp32 products, fp32 accumulation
+    assert rel_l2((x64 @ W64.T).ravel(), host(by)) < tol
+    assert rel_l2((dy64 @ W64).ravel(), host(bdx)) < tol
+    assert rel_l2((dy64.T @ x64).ravel(), host(bdW)) < tol
+
+
 def test_bf16_gemms_over_2gib_operand():
     """The head's dz at 8192 tokens x 151936 vocabulary (2.49 GB of bf16) is
     past the DMA path's 2 GiB views: dW = dz^T x runs in row chunks that

@@ -356,38 +356,60 @@ vkh_status vkh_fa_backward_from_o(const vkh_attn_params *p, const void *q, const
 
 // ── GEMMs ──────────────────────────────────────────────────────────────
 
-vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,
-                         uint32_t K, uint32_t precision, vkh_stream stream) {
-    CHECK_ARG(x && w && y, "null pointer");
-    VKH_HIP(gemm_nt(PR(precision), matf(x, K), matf(w, K), y, N, M, N, K, nullptr, 0, 1.f, 0.f, S(stream)));
-    return VKH_OK;
-}
-
-vkh_status vkh_linear_backward_dx(const float *dy, const float *w, float *dx, uint32_t M,
-                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream) {
-    CHECK_ARG(dy && w && dx, "null pointer");
-    VKH_HIP(gemm_nn(PR(precision), matf(dy, N), matf(w, K), dx, K, M, N, K, 1.f, 0.f, S(stream)));
-    return VKH_OK;
-}
-
-vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, uint32_t M,
-                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream) {
-    CHECK_ARG(dy && x && dw, "null pointer");
-    VKH_HIP(gemm_tn(PR(precision), matf(dy, N), matf(x, K), dw, K, M, N, K, 1.f, 0.f, S(stream)));
-    return VKH_OK;
-}
-
 // Split-K workspace for one call (stream-ordered allocation), if the plan wants one.
 extern "C++" {
 template <class F>
-static vkh_status with_g16_ws(int M, int N, int K, hipStream_t st, const char *what, F &&f) {
-    GemmWs ws{nullptr, g16_ws_bytes_for(M, N, K)};
+static vkh_status with_ws(size_t bytes, hipStream_t st, const char *what, F &&f) {
+    GemmWs ws{nullptr, bytes};
     ScratchLease lease;
     if (ws.bytes) VKH_TRY(lease.acquire(ws.bytes, st, &ws.p));
     const hipError_t e = f(ws);
     if (e != hipSuccess) return hip_fail(e, what);
     return VKH_OK;
 }
+template <class F>
+static vkh_status with_g16_ws(int M, int N, int K, hipStream_t st, const char *what, F &&f) {
+    return with_ws(g16_ws_bytes_for(M, N, K), st, what, f);
+}
+}
+
+// Precision FP32: the DMA-staged fp32 MFMA kernels (g32_*), which take the
+// generic kernel for operands outside their layout rules; BF16: operands
+// rounded to bf16 on their way into the generic kernel's LDS tiles.
+vkh_status vkh_matmul_nt(const float *x, const float *w, float *y, uint32_t M, uint32_t N,
+                         uint32_t K, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(x && w && y, "null pointer");
+    hipStream_t st = S(stream);
+    if (PR(precision) == Precision::FP32)
+        return with_ws(g32_ws_bytes_for(M, N, K), st, "matmul_nt", [&](const GemmWs &ws) {
+            return g32_nt(x, K, w, K, y, N, M, N, K, nullptr, 0, 1.f, 0.f, ws, st);
+        });
+    VKH_HIP(gemm_nt(PR(precision), matf(x, K), matf(w, K), y, N, M, N, K, nullptr, 0, 1.f, 0.f, st));
+    return VKH_OK;
+}
+
+vkh_status vkh_linear_backward_dx(const float *dy, const float *w, float *dx, uint32_t M,
+                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(dy && w && dx, "null pointer");
+    hipStream_t st = S(stream);
+    if (PR(precision) == Precision::FP32)
+        return with_ws(g32_ws_bytes_for(M, K, N), st, "linear_backward_dx", [&](const GemmWs &ws) {
+            return g32_nn(dy, N, w, K, dx, K, M, N, K, 1.f, 0.f, ws, st);
+        });
+    VKH_HIP(gemm_nn(PR(precision), matf(dy, N), matf(w, K), dx, K, M, N, K, 1.f, 0.f, st));
+    return VKH_OK;
+}
+
+vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, uint32_t M,
+                                  uint32_t N, uint32_t K, uint32_t precision, vkh_stream stream) {
+    CHECK_ARG(dy && x && dw, "null pointer");
+    hipStream_t st = S(stream);
+    if (PR(precision) == Precision::FP32)
+        return with_ws(g32_ws_bytes_for(N, K, M), st, "linear_backward_dw", [&](const GemmWs &ws) {
+            return g32_tn(dy, N, x, K, dw, K, M, N, K, 1.f, 0.f, ws, st);
+        });
+    VKH_HIP(gemm_tn(PR(precision), matf(dy, N), matf(x, K), dw, K, M, N, K, 1.f, 0.f, st));
+    return VKH_OK;
 }
 
 vkh_status vkh_matmul_nt_bf16(const void *x, const void *w, float *y, uint32_t M, uint32_t N,

@@ -142,33 +142,43 @@ VKH_DEV void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::
 // Byte offset (into the operand) of the 16 bytes lane `lane` moves for 1 KB
 // piece `ins` of an operand tile's slab (R rows x 64 k at k0); the piece
 // lands at tile + 1024 ins + 16 lane.  kOOB past the edges.
-template <Lay L, int R>
+// fp32 operands (ES = 4): a slab is 32 k wide, so a K-major tile row is again
+// 128 bytes (eight 16-byte chunks of 4 floats, the same swizzle) and an
+// MN-major tile is 32 k rows of R floats; their fragments are read one float
+// per lane (frag32), so the MN swizzle only has to put the rows 4 fg + e of
+// one read (fg = 0..3) on two disjoint bank halves: chunk c of row k at
+// c ^ (4 ((k >> 2) & 1)).
+VKH_DEV int mn_swz32(int k) { return ((k >> 2) & 1) << 2; }
+
+template <Lay L, int R, int ES = 2>
 VKH_DEV unsigned tile_off(const Op16 &o, int ins, int lane, int r0, int rmax, int k0, int kmax) {
+    constexpr int EPC = 16 / ES;  // elements per 16-byte chunk
     if constexpr (L == Lay::K) {
         const int r = ins * 8 + lane / 8, c = (lane % 8) ^ ((lane / 8) & 7);
-        const int gr = r0 + r, gk = k0 + 8 * c;
-        return (gr < rmax && gk < kmax) ? (unsigned)(((long)gr * o.ld + gk) * 2) : kOOB;
+        const int gr = r0 + r, gk = k0 + EPC * c;
+        return (gr < rmax && gk < kmax) ? (unsigned)(((long)gr * o.ld + gk) * ES) : kOOB;
     } else {
-        constexpr int CPR = R / 8;        // 16-byte chunks per k row
-        static_assert(R == 64 || R % 128 == 0, "MN tile width");
+        constexpr int CPR = R / EPC;      // 16-byte chunks per k row
+        static_assert(ES == 4 || R == 64 || R % 128 == 0, "MN tile width");
+        static_assert(CPR <= 64 && 64 % CPR == 0, "MN rows per instruction");
         constexpr int RPI = 64 / CPR;     // k rows per instruction
         const int k = ins * RPI + lane / CPR, pch = lane % CPR;
-        const int c = pch ^ mn_swz<R>(k);
-        const int gk = k0 + k, gm = r0 + 8 * c;
-        return (gk < kmax && gm < rmax) ? (unsigned)(((long)gk * o.ld + gm) * 2) : kOOB;
+        const int c = pch ^ (ES == 2 ? mn_swz<R>(k) : mn_swz32(k));
+        const int gk = k0 + k, gm = r0 + EPC * c;
+        return (gk < kmax && gm < rmax) ? (unsigned)(((long)gk * o.ld + gm) * ES) : kOOB;
     }
 }
 
 // Issue this wave's share of one slab of an operand tile (R x 64).
-template <Lay L, int R, int NW>
+template <Lay L, int R, int NW, int ES = 2>
 VKH_DEV void dma_tile(const sgpr4 &rs, const Op16 &o, char *tile, int r0, int rmax, int k0,
                       int kmax, int wave, int lane) {
-    constexpr int PW = R / 8 / NW;  // 1 KB instructions per wave
+    constexpr int PW = R / 8 / NW;  // 1 KB instructions per wave (a slab is 128 R bytes)
     static_assert(PW >= 1 && PW * NW * 8 == R, "tile / wave mismatch");
 #pragma unroll
     for (int j = 0; j < PW; ++j) {
         const int ins = wave * PW + j;
-        dma16_async(rs, tile + ins * 1024, tile_off<L, R>(o, ins, lane, r0, rmax, k0, kmax));
+        dma16_async(rs, tile + ins * 1024, tile_off<L, R, ES>(o, ins, lane, r0, rmax, k0, kmax));
     }
 }
 
@@ -191,18 +201,42 @@ VKH_DEV bf16x8 frag16(const char *tile, int row16, int ks, int lane) {
     }
 }
 
+// fp32 fragment for v_mfma_f32_16x16x4_f32 at k-step ks (16 k): lane (fg, fr)
+// holds operand row row16 + fr at k = 16 ks + 4 fg + e in element e, the
+// contraction index of MFMA step e (the same index for both operands).
+template <Lay L, int R>
+VKH_DEV f32x4 frag32(const char *tile, int row16, int ks, int lane) {
+    const int fr = lane % 16, fg = lane / 16;
+    if constexpr (L == Lay::K) {
+        const int r = row16 + fr;
+        return *reinterpret_cast<const f32x4 *>(tile + r * 128 + ((((ks << 2) + fg) ^ (r & 7)) << 4));
+    } else {
+        const int m = row16 + fr;
+        f32x4 v;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int k = 16 * ks + 4 * fg + e;
+            v[e] = *reinterpret_cast<const float *>(tile + k * (R * 4) + (((m >> 2) ^ mn_swz32(k)) << 4) +
+                                                    (m & 3) * 4);
+        }
+        return v;
+    }
+}
+
 VKH_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0), exp/lgkm untouched
 
-// One block's BM x BN output tile over the K slabs [kbase, kbase + 64 nk):
+// One block's BM x BN output tile over the K slabs [kbase, kbase + KW nk)
+// (KW = 64 bf16 or, with F32, 32 fp32 values: 128-byte tile rows either way):
 // acc (per wave, accumulator layout) += A(m0.., k) B(n0.., k).  `smem` must
 // hold Cfg::LDS bytes.  Shared by the GEMM kernels and the attention dQ kernel.
 // `wave` is the wave's index among the Cfg::WGM x Cfg::WGN waves that share
 // this tile (-1: threadIdx.x / 64, the whole block).  Every wave of the
 // workgroup must run the same number of slabs: the routine's barriers are
 // workgroup-wide.
-template <class Cfg, Lay LA, Lay LB, int TM, int TN>
+template <class Cfg, Lay LA, Lay LB, int TM, int TN, bool F32 = false>
 VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
                              int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem, int wave_in = -1) {
+    constexpr int KW = F32 ? 32 : 64, ES = F32 ? 4 : 2;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::WGM * Cfg::WGN, ST = Cfg::ST;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
     static_assert(TM == WM / 16 && TN == WN / 16, "fragment grid");
@@ -217,8 +251,8 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
     const sgpr4 ra = rsrc4(a), rb = rsrc4(b);
     auto issue = [&](int kt) {
         char *stage = smem + (kt % ST) * STAGE;
-        dma_tile<LA, BM, NW>(ra, a, stage, m0, M, kbase + kt * 64, Kmax, wave, lane);
-        dma_tile<LB, BN, NW>(rb, b, stage + ABYTES, n0, N, kbase + kt * 64, Kmax, wave, lane);
+        dma_tile<LA, BM, NW, ES>(ra, a, stage, m0, M, kbase + kt * KW, Kmax, wave, lane);
+        dma_tile<LB, BN, NW, ES>(rb, b, stage + ABYTES, n0, N, kbase + kt * KW, Kmax, wave, lane);
     };
     // ST - 1 slabs in flight ahead of the one computing
     for (int j = 0; j < ST - 1 && j < nk; ++j) issue(j);
@@ -232,6 +266,28 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
         if (kt + ST - 1 < nk) issue(kt + ST - 1);
         // Both k-steps' fragments are requested before the first MFMA, so the
         // LDS latency of the second set hides behind the first set's MFMAs.
+        if constexpr (F32) {
+            f32x4 af[2][TM], bfr[2][TN];
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+                for (int i = 0; i < TM; ++i) af[ks][i] = frag32<LA, BM>(cur, wm * WM + 16 * i, ks, lane);
+#pragma unroll
+                for (int j = 0; j < TN; ++j)
+                    bfr[ks][j] = frag32<LB, BN>(cur + ABYTES, wn * WN + 16 * j, ks, lane);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+                for (int i = 0; i < TM; ++i)
+#pragma unroll
+                    for (int j = 0; j < TN; ++j)
+#pragma unroll
+                        for (int e = 0; e < 4; ++e)
+                            acc[i][j] = mfma16x16x4(af[ks][i][e], bfr[ks][j][e], acc[i][j]);
+            continue;
+        }
         bf16x8 af[2][TM], bfr[2][TN];
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
@@ -252,7 +308,7 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
     lds_barrier();  // the caller may reuse smem
 }
 
-template <class Cfg, Lay LA, Lay LB, class Epi>
+template <class Cfg, Lay LA, Lay LB, class Epi, bool F32 = false>
 __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, GemmShape s, Epi epi,
                                                             SplitK sk, int tgrp) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
@@ -279,10 +335,11 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nk_all = (s.K + 63) / 64;
+    constexpr int KW = F32 ? 32 : 64;  // k per slab
+    const int nk_all = (s.K + KW - 1) / KW;
     const int kt0 = (int)((long)nk_all * split / sk.splits);
     const int nk = (int)((long)nk_all * (split + 1) / sk.splits) - kt0;
-    gemm16_tile_dma<Cfg, LA, LB, TM, TN>(a, b, m0, n0, s.M, s.N, kt0 * 64, nk, s.K, acc, smem);
+    gemm16_tile_dma<Cfg, LA, LB, TM, TN, F32>(a, b, m0, n0, s.M, s.N, kt0 * KW, nk, s.K, acc, smem);
 
     if (sk.splits > 1) {
         f32x4 *own = sk.ws + ((size_t)tile * sk.splits + split) * (BM * BN / 4);
@@ -303,7 +360,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_kernel(Op16 a, Op16 b, Gemm
 // (first half + second half, a fixed order) and runs the epilogue.  For
 // shapes with too few tiles to fill the chip this doubles the waves per CU
 // without the partial round trip and the second launch of split-K.
-template <class Cfg, Lay LA, Lay LB, class Epi>
+template <class Cfg, Lay LA, Lay LB, class Epi, bool F32 = false>
 __global__ __launch_bounds__(2 * Cfg::NT, 1) void gemm16_ks2_kernel(Op16 a, Op16 b, GemmShape s,
                                                                    Epi epi, int tgrp) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT;
@@ -330,8 +387,9 @@ __global__ __launch_bounds__(2 * Cfg::NT, 1) void gemm16_ks2_kernel(Op16 a, Op16
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const int nkh = ((s.K + 63) / 64 + 1) / 2;
-    gemm16_tile_dma<Cfg, LA, LB, TM, TN>(a, b, m0, n0, s.M, s.N, grp * nkh * 64, nkh, s.K, acc,
+    constexpr int KW = F32 ? 32 : 64;
+    const int nkh = ((s.K + KW - 1) / KW + 1) / 2;
+    gemm16_tile_dma<Cfg, LA, LB, TM, TN, F32>(a, b, m0, n0, s.M, s.N, grp * nkh * KW, nkh, s.K, acc,
                                          smem + grp * Cfg::LDS, wave);
     f32x4 *hand = reinterpret_cast<f32x4 *>(smem);  // both groups are past their last slab
     if (grp == 1) {
@@ -350,12 +408,12 @@ __global__ __launch_bounds__(2 * Cfg::NT, 1) void gemm16_ks2_kernel(Op16 a, Op16
     epi.template apply<TM, TN>(acc, fp, s);
 }
 
-template <class Cfg, Lay LA, Lay LB, class Epi>
+template <class Cfg, Lay LA, Lay LB, class Epi, bool F32 = false>
 hipError_t launch_gemm16_ks2(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &epi,
                              int tgrp, hipStream_t st) {
     if (s.M <= 0 || s.N <= 0) return hipSuccess;
     const unsigned tiles = ceil_div(s.M, Cfg::BM) * ceil_div(s.N, Cfg::BN);
-    hipLaunchKernelGGL((gemm16_ks2_kernel<Cfg, LA, LB, Epi>), dim3(tiles), dim3(2 * Cfg::NT), 0, st,
+    hipLaunchKernelGGL((gemm16_ks2_kernel<Cfg, LA, LB, Epi, F32>), dim3(tiles), dim3(2 * Cfg::NT), 0, st,
                        a, b, s, epi, tgrp);
     return hipGetLastError();
 }
@@ -396,13 +454,13 @@ size_t gemm16_ws_bytes(const GemmShape &s, int splits) {
     return (size_t)ceil_div(s.M, Cfg::BM) * ceil_div(s.N, Cfg::BN) * splits * Cfg::BM * Cfg::BN * 4;
 }
 
-template <class Cfg, Lay LA, Lay LB, class Epi>
+template <class Cfg, Lay LA, Lay LB, class Epi, bool F32 = false>
 hipError_t launch_gemm16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &epi,
                          const SplitK &sk, int tgrp, hipStream_t st) {
     if (s.M <= 0 || s.N <= 0) return hipSuccess;
     if (sk.splits < 1 || (sk.splits > 1 && !sk.ws)) return hipErrorInvalidValue;
     const unsigned tiles = ceil_div(s.M, Cfg::BM) * ceil_div(s.N, Cfg::BN);
-    hipLaunchKernelGGL((gemm16_kernel<Cfg, LA, LB, Epi>), dim3(tiles * sk.splits), dim3(Cfg::NT),
+    hipLaunchKernelGGL((gemm16_kernel<Cfg, LA, LB, Epi, F32>), dim3(tiles * sk.splits), dim3(Cfg::NT),
                        0, st, a, b, s, epi, sk, tgrp);
     if (sk.splits > 1)
         hipLaunchKernelGGL((gemm16_reduce_kernel<Cfg, Epi>), dim3(tiles), dim3(Cfg::NT), 0, st, s,

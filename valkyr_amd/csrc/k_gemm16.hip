@@ -95,6 +95,49 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
     }
 }
 
+// ── fp32 operands (the reference-precision step) ───────────────────────
+// The same kernels with F32 set: slabs of 32 fp32 values (128-byte tile rows,
+// the bf16 slab's layout), four v_mfma_f32_16x16x4_f32 per 16-byte fragment.
+// At a sixteenth of the bf16 matrix rate the slab DMA has ample time to land,
+// so the plan only has to spread the tiles over the CUs.
+Plan plan32(const GemmShape &s, size_t ws_bytes) {
+    auto tiles = [&](int bm, int bn) { return (long)ceil_div(s.M, bm) * (long)ceil_div(s.N, bn); };
+    const int nk = (s.K + 31) / 32;
+    Plan p{Pick::T128x64, 1};
+    if (tiles(256, 256) >= 256) p = Plan{Pick::Big, 1};
+    else if (tiles(128, 128) >= 256) p = Plan{Pick::T128w8, 1};
+    else if (tiles(128, 64) < 256 && s.K >= 2048) p = Plan{Pick::T128x64ks2, 1};
+    while (p.splits > 1 && (nk / p.splits < 8 || ws_for(p, s) > ws_bytes)) --p.splits;
+    return p;
+}
+
+template <Lay LA, Lay LB, class Epi>
+hipError_t run32(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e, const GemmWs &ws,
+                 hipStream_t st) {
+    const Plan p = plan32(s, ws.p ? ws.bytes : 0);
+    const SplitK sk{p.splits, (f32x4 *)ws.p};
+    const int g = p.column_order ? 0 : tile_group_rows<LA, LB>();
+    switch (p.tile) {
+    case Pick::Big: return launch_gemm16<TBig, LA, LB, Epi, true>(a, b, s, e, sk, g, st);
+    case Pick::T128: return launch_gemm16<T128, LA, LB, Epi, true>(a, b, s, e, sk, g, st);
+    case Pick::T128w8: return launch_gemm16<T128w8, LA, LB, Epi, true>(a, b, s, e, sk, g, st);
+    case Pick::T128x64ks2: return launch_gemm16_ks2<T128x64, LA, LB, Epi, true>(a, b, s, e, g, st);
+    default: return launch_gemm16<T128x64, LA, LB, Epi, true>(a, b, s, e, sk, g, st);
+    }
+}
+
+// fp32 operand view: 16-byte aligned, ld and the contiguous run multiples of 4
+// floats (whole 16-byte chunks), under 2 GiB (32-bit buffer offsets).
+bool make_op32(const float *p, long ld, long rows, long run, Op16 &o) {
+    if (((uintptr_t)p & 15u) || ld % 4 || run % 4 || rows <= 0) return false;
+    const size_t bytes = ((size_t)(rows - 1) * ld + run) * 4;
+    if (bytes >= (1ull << 31)) return false;
+    o = Op16{reinterpret_cast<const bf16 *>(p), ld, (unsigned)bytes};
+    return true;
+}
+
+Mat matf32(const float *p, long ld) { return Mat{p, ld, DType::F32}; }
+
 // Operand of `rows` storage rows whose contiguous run is `run` elements.
 bool make_op(const bf16 *p, long ld, long rows, long run, Op16 &o) {
     if (((uintptr_t)p & 15u) || ld % 8 || run % 8 || rows <= 0) return false;
@@ -297,6 +340,42 @@ hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw,
                        beta, st);
     EpiStore e{dw, lddw, nullptr, 0, alpha, beta};
     return run16<Lay::MN, Lay::MN>(a, b, GemmShape{N, K, M}, e, ws, st);
+}
+
+hipError_t g32_nt(const float *x, long ldx, const float *w, long ldw, float *y, long ldy, int M,
+                  int N, int K, const float *R, long ldr, float alpha, float beta,
+                  const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op32(x, ldx, M, K, a) || !make_op32(w, ldw, N, K, b))
+        return gemm_nt(Precision::FP32, matf32(x, ldx), matf32(w, ldw), y, ldy, M, N, K, R, ldr,
+                       alpha, beta, st);
+    EpiStore e{y, ldy, R, ldr, alpha, beta};
+    return run32<Lay::K, Lay::K>(a, b, GemmShape{M, N, K}, e, ws, st);
+}
+
+hipError_t g32_nn(const float *dy, long lddy, const float *w, long ldw, float *dx, long lddx, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op32(dy, lddy, M, N, a) || !make_op32(w, ldw, N, K, b))
+        return gemm_nn(Precision::FP32, matf32(dy, lddy), matf32(w, ldw), dx, lddx, M, N, K, alpha,
+                       beta, st);
+    EpiStore e{dx, lddx, nullptr, 0, alpha, beta};
+    return run32<Lay::K, Lay::MN>(a, b, GemmShape{M, K, N}, e, ws, st);
+}
+
+hipError_t g32_tn(const float *dy, long lddy, const float *x, long ldx, float *dw, long lddw, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
+    Op16 a, b;
+    if (!make_op32(dy, lddy, M, N, a) || !make_op32(x, ldx, M, K, b))
+        return gemm_tn(Precision::FP32, matf32(dy, lddy), matf32(x, ldx), dw, lddw, M, N, K, alpha,
+                       beta, st);
+    EpiStore e{dw, lddw, nullptr, 0, alpha, beta};
+    return run32<Lay::MN, Lay::MN>(a, b, GemmShape{N, K, M}, e, ws, st);
+}
+
+size_t g32_ws_bytes_for(int M, int N, int K) {
+    const GemmShape s{M, N, K};
+    return ws_for(plan32(s, ~size_t(0)), s);
 }
 
 size_t g16_ws_bytes_for(int M, int N, int K) {

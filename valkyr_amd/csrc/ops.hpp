@@ -49,6 +49,17 @@ hipError_t g16_nn_bf16(const bf16 *dy, long lddy, const bf16 *w, long ldw, bf16 
 hipError_t g16_tn(const bf16 *dy, long lddy, const bf16 *x, long ldx, float *dw, long lddw, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
 size_t g16_ws_bytes_for(int M, int N, int K);
+// fp32 operands on the same DMA-staged kernels (fp32 matrix cores); operands
+// the DMA path cannot take (alignment, ld or extent not a multiple of 4, over
+// 2 GiB) go to gemm_nt / gemm_nn / gemm_tn at Precision::FP32.
+hipError_t g32_nt(const float *x, long ldx, const float *w, long ldw, float *y, long ldy, int M,
+                  int N, int K, const float *R, long ldr, float alpha, float beta,
+                  const GemmWs &ws, hipStream_t st);
+hipError_t g32_nn(const float *dy, long lddy, const float *w, long ldw, float *dx, long lddx, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
+hipError_t g32_tn(const float *dy, long lddy, const float *x, long ldx, float *dw, long lddw, int M,
+                  int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
+size_t g32_ws_bytes_for(int M, int N, int K);
 
 // ── LoRA rank-r products (k_lora.hip) ───────────────────────────────────
 // One adapter of a launch: its columns [col, col + ncols) of the shared X

@@ -548,6 +548,17 @@ struct vkh_runner {
             }
         } else {
             VKH_TRY(alloc(fn_out, (size_t)T * D));
+            // split-K workspace of the fp32 GEMMs (g32_*), if their plan asks for one
+            size_t wsb = 0;
+            auto need = [&](int m, int n, int k) { wsb = std::max(wsb, g32_ws_bytes_for(m, n, k)); };
+            need(T, qkvd, D); need(T, D, qd); need(T, 2 * F, D); need(T, D, F);
+            need(T, F, D); need(T, D, 2 * F); need(T, qd, D); need(T, D, qkvd);
+            need(D, F, T); need(2 * F, D, T); need(D, qd, T); need(qkvd, D, T);
+            if (wsb) {
+                char *w = nullptr;
+                VKH_TRY(alloc(w, wsb));
+                gws = GemmWs{w, wsb};
+            }
         }
         VKH_TRY(alloc(ce_lse, T));
         VKH_TRY(alloc(loss_row, T));
@@ -874,7 +885,7 @@ struct vkh_runner {
         if (b16())
             VKH_HIP(g16_nt((const bf16 *)x.p, x.ld, Wb(w), K, y, ldy, T, N, K, R, ldr, 1.f, 0.f, gws, cur));
         else
-            VKH_HIP(gemm_nt(pr, x, matf(W(w), K), y, ldy, T, N, K, R, ldr, 1.f, 0.f, cur));
+            VKH_HIP(g32_nt((const float *)x.p, x.ld, W(w), K, y, ldy, T, N, K, R, ldr, 1.f, 0.f, gws, cur));
         return VKH_OK;
     }
     // dx[T, K] = dy[T, N] W[N, K]
@@ -882,7 +893,7 @@ struct vkh_runner {
         if (b16())
             VKH_HIP(g16_nn((const bf16 *)dy.p, dy.ld, Wb(w), K, dx, lddx, T, N, K, 1.f, 0.f, gws, cur));
         else
-            VKH_HIP(gemm_nn(pr, dy, matf(W(w), K), dx, lddx, T, N, K, 1.f, 0.f, cur));
+            VKH_HIP(g32_nn((const float *)dy.p, dy.ld, W(w), K, dx, lddx, T, N, K, 1.f, 0.f, gws, cur));
         return VKH_OK;
     }
     // dW[N, K] = dy[T, N]^T x[T, K] (overwrite)
@@ -896,7 +907,8 @@ struct vkh_runner {
             VKH_HIP(g16_tn((const bf16 *)dy.p, dy.ld, (const bf16 *)x.p, x.ld, Gd(w), K, T, N, K, 1.f,
                            0.f, ws, st));
         else
-            VKH_HIP(gemm_tn(pr, dy, x, Gd(w), K, T, N, K, 1.f, 0.f, st));
+            VKH_HIP(g32_tn((const float *)dy.p, dy.ld, (const float *)x.p, x.ld, Gd(w), K, T, N, K, 1.f,
+                           0.f, ws, st));
         return VKH_OK;
     }
     // The four weight-gradient GEMMs of layer l on the side stream (concurrent
