@@ -186,6 +186,16 @@ hipError_t logits_gemm(Precision pr, const CceShape &s, const float *h, const fl
     GemmShape sh{s.N, s.V, s.D};
     if (pr == Precision::BF16)
         return launch_gemm<TileCfg<128, 128, 64>, true, float, Lay::K, float, Lay::K>(a, b, sh, epi, st);
+    // fp32: the DMA-staged 256 x 256 tile on the fp32 matrix cores (64-column
+    // wave slices, as the epilogues need) where the operands fit its rules
+    const size_t hb = ((size_t)(s.N - 1) * s.D + s.D) * 4, wb = ((size_t)(s.V - 1) * s.D + s.D) * 4;
+    if (s.D % 4 == 0 && ((uintptr_t)h & 15u) == 0 && ((uintptr_t)w & 15u) == 0 &&
+        hb < (1ull << 31) && wb < (1ull << 31)) {
+        const Op16 a16{(const bf16 *)h, s.D, (unsigned)hb}, b16{(const bf16 *)w, s.D, (unsigned)wb};
+        const SplitK one{1, nullptr};
+        return launch_gemm16<Tile16<256, 256, 2, 4>, Lay::K, Lay::K, Epi, true>(
+            a16, b16, sh, epi, one, tile_group_rows<Lay::K, Lay::K>(), st);
+    }
     return launch_gemm<TileCfg<128, 128, 32>, false, float, Lay::K, float, Lay::K>(a, b, sh, epi, st);
 }
 
@@ -250,6 +260,15 @@ hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const f
     }
     if (err != hipSuccess) return err;
     const Mat mz{dz, s.V, zdt};
+    if (zdt == DType::F32) {  // fp32: the DMA-staged fp32 kernels (generic where they do not apply)
+        const GemmWs none{nullptr, 0};
+        if (dw) {
+            err = g32_tn((const float *)dz, s.V, h, s.D, dw, s.D, s.N, s.V, s.D, 1.f, dw_beta, none, st);
+            if (err != hipSuccess) return err;
+        }
+        if (dh) err = g32_nn((const float *)dz, s.V, w, s.D, dh, s.D, s.N, s.V, s.D, 1.f, 0.f, none, st);
+        return err;
+    }
     if (dw) {
         err = gemm_tn(pr, mz, matf(h, s.D), dw, s.D, s.N, s.V, s.D, 1.f, dw_beta, st);
         if (err != hipSuccess) return err;

@@ -99,14 +99,24 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
 // The same kernels with F32 set: slabs of 32 fp32 values (128-byte tile rows,
 // the bf16 slab's layout), four v_mfma_f32_16x16x4_f32 per 16-byte fragment.
 // At a sixteenth of the bf16 matrix rate the slab DMA has ample time to land,
-// so the plan only has to spread the tiles over the CUs.
+// so the plan only has to spread whole rounds of tiles over the 256 CUs.
+// Measured per shape alone at the config-3 step's 12 layer GEMMs (T = 2048):
+//   * 128 x 128 on 8 waves where its tile count fills rounds at least as
+//     evenly as 128 x 64 (q/k/v and gate/up forward, o dx, q/k/v dW: 130-196 us
+//     against 143-210 on 128 x 64 and 210-290 on 4-wave 128 x 128 or 256 x 256);
+//   * 128 x 64 where that evens the rounds (384 tiles of 128 x 128 = 768 of
+//     128 x 64: down dx 107 against 134 us, gate/up dW 209 against 259);
+//   * fewer than 512 tiles of 128 x 64 (the N = 1024 outputs and dW of o /
+//     down): 128 x 64 split 2 ways along K (q/k/v dx 149, gate/up dx 213, down
+//     dW 119 us against 174, 254, 154 unsplit in one block pair).
 Plan plan32(const GemmShape &s, size_t ws_bytes) {
     auto tiles = [&](int bm, int bn) { return (long)ceil_div(s.M, bm) * (long)ceil_div(s.N, bn); };
+    auto fill = [](long t) { return (double)t / (256.0 * (double)((t + 255) / 256)); };
+    const long t128 = tiles(128, 128), t64 = tiles(128, 64);
     const int nk = (s.K + 31) / 32;
     Plan p{Pick::T128x64, 1};
-    if (tiles(256, 256) >= 256) p = Plan{Pick::Big, 1};
-    else if (tiles(128, 128) >= 256) p = Plan{Pick::T128w8, 1};
-    else if (tiles(128, 64) < 256 && s.K >= 2048) p = Plan{Pick::T128x64ks2, 1};
+    if (t128 >= 256 && fill(t128) >= fill(t64)) p = Plan{Pick::T128w8, 1};
+    else if (t64 < 512) p = Plan{Pick::T128x64, 2};
     while (p.splits > 1 && (nk / p.splits < 8 || ws_for(p, s) > ws_bytes)) --p.splits;
     return p;
 }
