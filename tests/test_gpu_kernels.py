@@ -477,6 +477,9 @@ FA_F32_CASES = [  # smoke/cpu.zig:909-916 shapes (n_q, n_kv, H, Hkv, hd, causal)
     (128, 128, 4, 2, 64, True, 3), (256, 256, 16, 8, 128, True, 2),
     (192, 192, 8, 2, 64, True, 1), (128, 256, 4, 2, 128, False, 1),
     (256, 128, 8, 2, 64, False, 2), (512, 512, 16, 8, 128, True, 4),
+    # grids of 512 blocks and more (each CU holds two blocks at a time; the
+    # zigzag block order of the causal kernels pairs heavy and light ones)
+    (64, 64, 64, 32, 64, True, 16), (128, 128, 32, 32, 128, True, 16),
 ]
 
 
