@@ -94,4 +94,19 @@ VKH_DEV float block_sum(float v, float *sh) {
 
 inline unsigned ceil_div(size_t a, size_t b) { return (unsigned)((a + b - 1) / b); }
 
+// Causal grids with row 0 the heaviest: the block row of grid row y (of n)
+// when the whole grid is resident at once with two blocks per CU.  The first
+// half of the rows goes heaviest first and the second half lightest first, so
+// blocks y and y + n / 2, which the in-order dispatch places on one CU, carry
+// about equal work together.  (A grid larger than the resident slots keeps
+// heaviest-first order: blocks then start as CUs free up.)
+VKH_DEV int zigzag(int y, int n) {
+    const int h = n / 2;
+    return y < h ? y : n - 1 - (y - h);
+}
+// Compute units of the current device (cached per device).
+int cu_count();
+// Whether a grid of `blocks` fits the device's CUs at two blocks each.
+inline bool fits_two_per_cu(long blocks) { return blocks <= 2L * cu_count(); }
+
 }  // namespace vkh

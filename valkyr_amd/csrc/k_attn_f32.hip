@@ -52,16 +52,6 @@ VKH_DEV float xsum(float v) {
     return v + __shfl_xor(v, 32);
 }
 
-// Causal grids: the block row of grid row y (of n) when row 0 is the heaviest.
-// The first half of the rows goes heaviest first and the second half lightest
-// first, so blocks y and y + n / 2, which the dispatcher places on one CU
-// when the grid is twice the CU count with two blocks resident per CU, carry
-// about equal work together (the heavy block's share plus the light one's).
-VKH_DEV int zigzag(int y, int n) {
-    const int h = n / 2;
-    return y < h ? y : n - 1 - (y - h);
-}
-
 // A FT x HD fp32 tile moved global -> registers -> LDS (pitch HD + 4) by NT threads.
 template <int HD, int NT = FNT>
 struct Tile {
@@ -88,12 +78,13 @@ struct Tile {
 template <int HD>
 __global__ __launch_bounds__(FNT, 2) void fa_fwd_f32m_k(AttnShape s, const float *q, long ldq,
                                                        const float *k, long ldk, const float *v,
-                                                       long ldv, float *o, long ldo, float *lse) {
+                                                       long ldv, float *o, long ldo, float *lse,
+                                                       bool zz) {
     constexpr int P = HD + 4, NU = HD / 16;
     __shared__ __attribute__((aligned(16))) float Ks[2][FT * P], Vs[2][FT * P];
     const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int nqb = s.n_q / 64;
-    const int qb = s.causal ? nqb - 1 - zigzag((int)blockIdx.y, nqb) : (int)blockIdx.y;
+    const int y = (int)blockIdx.y, qb = s.causal ? nqb - 1 - (zz ? zigzag(y, nqb) : y) : y;
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int q0 = qb * 64, qw = q0 + 16 * wave, qi = qw + c;
@@ -193,14 +184,14 @@ __global__ __launch_bounds__(FNT, 2) void fa_fwd_f32m_k(AttnShape s, const float
 // keys.  Where the 64-key grid is one block per CU, the causal 8:1 spread of
 // block work stays.)
 template <int HD>
-__global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtrs p) {
+__global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtrs p, bool zz) {
     constexpr int P = HD + 4, NU = HD / 16;
     __shared__ __attribute__((aligned(16))) float Qs[2][FT * P], Os[2][FT * P];
     __shared__ float Ls[2][FT], Dl[2][FT];
     const int kvh = blockIdx.x % s.n_kv_heads, b = blockIdx.x / s.n_kv_heads;
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int kb = s.causal ? zigzag((int)blockIdx.y, s.n_kv / 64) : (int)blockIdx.y;
+    const int kb = s.causal && zz ? zigzag((int)blockIdx.y, s.n_kv / 64) : (int)blockIdx.y;
     const int k0 = kb * 64, kw = k0 + 16 * wave, ki = kw + c;
     const int hpk = s.n_heads / s.n_kv_heads;
     const float c2 = s.inv_sqrt_dim * F_LOG2E;
@@ -311,12 +302,12 @@ __global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtr
 
 // ── dQ: block = 64 queries of one (sequence, head) ──────────────────────
 template <int HD>
-__global__ __launch_bounds__(FNT, 2) void fa_bwd_dq_f32m_k(AttnShape s, AttnPtrs p) {
+__global__ __launch_bounds__(FNT, 2) void fa_bwd_dq_f32m_k(AttnShape s, AttnPtrs p, bool zz) {
     constexpr int P = HD + 4, NU = HD / 16;
     __shared__ __attribute__((aligned(16))) float Ks[2][FT * P], Vs[2][FT * P];
     const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
     const int nqb = s.n_q / 64;
-    const int qb = s.causal ? nqb - 1 - zigzag((int)blockIdx.y, nqb) : (int)blockIdx.y;
+    const int y = (int)blockIdx.y, qb = s.causal ? nqb - 1 - (zz ? zigzag(y, nqb) : y) : y;
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
     const int q0 = qb * 64, qw = q0 + 16 * wave, qi = qw + c;
@@ -422,10 +413,11 @@ bool fa_f32m_fwd(const AttnShape &s, const float *q, long ldq, const float *k, l
         ldv % 4 || ldo % 4)
         return false;
     const dim3 grid(s.n_heads * s.n_batch, s.n_q / 64);
+    const bool zz = fits_two_per_cu((long)grid.x * grid.y);
     if (s.head_dim == 128)
-        hipLaunchKernelGGL(fa_fwd_f32m_k<128>, grid, dim3(FNT), 0, st, s, q, ldq, k, ldk, v, ldv, o, ldo, lse);
+        hipLaunchKernelGGL(fa_fwd_f32m_k<128>, grid, dim3(FNT), 0, st, s, q, ldq, k, ldk, v, ldv, o, ldo, lse, zz);
     else
-        hipLaunchKernelGGL(fa_fwd_f32m_k<64>, grid, dim3(FNT), 0, st, s, q, ldq, k, ldk, v, ldv, o, ldo, lse);
+        hipLaunchKernelGGL(fa_fwd_f32m_k<64>, grid, dim3(FNT), 0, st, s, q, ldq, k, ldk, v, ldv, o, ldo, lse, zz);
     return true;
 }
 
@@ -438,16 +430,18 @@ bool fa_f32m_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     if (!fa_f32m_ok(s) || !ptrs_ok(p) || !al16(p.dk) || !al16(p.dv) || p.lddk % 4 || p.lddv % 4)
         return false;
     const dim3 grid(s.n_kv_heads * s.n_batch, s.n_kv / 64);
-    if (s.head_dim == 128) hipLaunchKernelGGL(fa_bwd_dkv_f32m_k<128>, grid, dim3(FNT), 0, st, s, p);
-    else hipLaunchKernelGGL(fa_bwd_dkv_f32m_k<64>, grid, dim3(FNT), 0, st, s, p);
+    const bool zz = fits_two_per_cu((long)grid.x * grid.y);
+    if (s.head_dim == 128) hipLaunchKernelGGL(fa_bwd_dkv_f32m_k<128>, grid, dim3(FNT), 0, st, s, p, zz);
+    else hipLaunchKernelGGL(fa_bwd_dkv_f32m_k<64>, grid, dim3(FNT), 0, st, s, p, zz);
     return true;
 }
 
 bool fa_f32m_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     if (!fa_f32m_ok(s) || !ptrs_ok(p) || !al16(p.dq) || p.lddq % 4) return false;
     const dim3 grid(s.n_heads * s.n_batch, s.n_q / 64);
-    if (s.head_dim == 128) hipLaunchKernelGGL(fa_bwd_dq_f32m_k<128>, grid, dim3(FNT), 0, st, s, p);
-    else hipLaunchKernelGGL(fa_bwd_dq_f32m_k<64>, grid, dim3(FNT), 0, st, s, p);
+    const bool zz = fits_two_per_cu((long)grid.x * grid.y);
+    if (s.head_dim == 128) hipLaunchKernelGGL(fa_bwd_dq_f32m_k<128>, grid, dim3(FNT), 0, st, s, p, zz);
+    else hipLaunchKernelGGL(fa_bwd_dq_f32m_k<64>, grid, dim3(FNT), 0, st, s, p, zz);
     return true;
 }
 

@@ -2,6 +2,8 @@
 // embedding lookup and Adam.  All are float4-vectorised grid-stride loops
 // sized to fill the 256 CUs; fp contraction is disabled so each kernel
 // rounds exactly like the scalar reference formula it restates.
+#include <atomic>
+
 #include "ops.hpp"
 #include "adam.hpp"
 
@@ -488,6 +490,19 @@ __global__ __launch_bounds__(NT) void adam_k(float *p_, const float *g_, float *
 inline bool al16(const void *p) { return ((uintptr_t)p & 15u) == 0; }
 
 }  // namespace
+
+int cu_count() {
+    static std::atomic<int> cached[64];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+    int n = cached[dev].load(std::memory_order_relaxed);
+    if (n <= 0) {
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0)
+            n = 256;
+        cached[dev].store(n, std::memory_order_relaxed);
+    }
+    return n;
+}
 
 hipError_t fill_f32(float *p, size_t n, float v, hipStream_t st) {
     if (!n) return hipSuccess;
