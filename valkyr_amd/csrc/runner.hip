@@ -150,7 +150,10 @@ struct vkh_runner {
     // and its Adam update run on a second stream one layer behind the main
     // stream's backward, reading per-layer copies of the bf16 gradients.
     struct LayerGrads {
+        // the layer's gradient operands of its weight-gradient GEMMs: bf16
+        // copies in the bf16 precision, the fp32 tensors themselves in fp32
         bf16 *dyb = nullptr, *gub = nullptr, *midb = nullptr, *qkvb = nullptr;
+        float *dyf = nullptr, *guf = nullptr, *midf = nullptr, *qkvf = nullptr;
         // norm-gain partial sums (n1, n2, q/k norm), reduced on the side stream
         float *pn1 = nullptr, *pn2 = nullptr, *pqk = nullptr;
         int qk_parts = 0;
@@ -432,7 +435,7 @@ struct vkh_runner {
 
         const size_t asz = adt == DType::BF16 ? 2 : 4;
         recompute = cfg.recompute != 0;
-        concurrent = b16() && !lora;
+        concurrent = !lora;
         const int n_sets = recompute ? std::min(L, kActSets) : L;
         acts.assign(L, Acts{});
         for (int l = 0; l < L; ++l) {
@@ -504,48 +507,6 @@ struct vkh_runner {
                 VKH_TRY(alloc(w, wsb));
                 gws = GemmWs{w, wsb};
             }
-            if (concurrent) {
-                VKH_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
-                ev_layer.assign(L, nullptr);
-                for (int l = 0; l < L; ++l)
-                    VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], kOrderEvent));
-                if (recompute) {
-                    ev_sdone.assign(L, nullptr);
-                    for (int l = 0; l < L; ++l)
-                        VKH_HIP(hipEventCreateWithFlags(&ev_sdone[l], kOrderEvent));
-                }
-                VKH_HIP(hipEventCreateWithFlags(&ev_side, kOrderEvent));
-                VKH_HIP(hipEventCreateWithFlags(&ev_head, kOrderEvent));
-                VKH_HIP(hipEventCreateWithFlags(&ev_lm, kOrderEvent));
-                if (embed_split_ok()) {
-                    VKH_TRY(alloc(emb_mark, (size_t)V));
-                    VKH_HIP(fill_f32(reinterpret_cast<float *>(emb_mark), (size_t)V, 0.f, own));
-                }
-                lg.assign(L, LayerGrads{});
-                const int n_g = recompute ? std::min(L, kGradSets) : L;
-                const int n_dy = recompute ? std::min(L, kDyRing) : L;
-                for (int l = 0; l < L; ++l) {
-                    if (l < n_dy) VKH_TRY(alloc(lg[l].dyb, (size_t)T * D));
-                    else lg[l].dyb = lg[l % n_dy].dyb;
-                    if (l >= n_g) {
-                        const LayerGrads &o = lg[l % n_g];
-                        lg[l].gub = o.gub; lg[l].midb = o.midb; lg[l].qkvb = o.qkvb;
-                        lg[l].pn1 = o.pn1; lg[l].pn2 = o.pn2; lg[l].pqk = o.pqk;
-                        continue;
-                    }
-                    VKH_TRY(alloc(lg[l].gub, (size_t)T * 2 * F));
-                    VKH_TRY(alloc(lg[l].midb, (size_t)T * D));
-                    VKH_TRY(alloc(lg[l].qkvb, (size_t)T * qkvd));
-                    VKH_TRY(alloc(lg[l].pn1, rmsnorm_partial_floats(T, D)));
-                    VKH_TRY(alloc(lg[l].pn2, rmsnorm_partial_floats(T, D)));
-                    if (cfg.qk_norm) VKH_TRY(alloc(lg[l].pqk, qk_partial_floats()));
-                }
-                if (wsb) {
-                    char *w = nullptr;
-                    VKH_TRY(alloc(w, wsb));
-                    gws2 = GemmWs{w, wsb};
-                }
-            }
         } else {
             VKH_TRY(alloc(fn_out, (size_t)T * D));
             // split-K workspace of the fp32 GEMMs (g32_*), if their plan asks for one
@@ -558,6 +519,68 @@ struct vkh_runner {
                 char *w = nullptr;
                 VKH_TRY(alloc(w, wsb));
                 gws = GemmWs{w, wsb};
+            }
+        }
+        if (concurrent) {
+            // the side stream (weight gradients, Adam) and each layer's gradient
+            // operands for it, in the step's precision
+            VKH_HIP(hipStreamCreateWithFlags(&side, hipStreamNonBlocking));
+            ev_layer.assign(L, nullptr);
+            for (int l = 0; l < L; ++l)
+                VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], kOrderEvent));
+            if (recompute) {
+                ev_sdone.assign(L, nullptr);
+                for (int l = 0; l < L; ++l)
+                    VKH_HIP(hipEventCreateWithFlags(&ev_sdone[l], kOrderEvent));
+            }
+            VKH_HIP(hipEventCreateWithFlags(&ev_side, kOrderEvent));
+            VKH_HIP(hipEventCreateWithFlags(&ev_head, kOrderEvent));
+            VKH_HIP(hipEventCreateWithFlags(&ev_lm, kOrderEvent));
+            if (embed_split_ok()) {
+                VKH_TRY(alloc(emb_mark, (size_t)V));
+                VKH_HIP(fill_f32(reinterpret_cast<float *>(emb_mark), (size_t)V, 0.f, own));
+            }
+            lg.assign(L, LayerGrads{});
+            const int n_g = recompute ? std::min(L, kGradSets) : L;
+            const int n_dy = recompute ? std::min(L, kDyRing) : L;
+            for (int l = 0; l < L; ++l) {
+                if (l < n_dy) {
+                    if (b16()) VKH_TRY(alloc(lg[l].dyb, (size_t)T * D));
+                    else VKH_TRY(alloc(lg[l].dyf, (size_t)T * D));
+                } else {
+                    lg[l].dyb = lg[l % n_dy].dyb;
+                    lg[l].dyf = lg[l % n_dy].dyf;
+                }
+                if (l >= n_g) {
+                    const LayerGrads &o = lg[l % n_g];
+                    lg[l].gub = o.gub; lg[l].midb = o.midb; lg[l].qkvb = o.qkvb;
+                    lg[l].guf = o.guf; lg[l].midf = o.midf; lg[l].qkvf = o.qkvf;
+                    lg[l].pn1 = o.pn1; lg[l].pn2 = o.pn2; lg[l].pqk = o.pqk;
+                    continue;
+                }
+                if (b16()) {
+                    VKH_TRY(alloc(lg[l].gub, (size_t)T * 2 * F));
+                    VKH_TRY(alloc(lg[l].midb, (size_t)T * D));
+                    VKH_TRY(alloc(lg[l].qkvb, (size_t)T * qkvd));
+                } else {
+                    VKH_TRY(alloc(lg[l].guf, (size_t)T * 2 * F));
+                    VKH_TRY(alloc(lg[l].midf, (size_t)T * D));
+                    VKH_TRY(alloc(lg[l].qkvf, (size_t)T * qkvd));
+                }
+                VKH_TRY(alloc(lg[l].pn1, rmsnorm_partial_floats(T, D)));
+                VKH_TRY(alloc(lg[l].pn2, rmsnorm_partial_floats(T, D)));
+                if (cfg.qk_norm) VKH_TRY(alloc(lg[l].pqk, qk_partial_floats()));
+            }
+            // the side stream's own split-K workspace
+            size_t wsb2 = 0;
+            auto need2 = [&](int m, int n, int k) {
+                wsb2 = std::max(wsb2, b16() ? g16_ws_bytes_for(m, n, k) : g32_ws_bytes_for(m, n, k));
+            };
+            need2(D, F, T); need2(2 * F, D, T); need2(D, qd, T); need2(qkvd, D, T); need2(V, D, T);
+            if (wsb2) {
+                char *w = nullptr;
+                VKH_TRY(alloc(w, wsb2));
+                gws2 = GemmWs{w, wsb2};
             }
         }
         VKH_TRY(alloc(ce_lse, T));
@@ -918,10 +941,13 @@ struct vkh_runner {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const LayerGrads &g = lg[l];
-        VKH_TRY(linear_dw_on(matb(g.dyb, D), m_gated(a), s.t[8], D, F, gws2, side));
-        VKH_TRY(linear_dw_on(matb(g.gub, 2 * F), m_n2(a), s.t[6], 2 * F, D, gws2, side));
-        VKH_TRY(linear_dw_on(matb(g.midb, D), m_attn(a), s.t[4], D, qd, gws2, side));
-        VKH_TRY(linear_dw_on(matb(g.qkvb, qkvd), m_n1(a), s.t[1], qkvd, D, gws2, side));
+        const bool h = b16();
+        VKH_TRY(linear_dw_on(h ? matb(g.dyb, D) : matf(g.dyf, D), m_gated(a), s.t[8], D, F, gws2, side));
+        VKH_TRY(linear_dw_on(h ? matb(g.gub, 2 * F) : matf(g.guf, 2 * F), m_n2(a), s.t[6], 2 * F, D,
+                             gws2, side));
+        VKH_TRY(linear_dw_on(h ? matb(g.midb, D) : matf(g.midf, D), m_attn(a), s.t[4], D, qd, gws2, side));
+        VKH_TRY(linear_dw_on(h ? matb(g.qkvb, qkvd) : matf(g.qkvf, qkvd), m_n1(a), s.t[1], qkvd, D,
+                             gws2, side));
         if (gains_in_adam) return VKH_OK;
         // norm-gain gradients from the partial sums the main stream wrote
         const int rp = rmsnorm_partial_rows(T);
@@ -1064,10 +1090,15 @@ struct vkh_runner {
         Acts &a = acts[l];
         LayerSpans &s = ls[l];
         const float *x_in = l == 0 ? x_emb : acts[l - 1].y;
-        // concurrent mode: this layer's own gradient copies; dW is deferred to the side stream
+        // concurrent mode: this layer's own gradient operands (bf16 copies, or
+        // in fp32 the tensors themselves); dW is deferred to the side stream
+        const bool c32 = concurrent && !b16();
         bf16 *d_gub = concurrent ? lg[l].gub : this->d_gub;
         bf16 *d_midb = concurrent ? lg[l].midb : this->d_midb;
         bf16 *d_qkvb = concurrent ? lg[l].qkvb : this->d_qkvb;
+        float *d_gu = c32 ? lg[l].guf : this->d_gu;
+        float *d_mid = c32 ? lg[l].midf : this->d_mid;
+        float *d_qkv = c32 ? lg[l].qkvf : this->d_qkv;
         auto linear_dw = [&](Mat dy_, Mat x_, const Span &w_, int N_, int K_) -> vkh_status {
             if (concurrent) return VKH_OK;
             return this->linear_dw(dy_, x_, w_, N_, K_);
@@ -1243,12 +1274,31 @@ struct vkh_runner {
         } else {
             VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
                                 cce_work, cur));
-            VKH_HIP(cce_backward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, dz, d_fn, dw_lm, 0.f, cur));
+            VKH_HIP(cce_backward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, dz, d_fn,
+                                 concurrent ? nullptr : dw_lm, 0.f, cur));
+            if (concurrent && dw_lm) {  // as above, on the fp32 logits gradient
+                if (split) {
+                    if (++mark_stamp == 0) {
+                        VKH_HIP(fill_f32(reinterpret_cast<float *>(emb_mark), (size_t)V, 0.f, cur));
+                        mark_stamp = 1;
+                    }
+                    VKH_HIP(mark_rows(tok_d, T, emb_mark, V, mark_stamp, cur));
+                }
+                VKH_HIP(hipEventRecord(ev_head, cur));
+                VKH_HIP(hipStreamWaitEvent(side, ev_head, 0));
+                VKH_HIP(g32_tn((const float *)dz, V, fn_out, D, dw_lm, D, T, V, D, 1.f, 0.f, gws2, side));
+                if (split) VKH_TRY(embed_adam_early());
+                VKH_HIP(hipEventRecord(ev_lm, side));
+            }
         }
-        VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), dx[0],
-                                 concurrent ? lg[L - 1].dyb : dxb[0], nullptr, Gd(final_norm),
-                                 partial, T, D, cfg.rms_eps, 0, cur));
-        VKH_TRY(capture_boundary(L, dx[0]));
+        // fp32 concurrent: each layer's dy is its own buffer (the side stream's
+        // dW_down reads it after the main stream has moved on)
+        const bool c32 = concurrent && !b16();
+        float *top = c32 ? lg[L - 1].dyf : dx[0];
+        VKH_HIP(rmsnorm_backward(d_fn, acts[L - 1].y, W(final_norm), top,
+                                 b16() ? (concurrent ? lg[L - 1].dyb : dxb[0]) : nullptr, nullptr,
+                                 Gd(final_norm), partial, T, D, cfg.rms_eps, 0, cur));
+        VKH_TRY(capture_boundary(L, top));
         int c = 0;
         for (int l = L - 1; l >= 0; --l) {
             if (recompute) {
@@ -1257,8 +1307,10 @@ struct vkh_runner {
                 // the set holds layer l + kActSets's activations: run l's forward again
                 if (l + kActSets < L) VKH_TRY(layer_forward(l, false));
             }
+            float *out = c32 && l > 0 ? lg[l - 1].dyf : dx[c ^ 1];
             if (concurrent) {
-                VKH_TRY(layer_backward(l, dx[c], lg[l].dyb, dx[c ^ 1], l > 0 ? lg[l - 1].dyb : nullptr));
+                VKH_TRY(layer_backward(l, c32 ? lg[l].dyf : dx[c], c32 ? nullptr : lg[l].dyb, out,
+                                       !c32 && l > 0 ? lg[l - 1].dyb : nullptr));
                 // layer l's gradient inputs are final: its dW GEMMs (and, with Adam,
                 // its update) run on the side stream while the main stream goes on
                 VKH_HIP(hipEventRecord(ev_layer[l], cur));
@@ -1269,7 +1321,7 @@ struct vkh_runner {
             } else {
                 VKH_TRY(layer_backward(l, dx[c], dxb[c], dx[c ^ 1], dxb[c ^ 1]));
             }
-            VKH_TRY(capture_boundary(l, dx[c ^ 1]));
+            VKH_TRY(capture_boundary(l, out));
             c ^= 1;
         }
         // the adapters' last gradients before Adam and the next forward
