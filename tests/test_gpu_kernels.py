@@ -127,7 +127,8 @@ def test_embed_lookup_is_exact_gather():
     assert np.array_equal(host(out), O.embedding_forward(E, ids, D))
 
 
-@pytest.mark.parametrize("n,V,D", [(6, 16, 5), (2048, 151936, 1024), (8192, 4096, 64)])
+@pytest.mark.parametrize("n,V,D", [(6, 16, 5), (2048, 151936, 1024), (8192, 4096, 64),
+                                   (1001, 300, 128), (2500, 40, 2560)])
 def test_embedding_backward_bit_exact(n, V, D):
     """gpu_train.zig:4845-4930: exact scatter targets and position-order sums."""
     from valkyr_amd import kernels as K
