@@ -510,6 +510,39 @@ def test_lora_step_parity(precision, over):
     assert np.array_equal(base_before, r.get(0, 0, 1))
 
 
+QWEN3_4B_WIDTHS = dict(dim=2560, n_heads=32, n_kv_heads=8, head_dim=128, ff_dim=9728,
+                       vocab_size=151936, tied_embeddings=1, rotary_dim=128, seq_len=2048,
+                       n_seqs=1, n_layers=2, lora_targets=0xF, lora_rank=16, lora_alpha=32.0,
+                       lora_lr_b_scale=1.0)
+
+
+def test_lora_step_qwen3_4b_widths():
+    """Config 4 in every respect except n_layers = 2 (Qwen3-4B widths, 1 x 2048,
+    32 / 8 heads of 128, V = 151936 tied, LoRA r = 16 on q/k/v/o over a frozen bf16
+    base): the kernels the config-4 step launches at their real shapes, i.e. the
+    base GEMMs with the rank-16 update in their epilogues on the 128 x 128 plans and
+    the split dK/dV grid (8 KV heads x 16 key blocks, launched as 256 blocks), held
+    to the oracle's bf16-operand model stage by stage (each layer's output, boundary
+    gradient and adapter gradients from the GPU's own boundary tensors) at 1e-2, at
+    step 1 (B = 0: dA exactly 0) and step 2.  Stage by stage because the whole-step
+    bf16 distance of dB at these widths measured 9.8e-3, at the bf16 step's own
+    sensitivity floor."""
+    note("lora step at Qwen3-4B widths, 2 layers")
+    m, r, tok, tgt, cfg = build_pair(1, **QWEN3_4B_WIDTHS)
+    plan = r.attention_backward_plan()
+    note(f"  attention backward plan {plan}")
+    assert plan["path"] == "recompute" and plan["dkv_blocks"] == 256 and plan["qk_epilogue"], plan
+    lk = lora_keys(cfg)
+    stage_compare(m, r, tok, tgt, cfg, 1e-2, "lora step 1 stages")
+    for (l, w) in lk:
+        if w % 2 == 0:  # dA == 0 exactly at B = 0
+            assert np.all(r.get(1, l, w) == 0)
+    r.step(tok, tgt)
+    for k in lk:  # step-2 gradients from identical adapters (see test_lora_step_parity)
+        m.tensor(0, *k)[:] = r.get(0, *k)
+    stage_compare(m, r, tok, tgt, cfg, 1e-2, "lora step 2 stages")
+
+
 def test_lora_bf16_base_stored_in_bf16(tmp_path):
     """A bf16 LoRA runner (frozen bf16 base, config 4's class) holds its base
     matrices in bf16 only: no fp32 copy in device memory, set_tensor rounds to
