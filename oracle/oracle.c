@@ -837,21 +837,51 @@ void orc_softmax_ce_loss_grad(float *d_logits, const float *logits, const uint32
 
 /* ── LoRA: src/cpu/lora.zig:75-199 ─────────────────────────────────────── */
 
+/* out[m, n] = (float) sum_k (double) x[m, k] * (double) W[n, k]: every output its own
+ * fp64 sum, k ascending.  Rows go DR_G at a time over a transposed copy of their x
+ * values, so the DR_G sums of one W row advance together (vectorised across rows, each
+ * still summed in k order: the values do not depend on the grouping). */
+static void dot_rows_f64(float *out, const float *x, const float *W, size_t M, size_t N,
+                         size_t K) {
+    enum { DR_G = 16 };
+    const size_t ng = M / DR_G;
+    float *xt = malloc((ng ? ng : 1) * K * DR_G * sizeof(float));
+#pragma omp parallel for schedule(static)
+    for (size_t g = 0; g < ng; ++g)
+        for (size_t j = 0; j < DR_G; ++j)
+            for (size_t k = 0; k < K; ++k) xt[(g * K + k) * DR_G + j] = x[(g * DR_G + j) * K + k];
+    const long long tasks = (long long)ng * (long long)N;
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < tasks; ++i) {
+        const size_t g = (size_t)i / N, n = (size_t)i % N;
+        const float *xg = xt + g * K * DR_G, *wr = W + n * K;
+        double acc[DR_G];
+        for (int j = 0; j < DR_G; ++j) acc[j] = 0;
+        for (size_t k = 0; k < K; ++k) {
+            const double wv = (double)wr[k];
+            for (int j = 0; j < DR_G; ++j) acc[j] += (double)xg[k * DR_G + j] * wv;
+        }
+        for (int j = 0; j < DR_G; ++j) out[(g * DR_G + j) * N + n] = (float)acc[j];
+    }
+    free(xt);
+    const long long rest = (long long)(M - ng * DR_G) * (long long)N;
+#pragma omp parallel for schedule(static)
+    for (long long i = 0; i < rest; ++i) {
+        const size_t m = ng * DR_G + (size_t)i / N, n = (size_t)i % N;
+        double s = 0;
+        for (size_t k = 0; k < K; ++k) s += (double)x[m * K + k] * (double)W[n * K + k];
+        out[m * N + n] = (float)s;
+    }
+}
+
+/* y = x w^T (fp64 sums, k ascending), inter = x a^T, then y += alpha/r * (inter b^T
+ * summed in fp64, i ascending, rounded to fp32 before the scale). */
 void orc_lora_forward(const float *x, const float *w, const float *a, const float *b,
                       size_t M, size_t N, size_t K, size_t r, float alpha_over_r,
                       float *y_out, float *inter) {
-    for (size_t m = 0; m < M; ++m)
-        for (size_t n = 0; n < N; ++n) {
-            double s = 0;
-            for (size_t k = 0; k < K; ++k) s += (double)x[m * K + k] * (double)w[n * K + k];
-            y_out[m * N + n] = (float)s;
-        }
-    for (size_t m = 0; m < M; ++m)
-        for (size_t i = 0; i < r; ++i) {
-            double s = 0;
-            for (size_t k = 0; k < K; ++k) s += (double)x[m * K + k] * (double)a[i * K + k];
-            inter[m * r + i] = (float)s;
-        }
+    dot_rows_f64(y_out, x, w, M, N, K);
+    dot_rows_f64(inter, x, a, M, r, K);
+#pragma omp parallel for schedule(static)
     for (size_t m = 0; m < M; ++m)
         for (size_t n = 0; n < N; ++n) {
             double s = 0;
@@ -860,44 +890,100 @@ void orc_lora_forward(const float *x, const float *w, const float *a, const floa
         }
 }
 
+/* dy_B = dy b (fp64 over n ascending); dx = dy w + alpha/r * dy_B a, the base part an
+ * fp64 sum over n ascending and the update an fp64 sum over i ascending, added in fp64;
+ * dA += alpha/r * dy_B^T x and dB += alpha/r * dy^T inter, fp64 sums over m ascending.
+ * Parallel over independent outputs; every output keeps its own summation order. */
 void orc_lora_backward(const float *dy, const float *x, const float *w, const float *a,
                        const float *b, const float *inter, size_t M, size_t N, size_t K,
                        size_t r, float alpha_over_r, float *dx, float *dA, float *dB) {
-    float *dy_B = malloc(M * r * sizeof(float));
-    for (size_t m = 0; m < M; ++m)
-        for (size_t i = 0; i < r; ++i) {
-            double s = 0;
-            for (size_t n = 0; n < N; ++n) s += (double)dy[m * N + n] * (double)b[n * r + i];
-            dy_B[m * r + i] = (float)s;
-        }
-    if (dx) {
-        double *acc = malloc(K * sizeof(double));
-        for (size_t m = 0; m < M; ++m) {
-            for (size_t k = 0; k < K; ++k) acc[k] = 0;
-            for (size_t n = 0; n < N; ++n) {
-                double g = dy[m * N + n];
-                for (size_t k = 0; k < K; ++k) acc[k] += g * (double)w[n * K + k];
-            }
-            for (size_t k = 0; k < K; ++k) {
-                double s_lora = 0;
-                for (size_t i = 0; i < r; ++i) s_lora += (double)dy_B[m * r + i] * (double)a[i * K + k];
-                dx[m * K + k] = (float)(acc[k] + alpha_over_r * s_lora);
-            }
-        }
-        free(acc);
-    }
-    for (size_t i = 0; i < r; ++i)
-        for (size_t k = 0; k < K; ++k) {
-            double s = 0;
-            for (size_t m = 0; m < M; ++m) s += (double)dy_B[m * r + i] * (double)x[m * K + k];
-            dA[i * K + k] += alpha_over_r * (float)s;
-        }
+    float *dy_B = malloc((M ? M : 1) * (r ? r : 1) * sizeof(float));
+    float *bt = malloc((N ? N : 1) * (r ? r : 1) * sizeof(float));
     for (size_t n = 0; n < N; ++n)
-        for (size_t i = 0; i < r; ++i) {
-            double s = 0;
-            for (size_t m = 0; m < M; ++m) s += (double)dy[m * N + n] * (double)inter[m * r + i];
-            dB[n * r + i] += alpha_over_r * (float)s;
+        for (size_t i = 0; i < r; ++i) bt[i * N + n] = b[n * r + i];
+    dot_rows_f64(dy_B, dy, bt, M, r, N);
+    free(bt);
+    if (dx) {
+        enum { LX_G = 8 };
+        const size_t nb = (M + LX_G - 1) / LX_G;
+#pragma omp parallel
+        {
+            double *acc = malloc(LX_G * K * sizeof(double));
+#pragma omp for schedule(static)
+            for (size_t blk = 0; blk < nb; ++blk) {
+                const size_t m0 = blk * LX_G, mr = m0 + LX_G <= M ? LX_G : M - m0;
+                for (size_t i = 0; i < mr * K; ++i) acc[i] = 0;
+                for (size_t n = 0; n < N; ++n) {
+                    const float *wr = w + n * K;
+                    for (size_t q = 0; q < mr; ++q) {
+                        const double g = dy[(m0 + q) * N + n];
+                        double *aq = acc + q * K;
+                        for (size_t k = 0; k < K; ++k) aq[k] += g * (double)wr[k];
+                    }
+                }
+                for (size_t q = 0; q < mr; ++q) {
+                    const size_t m = m0 + q;
+                    for (size_t k = 0; k < K; ++k) {
+                        double s_lora = 0;
+                        for (size_t i = 0; i < r; ++i)
+                            s_lora += (double)dy_B[m * r + i] * (double)a[i * K + k];
+                        dx[m * K + k] = (float)(acc[q * K + k] + alpha_over_r * s_lora);
+                    }
+                }
+            }
+            free(acc);
         }
+    }
+    {
+        enum { LA_KC = 256 };
+        const size_t nkc = (K + LA_KC - 1) / LA_KC;
+#pragma omp parallel
+        {
+            double *acc = malloc((r ? r : 1) * LA_KC * sizeof(double));
+#pragma omp for schedule(static)
+            for (size_t c = 0; c < nkc; ++c) {
+                const size_t k0 = c * LA_KC, kn = k0 + LA_KC <= K ? LA_KC : K - k0;
+                for (size_t i = 0; i < r * LA_KC; ++i) acc[i] = 0;
+                for (size_t m = 0; m < M; ++m) {
+                    const float *xr = x + m * K + k0;
+                    for (size_t i = 0; i < r; ++i) {
+                        const double g = dy_B[m * r + i];
+                        double *ai = acc + i * LA_KC;
+                        for (size_t k = 0; k < kn; ++k) ai[k] += g * (double)xr[k];
+                    }
+                }
+                for (size_t i = 0; i < r; ++i)
+                    for (size_t k = 0; k < kn; ++k)
+                        dA[i * K + k0 + k] += alpha_over_r * (float)acc[i * LA_KC + k];
+            }
+            free(acc);
+        }
+    }
+    {
+        enum { LB_NC = 64 };
+        const size_t nnc = (N + LB_NC - 1) / LB_NC;
+#pragma omp parallel
+        {
+            double *acc = malloc(LB_NC * (r ? r : 1) * sizeof(double));
+#pragma omp for schedule(static)
+            for (size_t c = 0; c < nnc; ++c) {
+                const size_t n0 = c * LB_NC, nn = n0 + LB_NC <= N ? LB_NC : N - n0;
+                for (size_t i = 0; i < LB_NC * r; ++i) acc[i] = 0;
+                for (size_t m = 0; m < M; ++m) {
+                    const float *ir = inter + m * r;
+                    for (size_t q = 0; q < nn; ++q) {
+                        const double g = dy[m * N + n0 + q];
+                        double *aq = acc + q * r;
+                        for (size_t i = 0; i < r; ++i) aq[i] += g * (double)ir[i];
+                    }
+                }
+                for (size_t q = 0; q < nn; ++q)
+                    for (size_t i = 0; i < r; ++i)
+                        dB[(n0 + q) * r + i] += alpha_over_r * (float)acc[q * r + i];
+            }
+            free(acc);
+        }
+    }
     free(dy_B);
 }
 

@@ -516,29 +516,44 @@ QWEN3_4B_WIDTHS = dict(dim=2560, n_heads=32, n_kv_heads=8, head_dim=128, ff_dim=
                        lora_lr_b_scale=1.0)
 
 
-def test_lora_step_qwen3_4b_widths():
+@pytest.fixture(scope="module")
+def qwen3_4b_pair():
     """Config 4 in every respect except n_layers = 2 (Qwen3-4B widths, 1 x 2048,
     32 / 8 heads of 128, V = 151936 tied, LoRA r = 16 on q/k/v/o over a frozen bf16
-    base): the kernels the config-4 step launches at their real shapes, i.e. the
-    base GEMMs with the rank-16 update in their epilogues on the 128 x 128 plans and
-    the split dK/dV grid (8 KV heads x 16 key blocks, launched as 256 blocks), held
-    to the oracle's bf16-operand model stage by stage (each layer's output, boundary
-    gradient and adapter gradients from the GPU's own boundary tensors) at 1e-2, at
-    step 1 (B = 0: dA exactly 0) and step 2.  Stage by stage because the whole-step
-    bf16 distance of dB at these widths measured 9.8e-3, at the bf16 step's own
-    sensitivity floor."""
+    base) and the oracle on the same weights, shared by the step-1 and step-2 tests
+    below (each about a minute of oracle work)."""
     note("lora step at Qwen3-4B widths, 2 layers")
     m, r, tok, tgt, cfg = build_pair(1, **QWEN3_4B_WIDTHS)
+    yield m, r, tok, tgt, cfg
+    r.close()
+
+
+def test_lora_step_qwen3_4b_widths(qwen3_4b_pair):
+    """The kernels the config-4 step launches at their real shapes, i.e. the base
+    GEMMs with the rank-16 update in their epilogues on the 128 x 128 plans and the
+    split dK/dV grid (8 KV heads x 16 key blocks, launched as 256 blocks), held to
+    the oracle's bf16-operand model stage by stage (each layer's output, boundary
+    gradient and adapter gradients from the GPU's own boundary tensors) at 1e-2, at
+    step 1 (B = 0: dA exactly 0).  Stage by stage because the whole-step bf16
+    distance of dB at these widths measured 9.8e-3, at the bf16 step's own
+    sensitivity floor."""
+    m, r, tok, tgt, cfg = qwen3_4b_pair
     plan = r.attention_backward_plan()
     note(f"  attention backward plan {plan}")
     assert plan["path"] == "recompute" and plan["dkv_blocks"] == 256 and plan["qk_epilogue"], plan
-    lk = lora_keys(cfg)
     stage_compare(m, r, tok, tgt, cfg, 1e-2, "lora step 1 stages")
-    for (l, w) in lk:
+    for (l, w) in lora_keys(cfg):
         if w % 2 == 0:  # dA == 0 exactly at B = 0
             assert np.all(r.get(1, l, w) == 0)
+
+
+def test_lora_step2_qwen3_4b_widths(qwen3_4b_pair):
+    """Step 2 at the same widths (B != 0 after one Adam step, so both adapter
+    gradients and the update in the epilogues are live), stage by stage at 1e-2
+    from adapters copied to the oracle (see test_lora_step_parity)."""
+    m, r, tok, tgt, cfg = qwen3_4b_pair
     r.step(tok, tgt)
-    for k in lk:  # step-2 gradients from identical adapters (see test_lora_step_parity)
+    for k in lora_keys(cfg):
         m.tensor(0, *k)[:] = r.get(0, *k)
     stage_compare(m, r, tok, tgt, cfg, 1e-2, "lora step 2 stages")
 
