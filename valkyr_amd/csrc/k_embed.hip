@@ -100,6 +100,9 @@ __global__ __launch_bounds__(EO_NT) void embed_own_k(const float *dy, const uint
 // entries (4 KB of LDS, so occupancy is not bounded by the list), and the
 // owner adds their dy rows in that order.  Each thread owns float4 column
 // chunks tid + 256 j (dim <= 4096), kept in registers across the chunks.
+// Where no other position of a chunk holds the id (every position of a
+// batch of distinct ids), the one barrier of the duplicate test also says
+// so, and the chunk's list is p alone: no scan, no list, no further barrier.
 constexpr int EO_CH = 8 * EO_NT;  // positions per chunk
 template <bool ADAM>
 __global__ __launch_bounds__(EO_NT) void embed_own2_k(const float *dy, const uint32_t *ids, int n,
@@ -107,6 +110,7 @@ __global__ __launch_bounds__(EO_NT) void embed_own2_k(const float *dy, const uin
                                                        int accumulate, EmbedAdam ea) {
     __shared__ uint16_t list[EO_CH];
     __shared__ int wtot[EO_NT / 64];
+    __shared__ int wflag[2][EO_NT / 64];
     const int p = blockIdx.x, t = threadIdx.x, lane = t % 64, w = t / 64;
     const uint32_t tok = ids[p];
     if (tok >= (uint32_t)vocab) return;  // uniform over the block
@@ -155,8 +159,32 @@ __global__ __launch_bounds__(EO_NT) void embed_own2_k(const float *dy, const uin
             dup |= eq && i0 + j < p;
             mb |= (eq && i0 + j >= p) ? 1u << j : 0u;
         }
-        if (__syncthreads_or(dup)) return;  // an earlier position owns tok
-        if (base + EO_CH <= p) continue;     // this chunk holds no position >= p
+        // one barrier answers both block-wide questions: does an earlier
+        // position hold tok (bit 0), and does a position of this chunk other
+        // than p (bit 1); the flags alternate between two slots by chunk
+        const unsigned other = mb & ~(p >= i0 && p < i0 + 8 ? 1u << (p - i0) : 0u);
+        const int par = (base / EO_CH) & 1;
+        const bool any_dup = __ballot(dup) != 0, any_other = __ballot(other != 0) != 0;
+        if (lane == 0) wflag[par][w] = (any_dup ? 1 : 0) | (any_other ? 2 : 0);
+        __syncthreads();
+        int fl = 0;
+#pragma unroll
+        for (int k = 0; k < EO_NT / 64; ++k) fl |= wflag[par][k];
+        if (fl & 1) return;              // an earlier position owns tok
+        if (base + EO_CH <= p) continue;  // this chunk holds no position >= p
+        if (!(fl & 2)) {
+            // no other position of the chunk holds tok: its list would be p
+            // alone (p in this chunk) or empty, so neither list nor scan
+            if (p >= base) {
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    if (t + EO_NT * j < d4) {
+                        acc[j].x += own[j].x; acc[j].y += own[j].y;
+                        acc[j].z += own[j].z; acc[j].w += own[j].w;
+                    }
+            }
+            continue;
+        }
         // wave-inclusive prefix of the match counts, then the block offsets
         const int c = __popc(mb);
         int x = c;
