@@ -182,7 +182,12 @@ __global__ __launch_bounds__(FNT, 2) void fa_fwd_f32m_k(AttnShape s, const float
 // (32-key blocks on 2 waves, twice the grid in zigzag order, measured 185.5
 // against 173.1 us at config 3: each staged query tile then feeds half the
 // keys.  Where the 64-key grid is one block per CU, the causal 8:1 spread of
-// block work stays.)
+// block work stays.  Two groups of 4 waves per 64-key block, each taking
+// every other (head, query tile) step from its own staged tiles and adding
+// its sums to the other group's through LDS at the end: 159.5 against 178 us
+// alone, but the fp32 step 78.2 against 77.0 ms, since the 136 KB block and
+// its 8 waves of 242 VGPRs leave no room on the CU for the second stream's
+// GEMM blocks.)
 template <int HD>
 __global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtrs p, bool zz) {
     constexpr int P = HD + 4, NU = HD / 16;
