@@ -187,7 +187,12 @@ __global__ __launch_bounds__(FNT, 2) void fa_fwd_f32m_k(AttnShape s, const float
 // its sums to the other group's through LDS at the end: 159.5 against 178 us
 // alone, but the fp32 step 78.2 against 77.0 ms, since the 136 KB block and
 // its 8 waves of 242 VGPRs leave no room on the CU for the second stream's
-// GEMM blocks.)
+// GEMM blocks.  Splitting the heavier half of the key blocks in two, each
+// half of the steps summed raw and the halves added by a combine kernel in a
+// fixed order: dK/dV 305 -> 205 us in the step plus a 20.5 us combine, but dQ
+// then meets more of the second stream's work (98 -> 153 us) and the step
+// went 77.0 -> 77.2 ms: with both streams busy the step is set by their
+// total work, not by this kernel's span.)
 template <int HD>
 __global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtrs p, bool zz) {
     constexpr int P = HD + 4, NU = HD / 16;
