@@ -107,8 +107,12 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
 //   * 128 x 64 where that evens the rounds (384 tiles of 128 x 128 = 768 of
 //     128 x 64: down dx 107 against 134 us, gate/up dW 209 against 259);
 //   * fewer than 512 tiles of 128 x 64 (the N = 1024 outputs and dW of o /
-//     down): 128 x 64 split 2 ways along K (q/k/v dx 149, gate/up dx 213, down
-//     dW 119 us against 174, 254, 154 unsplit in one block pair).
+//     down): 128 x 64 with the K range split over the two wave groups of one
+//     block.  Alone, split-K over two launches plus the reduce is faster
+//     (q/k/v dx 149, gate/up dx 213, down dW 119 us against 174, 254, 154),
+//     but in the two-stream step the in-block form is (76.3-77.0 against
+//     76.5-77.1 ms in four alternating pairs; plain 128 x 64: 77.3-77.4): the
+//     reduce launches' 4.2 ms of partial traffic per step is gone.
 Plan plan32(const GemmShape &s, size_t ws_bytes) {
     auto tiles = [&](int bm, int bn) { return (long)ceil_div(s.M, bm) * (long)ceil_div(s.N, bn); };
     auto fill = [](long t) { return (double)t / (256.0 * (double)((t + 255) / 256)); };
@@ -116,7 +120,7 @@ Plan plan32(const GemmShape &s, size_t ws_bytes) {
     const int nk = (s.K + 31) / 32;
     Plan p{Pick::T128x64, 1};
     if (t128 >= 256 && fill(t128) >= fill(t64)) p = Plan{Pick::T128w8, 1};
-    else if (t64 < 512) p = Plan{Pick::T128x64, 2};
+    else if (t64 < 512) p = Plan{Pick::T128x64ks2, 1};
     while (p.splits > 1 && (nk / p.splits < 8 || ws_for(p, s) > ws_bytes)) --p.splits;
     return p;
 }
