@@ -26,6 +26,13 @@ using TBig = Tile16<256, 256, 2, 4>;
 using T128 = Tile16<128, 128, 2, 2>;
 using T128x64 = Tile16<128, 64, 2, 2>;
 using T128w8 = Tile16<128, 128, 2, 4>;  // 8 waves of 64 x 32
+// The in-block split-K block (two 4-wave groups, one block per CU whatever its
+// LDS) with three slab buffers per group (144 KB): two slabs in flight per
+// group for these latency-bound N = 1024 shapes.  Alone: o / down forward
+// 20.0 / 27.8 -> 18.4 / 24.5 us, gate/up and q/k/v dx 50.3 / 34.7 -> 48.4 / 33.6
+// us; the bf16 step 19.33-19.34 -> 19.31-19.32 ms.  (In fp32 mode, whose slabs
+// are half as deep, it made the fp32 step slower: 77.3 against 76.65 ms.)
+using T128x64s3 = Tile16<128, 64, 2, 2, 3>;
 // (Three slab buffers were measured slower for these tiles: the larger LDS
 // footprint drops a block per CU.  Staging the slabs through VGPRs two slabs
 // ahead, which doubles the time a load has to arrive without more LDS, was
@@ -90,7 +97,7 @@ hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e,
     case Pick::Big: return launch_gemm16<TBig, LA, LB>(a, b, s, e, sk, g, st);
     case Pick::T128: return launch_gemm16<T128, LA, LB>(a, b, s, e, sk, g, st);
     case Pick::T128w8: return launch_gemm16<T128w8, LA, LB>(a, b, s, e, sk, g, st);
-    case Pick::T128x64ks2: return launch_gemm16_ks2<T128x64, LA, LB>(a, b, s, e, g, st);
+    case Pick::T128x64ks2: return launch_gemm16_ks2<T128x64s3, LA, LB>(a, b, s, e, g, st);
     default: return launch_gemm16<T128x64, LA, LB>(a, b, s, e, sk, g, st);
     }
 }
