@@ -566,6 +566,16 @@ vkh_status vkh_linear_backward_dw(const float *dy, const float *x, float *dw, ui
  * have no direct counterpart there beyond the three entry points above. */
 vkh_status vkh_matmul_nt_bf16(const void *x, const void *w, float *y, uint32_t M, uint32_t N,
                               uint32_t K, vkh_stream stream);
+/* The bf16 step's gate/up projection and SwiGLU forward: gu[M, 2F] = x[M, K]
+ * w_gu[2F, K]^T (w_gu = the gate rows, then the up rows, as Runner stacks
+ * them), gated[M, F] = bf16(swiglu(gu[:, f], gu[:, F + f])).  No single
+ * counterpart in the reference: it is matmul_nt_v2.comp for w_gate and w_up
+ * followed by swiglu_forward.comp (train_transformer.zig:839-851), run as one
+ * launch with the SwiGLU in the GEMM's epilogue where the tile plan allows
+ * (the 8-wave 128 x 128 tile) and as the two passes elsewhere, with the same
+ * bits either way. */
+vkh_status vkh_gate_up_swiglu_bf16(const void *x, const void *w_gu, float *gu, void *gated,
+                                   uint32_t M, uint32_t F, uint32_t K, vkh_stream stream);
 vkh_status vkh_linear_backward_dx_bf16(const void *dy, const void *w, float *dx, uint32_t M,
                                        uint32_t N, uint32_t K, vkh_stream stream);
 vkh_status vkh_linear_backward_dw_bf16(const void *dy, const void *x, float *dw, uint32_t M,

@@ -307,6 +307,40 @@ def test_linear_gemms_bf16_operands(shape):
         assert e < 1e-5, name
 
 
+@pytest.mark.parametrize("shape", [(2048, 3072, 1024), (2000, 3072, 1000), (256, 192, 128),
+                                   (130, 100, 72)])
+def test_gate_up_swiglu_matches_two_passes(shape):
+    """vkh_gate_up_swiglu_bf16 (the step's gate/up projection with the SwiGLU
+    in the GEMM's epilogue) bit for bit against the two passes it replaces:
+    vkh_matmul_nt_bf16 over the stacked [2F, K] weight, and the SwiGLU of the
+    product's halves (vkh_swiglu_forward in fp32, rounded to nearest even as
+    the epilogue stores bf16).  The first two shapes take the fused launch
+    (config 3's, and a ragged one: M and K off the tile multiples); the last
+    two the two-pass form (a plan other than the 128 x 128 tile; F not a
+    multiple of 64).  gu is also held to float64 products."""
+    from valkyr_amd import kernels as K
+    from valkyr_amd.device import f32_to_bf16_bits
+
+    M, F, Kd = shape
+    note(f"gate/up + SwiGLU M={M} F={F} K={Kd}")
+    bx, x = bf16_dev(O.normal(M * Kd, 81))
+    bW, W = bf16_dev(O.normal(2 * F * Kd, 82, 0.05))
+    bgu, bg = zeros(M * 2 * F), zeros(M * F, np.uint16)
+    K.gate_up_swiglu_bf16(bx, bW, bgu, bg, M, F, Kd)
+    gu, gated = host(bgu), host(bg, dtype=np.uint16)
+    bref = zeros(M * 2 * F)
+    K.matmul_nt_bf16(bx, bW, bref, M, 2 * F, Kd)
+    gu_ref = host(bref)
+    assert np.array_equal(gu, gu_ref)
+    g64 = x.astype(np.float64).reshape(M, Kd) @ W.astype(np.float64).reshape(2 * F, Kd).T
+    assert rel_l2(g64.ravel(), gu) < 1e-5
+    pg = dev(gu_ref.reshape(M, 2 * F)[:, :F].copy())
+    up = dev(gu_ref.reshape(M, 2 * F)[:, F:].copy())
+    out = zeros(M * F)
+    K.swiglu_forward(pg, up, out, M * F)
+    assert np.array_equal(gated, f32_to_bf16_bits(host(out)))
+
+
 # (M, N, K, r): the rank-r kernels' shapes (r a multiple of 4 up to 64, N and
 # K multiples of 64; ragged M; config 4's k/v projection width at a smaller
 # M) and a shape outside them that takes the general GEMMs.

@@ -219,6 +219,7 @@ SIGNATURES = [
     ("vkh_linear_backward_dx", ST, [P, P, P, U32, U32, U32, U32, P]),
     ("vkh_linear_backward_dw", ST, [P, P, P, U32, U32, U32, U32, P]),
     ("vkh_matmul_nt_bf16", ST, [P, P, P, U32, U32, U32, P]),
+    ("vkh_gate_up_swiglu_bf16", ST, [P, P, P, P, U32, U32, U32, P]),
     ("vkh_linear_backward_dx_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_linear_backward_dw_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_lora_forward", ST, [P, P, P, P, P, P, U32, U32, U32, U32, F, U32, P]),

@@ -422,6 +422,24 @@ vkh_status vkh_matmul_nt_bf16(const void *x, const void *w, float *y, uint32_t M
     });
 }
 
+vkh_status vkh_gate_up_swiglu_bf16(const void *x, const void *w_gu, float *gu, void *gated,
+                                   uint32_t M, uint32_t F, uint32_t K, vkh_stream stream) {
+    CHECK_ARG(x && w_gu && gu && gated, "null pointer");
+    CHECK_ARG(2ull * F < (1ull << 31), "F too large");
+    hipStream_t st = S(stream);
+    const hipError_t e = g16_gate_up_swiglu((const bf16 *)x, K, (const bf16 *)w_gu, K, gu, 2L * F,
+                                            (bf16 *)gated, F, (int)M, (int)F, (int)K, st);
+    if (e != hipErrorNotSupported) {
+        VKH_HIP(e);
+        return VKH_OK;
+    }
+    // the two-pass form: the [M, 2F] product, then the SwiGLU over its halves
+    const vkh_status r = vkh_matmul_nt_bf16(x, w_gu, gu, M, 2 * F, K, stream);
+    if (r != VKH_OK) return r;
+    VKH_HIP(swiglu_forward(gu, 2L * F, gu + F, 2L * F, gated, F, DType::BF16, (int)M, (int)F, st));
+    return VKH_OK;
+}
+
 vkh_status vkh_linear_backward_dx_bf16(const void *dy, const void *w, float *dx, uint32_t M,
                                        uint32_t N, uint32_t K, vkh_stream stream) {
     CHECK_ARG(dy && w && dx, "null pointer");

@@ -25,6 +25,16 @@ VKH_DEV bf16 to_bf16(float x) { return (bf16)x; }
 VKH_DEV float to_f32(bf16 x) { return (float)x; }
 VKH_DEV float to_f32(float x) { return x; }
 
+// SwiGLU of one element (swiglu_forward.comp / train_transformer.zig:839-851):
+// z sigmoid(z) u with sigmoid(z) = 1 / (1 + e^-z), every operation rounded on
+// its own, shared by the standalone kernel and the gate/up GEMM's epilogue so
+// both give the same bits.
+VKH_DEV float swiglu1(float z, float u) {
+#pragma clang fp contract(off)
+    const float sig = 1.0f / (1.0f + expf(-z));
+    return z * sig * u;
+}
+
 VKH_DEV bf16x8 cvt8(float a0, float a1, float a2, float a3, float a4, float a5, float a6,
                     float a7) {
     bf16x8 r;

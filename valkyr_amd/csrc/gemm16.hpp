@@ -233,9 +233,12 @@ VKH_DEV void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0f70); }  // vmcnt(0), ex
 // this tile (-1: threadIdx.x / 64, the whole block).  Every wave of the
 // workgroup must run the same number of slabs: the routine's barriers are
 // workgroup-wide.
-template <class Cfg, Lay LA, Lay LB, int TM, int TN, bool F32 = false>
+// DUALB: the B tile is two halves of BN / 2 operand rows, n0.. and bsplit + n0..
+// (the gate and up rows of one feature range for the fused SwiGLU epilogue).
+template <class Cfg, Lay LA, Lay LB, int TM, int TN, bool F32 = false, bool DUALB = false>
 VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M, int N, int kbase,
-                             int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem, int wave_in = -1) {
+                             int nk, int Kmax, f32x4 (&acc)[TM][TN], char *smem, int wave_in = -1,
+                             int bsplit = 0) {
     constexpr int KW = F32 ? 32 : 64, ES = F32 ? 4 : 2;
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NW = Cfg::WGM * Cfg::WGN, ST = Cfg::ST;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
@@ -252,7 +255,13 @@ VKH_DEV void gemm16_tile_dma(const Op16 &a, const Op16 &b, int m0, int n0, int M
     auto issue = [&](int kt) {
         char *stage = smem + (kt % ST) * STAGE;
         dma_tile<LA, BM, NW, ES>(ra, a, stage, m0, M, kbase + kt * KW, Kmax, wave, lane);
-        dma_tile<LB, BN, NW, ES>(rb, b, stage + ABYTES, n0, N, kbase + kt * KW, Kmax, wave, lane);
+        if constexpr (DUALB) {
+            dma_tile<LB, BN / 2, NW, ES>(rb, b, stage + ABYTES, n0, N, kbase + kt * KW, Kmax, wave, lane);
+            dma_tile<LB, BN / 2, NW, ES>(rb, b, stage + ABYTES + BN / 2 * 128, bsplit + n0, N,
+                                         kbase + kt * KW, Kmax, wave, lane);
+        } else {
+            dma_tile<LB, BN, NW, ES>(rb, b, stage + ABYTES, n0, N, kbase + kt * KW, Kmax, wave, lane);
+        }
     };
     // ST - 1 slabs in flight ahead of the one computing
     for (int j = 0; j < ST - 1 && j < nk; ++j) issue(j);
@@ -416,6 +425,77 @@ hipError_t launch_gemm16_ks2(const Op16 &a, const Op16 &b, const GemmShape &s, c
     hipLaunchKernelGGL((gemm16_ks2_kernel<Cfg, LA, LB, Epi, F32>), dim3(tiles), dim3(2 * Cfg::NT), 0, st,
                        a, b, s, epi, tgrp);
     return hipGetLastError();
+}
+
+// The gate/up projection with the SwiGLU forward in its epilogue: a block
+// computes 128 tokens x (64 gate features f0.. and the same 64 up features,
+// the B rows f0.. and F + f0.. of the stacked [2F, K] weight), so both halves
+// of every SwiGLU input are in one block.  Each wave stores its fp32
+// pre-activations (gu[:, f] and gu[:, F + f], the backward's inputs); the up
+// waves hand their accumulators to the gate waves of the same rows and
+// features through the idle slab buffers, which write gated = swiglu1(gate,
+// up) in bf16.  One pass instead of the GEMM plus a SwiGLU pass that reads the
+// whole gu back.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm16_swiglu_kernel(Op16 a, Op16 b, int M, int F, int K,
+                                                                  float *gu, long ldgu, bf16 *gated,
+                                                                  long ldg, int tgrp) {
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, WGN = Cfg::WGN;
+    constexpr int WM = BM / Cfg::WGM, WN = BN / WGN;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    static_assert(WGN % 2 == 0, "gate and up wave columns");
+    static_assert(Cfg::WGM * (WGN / 2) * TM * TN * 64 * 16 <= Cfg::LDS, "hand-over buffer");
+    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int wm = wave / WGN, wn = wave % WGN;
+    const int nbm = (M + BM - 1) / BM, nbn = F / (BN / 2);
+    const int nb = nbm * nbn;
+    int bid = blockIdx.x;
+    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+    int bm, bn;
+    tile_rc(bid, nbm, nbn, tgrp, bm, bn);
+    const int m0 = bm * BM, f0 = bn * (BN / 2);
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gemm16_tile_dma<Cfg, Lay::K, Lay::K, TM, TN, false, true>(a, b, m0, f0, M, 2 * F, 0,
+                                                              (K + 63) / 64, K, acc, smem, -1, F);
+    const bool up = wn >= WGN / 2;
+    const int ws = wm * (WGN / 2) + (up ? wn - WGN / 2 : wn);  // gate / up wave pair
+    const int fw = f0 + (ws % (WGN / 2)) * WN;                 // feature of the wave's column 0
+    const int g = lane / 16, c = lane % 16;
+    float *dst = gu + (up ? F : 0);
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * WM + 16 * i + 4 * g + r;
+                if (row < M) dst[(long)row * ldgu + fw + 16 * j + c] = acc[i][j][r];
+            }
+    f32x4 *xs = reinterpret_cast<f32x4 *>(smem);  // the slab loop ended with a barrier
+    if (up) {
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) xs[((ws * TM + i) * TN + j) * 64 + lane] = acc[i][j];
+    }
+    lds_barrier();
+    if (up) return;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+            const f32x4 u = xs[((ws * TM + i) * TN + j) * 64 + lane];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int row = m0 + wm * WM + 16 * i + 4 * g + r;
+                if (row < M) gated[(long)row * ldg + fw + 16 * j + c] = (bf16)swiglu1(acc[i][j][r], u[r]);
+            }
+        }
 }
 
 // One block per output tile: sum the split partials in order, then the epilogue.

@@ -137,10 +137,10 @@ __global__ __launch_bounds__(NT) void swiglu_fwd_k(const float *pg, long ldpg, c
     for (int k = 0; k < SW_U; ++k) {
         if (c0 + k * NT >= cols4) continue;
         float4 o;
-        o.x = z[k].x * sigmoidf_(z[k].x) * u[k].x;
-        o.y = z[k].y * sigmoidf_(z[k].y) * u[k].y;
-        o.z = z[k].z * sigmoidf_(z[k].z) * u[k].z;
-        o.w = z[k].w * sigmoidf_(z[k].w) * u[k].w;
+        o.x = swiglu1(z[k].x, u[k].x);
+        o.y = swiglu1(z[k].y, u[k].y);
+        o.z = swiglu1(z[k].z, u[k].z);
+        o.w = swiglu1(z[k].w, u[k].w);
         st4(g + r * ldg + 4 * (c0 + k * NT), o);
     }
 }
@@ -194,7 +194,7 @@ __global__ void swiglu_fwd_s(const float *pg, long ldpg, const float *up, long l
         const long r = (long)(i / cols);
         const int c = (int)(i % cols);
         const float z = pg[r * ldpg + c];
-        st1(g + r * ldg + c, z * sigmoidf_(z) * up[r * ldup + c]);
+        st1(g + r * ldg + c, swiglu1(z, up[r * ldup + c]));
     }
 }
 

@@ -313,6 +313,24 @@ hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, lo
     return run16<Lay::K, Lay::K>(a, b, GemmShape{M, N, K}, e, ws, st);
 }
 
+// gu[M, 2F] = x[M, K] w_gu[2F, K]^T and gated[M, F] = bf16(swiglu1(gu[:, f], gu[:, F + f])) in
+// one launch, where the plain plan for the [M, 2F] product is the 8-wave 128 x 128 tile
+// (each block then takes 64 gate and the matching 64 up features); hipErrorNotSupported
+// (nothing launched) elsewhere, and the caller runs g16_nt + swiglu_forward.
+hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, float *gu,
+                              long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st) {
+    if (M <= 0 || F <= 0 || F % 64) return hipErrorNotSupported;
+    const GemmShape s{M, 2 * F, K};
+    const Plan p = plan(s, 0);
+    if (p.tile != Pick::T128w8 || p.splits != 1) return hipErrorNotSupported;
+    Op16 a, b;
+    if (!make_op(x, ldx, M, K, a) || !make_op(w, ldw, 2L * F, K, b)) return hipErrorNotSupported;
+    const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (F / (T128w8::BN / 2)));
+    hipLaunchKernelGGL((gemm16_swiglu_kernel<T128w8>), dim3(tiles), dim3(T128w8::NT), 0, st, a, b, M,
+                       F, K, gu, ldgu, gated, ldg, tile_group_rows<Lay::K, Lay::K>());
+    return hipGetLastError();
+}
+
 hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st) {
     // an over-2 GiB dy (the head's dz at 8192 tokens): independent row chunks

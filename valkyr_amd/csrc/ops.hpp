@@ -41,6 +41,11 @@ struct GemmWs {
 hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy, int M,
                   int N, int K, const float *R, long ldr, float alpha, float beta,
                   const GemmWs &ws, hipStream_t st);
+// The gate/up projection with the SwiGLU forward fused into its epilogue (gu fp32 for
+// the backward, gated bf16 for the down projection); hipErrorNotSupported, launching
+// nothing, where the [M, 2F] product's plan is not the 8-wave 128 x 128 tile.
+hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, float *gu,
+                              long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st);
 hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
 // dx as bf16 (the operand precision of the next kernel), no split-K / fp32 copy.

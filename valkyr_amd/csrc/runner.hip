@@ -1011,9 +1011,18 @@ struct vkh_runner {
         VKH_HIP(rmsnorm_forward(a.mid, W(s.t[5]), b16() ? (void *)a.n2b : (void *)a.n2, odt, T, D,
                                 cfg.rms_eps, 0, cur));
         const Mat n2 = m_n2(a);
-        VKH_TRY(linear_fwd_lora(l, {4, 5}, n2, s.t[6], a.gu, 2 * F, 2 * F, D, nullptr, 0));
-        VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F, b16() ? (void *)a.gatedb : (void *)a.gated,
-                               F, odt, T, F, cur));
+        // gate/up with the SwiGLU in its epilogue where the fused form applies
+        hipError_t fused = hipErrorNotSupported;
+        if (b16() && !proj_lora(4) && !proj_lora(5))
+            fused = g16_gate_up_swiglu((const bf16 *)n2.p, n2.ld, Wb(s.t[6]), D, a.gu, 2 * F,
+                                       a.gatedb, F, T, F, D, cur);
+        if (fused != hipErrorNotSupported) {
+            VKH_HIP(fused);
+        } else {
+            VKH_TRY(linear_fwd_lora(l, {4, 5}, n2, s.t[6], a.gu, 2 * F, 2 * F, D, nullptr, 0));
+            VKH_HIP(swiglu_forward(a.gu, 2 * F, a.gu + F, 2 * F,
+                                   b16() ? (void *)a.gatedb : (void *)a.gated, F, odt, T, F, cur));
+        }
         const Mat gt = m_gated(a);
         if (!need_y) return lora_fwd_group(l, {6}, gt, nullptr, 0, false);
         // y = mid + gated W_down^T (+ LoRA)

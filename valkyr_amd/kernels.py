@@ -98,6 +98,11 @@ def matmul_nt_bf16(x, w, y, M, N, K, stream=None):
     check(lib().vkh_matmul_nt_bf16(_p(x), _p(w), _p(y), M, N, K, _s(stream)))
 
 
+def gate_up_swiglu_bf16(x, w_gu, gu, gated, M, F, K, stream=None):
+    """gu[M, 2F] = x w_gu^T and gated[M, F] = bf16 SwiGLU of its halves (bf16 operands)."""
+    check(lib().vkh_gate_up_swiglu_bf16(_p(x), _p(w_gu), _p(gu), _p(gated), M, F, K, _s(stream)))
+
+
 def linear_backward_dx_bf16(dy, w, dx, M, N, K, stream=None):
     """dx[M,K] = dy[M,N] w[N,K] on bf16 operands."""
     check(lib().vkh_linear_backward_dx_bf16(_p(dy), _p(w), _p(dx), M, N, K, _s(stream)))
