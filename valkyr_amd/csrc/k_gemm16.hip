@@ -316,7 +316,10 @@ hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, lo
 // gu[M, 2F] = x[M, K] w_gu[2F, K]^T and gated[M, F] = bf16(swiglu1(gu[:, f], gu[:, F + f])) in
 // one launch, where the plain plan for the [M, 2F] product is the 8-wave 128 x 128 tile
 // (each block then takes 64 gate and the matching 64 up features); hipErrorNotSupported
-// (nothing launched) elsewhere, and the caller runs g16_nt + swiglu_forward.
+// (nothing launched) elsewhere, and the caller runs g16_nt + swiglu_forward.  (The same
+// epilogue on the 256 x 256 tile, 128 + 128 features per block and a 128 KB hand-over, was
+// parity-green but measured config 4 at 59.93-60.07 against 59.68-59.73 ms and config 5
+// unchanged, 584.1-584.6 against 584.0-585.0 ms.)
 hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, float *gu,
                               long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st) {
     if (M <= 0 || F <= 0 || F % 64) return hipErrorNotSupported;
