@@ -17,6 +17,7 @@
 
 #include "gemm16.hpp"
 #include "ops.hpp"
+#include "qkv8.hpp"
 
 namespace vkh {
 
@@ -331,6 +332,121 @@ hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, 
     const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (F / (T128w8::BN / 2)));
     hipLaunchKernelGGL((gemm16_swiglu_kernel<T128w8>), dim3(tiles), dim3(T128w8::NT), 0, st, a, b, M,
                        F, K, gu, ldgu, gated, ldg, tile_group_rows<Lay::K, Lay::K>());
+    return hipGetLastError();
+}
+
+namespace {
+
+struct QkvEpi {
+    QkvLayout L;
+    const float *wq, *wk;  // q / k RMSNorm gains (qk_norm)
+    bf16 *out;             // the attention operand [rows, (Hq + 2 Hkv) hd]
+    long ld_out;
+    const float2 *tab;     // RoPE cos / sin [seq_len][rotary_dim / 2]
+};
+
+// The q|k|v projection with the Q/K-RMSNorm + RoPE forward in its epilogue (head_dim
+// 128, so a 128 x 128 tile is 128 rows of one head): the tile stores its fp32
+// projection (the backward's pre-norm values), stages it in the idle slab buffers (16-float
+// group u of row r at u ^ ((r >> 2) & 3), so the four row groups of a store land on
+// different banks), and its waves then run the standalone pass's item code
+// (qkv_fwd_item8, 16 lanes per row) on it and write the bf16 attention operand.
+template <class Cfg>
+__global__ __launch_bounds__(Cfg::NT, 1) void gemm16_qkv_kernel(Op16 a, Op16 b, GemmShape s, float *C,
+                                                               long ldc, QkvEpi q, int tgrp) {
+    constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT, NW = NT / 64;
+    constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
+    constexpr int TM = WM / 16, TN = WN / 16;
+    constexpr int LPH = 16, G = 64 / LPH;  // lanes per row, rows per wave
+    static_assert(BN == 128 && BM * BN * 4 <= Cfg::LDS && BM % (NW * G) == 0, "one head per tile");
+    __shared__ __attribute__((aligned(16))) char smem[Cfg::LDS];
+    const int tid = threadIdx.x, lane = tid % 64, wave = tid / 64;
+    const int wm = wave / Cfg::WGN, wn = wave % Cfg::WGN;
+    const int nbm = (s.M + BM - 1) / BM, nbn = s.N / BN;
+    const int nb = nbm * nbn;
+    int bid = blockIdx.x;
+    if (nb % 8 == 0) bid = (bid % 8) * (nb / 8) + bid / 8;
+    int bm, bn;
+    tile_rc(bid, nbm, nbn, tgrp, bm, bn);
+    const int m0 = bm * BM, n0 = bn * BN;
+    f32x4 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
+    gemm16_tile_dma<Cfg, Lay::K, Lay::K, TM, TN>(a, b, m0, n0, s.M, s.N, 0, (s.K + 63) / 64, s.K, acc,
+                                                 smem);
+    float *lt = reinterpret_cast<float *>(smem);  // the slab loop ended with a barrier
+    const int g = lane / 16, c = lane % 16;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int tr = wm * WM + 16 * i + 4 * g + r, tc = wn * WN + 16 * j + c;
+                if (m0 + tr < s.M) C[(long)(m0 + tr) * ldc + n0 + tc] = acc[i][j][r];
+                lt[tr * BN + (tc ^ (((tr >> 2) & 3) << 4))] = acc[i][j][r];
+            }
+    lds_barrier();
+    const QkvLayout &L = q.L;
+    const int h = bn, half = L.rotary_dim / 2, j8 = lane % LPH;
+    const Rope8 rp = rope8(j8, half);
+    const bool is_q = h < L.n_q_heads, qkh = h < L.n_q_heads + L.n_kv_heads;
+    float gq[8], gk[8];
+    if (L.qk_norm) {
+        ld8(q.wq + 8 * j8, gq);
+        ld8(q.wk + 8 * j8, gk);
+    }
+    for (int tr = wave * G + lane / LPH; tr < BM; tr += NW * G) {
+        const int t = m0 + tr;
+        const bool valid = t < s.M, qk = valid && qkh;
+        float y[8];
+        ld8(lt + tr * BN + ((8 * j8) ^ (((tr >> 2) & 3) << 4)), y);
+        float2 cs[8];
+        if (qk && rp.rot_lane) {
+            const float4 *tp =
+                reinterpret_cast<const float4 *>(q.tab + (long)(t % L.seq_len) * half + rp.col);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float4 v = tp[i];
+                cs[2 * i] = make_float2(v.x, v.y);
+                cs[2 * i + 1] = make_float2(v.z, v.w);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 8; ++i) cs[i] = make_float2(1.f, 0.f);
+        }
+        qkv_fwd_item8<LPH>(L, y, cs, qk, is_q, gq, gk, rp, lane, half);
+        if (valid) st8(q.out + (long)t * q.ld_out + h * BN + 8 * j8, y);
+    }
+}
+
+}  // namespace
+
+// y[M, N] = x w^T (the fp32 q|k|v projection) and the bf16 attention operand out = RoPE(
+// Q/K-RMSNorm(y)) (qkv_prepare_forward's values, bit for bit) in one launch, where head_dim
+// is 128 and the product's plain plan is the 8-wave 128 x 128 tile; hipErrorNotSupported
+// (nothing launched) elsewhere.
+hipError_t g16_qkv_norm_rope(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy,
+                             int M, int N, int K, const QkvLayout &L, const float *wq,
+                             const float *wk, bf16 *out, long ld_out, const float2 *tab,
+                             hipStream_t st) {
+    if (M <= 0 || L.head_dim != 128 || L.n_rows != M || L.seq_len <= 0 || L.rotary_dim % 16 ||
+        L.rotary_dim > 128 || N != (L.n_q_heads + 2 * L.n_kv_heads) * 128)
+        return hipErrorNotSupported;
+    const GemmShape s{M, N, K};
+    const Plan p = plan(s, 0);
+    if (p.tile != Pick::T128w8 || p.splits != 1) return hipErrorNotSupported;
+    if (((uintptr_t)out & 15u) || ld_out % 8 || (L.qk_norm && (((uintptr_t)wq | (uintptr_t)wk) & 15u)) ||
+        (L.rotary_dim && ((uintptr_t)tab & 15u)))
+        return hipErrorNotSupported;
+    Op16 a, b;
+    if (!make_op(x, ldx, M, K, a) || !make_op(w, ldw, N, K, b)) return hipErrorNotSupported;
+    const int g = p.column_order ? 0 : tile_group_rows<Lay::K, Lay::K>();
+    const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (N / T128w8::BN));
+    hipLaunchKernelGGL((gemm16_qkv_kernel<T128w8>), dim3(tiles), dim3(T128w8::NT), 0, st, a, b, s, y,
+                       ldy, QkvEpi{L, wq, wk, out, ld_out, tab}, g);
     return hipGetLastError();
 }
 

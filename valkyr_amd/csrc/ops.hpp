@@ -217,6 +217,14 @@ struct QkvLayout {
 hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv,
                                const float *wq, const float *wk, void *out, long ld_out,
                                DType out_dt, const float2 *rope_tab, hipStream_t st);
+// The q|k|v projection y = x w^T (bf16 operands, fp32 y) with qkv_prepare_forward's
+// bf16 output fused into the GEMM's epilogue (the same values bit for bit);
+// hipErrorNotSupported, launching nothing, unless head_dim is 128 and the product's
+// plan is the 8-wave 128 x 128 tile.
+hipError_t g16_qkv_norm_rope(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy,
+                             int M, int N, int K, const QkvLayout &L, const float *wq,
+                             const float *wk, bf16 *out, long ld_out, const float2 *tab,
+                             hipStream_t st);
 // Backward of the above on the fused d_qkv buffer: d(post-rope) ->
 // d(pre-norm) for the q/k columns, in place, or (outb non-null) written with
 // the v columns to the bf16 copy outb; dwq/dwk reduced gains (overwrite).

@@ -989,11 +989,22 @@ struct vkh_runner {
         VKH_HIP(rmsnorm_forward(x_in, W(s.t[0]), b16() ? (void *)a.n1b : (void *)a.n1, odt, T, D,
                                 cfg.rms_eps, 0, cur));
         const Mat n1 = m_n1(a);
-        VKH_TRY(linear_fwd_lora(l, {0, 1, 2}, n1, s.t[1], a.qkv, qkvd, qkvd, D, nullptr, 0));
         const QkvLayout ql = qkv_layout();
-        VKH_HIP(qkv_prepare_forward(ql, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
-                                    cfg.qk_norm ? W(s.t[10]) : nullptr, a.qkv_attn, qkvd, adt,
-                                    rope_tab, cur));
+        // the Q/K-norm + RoPE in the q|k|v GEMM's epilogue where the fused form applies
+        hipError_t fq = hipErrorNotSupported;
+        if (b16() && adt == DType::BF16 && !proj_lora(0) && !proj_lora(1) && !proj_lora(2))
+            fq = g16_qkv_norm_rope((const bf16 *)n1.p, n1.ld, Wb(s.t[1]), D, a.qkv, qkvd, T, qkvd, D,
+                                   ql, cfg.qk_norm ? W(s.t[9]) : nullptr,
+                                   cfg.qk_norm ? W(s.t[10]) : nullptr, (bf16 *)a.qkv_attn, qkvd,
+                                   rope_tab, cur);
+        if (fq != hipErrorNotSupported) {
+            VKH_HIP(fq);
+        } else {
+            VKH_TRY(linear_fwd_lora(l, {0, 1, 2}, n1, s.t[1], a.qkv, qkvd, qkvd, D, nullptr, 0));
+            VKH_HIP(qkv_prepare_forward(ql, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
+                                        cfg.qk_norm ? W(s.t[10]) : nullptr, a.qkv_attn, qkvd, adt,
+                                        rope_tab, cur));
+        }
         const AttnShape as = attn_shape();
         const size_t es = adt == DType::BF16 ? 2 : 4;
         const char *qa = (const char *)a.qkv_attn;
