@@ -690,6 +690,18 @@ vkh_status vkh_qk_rope_forward(const vkh_rope_params *p, const float *q_in, floa
                                const float *k_in, float *k_out, vkh_stream stream);
 vkh_status vkh_qk_rope_backward(const vkh_rope_params *p, const float *dq_out, float *dq_in,
                                 const float *dk_out, float *dk_in, vkh_stream stream);
+/* The bf16 step's q|k|v projection and attention operand: y[n_pos, (Hq + 2 Hkv) hd]
+ * = x[n_pos, K] w^T (bf16 operands, fp32 y: the backward's pre-norm values) and
+ * out = bf16 of the q and k heads Q/K-RMSNorm'd (qk_norm, gains wq / wk, eps) and
+ * rotated (p), the v heads as they are.  No single counterpart in the reference:
+ * it is matmul_nt_v2.comp for w_q, w_k and w_v, rmsnorm.comp over each q and k
+ * head, and qk_rope_partial_batched.comp (transformer.zig's forward order),
+ * run as one launch with the norm and rotation in the GEMM's epilogue where
+ * head_dim is 128 and the tile plan allows (fused != 0), as the two passes
+ * otherwise (fused = 0 forces them); the same bits either way. */
+vkh_status vkh_qkv_project_bf16(const vkh_rope_params *p, uint32_t K, float eps, int qk_norm,
+                                const void *x, const void *w, const float *wq, const float *wk,
+                                float *y, void *out, int fused, vkh_stream stream);
 /* shaders/embed_lookup_batched.comp (EmbedLookupBatchedPush {dim, n_pos, scale}) */
 vkh_status vkh_embed_lookup(const float *embed, const uint32_t *ids, float *out, uint32_t n_pos,
                             uint32_t dim, float scale, vkh_stream stream);

@@ -341,6 +341,42 @@ def test_gate_up_swiglu_matches_two_passes(shape):
     assert np.array_equal(gated, f32_to_bf16_bits(host(out)))
 
 
+# (rows, q heads, kv heads, K, seq_len, rotary_dim, qk_norm): config 3's layer (the fused
+# launch), ragged rows, a partial and no rotation, no Q/K-norm, GQA 4:1, and a shape whose
+# plan is not the 128 x 128 tile (the two passes either way)
+QKV_PROJ_CASES = [(2048, 16, 8, 1024, 512, 128, 1), (2000, 16, 8, 1000, 500, 128, 1),
+                  (2048, 16, 8, 1024, 512, 64, 1), (2048, 16, 8, 1024, 512, 0, 0),
+                  (4096, 16, 4, 512, 2048, 128, 1), (256, 4, 2, 256, 128, 128, 1)]
+
+
+@pytest.mark.parametrize("case", QKV_PROJ_CASES)
+def test_qkv_project_fused_matches_two_passes(case):
+    """vkh_qkv_project_bf16 with the Q/K-RMSNorm + RoPE in the q|k|v GEMM's
+    epilogue against its two passes (the product, then the standalone
+    norm-and-rotation pass over it) bit for bit: the fp32 projection and the
+    bf16 attention operand; the projection also against float64 products."""
+    from valkyr_amd import kernels as K
+
+    M, Hq, Hkv, Kd, S, rot, qkn = case
+    hd = 128
+    N = (Hq + 2 * Hkv) * hd
+    note(f"qkv project rows={M} heads={Hq}/{Hkv} K={Kd} seq={S} rot={rot} qk_norm={qkn}")
+    bx, x = bf16_dev(O.normal(M * Kd, 91))
+    bW, W = bf16_dev(O.normal(N * Kd, 92, 0.05))
+    wq, wk = dev(O.uniform(hd, 93, 0.5, 1.5)), dev(O.uniform(hd, 94, 0.5, 1.5))
+    p = K.rope_params(M, Hq, Hkv, hd, rot, 1e6, S)
+    outs = []
+    for fused in (True, False):
+        by, bo = zeros(M * N), zeros(M * N, np.uint16)
+        K.qkv_project_bf16(p, Kd, 1e-6, qkn, bx, bW, wq, wk, by, bo, fused=fused)
+        outs.append((host(by), host(bo, dtype=np.uint16)))
+    (y1, o1), (y0, o0) = outs
+    assert np.array_equal(y1, y0)
+    assert np.array_equal(o1, o0)
+    y64 = x.astype(np.float64).reshape(M, Kd) @ W.astype(np.float64).reshape(N, Kd).T
+    assert rel_l2(y64.ravel(), y1) < 1e-5
+
+
 # (M, N, K, r): the rank-r kernels' shapes (r a multiple of 4 up to 64, N and
 # K multiples of 64; ragged M; config 4's k/v projection width at a smaller
 # M) and a shape outside them that takes the general GEMMs.

@@ -760,6 +760,34 @@ vkh_status vkh_qk_rope_backward(const vkh_rope_params *p, const float *dq_out, f
     return rope_common(p, dq_out, dq_in, dk_out, dk_in, true, stream);
 }
 
+vkh_status vkh_qkv_project_bf16(const vkh_rope_params *p, uint32_t K, float eps, int qk_norm,
+                                const void *x, const void *w, const float *wq, const float *wk,
+                                float *y, void *out, int fused, vkh_stream stream) {
+    CHECK_ARG(p && x && w && y && out, "null pointer");
+    CHECK_ARG(!qk_norm || (wq && wk), "null norm gains");
+    CHECK_ARG(p->rotary_dim <= p->head_dim && (p->rotary_dim % 2) == 0, "rotary_dim");
+    QkvLayout L;
+    L.n_rows = (int)p->n_pos; L.n_q_heads = (int)p->n_q_heads; L.n_kv_heads = (int)p->n_kv_heads;
+    L.head_dim = (int)p->head_dim; L.seq_len = p->seq_len ? (int)p->seq_len : (int)p->n_pos;
+    L.rotary_dim = (int)p->rotary_dim; L.theta = p->theta_base; L.eps = eps; L.qk_norm = qk_norm ? 1 : 0;
+    const float2 *tab = nullptr;
+    VKH_TRY(rope_table_cached(L.seq_len, L.rotary_dim, L.theta, &tab));
+    const uint32_t N = (p->n_q_heads + 2 * p->n_kv_heads) * p->head_dim;
+    hipStream_t st = S(stream);
+    if (fused) {
+        const hipError_t e = g16_qkv_norm_rope((const bf16 *)x, K, (const bf16 *)w, K, y, N, L.n_rows,
+                                               (int)N, (int)K, L, wq, wk, (bf16 *)out, N, tab, st);
+        if (e != hipErrorNotSupported) {
+            VKH_HIP(e);
+            return VKH_OK;
+        }
+    }
+    const vkh_status r = vkh_matmul_nt_bf16(x, w, y, p->n_pos, N, K, stream);
+    if (r != VKH_OK) return r;
+    VKH_HIP(qkv_prepare_forward(L, y, N, wq, wk, out, N, DType::BF16, tab, st));
+    return VKH_OK;
+}
+
 vkh_status vkh_embed_lookup(const float *embed, const uint32_t *ids, float *out, uint32_t n_pos,
                             uint32_t dim, float scale, vkh_stream stream) {
     CHECK_ARG(embed && ids && out, "null pointer");
