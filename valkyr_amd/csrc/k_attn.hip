@@ -1823,7 +1823,10 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
 }
 
 // ── forward v3 (head_dim 128): DMA-staged K / V tiles ────────────────────
-// One (q tile of 128 rows, head, sequence) per block, 4 waves x 32 queries,
+// One (q tile of 64 QS rows, head, sequence) per block, 4 waves x 16 QS queries
+// (QS = 1 where 128-query blocks would be at most one per CU: config 3's 256
+// become 512 blocks of 64, two per CU, and the forward 23.8 -> ~16 us per
+// layer; the step 19.06-19.10 -> 18.86-18.89 ms),
 // Q fragments in registers.  64-key K and V tiles arrive by DMA into the
 // swizzled LDS layout of the backward kernel (two buffers, the next tile in
 // flight while the current one computes, one barrier per tile); K feeds the
@@ -1831,12 +1834,13 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
 // tile through the transposing LDS read (no transposed staging copy).
 // Causal q tiles go heaviest first (a zigzag order, zigzag in common.hpp,
 // measured 77.6 against 78.9 us at config 4's 512-block grid: within noise).
+template <int QS>
 __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, long ldq,
                                                      const bf16 *k, long ldk, const bf16 *v,
                                                      long ldv, float *o, long ldo, float *lse,
                                                      bf16 *ob, long ldob) {
     using namespace dkv3;
-    constexpr int FBM = 128, FBN = 64, KT = FBN * HD * 2;
+    constexpr int FBM = 64 * QS, FBN = 64, KT = FBN * HD * 2;
     __shared__ __attribute__((aligned(16))) char Ks[2][KT];
     __shared__ __attribute__((aligned(16))) char Vs[2][KT];
 
@@ -1847,24 +1851,29 @@ __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, 
     const int kvh = h / (s.n_heads / s.n_kv_heads);
     const int tid = threadIdx.x, lane = tid % 64, g = lane / 16, c16 = lane % 16;
     const int wave = __builtin_amdgcn_readfirstlane(tid / 64);
-    const int q0 = qt * FBM, qw0 = q0 + wave * 32;
+    const int q0 = qt * FBM, qw0 = q0 + wave * 16 * QS;
     const int off = s.n_kv - s.n_q;
     const bf16 *qb = q + (long)b * s.n_q * ldq + h * HD;
     const float c2 = s.inv_sqrt_dim * LOG2E;
 
-    bf16x8 qf[2][DS];
+    bf16x8 qf[QS][DS];
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
         const int qr = qw0 + 16 * qs + c16;
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds)
             qf[qs][ds] = qr < s.n_q ? ld_frag(qb + (long)qr * ldq + 32 * ds + 8 * g) : bf16x8{};
     }
     wait_vm0();  // Q fragments are in registers before any DMA is queued
-    f32x4 oacc[DSUB][2];
+    f32x4 oacc[DSUB][QS];
+    float m[QS], l[QS];
 #pragma unroll
-    for (int i = 0; i < DSUB; ++i) oacc[i][0] = oacc[i][1] = f32x4{0, 0, 0, 0};
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.f, 0.f};
+    for (int qs = 0; qs < QS; ++qs) {
+        m[qs] = -INFINITY;
+        l[qs] = 0.f;
+#pragma unroll
+        for (int i = 0; i < DSUB; ++i) oacc[i][qs] = f32x4{0, 0, 0, 0};
+    }
 
     int kend = s.n_kv;
     if (s.causal) kend = min(s.n_kv, q0 + FBM + off);
@@ -1886,7 +1895,7 @@ __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, 
         }
     };
     if (nkt > 0) dma(0, 0);
-    const int wave_last_q = min(qw0 + 31, s.n_q - 1);
+    const int wave_last_q = min(qw0 + 16 * QS - 1, s.n_q - 1);
     for (int kt = 0; kt < nkt; ++kt) {
         const int k0 = kt * FBN, buf = kt & 1;
         wait_vm0();
@@ -1896,21 +1905,23 @@ __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, 
         if (s.causal && k0 > wave_last_q + off) continue;
         const char *Kb = Ks[buf], *Vb = Vs[buf];
 
-        f32x4 st[4][2];
+        f32x4 st[4][QS];
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) st[ks][0] = st[ks][1] = f32x4{0, 0, 0, 0};
+        for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+            for (int qs = 0; qs < QS; ++qs) st[ks][qs] = f32x4{0, 0, 0, 0};
 #pragma unroll
         for (int ds = 0; ds < DS; ++ds)
 #pragma unroll
             for (int ks = 0; ks < 4; ++ks) {
                 const bf16x8 kf = frag_row(Kb, 16 * ks + c16, 32 * ds + 8 * g);
-                st[ks][0] = mfma16x16x32(kf, qf[0][ds], st[ks][0]);
-                st[ks][1] = mfma16x16x32(kf, qf[1][ds], st[ks][1]);
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs) st[ks][qs] = mfma16x16x32(kf, qf[qs][ds], st[ks][qs]);
             }
         const bool edge = (s.causal && k0 + FBN - 1 > qw0 + off) || k0 + FBN > s.n_kv;
-        bf16x8 pf[2][2];
+        bf16x8 pf[QS][2];
 #pragma unroll
-        for (int qs = 0; qs < 2; ++qs) {
+        for (int qs = 0; qs < QS; ++qs) {
             const int qa = qw0 + 16 * qs + c16;
             float mt = -INFINITY;
 #pragma unroll
@@ -1953,12 +1964,12 @@ __global__ __launch_bounds__(256, 2) void fa_fwd3_k(AttnShape s, const bf16 *q, 
 #pragma unroll
             for (int i = 0; i < DSUB; ++i) {
                 const bf16x8 vf = frag_t(Vb, 16 * i, 32 * kst, g, c16);
-                oacc[i][0] = mfma16x16x32(vf, pf[0][kst], oacc[i][0]);
-                oacc[i][1] = mfma16x16x32(vf, pf[1][kst], oacc[i][1]);
+#pragma unroll
+                for (int qs = 0; qs < QS; ++qs) oacc[i][qs] = mfma16x16x32(vf, pf[qs][kst], oacc[i][qs]);
             }
     }
 #pragma unroll
-    for (int qs = 0; qs < 2; ++qs) {
+    for (int qs = 0; qs < QS; ++qs) {
         const int qa = qw0 + 16 * qs + c16;
         if (qa >= s.n_q) continue;
         const float inv = l[qs] > 0.f ? 1.0f / l[qs] : 0.f;
@@ -2177,8 +2188,15 @@ hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k
         dim3 grid(s.n_heads * s.n_batch, (s.n_q + 127) / 128);
         const bool dma_ok = ((uintptr_t)k & 15) == 0 && ((uintptr_t)v & 15) == 0 && ldk % 8 == 0 &&
                             ldv % 8 == 0 && (long)s.n_kv * std::max(ldk, ldv) * 2 < (1L << 31);
-        if (s.head_dim == 128 && dma_ok)
-            hipLaunchKernelGGL(fa_fwd3_k, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
+        // grids of 128-query blocks that leave the CUs one block each or fewer
+        // (short sequences: config 3's 256) take 64-query blocks, two per CU
+        const bool q64 = (long)grid.x * grid.y <= cu_count();
+        if (s.head_dim == 128 && dma_ok && q64)
+            hipLaunchKernelGGL(fa_fwd3_k<1>, dim3(grid.x, (s.n_q + 63) / 64), dim3(NT), 0, st, s,
+                               (const bf16 *)q, ldq, (const bf16 *)k, ldk, (const bf16 *)v, ldv, o,
+                               ldo, lse, ob, ldob);
+        else if (s.head_dim == 128 && dma_ok)
+            hipLaunchKernelGGL(fa_fwd3_k<2>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
                                (const bf16 *)k, ldk, (const bf16 *)v, ldv, o, ldo, lse, ob, ldob);
         else if (s.head_dim == 128)
             hipLaunchKernelGGL(fa_fwd_bf16_k<128>, grid, dim3(NT), 0, st, s, (const bf16 *)q, ldq,
