@@ -1825,8 +1825,8 @@ __global__ __launch_bounds__(NWV * 64, 1) void fa_bwd_dq4_k(AttnShape s, AttnPtr
 // ── forward v3 (head_dim 128): DMA-staged K / V tiles ────────────────────
 // One (q tile of 64 QS rows, head, sequence) per block, 4 waves x 16 QS queries
 // (QS = 1 where 128-query blocks would be at most one per CU: config 3's 256
-// become 512 blocks of 64, two per CU, and the forward 23.8 -> ~16 us per
-// layer; the step 19.06-19.10 -> 18.86-18.89 ms),
+// become 512 blocks of 64, two per CU: the step 19.06-19.10 -> 18.86-18.89
+// ms),
 // Q fragments in registers.  64-key K and V tiles arrive by DMA into the
 // swizzled LDS layout of the backward kernel (two buffers, the next tile in
 // flight while the current one computes, one barrier per tile); K feeds the
