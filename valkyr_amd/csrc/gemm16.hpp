@@ -434,11 +434,11 @@ hipError_t launch_gemm16_ks2(const Op16 &a, const Op16 &b, const GemmShape &s, c
 // pre-activations (gu[:, f] and gu[:, F + f], the backward's inputs); the up
 // waves hand their accumulators to the gate waves of the same rows and
 // features through the idle slab buffers, which write gated = swiglu1(gate,
-// up) in bf16.  One pass instead of the GEMM plus a SwiGLU pass that reads the
-// whole gu back.
-template <class Cfg>
+// up) in TO (bf16; fp32 in the fp32 slab mode, F32).  One pass instead of the
+// GEMM plus a SwiGLU pass that reads the whole gu back.
+template <class Cfg, bool F32 = false, typename TO = bf16>
 __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_swiglu_kernel(Op16 a, Op16 b, int M, int F, int K,
-                                                                  float *gu, long ldgu, bf16 *gated,
+                                                                  float *gu, long ldgu, TO *gated,
                                                                   long ldg, int tgrp) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, WGN = Cfg::WGN;
     constexpr int WM = BM / Cfg::WGM, WN = BN / WGN;
@@ -460,8 +460,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_swiglu_kernel(Op16 a, Op16 
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    gemm16_tile_dma<Cfg, Lay::K, Lay::K, TM, TN, false, true>(a, b, m0, f0, M, 2 * F, 0,
-                                                              (K + 63) / 64, K, acc, smem, -1, F);
+    constexpr int KW = F32 ? 32 : 64;  // k per slab
+    gemm16_tile_dma<Cfg, Lay::K, Lay::K, TM, TN, F32, true>(a, b, m0, f0, M, 2 * F, 0,
+                                                            (K + KW - 1) / KW, K, acc, smem, -1, F);
     const bool up = wn >= WGN / 2;
     const int ws = wm * (WGN / 2) + (up ? wn - WGN / 2 : wn);  // gate / up wave pair
     const int fw = f0 + (ws % (WGN / 2)) * WN;                 // feature of the wave's column 0
@@ -493,7 +494,7 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_swiglu_kernel(Op16 a, Op16 
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int row = m0 + wm * WM + 16 * i + 4 * g + r;
-                if (row < M) gated[(long)row * ldg + fw + 16 * j + c] = (bf16)swiglu1(acc[i][j][r], u[r]);
+                if (row < M) gated[(long)row * ldg + fw + 16 * j + c] = (TO)swiglu1(acc[i][j][r], u[r]);
             }
         }
 }

@@ -337,10 +337,11 @@ hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, 
 
 namespace {
 
+template <typename TO>
 struct QkvEpi {
     QkvLayout L;
     const float *wq, *wk;  // q / k RMSNorm gains (qk_norm)
-    bf16 *out;             // the attention operand [rows, (Hq + 2 Hkv) hd]
+    TO *out;               // the attention operand [rows, (Hq + 2 Hkv) hd]
     long ld_out;
     const float2 *tab;     // RoPE cos / sin [seq_len][rotary_dim / 2]
 };
@@ -351,9 +352,9 @@ struct QkvEpi {
 // group u of row r at u ^ ((r >> 2) & 3), so the four row groups of a store land on
 // different banks), and its waves then run the standalone pass's item code
 // (qkv_fwd_item8, 16 lanes per row) on it and write the bf16 attention operand.
-template <class Cfg>
+template <class Cfg, bool F32 = false, typename TO = bf16>
 __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_qkv_kernel(Op16 a, Op16 b, GemmShape s, float *C,
-                                                               long ldc, QkvEpi q, int tgrp) {
+                                                               long ldc, QkvEpi<TO> q, int tgrp) {
     constexpr int BM = Cfg::BM, BN = Cfg::BN, NT = Cfg::NT, NW = NT / 64;
     constexpr int WM = BM / Cfg::WGM, WN = BN / Cfg::WGN;
     constexpr int TM = WM / 16, TN = WN / 16;
@@ -374,8 +375,9 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_qkv_kernel(Op16 a, Op16 b, 
     for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j) acc[i][j] = f32x4{0.f, 0.f, 0.f, 0.f};
-    gemm16_tile_dma<Cfg, Lay::K, Lay::K, TM, TN>(a, b, m0, n0, s.M, s.N, 0, (s.K + 63) / 64, s.K, acc,
-                                                 smem);
+    constexpr int KW = F32 ? 32 : 64;  // k per slab
+    gemm16_tile_dma<Cfg, Lay::K, Lay::K, TM, TN, F32>(a, b, m0, n0, s.M, s.N, 0, (s.K + KW - 1) / KW,
+                                                      s.K, acc, smem);
     float *lt = reinterpret_cast<float *>(smem);  // the slab loop ended with a barrier
     const int g = lane / 16, c = lane % 16;
 #pragma unroll
@@ -446,7 +448,45 @@ hipError_t g16_qkv_norm_rope(const bf16 *x, long ldx, const bf16 *w, long ldw, f
     const int g = p.column_order ? 0 : tile_group_rows<Lay::K, Lay::K>();
     const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (N / T128w8::BN));
     hipLaunchKernelGGL((gemm16_qkv_kernel<T128w8>), dim3(tiles), dim3(T128w8::NT), 0, st, a, b, s, y,
-                       ldy, QkvEpi{L, wq, wk, out, ld_out, tab}, g);
+                       ldy, QkvEpi<bf16>{L, wq, wk, out, ld_out, tab}, g);
+    return hipGetLastError();
+}
+
+// The fp32 forms of the two fused projections (fp32 operands on the DMA-staged kernels'
+// fp32 slab mode, fp32 outputs), where the fp32 plan is the 8-wave 128 x 128 tile.
+hipError_t g32_qkv_norm_rope(const float *x, long ldx, const float *w, long ldw, float *y, long ldy,
+                             int M, int N, int K, const QkvLayout &L, const float *wq,
+                             const float *wk, float *out, long ld_out, const float2 *tab,
+                             hipStream_t st) {
+    if (M <= 0 || L.head_dim != 128 || L.n_rows != M || L.seq_len <= 0 || L.rotary_dim % 16 ||
+        L.rotary_dim > 128 || N != (L.n_q_heads + 2 * L.n_kv_heads) * 128)
+        return hipErrorNotSupported;
+    const GemmShape s{M, N, K};
+    const Plan p = plan32(s, 0);
+    if (p.tile != Pick::T128w8 || p.splits != 1) return hipErrorNotSupported;
+    if (((uintptr_t)out & 15u) || ld_out % 4 || (L.qk_norm && (((uintptr_t)wq | (uintptr_t)wk) & 15u)) ||
+        (L.rotary_dim && ((uintptr_t)tab & 15u)))
+        return hipErrorNotSupported;
+    Op16 a, b;
+    if (!make_op32(x, ldx, M, K, a) || !make_op32(w, ldw, N, K, b)) return hipErrorNotSupported;
+    const int g = p.column_order ? 0 : tile_group_rows<Lay::K, Lay::K>();
+    const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (N / T128w8::BN));
+    hipLaunchKernelGGL((gemm16_qkv_kernel<T128w8, true, float>), dim3(tiles), dim3(T128w8::NT), 0, st,
+                       a, b, s, y, ldy, QkvEpi<float>{L, wq, wk, out, ld_out, tab}, g);
+    return hipGetLastError();
+}
+
+hipError_t g32_gate_up_swiglu(const float *x, long ldx, const float *w, long ldw, float *gu,
+                              long ldgu, float *gated, long ldg, int M, int F, int K, hipStream_t st) {
+    if (M <= 0 || F <= 0 || F % 64) return hipErrorNotSupported;
+    const GemmShape s{M, 2 * F, K};
+    const Plan p = plan32(s, 0);
+    if (p.tile != Pick::T128w8 || p.splits != 1) return hipErrorNotSupported;
+    Op16 a, b;
+    if (!make_op32(x, ldx, M, K, a) || !make_op32(w, ldw, 2L * F, K, b)) return hipErrorNotSupported;
+    const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (F / (T128w8::BN / 2)));
+    hipLaunchKernelGGL((gemm16_swiglu_kernel<T128w8, true, float>), dim3(tiles), dim3(T128w8::NT), 0,
+                       st, a, b, M, F, K, gu, ldgu, gated, ldg, p.column_order ? 0 : tile_group_rows<Lay::K, Lay::K>());
     return hipGetLastError();
 }
 

@@ -225,6 +225,13 @@ hipError_t g16_qkv_norm_rope(const bf16 *x, long ldx, const bf16 *w, long ldw, f
                              int M, int N, int K, const QkvLayout &L, const float *wq,
                              const float *wk, bf16 *out, long ld_out, const float2 *tab,
                              hipStream_t st);
+// fp32 forms (fp32 operands and outputs), where the fp32 plan is the 8-wave 128 x 128 tile.
+hipError_t g32_qkv_norm_rope(const float *x, long ldx, const float *w, long ldw, float *y, long ldy,
+                             int M, int N, int K, const QkvLayout &L, const float *wq,
+                             const float *wk, float *out, long ld_out, const float2 *tab,
+                             hipStream_t st);
+hipError_t g32_gate_up_swiglu(const float *x, long ldx, const float *w, long ldw, float *gu,
+                              long ldgu, float *gated, long ldg, int M, int F, int K, hipStream_t st);
 // Backward of the above on the fused d_qkv buffer: d(post-rope) ->
 // d(pre-norm) for the q/k columns, in place, or (outb non-null) written with
 // the v columns to the bf16 copy outb; dwq/dwk reduced gains (overwrite).

@@ -997,6 +997,11 @@ struct vkh_runner {
                                    ql, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                    cfg.qk_norm ? W(s.t[10]) : nullptr, (bf16 *)a.qkv_attn, qkvd,
                                    rope_tab, cur);
+        else if (!b16() && adt == DType::F32 && !lora)
+            fq = g32_qkv_norm_rope((const float *)n1.p, n1.ld, W(s.t[1]), D, a.qkv, qkvd, T, qkvd, D,
+                                   ql, cfg.qk_norm ? W(s.t[9]) : nullptr,
+                                   cfg.qk_norm ? W(s.t[10]) : nullptr, (float *)a.qkv_attn, qkvd,
+                                   rope_tab, cur);
         if (fq != hipErrorNotSupported) {
             VKH_HIP(fq);
         } else {
@@ -1027,6 +1032,9 @@ struct vkh_runner {
         if (b16() && !proj_lora(4) && !proj_lora(5))
             fused = g16_gate_up_swiglu((const bf16 *)n2.p, n2.ld, Wb(s.t[6]), D, a.gu, 2 * F,
                                        a.gatedb, F, T, F, D, cur);
+        else if (!b16() && !lora)
+            fused = g32_gate_up_swiglu((const float *)n2.p, n2.ld, W(s.t[6]), D, a.gu, 2 * F, a.gated,
+                                       F, T, F, D, cur);
         if (fused != hipErrorNotSupported) {
             VKH_HIP(fused);
         } else {
