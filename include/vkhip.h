@@ -576,6 +576,10 @@ vkh_status vkh_matmul_nt_bf16(const void *x, const void *w, float *y, uint32_t M
  * bits either way. */
 vkh_status vkh_gate_up_swiglu_bf16(const void *x, const void *w_gu, float *gu, void *gated,
                                    uint32_t M, uint32_t F, uint32_t K, vkh_stream stream);
+/* The same at the reference's precision (the fp32 step's): fp32 x, w_gu and gated;
+ * fused = 0 forces the two passes. */
+vkh_status vkh_gate_up_swiglu(const float *x, const float *w_gu, float *gu, float *gated,
+                              uint32_t M, uint32_t F, uint32_t K, int fused, vkh_stream stream);
 vkh_status vkh_linear_backward_dx_bf16(const void *dy, const void *w, float *dx, uint32_t M,
                                        uint32_t N, uint32_t K, vkh_stream stream);
 vkh_status vkh_linear_backward_dw_bf16(const void *dy, const void *x, float *dw, uint32_t M,
@@ -702,6 +706,10 @@ vkh_status vkh_qk_rope_backward(const vkh_rope_params *p, const float *dq_out, f
 vkh_status vkh_qkv_project_bf16(const vkh_rope_params *p, uint32_t K, float eps, int qk_norm,
                                 const void *x, const void *w, const float *wq, const float *wk,
                                 float *y, void *out, int fused, vkh_stream stream);
+/* The same at the reference's precision (the fp32 step's): fp32 x, w and out. */
+vkh_status vkh_qkv_project(const vkh_rope_params *p, uint32_t K, float eps, int qk_norm,
+                           const float *x, const float *w, const float *wq, const float *wk,
+                           float *y, float *out, int fused, vkh_stream stream);
 /* shaders/embed_lookup_batched.comp (EmbedLookupBatchedPush {dim, n_pos, scale}) */
 vkh_status vkh_embed_lookup(const float *embed, const uint32_t *ids, float *out, uint32_t n_pos,
                             uint32_t dim, float scale, vkh_stream stream);

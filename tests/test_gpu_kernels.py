@@ -377,6 +377,55 @@ def test_qkv_project_fused_matches_two_passes(case):
     assert rel_l2(y64.ravel(), y1) < 1e-5
 
 
+@pytest.mark.parametrize("case", QKV_PROJ_CASES[:3] + QKV_PROJ_CASES[4:])
+def test_qkv_project_fp32_fused_matches_two_passes(case):
+    """vkh_qkv_project (fp32 operands, the fp32 step's q|k|v projection with
+    the Q/K-RMSNorm + RoPE in the epilogue of the fp32 slab mode) bit for bit
+    against its two passes; the projection against float64 products."""
+    from valkyr_amd import kernels as K
+
+    M, Hq, Hkv, Kd, S, rot, qkn = case
+    hd = 128
+    N = (Hq + 2 * Hkv) * hd
+    note(f"qkv project fp32 rows={M} heads={Hq}/{Hkv} K={Kd} seq={S} rot={rot}")
+    x, W = O.normal(M * Kd, 95), O.normal(N * Kd, 96, 0.05)
+    bx, bW = dev(x), dev(W)
+    wq, wk = dev(O.uniform(hd, 97, 0.5, 1.5)), dev(O.uniform(hd, 98, 0.5, 1.5))
+    p = K.rope_params(M, Hq, Hkv, hd, rot, 1e6, S)
+    outs = []
+    for fused in (True, False):
+        by, bo = zeros(M * N), zeros(M * N)
+        K.qkv_project(p, Kd, 1e-6, qkn, bx, bW, wq, wk, by, bo, fused=fused)
+        outs.append((host(by), host(bo)))
+    (y1, o1), (y0, o0) = outs
+    assert np.array_equal(y1, y0) and np.array_equal(o1, o0)
+    y64 = x.astype(np.float64).reshape(M, Kd) @ W.astype(np.float64).reshape(N, Kd).T
+    assert rel_l2(y64.ravel(), y1) < 1e-5
+
+
+@pytest.mark.parametrize("shape", [(2048, 3072, 1024), (2000, 3072, 1000), (256, 192, 128)])
+def test_gate_up_swiglu_fp32_fused_matches_two_passes(shape):
+    """vkh_gate_up_swiglu (fp32: the fp32 step's gate/up projection with the
+    SwiGLU in the epilogue) bit for bit against its two passes; gu against
+    float64 products.  The last shape's plan is not the 128 x 128 tile (two
+    passes either way)."""
+    from valkyr_amd import kernels as K
+
+    M, F, Kd = shape
+    note(f"gate/up + SwiGLU fp32 M={M} F={F} K={Kd}")
+    x, W = O.normal(M * Kd, 99), O.normal(2 * F * Kd, 100, 0.05)
+    bx, bW = dev(x), dev(W)
+    outs = []
+    for fused in (True, False):
+        bgu, bg = zeros(M * 2 * F), zeros(M * F)
+        K.gate_up_swiglu(bx, bW, bgu, bg, M, F, Kd, fused=fused)
+        outs.append((host(bgu), host(bg)))
+    (g1, s1), (g0, s0) = outs
+    assert np.array_equal(g1, g0) and np.array_equal(s1, s0)
+    g64 = x.astype(np.float64).reshape(M, Kd) @ W.astype(np.float64).reshape(2 * F, Kd).T
+    assert rel_l2(g64.ravel(), g1) < 1e-5
+
+
 # (M, N, K, r): the rank-r kernels' shapes (r a multiple of 4 up to 64, N and
 # K multiples of 64; ragged M; config 4's k/v projection width at a smaller
 # M) and a shape outside them that takes the general GEMMs.

@@ -221,6 +221,8 @@ SIGNATURES = [
     ("vkh_matmul_nt_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_gate_up_swiglu_bf16", ST, [P, P, P, P, U32, U32, U32, P]),
     ("vkh_qkv_project_bf16", ST, [P, U32, C.c_float, C.c_int, P, P, P, P, P, P, C.c_int, P]),
+    ("vkh_qkv_project", ST, [P, U32, C.c_float, C.c_int, P, P, P, P, P, P, C.c_int, P]),
+    ("vkh_gate_up_swiglu", ST, [P, P, P, P, U32, U32, U32, C.c_int, P]),
     ("vkh_linear_backward_dx_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_linear_backward_dw_bf16", ST, [P, P, P, U32, U32, U32, P]),
     ("vkh_lora_forward", ST, [P, P, P, P, P, P, U32, U32, U32, U32, F, U32, P]),

@@ -440,6 +440,25 @@ vkh_status vkh_gate_up_swiglu_bf16(const void *x, const void *w_gu, float *gu, v
     return VKH_OK;
 }
 
+vkh_status vkh_gate_up_swiglu(const float *x, const float *w_gu, float *gu, float *gated,
+                              uint32_t M, uint32_t F, uint32_t K, int fused, vkh_stream stream) {
+    CHECK_ARG(x && w_gu && gu && gated, "null pointer");
+    CHECK_ARG(2ull * F < (1ull << 31), "F too large");
+    hipStream_t st = S(stream);
+    if (fused) {
+        const hipError_t e = g32_gate_up_swiglu(x, K, w_gu, K, gu, 2L * F, gated, F, (int)M, (int)F,
+                                                (int)K, st);
+        if (e != hipErrorNotSupported) {
+            VKH_HIP(e);
+            return VKH_OK;
+        }
+    }
+    const vkh_status r = vkh_matmul_nt(x, w_gu, gu, M, 2 * F, K, VKH_PRECISION_FP32, stream);
+    if (r != VKH_OK) return r;
+    VKH_HIP(swiglu_forward(gu, 2L * F, gu + F, 2L * F, gated, F, DType::F32, (int)M, (int)F, st));
+    return VKH_OK;
+}
+
 vkh_status vkh_linear_backward_dx_bf16(const void *dy, const void *w, float *dx, uint32_t M,
                                        uint32_t N, uint32_t K, vkh_stream stream) {
     CHECK_ARG(dy && w && dx, "null pointer");
@@ -785,6 +804,34 @@ vkh_status vkh_qkv_project_bf16(const vkh_rope_params *p, uint32_t K, float eps,
     const vkh_status r = vkh_matmul_nt_bf16(x, w, y, p->n_pos, N, K, stream);
     if (r != VKH_OK) return r;
     VKH_HIP(qkv_prepare_forward(L, y, N, wq, wk, out, N, DType::BF16, tab, st));
+    return VKH_OK;
+}
+
+vkh_status vkh_qkv_project(const vkh_rope_params *p, uint32_t K, float eps, int qk_norm,
+                           const float *x, const float *w, const float *wq, const float *wk,
+                           float *y, float *out, int fused, vkh_stream stream) {
+    CHECK_ARG(p && x && w && y && out, "null pointer");
+    CHECK_ARG(!qk_norm || (wq && wk), "null norm gains");
+    CHECK_ARG(p->rotary_dim <= p->head_dim && (p->rotary_dim % 2) == 0, "rotary_dim");
+    QkvLayout L;
+    L.n_rows = (int)p->n_pos; L.n_q_heads = (int)p->n_q_heads; L.n_kv_heads = (int)p->n_kv_heads;
+    L.head_dim = (int)p->head_dim; L.seq_len = p->seq_len ? (int)p->seq_len : (int)p->n_pos;
+    L.rotary_dim = (int)p->rotary_dim; L.theta = p->theta_base; L.eps = eps; L.qk_norm = qk_norm ? 1 : 0;
+    const float2 *tab = nullptr;
+    VKH_TRY(rope_table_cached(L.seq_len, L.rotary_dim, L.theta, &tab));
+    const uint32_t N = (p->n_q_heads + 2 * p->n_kv_heads) * p->head_dim;
+    hipStream_t st = S(stream);
+    if (fused) {
+        const hipError_t e = g32_qkv_norm_rope(x, K, w, K, y, N, L.n_rows, (int)N, (int)K, L, wq, wk,
+                                               out, N, tab, st);
+        if (e != hipErrorNotSupported) {
+            VKH_HIP(e);
+            return VKH_OK;
+        }
+    }
+    const vkh_status r = vkh_matmul_nt(x, w, y, p->n_pos, N, K, VKH_PRECISION_FP32, stream);
+    if (r != VKH_OK) return r;
+    VKH_HIP(qkv_prepare_forward(L, y, N, wq, wk, out, N, DType::F32, tab, st));
     return VKH_OK;
 }
 

@@ -110,6 +110,18 @@ def qkv_project_bf16(p, K, eps, qk_norm, x, w, wq, wk, y, out, fused=True, strea
                                      _p(wk), _p(y), _p(out), 1 if fused else 0, _s(stream)))
 
 
+def qkv_project(p, K, eps, qk_norm, x, w, wq, wk, y, out, fused=True, stream=None):
+    """The fp32 form of qkv_project_bf16 (fp32 x, w and out)."""
+    check(lib().vkh_qkv_project(C.byref(p), K, eps, 1 if qk_norm else 0, _p(x), _p(w), _p(wq),
+                                _p(wk), _p(y), _p(out), 1 if fused else 0, _s(stream)))
+
+
+def gate_up_swiglu(x, w_gu, gu, gated, M, F, K, fused=True, stream=None):
+    """The fp32 form of gate_up_swiglu_bf16 (fp32 operands and gated)."""
+    check(lib().vkh_gate_up_swiglu(_p(x), _p(w_gu), _p(gu), _p(gated), M, F, K, 1 if fused else 0,
+                                   _s(stream)))
+
+
 def linear_backward_dx_bf16(dy, w, dx, M, N, K, stream=None):
     """dx[M,K] = dy[M,N] w[N,K] on bf16 operands."""
     check(lib().vkh_linear_backward_dx_bf16(_p(dy), _p(w), _p(dx), M, N, K, _s(stream)))
