@@ -8,7 +8,7 @@
 //   * >= 512 tiles of 128 x 128       -> 128 x 128, 8 waves of 64 x 32
 //   * K >= 16384 and >= 256 tiles of 128 x 128 -> 256 x 256 split-K 3 ways
 //   * K >= 4096 and >= 256 tiles of 128 x 128  -> 128 x 128, 8 waves
-//   * K >= 16384 and < 256 such tiles -> 128 x 128 split-K, up to 4 ways (head dh)
+//   * K >= 16384 and < 256 such tiles -> 256 x 256 split-K 8 ways (head dh)
 //   * < 384 tiles of 128 x 64, K >= 2048 -> 128 x 64 split-K 2 ways
 //   * otherwise                       -> 128 x 64
 // Operands that break the kernel's layout rules (16-byte alignment, ld and
@@ -77,7 +77,11 @@ Plan plan(const GemmShape &s, size_t ws_bytes) {
         // in column order (the LoRA step: 66.7 against 68.1 ms with row groups)
         p = Plan{Pick::T128w8, 1, true};
     else if (s.K >= 16384 && t128 < 256)
-        p = Plan{Pick::T128, (int)std::min<long>(4, std::max<long>(1, 512 / t128))};
+        // the head's dh at config 3 (M = 2048, N = 1024, K = 151936: 32 tiles of
+        // 256 x 256): split 8 ways, 256 blocks; in the step 18.78-18.79 against
+        // 18.91 ms for 128 x 128 split 4 (Big split 16: 18.93-18.96; 128 x 128
+        // split 8: 19.06-19.10)
+        p = Plan{Pick::Big, 8};
     else if (t64 < 384 && s.K >= 2048)
         // two wave groups in one block: alone, faster than split-K + reduce up
         // to K = 4096 and slower at 6144, but in the two-stream step faster
