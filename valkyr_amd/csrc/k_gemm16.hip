@@ -92,6 +92,18 @@ Plan plan(const GemmShape &s, size_t ws_bytes) {
     return p;
 }
 
+// Whether the fused-epilogue forward kernels (8-wave 128 x 128 tiles only) take
+// the product: where plan() picks that tile, or, for a launch paired with one
+// of the same shape on a second stream (the forward's two half batches), where
+// M is whole tiles and the pair together fills a chip-wide round (the config-3
+// step's q|k|v and gate/up halves: 256 + 256 and 384 + 384 tiles; the forward
+// as two concurrent half batches measured 18.58-18.59 against 18.85 ms).
+bool fused_tile_ok(const GemmShape &s, bool paired) {
+    const Plan p = plan(s, 0);
+    if (p.tile == Pick::T128w8 && p.splits == 1) return true;
+    return paired && s.M % 128 == 0 && 2L * (s.M / 128) * ceil_div(s.N, 128) >= 512;
+}
+
 template <Lay LA, Lay LB, class Epi>
 hipError_t run16(const Op16 &a, const Op16 &b, const GemmShape &s, const Epi &e, const GemmWs &ws,
                  hipStream_t st) {
@@ -326,11 +338,10 @@ hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, lo
 // parity-green but measured config 4 at 59.93-60.07 against 59.68-59.73 ms and config 5
 // unchanged, 584.1-584.6 against 584.0-585.0 ms.)
 hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, float *gu,
-                              long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st) {
+                              long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st,
+                              bool paired) {
     if (M <= 0 || F <= 0 || F % 64) return hipErrorNotSupported;
-    const GemmShape s{M, 2 * F, K};
-    const Plan p = plan(s, 0);
-    if (p.tile != Pick::T128w8 || p.splits != 1) return hipErrorNotSupported;
+    if (!fused_tile_ok(GemmShape{M, 2 * F, K}, paired)) return hipErrorNotSupported;
     Op16 a, b;
     if (!make_op(x, ldx, M, K, a) || !make_op(w, ldw, 2L * F, K, b)) return hipErrorNotSupported;
     const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (F / (T128w8::BN / 2)));
@@ -437,19 +448,19 @@ __global__ __launch_bounds__(Cfg::NT, 1) void gemm16_qkv_kernel(Op16 a, Op16 b, 
 hipError_t g16_qkv_norm_rope(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy,
                              int M, int N, int K, const QkvLayout &L, const float *wq,
                              const float *wk, bf16 *out, long ld_out, const float2 *tab,
-                             hipStream_t st) {
+                             hipStream_t st, bool paired) {
     if (M <= 0 || L.head_dim != 128 || L.n_rows != M || L.seq_len <= 0 || L.rotary_dim % 16 ||
         L.rotary_dim > 128 || N != (L.n_q_heads + 2 * L.n_kv_heads) * 128)
         return hipErrorNotSupported;
     const GemmShape s{M, N, K};
-    const Plan p = plan(s, 0);
-    if (p.tile != Pick::T128w8 || p.splits != 1) return hipErrorNotSupported;
+    if (!fused_tile_ok(s, paired)) return hipErrorNotSupported;
+    const Plan p = plan(s, 0);  // its tile order where it is this tile
     if (((uintptr_t)out & 15u) || ld_out % 8 || (L.qk_norm && (((uintptr_t)wq | (uintptr_t)wk) & 15u)) ||
         (L.rotary_dim && ((uintptr_t)tab & 15u)))
         return hipErrorNotSupported;
     Op16 a, b;
     if (!make_op(x, ldx, M, K, a) || !make_op(w, ldw, N, K, b)) return hipErrorNotSupported;
-    const int g = p.column_order ? 0 : tile_group_rows<Lay::K, Lay::K>();
+    const int g = p.tile == Pick::T128w8 && p.column_order ? 0 : tile_group_rows<Lay::K, Lay::K>();
     const unsigned tiles = (unsigned)(ceil_div(M, T128w8::BM) * (N / T128w8::BN));
     hipLaunchKernelGGL((gemm16_qkv_kernel<T128w8>), dim3(tiles), dim3(T128w8::NT), 0, st, a, b, s, y,
                        ldy, QkvEpi<bf16>{L, wq, wk, out, ld_out, tab}, g);

@@ -44,8 +44,12 @@ hipError_t g16_nt(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, lo
 // The gate/up projection with the SwiGLU forward fused into its epilogue (gu fp32 for
 // the backward, gated bf16 for the down projection); hipErrorNotSupported, launching
 // nothing, where the [M, 2F] product's plan is not the 8-wave 128 x 128 tile.
+// paired: the caller runs another M rows of the same product on a second stream at
+// the same time, so the tile is taken wherever the two launches together give it a
+// chip-wide round (fused_tile_ok).
 hipError_t g16_gate_up_swiglu(const bf16 *x, long ldx, const bf16 *w, long ldw, float *gu,
-                              long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st);
+                              long ldgu, bf16 *gated, long ldg, int M, int F, int K, hipStream_t st,
+                              bool paired = false);
 hipError_t g16_nn(const bf16 *dy, long lddy, const bf16 *w, long ldw, float *dx, long lddx, int M,
                   int N, int K, float alpha, float beta, const GemmWs &ws, hipStream_t st);
 // dx as bf16 (the operand precision of the next kernel), no split-K / fp32 copy.
@@ -220,11 +224,11 @@ hipError_t qkv_prepare_forward(const QkvLayout &L, const float *qkv, long ld_qkv
 // The q|k|v projection y = x w^T (bf16 operands, fp32 y) with qkv_prepare_forward's
 // bf16 output fused into the GEMM's epilogue (the same values bit for bit);
 // hipErrorNotSupported, launching nothing, unless head_dim is 128 and the product's
-// plan is the 8-wave 128 x 128 tile.
+// plan is the 8-wave 128 x 128 tile (paired: as for g16_gate_up_swiglu).
 hipError_t g16_qkv_norm_rope(const bf16 *x, long ldx, const bf16 *w, long ldw, float *y, long ldy,
                              int M, int N, int K, const QkvLayout &L, const float *wq,
                              const float *wk, bf16 *out, long ld_out, const float2 *tab,
-                             hipStream_t st);
+                             hipStream_t st, bool paired = false);
 // fp32 forms (fp32 operands and outputs), where the fp32 plan is the 8-wave 128 x 128 tile.
 hipError_t g32_qkv_norm_rope(const float *x, long ldx, const float *w, long ldw, float *y, long ldy,
                              int M, int N, int K, const QkvLayout &L, const float *wq,

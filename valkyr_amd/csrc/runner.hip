@@ -137,6 +137,11 @@ struct vkh_runner {
     // ... with the dQ kernel on a second stream beside dK/dV (one stream
     // otherwise: no side stream, and the dK/dV grid leaves CUs idle)
     bool attn_fork = false;
+    // bf16 two-stream mode: the forward runs as two half batches, the first
+    // on the main stream and the second on the side stream (forward_halves)
+    bool half_fwd = false;
+    std::vector<Acts> acts_h[2];
+    hipEvent_t ev_hf = nullptr, ev_hj = nullptr;
     hipStream_t aux = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // LoRA: each layer's adapter gradients dA, dB (lora_cols) run on `aux`
@@ -237,6 +242,8 @@ struct vkh_runner {
         if (side) (void)hipStreamDestroy(side);
         if (aux) (void)hipStreamSynchronize(aux);
         if (ev_fork) (void)hipEventDestroy(ev_fork);
+        if (ev_hf) (void)hipEventDestroy(ev_hf);
+        if (ev_hj) (void)hipEventDestroy(ev_hj);
         if (ev_join) (void)hipEventDestroy(ev_join);
         for (hipEvent_t e : ev_laux) (void)hipEventDestroy(e);
         if (aux) (void)hipStreamDestroy(aux);
@@ -528,6 +535,11 @@ struct vkh_runner {
             ev_layer.assign(L, nullptr);
             for (int l = 0; l < L; ++l)
                 VKH_HIP(hipEventCreateWithFlags(&ev_layer[l], kOrderEvent));
+            half_fwd = b16() && !recompute && B % 2 == 0;
+            if (half_fwd) {
+                VKH_HIP(hipEventCreateWithFlags(&ev_hf, kOrderEvent));
+                VKH_HIP(hipEventCreateWithFlags(&ev_hj, kOrderEvent));
+            }
             if (recompute) {
                 ev_sdone.assign(L, nullptr);
                 for (int l = 0; l < L; ++l)
@@ -996,7 +1008,7 @@ struct vkh_runner {
             fq = g16_qkv_norm_rope((const bf16 *)n1.p, n1.ld, Wb(s.t[1]), D, a.qkv, qkvd, T, qkvd, D,
                                    ql, cfg.qk_norm ? W(s.t[9]) : nullptr,
                                    cfg.qk_norm ? W(s.t[10]) : nullptr, (bf16 *)a.qkv_attn, qkvd,
-                                   rope_tab, cur);
+                                   rope_tab, cur, half_fwd);
         else if (!b16() && adt == DType::F32 && !lora)
             fq = g32_qkv_norm_rope((const float *)n1.p, n1.ld, W(s.t[1]), D, a.qkv, qkvd, T, qkvd, D,
                                    ql, cfg.qk_norm ? W(s.t[9]) : nullptr,
@@ -1031,7 +1043,7 @@ struct vkh_runner {
         hipError_t fused = hipErrorNotSupported;
         if (b16() && !proj_lora(4) && !proj_lora(5))
             fused = g16_gate_up_swiglu((const bf16 *)n2.p, n2.ld, Wb(s.t[6]), D, a.gu, 2 * F,
-                                       a.gatedb, F, T, F, D, cur);
+                                       a.gatedb, F, T, F, D, cur, half_fwd);
         else if (!b16() && !lora)
             fused = g32_gate_up_swiglu((const float *)n2.p, n2.ld, W(s.t[6]), D, a.gu, 2 * F, a.gated,
                                        F, T, F, D, cur);
@@ -1049,11 +1061,64 @@ struct vkh_runner {
         return VKH_OK;
     }
 
+    // The layers' forward as two half batches of whole sequences at once, the
+    // first half on the main stream and the second on the side stream (idle
+    // in the forward).  Every forward kernel works on rows, attention on whole
+    // sequences, so the halves exchange nothing until the final norm, and one
+    // stream's kernel tails and launch gaps overlap the other's work: the
+    // config-3 step 18.85 -> 18.58-18.59 ms with the same losses (the fp32
+    // step, whose forward GEMMs are compute-bound, measured slower: 76.55
+    // against 75.9 ms).  Each half is layer_forward on the row range: T, B,
+    // the stream, its split-K workspace, the input rows and the activation
+    // pointers are switched for the call and restored after it.
+    vkh_status forward_halves() {
+        const int T0 = T, B0 = B;
+        const long th = T0 / 2;
+        const size_t es = adt == DType::BF16 ? 2 : 4;
+        for (int h = 0; h < 2; ++h) {
+            acts_h[h] = acts;
+            const long r0 = h * th;
+            auto off = [&](auto *&ptr, long ld) {
+                if (ptr) ptr += r0 * ld;
+            };
+            for (Acts &a : acts_h[h]) {
+                off(a.n1, D); off(a.qkv, qkvd); off(a.attn_out, qd); off(a.lse, H); off(a.mid, D);
+                off(a.n2, D); off(a.gu, 2 * F); off(a.gated, F); off(a.y, D);
+                off(a.n1b, D); off(a.attn_b, qd); off(a.n2b, D); off(a.gatedb, F);
+                if (a.qkv_attn) a.qkv_attn = (char *)a.qkv_attn + r0 * qkvd * (long)es;
+            }
+        }
+        hipStream_t c0 = cur;
+        const GemmWs w0 = gws;
+        float *x0 = x_emb;
+        VKH_HIP(hipEventRecord(ev_hf, c0));
+        VKH_HIP(hipStreamWaitEvent(side, ev_hf, 0));
+        vkh_status st = VKH_OK;
+        T = (int)th;
+        B = B0 / 2;
+        for (int l = 0; l < L && st == VKH_OK; ++l)
+            for (int h = 0; h < 2 && st == VKH_OK; ++h) {
+                cur = h ? side : c0;
+                gws = h ? gws2 : w0;
+                x_emb = x0 + h * th * D;
+                std::swap(acts, acts_h[h]);
+                st = layer_forward(l);
+                std::swap(acts, acts_h[h]);
+            }
+        T = T0; B = B0; cur = c0; gws = w0; x_emb = x0;
+        VKH_TRY(st);
+        VKH_HIP(hipEventRecord(ev_hj, side));
+        VKH_HIP(hipStreamWaitEvent(cur, ev_hj, 0));
+        return VKH_OK;
+    }
+
     vkh_status forward_all() {
         VKH_TRY(sync_shadow());
         if (bf16_only(embed)) VKH_HIP(embed_lookup_bf16(Wb(embed), tok_d, x_emb, T, D, 1.0f, cur));
         else VKH_HIP(embed_lookup(W(embed), tok_d, x_emb, T, D, 1.0f, cur));
-        for (int l = 0; l < L; ++l) VKH_TRY(layer_forward(l));
+        if (half_fwd) VKH_TRY(forward_halves());
+        else
+            for (int l = 0; l < L; ++l) VKH_TRY(layer_forward(l));
         VKH_HIP(rmsnorm_forward(acts[L - 1].y, W(final_norm), b16() ? (void *)fn_outb : (void *)fn_out,
                                 b16() ? DType::BF16 : DType::F32, T, D, cfg.rms_eps, 0, cur));
         return VKH_OK;
