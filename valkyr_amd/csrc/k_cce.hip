@@ -15,6 +15,12 @@
 // cce_backward_dh.comp:109-123, cce_backward_dw.comp:73-103); on a 288 GB
 // part the [N, V] dz buffer (0.6 GB at N = 2048) is cheap and turns the
 // backward into three dense GEMMs.
+//
+// With fp32 dz (the fp32 precision) the forward's epilogue can also store the
+// fp32 logits into the dz buffer (z_out), and the backward then forms dz from
+// them in place with one streaming pass (cce_dz_k, the dz epilogue's
+// arithmetic element by element) instead of recomputing the logits GEMM: the
+// same values bit for bit, 2.5 GB of traffic in place of a 0.64 TFLOP product.
 #include "gemm16.hpp"
 #include "ops.hpp"
 
@@ -41,6 +47,7 @@ struct EpiCceStats {
     CceWork w;
     const uint32_t *tgt;
     int V;
+    float *zo = nullptr;  // when set: the logits themselves, [N, V] row-major
 
     template <int TM, int TN>
     VKH_DEV void apply(const f32x4 (&acc)[TM][TN], const FragPos &fp, const GemmShape &s) const {
@@ -75,6 +82,7 @@ struct EpiCceStats {
                         mx = fmaxf(mx, z);
                         zs += z;
                         if (tc == 16 * j) w.zt[row] = z;
+                        if (zo && rok) zo[(size_t)row * V + fp.col0 + 16 * j + c16] = z;
                     }
                 }
                 mx = row16_max(mx);
@@ -95,6 +103,20 @@ struct EpiCceStats {
             }
     }
 };
+
+// dz of one row: the coefficients of dz = sf exp(z - lse) - off - [v == t] tsc
+// (the 1 / N folded in), and one element of it.  The dz epilogue and cce_dz_k
+// both compute through these, so their results agree bit for bit.
+struct DzRow {
+    float lL2, sf;
+};
+VKH_DEV DzRow dz_row(float l, float zl2, float inv_n) { return DzRow{l * LOG2E, (1.0f + zl2 * l) * inv_n}; }
+VKH_DEV float dz_elem(float z, const DzRow &r, float off, float tsc, bool is_t) {
+    const float p = __builtin_amdgcn_exp2f(fmaf(z, LOG2E, -r.lL2));
+    float d = fmaf(r.sf, p, -off);
+    if (is_t) d -= tsc;
+    return d;
+}
 
 template <typename TZ>
 struct EpiCceDz {
@@ -122,22 +144,45 @@ struct EpiCceDz {
             for (int r = 0; r < 4; ++r) {
                 const int row = fp.row0 + 16 * i + 4 * g + r;
                 if (row >= s.M) continue;
-                const float l = lse[row];
-                const float lL2 = l * LOG2E;
-                const float sf = (1.0f + zl2 * l) * inv_n;
+                const DzRow dr = dz_row(lse[row], zl2, inv_n);
                 const int tc = (int)tgt[row] - fp.col0 - c16;
                 TZ *out = dz + (size_t)row * V + fp.col0 + c16;
 #pragma unroll
                 for (int j = 0; j < TN; ++j) {
                     if (!FULL && fp.col0 + 16 * j + c16 >= V) continue;
-                    const float p = __builtin_amdgcn_exp2f(fmaf(acc[i][j][r], LOG2E, -lL2));
-                    float d = fmaf(sf, p, -off);
-                    if (tc == 16 * j) d -= tsc;
-                    out[16 * j] = (TZ)d;
+                    out[16 * j] = (TZ)dz_elem(acc[i][j][r], dr, off, tsc, tc == 16 * j);
                 }
             }
     }
 };
+
+// dz from the stored fp32 logits z [N, V] (z and dz may be the same buffer: each
+// element is read and then written by one thread).  Block (x, row): 4 columns
+// per thread with 16-byte rows (V % 4 == 0 and 16-byte aligned), else 1.
+template <typename TZ, int VEC>
+__global__ __launch_bounds__(256) void cce_dz_k(const float *z, TZ *dz, const uint32_t *tgt,
+                                                const float *lse, int V, float inv_n, float t_scale,
+                                                float eps_over_v, float zl2) {
+    const int row = blockIdx.y;
+    const int c0 = (blockIdx.x * 256 + threadIdx.x) * VEC;
+    if (c0 >= V) return;
+    const DzRow dr = dz_row(lse[row], zl2, inv_n);
+    const float off = eps_over_v * inv_n, tsc = t_scale * inv_n;
+    const int t = (int)tgt[row];
+    const size_t i = (size_t)row * V + c0;
+    if constexpr (VEC == 4) {
+        const float4 zv = *reinterpret_cast<const float4 *>(z + i);
+        const float d0 = dz_elem(zv.x, dr, off, tsc, t == c0), d1 = dz_elem(zv.y, dr, off, tsc, t == c0 + 1),
+                    d2 = dz_elem(zv.z, dr, off, tsc, t == c0 + 2), d3 = dz_elem(zv.w, dr, off, tsc, t == c0 + 3);
+        if constexpr (sizeof(TZ) == 4) {
+            *reinterpret_cast<float4 *>(dz + i) = make_float4(d0, d1, d2, d3);
+        } else {
+            dz[i] = (TZ)d0; dz[i + 1] = (TZ)d1; dz[i + 2] = (TZ)d2; dz[i + 3] = (TZ)d3;
+        }
+    } else {
+        dz[i] = (TZ)dz_elem(z[i], dr, off, tsc, t == c0);
+    }
+}
 
 __global__ void cce_merge_k(CceShape s, CceWork w, float *lse, float *loss_row) {
     const int lane = threadIdx.x % 64;
@@ -230,10 +275,10 @@ size_t cce_work_floats(const CceShape &s) {
 
 hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const float *w,
                        const uint32_t *tgt, float *lse, float *loss_row, float *loss_mean,
-                       float *work, hipStream_t st) {
+                       float *work, hipStream_t st, float *z_out) {
     if (s.N <= 0) return hipSuccess;
     CceWork cw = carve(work, s);
-    EpiCceStats e{cw, tgt, s.V};
+    EpiCceStats e{cw, tgt, s.V, z_out};
     hipError_t err = logits_gemm(pr, s, h, w, e, st);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(cce_merge_k, dim3(ceil_div(s.N, 4)), dim3(256), 0, st, s, cw, lse, loss_row);
@@ -243,7 +288,7 @@ hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const fl
 
 hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const float *w,
                         const uint32_t *tgt, const float *lse, void *dz, float *dh, float *dw,
-                        float dw_beta, hipStream_t st) {
+                        float dw_beta, hipStream_t st, const float *z) {
     if (s.N <= 0) return hipSuccess;
     const float inv_n = 1.0f / (float)s.N;
     const float t_scale = 1.0f - s.label_smoothing;
@@ -251,7 +296,18 @@ hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const f
     const float zl2 = 2.0f * s.z_loss_scale;
     hipError_t err;
     const DType zdt = pr == Precision::BF16 ? DType::BF16 : DType::F32;
-    if (zdt == DType::BF16) {
+    if (z) {  // the logits the forward stored: dz in one streaming pass
+        const bool v4 = s.V % 4 == 0 && ((uintptr_t)z & 15u) == 0 && ((uintptr_t)dz & 15u) == 0;
+        const dim3 grid((unsigned)ceil_div(s.V, 256 * (v4 ? 4 : 1)), (unsigned)s.N);
+        if (zdt == DType::BF16) {
+            if (v4) hipLaunchKernelGGL((cce_dz_k<bf16, 4>), grid, dim3(256), 0, st, z, (bf16 *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2);
+            else hipLaunchKernelGGL((cce_dz_k<bf16, 1>), grid, dim3(256), 0, st, z, (bf16 *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2);
+        } else {
+            if (v4) hipLaunchKernelGGL((cce_dz_k<float, 4>), grid, dim3(256), 0, st, z, (float *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2);
+            else hipLaunchKernelGGL((cce_dz_k<float, 1>), grid, dim3(256), 0, st, z, (float *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2);
+        }
+        err = hipGetLastError();
+    } else if (zdt == DType::BF16) {
         EpiCceDz<bf16> e{(bf16 *)dz, tgt, lse, s.V, inv_n, t_scale, eps_over_v, zl2};
         err = logits_gemm(pr, s, h, w, e, st);
     } else {

@@ -369,9 +369,11 @@ struct CceShape {
     float z_loss_scale, label_smoothing;
 };
 size_t cce_work_floats(const CceShape &s);
+// z_out (optional): the fp32 logits [N, V] are stored there too, for
+// cce_backward's z.
 hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const float *w,
                        const uint32_t *tgt, float *lse, float *loss_row, float *loss_mean,
-                       float *work, hipStream_t st);
+                       float *work, hipStream_t st, float *z_out = nullptr);
 // bf16-operand forms (h, W bf16; dz bf16), on the gemm16 kernel.
 hipError_t cce_forward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
                          float *lse, float *loss_row, float *loss_mean, float *work,
@@ -380,9 +382,11 @@ hipError_t cce_backward16(const CceShape &s, const bf16 *h, const bf16 *w, const
                           const float *lse, bf16 *dz, float *dh, float *dw, float dw_beta,
                           const GemmWs &ws, hipStream_t st);
 // dz (bf16 for Precision::BF16 else fp32) [N, V] is materialised in `dz`;
-// dh overwritten (if non-null); dW = beta*dW + dz^T h (if non-null).
+// dh overwritten (if non-null); dW = beta*dW + dz^T h (if non-null).  z: the
+// logits cce_forward stored with z_out (may be dz itself), read instead of
+// recomputing them; nullptr recomputes.
 hipError_t cce_backward(Precision pr, const CceShape &s, const float *h, const float *w,
                         const uint32_t *tgt, const float *lse, void *dz, float *dh, float *dw,
-                        float dw_beta, hipStream_t st);
+                        float dw_beta, hipStream_t st, const float *z = nullptr);
 
 }  // namespace vkh

@@ -1370,15 +1370,17 @@ struct vkh_runner {
                 VKH_HIP(hipEventRecord(ev_lm, side));
             }
         } else {
+            // the fp32 logits kept in the dz buffer, which the backward turns
+            // into dz in place (no second logits GEMM)
             VKH_HIP(cce_forward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
-                                cce_work, cur));
+                                cce_work, cur, (float *)dz));
             // two streams: dW_lm on the side stream starts as soon as dz is
             // written, beside dh on the main stream (fp32: 75.97-75.99 -> 75.30 ms,
             // same losses; the bf16 step, whose dh is the short split-K form,
             // measured 0.05-0.09 ms slower this way and keeps dh first)
             const bool dw_early = concurrent && dw_lm;
             VKH_HIP(cce_backward(pr, cs, fn_out, W(lm_head), tgt_d, ce_lse, dz, dw_early ? nullptr : d_fn,
-                                 concurrent ? nullptr : dw_lm, 0.f, cur));
+                                 concurrent ? nullptr : dw_lm, 0.f, cur, (const float *)dz));
             if (concurrent && dw_lm) {  // as above, on the fp32 logits gradient
                 if (split) {
                     if (++mark_stamp == 0) {
