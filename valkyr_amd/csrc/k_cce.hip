@@ -339,10 +339,10 @@ namespace vkh {
 
 hipError_t cce_forward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
                          float *lse, float *loss_row, float *loss_mean, float *work,
-                         hipStream_t st) {
+                         hipStream_t st, float *z_out) {
     if (s.N <= 0) return hipSuccess;
     CceWork cw = carve(work, s);
-    EpiCceStats e{cw, tgt, s.V};
+    EpiCceStats e{cw, tgt, s.V, z_out};
     hipError_t err = logits16(s, h, w, e, st);
     if (err != hipSuccess) return err;
     hipLaunchKernelGGL(cce_merge_k, dim3(ceil_div(s.N, 4)), dim3(256), 0, st, s, cw, lse, loss_row);
@@ -352,11 +352,20 @@ hipError_t cce_forward16(const CceShape &s, const bf16 *h, const bf16 *w, const 
 
 hipError_t cce_backward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
                           const float *lse, bf16 *dz, float *dh, float *dw, float dw_beta,
-                          const GemmWs &ws, hipStream_t st) {
+                          const GemmWs &ws, hipStream_t st, const float *z) {
     if (s.N <= 0) return hipSuccess;
     EpiCceDz<bf16> e{dz, tgt, lse, s.V, 1.0f / (float)s.N, 1.0f - s.label_smoothing,
                      s.label_smoothing / (float)s.V, 2.0f * s.z_loss_scale};
-    hipError_t err = logits16(s, h, w, e, st);
+    hipError_t err;
+    if (z) {
+        const bool v4 = s.V % 4 == 0 && ((uintptr_t)z & 15u) == 0;
+        const dim3 grid((unsigned)ceil_div(s.V, 256 * (v4 ? 4 : 1)), (unsigned)s.N);
+        if (v4) hipLaunchKernelGGL((cce_dz_k<bf16, 4>), grid, dim3(256), 0, st, z, dz, tgt, lse, s.V, e.inv_n, e.t_scale, e.eps_over_v, e.zl2);
+        else hipLaunchKernelGGL((cce_dz_k<bf16, 1>), grid, dim3(256), 0, st, z, dz, tgt, lse, s.V, e.inv_n, e.t_scale, e.eps_over_v, e.zl2);
+        err = hipGetLastError();
+    } else {
+        err = logits16(s, h, w, e, st);
+    }
     if (err != hipSuccess) return err;
     // dW[V, D] = dz^T h ;  dh[N, D] = dz W
     if (dw) {

@@ -377,10 +377,10 @@ hipError_t cce_forward(Precision pr, const CceShape &s, const float *h, const fl
 // bf16-operand forms (h, W bf16; dz bf16), on the gemm16 kernel.
 hipError_t cce_forward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
                          float *lse, float *loss_row, float *loss_mean, float *work,
-                         hipStream_t st);
+                         hipStream_t st, float *z_out = nullptr);
 hipError_t cce_backward16(const CceShape &s, const bf16 *h, const bf16 *w, const uint32_t *tgt,
                           const float *lse, bf16 *dz, float *dh, float *dw, float dw_beta,
-                          const GemmWs &ws, hipStream_t st);
+                          const GemmWs &ws, hipStream_t st, const float *z = nullptr);
 // dz (bf16 for Precision::BF16 else fp32) [N, V] is materialised in `dz`;
 // dh overwritten (if non-null); dW = beta*dW + dz^T h (if non-null).  z: the
 // logits cce_forward stored with z_out (may be dz itself), read instead of

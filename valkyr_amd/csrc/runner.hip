@@ -145,6 +145,11 @@ struct vkh_runner {
     // fp32 two-stream mode: the head's dh done on the main stream (the table
     // updates on the side stream wait for it)
     hipEvent_t ev_dh = nullptr;
+    // bf16 two-stream mode: the head forward's fp32 logits [T, V], from which
+    // the backward forms dz in one pass (the fp32 precision keeps them in the
+    // fp32 dz buffer itself); null where they would exceed kLogitsCap
+    float *zf = nullptr;
+    static constexpr size_t kLogitsCap = 4ull << 30;
     hipStream_t aux = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // LoRA: each layer's adapter gradients dA, dB (lora_cols) run on `aux`
@@ -621,6 +626,8 @@ struct vkh_runner {
         VKH_TRY(alloc(cce_work, cce_work_floats(cs)));
         char *z = nullptr;
         VKH_TRY(alloc(z, (size_t)T * V * (b16() ? 2 : 4)));
+        // 18.41-18.47 -> 18.27-18.29 ms at config 3 (1.24 GB), same losses
+        if (b16() && concurrent && (size_t)T * V * 4 <= kLogitsCap) VKH_TRY(alloc(zf, (size_t)T * V));
         dz = z;
         char *ew = nullptr;
         VKH_TRY(alloc(ew, embed_bw_work_bytes(T)));
@@ -1350,9 +1357,9 @@ struct vkh_runner {
         const bool split = with_adam && embed_split_ok();
         if (b16()) {
             VKH_HIP(cce_forward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, loss_row, loss_mean,
-                                  cce_work, cur));
+                                  cce_work, cur, zf));
             VKH_HIP(cce_backward16(cs, fn_outb, Wb(lm_head), tgt_d, ce_lse, (bf16 *)dz, d_fn,
-                                   concurrent ? nullptr : dw_lm, 0.f, gws, cur));
+                                   concurrent ? nullptr : dw_lm, 0.f, gws, cur, zf));
             if (concurrent && dw_lm) {
                 if (split) {  // this step's token rows, for the split embedding update
                     if (++mark_stamp == 0) {
