@@ -145,7 +145,7 @@ struct vkh_runner {
     // fp32 two-stream mode: the head's dh done on the main stream (the table
     // updates on the side stream wait for it)
     hipEvent_t ev_dh = nullptr;
-    // bf16 two-stream mode: the head forward's fp32 logits [T, V], from which
+    // bf16 precision: the head forward's fp32 logits [T, V], from which
     // the backward forms dz in one pass (the fp32 precision keeps them in the
     // fp32 dz buffer itself); null where they would exceed kLogitsCap
     float *zf = nullptr;
@@ -627,7 +627,7 @@ struct vkh_runner {
         char *z = nullptr;
         VKH_TRY(alloc(z, (size_t)T * V * (b16() ? 2 : 4)));
         // 18.41-18.47 -> 18.27-18.29 ms at config 3 (1.24 GB), same losses
-        if (b16() && concurrent && (size_t)T * V * 4 <= kLogitsCap) VKH_TRY(alloc(zf, (size_t)T * V));
+        if (b16() && (size_t)T * V * 4 <= kLogitsCap) VKH_TRY(alloc(zf, (size_t)T * V));
         dz = z;
         char *ew = nullptr;
         VKH_TRY(alloc(ew, embed_bw_work_bytes(T)));
