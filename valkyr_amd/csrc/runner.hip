@@ -149,7 +149,7 @@ struct vkh_runner {
     // the backward forms dz in one pass (the fp32 precision keeps them in the
     // fp32 dz buffer itself); null where they would exceed kLogitsCap
     float *zf = nullptr;
-    static constexpr size_t kLogitsCap = 4ull << 30;
+    static constexpr size_t kLogitsCap = 8ull << 30;
     hipStream_t aux = nullptr;
     hipEvent_t ev_fork = nullptr, ev_join = nullptr;
     // LoRA: each layer's adapter gradients dA, dB (lora_cols) run on `aux`
@@ -626,7 +626,8 @@ struct vkh_runner {
         VKH_TRY(alloc(cce_work, cce_work_floats(cs)));
         char *z = nullptr;
         VKH_TRY(alloc(z, (size_t)T * V * (b16() ? 2 : 4)));
-        // 18.41-18.47 -> 18.27-18.29 ms at config 3 (1.24 GB), same losses
+        // 18.41-18.47 -> 18.27-18.29 ms at config 3 (1.24 GB), same losses; config 5
+        // (8192 tokens, 4.98 GB): 587.4 -> 581.4-581.7 ms in 157.1 GiB
         if (b16() && (size_t)T * V * 4 <= kLogitsCap) VKH_TRY(alloc(zf, (size_t)T * V));
         dz = z;
         char *ew = nullptr;
