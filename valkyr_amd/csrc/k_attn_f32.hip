@@ -24,6 +24,7 @@
 #include <math.h>
 
 #include "ops.hpp"
+#include "qkbwd.hpp"
 
 #pragma clang fp contract(off)
 
@@ -193,8 +194,11 @@ __global__ __launch_bounds__(FNT, 2) void fa_fwd_f32m_k(AttnShape s, const float
 // then meets more of the second stream's work (98 -> 153 us) and the step
 // went 77.0 -> 77.2 ms: with both streams busy the step is set by their
 // total work, not by this kernel's span.)
-template <int HD>
+// QKE: dK leaves through RoPE^T and the K-RMSNorm backward (p.qk), each block
+// writing its k-gain partial to p.qk.pk[block].
+template <int HD, bool QKE>
 __global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtrs p, bool zz) {
+    static_assert(!QKE || HD == 128, "the fused q/k epilogue takes 128-wide head rows");
     constexpr int P = HD + 4, NU = HD / 16;
     __shared__ __attribute__((aligned(16))) float Qs[2][FT * P], Os[2][FT * P];
     __shared__ float Ls[2][FT], Dl[2][FT];
@@ -302,6 +306,24 @@ __global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtr
     float *dkr = p.dk + ((long)b * s.n_kv + ki) * p.lddk + kvh * HD + 4 * g;
     float *dvr = p.dv + ((long)b * s.n_kv + ki) * p.lddv + kvh * HD + 4 * g;
     const float sc = s.inv_sqrt_dim;
+    if constexpr (QKE) {
+        __shared__ float red[4 * 128];
+        const QkEpi &e = p.qk;
+        float v[8][4], dw[8][4] = {};
+#pragma unroll
+        for (int j = 0; j < NU; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[j][r] = dkt[j][r] * sc;
+        qk_row_bwd(v, dw, true, e, e.x + ((long)b * s.n_kv + ki) * e.ldx + (s.n_heads + kvh) * HD, e.gk, ki, g);
+#pragma unroll
+        for (int j = 0; j < NU; ++j) {
+            *reinterpret_cast<float4 *>(dkr + 16 * j) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+            *reinterpret_cast<float4 *>(dvr + 16 * j) = make_float4(dvt[j][0], dvt[j][1], dvt[j][2], dvt[j][3]);
+        }
+        if (e.gk)  // uniform
+            qk_dw_block(dw, red, wave, FNT / 64, true, lane, e.pk + ((long)blockIdx.y * gridDim.x + blockIdx.x) * HD);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NU; ++j) {
         *reinterpret_cast<float4 *>(dkr + 16 * j) =
@@ -311,8 +333,11 @@ __global__ __launch_bounds__(FNT, 2) void fa_bwd_dkv_f32m_k(AttnShape s, AttnPtr
 }
 
 // ── dQ: block = 64 queries of one (sequence, head) ──────────────────────
-template <int HD>
+// QKE: dQ leaves through RoPE^T and the Q-RMSNorm backward (p.qk), each block
+// writing its q-gain partial to p.qk.pq[block].
+template <int HD, bool QKE>
 __global__ __launch_bounds__(FNT, 2) void fa_bwd_dq_f32m_k(AttnShape s, AttnPtrs p, bool zz) {
+    static_assert(!QKE || HD == 128, "the fused q/k epilogue takes 128-wide head rows");
     constexpr int P = HD + 4, NU = HD / 16;
     __shared__ __attribute__((aligned(16))) float Ks[2][FT * P], Vs[2][FT * P];
     const int h = blockIdx.x % s.n_heads, b = blockIdx.x / s.n_heads;
@@ -399,6 +424,22 @@ __global__ __launch_bounds__(FNT, 2) void fa_bwd_dq_f32m_k(AttnShape s, AttnPtrs
     }
     float *dqr = p.dq + ((long)b * s.n_q + qi) * p.lddq + h * HD + 4 * g;
     const float sc = s.inv_sqrt_dim;
+    if constexpr (QKE) {
+        __shared__ float red[4 * 128];
+        const QkEpi &e = p.qk;
+        float v[8][4], dw[8][4] = {};
+#pragma unroll
+        for (int j = 0; j < NU; ++j)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) v[j][r] = dqt[j][r] * sc;
+        qk_row_bwd(v, dw, true, e, e.x + ((long)b * s.n_q + qi) * e.ldx + h * HD, e.gq, qi, g);
+#pragma unroll
+        for (int j = 0; j < NU; ++j)
+            *reinterpret_cast<float4 *>(dqr + 16 * j) = make_float4(v[j][0], v[j][1], v[j][2], v[j][3]);
+        if (e.gq)  // uniform
+            qk_dw_block(dw, red, wave, FNT / 64, true, lane, e.pq + ((long)blockIdx.y * gridDim.x + blockIdx.x) * HD);
+        return;
+    }
 #pragma unroll
     for (int j = 0; j < NU; ++j)
         *reinterpret_cast<float4 *>(dqr + 16 * j) =
@@ -439,20 +480,37 @@ static bool ptrs_ok(const AttnPtrs &p) {
 bool fa_f32m_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     if (!fa_f32m_ok(s) || !ptrs_ok(p) || !al16(p.dk) || !al16(p.dv) || p.lddk % 4 || p.lddv % 4)
         return false;
+    if (p.qk_fp32 && !fa_f32m_qk_ok(s, p)) return false;
     const dim3 grid(s.n_kv_heads * s.n_batch, s.n_kv / 64);
     const bool zz = fits_two_per_cu((long)grid.x * grid.y);
-    if (s.head_dim == 128) hipLaunchKernelGGL(fa_bwd_dkv_f32m_k<128>, grid, dim3(FNT), 0, st, s, p, zz);
-    else hipLaunchKernelGGL(fa_bwd_dkv_f32m_k<64>, grid, dim3(FNT), 0, st, s, p, zz);
+    if (p.qk_fp32) hipLaunchKernelGGL((fa_bwd_dkv_f32m_k<128, true>), grid, dim3(FNT), 0, st, s, p, zz);
+    else if (s.head_dim == 128) hipLaunchKernelGGL((fa_bwd_dkv_f32m_k<128, false>), grid, dim3(FNT), 0, st, s, p, zz);
+    else hipLaunchKernelGGL((fa_bwd_dkv_f32m_k<64, false>), grid, dim3(FNT), 0, st, s, p, zz);
     return true;
 }
 
 bool fa_f32m_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st) {
     if (!fa_f32m_ok(s) || !ptrs_ok(p) || !al16(p.dq) || p.lddq % 4) return false;
+    if (p.qk_fp32 && !fa_f32m_qk_ok(s, p)) return false;
     const dim3 grid(s.n_heads * s.n_batch, s.n_q / 64);
     const bool zz = fits_two_per_cu((long)grid.x * grid.y);
-    if (s.head_dim == 128) hipLaunchKernelGGL(fa_bwd_dq_f32m_k<128>, grid, dim3(FNT), 0, st, s, p, zz);
-    else hipLaunchKernelGGL(fa_bwd_dq_f32m_k<64>, grid, dim3(FNT), 0, st, s, p, zz);
+    if (p.qk_fp32) hipLaunchKernelGGL((fa_bwd_dq_f32m_k<128, true>), grid, dim3(FNT), 0, st, s, p, zz);
+    else if (s.head_dim == 128) hipLaunchKernelGGL((fa_bwd_dq_f32m_k<128, false>), grid, dim3(FNT), 0, st, s, p, zz);
+    else hipLaunchKernelGGL((fa_bwd_dq_f32m_k<64, false>), grid, dim3(FNT), 0, st, s, p, zz);
     return true;
 }
+
+// The fused q/k epilogue's conditions: the tile kernels' shapes with 128-wide
+// heads, a rotary span of 0 or the whole head, 16-byte aligned q/k input rows
+// and gains, and every output pointer the tile kernels need.
+bool fa_f32m_qk_ok(const AttnShape &s, const AttnPtrs &p) {
+    const QkEpi &e = p.qk;
+    return fa_f32m_ok(s) && s.head_dim == 128 && ptrs_ok(p) && al16(p.dq) && al16(p.dk) &&
+           al16(p.dv) && p.lddq % 4 == 0 && p.lddk % 4 == 0 && p.lddv % 4 == 0 && e.x && al16(e.x) &&
+           e.ldx % 4 == 0 && (e.rot == 0 || (e.rot == 128 && e.rope && al16(e.rope))) &&
+           (!e.gq || (al16(e.gq) && e.pq)) && (!e.gk || (al16(e.gk) && e.pk));
+}
+int fa_f32m_dq_blocks(const AttnShape &s) { return s.n_heads * s.n_batch * (s.n_q / 64); }
+int fa_f32m_dkv_blocks(const AttnShape &s) { return s.n_kv_heads * s.n_batch * (s.n_kv / 64); }
 
 }  // namespace vkh

@@ -313,7 +313,10 @@ struct AttnPtrs {
     // bf16 O: when set on the recompute path, the dQ kernel forms
     // D = rowsum(O dO) for its rows itself (written to d) and runs first
     const void *o16 = nullptr; long ldo16 = 0;
-    QkEpi qk;  // recompute path only
+    QkEpi qk;  // recompute path, and the fp32 tile kernels with qk_fp32
+    // fp32 tile kernels: dQ / dK leave through p.qk's RoPE^T and Q/K-norm
+    // backward (fa_f32m_qk_ok must hold; fa_bw_dq / fa_bw_dkv fail otherwise)
+    bool qk_fp32 = false;
     // recompute path: workspace of fa_bw_v4_split_ws_floats(s) floats; when set
     // on a shape fa_bw_v4_split accepts, the dK / dV launch is split in two
     float *split_ws = nullptr;
@@ -327,6 +330,10 @@ bool fa_f32m_fwd(const AttnShape &s, const float *q, long ldq, const float *k, l
                  const float *v, long ldv, float *o, long ldo, float *lse, hipStream_t st);
 bool fa_f32m_dkv(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
 bool fa_f32m_dq(const AttnShape &s, const AttnPtrs &p, hipStream_t st);
+bool fa_f32m_qk_ok(const AttnShape &s, const AttnPtrs &p);
+// blocks of the fp32 dQ and dK/dV grids: the fused epilogue's gain partials
+int fa_f32m_dq_blocks(const AttnShape &s);
+int fa_f32m_dkv_blocks(const AttnShape &s);
 // ob (optional, bf16 operands only): bf16 copy of O for the output projection.
 hipError_t fa_forward(const AttnShape &s, const void *q, long ldq, const void *k, long ldk,
                       const void *v, long ldv, float *o, long ldo, float *lse, DType dt,

@@ -661,6 +661,11 @@ struct vkh_runner {
     // floats of q / k gain partials one layer's backward writes (either path)
     size_t qk_partial_floats() const {
         size_t n = qkv_partial_floats(qkv_layout());
+        if (!b16() && cfg.qk_norm) {  // the fp32 tile kernels' fused epilogue
+            const AttnShape as = attn_shape();
+            if (fa_f32m_ok(as))
+                n = std::max(n, (size_t)(fa_f32m_dq_blocks(as) + fa_f32m_dkv_blocks(as)) * hd);
+        }
         if (qk_fused) {
             const AttnShape as = attn_shape();
             n = std::max(n, (size_t)(fa_bw_v4_q_blocks(as) + fa_bw_v4_k_gain_parts(as, attn_split)) * hd);
@@ -1310,24 +1315,47 @@ struct vkh_runner {
                 VKH_HIP(column_sums(e.pk, fa_bw_v4_k_gain_parts(as, attn_split), hd, hd, Gd(s.t[10]), cur));
             }
         } else {
+            // fp32 with the gains on the side stream: RoPE^T and the Q/K-norm
+            // backward in the fp32 dQ and dK/dV kernels' epilogues (gain partials
+            // per block), where those kernels take the shape
+            bool qk32 = false;
+            if (adt == DType::F32 && !b16() && qk_side && !attn_fused &&
+                (cfg.rotary_dim == 0 || (int)cfg.rotary_dim == hd)) {
+                QkEpi &e = ap.qk;
+                e.x = a.qkv; e.ldx = qkvd;
+                e.gq = W(s.t[9]); e.gk = W(s.t[10]);
+                e.eps = cfg.rms_eps;
+                e.rope = rope_tab; e.rot = (int)cfg.rotary_dim;
+                e.pq = qkp;
+                e.pk = qkp + (size_t)fa_f32m_dq_blocks(as) * hd;
+                qk32 = fa_f32m_qk_ok(as, ap);
+                ap.qk_fp32 = qk32;
+            }
             if (attn_fused) {
                 VKH_TRY(attn_bw());
             } else {
                 VKH_HIP(fa_bw_dkv(as, ap, cur));
                 VKH_HIP(fa_bw_dq(as, ap, cur));
             }
-            // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
-            const QkvLayout ql = qkv_layout();
-            VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
-                                         cfg.qk_norm ? W(s.t[10]) : nullptr,
-                                         cfg.qk_norm && !qk_side ? Gd(s.t[9]) : nullptr,
-                                         cfg.qk_norm && !qk_side ? Gd(s.t[10]) : nullptr, qkp,
-                                         rope_tab, b16() ? d_qkvb : nullptr, qkvd, cur,
-                                         qk_side ? &lg[l].qk_parts : nullptr));
-            if (qk_side) {
-                lg[l].pq = qkp; lg[l].pk = qkp + hd;
-                lg[l].q_parts = lg[l].k_parts = lg[l].qk_parts;
-                lg[l].qk_stride = 2L * hd;
+            if (qk32) {
+                lg[l].pq = ap.qk.pq; lg[l].pk = ap.qk.pk;
+                lg[l].q_parts = fa_f32m_dq_blocks(as);
+                lg[l].k_parts = fa_f32m_dkv_blocks(as);
+                lg[l].qk_stride = hd;
+            } else {
+                // RoPE^T and Q/K-norm backward on the q/k columns (in place, or into the bf16 copy)
+                const QkvLayout ql = qkv_layout();
+                VKH_HIP(qkv_prepare_backward(ql, d_qkv, qkvd, a.qkv, qkvd, cfg.qk_norm ? W(s.t[9]) : nullptr,
+                                             cfg.qk_norm ? W(s.t[10]) : nullptr,
+                                             cfg.qk_norm && !qk_side ? Gd(s.t[9]) : nullptr,
+                                             cfg.qk_norm && !qk_side ? Gd(s.t[10]) : nullptr, qkp,
+                                             rope_tab, b16() ? d_qkvb : nullptr, qkvd, cur,
+                                             qk_side ? &lg[l].qk_parts : nullptr));
+                if (qk_side) {
+                    lg[l].pq = qkp; lg[l].pk = qkp + hd;
+                    lg[l].q_parts = lg[l].k_parts = lg[l].qk_parts;
+                    lg[l].qk_stride = 2L * hd;
+                }
             }
         }
         const Mat mdqkv = b16() ? matb(d_qkvb, qkvd) : matf(d_qkv, qkvd);
