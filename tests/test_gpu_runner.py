@@ -614,6 +614,18 @@ def test_forward_logits_matches_oracle():
     assert rel_l2(ref, got) < 1e-4
 
 
+def test_forward_logits_bf16_half_batches():
+    """bf16 with an even number of sequences: the forward runs as two concurrent
+    half batches (sequence 0 on the main stream, 1 on the second).  The logits
+    of the two-sequence batch against the oracle's bf16-operand model."""
+    m, r, tok, tgt, cfg = build_pair(1, n_seqs=2, seq_len=64)
+    ref = m.forward_logits(tok)
+    got = r.forward_logits(tok)
+    e = rel_l2(ref, got)
+    note(f"  bf16 half-batch forward logits rel-L2 {e:.2e}")
+    assert e < 5e-3
+
+
 def test_loss_decreases_over_steps():
     m, r, tok, tgt, cfg = build_pair(0, lr=1e-3)
     losses = []
