@@ -359,13 +359,16 @@ static_assert(GN_COLS * GN_GROUPS == NT, "gain block shape");
 __global__ __launch_bounds__(NT) void adam_gains_k(float *p_, float *g_, float *m_, float *v_,
                                                     bf16 *pb, size_t n, unsigned nchunk,
                                                     AdamGains gs, float lr, float b1, float b2,
-                                                    float eps, float bc1, float bc2, float wd) {
-    if (blockIdx.x < nchunk) {
+                                                    float eps, float bc1, float bc2, float wd,
+                                                    unsigned nblk) {
+    // blocks [0, nblk) walk the nchunk chunks; the gain blocks follow
+    if (blockIdx.x < nblk) {
+      for (unsigned ch = blockIdx.x; ch < nchunk; ch += nblk) {
         const size_t n4 = n / 4;
         f32x4 *p = reinterpret_cast<f32x4 *>(p_), *m = reinterpret_cast<f32x4 *>(m_),
               *v = reinterpret_cast<f32x4 *>(v_);
         const f32x4 *g = reinterpret_cast<const f32x4 *>(g_);
-        const size_t base = (size_t)blockIdx.x * (NT * ADAM_U) + threadIdx.x;
+        const size_t base = (size_t)ch * (NT * ADAM_U) + threadIdx.x;
         auto gain_elem = [&](size_t j) {
             bool in = false;
 #pragma unroll
@@ -398,10 +401,11 @@ __global__ __launch_bounds__(NT) void adam_gains_k(float *p_, float *g_, float *
                 __builtin_nontemporal_store(b, reinterpret_cast<bf16x4 *>(pb) + j);
             }
         }
+      }
         return;
     }
     // a gain block: which gain, which columns
-    unsigned blk = blockIdx.x - nchunk;
+    unsigned blk = blockIdx.x - nblk;
     int gi = 0;
     for (; gi < gs.n; ++gi) {
         const unsigned nb = (gs.g[gi].dim + GN_COLS - 1) / GN_COLS;
@@ -617,7 +621,7 @@ hipError_t embed_lookup_bf16(const bf16 *embed, const uint32_t *ids, float *out,
 
 hipError_t adam_step_gains(float *p, float *g, float *m, float *v, size_t n, float lr, float beta1,
                            float beta2, float eps, float bc1, float bc2, float wd, bf16 *pb,
-                           const AdamGains &gs, hipStream_t st) {
+                           const AdamGains &gs, hipStream_t st, unsigned max_blocks) {
     if (!n) return hipSuccess;
     const bool vec = al16(p) && al16(g) && al16(m) && al16(v) && ((uintptr_t)pb & 7u) == 0 &&
                      n % 4 == 0;
@@ -630,8 +634,9 @@ hipError_t adam_step_gains(float *p, float *g, float *m, float *v, size_t n, flo
     if (!vec || gs.n > kAdamMaxGains) return hipErrorInvalidValue;
     const size_t nchunk = std::max<size_t>(1, (n / 4 + NT * ADAM_U - 1) / (NT * ADAM_U));
     if (nchunk + gain_blocks >= (1u << 31)) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(adam_gains_k, dim3((unsigned)(nchunk + gain_blocks)), dim3(NT), 0, st, p, g,
-                       m, v, pb, n, (unsigned)nchunk, gs, lr, beta1, beta2, eps, bc1, bc2, wd);
+    const unsigned nblk = (unsigned)(max_blocks ? std::min<size_t>(nchunk, max_blocks) : nchunk);
+    hipLaunchKernelGGL(adam_gains_k, dim3(nblk + gain_blocks), dim3(NT), 0, st, p, g, m, v, pb, n,
+                       (unsigned)nchunk, gs, lr, beta1, beta2, eps, bc1, bc2, wd, nblk);
     return hipGetLastError();
 }
 

@@ -179,9 +179,11 @@ struct AdamGains {
     AdamGain g[kAdamMaxGains];
     int n;
 };
+// max_blocks (0: one block per chunk): at most that many blocks walk the span's
+// chunks, lowering the update's instantaneous share of HBM beside other work.
 hipError_t adam_step_gains(float *p, float *g, float *m, float *v, size_t n, float lr, float beta1,
                            float beta2, float eps, float bc1, float bc2, float wd, bf16 *pb,
-                           const AdamGains &gs, hipStream_t st);
+                           const AdamGains &gs, hipStream_t st, unsigned max_blocks = 0);
 
 // y (fp32 or bf16 per ydt) = rmsnorm(x) * w
 hipError_t rmsnorm_forward(const float *x, const float *w, void *y, DType ydt, int rows, int dim,

@@ -1517,8 +1517,16 @@ struct vkh_runner {
         const float t = (float)step_t;
         const float bc1 = 1.0f - powf(cfg.beta1, t);
         const float bc2 = 1.0f - powf(cfg.beta2, t);
+        // bf16 without recompute: three blocks per CU walk the layer's chunks, so the
+        // update streams beside the main stream's latency-bound backward kernels
+        // at a lower share of HBM (config 3: 18.07-18.33 -> 17.74-18.01 ms in three
+        // alternating pairs, same losses; on one box 3 / 2 / 4 / 5 per CU measured
+        // 18.02-18.04 / 18.23-18.26 / 18.09-18.12 / 18.36-18.37).  The
+        // fp32 step (71.30-71.35 against 70.90-70.94) and config 5 (582.3 against
+        // 578.7), whose side streams have no slack to spare, keep the full grid.
+        const unsigned cap = b16() && !recompute ? 3u * (unsigned)cu_count() : 0u;
         VKH_HIP(adam_step_gains(Pat(b), G + b, M + b, Vm + b, e - b, cfg.lr, cfg.beta1, cfg.beta2,
-                                cfg.eps_adam, bc1, bc2, 0.f, b16() ? Pb + b : nullptr, gs, side));
+                                cfg.eps_adam, bc1, bc2, 0.f, b16() ? Pb + b : nullptr, gs, side, cap));
         return VKH_OK;
     }
 
